@@ -1,0 +1,215 @@
+/*
+ * wavo_hip.h — the C ABI of the MI355X (gfx950) backend for wavo's encoder/decoder compute path.
+ *
+ * The entry points mirror wavo's crate-internal GPU operator API one to one (src/gpu/mod.rs: `Gpu`,
+ * `Linear`, `Channels`, `Epilogue`, `Pass`), so that a Rust `src/gpu/hip.rs` binds them through a
+ * thin `extern "C"` block.  Each declaration cites the reference interface it
+ * replaces.  Plain pointers and sizes only: no HIP or torch types cross this boundary.
+ *
+ * Conventions
+ *  - Every entry returns 0 on success or a negative WH_E* code; wh_last_error(ctx) gives the text
+ *    that the Rust side turns into Error::Gpu (device failures) or Error::Model (shapes/arguments).
+ *  - Device pointers come from wh_alloc().  Activations are f32 row-major [rows][cols], as in the
+ *    reference.  Ops are queued on the context's stream in call order (the reference records them
+ *    into one compute pass); wh_sync()/wh_read() wait for them and report deferred device errors,
+ *    as Gpu::run's final poll does (src/gpu/mod.rs:969-1002).
+ *  - A context is not internally synchronized (the reference serializes calls with Gpu::busy,
+ *    src/gpu/mod.rs:232-233): one thread at a time per context.
+ */
+#ifndef WAVO_HIP_H
+#define WAVO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error codes.  WH_EARG ≙ Error::Model (bad shape or argument, not fatal); WH_EGPU and WH_EOOM ≙
+ * Error::Gpu (Error::is_fatal, src/error.rs:129-140: the caller reloads). */
+#define WH_OK 0
+#define WH_EARG (-1)
+#define WH_EGPU (-2)
+#define WH_EOOM (-3)
+
+/* ggml tensor types of GGUF weights (src/gguf.rs:14-38, plus ggml's Q4_0 = 2). */
+#define WH_F32 0
+#define WH_F16 1
+#define WH_Q4_0 2
+#define WH_Q8_0 8
+
+/* Epilogue modes, equal to Epilogue::params (src/gpu/mod.rs:430-456). */
+#define WH_BIAS 0
+#define WH_SILU 1
+#define WH_RELU 2
+#define WH_RESIDUAL 3 /* c += alpha * v */
+#define WH_GELU 4
+#define WH_GELU_RESIDUAL 5
+#define WH_TANH 6
+
+typedef struct wh_ctx wh_ctx;
+typedef struct wh_linear wh_linear;
+typedef struct wh_model wh_model;
+
+/* ------------------------------------------------------------------------- device and memory */
+
+/* Gpu::new(fast, index) (src/gpu/mod.rs:461).  device_index < 0 picks device 0. */
+int wh_open(int device_index, wh_ctx **out);
+/* Drop for Gpu. */
+void wh_close(wh_ctx *ctx);
+/* The message of the last failed call on ctx (or of the last failed wh_open when ctx is NULL). */
+const char *wh_last_error(const wh_ctx *ctx);
+/* Gpu::info / Device (src/gpu/mod.rs:580, :30-46): name, compute units, wavefront size. */
+int wh_device_info(wh_ctx *ctx, char *name, size_t name_len, int *compute_units, int *wave);
+/* Gpu::buffer / readback (src/gpu/mod.rs:675-697): n_f32 floats of device memory, uninitialized. */
+int wh_alloc(wh_ctx *ctx, size_t n_f32, float **dptr);
+int wh_free(wh_ctx *ctx, void *dptr);
+/* Gpu::write / upload (src/gpu/mod.rs:741-750): bytes from host memory, complete on return. */
+int wh_write(wh_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Device-to-device copy on the stream. */
+int wh_copy(wh_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Zero `bytes` of device memory with a fill kernel (safe inside stream capture). */
+int wh_zero(wh_ctx *ctx, void *dst, size_t bytes);
+/* The readback of Gpu::run / finish (src/gpu/mod.rs:969-1002): waits for the queued work, reports
+ * deferred device errors, then copies `bytes` from device memory to host memory. */
+int wh_read(wh_ctx *ctx, void *host, const void *dptr, size_t bytes);
+/* Waits for the queued work; reports deferred device errors (Gpu::complete's poll). */
+int wh_sync(wh_ctx *ctx);
+/* The context's hipStream_t as an opaque pointer, for callers that time with HIP events. */
+void *wh_stream(wh_ctx *ctx);
+/* Per-launch profiling (no counterpart in the reference, whose timing lives in `wavo bench` and GPU
+ * timestamp queries, docs/perf.md:54): with on != 0 every kernel launch gets HIP events on the
+ * stream around it; wh_profile_read waits, then writes JSON text: per kernel variant its launches,
+ * total milliseconds and algorithmic flops and bytes.  Turning it on or off clears the records. */
+int wh_profile(wh_ctx *ctx, int on);
+int wh_profile_read(wh_ctx *ctx, char *out, size_t len);
+
+/* -------------------------------------------------------------------------------- weights */
+
+/* One GGUF weight tensor [rows][k] in its file bytes (ggml dims [k, rows], dims[0] contiguous:
+ * src/gguf.rs:109-111), type WH_F32/F16/Q4_0/Q8_0. */
+typedef struct wh_tensor {
+  const void *data;
+  int type;
+  int k;
+  int rows;
+} wh_tensor;
+
+/* Gpu::linear (src/gpu/mod.rs:758) and, with pad_k != 0, Gpu::conv (:766): the tensors stacked
+ * along n, kept on the device in their GGUF bytes (Q8_0 34-byte / Q4_0 18-byte blocks as stored),
+ * with the bias of the stacked rows (n_bias == 0: zeros).  A bias with `dual` more values than the
+ * rows writes the first `dual` outputs again after the others with those biases (upload_linear,
+ * :770-834).  k % 32 == 0 unless pad_k, which pads k to 32 with zero columns in F32 (exact, as the
+ * GEMM rounds W to f16 either way). */
+int wh_linear_new(wh_ctx *ctx, const wh_tensor *ws, int count, const float *bias, int n_bias,
+                  int pad_k, wh_linear **out);
+/* Linear::width (src/gpu/mod.rs:406-412): output columns per row of c, `cols + dual`, where cols =
+ * rows when rows % 32 == 0, else rows rounded up to 64. */
+int wh_linear_width(const wh_linear *l);
+/* The (padded) k the layer takes, and its weight type. */
+int wh_linear_k(const wh_linear *l);
+int wh_linear_type(const wh_linear *l);
+void wh_linear_free(wh_ctx *ctx, wh_linear *l);
+
+/* --------------------------------------------------------------------------------- Pass ops */
+
+/* Pass::gemm (src/gpu/mod.rs:1394-1426): c = epi(h(a)·h(W)ᵀ + b) for m rows of a [m][k], h =
+ * round-to-f16, f32 accumulation; rows of c are wh_linear_width() wide; columns rows..cols get
+ * epi(0); dual columns get acc + bias with no epilogue.  Residual modes read c. */
+int wh_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int epi,
+            float alpha);
+/* Pass::gemv (src/gpu/mod.rs:1461-1467): c[offset + j] = epi(a·W[j] + b[j]) for one row a, W not
+ * rounded. */
+int wh_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,
+            int offset);
+/* Pass::embed (src/gpu/mod.rs:1469-1482): c = W[ids[i]] + pos[offset..] + b, k values. */
+int wh_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, const uint32_t *ids,
+             int i, int offset);
+/* Pass::layer_norm (src/gpu/mod.rs:1428-1446): LayerNorm (eps 1e-5) of rows x [rows][cols] with
+ * gain g and bias b into y; with table != NULL also into yr with RoPE (NEOX split-half per head of
+ * head_dim; table [rows][cos(hd/2) | sin(hd/2)]).  Pass::layer_norm_row is rows = 1. */
+int wh_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *b, float *y, int rows,
+                  int cols, const float *table, float *yr, int head_dim);
+/* Pass::attend (src/gpu/mod.rs:1484-1505): one query per head q [heads·hd] over keys 0..n of an f16
+ * cache of `cols` positions (wh_pack's layout) into o, through `part` (wh_attend_len floats). */
+int wh_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, float *o, int n,
+              int cols, int heads, int hd);
+size_t wh_attend_len(int n, int heads, int hd); /* attend_len (src/gpu/mod.rs:1045-1049) */
+/* Pass::pack (src/gpu/mod.rs:1507-1523): rows of x (from float src, stride floats apart, each K
+ * then V of d floats) into the f16 cache y of cols positions at positions col..: K transposed (pair
+ * i of position j at word i·cols + j), then V by position (word d/2·cols + j·d/2 + i). */
+int wh_pack(wh_ctx *ctx, const float *x, int src, int stride, uint32_t *y, int rows, int d,
+            int cols, int col);
+/* Pass::im2col (src/gpu/mod.rs:1525-1533): columns col[i][c·kernel + k] = x[stride·i + k − pad][c],
+ * rows padded with zeros to a multiple of 32. */
+int wh_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int kernel, int stride,
+              int pad);
+/* Pass::conv_glu (src/gpu/mod.rs:1535-1557): GLU of h [t][2ch], depthwise conv (odd kernel,
+ * centred; taps dw_w [ch][kernel] + dw_b), LayerNorm (layer_norm != 0) or affine x·g + b, SiLU,
+ * into y [t][ch].  `valid` (< t) zeroes the GLU output of frames >= valid first (a padded window's
+ * frame mask, src/ane/conformer.rs:301-309); valid >= t is unmasked. */
+int wh_conv_glu(wh_ctx *ctx, const float *h, const float *dw_w, const float *dw_b, int kernel,
+                const float *g, const float *b, int layer_norm, float *y, int t, int ch,
+                int valid);
+/* Pass::attention (src/gpu/mod.rs:1559-1601): multi-head attention, scale 1/√head_dim, into o
+ * [t][heads·hd]:
+ *   v != NULL, pos == NULL: qk [t][q | k], v [t][heads·hd]            (rotary, GigaAM)
+ *   v == NULL, pos == NULL: qk [t][q | k | v]                          (Whisper)
+ *   v == NULL, pos != NULL: qk [t][q + u | k | v | q + v], pos [2t + 15][heads·hd] (row r is
+ *     position t + 15 − r); score (i, j) = ((q+u)_i·k_j + (q+v)_i·pos[j − i + t + 15]) / √hd.
+ * `valid` (< t) masks keys >= valid (additive key mask, src/ane/mod.rs:463-466). */
+int wh_attention(wh_ctx *ctx, const float *qk, const float *v, const float *pos, float *o, int t,
+                 int heads, int hd, int valid);
+/* Pass::depthwise (src/gpu/mod.rs:1603-1630): 3×3 stride-2 pad-1 depthwise conv + bias (w [9][ch])
+ * over the image [t][f][ch] into output rows t0..t0+rows of y; x holds the image's rows from
+ * 2·t0 − 1.  With first_w (the first conv, 1 → ch, + first_b, then ReLU, never stored) x is the
+ * one-channel image [t][f] and y gets `rows` rows of [⌈f/4⌉][ch] from output row 2·t0 − 1, rows
+ * from ⌈t/4⌉ on zero. */
+int wh_depthwise(wh_ctx *ctx, const float *x, const float *first_w, const float *first_b,
+                 const float *w, const float *b, float *y, int t, int f, int ch, int t0,
+                 int rows);
+/* Pass::flatten (src/gpu/mod.rs:1674-1678): [t][f][ch] -> [t][ch·f]. */
+int wh_flatten(wh_ctx *ctx, const float *x, float *y, int t, int f, int ch);
+/* Pass::argmax (src/gpu/mod.rs:1669-1672): index of the first maximum of x[..n] into out[0]. */
+int wh_argmax(wh_ctx *ctx, const float *x, uint32_t *out, int n);
+
+/* --------------------------------------------------------------------- model graph drivers */
+
+/* Model::load_with for the GGUF families on this backend (src/lib.rs:580-617): reads the file's
+ * header and weights (src/gguf.rs) and uploads them (gigaam: src/gigaam/encoder.rs:39-57; parakeet:
+ * src/parakeet/encoder.rs:51-74; whisper: src/whisper/encoder.rs:32-45, src/transformer.rs:180-212). */
+int wh_model_load(wh_ctx *ctx, const char *gguf_path, wh_model **out);
+void wh_model_free(wh_model *m);
+/* arch: 0 gigaam, 1 parakeet, 2 whisper; d_model, encoder layers, mel bins, output width. */
+int wh_model_info(const wh_model *m, int *arch, int *d, int *layers, int *mels, int *width);
+/* Encoder frames and output width for mel_frames mel frames (src/parakeet/mod.rs:44-46 etc.). */
+int wh_model_frames(const wh_model *m, int mel_frames, int *frames, int *width);
+/* The family's Encoder::record on device buffers (src/gigaam/encoder.rs:83-93,
+ * src/parakeet/encoder.rs:103-124, src/whisper/encoder.rs:67-74): mel_dev [mel_frames][mels] →
+ * out_dev [frames][width].  `valid` < mel_frames marks the frames past it as padding (kestrel
+ * length masking, src/parakeet/encoder.rs:77-80).  Queued; wh_sync waits. */
+int wh_model_encode(wh_model *m, const float *mel_dev, int mel_frames, int valid, float *out_dev);
+/* A batch of padded windows through the Parakeet encoder (one segment per window, each padded to
+ * mel_frames): valid[b] mel frames of window b are real; keys and conv inputs past a window's valid
+ * frames are masked, as the Neural Engine graph masks them (src/ane/conformer.rs:161-178, :301-309;
+ * src/ane/mod.rs:463-466).  mel_dev [batch][mel_frames][mels] → out_dev [batch][frames][width]. */
+int wh_model_encode_batch(wh_model *m, const float *mel_dev, int batch, int mel_frames,
+                          const int *valid, float *out_dev);
+/* Conformer blocks only, over x_dev [t][d] in place (layers = how many of them). */
+int wh_model_blocks(wh_model *m, float *x_dev, int t, int layers);
+/* Greedy token ids of an encoder output on the host: CTC (GigaAM, src/gigaam/decoder.rs:135-151)
+ * or TDT (Parakeet, src/parakeet/decoder.rs:91-191).  Writes up to cap (token, frame) pairs;
+ * returns the count or a negative error. */
+int wh_model_greedy(wh_model *m, const float *enc_host, int frames, int width, uint32_t *out,
+                    int cap);
+/* Whisper decoding on the device: wh_whisper_begin computes every layer's cross-attention K/V from
+ * the encoder output (Decoder::record_cross, src/transformer.rs:243-248); wh_whisper_step runs one
+ * token at position pos (Decoder::record_step, :254-290) and leaves the logits in logits_dev. */
+int wh_whisper_begin(wh_model *m, const float *enc_dev, int frames);
+int wh_whisper_step(wh_model *m, int token, int pos, float *logits_dev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

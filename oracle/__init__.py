@@ -1,0 +1,369 @@
+"""ctypes binding of the CPU parity oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this package, and only as the checker or the timed CPU baseline; the product (wavo_amd) never
+does.  The C sources restate wavo's CPU backend (src/cpu/) in its portable f16-rounded arithmetic;
+see oracle.h for the per-function citations.
+"""
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+F32, F16, Q4_0, Q8_0 = 0, 1, 2, 8
+BIAS, SILU, RELU, RESIDUAL, GELU, GELU_RESIDUAL, TANH = range(7)
+
+_lib = None
+_fp = ctypes.POINTER(ctypes.c_float)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_ip = ctypes.POINTER(ctypes.c_int)
+
+
+def build():
+    """Compiles liboracle.so with its Makefile (gcc, OpenMP)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "ox_to_half": (ctypes.c_float, [ctypes.c_float]),
+            "ox_half_to_float": (ctypes.c_float, [ctypes.c_uint16]),
+            "ox_float_to_half_bits": (ctypes.c_uint16, [ctypes.c_float]),
+            "ox_exp": (ctypes.c_float, [ctypes.c_float]),
+            "ox_silu": (ctypes.c_float, [ctypes.c_float]),
+            "ox_gelu": (ctypes.c_float, [ctypes.c_float]),
+            "ox_dot": (ctypes.c_float, [_fp, _fp, ctypes.c_size_t]),
+            "ox_type_size": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_size_t]),
+            "ox_dequant": (ctypes.c_int, [ctypes.c_int, ctypes.c_void_p, _fp, ctypes.c_size_t]),
+            "ox_quantize_q8_0": (None, [_fp, ctypes.c_void_p, ctypes.c_size_t]),
+            "ox_quantize_q4_0": (None, [_fp, ctypes.c_void_p, ctypes.c_size_t]),
+            "ox_linear_new": (ctypes.c_void_p, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                ctypes.POINTER(ctypes.c_void_p), _ip, _fp]),
+            "ox_linear_free": (None, [ctypes.c_void_p]),
+            "ox_gemm": (None, [_fp, ctypes.c_void_p, _fp, ctypes.c_int, ctypes.c_int, ctypes.c_float]),
+            "ox_gemm_wide": (None, [_fp, ctypes.c_void_p, _fp, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_float, _fp, ctypes.c_int]),
+            "ox_gemv": (None, [_fp, ctypes.c_void_p, _fp, ctypes.c_int, ctypes.c_float]),
+            "ox_layer_norm": (None, [_fp, _fp, _fp, _fp, ctypes.c_int, ctypes.c_int, _fp, _fp,
+                                     ctypes.c_int]),
+            "ox_im2col": (None, [_fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                 ctypes.c_int, _fp, ctypes.c_int]),
+            "ox_conv_glu": (None, [_fp, _fp, _fp, ctypes.c_int, _fp, _fp, ctypes.c_int, _fp,
+                                   ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+            "ox_attention": (None, [_fp, ctypes.c_int, _fp, ctypes.c_int, _fp, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+            "ox_relative_attention": (None, [_fp, _fp, _fp, _fp, _fp, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_int, ctypes.c_int]),
+            "ox_attend": (None, [_fp, _fp, ctypes.c_int, ctypes.c_int, _fp, ctypes.c_int,
+                                 ctypes.c_int]),
+            "ox_pack": (None, [_fp, ctypes.c_int, ctypes.c_int, _u32p, ctypes.c_int, ctypes.c_int,
+                               ctypes.c_int, ctypes.c_int]),
+            "ox_rope_table": (None, [ctypes.c_int, ctypes.c_int, ctypes.c_double, _fp]),
+            "ox_rel_positions": (None, [ctypes.c_int, ctypes.c_long, ctypes.c_int, _fp]),
+            "ox_batch_norm": (None, [_fp, _fp, _fp, _fp, ctypes.c_int, _fp, _fp]),
+            "ox_sub_first": (None, [_fp, ctypes.c_int, ctypes.c_int, _fp, _fp, _fp, _fp,
+                                    ctypes.c_int, _fp, ctypes.c_int, ctypes.c_int]),
+            "ox_depthwise": (None, [_fp, _fp, _fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _fp,
+                                    ctypes.c_int, ctypes.c_int]),
+            "ox_flatten": (None, [_fp, _fp, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+            "ox_argmax": (ctypes.c_int, [_fp, ctypes.c_int]),
+            "ox_ctc": (ctypes.c_int, [_fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _u32p]),
+            "ox_tdt_scripted": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _ip, ctypes.c_int,
+                                               ctypes.c_int, _ip, ctypes.c_int, _u32p, _ip, _ip]),
+            "ox_model_load": (ctypes.c_void_p, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]),
+            "ox_model_free": (None, [ctypes.c_void_p]),
+            "ox_model_encode": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_int, ctypes.c_int,
+                                               _fp, _ip, _ip]),
+            "ox_model_blocks": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_int, ctypes.c_int]),
+            "ox_model_info": (ctypes.c_int, [ctypes.c_void_p, _ip, _ip, _ip, _ip, _ip]),
+            "ox_model_tdt": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_int, ctypes.c_int,
+                                            _u32p, ctypes.c_int]),
+            "ox_whisper_begin": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_int]),
+            "ox_whisper_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _fp]),
+            "ox_threads": (ctypes.c_int, []),
+            "ox_set_threads": (None, [ctypes.c_int]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def f32(a):
+    """A C-contiguous float32 copy/view of `a` and its pointer."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a, a.ctypes.data_as(_fp)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(_fp)
+
+
+def to_half(x):
+    L = lib()
+    x = np.asarray(x, dtype=np.float32)
+    return np.array([L.ox_to_half(float(v)) for v in x.ravel()], dtype=np.float32).reshape(x.shape)
+
+
+def quantize(x, wtype):
+    """GGUF bytes of the rows of x (float32) in type wtype (convert.py's quantizers for Q8_0)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.size
+    if wtype == F32:
+        return x.tobytes()
+    if wtype == F16:
+        return x.astype(np.float16).tobytes()
+    L = lib()
+    out = ctypes.create_string_buffer(L.ox_type_size(wtype, n))
+    if wtype == Q8_0:
+        L.ox_quantize_q8_0(_ptr(x), out, n)
+    elif wtype == Q4_0:
+        L.ox_quantize_q4_0(_ptr(x), out, n)
+    else:
+        raise ValueError(wtype)
+    return out.raw
+
+
+def dequant(raw, wtype, n):
+    L = lib()
+    out = np.zeros(n, np.float32)
+    buf = ctypes.create_string_buffer(bytes(raw), len(raw))
+    if L.ox_dequant(wtype, buf, _ptr(out), n):
+        raise ValueError(wtype)
+    return out
+
+
+class Linear:
+    """ox_linear: weights [n][k] in GGUF bytes, stacked, with a bias (src/cpu/gemm.rs:35-72)."""
+
+    def __init__(self, wtype, k, tensors, bias=None):
+        L = lib()
+        self._keep = [ctypes.create_string_buffer(bytes(t), len(t)) for t, _ in tensors]
+        rows = [r for _, r in tensors]
+        ws = (ctypes.c_void_p * len(tensors))(*[ctypes.cast(b, ctypes.c_void_p) for b in self._keep])
+        rr = (ctypes.c_int * len(rows))(*rows)
+        self.n = sum(rows)
+        self.k = k
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self.h = L.ox_linear_new(wtype, k, len(tensors), ws, rr, _ptr(b))
+        if not self.h:
+            raise ValueError("bad linear layer")
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().ox_linear_free(self.h)
+            self.h = None
+
+
+def gemm(a, l, m, epi, alpha=0.0, c=None):
+    a, pa = f32(a)
+    c = np.zeros((m, l.n), np.float32) if c is None else np.ascontiguousarray(c, np.float32).copy()
+    lib().ox_gemm(pa, l.h, _ptr(c), m, epi, alpha)
+    return c
+
+
+def gemm_wide(a, l, m, epi, alpha=0.0, c=None, bias2=None, dual=0):
+    a, pa = f32(a)
+    cols = l.n if l.n % 32 == 0 else (l.n + 63) // 64 * 64
+    c = np.zeros((m, cols + dual), np.float32) if c is None else np.ascontiguousarray(c, np.float32).copy()
+    b2 = None if bias2 is None else np.ascontiguousarray(bias2, np.float32)
+    lib().ox_gemm_wide(pa, l.h, _ptr(c), m, epi, alpha, _ptr(b2), dual)
+    return c
+
+
+def gemv(x, l, epi, alpha=0.0, c=None):
+    x, px = f32(x)
+    c = np.zeros(l.n, np.float32) if c is None else np.ascontiguousarray(c, np.float32).copy()
+    lib().ox_gemv(px, l.h, _ptr(c), epi, alpha)
+    return c
+
+
+def layer_norm(x, g, b, table=None, head_dim=0):
+    x, px = f32(x)
+    rows, cols = x.shape
+    y = np.zeros_like(x)
+    yr = np.zeros_like(x) if table is not None else None
+    tb = None if table is None else np.ascontiguousarray(table, np.float32)
+    lib().ox_layer_norm(px, _ptr(f32(g)[0]), _ptr(f32(b)[0]), _ptr(y), rows, cols, _ptr(tb),
+                        _ptr(yr), head_dim)
+    return (y, yr) if table is not None else y
+
+
+def im2col(x, t, ch, kernel, stride, pad, width=None):
+    x, px = f32(x)
+    rows = (t + 2 * pad - kernel) // stride + 1
+    width = width or ch * kernel
+    col = np.zeros((rows, width), np.float32)
+    lib().ox_im2col(px, t, ch, kernel, stride, pad, _ptr(col), width)
+    return col
+
+
+def conv_glu(h, taps, tb, kernel, g, beta, layer_norm_, t, ch, valid=-1):
+    """taps [kernel][ch] (the CPU layout)."""
+    h = np.ascontiguousarray(h, np.float32).copy()
+    y = np.zeros((t, ch), np.float32)
+    lib().ox_conv_glu(_ptr(h), _ptr(f32(taps)[0]), _ptr(f32(tb)[0]), kernel, _ptr(f32(g)[0]),
+                      _ptr(f32(beta)[0]), int(layer_norm_), _ptr(y), t, ch, valid)
+    return y
+
+
+def attention(qk, ld, v, ldv, t, heads, hd, valid=-1):
+    qk, pq = f32(qk)
+    v, pv = f32(v)
+    o = np.zeros((t, heads * hd), np.float32)
+    lib().ox_attention(pq, ld, pv, ldv, _ptr(o), t, heads, hd, valid)
+    return o
+
+
+def relative_attention(qkv, pos, u, vb, t, heads, hd, valid=-1):
+    qkv, pq = f32(qkv)
+    pos, pp = f32(pos)
+    o = np.zeros((t, heads * hd), np.float32)
+    lib().ox_relative_attention(pq, pp, _ptr(f32(u)[0]), _ptr(f32(vb)[0]), _ptr(o), t, heads, hd,
+                                valid)
+    return o
+
+
+def attend(q, kv, cols, n, heads, hd):
+    q, pq = f32(q)
+    kv, pk = f32(kv)
+    o = np.zeros(heads * hd, np.float32)
+    lib().ox_attend(pq, pk, cols, n, _ptr(o), heads, hd)
+    return o
+
+
+def pack(x, src, stride, cache, rows, d, cols, col):
+    x, px = f32(x)
+    cache = np.ascontiguousarray(cache, np.uint32).copy()
+    lib().ox_pack(px, src, stride, cache.ctypes.data_as(_u32p), rows, d, cols, col)
+    return cache
+
+
+def rope_table(frames, hd, theta):
+    out = np.zeros((frames, hd), np.float32)
+    lib().ox_rope_table(frames, hd, theta, _ptr(out))
+    return out
+
+
+def rel_positions(d, first, rows):
+    out = np.zeros((rows, d), np.float32)
+    lib().ox_rel_positions(d, first, rows, _ptr(out))
+    return out
+
+
+def half_len(n):
+    return (n - 1) // 2 + 1
+
+
+def sub_first(mel, valid, mels, w0, b0, w2, b2, ch, rows, t0):
+    mel, pm = f32(mel)
+    y = np.zeros((rows, half_len(half_len(mels)), ch), np.float32)
+    lib().ox_sub_first(pm, valid, mels, _ptr(f32(w0)[0]), _ptr(f32(b0)[0]), _ptr(f32(w2)[0]),
+                       _ptr(f32(b2)[0]), ch, _ptr(y), rows, t0)
+    return y
+
+
+def depthwise(x, w, b, t, f, ch, n, t0):
+    x, px = f32(x)
+    y = np.zeros((n, half_len(f), ch), np.float32)
+    lib().ox_depthwise(px, _ptr(f32(w)[0]), _ptr(f32(b)[0]), t, f, ch, _ptr(y), n, t0)
+    return y
+
+
+def flatten(x, t, f, ch):
+    x, px = f32(x)
+    y = np.zeros((t, f * ch), np.float32)
+    lib().ox_flatten(px, _ptr(y), t, f, ch)
+    return y
+
+
+def ctc(logits, blank):
+    logits, pl = f32(logits)
+    frames, classes = logits.shape
+    out = np.zeros(2 * frames, np.uint32)
+    n = lib().ox_ctc(pl, frames, classes, blank, out.ctypes.data_as(_u32p))
+    return [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(n)]
+
+
+def tdt_scripted(frames, blank, durations, max_symbols, global_, script):
+    """The TDT loop over scripted (token, duration index) decisions: (pairs, calls)."""
+    d = (ctypes.c_int * len(durations))(*durations)
+    flat = [v for pair in script for v in pair]
+    sc = (ctypes.c_int * max(1, len(flat)))(*flat)
+    out = np.zeros(2 * 4096, np.uint32)
+    calls = (ctypes.c_int * (2 * 4096))()
+    used = ctypes.c_int()
+    n = lib().ox_tdt_scripted(frames, blank, d, max_symbols, int(global_), sc, len(script),
+                              out.ctypes.data_as(_u32p), calls, ctypes.byref(used))
+    pairs = [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(n)]
+    cl = [(calls[2 * i], None if calls[2 * i + 1] < 0 else calls[2 * i + 1]) for i in range(used.value)]
+    return pairs, cl
+
+
+class Model:
+    """ox_model: a whole encoder (and decoder) restated on the CPU, loaded from a GGUF file."""
+
+    def __init__(self, path):
+        err = ctypes.create_string_buffer(512)
+        self.h = lib().ox_model_load(path.encode(), err, 512)
+        if not self.h:
+            raise ValueError(err.value.decode())
+        a, d, layers, mels, width = (ctypes.c_int() for _ in range(5))
+        lib().ox_model_info(self.h, ctypes.byref(a), ctypes.byref(d), ctypes.byref(layers),
+                            ctypes.byref(mels), ctypes.byref(width))
+        self.arch, self.d, self.layers, self.mels, self.width = (v.value for v in (a, d, layers, mels, width))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().ox_model_free(self.h)
+            self.h = None
+
+    def encode(self, mel, valid=None):
+        mel, pm = f32(mel)
+        frames, width = ctypes.c_int(), ctypes.c_int()
+        mf = mel.shape[0]
+        valid = mf if valid is None else valid
+        lib().ox_model_encode(self.h, pm, mf, valid, None, ctypes.byref(frames), ctypes.byref(width))
+        out = np.zeros((frames.value, width.value), np.float32)
+        rc = lib().ox_model_encode(self.h, pm, mf, valid, _ptr(out), ctypes.byref(frames),
+                                   ctypes.byref(width))
+        if rc:
+            raise ValueError("encode failed")
+        return out
+
+    def blocks(self, x, layers):
+        x = np.ascontiguousarray(x, np.float32).copy()
+        if lib().ox_model_blocks(self.h, _ptr(x), x.shape[0], layers):
+            raise ValueError("blocks failed")
+        return x
+
+    def tdt(self, enc):
+        enc, pe = f32(enc)
+        out = np.zeros(2 * 16384, np.uint32)
+        n = lib().ox_model_tdt(self.h, pe, enc.shape[0], enc.shape[1], out.ctypes.data_as(_u32p), 16384)
+        if n < 0:
+            raise ValueError("tdt failed")
+        return [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(min(n, 16384))]
+
+    def whisper_begin(self, enc):
+        enc, pe = f32(enc)
+        if lib().ox_whisper_begin(self.h, pe, enc.shape[0]):
+            raise ValueError("whisper_begin failed")
+
+    def whisper_step(self, token, pos, vocab):
+        out = np.zeros(vocab, np.float32)
+        if lib().ox_whisper_step(self.h, token, pos, _ptr(out)):
+            raise ValueError("whisper_step failed")
+        return out

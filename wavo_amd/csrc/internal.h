@@ -1,0 +1,87 @@
+// Internal declarations of the gfx950 backend: the context, weights, and the kernel launchers that
+// the C ABI (include/wavo_hip.h) and the graph drivers call.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../../include/wavo_hip.h"
+
+// One profiled launch: HIP events on the context's stream around it, and its algorithmic work.
+struct wh_prof_rec {
+  std::string kernel;
+  double flops = 0, bytes = 0;
+  int ev0 = -1, ev1 = -1;
+};
+
+struct wh_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int cus = 0;
+  std::string name;
+  std::string error;
+  // Per-launch profiling (wh_profile): off by default.
+  bool prof = false;
+  std::vector<hipEvent_t> events;
+  size_t next_event = 0;
+  std::vector<wh_prof_rec> recs;
+};
+
+// Profiling scope of one launch: records an event before and after it when profiling is on.
+struct ProfScope {
+  ProfScope(wh_ctx *ctx, const char *kernel, double flops, double bytes);
+  ~ProfScope();
+  wh_ctx *ctx;
+  int rec = -1;
+};
+
+// A linear layer on the device (src/gpu/mod.rs:390-413): W [rows][k] in its GGUF bytes, rows
+// contiguous; the bias padded to `cols + dual`.
+struct wh_linear {
+  int rows = 0;   // real rows of W (stacked)
+  int cols = 0;   // output columns before the dual ones
+  int dual = 0;
+  int k = 0;      // inner size (padded to 32 for a conv)
+  int type = 0;   // WH_F32 / WH_F16 / WH_Q4_0 / WH_Q8_0
+  size_t row_bytes = 0;
+  uint8_t *w = nullptr;
+  float *bias = nullptr;  // cols + dual values
+};
+
+// Sets ctx->error and returns code.
+int wh_fail(wh_ctx *ctx, int code, const char *fmt, ...);
+// Checks the last launch; returns WH_OK or WH_EGPU with the HIP error text.
+int wh_launched(wh_ctx *ctx, const char *what);
+
+// Bytes of n weights of a GGUF type.
+size_t wh_type_bytes(int type, size_t n);
+
+// ---- launchers (each validates its shapes, then queues on ctx->stream) ----
+int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int ldc, int epi,
+                float alpha);
+int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,
+                int offset);
+int launch_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, const uint32_t *ids,
+                 int i, int offset);
+int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *b, float *y, int rows,
+                      int cols, const float *table, float *yr, int head_dim);
+int launch_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int kernel, int stride,
+                  int pad, int batch, long x_batch_stride, long col_batch_stride);
+int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb, int kernel,
+                    const float *g, const float *b, int layer_norm, float *y, int t, int ch,
+                    const int *valid_dev, int valid, int batch);
+int launch_attention(wh_ctx *ctx, const float *qk, const float *v, const float *pos, float *o, int t,
+                     int heads, int hd, const int *valid_dev, int valid, int batch);
+int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *b0, const float *w,
+                     const float *b, float *y, int t, int f, int ch, int t0, int rows);
+int launch_flatten(wh_ctx *ctx, const float *x, float *y, int t, int f, int ch);
+int launch_argmax(wh_ctx *ctx, const float *x, uint32_t *out, int n);
+int launch_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, float *o, int n,
+                  int cols, int heads, int hd);
+int launch_pack(wh_ctx *ctx, const float *x, int src, int stride, uint32_t *y, int rows, int d,
+                int cols, int col);
+int launch_zero(wh_ctx *ctx, void *dst, size_t bytes);
+int launch_add_rows(wh_ctx *ctx, float *x, const float *add, size_t n);

@@ -1,0 +1,1171 @@
+// Graph drivers of the family encoders and the Whisper decoder on the gfx950 kernels, and the host
+// greedy decoders of their outputs.  They record the ops in the order the reference's GPU graph
+// builders do:
+//   GGUF v3 reading ............ src/gguf.rs:121-287
+//   Conformer blocks ........... src/conformer.rs:34-61 (Config::load), :107-116, :180-265
+//   GigaAM encoder ............. src/gigaam/encoder.rs:39-118, rope table src/gigaam/mod.rs:86-97
+//   Parakeet encoder ........... src/parakeet/encoder.rs:51-153, frames src/parakeet/mod.rs:44-46
+//   Whisper encoder/decoder .... src/whisper/encoder.rs:32-74, src/transformer.rs:103-290
+//   CTC greedy ................. src/gigaam/decoder.rs:135-151
+//   TDT greedy ................. src/parakeet/decoder.rs:91-191 (host, as the reference runs it)
+// Activations live in an arena of device buffers sized for the longest input so far (the
+// reference's per-family Arena, e.g. src/gigaam/encoder.rs:25-35, :61-72).  The Parakeet
+// subsampling runs unchunked: the reference splits it into 8 chunks to bound memory
+// (src/parakeet/encoder.rs:17-19), which 288 GB of HBM does not need, and one launch per conv keeps
+// its GEMM large.
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+
+namespace {
+
+// ------------------------------------------------------------------------------- GGUF reader
+
+struct Tensor {
+  std::vector<size_t> dims;
+  int type = 0;
+  const uint8_t *data = nullptr;
+  size_t count() const {
+    size_t n = 1;
+    for (size_t d : dims) n *= d;
+    return n;
+  }
+};
+
+struct Value {
+  unsigned type = 0;
+  const uint8_t *p = nullptr;
+};
+
+class Gguf {
+ public:
+  ~Gguf() {
+    if (map_) munmap(map_, len_);
+  }
+
+  bool open(const char *path, std::string &err) {
+    int fd = ::open(path, O_RDONLY);
+    if (fd < 0) return err = std::string("cannot open ") + path, false;
+    struct stat st;
+    fstat(fd, &st);
+    len_ = (size_t)st.st_size;
+    void *m = mmap(nullptr, len_, PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);
+    if (m == MAP_FAILED) return err = "cannot map the file", false;
+    map_ = (uint8_t *)m;
+    p_ = map_;
+    end_ = map_ + len_;
+    if (len_ < 4 || memcmp(map_, "GGUF", 4)) return err = "not a GGUF file", false;
+    p_ += 4;
+    uint32_t version = (uint32_t)rd(4);
+    if (version != 3) return err = "unsupported GGUF version " + std::to_string(version), false;
+    uint64_t n_t = rd(8), n_kv = rd(8);
+    if (bad_ || n_t > (1u << 24) || n_kv > (1u << 24)) return err = "truncated GGUF header", false;
+    size_t align = 32;
+    for (uint64_t i = 0; i < n_kv && !bad_; i++) {
+      std::string key = str();
+      Value v;
+      v.type = (unsigned)rd(4);
+      v.p = p_;
+      if (key == "general.alignment" && v.type == 4) {
+        uint32_t a;
+        memcpy(&a, p_, 4);
+        align = a;
+      }
+      skip(v.type);
+      kv_[key] = v;
+    }
+    std::vector<std::pair<std::string, std::pair<Tensor, uint64_t>>> infos;
+    for (uint64_t i = 0; i < n_t && !bad_; i++) {
+      std::string name = str();
+      uint32_t nd = (uint32_t)rd(4);
+      if (nd < 1 || nd > 4) bad_ = true;
+      Tensor t;
+      for (uint32_t d = 0; d < nd && !bad_; d++) t.dims.push_back((size_t)rd(8));
+      t.type = (int)rd(4);
+      uint64_t off = rd(8);
+      infos.push_back({name, {t, off}});
+    }
+    if (bad_) return err = "truncated GGUF header", false;
+    size_t data = ((size_t)(p_ - map_) + align - 1) / align * align;
+    for (auto &in : infos) {
+      Tensor t = in.second.first;
+      size_t bytes = wh_type_bytes(t.type, t.count());
+      if (!bytes || data + in.second.second + bytes > len_)
+        return err = "tensor " + in.first + " is out of file bounds or of an unsupported type", false;
+      t.data = map_ + data + in.second.second;
+      tensors_[in.first] = t;
+    }
+    return true;
+  }
+
+  const Tensor *tensor(const std::string &name) const {
+    auto it = tensors_.find(name);
+    return it == tensors_.end() ? nullptr : &it->second;
+  }
+
+  bool has(const std::string &key) const { return kv_.count(key) != 0; }
+
+  long integer(const std::string &key, long dflt) const {
+    auto it = kv_.find(key);
+    if (it == kv_.end()) return dflt;
+    const uint8_t *p = it->second.p;
+    switch (it->second.type) {
+      case 0: return p[0];
+      case 1: return (int8_t)p[0];
+      case 2: { uint16_t v; memcpy(&v, p, 2); return v; }
+      case 3: { int16_t v; memcpy(&v, p, 2); return v; }
+      case 4: { uint32_t v; memcpy(&v, p, 4); return v; }
+      case 5: { int32_t v; memcpy(&v, p, 4); return v; }
+      case 7: return p[0];
+      case 10: case 11: { int64_t v; memcpy(&v, p, 8); return (long)v; }
+    }
+    return dflt;
+  }
+
+  std::string string(const std::string &key) const {
+    auto it = kv_.find(key);
+    if (it == kv_.end() || it->second.type != 8) return "";
+    uint64_t n;
+    memcpy(&n, it->second.p, 8);
+    return std::string((const char *)it->second.p + 8, n);
+  }
+
+  std::vector<long> ints(const std::string &key) const {
+    std::vector<long> out;
+    auto it = kv_.find(key);
+    if (it == kv_.end() || it->second.type != 9) return out;
+    uint32_t item;
+    uint64_t n;
+    memcpy(&item, it->second.p, 4);
+    memcpy(&n, it->second.p + 4, 8);
+    const uint8_t *p = it->second.p + 12;
+    size_t s = item == 4 || item == 5 ? 4 : (item == 10 || item == 11 ? 8 : 0);
+    for (uint64_t i = 0; s && i < n; i++, p += s) {
+      if (s == 4) {
+        int32_t v;
+        memcpy(&v, p, 4);
+        out.push_back(item == 4 ? (long)(uint32_t)v : (long)v);
+      } else {
+        int64_t v;
+        memcpy(&v, p, 8);
+        out.push_back((long)v);
+      }
+    }
+    return out;
+  }
+
+ private:
+  uint64_t rd(int n) {
+    if (p_ + n > end_) {
+      bad_ = true;
+      return 0;
+    }
+    uint64_t v = 0;
+    for (int i = 0; i < n; i++) v |= (uint64_t)p_[i] << (8 * i);
+    p_ += n;
+    return v;
+  }
+  std::string str() {
+    uint64_t n = rd(8);
+    if (bad_ || p_ + n > end_) {
+      bad_ = true;
+      return "";
+    }
+    std::string s((const char *)p_, n);
+    p_ += n;
+    return s;
+  }
+  void skip(unsigned t) {
+    static const int sz[] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
+    if (t == 8) {
+      str();
+    } else if (t == 9) {
+      unsigned it = (unsigned)rd(4);
+      uint64_t n = rd(8);
+      for (uint64_t i = 0; i < n && !bad_; i++) skip(it);
+    } else if (t < 13 && sz[t]) {
+      if (p_ + sz[t] > end_) bad_ = true;
+      else p_ += sz[t];
+    } else {
+      bad_ = true;
+    }
+  }
+
+  uint8_t *map_ = nullptr;
+  size_t len_ = 0;
+  const uint8_t *p_ = nullptr, *end_ = nullptr;
+  bool bad_ = false;
+  std::map<std::string, Value> kv_;
+  std::map<std::string, Tensor> tensors_;
+};
+
+float half_to_float(uint16_t h) {
+  uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31, m = h & 0x3ff, u;
+  if (e == 0) {
+    float v = (float)m * 5.9604644775390625e-8f;
+    return s ? -v : v;
+  }
+  u = e == 31 ? (s | 0x7f800000u | (m << 13)) : (s | ((e + 112) << 23) | (m << 13));
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// Tensor::to_f32 (src/gguf.rs:274-287), plus Q4_0.
+std::vector<float> to_f32(const Tensor &t) {
+  size_t n = t.count();
+  std::vector<float> out(n);
+  const uint8_t *s = t.data;
+  switch (t.type) {
+    case WH_F32: memcpy(out.data(), s, n * 4); break;
+    case WH_F16:
+      for (size_t i = 0; i < n; i++) {
+        uint16_t h;
+        memcpy(&h, s + 2 * i, 2);
+        out[i] = half_to_float(h);
+      }
+      break;
+    case WH_Q8_0:
+      for (size_t b = 0; b < n / 32; b++) {
+        uint16_t h;
+        memcpy(&h, s + 34 * b, 2);
+        float d = half_to_float(h);
+        for (int i = 0; i < 32; i++) out[32 * b + i] = (float)(int8_t)s[34 * b + 2 + i] * d;
+      }
+      break;
+    case WH_Q4_0:
+      for (size_t b = 0; b < n / 32; b++) {
+        uint16_t h;
+        memcpy(&h, s + 18 * b, 2);
+        float d = half_to_float(h);
+        for (int i = 0; i < 16; i++) {
+          out[32 * b + i] = (float)((int)(s[18 * b + 2 + i] & 15) - 8) * d;
+          out[32 * b + 16 + i] = (float)((int)(s[18 * b + 2 + i] >> 4) - 8) * d;
+        }
+      }
+      break;
+  }
+  return out;
+}
+
+// ----------------------------------------------------------------------------- device helpers
+
+// A device f32 array owned by the model.
+struct DevArray {
+  float *p = nullptr;
+  size_t n = 0;
+};
+
+struct Chan {
+  float *w = nullptr, *b = nullptr;
+};
+
+class Loader {
+ public:
+  Loader(wh_ctx *ctx, const Gguf &g) : ctx_(ctx), g_(g) {}
+  std::string err;
+
+  const Tensor *need(const std::string &name, size_t want = 0) {
+    const Tensor *t = g_.tensor(name);
+    if (!t) {
+      fail("missing tensor " + name);
+      return nullptr;
+    }
+    if (want && t->count() != want) {
+      fail("tensor " + name + " has " + std::to_string(t->count()) + " values, expected " + std::to_string(want));
+      return nullptr;
+    }
+    return t;
+  }
+
+  std::vector<float> f32s(const std::string &name, size_t want) {
+    const Tensor *t = need(name, want);
+    return t ? to_f32(*t) : std::vector<float>(want, 0.0f);
+  }
+
+  float *upload(const std::vector<float> &v) {
+    if (!err.empty()) return nullptr;
+    float *p = nullptr;
+    if (wh_alloc(ctx_, v.size(), &p)) {
+      fail(ctx_->error);
+      return nullptr;
+    }
+    owned.push_back(p);
+    if (!v.empty() && wh_write(ctx_, p, v.data(), v.size() * 4)) fail(ctx_->error);
+    return p;
+  }
+
+  Chan norm(const std::string &name, int d, bool bias) {
+    Chan c;
+    c.w = upload(f32s(name + ".weight", d));
+    c.b = upload(bias ? f32s(name + ".bias", d) : std::vector<float>(d, 0.0f));
+    return c;
+  }
+
+  // conformer::linear / transformer::stacked: the weights `names[i].weight` stacked along n with
+  // their biases (index `zero` has none: Whisper's k); `extra` appended after (dual outputs).
+  wh_linear *linear(const std::vector<std::string> &names, bool bias, int zero = -1,
+                    const std::vector<float> &override_bias = {}, int pad_k = 0) {
+    if (!err.empty()) return nullptr;
+    std::vector<wh_tensor> ws;
+    std::vector<float> b;
+    for (size_t i = 0; i < names.size(); i++) {
+      const Tensor *t = need(names[i] + ".weight");
+      if (!t) return nullptr;
+      int k = (int)t->dims[0];
+      for (size_t d = 1; d + 1 < t->dims.size(); d++) k *= (int)t->dims[d];
+      int rows = (int)t->dims.back();
+      ws.push_back(wh_tensor{t->data, t->type, k, rows});
+      if (bias) {
+        if ((int)i == zero) b.insert(b.end(), rows, 0.0f);
+        else {
+          auto bi = f32s(names[i] + ".bias", rows);
+          b.insert(b.end(), bi.begin(), bi.end());
+        }
+      }
+    }
+    const std::vector<float> &bb = override_bias.empty() ? b : override_bias;
+    wh_linear *l = nullptr;
+    if (wh_linear_new(ctx_, ws.data(), (int)ws.size(), bb.empty() ? nullptr : bb.data(), (int)bb.size(), pad_k, &l)) {
+      fail(names[0] + ": " + ctx_->error);
+      return nullptr;
+    }
+    linears.push_back(l);
+    return l;
+  }
+
+  void fail(const std::string &m) {
+    if (err.empty()) err = m;
+  }
+
+  std::vector<float *> owned;
+  std::vector<wh_linear *> linears;
+
+ private:
+  wh_ctx *ctx_;
+  const Gguf &g_;
+};
+
+// ----------------------------------------------------------------------------------- model
+
+enum Arch { GIGAAM = 0, PARAKEET = 1, WHISPER = 2 };
+
+struct Block {
+  Chan norm_ff1, norm_attn, norm_conv, norm_ff2, norm_out, conv_norm, dw;
+  wh_linear *ff1[2] = {}, *ff2[2] = {}, *out = nullptr, *pw1 = nullptr, *pw2 = nullptr;
+  wh_linear *qk = nullptr, *v = nullptr;     // rotary: q stacked over k, and v
+  wh_linear *qkv = nullptr, *pos = nullptr;  // relative: [q + u | k | v | q + v], linear_pos
+};
+
+struct WBlock {
+  Chan norm_attn, norm_ffn;
+  wh_linear *qkv = nullptr, *out = nullptr, *fc1 = nullptr, *fc2 = nullptr;
+};
+
+struct DLayer {
+  Chan norm_self, norm_cross, norm_ffn;
+  wh_linear *qkv = nullptr, *self_out = nullptr, *cross_q = nullptr, *cross_kv = nullptr, *cross_out = nullptr,
+            *fc1 = nullptr, *fc2 = nullptr;
+};
+
+// A decoder matrix on the host for the TDT greedy loop: rows of f32 (dequantized, exact).
+struct HostMat {
+  int rows = 0, k = 0;
+  std::vector<float> w;
+};
+
+int half_len(int n) { return (n - 1) / 2 + 1; }
+
+}  // namespace
+
+struct wh_model {
+  wh_ctx *ctx = nullptr;
+  Arch arch = GIGAAM;
+  std::unique_ptr<Gguf> g;
+  std::vector<float *> owned;
+  std::vector<wh_linear *> linears;
+  // Conformer config.
+  int layers = 0, d = 0, heads = 0, d_ff = 0, kernel = 0, mels = 0;
+  bool layer_norm_conv = false, relative = false;
+  std::vector<Block> blocks;
+  // GigaAM
+  double theta = 5000.0;
+  wh_linear *conv0 = nullptr, *conv2 = nullptr, *head = nullptr;
+  int outputs = 0, blank = 0;
+  // Parakeet
+  int ch = 0;
+  Chan sc0, sc2, sc5;
+  wh_linear *conv3 = nullptr, *conv6 = nullptr, *pre_out = nullptr, *joint_enc = nullptr;
+  // TDT decoder (host)
+  int hidden = 0, joint = 0, classes = 0, max_symbols = 10, lstm_layers = 0;
+  bool global = false;
+  std::vector<int> durations;
+  HostMat embed_h, pred_w, out_w;
+  std::vector<HostMat> wx, wh;
+  std::vector<std::vector<float>> lstm_b;
+  std::vector<float> pred_b, out_b;
+  // Whisper
+  int frames = 1500, dec_layers = 0, dec_heads = 0, dec_ff = 0, vocab = 0, context = 0;
+  wh_linear *wconv0 = nullptr, *wconv1 = nullptr, *token_embd = nullptr;
+  float *enc_pos = nullptr, *dec_pos = nullptr;
+  std::vector<WBlock> wblocks;
+  std::vector<DLayer> dl;
+  Chan enc_norm, dec_norm;
+  // Arena (device activations), sized for `cap` encoder frames × `cap_batch` windows.
+  int cap = 0, cap_batch = 0;
+  float *x = nullptr, *y = nullptr, *h = nullptr, *qk = nullptr, *yr = nullptr, *pos = nullptr, *sub = nullptr;
+  int *valid_dev = nullptr;
+  float *sub2 = nullptr;   // Parakeet conv3 output (the subsampling's second buffer)
+  float *rope = nullptr;   // GigaAM rope table for `cap` frames
+  const float *pos_cur = nullptr;  // Parakeet: the positions of this call (rows from cap - t)
+  // Whisper decoding state.
+  float *dx = nullptr, *dy = nullptr, *dqkv = nullptr, *dh = nullptr, *datt = nullptr, *dpart = nullptr,
+        *dscratch = nullptr;
+  uint32_t *ids = nullptr;
+  std::vector<uint32_t *> own, cross;
+  int cross_frames = 0;
+};
+
+namespace {
+
+int fail(wh_model *m, const std::string &msg, int code = WH_EARG) { return wh_fail(m->ctx, code, "%s", msg.c_str()); }
+
+#define CK(expr)             \
+  do {                       \
+    int rc_ = (expr);        \
+    if (rc_) return rc_;     \
+  } while (0)
+
+float *dev_alloc(wh_model *m, size_t n) {
+  float *p = nullptr;
+  if (wh_alloc(m->ctx, n, &p)) return nullptr;
+  m->owned.push_back(p);
+  return p;
+}
+
+// Conformer config (src/conformer.rs:34-61).
+bool conformer_config(const Gguf &g, wh_model *m, const std::string &arch, std::string &err) {
+  auto u = [&](const char *name) { return (int)g.integer("stt." + arch + ".encoder." + name, -1); };
+  m->layers = u("n_layers");
+  m->d = u("d_model");
+  m->heads = u("n_heads");
+  m->d_ff = u("d_ff");
+  m->kernel = u("conv_kernel");
+  std::string cn = g.string("stt." + arch + ".encoder.conv_norm_type");
+  if (cn != "layer_norm" && cn != "batch_norm") return err = "unsupported conv_norm_type \"" + cn + "\"", false;
+  m->layer_norm_conv = cn == "layer_norm";
+  int d = m->d, heads = m->heads;
+  if (m->layers <= 0 || d <= 0 || heads <= 0 || d % heads || d > 1024 || d / heads > 128 || (d / heads) % 2) {
+    err = "unsupported attention shape: d_model " + std::to_string(d) + ", " + std::to_string(heads) + " heads";
+    return false;
+  }
+  if (m->kernel <= 0 || m->kernel % 2 == 0) return err = "conv kernel " + std::to_string(m->kernel) + ": only odd kernels are supported", false;
+  if ((d / heads) % 4) return err = "head_dim must be a multiple of 4 on this backend", false;
+  return true;
+}
+
+// Block::load (src/conformer.rs:180-229).
+void load_block(Loader &L, wh_model *m, int i, Block &k) {
+  int d = m->d, hd = d / m->heads;
+  std::string p = "enc.blocks." + std::to_string(i) + ".";
+  bool bias = !m->relative;  // GigaAM has layer biases, Parakeet none
+  k.norm_ff1 = L.norm(p + "norm_ff1", d, true);
+  k.ff1[0] = L.linear({p + "ff1.linear1"}, bias);
+  k.ff1[1] = L.linear({p + "ff1.linear2"}, bias);
+  k.norm_attn = L.norm(p + "norm_attn", d, true);
+  if (!m->relative) {
+    k.qk = L.linear({p + "attn.linear_q", p + "attn.linear_k"}, bias);
+    k.v = L.linear({p + "attn.linear_v"}, bias);
+  } else {
+    // [q | k | v] with biases [pos_bias_u | 0 | 0], and q again with pos_bias_v (dual outputs).
+    auto u = L.f32s(p + "attn.pos_bias_u", (size_t)hd * m->heads);
+    auto v = L.f32s(p + "attn.pos_bias_v", (size_t)hd * m->heads);
+    std::vector<float> b(u);
+    b.insert(b.end(), 2 * (size_t)d, 0.0f);
+    b.insert(b.end(), v.begin(), v.end());
+    k.qkv = L.linear({p + "attn.linear_q", p + "attn.linear_k", p + "attn.linear_v"}, false, -1, b);
+    k.pos = L.linear({p + "attn.linear_pos"}, false);
+  }
+  k.out = L.linear({p + "attn.linear_out"}, bias);
+  k.norm_conv = L.norm(p + "norm_conv", d, true);
+  k.pw1 = L.linear({p + "conv.pointwise1"}, bias);
+  if (m->layer_norm_conv) {
+    k.conv_norm = L.norm(p + "conv.ln", d, true);
+  } else {
+    // batch_norm (src/conformer.rs:132-139): x·scale + shift.
+    auto w = L.f32s(p + "conv.bn.weight", d), b = L.f32s(p + "conv.bn.bias", d);
+    auto mean = L.f32s(p + "conv.bn.running_mean", d), var = L.f32s(p + "conv.bn.running_var", d);
+    std::vector<float> scale(d), shift(d);
+    for (int c = 0; c < d; c++) {
+      scale[c] = w[c] / std::sqrt(var[c] + 1e-5f);
+      shift[c] = b[c] - mean[c] * scale[c];
+    }
+    k.conv_norm.w = L.upload(scale);
+    k.conv_norm.b = L.upload(shift);
+  }
+  // Depthwise taps [d][kernel] as the file stores them (the GPU layout).
+  k.dw.w = L.upload(L.f32s(p + "conv.depthwise.weight", (size_t)d * m->kernel));
+  k.dw.b = L.upload(bias ? L.f32s(p + "conv.depthwise.bias", d) : std::vector<float>(d, 0.0f));
+  k.pw2 = L.linear({p + "conv.pointwise2"}, bias);
+  k.norm_ff2 = L.norm(p + "norm_ff2", d, true);
+  k.ff2[0] = L.linear({p + "ff2.linear1"}, bias);
+  k.ff2[1] = L.linear({p + "ff2.linear2"}, bias);
+  k.norm_out = L.norm(p + "norm_out", d, true);
+}
+
+HostMat host_mat(Loader &L, const std::string &name) {
+  HostMat h;
+  const Tensor *t = L.need(name);
+  if (!t) return h;
+  h.k = (int)t->dims[0];
+  h.rows = (int)(t->count() / h.k);
+  h.w = to_f32(*t);
+  return h;
+}
+
+bool load_parakeet(const Gguf &g, Loader &L, wh_model *m, std::string &err) {
+  m->relative = true;
+  if (!conformer_config(g, m, "parakeet", err)) return false;
+  m->mels = (int)g.integer("stt.frontend.num_mels", -1);
+  m->ch = (int)g.integer("stt.parakeet.encoder.subsampling_channels", -1);
+  if (m->mels <= 0 || m->ch <= 0 || m->ch > 4096) return err = "bad Parakeet subsampling metadata", false;
+  // 3×3 taps [ch][time tap][freq tap] → [tap][ch] (src/parakeet/encoder.rs:54-59).
+  auto taps = [&](int i) {
+    std::string p = "enc.pre_encode.conv." + std::to_string(i);
+    auto w = L.f32s(p + ".weight", (size_t)9 * m->ch);
+    std::vector<float> t(9 * (size_t)m->ch);
+    for (size_t e = 0; e < t.size(); e++) t[e] = w[(e % m->ch) * 9 + e / m->ch];
+    Chan c;
+    c.w = L.upload(t);
+    c.b = L.upload(L.f32s(p + ".bias", m->ch));
+    return c;
+  };
+  m->sc0 = taps(0);
+  m->sc2 = taps(2);
+  m->sc5 = taps(5);
+  m->conv3 = L.linear({"enc.pre_encode.conv.3"}, true);
+  m->conv6 = L.linear({"enc.pre_encode.conv.6"}, true);
+  m->pre_out = L.linear({"enc.pre_encode.out"}, true);
+  m->joint_enc = L.linear({"joint.enc"}, true);
+  m->blocks.resize(m->layers);
+  for (int i = 0; i < m->layers && L.err.empty(); i++) load_block(L, m, i, m->blocks[i]);
+  // TDT decoder (src/parakeet/decoder.rs:46-89), kept on the host as the reference keeps it.
+  m->blank = (int)g.integer("tokenizer.ggml.blank_token_id", -1);
+  m->hidden = (int)g.integer("stt.parakeet.predictor.hidden", -1);
+  m->joint = (int)g.integer("stt.parakeet.joint.hidden", -1);
+  m->max_symbols = (int)g.integer("stt.parakeet.tdt.max_symbols", 10);
+  m->global = g.string("stt.parakeet.tdt.symbol_budget") == "global";
+  for (long v : g.ints("stt.parakeet.tdt.durations")) m->durations.push_back((int)v);
+  m->lstm_layers = (int)g.integer("stt.parakeet.predictor.n_layers", 1);
+  if (g.tensor("pred.embed.weight") && !m->durations.empty()) {
+    m->embed_h = host_mat(L, "pred.embed.weight");
+    m->classes = m->embed_h.rows;
+    for (int l = 0; l < m->lstm_layers; l++) {
+      std::string p = "pred.lstm." + std::to_string(l);
+      m->wx.push_back(host_mat(L, p + ".Wx"));
+      m->wh.push_back(host_mat(L, p + ".Wh"));
+      m->lstm_b.push_back(L.f32s(p + ".bias", (size_t)4 * m->hidden));
+    }
+    m->pred_w = host_mat(L, "joint.pred.weight");
+    m->pred_b = L.f32s("joint.pred.bias", m->joint);
+    m->out_w = host_mat(L, "joint.out.weight");
+    m->out_b = L.f32s("joint.out.bias", (size_t)(m->classes + m->durations.size()));
+  }
+  return L.err.empty();
+}
+
+bool load_gigaam(const Gguf &g, Loader &L, wh_model *m, std::string &err) {
+  if (g.string("stt.gigaam.encoder.self_attention_model") != "rotary")
+    return err = "stt.gigaam.encoder.self_attention_model must be \"rotary\"", false;
+  m->relative = false;
+  if (!conformer_config(g, m, "gigaam", err)) return false;
+  m->mels = (int)g.integer("stt.frontend.num_mels", -1);
+  m->theta = (double)g.integer("stt.gigaam.encoder.pos_emb_max_len", 5000);
+  m->conv0 = L.linear({"enc.pre_encode.conv.0"}, true);
+  m->conv2 = L.linear({"enc.pre_encode.conv.2"}, true);
+  bool rnnt = g.string("stt.gigaam.head_kind") == "rnnt";
+  m->head = L.linear({rnnt ? "joint.enc" : "head.ctc"}, true);
+  const Tensor *ht = g.tensor(rnnt ? "joint.enc.weight" : "head.ctc.weight");
+  m->outputs = ht ? (int)ht->dims.back() : 0;
+  m->blank = (int)g.integer("tokenizer.ggml.blank_token_id", -1);
+  m->blocks.resize(m->layers);
+  for (int i = 0; i < m->layers && L.err.empty(); i++) load_block(L, m, i, m->blocks[i]);
+  return L.err.empty();
+}
+
+bool load_whisper(const Gguf &g, Loader &L, wh_model *m, std::string &err) {
+  auto u = [&](const char *k) { return (int)g.integer(std::string("stt.whisper.") + k, -1); };
+  m->d = u("encoder.d_model");
+  m->heads = u("encoder.n_heads");
+  m->layers = u("encoder.n_layers");
+  m->d_ff = u("encoder.ffn_dim");
+  m->dec_heads = u("decoder.n_heads");
+  m->dec_layers = u("decoder.n_layers");
+  m->dec_ff = u("decoder.ffn_dim");
+  m->vocab = u("decoder.vocab_size");
+  m->context = u("decoder.max_target_positions");
+  m->mels = u("encoder.num_mel_bins");
+  m->frames = u("encoder.max_source_positions");
+  int d = m->d;
+  for (int heads : {m->heads, m->dec_heads}) {
+    if (d <= 0 || heads <= 0 || d % heads || d / heads > 64 || (d / heads) % 8)
+      return err = "unsupported shape: d_model " + std::to_string(d) + ", " + std::to_string(heads) + " heads", false;
+  }
+  if (m->frames <= 0 || m->mels <= 0 || m->vocab <= 0 || m->context <= 0) return err = "bad Whisper metadata", false;
+  m->wconv0 = L.linear({"enc.conv.0"}, true, -1, {}, 1);
+  m->wconv1 = L.linear({"enc.conv.1"}, true, -1, {}, 1);
+  m->enc_pos = L.upload(L.f32s("enc.pos_emb.weight", (size_t)d * m->frames));
+  m->wblocks.resize(m->layers);
+  for (int i = 0; i < m->layers && L.err.empty(); i++) {
+    std::string p = "enc.blocks." + std::to_string(i) + ".";
+    WBlock &b = m->wblocks[i];
+    b.norm_attn = L.norm(p + "norm_attn", d, true);
+    b.qkv = L.linear({p + "attn.q", p + "attn.k", p + "attn.v"}, true, 1);
+    b.out = L.linear({p + "attn.out"}, true);
+    b.norm_ffn = L.norm(p + "norm_ffn", d, true);
+    b.fc1 = L.linear({p + "ffn.fc1"}, true);
+    b.fc2 = L.linear({p + "ffn.fc2"}, true);
+  }
+  m->enc_norm = L.norm("enc.final_norm", d, true);
+  m->dl.resize(m->dec_layers);
+  for (int i = 0; i < m->dec_layers && L.err.empty(); i++) {
+    std::string p = "dec.blocks." + std::to_string(i) + ".";
+    DLayer &l = m->dl[i];
+    l.norm_self = L.norm(p + "norm_self", d, true);
+    l.qkv = L.linear({p + "self_attn.q", p + "self_attn.k", p + "self_attn.v"}, true, 1);
+    l.self_out = L.linear({p + "self_attn.out"}, true);
+    l.norm_cross = L.norm(p + "norm_cross", d, true);
+    l.cross_q = L.linear({p + "cross_attn.q"}, true);
+    l.cross_kv = L.linear({p + "cross_attn.k", p + "cross_attn.v"}, true, 0);
+    l.cross_out = L.linear({p + "cross_attn.out"}, true);
+    l.norm_ffn = L.norm(p + "norm_ffn", d, true);
+    l.fc1 = L.linear({p + "ffn.fc1"}, true);
+    l.fc2 = L.linear({p + "ffn.fc2"}, true);
+  }
+  m->dec_norm = L.norm("dec.final_norm", d, true);
+  m->token_embd = L.linear({"dec.token_embd"}, false);
+  m->dec_pos = L.upload(L.f32s("dec.pos_emb.weight", (size_t)d * m->context));
+  return L.err.empty();
+}
+
+// rel_positions (src/conformer.rs:144-153): rows of [sin, cos] pairs from position `first` down.
+std::vector<float> rel_positions(int d, long first, int rows) {
+  std::vector<float> div(d / 2), out((size_t)rows * d);
+  for (int k = 0; k < d / 2; k++) div[k] = std::exp((float)(2 * k) * (-std::log(10000.0f) / (float)d));
+  for (int r = 0; r < rows; r++) {
+    float p = (float)(first - r);
+    for (int k = 0; k < d / 2; k++) {
+      out[(size_t)r * d + 2 * k] = std::sin(p * div[k]);
+      out[(size_t)r * d + 2 * k + 1] = std::cos(p * div[k]);
+    }
+  }
+  return out;
+}
+
+// The GigaAM rope table (src/gigaam/mod.rs:86-97), f64 then f32.
+std::vector<float> rope_table(int frames, int hd, double theta) {
+  std::vector<float> out((size_t)frames * hd);
+  for (int t = 0; t < frames; t++)
+    for (int i = 0; i < hd / 2; i++) {
+      double a = (double)t * std::pow(theta, -2.0 * i / hd);
+      out[(size_t)t * hd + i] = (float)std::cos(a);
+      out[(size_t)t * hd + hd / 2 + i] = (float)std::sin(a);
+    }
+  return out;
+}
+
+int parakeet_frames(int mel_frames) { return half_len(half_len(half_len(mel_frames - 1))); }
+
+// Grows the arena to `frames` encoder frames × `batch` windows (rounded up to 64 frames).
+int arena(wh_model *m, int frames, int batch) {
+  if (frames <= m->cap && batch <= m->cap_batch) return WH_OK;
+  int F = (std::max(frames, m->cap) + 63) / 64 * 64, B = std::max(batch, std::max(m->cap_batch, 1));
+  for (float *p : {m->x, m->y, m->h, m->qk, m->yr, m->pos, m->sub, m->sub2, m->rope})
+    if (p) {
+      wh_free(m->ctx, p);
+      for (auto &o : m->owned)
+        if (o == p) o = nullptr;
+    }
+  if (m->valid_dev) wh_free(m->ctx, m->valid_dev);
+  m->x = m->y = m->h = m->qk = m->yr = m->pos = m->sub = m->sub2 = m->rope = nullptr;
+  m->valid_dev = nullptr;
+  const int d = m->d;
+  const size_t rows = (size_t)F * B;
+  size_t hsz = rows * std::max(m->d_ff, d), qsz = rows * 4 * d, ysz = (size_t)(2 * F + 15 + 64) * d, sub = 0;
+  if (m->arch == PARAKEET) {
+    // The subsampling unchunked: conv2/conv3 outputs (2F + 1) rows of [MELS / 4][ch] per window, and
+    // conv5's [F][MELS / 8][ch].
+    int f2 = half_len(half_len(m->mels)), f = half_len(f2);
+    sub = (size_t)(2 * F + 1) * f2 * m->ch * B;
+    hsz = std::max(hsz, rows * f * m->ch);
+    qsz = std::max(qsz, rows * f * m->ch);
+  } else if (m->arch == GIGAAM) {
+    hsz = std::max(hsz, (size_t)2 * rows * ((5 * m->mels + 31) / 32 * 32));
+    hsz = std::max(hsz, rows * 5 * d);
+    qsz = std::max(qsz, 2 * rows * d);
+  } else {
+    // Whisper: conv columns (2F rows of 3·mels, F rows of 3·d) in qk, conv0's output 2F × d in h.
+    qsz = std::max(qsz, (size_t)2 * F * ((3 * m->mels + 31) / 32 * 32));
+    qsz = std::max(qsz, (size_t)F * 3 * d);
+    hsz = std::max(hsz, (size_t)2 * F * d);
+  }
+  m->x = dev_alloc(m, rows * d);
+  m->y = dev_alloc(m, rows * d);
+  m->h = dev_alloc(m, hsz);
+  m->qk = dev_alloc(m, qsz);
+  m->yr = dev_alloc(m, ysz);
+  m->pos = dev_alloc(m, ysz);
+  if (sub) {
+    m->sub = dev_alloc(m, sub);
+    m->sub2 = dev_alloc(m, sub);
+  }
+  if (wh_alloc(m->ctx, B, (float **)&m->valid_dev)) return WH_EOOM;
+  if (!m->x || !m->y || !m->h || !m->qk || !m->yr || !m->pos || (sub && (!m->sub || !m->sub2)))
+    return wh_fail(m->ctx, WH_EOOM, "arena of %d frames x %d windows: out of device memory", F, B);
+  if (m->arch == PARAKEET) {
+    // The sinusoidal table for F frames stays on the device; a call over t frames reads its
+    // pos_rows(t) rows from row F − t (src/parakeet/encoder.rs:93, :129-131).
+    auto table = rel_positions(d, (long)F + 15, 2 * F + 15);
+    CK(wh_write(m->ctx, m->pos, table.data(), table.size() * 4));
+  } else if (m->arch == GIGAAM) {
+    int hd = d / m->heads;
+    auto t = rope_table(F, hd, m->theta);
+    m->rope = dev_alloc(m, t.size());
+    if (!m->rope) return WH_EOOM;
+    CK(wh_write(m->ctx, m->rope, t.data(), t.size() * 4));
+  }
+  m->cap = F;
+  m->cap_batch = B;
+  return WH_OK;
+}
+
+// Conformer Block::record (src/conformer.rs:232-265) over `batch` windows of t frames in x; the
+// block's output goes to y.  `valid_dev` (or none) masks keys and conv inputs per window.
+int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int batch, const int *valid_dev) {
+  wh_ctx *c = m->ctx;
+  const int d = m->d, hd = d / m->heads, rows = t * batch;
+  CK(launch_layer_norm(c, x, k.norm_ff1.w, k.norm_ff1.b, y, rows, d, nullptr, nullptr, 0));
+  CK(launch_gemm(c, y, k.ff1[0], m->h, rows, k.ff1[0]->cols + k.ff1[0]->dual, WH_SILU, 0.0f));
+  CK(launch_gemm(c, m->h, k.ff1[1], x, rows, k.ff1[1]->cols + k.ff1[1]->dual, WH_RESIDUAL, 0.5f));
+  if (!m->relative) {
+    CK(launch_layer_norm(c, x, k.norm_attn.w, k.norm_attn.b, y, rows, d, m->rope, m->yr, hd));
+    CK(launch_gemm(c, m->yr, k.qk, m->qk, rows, k.qk->cols + k.qk->dual, WH_BIAS, 0.0f));
+    CK(launch_gemm(c, y, k.v, m->h, rows, k.v->cols + k.v->dual, WH_BIAS, 0.0f));
+    CK(launch_attention(c, m->qk, m->h, nullptr, y, t, m->heads, hd, valid_dev, t, batch));
+  } else {
+    const int pr = 2 * t + 15;
+    CK(launch_layer_norm(c, x, k.norm_attn.w, k.norm_attn.b, y, rows, d, nullptr, nullptr, 0));
+    CK(launch_gemm(c, y, k.qkv, m->qk, rows, k.qkv->cols + k.qkv->dual, WH_BIAS, 0.0f));
+    CK(launch_gemm(c, m->pos_cur, k.pos, m->yr, pr, k.pos->cols + k.pos->dual, WH_BIAS, 0.0f));
+    CK(launch_attention(c, m->qk, nullptr, m->yr, y, t, m->heads, hd, valid_dev, t, batch));
+  }
+  CK(launch_gemm(c, y, k.out, x, rows, k.out->cols + k.out->dual, WH_RESIDUAL, 1.0f));
+  CK(launch_layer_norm(c, x, k.norm_conv.w, k.norm_conv.b, y, rows, d, nullptr, nullptr, 0));
+  CK(launch_gemm(c, y, k.pw1, m->qk, rows, k.pw1->cols + k.pw1->dual, WH_BIAS, 0.0f));
+  CK(launch_conv_glu(c, m->qk, k.dw.w, k.dw.b, m->kernel, k.conv_norm.w, k.conv_norm.b, m->layer_norm_conv, y, t, d,
+                     valid_dev, t, batch));
+  CK(launch_gemm(c, y, k.pw2, x, rows, k.pw2->cols + k.pw2->dual, WH_RESIDUAL, 1.0f));
+  CK(launch_layer_norm(c, x, k.norm_ff2.w, k.norm_ff2.b, y, rows, d, nullptr, nullptr, 0));
+  CK(launch_gemm(c, y, k.ff2[0], m->h, rows, k.ff2[0]->cols + k.ff2[0]->dual, WH_SILU, 0.0f));
+  CK(launch_gemm(c, m->h, k.ff2[1], x, rows, k.ff2[1]->cols + k.ff2[1]->dual, WH_RESIDUAL, 0.5f));
+  // The block output is norm_out(x), not the residual stream.
+  return launch_layer_norm(c, x, k.norm_out.w, k.norm_out.b, y, rows, d, nullptr, nullptr, 0);
+}
+
+}  // namespace
+
+namespace {
+
+// Conformer::record (src/conformer.rs:107-116): `layers` blocks from m->x, output in m->x.
+int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layers) {
+  for (int i = 0; i < layers; i++) {
+    CK(record_block(m, m->blocks[i], m->x, m->y, t, batch, valid_dev));
+    std::swap(m->x, m->y);
+  }
+  return WH_OK;
+}
+
+int lin(wh_model *m, const float *a, const wh_linear *l, float *c, int rows, int epi, float alpha = 0.0f) {
+  return launch_gemm(m->ctx, a, l, c, rows, l->cols + l->dual, epi, alpha);
+}
+
+// Parakeet Encoder::record (src/parakeet/encoder.rs:103-124) over `batch` windows of mel_frames
+// [batch][mel_frames][mels]; window b's first valid[b] mel frames are real.  One window: kestrel
+// masking as the reference (conv0/conv2 see the valid frames, conv5 the whole image).  Several
+// windows: each is subsampled as if alone (conv5 sees its own valid image rows), and its keys and
+// conv inputs past its own encoder frames are masked.
+int parakeet_encode(wh_model *m, const float *mel, int batch, int mel_frames, const int *valid, float *out) {
+  const int mels = m->mels, ch = m->ch, d = m->d;
+  const int t2 = half_len(half_len(mel_frames)), f2 = half_len(half_len(mels));
+  const int t = parakeet_frames(mel_frames), f = half_len(f2);
+  if (mel_frames < 3 || t < 1) return fail(m, "too few mel frames");
+  CK(arena(m, t, batch));
+  m->pos_cur = m->pos + (size_t)(m->cap - t) * d;
+  wh_ctx *c = m->ctx;
+  const int rows1 = 2 * t + 1;  // conv2's output rows from −1 on
+  const size_t per = (size_t)rows1 * f2 * ch;
+  std::vector<int> enc_valid(batch);
+  for (int b = 0; b < batch; b++) {
+    int v = std::min(std::max(valid[b], 1), mel_frames);
+    CK(launch_depthwise(c, mel + (size_t)b * mel_frames * mels, m->sc0.w, m->sc0.b, m->sc2.w, m->sc2.b,
+                        m->sub + per * b, v, mels, ch, 0, rows1));
+    enc_valid[b] = batch == 1 ? t : std::min(t, parakeet_frames(std::max(v, 3)));
+  }
+  CK(lin(m, m->sub, m->conv3, m->sub2, rows1 * f2 * batch, WH_RELU));
+  for (int b = 0; b < batch; b++) {
+    int img = batch == 1 ? t2 : half_len(half_len(std::min(std::max(valid[b], 1), mel_frames)));
+    CK(launch_depthwise(c, m->sub2 + per * b, nullptr, nullptr, m->sc5.w, m->sc5.b, m->h + (size_t)b * t * f * ch,
+                        img, f2, ch, 0, t));
+  }
+  CK(lin(m, m->h, m->conv6, m->qk, t * f * batch, WH_RELU));
+  CK(launch_flatten(c, m->qk, m->h, t * batch, f, ch));
+  CK(lin(m, m->h, m->pre_out, m->x, t * batch, WH_BIAS));
+  const int *vd = nullptr;
+  if (batch > 1) {
+    hipError_t e = hipMemcpyAsync(m->valid_dev, enc_valid.data(), sizeof(int) * batch, hipMemcpyHostToDevice, c->stream);
+    if (e != hipSuccess) return wh_fail(c, WH_EGPU, "valid lengths: %s", hipGetErrorString(e));
+    e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return wh_fail(c, WH_EGPU, "valid lengths: %s", hipGetErrorString(e));
+    vd = m->valid_dev;
+  }
+  CK(record_blocks(m, t, batch, vd, m->layers));
+  return lin(m, m->x, m->joint_enc, out, t * batch, WH_BIAS);
+}
+
+// GigaAM Encoder::record (src/gigaam/encoder.rs:83-93).
+int gigaam_encode(wh_model *m, const float *mel, int mel_frames, float *out) {
+  const int t1 = half_len(mel_frames), t = half_len(t1), d = m->d;
+  if (mel_frames < 5) return fail(m, "too few mel frames");
+  CK(arena(m, t1, 1));
+  wh_ctx *c = m->ctx;
+  CK(launch_im2col(c, mel, m->h, mel_frames, m->mels, 5, 2, 2, 1, 0, 0));
+  CK(lin(m, m->h, m->conv0, m->qk, t1, WH_RELU));
+  CK(launch_im2col(c, m->qk, m->h, t1, d, 5, 2, 2, 1, 0, 0));
+  CK(lin(m, m->h, m->conv2, m->x, t, WH_RELU));
+  CK(record_blocks(m, t, 1, nullptr, m->layers));
+  return lin(m, m->x, m->head, out, t, WH_BIAS);
+}
+
+// Whisper Encoder::record (src/whisper/encoder.rs:67-74; transformer.rs:122-138) into out [t][d].
+int whisper_encode(wh_model *m, const float *mel, int mel_frames, float *out) {
+  const int t = m->frames, d = m->d, hd = d / m->heads;
+  if (mel_frames != 2 * t) return fail(m, "Whisper takes windows of " + std::to_string(2 * t) + " mel frames");
+  CK(arena(m, t, 1));
+  wh_ctx *c = m->ctx;
+  CK(launch_im2col(c, mel, m->qk, 2 * t, m->mels, 3, 1, 1, 1, 0, 0));
+  CK(lin(m, m->qk, m->wconv0, m->h, 2 * t, WH_GELU));
+  CK(launch_im2col(c, m->h, m->qk, 2 * t, d, 3, 2, 1, 1, 0, 0));
+  CK(wh_copy(c, m->x, m->enc_pos, (size_t)t * d * 4));
+  CK(lin(m, m->qk, m->wconv1, m->x, t, WH_GELU_RESIDUAL));
+  for (const WBlock &b : m->wblocks) {
+    CK(launch_layer_norm(c, m->x, b.norm_attn.w, b.norm_attn.b, m->y, t, d, nullptr, nullptr, 0));
+    CK(lin(m, m->y, b.qkv, m->qk, t, WH_BIAS));
+    CK(launch_attention(c, m->qk, nullptr, nullptr, m->y, t, m->heads, hd, nullptr, t, 1));
+    CK(lin(m, m->y, b.out, m->x, t, WH_RESIDUAL, 1.0f));
+    CK(launch_layer_norm(c, m->x, b.norm_ffn.w, b.norm_ffn.b, m->y, t, d, nullptr, nullptr, 0));
+    CK(lin(m, m->y, b.fc1, m->h, t, WH_GELU));
+    CK(lin(m, m->h, b.fc2, m->x, t, WH_RESIDUAL, 1.0f));
+  }
+  return launch_layer_norm(c, m->x, m->enc_norm.w, m->enc_norm.b, out, t, d, nullptr, nullptr, 0);
+}
+
+// dot (src/cpu/mod.rs:20-43): 16 fused lanes summed pairwise, then the tail.
+float dot16(const float *a, const float *b, int n) {
+  float acc[16] = {0};
+  int n16 = n / 16 * 16;
+  for (int i = 0; i < n16; i += 16)
+    for (int l = 0; l < 16; l++) acc[l] = std::fma(a[i + l], b[i + l], acc[l]);
+  for (int w = 8; w >= 1; w >>= 1)
+    for (int l = 0; l < w; l++) acc[l] += acc[l + w];
+  float tail = 0.0f;
+  for (int i = n16; i < n; i++) tail += a[i] * b[i];
+  return acc[0] + tail;
+}
+
+void matvec(const HostMat &w, const float *x, float *out) {
+  for (int r = 0; r < w.rows; r++) out[r] = dot16(&w.w[(size_t)r * w.k], x, w.k);
+}
+
+int argmax_first(const float *v, int n) {
+  int best = 0;
+  for (int i = 1; i < n; i++)
+    if (v[i] > v[best]) best = i;
+  return best;
+}
+
+// Decoder::predict (src/parakeet/decoder.rs:111-133).
+void predict(const wh_model *m, int token, const std::vector<float> &state, std::vector<float> &next,
+             std::vector<float> &pred) {
+  const int n = m->hidden;
+  std::vector<float> x(n, 0.0f), gx(4 * n), gh(4 * n);
+  if (token >= 0) x.assign(m->embed_h.w.begin() + (size_t)token * m->embed_h.k,
+                           m->embed_h.w.begin() + (size_t)(token + 1) * m->embed_h.k);
+  for (int l = 0; l < m->lstm_layers; l++) {
+    const float *h = &state[(size_t)2 * n * l], *cc = h + n;
+    float *nh = &next[(size_t)2 * n * l], *nc = nh + n;
+    matvec(m->wx[l], x.data(), gx.data());
+    matvec(m->wh[l], h, gh.data());
+    const float *bb = m->lstm_b[l].data();
+    auto sig = [](float v) { return 1.0f / (1.0f + std::exp(-v)); };
+    for (int k = 0; k < n; k++) {
+      float ig = gx[k] + gh[k] + bb[k], fg = gx[n + k] + gh[n + k] + bb[n + k];
+      float gg = gx[2 * n + k] + gh[2 * n + k] + bb[2 * n + k], og = gx[3 * n + k] + gh[3 * n + k] + bb[3 * n + k];
+      nc[k] = sig(fg) * cc[k] + sig(ig) * std::tanh(gg);
+      nh[k] = sig(og) * std::tanh(nc[k]);
+    }
+    x.assign(nh, nh + n);
+  }
+  pred.resize(m->joint);
+  matvec(m->pred_w, x.data(), pred.data());
+  for (int j = 0; j < m->joint; j++) pred[j] = pred[j] + m->pred_b[j];
+}
+
+// TDT greedy (src/parakeet/decoder.rs:91-103, loop :158-191).
+int tdt_greedy(const wh_model *m, const float *enc, int frames, int width, uint32_t *out, int cap) {
+  const int S = 2 * m->lstm_layers * m->hidden, nd = (int)m->durations.size(), outs = m->classes + nd;
+  std::vector<float> state(S, 0.0f), next(S, 0.0f), pred, z(m->joint), logits(outs);
+  predict(m, -1, state, next, pred);
+  int count = 0, t = 0, symbols = 0, emitted = -1;
+  long left = m->global ? (long)m->max_symbols * frames : -1;
+  while (t < frames && left != 0) {
+    if (emitted >= 0) {
+      state = next;
+      predict(m, emitted, state, next, pred);
+    }
+    const float *e = enc + (size_t)t * width;
+    for (int j = 0; j < m->joint; j++) z[j] = std::max(e[j] + pred[j], 0.0f);
+    matvec(m->out_w, z.data(), logits.data());
+    for (int i = 0; i < outs; i++) logits[i] = logits[i] + m->out_b[i];
+    int token = argmax_first(logits.data(), m->classes), di = argmax_first(logits.data() + m->classes, nd);
+    emitted = -1;
+    if (token != m->blank) {
+      if (count < cap) {
+        out[2 * count] = (uint32_t)token;
+        out[2 * count + 1] = (uint32_t)t;
+      }
+      count++;
+      emitted = token;
+    }
+    int dur = m->durations[di];
+    if (m->global) {
+      left--;
+      t += token == m->blank ? std::max(dur, 1) : dur;
+      continue;
+    }
+    t += dur;
+    symbols++;
+    if (dur != 0) symbols = 0;
+    else if (symbols >= m->max_symbols || token == m->blank) {
+      t++;
+      symbols = 0;
+    }
+  }
+  return count;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wh_model_load(wh_ctx *ctx, const char *path, wh_model **out) {
+  if (!ctx || !path || !out) return wh_fail(ctx, WH_EARG, "wh_model_load: bad arguments");
+  *out = nullptr;
+  auto m = std::make_unique<wh_model>();
+  m->ctx = ctx;
+  m->g = std::make_unique<Gguf>();
+  std::string err;
+  if (!m->g->open(path, err)) return wh_fail(ctx, WH_EARG, "%s", err.c_str());
+  const Gguf &g = *m->g;
+  Loader L(ctx, g);
+  std::string arch = g.string("general.architecture");
+  bool ok;
+  if (arch == "gigaam") m->arch = GIGAAM, ok = load_gigaam(g, L, m.get(), err);
+  else if (arch == "parakeet") m->arch = PARAKEET, ok = load_parakeet(g, L, m.get(), err);
+  else if (arch == "whisper") m->arch = WHISPER, ok = load_whisper(g, L, m.get(), err);
+  else ok = false, err = "unsupported general.architecture \"" + arch + "\"";
+  m->owned = L.owned;
+  m->linears = L.linears;
+  if (!ok || !L.err.empty()) {
+    std::string msg = err.empty() ? L.err : err;
+    wh_model_free(m.release());
+    return wh_fail(ctx, msg.find("memory") != std::string::npos ? WH_EOOM : WH_EARG, "%s", msg.c_str());
+  }
+  *out = m.release();
+  return WH_OK;
+}
+
+void wh_model_free(wh_model *m) {
+  if (!m) return;
+  for (float *p : m->owned)
+    if (p) wh_free(m->ctx, p);
+  if (m->valid_dev) wh_free(m->ctx, m->valid_dev);
+  for (wh_linear *l : m->linears) wh_linear_free(m->ctx, l);
+  for (uint32_t *p : m->own) wh_free(m->ctx, p);
+  for (uint32_t *p : m->cross) wh_free(m->ctx, p);
+  if (m->ids) wh_free(m->ctx, m->ids);
+  delete m;
+}
+
+int wh_model_info(const wh_model *m, int *arch, int *d, int *layers, int *mels, int *width) {
+  if (!m) return WH_EARG;
+  if (arch) *arch = (int)m->arch;
+  if (d) *d = m->d;
+  if (layers) *layers = m->layers;
+  if (mels) *mels = m->mels;
+  if (width) {
+    switch (m->arch) {
+      case GIGAAM: *width = wh_linear_width(m->head); break;
+      case PARAKEET: *width = wh_linear_width(m->joint_enc); break;
+      default: *width = m->d;
+    }
+  }
+  return WH_OK;
+}
+
+int wh_model_frames(const wh_model *m, int mel_frames, int *frames, int *width) {
+  if (!m || mel_frames <= 0) return WH_EARG;
+  int f = 0;
+  switch (m->arch) {
+    case GIGAAM: f = half_len(half_len(mel_frames)); break;
+    case PARAKEET: f = mel_frames >= 3 ? parakeet_frames(mel_frames) : 0; break;
+    default: f = m->frames;
+  }
+  if (frames) *frames = f;
+  return wh_model_info(m, nullptr, nullptr, nullptr, nullptr, width);
+}
+
+int wh_model_encode(wh_model *m, const float *mel, int mel_frames, int valid, float *out) {
+  if (!m || !mel || !out || mel_frames <= 0) return WH_EARG;
+  hipSetDevice(m->ctx->device);
+  switch (m->arch) {
+    case GIGAAM: return gigaam_encode(m, mel, mel_frames, out);
+    case PARAKEET: {
+      int v = valid <= 0 || valid > mel_frames ? mel_frames : valid;
+      return parakeet_encode(m, mel, 1, mel_frames, &v, out);
+    }
+    default: return whisper_encode(m, mel, mel_frames, out);
+  }
+}
+
+int wh_model_encode_batch(wh_model *m, const float *mel, int batch, int mel_frames, const int *valid, float *out) {
+  if (!m || !mel || !out || !valid || batch <= 0 || mel_frames <= 0) return WH_EARG;
+  if (m->arch != PARAKEET) return wh_fail(m->ctx, WH_EARG, "batched windows are built for the Parakeet encoder");
+  hipSetDevice(m->ctx->device);
+  return parakeet_encode(m, mel, batch, mel_frames, valid, out);
+}
+
+int wh_model_blocks(wh_model *m, float *x, int t, int layers) {
+  if (!m || !x || t <= 0 || layers < 0 || layers > m->layers || m->arch == WHISPER) return WH_EARG;
+  CK(arena(m, t, 1));
+  if (m->arch == PARAKEET) m->pos_cur = m->pos + (size_t)(m->cap - t) * m->d;
+  CK(wh_copy(m->ctx, m->x, x, (size_t)t * m->d * 4));
+  CK(record_blocks(m, t, 1, nullptr, layers));
+  return wh_copy(m->ctx, x, m->x, (size_t)t * m->d * 4);
+}
+
+int wh_model_greedy(wh_model *m, const float *enc, int frames, int width, uint32_t *out, int cap) {
+  if (!m || !enc || frames < 0 || width <= 0 || !out || cap < 0) return WH_EARG;
+  if (m->arch == GIGAAM) {
+    if (width < m->outputs) return WH_EARG;
+    // Greedy CTC (src/gigaam/decoder.rs:135-151) over the first `outputs` columns.
+    int count = 0, prev = -1;
+    for (int t = 0; t < frames; t++) {
+      int best = argmax_first(enc + (size_t)t * width, m->outputs);
+      if (prev != best && best != m->blank) {
+        if (count < cap) {
+          out[2 * count] = (uint32_t)best;
+          out[2 * count + 1] = (uint32_t)t;
+        }
+        count++;
+      }
+      prev = best;
+    }
+    return count;
+  }
+  if (m->arch == PARAKEET) {
+    if (m->embed_h.rows == 0 || width < m->joint) return wh_fail(m->ctx, WH_EARG, "model has no TDT decoder");
+    return tdt_greedy(m, enc, frames, width, out, cap);
+  }
+  return wh_fail(m->ctx, WH_EARG, "Whisper decodes through wh_whisper_step");
+}
+
+int wh_whisper_begin(wh_model *m, const float *enc, int frames) {
+  if (!m || !enc || frames <= 0 || m->arch != WHISPER) return WH_EARG;
+  const int d = m->d;
+  wh_ctx *c = m->ctx;
+  if (m->own.empty()) {
+    for (int i = 0; i < m->dec_layers; i++) {
+      float *a = nullptr, *b = nullptr;
+      CK(wh_alloc(c, (size_t)m->context * d, &a));
+      CK(wh_alloc(c, (size_t)m->frames * d, &b));
+      m->own.push_back((uint32_t *)a);
+      m->cross.push_back((uint32_t *)b);
+    }
+    size_t vp = (size_t)(m->vocab % 32 == 0 ? m->vocab : (m->vocab + 63) / 64 * 64);
+    m->dx = dev_alloc(m, d);
+    m->dy = dev_alloc(m, d);
+    m->dqkv = dev_alloc(m, 3 * (size_t)d);
+    m->dh = dev_alloc(m, (size_t)m->dec_ff);
+    m->datt = dev_alloc(m, d);
+    m->dpart = dev_alloc(m, wh_attend_len(std::max(m->frames, m->context), m->dec_heads, d / m->dec_heads));
+    m->dscratch = dev_alloc(m, (size_t)m->frames * 2 * d);
+    float *ids = nullptr;
+    CK(wh_alloc(c, 1, &ids));
+    m->ids = (uint32_t *)ids;
+    (void)vp;
+    if (!m->dx || !m->dy || !m->dqkv || !m->dh || !m->datt || !m->dpart || !m->dscratch) return WH_EOOM;
+  }
+  if (frames > m->frames) return WH_EARG;
+  // Decoder::record_cross (src/transformer.rs:243-248).
+  for (int i = 0; i < m->dec_layers; i++) {
+    CK(lin(m, enc, m->dl[i].cross_kv, m->dscratch, frames, WH_BIAS));
+    CK(launch_pack(c, m->dscratch, 0, 2 * d, m->cross[i], frames, d, frames, 0));
+  }
+  m->cross_frames = frames;
+  return WH_OK;
+}
+
+int wh_whisper_step(wh_model *m, int token, int pos, float *logits) {
+  if (!m || m->arch != WHISPER || !logits || m->own.empty() || pos < 0 || pos >= m->context || token < 0 ||
+      token >= m->vocab)
+    return WH_EARG;
+  const int d = m->d, heads = m->dec_heads, hd = d / heads;
+  wh_ctx *c = m->ctx;
+  uint32_t tok = (uint32_t)token;
+  hipError_t e = hipMemcpyAsync(m->ids, &tok, 4, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return wh_fail(c, WH_EGPU, "token: %s", hipGetErrorString(e));
+  // Decoder::record_step (src/transformer.rs:254-290).
+  CK(launch_embed(c, m->token_embd, m->dec_pos, m->dx, m->ids, 0, pos * d));
+  for (int i = 0; i < m->dec_layers; i++) {
+    const DLayer &l = m->dl[i];
+    CK(launch_layer_norm(c, m->dx, l.norm_self.w, l.norm_self.b, m->dy, 1, d, nullptr, nullptr, 0));
+    CK(launch_gemv(c, m->dy, l.qkv, m->dqkv, WH_BIAS, 0.0f, 0));
+    CK(launch_pack(c, m->dqkv, d, 0, m->own[i], 1, d, m->context, pos));
+    CK(launch_attend(c, m->dqkv, m->own[i], m->dpart, m->datt, pos + 1, m->context, heads, hd));
+    CK(launch_gemv(c, m->datt, l.self_out, m->dx, WH_RESIDUAL, 1.0f, 0));
+    CK(launch_layer_norm(c, m->dx, l.norm_cross.w, l.norm_cross.b, m->dy, 1, d, nullptr, nullptr, 0));
+    CK(launch_gemv(c, m->dy, l.cross_q, m->dqkv, WH_BIAS, 0.0f, 0));
+    CK(launch_attend(c, m->dqkv, m->cross[i], m->dpart, m->datt, m->cross_frames, m->cross_frames, heads, hd));
+    CK(launch_gemv(c, m->datt, l.cross_out, m->dx, WH_RESIDUAL, 1.0f, 0));
+    CK(launch_layer_norm(c, m->dx, l.norm_ffn.w, l.norm_ffn.b, m->dy, 1, d, nullptr, nullptr, 0));
+    CK(launch_gemv(c, m->dy, l.fc1, m->dh, WH_GELU, 0.0f, 0));
+    CK(launch_gemv(c, m->dh, l.fc2, m->dx, WH_RESIDUAL, 1.0f, 0));
+  }
+  CK(launch_layer_norm(c, m->dx, m->dec_norm.w, m->dec_norm.b, m->dy, 1, d, nullptr, nullptr, 0));
+  return launch_gemv(c, m->dy, m->token_embd, logits, WH_BIAS, 0.0f, 0);
+}
+
+}  // extern "C"

@@ -1,0 +1,381 @@
+// Row-wise and convolution side kernels of the encoders over time-major [t][ch] f32 activations:
+// LayerNorm (+RoPE), im2col, the Conformer conv module's middle (GLU, depthwise conv, norm, SiLU),
+// Parakeet's 3×3 stride-2 subsampling convs and flatten, argmax, and fills.  Semantics follow
+// src/gpu/ops.wgsl and src/gpu/spatial.wgsl (cited per kernel); the layout is one wavefront per row
+// (64 lanes over the channels, reductions by cross-lane shuffles) instead of a 256-thread
+// workgroup per row, so a row's data stays in registers and short rows keep every lane busy.
+#include "internal.h"
+
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+constexpr int ROW_REGS = 32;  // row values per lane held in registers: rows up to 2048
+
+// LayerNorm (eps 1e-5) of row `row`, one wavefront per row; with a table, the NEOX split-half RoPE
+// of each head into yr (ops.wgsl:44-95; src/cpu/ops.rs:68-110).
+__global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict__ x, const float *__restrict__ g,
+                                                         const float *__restrict__ b, float *__restrict__ y,
+                                                         int rows, int cols, const float *__restrict__ table,
+                                                         float *__restrict__ yr, int hd) {
+  extern __shared__ float srow[];  // 4 rows of cols (RoPE only)
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = blockIdx.x * 4 + w;
+  const bool active = row < rows;
+  float *sr = srow + w * cols;
+  if (active) {
+    const float *xr = x + (size_t)row * cols;
+    float v[ROW_REGS];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < ROW_REGS; j++) {
+      int i = lane + 64 * j;
+      v[j] = i < cols ? xr[i] : 0.0f;
+      s += v[j];
+    }
+    const float mean = wave_sum(s) / (float)cols;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < ROW_REGS; j++) {
+      int i = lane + 64 * j;
+      float d = i < cols ? v[j] - mean : 0.0f;
+      q += d * d;
+    }
+    const float rstd = rsqrtf(wave_sum(q) / (float)cols + 1e-5f);
+    float *yy = y + (size_t)row * cols;
+#pragma unroll
+    for (int j = 0; j < ROW_REGS; j++) {
+      int i = lane + 64 * j;
+      if (i < cols) {
+        float o = (v[j] - mean) * rstd * g[i] + b[i];
+        yy[i] = o;
+        if (table) sr[i] = o;
+      }
+    }
+  }
+  if (!table) return;  // uniform across the workgroup
+  __syncthreads();
+  if (!active) return;
+  const int half = hd / 2;
+  const float *tr = table + (size_t)row * hd;
+  float *out = yr + (size_t)row * cols;
+  for (int i = lane; i < cols; i += 64) {
+    int d = i % hd, f = d % half;
+    float c = tr[f], sn = tr[half + f];
+    out[i] = d < half ? sr[i] * c - sr[i + half] * sn : sr[i] * c + sr[i - half] * sn;
+  }
+}
+
+// Same for rows longer than ROW_REGS·64: the row is read three times.
+__global__ __launch_bounds__(64) void layer_norm_long(const float *__restrict__ x, const float *__restrict__ g,
+                                                      const float *__restrict__ b, float *__restrict__ y, int cols) {
+  const int lane = threadIdx.x;
+  const float *xr = x + (size_t)blockIdx.x * cols;
+  float s = 0.0f;
+  for (int i = lane; i < cols; i += 64) s += xr[i];
+  const float mean = wave_sum(s) / (float)cols;
+  float q = 0.0f;
+  for (int i = lane; i < cols; i += 64) {
+    float d = xr[i] - mean;
+    q += d * d;
+  }
+  const float rstd = rsqrtf(wave_sum(q) / (float)cols + 1e-5f);
+  float *yy = y + (size_t)blockIdx.x * cols;
+  for (int i = lane; i < cols; i += 64) yy[i] = (xr[i] - mean) * rstd * g[i] + b[i];
+}
+
+// im2col (ops.wgsl:97-119): col[i][c·kernel + k] = x[stride·i + k − pad][c], zero-padded to
+// `width` (a multiple of 32).  blockIdx.z is the batch item.
+__global__ void im2col_kernel(const float *__restrict__ x, float *__restrict__ col, int t, int ch, int kernel,
+                              int stride, int pad, int rows, int width, long xs, long cs) {
+  const int i = blockIdx.y;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= width || i >= rows) return;
+  x += xs * blockIdx.z;
+  col += cs * blockIdx.z;
+  float v = 0.0f;
+  int s = stride * i + e % kernel;
+  if (e < ch * kernel && s >= pad && s - pad < t) v = x[(size_t)(s - pad) * ch + e / kernel];
+  col[(size_t)i * width + e] = v;
+}
+
+// The Conformer conv module between the pointwise convs (ops.wgsl:121-164; src/cpu/ops.rs:137-182),
+// one wavefront per frame: h [t][2ch] → GLU x·σ(gate) (zero from the window's valid frames on) →
+// depthwise conv (odd kernel, centred, w [ch][kernel]) + bias → LayerNorm or affine → SiLU.
+// Frames are [batch][t]; the conv does not cross windows.
+__global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__ h, const float *__restrict__ w,
+                                                       const float *__restrict__ wb, int kernel,
+                                                       const float *__restrict__ g, const float *__restrict__ gb,
+                                                       int layer_norm, float *__restrict__ y, int t, int ch,
+                                                       const int *__restrict__ valid_dev, int valid, int frames) {
+  const int lane = threadIdx.x & 63;
+  const int f = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (f >= frames) return;
+  const int seg = f / t, i = f % t;
+  const int lim = valid_dev ? min(valid_dev[seg], t) : min(valid, t);
+  const int pad = kernel / 2;
+  const float *hs = h + (size_t)seg * t * 2 * ch;
+  float acc[16];
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    int c = lane + 64 * j;
+    float a = 0.0f;
+    if (c < ch) {
+      a = wb[c];
+      for (int k = 0; k < kernel; k++) {
+        int src = i + k - pad;
+        if (src < 0 || src >= lim) continue;
+        const float *r = hs + (size_t)src * 2 * ch;
+        a += w[c * kernel + k] * (r[c] / (1.0f + __expf(-r[ch + c])));
+      }
+    }
+    acc[j] = a;
+    s += a;
+  }
+  float mean = 0.0f, rstd = 1.0f;
+  if (layer_norm) {
+    mean = wave_sum(s) / (float)ch;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      int c = lane + 64 * j;
+      float d = c < ch ? acc[j] - mean : 0.0f;
+      q += d * d;
+    }
+    rstd = rsqrtf(wave_sum(q) / (float)ch + 1e-5f);
+  }
+  float *yy = y + (size_t)f * ch;
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    int c = lane + 64 * j;
+    if (c < ch) {
+      float v = (acc[j] - mean) * rstd * g[c] + gb[c];
+      yy[c] = v / (1.0f + __expf(-v));
+    }
+  }
+}
+
+__host__ __device__ __forceinline__ int half_len(int n) { return (n - 1) / 2 + 1; }
+
+// Depthwise 3×3 stride-2 pad-1 conv + bias over the image [t][f][ch]; x holds rows 2·t0 − 1..;
+// output rows t0 + blockIdx.y of y [⌈t/2⌉][⌈f/2⌉][ch] (spatial.wgsl:31-48).
+__global__ void depthwise_kernel(const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ b,
+                                 float *__restrict__ y, int t, int f, int ch, int t0) {
+  const int fo = blockIdx.x, k = blockIdx.y, fh = half_len(f);
+  for (int c = threadIdx.x; c < ch; c += blockDim.x) {
+    float acc = b[c];
+    for (int i = 0; i < 3; i++) {
+      int ti = 2 * (t0 + k) + i;
+      for (int j = 0; j < 3; j++) {
+        int fi = 2 * fo + j;
+        if (ti >= 1 && ti <= t && fi >= 1 && fi <= f)
+          acc += w[(i * 3 + j) * ch + c] * x[((size_t)(2 * k + i) * f + fi - 1) * ch + c];
+      }
+    }
+    y[((size_t)(t0 + k) * fh + fo) * ch + c] = acc;
+  }
+}
+
+// conv0 (1 → ch, 3×3 s2 p1) + ReLU, never stored, then the depthwise conv2 + bias, into row
+// blockIdx.y of a chunk (output row 2·t0 − 1 + blockIdx.y; rows from ⌈t/4⌉ on zero, as masked)
+// (spatial.wgsl:50-107; src/parakeet/cpu.rs:103-152).  The 7×7 input patch goes to LDS first.
+__global__ void first_depthwise_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                       const float *__restrict__ b, float *__restrict__ y,
+                                       const float *__restrict__ w0, const float *__restrict__ b0, int t,
+                                       int f, int ch, int t0) {
+  __shared__ float x7[49];
+  const int t1 = half_len(t), f1 = half_len(f), f2 = half_len(f1);
+  const int r = 2 * t0 + blockIdx.y;  // output row + 1
+  const int fo = blockIdx.x;
+  const int lid = threadIdx.x;
+  if (lid < 49) {
+    int tm = 4 * r + lid / 7 - 7, fm = 4 * fo + lid % 7 - 3;
+    x7[lid] = (tm >= 0 && tm < t && fm >= 0 && fm < f) ? x[(size_t)tm * f + fm] : 0.0f;
+  }
+  __syncthreads();
+  const bool masked = r > half_len(t1);
+  for (int c = lid; c < ch; c += blockDim.x) {
+    float a[9];
+#pragma unroll
+    for (int q = 0; q < 9; q++) a[q] = w0[q * ch + c];
+    float acc = b[c];
+    for (int i = 0; i < 3; i++) {
+      int ti = 2 * r + i - 2;
+      for (int j = 0; j < 3; j++) {
+        int fi = 2 * fo + j;
+        if (ti >= 1 && ti <= t1 && fi >= 1 && fi <= f1) {
+          int o = 14 * i + 2 * j;
+          float v = b0[c];
+          v += a[0] * x7[o];
+          v += a[1] * x7[o + 1];
+          v += a[2] * x7[o + 2];
+          v += a[3] * x7[o + 7];
+          v += a[4] * x7[o + 8];
+          v += a[5] * x7[o + 9];
+          v += a[6] * x7[o + 14];
+          v += a[7] * x7[o + 15];
+          v += a[8] * x7[o + 16];
+          acc += w[(i * 3 + j) * ch + c] * fmaxf(v, 0.0f);
+        }
+      }
+    }
+    y[((size_t)blockIdx.y * f2 + fo) * ch + c] = masked ? 0.0f : acc;
+  }
+}
+
+// [t][f][ch] → [t][ch·f] (spatial.wgsl:112-119).
+__global__ void flatten_kernel(const float *__restrict__ x, float *__restrict__ y, int f, int ch) {
+  const int n = f * ch;
+  const float *xr = x + (size_t)blockIdx.x * n;
+  float *yr = y + (size_t)blockIdx.x * n;
+  for (int e = threadIdx.x; e < n; e += blockDim.x) yr[e] = xr[(e % f) * ch + e / f];
+}
+
+// Index of the first maximum of x[..n] (ops.wgsl:266-287), one workgroup.
+__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ x, uint32_t *out, int n) {
+  __shared__ float bv[4];
+  __shared__ int bi[4];
+  float best = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    float v = x[i];
+    if (v > best || (v == best && i < idx)) best = v, idx = i;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(best, o, 64);
+    int oi = __shfl_xor(idx, o, 64);
+    if (ov > best || (ov == best && oi < idx)) best = ov, idx = oi;
+  }
+  if ((threadIdx.x & 63) == 0) bv[threadIdx.x >> 6] = best, bi[threadIdx.x >> 6] = idx;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; w++)
+      if (bv[w] > best || (bv[w] == best && bi[w] < idx)) best = bv[w], idx = bi[w];
+    // All NaN or n == 0: index 0.
+    out[0] = (uint32_t)(idx == 0x7fffffff ? 0 : idx);
+  }
+}
+
+__global__ void zero_kernel(uint32_t *p, size_t words) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i < words; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+__global__ void zero_bytes_kernel(uint8_t *p, size_t bytes) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < bytes) p[i] = 0;
+}
+
+__global__ void add_kernel(float *x, const float *a, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (; i < n; i += (size_t)gridDim.x * blockDim.x) x[i] += a[i];
+}
+
+}  // namespace
+
+int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *b, float *y, int rows,
+                      int cols, const float *table, float *yr, int hd) {
+  if (rows < 0 || cols <= 0 || (rows && (!x || !g || !b || !y)))
+    return wh_fail(ctx, WH_EARG, "layer_norm: bad arguments (%d x %d)", rows, cols);
+  if (table && (!yr || hd <= 0 || hd % 2 || cols % hd))
+    return wh_fail(ctx, WH_EARG, "layer_norm: rope needs cols %% head_dim == 0 and even head_dim");
+  if (!rows) return WH_OK;
+  ProfScope prof(ctx, "layer_norm", 0.0, 4.0 * rows * cols * (table ? 3 : 2));
+  if (cols <= ROW_REGS * 64) {
+    size_t lds = table ? (size_t)4 * cols * sizeof(float) : 0;
+    layer_norm_kernel<<<(rows + 3) / 4, 256, lds, ctx->stream>>>(x, g, b, y, rows, cols, table, yr, hd);
+  } else {
+    if (table) return wh_fail(ctx, WH_EARG, "layer_norm: rope rows of at most %d", ROW_REGS * 64);
+    layer_norm_long<<<rows, 64, 0, ctx->stream>>>(x, g, b, y, cols);
+  }
+  return wh_launched(ctx, "layer_norm");
+}
+
+int launch_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int kernel, int stride, int pad,
+                  int batch, long xs, long cs) {
+  if (t <= 0 || ch <= 0 || kernel <= 0 || stride <= 0 || pad < 0 || t + 2 * pad < kernel || batch <= 0)
+    return wh_fail(ctx, WH_EARG, "im2col: bad shape");
+  int rows = (t + 2 * pad - kernel) / stride + 1;
+  int width = (ch * kernel + 31) / 32 * 32;
+  dim3 grid((width + 255) / 256, rows, batch);
+  ProfScope prof(ctx, "im2col", 0.0, 4.0 * batch * ((double)rows * width + (double)t * ch));
+  im2col_kernel<<<grid, 256, 0, ctx->stream>>>(x, col, t, ch, kernel, stride, pad, rows, width, xs, cs);
+  return wh_launched(ctx, "im2col");
+}
+
+int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb, int kernel, const float *g,
+                    const float *b, int layer_norm, float *y, int t, int ch, const int *valid_dev, int valid,
+                    int batch) {
+  if (t <= 0 || ch <= 0 || ch > 1024 || kernel <= 0 || kernel % 2 == 0 || batch <= 0)
+    return wh_fail(ctx, WH_EARG, "conv_glu: bad shape (t %d, ch %d, kernel %d)", t, ch, kernel);
+  int frames = t * batch;
+  ProfScope prof(ctx, "conv_glu", 0.0, 12.0 * frames * ch);
+  conv_glu_kernel<<<(frames + 3) / 4, 256, 0, ctx->stream>>>(h, w, wb, kernel, g, b, layer_norm, y, t, ch,
+                                                             valid_dev, valid < 0 ? t : valid, frames);
+  return wh_launched(ctx, "conv_glu");
+}
+
+int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *b0, const float *w,
+                     const float *b, float *y, int t, int f, int ch, int t0, int rows) {
+  if (t <= 0 || f <= 0 || ch <= 0 || t0 < 0 || rows < 0) return wh_fail(ctx, WH_EARG, "depthwise: bad shape");
+  if (!rows) return WH_OK;
+  int threads = ch >= 256 ? 256 : ((ch + 63) / 64) * 64;
+  ProfScope prof(ctx, w0 ? "first_depthwise" : "depthwise", 0.0,
+                 4.0 * rows * half_len(w0 ? half_len(f) : f) * ch * (w0 ? 1 : 4));
+  if (w0) {
+    dim3 grid(half_len(half_len(f)) , rows);
+    first_depthwise_kernel<<<grid, threads < 64 ? 64 : threads, 0, ctx->stream>>>(x, w, b, y, w0, b0, t, f, ch, t0);
+  } else {
+    dim3 grid(half_len(f), rows);
+    depthwise_kernel<<<grid, threads, 0, ctx->stream>>>(x, w, b, y, t, f, ch, t0);
+  }
+  return wh_launched(ctx, "depthwise");
+}
+
+int launch_flatten(wh_ctx *ctx, const float *x, float *y, int t, int f, int ch) {
+  if (t < 0 || f <= 0 || ch <= 0) return wh_fail(ctx, WH_EARG, "flatten: bad shape");
+  if (!t) return WH_OK;
+  ProfScope prof(ctx, "flatten", 0.0, 8.0 * t * f * ch);
+  flatten_kernel<<<t, 256, 0, ctx->stream>>>(x, y, f, ch);
+  return wh_launched(ctx, "flatten");
+}
+
+int launch_argmax(wh_ctx *ctx, const float *x, uint32_t *out, int n) {
+  if (n < 0 || !out) return wh_fail(ctx, WH_EARG, "argmax: bad arguments");
+  argmax_kernel<<<1, 256, 0, ctx->stream>>>(x, out, n);
+  return wh_launched(ctx, "argmax");
+}
+
+int launch_zero(wh_ctx *ctx, void *dst, size_t bytes) {
+  if (!bytes) return WH_OK;
+  if (!dst) return wh_fail(ctx, WH_EARG, "zero: NULL");
+  size_t words = bytes / 4;
+  if ((uintptr_t)dst % 4 == 0 && words) {
+    size_t blocks = (words + 255) / 256;
+    zero_kernel<<<(unsigned)(blocks > 65535 ? 65535 : blocks), 256, 0, ctx->stream>>>((uint32_t *)dst, words);
+    if (bytes % 4)
+      zero_bytes_kernel<<<1, 4, 0, ctx->stream>>>((uint8_t *)dst + words * 4, bytes % 4);
+  } else {
+    zero_bytes_kernel<<<(unsigned)((bytes + 255) / 256), 256, 0, ctx->stream>>>((uint8_t *)dst, bytes);
+  }
+  return wh_launched(ctx, "zero");
+}
+
+int launch_add_rows(wh_ctx *ctx, float *x, const float *a, size_t n) {
+  if (!n) return WH_OK;
+  size_t blocks = (n + 255) / 256;
+  add_kernel<<<(unsigned)(blocks > 65535 ? 65535 : blocks), 256, 0, ctx->stream>>>(x, a, n);
+  return wh_launched(ctx, "add");
+}

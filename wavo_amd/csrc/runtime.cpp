@@ -1,0 +1,411 @@
+// Device, memory and weight management behind the C ABI (include/wavo_hip.h), and the thin
+// entry points of the Pass ops.  The reference's counterparts are in src/gpu/mod.rs: Gpu::new
+// (:461-577), buffer/readback/upload/write (:675-750), upload_linear (:770-834), run/complete
+// (:906-1002).  One HIP stream per context replaces wgpu's queue; errors that wgpu reports through
+// callbacks (:508-512, :995-1000) surface here as HIP status codes at the next wh_sync/wh_read.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "internal.h"
+
+static thread_local std::string g_open_error;
+
+int wh_fail(wh_ctx *ctx, int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->error = buf;
+  else g_open_error = buf;
+  return code;
+}
+
+int wh_launched(wh_ctx *ctx, const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "%s: %s", what, hipGetErrorString(e));
+  return WH_OK;
+}
+
+static int prof_event(wh_ctx *ctx) {
+  if (ctx->next_event == ctx->events.size()) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return -1;
+    ctx->events.push_back(e);
+  }
+  return (int)ctx->next_event++;
+}
+
+ProfScope::ProfScope(wh_ctx *c, const char *kernel, double flops, double bytes) : ctx(c) {
+  if (!ctx || !ctx->prof) return;
+  wh_prof_rec r;
+  r.kernel = kernel;
+  r.flops = flops;
+  r.bytes = bytes;
+  r.ev0 = prof_event(ctx);
+  r.ev1 = prof_event(ctx);
+  if (r.ev0 < 0 || r.ev1 < 0) return;
+  hipEventRecord(ctx->events[r.ev0], ctx->stream);
+  rec = (int)ctx->recs.size();
+  ctx->recs.push_back(r);
+}
+
+ProfScope::~ProfScope() {
+  if (rec >= 0) hipEventRecord(ctx->events[ctx->recs[rec].ev1], ctx->stream);
+}
+
+size_t wh_type_bytes(int type, size_t n) {
+  switch (type) {
+    case WH_F32: return n * 4;
+    case WH_F16: return n * 2;
+    case WH_Q8_0: return n / 32 * 34;
+    case WH_Q4_0: return n / 32 * 18;
+  }
+  return 0;
+}
+
+extern "C" {
+
+int wh_open(int device_index, wh_ctx **out) {
+  if (!out) return wh_fail(nullptr, WH_EARG, "wh_open: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0)
+    return wh_fail(nullptr, WH_EGPU, "no GPU: %s", e != hipSuccess ? hipGetErrorString(e) : "none");
+  int dev = device_index < 0 ? 0 : device_index;
+  if (dev >= n) return wh_fail(nullptr, WH_EGPU, "no GPU at index %d: %d listed", dev, n);
+  hipDeviceProp_t p;
+  if ((e = hipGetDeviceProperties(&p, dev)) != hipSuccess)
+    return wh_fail(nullptr, WH_EGPU, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+  if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+    return wh_fail(nullptr, WH_EGPU, "device %d is %s; this build runs on gfx950 (MI355X) only",
+                   dev, p.gcnArchName);
+  if ((e = hipSetDevice(dev)) != hipSuccess)
+    return wh_fail(nullptr, WH_EGPU, "hipSetDevice: %s", hipGetErrorString(e));
+  wh_ctx *ctx = new wh_ctx;
+  ctx->device = dev;
+  ctx->cus = p.multiProcessorCount;
+  ctx->name = p.name;
+  if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
+    delete ctx;
+    return wh_fail(nullptr, WH_EGPU, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  *out = ctx;
+  return WH_OK;
+}
+
+void wh_close(wh_ctx *ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);
+  for (hipEvent_t e : ctx->events) (void)hipEventDestroy(e);
+  hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+const char *wh_last_error(const wh_ctx *ctx) {
+  return ctx ? ctx->error.c_str() : g_open_error.c_str();
+}
+
+int wh_device_info(wh_ctx *ctx, char *name, size_t name_len, int *cus, int *wave) {
+  if (!ctx) return WH_EARG;
+  if (name && name_len) snprintf(name, name_len, "%s", ctx->name.c_str());
+  if (cus) *cus = ctx->cus;
+  if (wave) *wave = 64;
+  return WH_OK;
+}
+
+int wh_alloc(wh_ctx *ctx, size_t n_f32, float **dptr) {
+  if (!ctx || !dptr) return WH_EARG;
+  hipSetDevice(ctx->device);
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, (n_f32 ? n_f32 : 1) * sizeof(float));
+  if (e != hipSuccess) {
+    hipGetLastError();
+    return wh_fail(ctx, e == hipErrorOutOfMemory ? WH_EOOM : WH_EGPU, "hipMalloc of %zu floats: %s",
+                   n_f32, hipGetErrorString(e));
+  }
+  *dptr = (float *)p;
+  return WH_OK;
+}
+
+int wh_free(wh_ctx *ctx, void *dptr) {
+  if (!ctx) return WH_EARG;
+  if (!dptr) return WH_OK;
+  hipSetDevice(ctx->device);
+  hipError_t e = hipFree(dptr);
+  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "hipFree: %s", hipGetErrorString(e));
+  return WH_OK;
+}
+
+int wh_write(wh_ctx *ctx, void *dst, const void *src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return WH_EARG;
+  if (!bytes) return WH_OK;
+  hipSetDevice(ctx->device);
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "write of %zu bytes: %s", bytes, hipGetErrorString(e));
+  return WH_OK;
+}
+
+int wh_copy(wh_ctx *ctx, void *dst, const void *src, size_t bytes) {
+  if (!ctx || (!bytes)) return ctx ? WH_OK : WH_EARG;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream);
+  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "copy of %zu bytes: %s", bytes, hipGetErrorString(e));
+  return WH_OK;
+}
+
+int wh_zero(wh_ctx *ctx, void *dst, size_t bytes) {
+  if (!ctx) return WH_EARG;
+  return launch_zero(ctx, dst, bytes);
+}
+
+int wh_sync(wh_ctx *ctx) {
+  if (!ctx) return WH_EARG;
+  hipSetDevice(ctx->device);
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "device error: %s", hipGetErrorString(e));
+  return WH_OK;
+}
+
+int wh_read(wh_ctx *ctx, void *host, const void *dptr, size_t bytes) {
+  if (!ctx || (bytes && (!host || !dptr))) return WH_EARG;
+  int rc = wh_sync(ctx);
+  if (rc) return rc;
+  if (!bytes) return WH_OK;
+  hipError_t e = hipMemcpy(host, dptr, bytes, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "read of %zu bytes: %s", bytes, hipGetErrorString(e));
+  return WH_OK;
+}
+
+void *wh_stream(wh_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int wh_profile(wh_ctx *ctx, int on) {
+  if (!ctx) return WH_EARG;
+  int rc = wh_sync(ctx);
+  if (rc) return rc;
+  ctx->prof = on != 0;
+  ctx->recs.clear();
+  ctx->next_event = 0;
+  return WH_OK;
+}
+
+int wh_profile_read(wh_ctx *ctx, char *out, size_t len) {
+  if (!ctx || !out || !len) return WH_EARG;
+  int rc = wh_sync(ctx);
+  if (rc) return rc;
+  // Per kernel: launches, total milliseconds, algorithmic flops and bytes, in first-seen order.
+  std::vector<std::string> order;
+  std::vector<double> ms, fl, by;
+  std::vector<long> n;
+  for (const wh_prof_rec &r : ctx->recs) {
+    float t = 0.0f;
+    if (hipEventElapsedTime(&t, ctx->events[r.ev0], ctx->events[r.ev1]) != hipSuccess) t = 0.0f;
+    size_t i = 0;
+    while (i < order.size() && order[i] != r.kernel) i++;
+    if (i == order.size()) {
+      order.push_back(r.kernel);
+      ms.push_back(0), fl.push_back(0), by.push_back(0), n.push_back(0);
+    }
+    ms[i] += t, fl[i] += r.flops, by[i] += r.bytes, n[i]++;
+  }
+  std::string s = "[";
+  for (size_t i = 0; i < order.size(); i++) {
+    char buf[512];
+    snprintf(buf, sizeof buf, "%s{\"kernel\": \"%s\", \"launches\": %ld, \"ms\": %.6f, \"flops\": %.6g, \"bytes\": %.6g}",
+             i ? ", " : "", order[i].c_str(), n[i], ms[i], fl[i], by[i]);
+    s += buf;
+  }
+  s += "]";
+  snprintf(out, len, "%s", s.c_str());
+  return s.size() < len ? WH_OK : wh_fail(ctx, WH_EARG, "profile text needs %zu bytes", s.size() + 1);
+}
+
+// ------------------------------------------------------------------------------------ weights
+
+int wh_linear_new(wh_ctx *ctx, const wh_tensor *ws, int count, const float *bias, int n_bias,
+                  int pad_k, wh_linear **out) {
+  if (!ctx || !ws || count <= 0 || !out || n_bias < 0) return wh_fail(ctx, WH_EARG, "wh_linear_new: bad arguments");
+  *out = nullptr;
+  int type = ws[0].type, k = ws[0].k, rows = 0;
+  for (int i = 0; i < count; i++) {
+    if (ws[i].type != type || ws[i].k != k || ws[i].rows <= 0 || !ws[i].data)
+      return wh_fail(ctx, WH_EARG, "stacked weights differ in type or shape");
+    rows += ws[i].rows;
+  }
+  if (type != WH_F32 && type != WH_F16 && type != WH_Q8_0 && type != WH_Q4_0)
+    return wh_fail(ctx, WH_EARG, "unsupported weight type %d", type);
+  if (k <= 0) return wh_fail(ctx, WH_EARG, "linear layer with k = %d", k);
+  if ((type == WH_Q8_0 || type == WH_Q4_0) && k % 32)
+    return wh_fail(ctx, WH_EARG, "linear layer %d→%d: quantized rows need k %% 32 == 0", k, rows);
+  if (!pad_k && k % 32) return wh_fail(ctx, WH_EARG, "linear layer %d→%d: needs k %% 32 == 0", k, rows);
+  int dual = n_bias > rows ? n_bias - rows : 0;
+  if ((n_bias && n_bias < rows) || dual > rows)
+    return wh_fail(ctx, WH_EARG, "linear layer %d→%d: bias has %d values", k, rows, n_bias);
+  int n = (rows + 63) / 64 * 64;
+  int cols = rows % 32 == 0 ? rows : n;
+  int kp = (k + 31) / 32 * 32;
+  std::vector<uint8_t> host;
+  int dtype = type;
+  if (kp != k) {
+    // Padded k (Gpu::conv, src/gpu/mod.rs:787-796): the rows in F32 with zero columns.
+    dtype = WH_F32;
+    host.assign((size_t)rows * kp * 4, 0);
+    std::vector<float> row(k);
+    int at = 0;
+    for (int i = 0; i < count; i++) {
+      const uint8_t *src = (const uint8_t *)ws[i].data;
+      for (int r = 0; r < ws[i].rows; r++, at++) {
+        if (type == WH_F32) {
+          memcpy(host.data() + (size_t)at * kp * 4, src + (size_t)r * k * 4, (size_t)k * 4);
+        } else {  // F16 rows
+          const uint16_t *h = (const uint16_t *)(src + (size_t)r * k * 2);
+          float *o = (float *)(host.data() + (size_t)at * kp * 4);
+          for (int c = 0; c < k; c++) {
+            uint32_t x = h[c], s = (x & 0x8000u) << 16, e = (x >> 10) & 31, mnt = x & 0x3ff, u;
+            if (e == 0) {
+              float v = (float)mnt * 5.9604644775390625e-8f;
+              o[c] = s ? -v : v;
+              continue;
+            }
+            u = e == 31 ? (s | 0x7f800000u | (mnt << 13)) : (s | ((e + 112) << 23) | (mnt << 13));
+            memcpy(&o[c], &u, 4);
+          }
+        }
+      }
+    }
+  }
+  wh_linear *l = new wh_linear;
+  l->rows = rows;
+  l->cols = cols;
+  l->dual = dual;
+  l->k = kp;
+  l->type = dtype;
+  l->row_bytes = wh_type_bytes(dtype, (size_t)kp);
+  hipSetDevice(ctx->device);
+  size_t wbytes = l->row_bytes * rows;
+  // 256 bytes of slack: the GEMM's loaders read whole dwords of the last row.
+  hipError_t e = hipMalloc(&l->w, wbytes + 256);
+  if (e == hipSuccess) e = hipMalloc(&l->bias, sizeof(float) * (size_t)(n > cols + dual ? n : cols + dual));
+  if (e != hipSuccess) {
+    hipGetLastError();
+    int rc = wh_fail(ctx, e == hipErrorOutOfMemory ? WH_EOOM : WH_EGPU, "weights: %s", hipGetErrorString(e));
+    wh_linear_free(ctx, l);
+    return rc;
+  }
+  if (!host.empty()) {
+    e = hipMemcpy(l->w, host.data(), wbytes, hipMemcpyHostToDevice);
+  } else {
+    size_t at = 0;
+    for (int i = 0; i < count && e == hipSuccess; i++) {
+      size_t b = l->row_bytes * ws[i].rows;
+      e = hipMemcpy(l->w + at, ws[i].data, b, hipMemcpyHostToDevice);
+      at += b;
+    }
+  }
+  if (e == hipSuccess) e = hipMemset(l->w + wbytes, 0, 256);
+  std::vector<float> pb((size_t)(n > cols + dual ? n : cols + dual), 0.0f);
+  if (n_bias) {
+    memcpy(pb.data(), bias, sizeof(float) * rows);
+    if (dual) memcpy(pb.data() + cols, bias + rows, sizeof(float) * dual);
+  }
+  if (e == hipSuccess) e = hipMemcpy(l->bias, pb.data(), sizeof(float) * pb.size(), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    int rc = wh_fail(ctx, WH_EGPU, "weight upload: %s", hipGetErrorString(e));
+    wh_linear_free(ctx, l);
+    return rc;
+  }
+  *out = l;
+  return WH_OK;
+}
+
+int wh_linear_width(const wh_linear *l) { return l ? l->cols + l->dual : 0; }
+int wh_linear_k(const wh_linear *l) { return l ? l->k : 0; }
+int wh_linear_type(const wh_linear *l) { return l ? l->type : -1; }
+
+void wh_linear_free(wh_ctx *ctx, wh_linear *l) {
+  if (!l) return;
+  if (ctx) hipSetDevice(ctx->device);
+  if (l->w) hipFree(l->w);
+  if (l->bias) hipFree(l->bias);
+  delete l;
+}
+
+// ------------------------------------------------------------------------------------ Pass ops
+
+int wh_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int epi, float alpha) {
+  if (!ctx || !l) return WH_EARG;
+  return launch_gemm(ctx, a, l, c, m, l->cols + l->dual, epi, alpha);
+}
+
+int wh_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,
+            int offset) {
+  if (!ctx || !l) return WH_EARG;
+  return launch_gemv(ctx, a, l, c, epi, alpha, offset);
+}
+
+int wh_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, const uint32_t *ids, int i,
+             int offset) {
+  if (!ctx || !l) return WH_EARG;
+  return launch_embed(ctx, l, pos, c, ids, i, offset);
+}
+
+int wh_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *b, float *y, int rows,
+                  int cols, const float *table, float *yr, int head_dim) {
+  if (!ctx) return WH_EARG;
+  return launch_layer_norm(ctx, x, g, b, y, rows, cols, table, yr, head_dim);
+}
+
+size_t wh_attend_len(int n, int heads, int hd) {
+  return (size_t)((n + 255) / 256) * heads * (hd + 2);
+}
+
+int wh_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, float *o, int n, int cols,
+              int heads, int hd) {
+  if (!ctx) return WH_EARG;
+  return launch_attend(ctx, q, kv, part, o, n, cols, heads, hd);
+}
+
+int wh_pack(wh_ctx *ctx, const float *x, int src, int stride, uint32_t *y, int rows, int d, int cols,
+            int col) {
+  if (!ctx) return WH_EARG;
+  return launch_pack(ctx, x, src, stride, y, rows, d, cols, col);
+}
+
+int wh_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int kernel, int stride, int pad) {
+  if (!ctx) return WH_EARG;
+  return launch_im2col(ctx, x, col, t, ch, kernel, stride, pad, 1, 0, 0);
+}
+
+int wh_conv_glu(wh_ctx *ctx, const float *h, const float *dw_w, const float *dw_b, int kernel,
+                const float *g, const float *b, int layer_norm, float *y, int t, int ch, int valid) {
+  if (!ctx) return WH_EARG;
+  return launch_conv_glu(ctx, h, dw_w, dw_b, kernel, g, b, layer_norm, y, t, ch, nullptr, valid, 1);
+}
+
+int wh_attention(wh_ctx *ctx, const float *qk, const float *v, const float *pos, float *o, int t,
+                 int heads, int hd, int valid) {
+  if (!ctx) return WH_EARG;
+  return launch_attention(ctx, qk, v, pos, o, t, heads, hd, nullptr, valid, 1);
+}
+
+int wh_depthwise(wh_ctx *ctx, const float *x, const float *first_w, const float *first_b,
+                 const float *w, const float *b, float *y, int t, int f, int ch, int t0, int rows) {
+  if (!ctx) return WH_EARG;
+  return launch_depthwise(ctx, x, first_w, first_b, w, b, y, t, f, ch, t0, rows);
+}
+
+int wh_flatten(wh_ctx *ctx, const float *x, float *y, int t, int f, int ch) {
+  if (!ctx) return WH_EARG;
+  return launch_flatten(ctx, x, y, t, f, ch);
+}
+
+int wh_argmax(wh_ctx *ctx, const float *x, uint32_t *out, int n) {
+  if (!ctx) return WH_EARG;
+  return launch_argmax(ctx, x, out, n);
+}
+
+}  // extern "C"

@@ -88,6 +88,9 @@ def lib():
             "ox_model_info": (ctypes.c_int, [ctypes.c_void_p, _ip, _ip, _ip, _ip, _ip]),
             "ox_model_tdt": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_int, ctypes.c_int,
                                             _u32p, ctypes.c_int]),
+            "ox_model_tdt_trace": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_int, ctypes.c_int,
+                                                  _u32p, ctypes.c_int, _ip, _fp, ctypes.c_int]),
+            "ox_model_tdt_lipschitz": (ctypes.c_float, [ctypes.c_void_p]),
             "ox_whisper_begin": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_int]),
             "ox_whisper_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _fp]),
             "ox_threads": (ctypes.c_int, []),
@@ -356,6 +359,24 @@ class Model:
         if n < 0:
             raise ValueError("tdt failed")
         return [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(min(n, 16384))]
+
+    def tdt_trace(self, enc):
+        """TDT tokens and, per decision, (frame, token, duration index) and the smaller top-2 gap of
+        its token/duration logits."""
+        enc, pe = f32(enc)
+        cap = 16384
+        out = np.zeros(2 * cap, np.uint32)
+        frames = np.zeros(3 * 4 * cap, np.int32)
+        gaps = np.zeros(4 * cap, np.float32)
+        n = lib().ox_model_tdt_trace(self.h, pe, enc.shape[0], enc.shape[1], out.ctypes.data_as(_u32p), cap,
+                                     frames.ctypes.data_as(_ip), _ptr(gaps), 4 * cap)
+        if n < 0:
+            raise ValueError("tdt failed")
+        toks = [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(min(n, cap))]
+        return toks, frames.reshape(-1, 3), gaps
+
+    def tdt_lipschitz(self):
+        return float(lib().ox_model_tdt_lipschitz(self.h))
 
     def whisper_begin(self, enc):
         enc, pe = f32(enc)

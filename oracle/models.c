@@ -940,7 +940,25 @@ typedef struct {
   const float *enc;
   int width;
   float *state, *next, *pred;
+  /* Optional trace per decision: (frame, token, duration index) and the smaller top-2 gap of its
+   * token and duration logits (how far the decision is from flipping). */
+  int *trace_frame;
+  float *trace_gap;
+  int decisions, cap;
 } tdt_ctx;
+
+static float top2_gap(const float *v, int n) {
+  float a = -INFINITY, b = -INFINITY;
+  for (int i = 0; i < n; i++) {
+    if (v[i] > a) {
+      b = a;
+      a = v[i];
+    } else if (v[i] > b) {
+      b = v[i];
+    }
+  }
+  return n > 1 ? a - b : INFINITY;
+}
 
 /* Decoder::predict (src/parakeet/decoder.rs:111-133). */
 static void predict(ox_model *m, int token, const float *state, float *next, float *pred) {
@@ -992,15 +1010,24 @@ static void tdt_joint_fn(void *p, int t, int emitted, int *token, int *dur) {
   for (int i = 0; i < m->classes + m->n_dur; i++) logits[i] = logits[i] + m->out_b[i];
   *token = ox_argmax(logits, m->classes);
   *dur = ox_argmax(logits + m->classes, m->n_dur);
+  if (c->trace_gap && c->decisions < c->cap) {
+    float g1 = top2_gap(logits, m->classes), g2 = top2_gap(logits + m->classes, m->n_dur);
+    c->trace_frame[3 * c->decisions] = t;
+    c->trace_frame[3 * c->decisions + 1] = *token;
+    c->trace_frame[3 * c->decisions + 2] = *dur;
+    c->trace_gap[c->decisions] = g1 < g2 ? g1 : g2;
+  }
+  c->decisions++;
   free(z);
   free(logits);
 }
 
-int ox_model_tdt(ox_model *m, const float *enc, int frames, int width, uint32_t *out, int cap) {
+int ox_model_tdt_trace(ox_model *m, const float *enc, int frames, int width, uint32_t *out, int cap,
+                       int *trace_frame, float *trace_gap, int trace_cap) {
   if (m->arch != ARCH_PARAKEET || !m->embed) return -1;
   int S = 2 * m->lstm_layers * m->hidden;
   tdt_ctx c = {m, enc, width, (float *)calloc((size_t)S, 4), (float *)calloc((size_t)S, 4),
-               (float *)calloc((size_t)m->joint, 4)};
+               (float *)calloc((size_t)m->joint, 4), trace_frame, trace_gap, 0, trace_cap};
   predict(m, -1, c.state, c.next, c.pred);
   int n = ox_tdt_loop(frames, m->blank, m->durations, m->max_symbols, m->global, tdt_joint_fn, &c,
                       out, cap);
@@ -1008,6 +1035,25 @@ int ox_model_tdt(ox_model *m, const float *enc, int frames, int width, uint32_t 
   free(c.next);
   free(c.pred);
   return n;
+}
+
+int ox_model_tdt(ox_model *m, const float *enc, int frames, int width, uint32_t *out, int cap) {
+  return ox_model_tdt_trace(m, enc, frames, width, out, cap, NULL, NULL, 0);
+}
+
+/* max_i Σ_j |W_ij| of the joint's output layer: with the same predictor state, encoder rows that
+ * differ by at most ε per value give joint logits that differ by at most this times ε. */
+float ox_model_tdt_lipschitz(ox_model *m) {
+  if (m->arch != ARCH_PARAKEET || !m->out_w) return -1.0f;
+  float *w = (float *)malloc(sizeof(float) * (size_t)m->out_w->k), best = 0.0f;
+  for (int r = 0; r < m->out_w->n; r++) {
+    ox_linear_row(m->out_w, r, w);
+    float s = 0.0f;
+    for (int j = 0; j < m->out_w->k; j++) s += fabsf(w[j]);
+    if (s > best) best = s;
+  }
+  free(w);
+  return best;
 }
 
 /* ------------------------------------------------------------------------ Whisper decoding */

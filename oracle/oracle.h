@@ -150,6 +150,12 @@ int ox_model_blocks(ox_model *m, float *x, int t, int layers);
 int ox_model_info(ox_model *m, int *arch, int *d, int *layers, int *mels, int *width);
 /* TDT greedy decode (Parakeet) of an encoder output; returns token count, (token, frame) pairs. */
 int ox_model_tdt(ox_model *m, const float *enc, int frames, int width, uint32_t *out, int cap);
+/* The same, recording per decision (frame, token, duration index) in trace_frame[3i..3i+2] and the
+ * smaller top-2 gap of its token/duration logits in trace_gap[i] (first trace_cap decisions). */
+int ox_model_tdt_trace(ox_model *m, const float *enc, int frames, int width, uint32_t *out, int cap,
+                       int *trace_frame, float *trace_gap, int trace_cap);
+/* max_i Σ_j |W_ij| of the joint's output layer (the logits' sensitivity to the encoder row). */
+float ox_model_tdt_lipschitz(ox_model *m);
 /* Whisper: cross cache from encoder output, one decoder step's logits. */
 int ox_whisper_begin(ox_model *m, const float *enc, int frames);
 int ox_whisper_step(ox_model *m, int token, int pos, float *logits);

@@ -15,6 +15,7 @@ import pytest
 
 import oracle as ox
 import wavo_amd as wa
+from parity import ctc_parity, tdt_parity, top2_gap
 from wavo_amd import gguf, synth
 
 pytestmark = pytest.mark.gpu
@@ -32,19 +33,24 @@ def rel_l2(got, want):
 ENCODER_TOL = 1e-2
 
 
-def top2_gap(row):
-    s = np.sort(row)
-    return float(s[-1] - s[-2])
+def check_ctc(m, full, want):
+    """The product's CTC on the device output equals the oracle's CTC on the same logits; against the
+    oracle's encoder output only provable near-tie frames may differ."""
+    classes = want.shape[1]
+    got = full[:, :classes]
+    assert m.greedy(full) == ox.ctc(got, classes - 1)
+    flips = ctc_parity(got, want, classes)
+    if not flips:
+        assert m.greedy(full) == ox.ctc(want, classes - 1)
+    return flips
 
 
-def check_tokens(got, want, logits, what):
-    if got != want:
-        n = min(len(got), len(want))
-        first = next((i for i in range(n) if got[i] != want[i]), n)
-        frame = want[first][1] if first < len(want) else got[first][1]
-        gap = top2_gap(logits[frame]) if frame < len(logits) else float("nan")
-        pytest.fail(f"{what}: first token mismatch at #{first} (frame {frame}, top-2 gap {gap:.3g}): "
-                    f"{got[first:first + 3]} vs {want[first:first + 3]}")
+def check_tdt(m, om, got, want):
+    assert m.greedy(got) == om.tdt(got), "the product's TDT decoder differs from the oracle's"
+    flip, tg, tw = tdt_parity(om, got, want)
+    if flip is None:
+        assert tg == tw
+    return flip
 
 
 @pytest.mark.parametrize("wtype", [gguf.Q8_0, gguf.F16, gguf.Q4_0])
@@ -53,10 +59,10 @@ def test_gigaam_small(gpu, wtype):
     mel = synth.gigaam_mel(synth.audio(11, 1))
     want = ox.Model(path).encode(mel)
     m = wa.Model(gpu, path)
-    got = m.encode(mel)[:, :want.shape[1]]
-    assert rel_l2(got, want) < ENCODER_TOL, rel_l2(got, want)
     full = m.encode(mel)
-    check_tokens(m.greedy(full), ox.ctc(want, want.shape[1] - 1), want, "ctc")
+    got = full[:, :want.shape[1]]
+    assert rel_l2(got, want) < ENCODER_TOL, rel_l2(got, want)
+    check_ctc(m, full, want)
 
 
 @pytest.mark.parametrize("wtype", [gguf.Q8_0, gguf.F16])
@@ -69,7 +75,7 @@ def test_parakeet_small(gpu, wtype):
     got = m.encode(mel)
     assert got.shape == want.shape
     assert rel_l2(got, want) < ENCODER_TOL, rel_l2(got, want)
-    check_tokens(m.greedy(got), om.tdt(want), want, "tdt")
+    check_tdt(m, om, got, want)
 
 
 def test_parakeet_kestrel_valid(gpu):
@@ -130,5 +136,5 @@ def test_gigaam_full_config(gpu):
     got = full[:, :want.shape[1]]
     assert want.shape[0] == 275
     err = rel_l2(got, want)
-    assert err < 1e-2, err
-    check_tokens(m.greedy(full), ox.ctc(want, want.shape[1] - 1), want, "ctc")
+    assert err < ENCODER_TOL, err
+    check_ctc(m, full, want)

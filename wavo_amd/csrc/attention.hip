@@ -11,10 +11,10 @@
 //
 // Layout: a wavefront owns 16 queries and computes the transposed scores Sᵀ = K·Qᵀ and output
 // Oᵀ = Vᵀ·Pᵀ, so a query's softmax state lives in one lane column (lane % 16) of every MFMA
-// result.  The 4 waves of a workgroup (64 queries) share key blocks of 32 staged in LDS (K as
-// [key][dim], V transposed as [dim][key], both split).  The relative term is a band GEMM
-// Tᵀ[r][i] = P[r]·(q+v)_i over the 47 position rows a 16×32 block needs, skewed through LDS:
-// S_pos(i, j) = Tᵀ[j − i + 15][i].
+// result.  The waves of a workgroup (4 or 2: 64 or 32 queries) share key blocks of 32 staged in
+// LDS (K as [key][dim], V transposed as [dim][key], both split).  The relative term is a band GEMM
+// Tᵀ[r][i] = P[r]·(q+v)_i over the 47 position rows a wave's 16×32 block needs, out of the band of
+// 16·waves + 32 rows the workgroup stages in LDS, skewed through LDS: S_pos(i, j) = Tᵀ[j − i + 15][i].
 #include "internal.h"
 
 namespace {
@@ -59,22 +59,26 @@ __device__ __forceinline__ floatx4 mfma(half8 a, half8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-template <int NC, bool REL>
-__global__ __launch_bounds__(256) void flash_kernel(Args A) {
+template <int NC, bool REL, int QW>
+__global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
+  constexpr int NT = 64 * QW;          // threads
   constexpr int DP = NC * 32;          // head dims padded to the MFMA's k
-  constexpr int KROW = DP + KPAD;      // halves per K row in LDS
+  constexpr int KROW = DP + KPAD;      // halves per K / P row in LDS
   constexpr int OT = NC * 2;           // 16-dim output tiles (upper bound)
+  constexpr int PR = REL ? 16 * QW + 32 : 1;  // position rows of a key block's band
   __shared__ __attribute__((aligned(16))) _Float16 khi[KB * KROW], klo[KB * KROW];
   __shared__ __attribute__((aligned(16))) _Float16 vhi[DP * VROW], vlo[DP * VROW];
-  __shared__ float tt[REL ? 4 * 48 * 17 : 1];
+  __shared__ __attribute__((aligned(16))) _Float16 phi[PR * KROW], plo[PR * KROW];
+  __shared__ float tt[REL ? QW * 48 * 17 : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, g = lane >> 4;
   const int b = blockIdx.z, head = blockIdx.y;
   const int t = A.t, hd = A.hd;
   const int kv_len = A.valid_dev ? min(A.valid_dev[b], t) : min(A.valid, t);
-  const int qi0 = blockIdx.x * 64 + wave * 16;
-  const int qi = qi0 + li;  // this lane's query
+  const int q0 = blockIdx.x * 16 * QW;   // the workgroup's first query
+  const int qi0 = q0 + wave * 16;        // the wave's
+  const int qi = qi0 + li;               // this lane's query
   const int hoff = head * hd;
 
   const float *qb = A.q + A.bq * b + hoff;
@@ -102,28 +106,61 @@ __global__ __launch_bounds__(256) void flash_kernel(Args A) {
   float *tw = tt + wave * 48 * 17;
 
   for (int j0 = 0; j0 < kv_len; j0 += KB) {
-    // Stage K [key][dim] and V transposed [dim][key], split, zeros past the keys and dims.
-    for (int e = tid; e < KB * (DP / 4); e += 256) {
+    // Stage K [key][dim] and V transposed [dim][key] (two keys per 32-bit store), split.
+    for (int e = tid; e < KB * (DP / 4); e += NT) {
       int key = e / (DP / 4), d = 4 * (e % (DP / 4));
       int j = j0 + key;
-      float kx[4] = {0, 0, 0, 0}, vx[4] = {0, 0, 0, 0};
-      if (j < kv_len && d < hd) {  // hd % 4 == 0: a quad is inside or past the head
-        float4 k4 = *(const float4 *)(kb + (size_t)j * A.qs + d);
-        float4 v4 = *(const float4 *)(vb + (size_t)j * A.vs + d);
-        kx[0] = k4.x, kx[1] = k4.y, kx[2] = k4.z, kx[3] = k4.w;
-        vx[0] = v4.x, vx[1] = v4.y, vx[2] = v4.z, vx[3] = v4.w;
-      }
+      float4 k4 = make_float4(0, 0, 0, 0);
+      if (j < kv_len && d < hd) k4 = *(const float4 *)(kb + (size_t)j * A.qs + d);
+      const float kx[4] = {k4.x, k4.y, k4.z, k4.w};
       half4 h, lo;
 #pragma unroll
       for (int q = 0; q < 4; q++) {
         h[q] = (_Float16)kx[q];
         lo[q] = (_Float16)((kx[q] - (float)h[q]) * LO);
-        _Float16 vh = (_Float16)vx[q];
-        vhi[(d + q) * VROW + key] = vh;
-        vlo[(d + q) * VROW + key] = (_Float16)((vx[q] - (float)vh) * LO);
       }
       *(half4 *)(khi + key * KROW + d) = h;
       *(half4 *)(klo + key * KROW + d) = lo;
+    }
+    for (int e = tid; e < (KB / 2) * (DP / 4); e += NT) {
+      int kp = e / (DP / 4), d = 4 * (e % (DP / 4));
+      int j = j0 + 2 * kp;
+      float4 v0 = make_float4(0, 0, 0, 0), v1 = v0;
+      if (d < hd) {
+        if (j < kv_len) v0 = *(const float4 *)(vb + (size_t)j * A.vs + d);
+        if (j + 1 < kv_len) v1 = *(const float4 *)(vb + (size_t)(j + 1) * A.vs + d);
+      }
+      const float a0[4] = {v0.x, v0.y, v0.z, v0.w}, a1[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        _Float16 h0 = (_Float16)a0[q], h1 = (_Float16)a1[q];
+        typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+        half2v hh = {h0, h1};
+        half2v ll = {(_Float16)((a0[q] - (float)h0) * LO), (_Float16)((a1[q] - (float)h1) * LO)};
+        *(half2v *)(vhi + (d + q) * VROW + 2 * kp) = hh;
+        *(half2v *)(vlo + (d + q) * VROW + 2 * kp) = ll;
+      }
+    }
+    if constexpr (REL) {
+      // The band of position rows this key block needs for the workgroup's queries: rows
+      // r0 .. r0 + PR, r0 = j0 − q0 − 16·(QW − 1) + t (position row of key j and query i is
+      // j − i + t + 15).  Rows outside the table are zeros.
+      const int r0 = j0 - q0 - 16 * (QW - 1) + t, prow = 2 * t + 15;
+      for (int e = tid; e < PR * (DP / 4); e += NT) {
+        int rr = e / (DP / 4), d = 4 * (e % (DP / 4));
+        int r = r0 + rr;
+        float4 p4 = make_float4(0, 0, 0, 0);
+        if (r >= 0 && r < prow && d < hd) p4 = *(const float4 *)(A.pos + (size_t)r * A.os + hoff + d);
+        const float px[4] = {p4.x, p4.y, p4.z, p4.w};
+        half4 h, lo;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          h[q] = (_Float16)px[q];
+          lo[q] = (_Float16)((px[q] - (float)h[q]) * LO);
+        }
+        *(half4 *)(phi + rr * KROW + d) = h;
+        *(half4 *)(plo + rr * KROW + d) = lo;
+      }
     }
     __syncthreads();
 
@@ -145,22 +182,16 @@ __global__ __launch_bounds__(256) void flash_kernel(Args A) {
     }
 
     if constexpr (REL) {
-      // Band Tᵀ[r][i] = P[rbase + r]·(q+v)_i, r in 0..47 (local r = jj − ii + 15).
-      const int rbase = j0 - qi0 + t;
-      const int prow = 2 * t + 15;
+      // Band Tᵀ[r][i] = P[rbase + r]·(q+v)_i for the wave's queries, r in 0..47 (local r =
+      // jj − ii + 15); the wave's rows start 16·(QW − 1 − wave) into the staged band.
+      const int base = 16 * (QW - 1 - wave);
 #pragma unroll
       for (int rt = 0; rt < 3; rt++) {
         floatx4 am = floatx4{}, ac = floatx4{};
-        const int r = rbase + 16 * rt + li;
-        const bool in = r >= 0 && r < prow;
-        const float *pr = A.pos + (size_t)(in ? r : 0) * A.os + hoff;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-          float x[8];
-          int d0 = 32 * c + 8 * g;
-          load8(pr + d0, in ? min(8, hd - d0) : 0, x);
-          half8 ph, pl;
-          split8(x, ph, pl);
+          const int off = (base + 16 * rt + li) * KROW + 32 * c + 8 * g;
+          half8 ph = *(const half8 *)(phi + off), pl = *(const half8 *)(plo + off);
           am = mfma(ph, wh[c], am);
           ac = mfma(ph, wl[c], ac);
           ac = mfma(pl, wh[c], ac);
@@ -230,28 +261,40 @@ __global__ __launch_bounds__(256) void flash_kernel(Args A) {
   float *ob = A.o + A.bo * b + (size_t)qi * A.os + hoff;
 #pragma unroll
   for (int ot = 0; ot < OT; ot++) {
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-      int d = 16 * ot + 4 * g + v;
-      if (d < hd) ob[d] = (om[ot][v] + oc[ot][v] * LO_INV) * inv;
-    }
+    const int d = 16 * ot + 4 * g;
+    if (d >= hd) break;
+    float4 r;
+    r.x = (om[ot][0] + oc[ot][0] * LO_INV) * inv;
+    r.y = (om[ot][1] + oc[ot][1] * LO_INV) * inv;
+    r.z = (om[ot][2] + oc[ot][2] * LO_INV) * inv;
+    r.w = (om[ot][3] + oc[ot][3] * LO_INV) * inv;
+    *(float4 *)(ob + d) = r;  // hd % 4 == 0: a quad is inside or past the head
+  }
+}
+
+template <bool REL, int QW>
+void launch_qw(wh_ctx *ctx, const Args &a, dim3 grid, int nc) {
+  switch (nc) {
+    case 1: flash_kernel<1, REL, QW><<<grid, 64 * QW, 0, ctx->stream>>>(a); break;
+    case 2: flash_kernel<2, REL, QW><<<grid, 64 * QW, 0, ctx->stream>>>(a); break;
+    case 3: flash_kernel<3, REL, QW><<<grid, 64 * QW, 0, ctx->stream>>>(a); break;
+    default: flash_kernel<4, REL, QW><<<grid, 64 * QW, 0, ctx->stream>>>(a); break;
   }
 }
 
 template <bool REL>
 int launch_nc(wh_ctx *ctx, const Args &a, int heads, int batch) {
-  dim3 grid((a.t + 63) / 64, heads, batch);
   int nc = (a.hd + 31) / 32;
   // Algorithmic flops: 4·H·T²·hd (QKᵀ and PV), plus 2·H·T²·hd for the relative term, per window.
   double tt = (double)a.t * a.t * heads * a.hd * batch;
   double bytes = 4.0 * batch * a.t * heads * a.hd * (REL ? 5 : 4);
-  ProfScope prof(ctx, REL ? "attention_rel" : "attention", (REL ? 6.0 : 4.0) * tt, bytes);
-  switch (nc) {
-    case 1: flash_kernel<1, REL><<<grid, 256, 0, ctx->stream>>>(a); break;
-    case 2: flash_kernel<2, REL><<<grid, 256, 0, ctx->stream>>>(a); break;
-    case 3: flash_kernel<3, REL><<<grid, 256, 0, ctx->stream>>>(a); break;
-    default: flash_kernel<4, REL><<<grid, 256, 0, ctx->stream>>>(a); break;
-  }
+  // 64 queries per workgroup, or 32 when that leaves fewer workgroups than two per CU.
+  const long wg64 = (long)((a.t + 63) / 64) * heads * batch;
+  const bool narrow = wg64 < 2L * (ctx->cus > 0 ? ctx->cus : 256);
+  ProfScope prof(ctx, REL ? (narrow ? "attention_rel_q32" : "attention_rel_q64") : (narrow ? "attention_q32" : "attention_q64"),
+                 (REL ? 6.0 : 4.0) * tt, bytes);
+  if (narrow) launch_qw<REL, 2>(ctx, a, dim3((a.t + 31) / 32, heads, batch), nc);
+  else launch_qw<REL, 4>(ctx, a, dim3((a.t + 63) / 64, heads, batch), nc);
   return wh_launched(ctx, "attention");
 }
 

@@ -62,6 +62,9 @@ size_t wh_type_bytes(int type, size_t n);
 // ---- launchers (each validates its shapes, then queues on ctx->stream) ----
 int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int ldc, int epi,
                 float alpha);
+// The same with `a` already rounded to f16 (its producer wrote f16): half the A traffic.
+int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, float *c, int m, int ldc, int epi,
+                  float alpha);
 int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,
                 int offset);
 int launch_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, const uint32_t *ids,

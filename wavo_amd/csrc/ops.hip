@@ -33,33 +33,40 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict
   const int row = blockIdx.x * 4 + w;
   const bool active = row < rows;
   float *sr = srow + w * cols;
+  const int q4 = cols / 4;  // float4 per row (cols % 4 == 0)
   if (active) {
-    const float *xr = x + (size_t)row * cols;
-    float v[ROW_REGS];
+    const float4 *xr = (const float4 *)(x + (size_t)row * cols);
+    float4 v[ROW_REGS / 4];
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < ROW_REGS; j++) {
+    for (int j = 0; j < ROW_REGS / 4; j++) {
       int i = lane + 64 * j;
-      v[j] = i < cols ? xr[i] : 0.0f;
-      s += v[j];
+      v[j] = i < q4 ? xr[i] : make_float4(0, 0, 0, 0);
+      s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
     }
     const float mean = wave_sum(s) / (float)cols;
     float q = 0.0f;
 #pragma unroll
-    for (int j = 0; j < ROW_REGS; j++) {
-      int i = lane + 64 * j;
-      float d = i < cols ? v[j] - mean : 0.0f;
-      q += d * d;
+    for (int j = 0; j < ROW_REGS / 4; j++) {
+      if (lane + 64 * j < q4) {
+        float dx = v[j].x - mean, dy = v[j].y - mean, dz = v[j].z - mean, dw = v[j].w - mean;
+        q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+      }
     }
     const float rstd = rsqrtf(wave_sum(q) / (float)cols + 1e-5f);
-    float *yy = y + (size_t)row * cols;
+    float4 *yy = (float4 *)(y + (size_t)row * cols);
+    const float4 *g4 = (const float4 *)g, *b4 = (const float4 *)b;
 #pragma unroll
-    for (int j = 0; j < ROW_REGS; j++) {
+    for (int j = 0; j < ROW_REGS / 4; j++) {
       int i = lane + 64 * j;
-      if (i < cols) {
-        float o = (v[j] - mean) * rstd * g[i] + b[i];
+      if (i < q4) {
+        float4 gg = g4[i], bb = b4[i], o;
+        o.x = (v[j].x - mean) * rstd * gg.x + bb.x;
+        o.y = (v[j].y - mean) * rstd * gg.y + bb.y;
+        o.z = (v[j].z - mean) * rstd * gg.z + bb.z;
+        o.w = (v[j].w - mean) * rstd * gg.w + bb.w;
         yy[i] = o;
-        if (table) sr[i] = o;
+        if (table) *(float4 *)(sr + 4 * i) = o;
       }
     }
   }
@@ -109,22 +116,37 @@ __global__ void im2col_kernel(const float *__restrict__ x, float *__restrict__ c
   col[(size_t)i * width + e] = v;
 }
 
-// The Conformer conv module between the pointwise convs (ops.wgsl:121-164; src/cpu/ops.rs:137-182),
-// one wavefront per frame: h [t][2ch] → GLU x·σ(gate) (zero from the window's valid frames on) →
-// depthwise conv (odd kernel, centred, w [ch][kernel]) + bias → LayerNorm or affine → SiLU.
-// Frames are [batch][t]; the conv does not cross windows.
+// The Conformer conv module between the pointwise convs (ops.wgsl:121-164; src/cpu/ops.rs:137-182):
+// h [t][2ch] → GLU x·σ(gate) (zero from the window's valid frames on) → depthwise conv (odd kernel,
+// centred, w [ch][kernel]) + bias → LayerNorm or affine → SiLU.  A workgroup takes CF frames: it
+// computes the GLU of its frames and the kernel/2 frames either side once into LDS, then one
+// wavefront per frame runs the taps over LDS and the norm over its channels.  Frames are [batch][t];
+// the conv does not cross windows.
+constexpr int CF = 4;
+
 __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__ h, const float *__restrict__ w,
                                                        const float *__restrict__ wb, int kernel,
                                                        const float *__restrict__ g, const float *__restrict__ gb,
                                                        int layer_norm, float *__restrict__ y, int t, int ch,
-                                                       const int *__restrict__ valid_dev, int valid, int frames) {
-  const int lane = threadIdx.x & 63;
-  const int f = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (f >= frames) return;
-  const int seg = f / t, i = f % t;
+                                                       const int *__restrict__ valid_dev, int valid) {
+  extern __shared__ float glu[];  // [CF + kernel − 1][ch]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int seg = blockIdx.y, f0 = blockIdx.x * CF;
   const int lim = valid_dev ? min(valid_dev[seg], t) : min(valid, t);
-  const int pad = kernel / 2;
+  const int pad = kernel / 2, span = CF + kernel - 1;
   const float *hs = h + (size_t)seg * t * 2 * ch;
+  for (int e = threadIdx.x; e < span * ch; e += 256) {
+    int r = e / ch, c = e % ch, src = f0 - pad + r;
+    float v = 0.0f;
+    if (src >= 0 && src < lim) {
+      const float *hr = hs + (size_t)src * 2 * ch;
+      v = hr[c] / (1.0f + __expf(-hr[ch + c]));
+    }
+    glu[e] = v;
+  }
+  __syncthreads();
+  const int i = f0 + wave;
+  if (i >= t) return;
   float acc[16];
   float s = 0.0f;
 #pragma unroll
@@ -133,12 +155,7 @@ __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__
     float a = 0.0f;
     if (c < ch) {
       a = wb[c];
-      for (int k = 0; k < kernel; k++) {
-        int src = i + k - pad;
-        if (src < 0 || src >= lim) continue;
-        const float *r = hs + (size_t)src * 2 * ch;
-        a += w[c * kernel + k] * (r[c] / (1.0f + __expf(-r[ch + c])));
-      }
+      for (int k = 0; k < kernel; k++) a += w[c * kernel + k] * glu[(wave + k) * ch + c];
     }
     acc[j] = a;
     s += a;
@@ -155,7 +172,7 @@ __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__
     }
     rstd = rsqrtf(wave_sum(q) / (float)ch + 1e-5f);
   }
-  float *yy = y + (size_t)f * ch;
+  float *yy = y + ((size_t)seg * t + i) * ch;
 #pragma unroll
   for (int j = 0; j < 16; j++) {
     int c = lane + 64 * j;
@@ -293,11 +310,12 @@ int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *
     return wh_fail(ctx, WH_EARG, "layer_norm: rope needs cols %% head_dim == 0 and even head_dim");
   if (!rows) return WH_OK;
   ProfScope prof(ctx, "layer_norm", 0.0, 4.0 * rows * cols * (table ? 3 : 2));
-  if (cols <= ROW_REGS * 64) {
+  if (cols <= ROW_REGS * 64 && cols % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 &&
+      (uintptr_t)g % 16 == 0 && (uintptr_t)b % 16 == 0) {
     size_t lds = table ? (size_t)4 * cols * sizeof(float) : 0;
     layer_norm_kernel<<<(rows + 3) / 4, 256, lds, ctx->stream>>>(x, g, b, y, rows, cols, table, yr, hd);
   } else {
-    if (table) return wh_fail(ctx, WH_EARG, "layer_norm: rope rows of at most %d", ROW_REGS * 64);
+    if (table) return wh_fail(ctx, WH_EARG, "layer_norm: rope rows need cols %% 4 == 0, at most %d", ROW_REGS * 64);
     layer_norm_long<<<rows, 64, 0, ctx->stream>>>(x, g, b, y, cols);
   }
   return wh_launched(ctx, "layer_norm");
@@ -321,9 +339,11 @@ int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb
   if (t <= 0 || ch <= 0 || ch > 1024 || kernel <= 0 || kernel % 2 == 0 || batch <= 0)
     return wh_fail(ctx, WH_EARG, "conv_glu: bad shape (t %d, ch %d, kernel %d)", t, ch, kernel);
   int frames = t * batch;
+  if ((size_t)(CF + kernel - 1) * ch * 4 > 160 * 1024) return wh_fail(ctx, WH_EARG, "conv_glu: kernel %d too large", kernel);
   ProfScope prof(ctx, "conv_glu", 0.0, 12.0 * frames * ch);
-  conv_glu_kernel<<<(frames + 3) / 4, 256, 0, ctx->stream>>>(h, w, wb, kernel, g, b, layer_norm, y, t, ch,
-                                                             valid_dev, valid < 0 ? t : valid, frames);
+  dim3 grid((t + CF - 1) / CF, batch);
+  conv_glu_kernel<<<grid, 64 * CF, (size_t)(CF + kernel - 1) * ch * 4, ctx->stream>>>(
+      h, w, wb, kernel, g, b, layer_norm, y, t, ch, valid_dev, valid < 0 ? t : valid);
   return wh_launched(ctx, "conv_glu");
 }
 

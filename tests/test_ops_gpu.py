@@ -72,6 +72,25 @@ def test_gemm(gpu, wtype, k, n, cols):
                 assert got[-1] == c0[-1]
 
 
+@pytest.mark.parametrize("wtype", [wa.Q8_0, wa.Q4_0, wa.F16])
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 256), (750, 4096, 1024), (750, 1024, 4096), (1515, 1024, 1024)])
+def test_gemm_large(gpu, wtype, m, n, k):
+    # The tile plans of the main kernel at the encoder's shapes: 128×128 tiles of 8 wavefronts with
+    # 64- and 128-wide k steps, 64×64 tiles with k split 4 ways (partial sums finished in order).
+    w = np.random.default_rng(1).normal(0, 0.02, (n, k)).astype(np.float32)
+    raw = ox.quantize(w, wtype)
+    bias = rnd(n, 2)
+    l = gpu.linear([(raw, wtype, k, n)], bias)
+    ol = ox.Linear(wtype, k, [(raw, n)], bias)
+    a = rnd(m * k, 3).reshape(m, k)
+    ab, cb = gpu.upload(a), gpu.buffer(m * n)
+    for e in (wa.BIAS, wa.SILU):
+        gpu.gemm(ab, l, cb, m, e)
+        want = ox.gemm(a, ol, m, e)
+        close(gpu.read(cb, (m, n)), want, tol=2e-5 * max(1.0, float(np.abs(want).max())),
+              what=f"type {wtype} {m}x{n}x{k} epi {e}")
+
+
 def test_gemm_padded_k(gpu):
     # k = 40 is padded to 64 by Gpu::conv; input rows are 64 wide with zeros after 40 (from im2col).
     n, k, m = 64, 40, 37

@@ -2,12 +2,25 @@
 //   c[m][j] = epi(Σ_k h(a[m][k]) · h(W[j][k]) + bias[j]),  h = round to f16 (RNE), f32 accumulate,
 // as gemm.wgsl:170-242 and the CPU backend (src/cpu/gemm.rs:126-177) define it.  W stays in HBM as
 // the GGUF stores it (src/gguf.rs:14-38): Q8_0 34-byte blocks (f16 scale + 32 int8), Q4_0 18-byte
-// blocks (f16 scale + 16 bytes of nibbles), F16 or F32 rows.  Each workgroup stages a BM×64 tile of
-// `a` (rounded to f16, or already f16 from its producer) in LDS, double-buffered, while each lane
-// loads its own GGUF block of W from HBM straight into registers and dequantizes it to f16(q·d) —
-// the reference's exact rounding — as the operand of v_mfma_f32_32x32x16_f16; the epilogues of
-// Epilogue::params (src/gpu/mod.rs:445-455; gemm.wgsl:72-94) and the dual outputs are fused into
-// the store.
+// blocks (f16 scale + 16 bytes of nibbles), F16 or F32 rows.
+//
+// Main kernel (gemm_lds_kernel; k % 64 == 0, W in Q8_0 / Q4_0 / F16, `a` in f16): two LDS stages
+// fed by the LDS DMA of gfx950 — per 64- or 128-wide k step, the a tile (16-byte
+// global_load_lds_dwordx4) and each W row's GGUF blocks as stored (68 or 36 bytes per block pair,
+// 4-byte global_load_lds_dword; F16 rows like a) — so the next step's bytes land while the MFMAs
+// work on the current one.  Each lane dequantizes one block of its W row from LDS into the f16
+// operand of v_mfma_f32_32x32x16_f16: int8 q becomes the f16 1024 + (q + 128) by byte placement, an
+// exact subtraction gives q, and one packed f16 multiply by the block scale rounds q·d once to
+// nearest even — f16(q·d), the reference's exact rounding (products q·d have at most 19 significant
+// bits, so f32 and the f16 multiply round the same value).  The epilogues of Epilogue::params
+// (src/gpu/mod.rs:445-455; gemm.wgsl:72-94) and the dual outputs are fused into the store, in f32
+// or, for a consumer that rounds its input to f16 anyway (another GEMM), in f16.  Shapes with too
+// few output tiles for the 256 CUs split k 2 or 4 ways into f32 partial sums that a second kernel
+// adds in a fixed order before the epilogue.
+//
+// Fallback kernel (gemm_reg_kernel; any k % 32 == 0 and F32 weights): a double-buffered a tile in
+// LDS and W blocks loaded straight into registers.
+#include <algorithm>
 #include <cstdio>
 
 #include "internal.h"
@@ -16,6 +29,7 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BK = 64;       // k per stage: two quantized blocks
@@ -171,7 +185,7 @@ __device__ __forceinline__ void dequant_b(const BRaw<WT> &s, int g, half8 f[4]) 
 }
 
 template <int WT, int BM, int BN, bool ALIGNED, bool A16>
-__global__ __launch_bounds__(256) void gemm_kernel(const void *__restrict__ a, const uint8_t *__restrict__ w,
+__global__ __launch_bounds__(256) void gemm_reg_kernel(const void *__restrict__ a, const uint8_t *__restrict__ w,
                                                    const float *__restrict__ bias, float *__restrict__ c,
                                                    int m, int rows, int cols, int k, int dual, int ldc,
                                                    int epi, float alpha, size_t row_bytes) {
@@ -241,6 +255,368 @@ __global__ __launch_bounds__(256) void gemm_kernel(const void *__restrict__ a, c
     }
 }
 
+
+// ------------------------------------------------------------------------------------ LDS-DMA path
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// LDS DMA (counted by vmcnt): each lane copies 16 (dma16) or 4 (dma4) bytes at `src` to LDS byte
+// lds + 16·lane (4·lane); `lds` is wave-uniform.
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+__device__ __forceinline__ void dma4(const void *src, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Two f16 values 1024 + byte0, 1024 + byte1 of x (bytes 0-1, or 2-3 with HI).
+template <bool HI>
+__device__ __forceinline__ half2 magic_pair(uint32_t x) {
+  return __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, x, HI ? 0x04030402u : 0x04010400u));
+}
+
+// The MFMA fragment of substep s (elements 8s .. 8s + 7) of one block.  dw = the block's data
+// dwords as read from LDS at the lane's offset, `sh` = bytes of that offset before the data (2 for
+// the even block of a pair: data from byte 2; 0 for the odd one: data dword-aligned), d2 = the
+// block's scale twice.
+template <int WT>
+__device__ __forceinline__ half8 dequant_frag(const uint32_t *dw, uint32_t sh, half2 d2, int s) {
+  half8 f;
+  if constexpr (WT == WH_Q8_0) {
+    const half2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};  // 1024 + 128
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const uint32_t x = __builtin_amdgcn_alignbyte(dw[2 * s + h + 1], dw[2 * s + h], sh) ^ 0x80808080u;
+      const half2 p0 = (magic_pair<false>(x) - bias) * d2, p1 = (magic_pair<true>(x) - bias) * d2;
+      f[4 * h] = p0[0], f[4 * h + 1] = p0[1], f[4 * h + 2] = p1[0], f[4 * h + 3] = p1[1];
+    }
+  } else {
+    // ggml block_q4_0: element i < 16 is the low nibble of byte i, 16 + i the high one; value
+    // (nibble − 8)·d.  Substeps 0-1 take low nibbles of bytes 0-15, substeps 2-3 high ones.
+    const half2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};  // 1024 + 8
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int q = 2 * (s & 1) + h;
+      const uint32_t x = __builtin_amdgcn_alignbyte(dw[q + 1], dw[q], sh);
+      const uint32_t nib = s < 2 ? x & 0x0f0f0f0fu : (x >> 4) & 0x0f0f0f0fu;
+      const half2 p0 = (magic_pair<false>(nib) - bias) * d2, p1 = (magic_pair<true>(nib) - bias) * d2;
+      f[4 * h] = p0[0], f[4 * h + 1] = p0[1], f[4 * h + 2] = p1[0], f[4 * h + 3] = p1[1];
+    }
+  }
+  return f;
+}
+
+// Work of one gemm_lds_kernel launch.
+struct LdsArgs {
+  const _Float16 *a;
+  const uint8_t *w;
+  const float *bias;
+  void *c;          // output, or f32 partial sums [split][m][cols] with SPLIT
+  int m, rows, cols, k, dual, ldc, epi;
+  float alpha;
+  size_t row_bytes;
+};
+
+// c tile BM × BN per workgroup of WM × WN wavefronts, each a (BM/WM) × (BN/WN) block of 32×32 MFMA
+// tiles, over the k range of split blockIdx.z (k / gridDim.z, a multiple of BK).  Two LDS stages
+// of BK-wide k steps: the DMA of step kt + 1 runs while the MFMAs work on step kt.  Stage layout:
+// a rows of BK/8 16-byte chunks (chunk c of row r at (c + r) % (BK/8), so the 8 lanes that read one
+// chunk column of 8 rows hit distinct banks), then W: F16 rows like a, or quantized rows of BK/64
+// block pairs (68 or 36 bytes each).  At substep s of block pair p, the lane of MFMA column n and k
+// half g takes k slots 64p + 32g + 8s .. + 8 — block 2p + g of its W row — and the a fragments the
+// same slots.
+template <int WT, int BM, int BN, int WM, int WN, int BK, bool SPLIT, bool OUT16>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  static_assert(TM >= 1 && TN >= 1, "32×32 MFMA tiles per wave");
+  constexpr int PAIRS = BK / 64;
+  constexpr int PAIR1 = WT == WH_Q8_0 ? 68 : WT == WH_Q4_0 ? 36 : 128;  // bytes of 64 weights
+  constexpr bool WCH = WT == WH_F16;                                     // W moves in 16-byte chunks
+  constexpr int ACH = BK / 8;                                            // 16-byte chunks per a row
+  constexpr int A_BYTES = BM * BK * 2, W_BYTES = BN * PAIR1 * PAIRS, STAGE = A_BYTES + W_BYTES;
+  static_assert(STAGE % 16 == 0 && (WCH || W_BYTES % 256 == 0), "whole DMA instructions");
+  constexpr int NIA = BM * ACH / 64;                            // a: 16-byte DMA instructions per stage
+  constexpr int NIW = WCH ? BN * ACH / 64 : W_BYTES / 256;      // W: 16-byte or 4-byte ones
+  constexpr int PA = (NIA + NW - 1) / NW, PW = (NIW + NW - 1) / NW;
+  // (+16: the odd block of the last W row reads one dword past its row, unused)
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE + 16];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const int wm = (wave / WN) * (BM / WM), wn = (wave % WN) * (BN / WN);
+  const int lrow = lane & 31, g = lane >> 5;
+  const int m = P.m, k = P.k, rows = P.rows;
+  const int nk = k / BK / gridDim.z, kz = blockIdx.z * nk;
+
+  // DMA sources of this lane at k step 0 (rows past m or rows are clamped: their products land
+  // in outputs that are discarded or zeroed).
+  const uint8_t *asrc[PA];
+#pragma unroll
+  for (int i = 0; i < PA; i++) {
+    const int n = min(wave + NW * i, NIA - 1), r = (64 * n + lane) / ACH, lc = ((lane % ACH) - r) & (ACH - 1);
+    asrc[i] = (const uint8_t *)P.a + ((size_t)min(m0 + r, m - 1) * k + (size_t)kz * BK + 8 * lc) * 2;
+  }
+  const uint8_t *wsrc[PW];
+#pragma unroll
+  for (int i = 0; i < PW; i++) {
+    const int n = min(wave + NW * i, NIW - 1);
+    if constexpr (WCH) {
+      const int r = (64 * n + lane) / ACH, lc = ((lane % ACH) - r) & (ACH - 1);
+      wsrc[i] = P.w + (size_t)min(n0 + r, rows - 1) * P.row_bytes + (size_t)kz * BK * 2 + 16 * lc;
+    } else {
+      const int s = 64 * n + lane, r = s / (PAIRS * PAIR1 / 4), dwi = s % (PAIRS * PAIR1 / 4);
+      wsrc[i] = P.w + (size_t)min(n0 + r, rows - 1) * P.row_bytes + (size_t)kz * PAIRS * PAIR1 + 4 * dwi;
+    }
+  }
+  const uint32_t lds0 = lds_addr(lds);
+  auto issue = [&](int kt) {
+    const uint32_t st = lds0 + (kt & 1) * STAGE;
+#pragma unroll
+    for (int i = 0; i < PA; i++) {
+      const int n = wave + NW * i;
+      if (n < NIA) dma16(asrc[i] + (size_t)kt * BK * 2, st + 1024 * n);
+    }
+#pragma unroll
+    for (int i = 0; i < PW; i++) {
+      const int n = wave + NW * i;
+      if (n < NIW) {
+        if constexpr (WCH) dma16(wsrc[i] + (size_t)kt * BK * 2, st + A_BYTES + 1024 * n);
+        else dma4(wsrc[i] + (size_t)kt * PAIRS * PAIR1, st + A_BYTES + 256 * n);
+      }
+    }
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) acc[i][j] = floatx16{};
+
+  if (nk > 0) issue(0);
+  for (int kt = 0; kt < nk; kt++) {
+    dma_wait();
+    __syncthreads();
+    if (kt + 1 < nk) issue(kt + 1);
+    const uint8_t *st = lds + (kt & 1) * STAGE;
+    const _Float16 *as = (const _Float16 *)st;
+#pragma unroll
+    for (int pp = 0; pp < PAIRS; pp++) {
+      // This pair's blocks of the wave's W rows (quantized): data dwords, shift and scale.
+      constexpr int ND = WT == WH_Q8_0 ? 9 : 5;
+      uint32_t dw[TN][ND];
+      half2 d2[TN];
+      const uint32_t sh = g ? 0u : 2u;
+      if constexpr (!WCH) {
+        constexpr int BLK = PAIR1 / 2;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          // Even block: scale in the low half of dword 0, data from byte 2; odd block (bytes
+          // BLK..): scale in the high half of the dword before byte BLK + 2, where its data starts.
+          const uint32_t *row = (const uint32_t *)(st + A_BYTES) + (wn + 32 * j + lrow) * (PAIRS * PAIR1 / 4) + pp * (PAIR1 / 4);
+          const uint32_t *p = row + (g ? (BLK + 2) / 4 : 0);
+          const uint32_t sc = g ? row[(BLK + 2) / 4 - 1] >> 16 : row[0] & 0xffffu;
+#pragma unroll
+          for (int i = 0; i < ND; i++) dw[j][i] = p[i];
+          const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)sc);
+          d2[j] = half2{d, d};
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        half8 af[TM], bf[TN];
+        const int lc = 8 * pp + 4 * g + s;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          if constexpr (WCH) {
+            const int r = wn + 32 * j + lrow;
+            bf[j] = *(const half8 *)((const _Float16 *)(st + A_BYTES) + r * BK + 8 * ((lc + r) & (ACH - 1)));
+          } else {
+            bf[j] = dequant_frag<WT>(dw[j], sh, d2[j], s);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          const int r = wm + 32 * i + lrow;
+          af[i] = *(const half8 *)(as + r * BK + 8 * ((lc + r) & (ACH - 1)));
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // D[i][j] of a 32×32 tile sits in lane j (mod 32), register v: i = 8·(v/4) + 4·(lane/32) + v%4.
+  // Columns past the real W rows (padding) get epi(0 + bias) as the reference's zero rows do.
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int col = n0 + wn + 32 * j + lrow;
+      if (col >= P.cols) continue;
+      if constexpr (SPLIT) {
+        float *cp = (float *)P.c + (size_t)blockIdx.z * m * P.cols + col;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+          const int row = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
+          if (row < m) cp[(size_t)row * P.cols] = acc[i][j][v];
+        }
+        continue;
+      }
+      const bool pad = col >= rows;
+      const float bv = P.bias[col];
+      const float b2 = col < P.dual ? P.bias[P.cols + col] : 0.0f;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        const int row = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
+        if (row >= m) continue;
+        const float x = pad ? 0.0f : acc[i][j][v];
+        const size_t at = (size_t)row * P.ldc + col;
+        if constexpr (OUT16) {
+          _Float16 *cp = (_Float16 *)P.c + at;
+          *cp = (_Float16)epilogue(P.epi, P.alpha, x + bv, nullptr);
+          if (col < P.dual) cp[P.cols] = (_Float16)(x + b2);
+        } else {
+          float *cp = (float *)P.c + at;
+          *cp = epilogue(P.epi, P.alpha, x + bv, cp);
+          if (col < P.dual) cp[P.cols] = x + b2;
+        }
+      }
+    }
+}
+
+// Split-k finish: c = epi(Σ_z part[z] + bias) with the partial sums added in split order (the same
+// result on every run), dual outputs and padding columns as in the kernel above.
+template <bool OUT16>
+__global__ __launch_bounds__(256) void split_finish_kernel(const float *__restrict__ part, int splits, const float *__restrict__ bias,
+                                                           void *__restrict__ c, int m, int rows, int cols, int dual,
+                                                           int ldc, int epi, float alpha) {
+  const size_t n = (size_t)m * cols, plane = n;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const int row = (int)(i / cols), col = (int)(i % cols);
+    float x = 0.0f;
+    for (int z = 0; z < splits; z++) x += part[z * plane + i];
+    if (col >= rows) x = 0.0f;
+    const size_t at = (size_t)row * ldc + col;
+    if constexpr (OUT16) {
+      _Float16 *cp = (_Float16 *)c + at;
+      *cp = (_Float16)epilogue(epi, alpha, x + bias[col], nullptr);
+      if (col < dual) cp[cols] = (_Float16)(x + bias[cols + col]);
+    } else {
+      float *cp = (float *)c + at;
+      *cp = epilogue(epi, alpha, x + bias[col], cp);
+      if (col < dual) cp[cols] = x + bias[cols + col];
+    }
+  }
+}
+
+// a (f32) rounded to f16 (RNE; h of the reference), for the GEMMs whose producer wrote f32.
+__global__ __launch_bounds__(256) void to_half_kernel(const float4 *__restrict__ x, half4 *__restrict__ y, size_t n4) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+    const float4 v = x[i];
+    y[i] = half4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+  }
+}
+
+// Launch shapes of the LDS-DMA kernel (tile, wavefronts, k step, split).
+struct Plan {
+  int bm, bn, wm, wn, bk, split;
+};
+
+// Chosen per GEMM shape from measurements on MI355X (one workgroup resident per CU at a time):
+// many output tiles → 128×128 tiles of 8 wavefronts; a few hundred → the same with 128-wide k steps;
+// fewer → 64×64 tiles of 4 wavefronts, and when even those leave CUs idle, k split 2 or 4 ways.
+Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
+  const int cus = ctx->cus > 0 ? ctx->cus : 256;
+  const long t128 = (long)((cols + 127) / 128) * ((m + 127) / 128), t64 = (long)((cols + 63) / 64) * ((m + 63) / 64);
+  Plan p{64, 64, 2, 2, 128, 1};
+  if (t128 >= 2L * cus) p = {128, 128, 2, 4, 64, 1};
+  else if (t128 >= cus / 2) p = {128, 128, 2, 4, 128, 1};
+  else if (t64 < cus)
+    while (p.split < 4 && t64 * p.split < 2L * cus && k % (2 * p.split * p.bk) == 0) p.split *= 2;
+  if (k % p.bk) p.bk = 64;
+  if (ctx->gemm_bm) {  // tuning override: the tile, with 8 wavefronts for 128×128
+    p.bm = ctx->gemm_bm, p.bn = ctx->gemm_bn, p.split = 1;
+    p.wm = 2, p.wn = p.bm == 128 && p.bn == 128 ? 4 : 2;
+    if (p.bm != p.bn) p.bk = 128;
+    if (k % p.bk) p.bm = p.bn = 64, p.bk = 64, p.wn = 2;
+  }
+  return p;
+}
+
+template <int WT, int BM, int BN, int WM, int WN, int BK>
+void lds_launch(wh_ctx *ctx, dim3 grid, const LdsArgs &a, bool split, bool out16) {
+  if (split) gemm_lds_kernel<WT, BM, BN, WM, WN, BK, true, false><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
+  else if (out16) gemm_lds_kernel<WT, BM, BN, WM, WN, BK, false, true><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
+  else gemm_lds_kernel<WT, BM, BN, WM, WN, BK, false, false><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
+}
+
+template <int WT>
+int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
+                 bool out16, float *part) {
+  Plan p = plan_for(ctx, m, l->cols, l->k);
+  if (p.split > 1 && !part) p.split = 1;
+  LdsArgs args{a, l->w, l->bias, p.split > 1 ? (void *)part : c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha,
+               l->row_bytes};
+  dim3 grid((l->cols + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.split);
+  static const char *tn = WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
+  char name[64];
+  snprintf(name, sizeof name, "gemm_%s_%dx%d%s", tn, p.bm, p.bn, p.split > 1 ? (p.split == 2 ? "_k2" : "_k4") : "");
+  const double width = l->cols + l->dual;
+  const double bytes = (double)l->rows * l->row_bytes + 2.0 * m * l->k +
+                       (out16 ? 2.0 : 4.0) * m * width * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
+  {
+    ProfScope prof(ctx, name, 2.0 * m * l->rows * l->k, bytes);
+    const bool sp = p.split > 1;
+    if (p.bm == 128 && p.bn == 128 && p.bk == 64) lds_launch<WT, 128, 128, 2, 4, 64>(ctx, grid, args, sp, out16);
+    else if (p.bm == 128 && p.bn == 128) lds_launch<WT, 128, 128, 2, 4, 128>(ctx, grid, args, sp, out16);
+    else if (p.bm == 64 && p.bn == 128) lds_launch<WT, 64, 128, 2, 2, 128>(ctx, grid, args, sp, out16);
+    else if (p.bm == 128) lds_launch<WT, 128, 64, 2, 2, 128>(ctx, grid, args, sp, out16);
+    else if (p.bk == 64) lds_launch<WT, 64, 64, 2, 2, 64>(ctx, grid, args, sp, out16);
+    else lds_launch<WT, 64, 64, 2, 2, 128>(ctx, grid, args, sp, out16);
+    if (int rc = wh_launched(ctx, "gemm")) return rc;
+  }
+  if (p.split > 1) {
+    ProfScope prof(ctx, "gemm_split_finish", 0.0, 4.0 * p.split * m * l->cols + 4.0 * m * width);
+    const size_t n = (size_t)m * l->cols;
+    const int blocks = (int)std::min<size_t>((n + 255) / 256, 8192);
+    if (out16)
+      split_finish_kernel<true><<<blocks, 256, 0, ctx->stream>>>(part, p.split, l->bias, c, m, l->rows, l->cols, l->dual, ldc, epi, alpha);
+    else
+      split_finish_kernel<false><<<blocks, 256, 0, ctx->stream>>>(part, p.split, l->bias, c, m, l->rows, l->cols, l->dual, ldc, epi, alpha);
+    return wh_launched(ctx, "gemm split finish");
+  }
+  return WH_OK;
+}
+
+bool lds_path(const wh_linear *l) {
+  return l->k % 64 == 0 && (l->type == WH_Q8_0 || l->type == WH_Q4_0 || l->type == WH_F16) && l->row_bytes % 4 == 0;
+}
+
+// Scratch bytes for the split-k partial sums of an m-row GEMM (0 when it does not split).
+size_t split_bytes(const wh_ctx *ctx, const wh_linear *l, int m) {
+  const Plan p = plan_for(ctx, m, l->cols, l->k);
+  return p.split > 1 ? (size_t)p.split * m * l->cols * 4 : 0;
+}
+
+// a16: f16 rows; part: scratch for split-k partial sums (or NULL: no split).
+int launch_lds(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
+               bool out16, float *part) {
+  switch (l->type) {
+    case WH_Q8_0: return launch_lds_t<WH_Q8_0>(ctx, a, l, c, m, ldc, epi, alpha, out16, part);
+    case WH_Q4_0: return launch_lds_t<WH_Q4_0>(ctx, a, l, c, m, ldc, epi, alpha, out16, part);
+    default: return launch_lds_t<WH_F16>(ctx, a, l, c, m, ldc, epi, alpha, out16, part);
+  }
+}
+
 template <int WT, bool ALIGNED, bool A16>
 int launch_t(wh_ctx *ctx, const void *a, const wh_linear *l, float *c, int m, int ldc, int epi, float alpha) {
   // Tile: the largest whose grid still gives every CU a workgroup, else the smallest.
@@ -261,11 +637,11 @@ int launch_t(wh_ctx *ctx, const void *a, const wh_linear *l, float *c, int m, in
                  4.0 * m * width * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
   ProfScope prof(ctx, name, 2.0 * m * l->rows * l->k, bytes);
   if (bm == 128)
-    gemm_kernel<WT, 128, 128, ALIGNED, A16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
+    gemm_reg_kernel<WT, 128, 128, ALIGNED, A16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
   else if (bn == 128)
-    gemm_kernel<WT, 64, 128, ALIGNED, A16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
+    gemm_reg_kernel<WT, 64, 128, ALIGNED, A16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
   else
-    gemm_kernel<WT, 64, 64, ALIGNED, A16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
+    gemm_reg_kernel<WT, 64, 64, ALIGNED, A16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
   return wh_launched(ctx, "gemm");
 }
 
@@ -287,20 +663,44 @@ int launch_typed(wh_ctx *ctx, const void *a, const wh_linear *l, float *c, int m
 
 }  // namespace
 
-int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int ldc, int epi,
-                float alpha) {
+static int check(wh_ctx *ctx, const void *a, const wh_linear *l, const void *c, int m, int epi) {
   if (m < 0 || !l || (m && (!a || !c))) return wh_fail(ctx, WH_EARG, "gemm: bad arguments (m %d)", m);
   if (epi < WH_BIAS || epi > WH_TANH) return wh_fail(ctx, WH_EARG, "gemm: epilogue %d", epi);
-  if (m == 0) return WH_OK;
   if ((uintptr_t)a % 16) return wh_fail(ctx, WH_EARG, "gemm: a must be 16-byte aligned");
-  return launch_typed<false>(ctx, a, l, c, m, ldc, epi, alpha);
+  return WH_OK;
 }
 
-int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, float *c, int m, int ldc, int epi,
-                  float alpha) {
-  if (m < 0 || !l || (m && (!a16 || !c))) return wh_fail(ctx, WH_EARG, "gemm: bad arguments (m %d)", m);
-  if (epi < WH_BIAS || epi > WH_TANH) return wh_fail(ctx, WH_EARG, "gemm: epilogue %d", epi);
+int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int ldc, int epi, float alpha) {
+  if (int rc = check(ctx, a, l, c, m, epi)) return rc;
   if (m == 0) return WH_OK;
-  if ((uintptr_t)a16 % 16) return wh_fail(ctx, WH_EARG, "gemm: a must be 16-byte aligned");
-  return launch_typed<true>(ctx, a16, l, c, m, ldc, epi, alpha);
+  if (!lds_path(l)) return launch_typed<false>(ctx, a, l, c, m, ldc, epi, alpha);
+  // The main kernel takes a in f16: round it once into scratch (followed by the split partials).
+  const size_t n = (size_t)m * l->k, abytes = (n * 2 + 255) / 256 * 256;
+  uint8_t *ws = (uint8_t *)wh_scratch(ctx, abytes + split_bytes(ctx, l, m));
+  if (!ws) return WH_EOOM;
+  _Float16 *a16 = (_Float16 *)ws;
+  {
+    ProfScope prof(ctx, "to_half", 0.0, 6.0 * n);
+    const size_t n4 = n / 4;
+    const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 4096);
+    to_half_kernel<<<blocks, 256, 0, ctx->stream>>>((const float4 *)a, (half4 *)a16, n4);
+    if (int rc = wh_launched(ctx, "gemm: rounding a")) return rc;
+  }
+  return launch_lds(ctx, a16, l, c, m, ldc, epi, alpha, false, (float *)(ws + abytes));
+}
+
+int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
+                  int out16) {
+  if (int rc = check(ctx, a16, l, c, m, epi)) return rc;
+  if (out16 && (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL))
+    return wh_fail(ctx, WH_EARG, "gemm: residual epilogues accumulate into f32 outputs");
+  if (m == 0) return WH_OK;
+  if (lds_path(l)) {
+    const size_t pb = split_bytes(ctx, l, m);
+    float *part = nullptr;
+    if (pb && !(part = (float *)wh_scratch(ctx, pb))) return WH_EOOM;
+    return launch_lds(ctx, (const _Float16 *)a16, l, c, m, ldc, epi, alpha, out16 != 0, part);
+  }
+  if (out16) return wh_fail(ctx, WH_EARG, "gemm: f16 output needs a Q8_0/Q4_0/F16 weight with k %% 64 == 0");
+  return launch_typed<true>(ctx, a16, l, (float *)c, m, ldc, epi, alpha);
 }

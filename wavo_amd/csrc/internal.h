@@ -21,6 +21,9 @@ struct wh_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   int cus = 0;
+  // GEMM tile override from WAVO_GEMM_TILE ("128x128", "64x128", "128x64", "64x64"; tuning sweeps
+  // only): 0 = chosen per shape.
+  int gemm_bm = 0, gemm_bn = 0;
   std::string name;
   std::string error;
   // Per-launch profiling (wh_profile): off by default.
@@ -28,7 +31,15 @@ struct wh_ctx {
   std::vector<hipEvent_t> events;
   size_t next_event = 0;
   std::vector<wh_prof_rec> recs;
+  // Device scratch of the ops that stage data between kernels of one call (attention's split
+  // operands): grown on demand, reused by every later call on this stream.
+  void *scratch = nullptr;
+  size_t scratch_bytes = 0;
 };
+
+// At least `bytes` of device scratch (256-byte aligned), or nullptr with ctx->error set.  Growing
+// it drains the stream first; a caller that must not allocate reserves the size up front.
+void *wh_scratch(wh_ctx *ctx, size_t bytes);
 
 // Profiling scope of one launch: records an event before and after it when profiling is on.
 struct ProfScope {
@@ -62,9 +73,11 @@ size_t wh_type_bytes(int type, size_t n);
 // ---- launchers (each validates its shapes, then queues on ctx->stream) ----
 int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int ldc, int epi,
                 float alpha);
-// The same with `a` already rounded to f16 (its producer wrote f16): half the A traffic.
-int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, float *c, int m, int ldc, int epi,
-                  float alpha);
+// The same with `a` already rounded to f16 (its producer wrote f16): half the A traffic.  With
+// out16 the outputs are stored as f16 (for a consumer that rounds them to f16 anyway); residual
+// epilogues need f32 outputs.
+int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int ldc, int epi,
+                  float alpha, int out16);
 int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,
                 int offset);
 int launch_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, const uint32_t *ids,
@@ -78,6 +91,8 @@ int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb
                     const int *valid_dev, int valid, int batch);
 int launch_attention(wh_ctx *ctx, const float *qk, const float *v, const float *pos, float *o, int t,
                      int heads, int hd, const int *valid_dev, int valid, int batch);
+// Scratch bytes launch_attention uses for t frames × batch windows (rel: relative positions).
+size_t attention_scratch_bytes(int t, int heads, int hd, int batch, int rel);
 int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *b0, const float *w,
                      const float *b, float *y, int t, int f, int ch, int t0, int rows);
 int launch_flatten(wh_ctx *ctx, const float *x, float *y, int t, int f, int ch);

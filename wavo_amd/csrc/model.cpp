@@ -734,6 +734,9 @@ int arena(wh_model *m, int frames, int batch) {
   if (wh_alloc(m->ctx, B, (float **)&m->valid_dev)) return WH_EOOM;
   if (!m->x || !m->y || !m->h || !m->qk || !m->yr || !m->pos || (sub && (!m->sub || !m->sub2)))
     return wh_fail(m->ctx, WH_EOOM, "arena of %d frames x %d windows: out of device memory", F, B);
+  // Attention's split operands for the largest call, so that encoding allocates nothing.
+  if (!wh_scratch(m->ctx, attention_scratch_bytes(F, m->heads, d / m->heads, B, m->arch == PARAKEET)))
+    return WH_EOOM;
   if (m->arch == PARAKEET) {
     // The sinusoidal table for F frames stays on the device; a call over t frames reads its
     // pos_rows(t) rows from row F − t (src/parakeet/encoder.rs:93, :129-131).
@@ -1048,7 +1051,7 @@ int wh_model_frames(const wh_model *m, int mel_frames, int *frames, int *width) 
 
 int wh_model_encode(wh_model *m, const float *mel, int mel_frames, int valid, float *out) {
   if (!m || !mel || !out || mel_frames <= 0) return WH_EARG;
-  hipSetDevice(m->ctx->device);
+  (void)hipSetDevice(m->ctx->device);
   switch (m->arch) {
     case GIGAAM: return gigaam_encode(m, mel, mel_frames, out);
     case PARAKEET: {
@@ -1062,7 +1065,7 @@ int wh_model_encode(wh_model *m, const float *mel, int mel_frames, int valid, fl
 int wh_model_encode_batch(wh_model *m, const float *mel, int batch, int mel_frames, const int *valid, float *out) {
   if (!m || !mel || !out || !valid || batch <= 0 || mel_frames <= 0) return WH_EARG;
   if (m->arch != PARAKEET) return wh_fail(m->ctx, WH_EARG, "batched windows are built for the Parakeet encoder");
-  hipSetDevice(m->ctx->device);
+  (void)hipSetDevice(m->ctx->device);
   return parakeet_encode(m, mel, batch, mel_frames, valid, out);
 }
 

@@ -4,6 +4,7 @@
 // (:906-1002).  One HIP stream per context replaces wgpu's queue; errors that wgpu reports through
 // callbacks (:508-512, :995-1000) surface here as HIP status codes at the next wh_sync/wh_read.
 #include <cstdarg>
+#include <cstdlib>
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -47,13 +48,30 @@ ProfScope::ProfScope(wh_ctx *c, const char *kernel, double flops, double bytes) 
   r.ev0 = prof_event(ctx);
   r.ev1 = prof_event(ctx);
   if (r.ev0 < 0 || r.ev1 < 0) return;
-  hipEventRecord(ctx->events[r.ev0], ctx->stream);
+  (void)hipEventRecord(ctx->events[r.ev0], ctx->stream);
   rec = (int)ctx->recs.size();
   ctx->recs.push_back(r);
 }
 
 ProfScope::~ProfScope() {
-  if (rec >= 0) hipEventRecord(ctx->events[ctx->recs[rec].ev1], ctx->stream);
+  if (rec >= 0) (void)hipEventRecord(ctx->events[ctx->recs[rec].ev1], ctx->stream);
+}
+
+void *wh_scratch(wh_ctx *ctx, size_t bytes) {
+  if (bytes <= ctx->scratch_bytes) return ctx->scratch;
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  if (e == hipSuccess && ctx->scratch) e = hipFree(ctx->scratch);
+  ctx->scratch = nullptr;
+  ctx->scratch_bytes = 0;
+  if (e == hipSuccess) e = hipMalloc(&ctx->scratch, bytes);
+  if (e != hipSuccess) {
+    ctx->scratch = nullptr;
+    (void)hipGetLastError();
+    wh_fail(ctx, e == hipErrorOutOfMemory ? WH_EOOM : WH_EGPU, "scratch of %zu bytes: %s", bytes, hipGetErrorString(e));
+    return nullptr;
+  }
+  ctx->scratch_bytes = bytes;
+  return ctx->scratch;
 }
 
 size_t wh_type_bytes(int type, size_t n) {
@@ -89,6 +107,11 @@ int wh_open(int device_index, wh_ctx **out) {
   ctx->device = dev;
   ctx->cus = p.multiProcessorCount;
   ctx->name = p.name;
+  if (const char *t = getenv("WAVO_GEMM_TILE")) {
+    int bm = 0, bn = 0;
+    if (sscanf(t, "%dx%d", &bm, &bn) == 2 && (bm == 64 || bm == 128) && (bn == 64 || bn == 128))
+      ctx->gemm_bm = bm, ctx->gemm_bn = bn;
+  }
   if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
     delete ctx;
     return wh_fail(nullptr, WH_EGPU, "hipStreamCreate: %s", hipGetErrorString(e));
@@ -102,7 +125,8 @@ void wh_close(wh_ctx *ctx) {
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
   for (hipEvent_t e : ctx->events) (void)hipEventDestroy(e);
-  hipStreamDestroy(ctx->stream);
+  if (ctx->scratch) (void)hipFree(ctx->scratch);
+  (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
 
@@ -120,11 +144,11 @@ int wh_device_info(wh_ctx *ctx, char *name, size_t name_len, int *cus, int *wave
 
 int wh_alloc(wh_ctx *ctx, size_t n_f32, float **dptr) {
   if (!ctx || !dptr) return WH_EARG;
-  hipSetDevice(ctx->device);
+  (void)hipSetDevice(ctx->device);
   void *p = nullptr;
   hipError_t e = hipMalloc(&p, (n_f32 ? n_f32 : 1) * sizeof(float));
   if (e != hipSuccess) {
-    hipGetLastError();
+    (void)hipGetLastError();
     return wh_fail(ctx, e == hipErrorOutOfMemory ? WH_EOOM : WH_EGPU, "hipMalloc of %zu floats: %s",
                    n_f32, hipGetErrorString(e));
   }
@@ -135,7 +159,7 @@ int wh_alloc(wh_ctx *ctx, size_t n_f32, float **dptr) {
 int wh_free(wh_ctx *ctx, void *dptr) {
   if (!ctx) return WH_EARG;
   if (!dptr) return WH_OK;
-  hipSetDevice(ctx->device);
+  (void)hipSetDevice(ctx->device);
   hipError_t e = hipFree(dptr);
   if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "hipFree: %s", hipGetErrorString(e));
   return WH_OK;
@@ -144,7 +168,7 @@ int wh_free(wh_ctx *ctx, void *dptr) {
 int wh_write(wh_ctx *ctx, void *dst, const void *src, size_t bytes) {
   if (!ctx || (!dst && bytes) || (!src && bytes)) return WH_EARG;
   if (!bytes) return WH_OK;
-  hipSetDevice(ctx->device);
+  (void)hipSetDevice(ctx->device);
   hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "write of %zu bytes: %s", bytes, hipGetErrorString(e));
@@ -165,7 +189,7 @@ int wh_zero(wh_ctx *ctx, void *dst, size_t bytes) {
 
 int wh_sync(wh_ctx *ctx) {
   if (!ctx) return WH_EARG;
-  hipSetDevice(ctx->device);
+  (void)hipSetDevice(ctx->device);
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "device error: %s", hipGetErrorString(e));
   return WH_OK;
@@ -285,13 +309,13 @@ int wh_linear_new(wh_ctx *ctx, const wh_tensor *ws, int count, const float *bias
   l->k = kp;
   l->type = dtype;
   l->row_bytes = wh_type_bytes(dtype, (size_t)kp);
-  hipSetDevice(ctx->device);
+  (void)hipSetDevice(ctx->device);
   size_t wbytes = l->row_bytes * rows;
   // 256 bytes of slack: the GEMM's loaders read whole dwords of the last row.
   hipError_t e = hipMalloc(&l->w, wbytes + 256);
   if (e == hipSuccess) e = hipMalloc(&l->bias, sizeof(float) * (size_t)(n > cols + dual ? n : cols + dual));
   if (e != hipSuccess) {
-    hipGetLastError();
+    (void)hipGetLastError();
     int rc = wh_fail(ctx, e == hipErrorOutOfMemory ? WH_EOOM : WH_EGPU, "weights: %s", hipGetErrorString(e));
     wh_linear_free(ctx, l);
     return rc;
@@ -328,9 +352,9 @@ int wh_linear_type(const wh_linear *l) { return l ? l->type : -1; }
 
 void wh_linear_free(wh_ctx *ctx, wh_linear *l) {
   if (!l) return;
-  if (ctx) hipSetDevice(ctx->device);
-  if (l->w) hipFree(l->w);
-  if (l->bias) hipFree(l->bias);
+  if (ctx) (void)hipSetDevice(ctx->device);
+  if (l->w) (void)hipFree(l->w);
+  if (l->bias) (void)hipFree(l->bias);
   delete l;
 }
 

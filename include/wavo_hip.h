@@ -3,7 +3,7 @@
  *
  * The entry points mirror wavo's crate-internal GPU operator API one to one (src/gpu/mod.rs: `Gpu`,
  * `Linear`, `Channels`, `Epilogue`, `Pass`), so that a Rust `src/gpu/hip.rs` binds them through a
- * thin `extern "C"` block (see INTEGRATION.md).  Each declaration cites the reference interface it
+ * thin `extern "C"` block.  Each declaration cites the reference interface it
  * replaces.  Plain pointers and sizes only: no HIP or torch types cross this boundary.
  *
  * Conventions

@@ -1,7 +1,7 @@
 """End-to-end parity of the family encoders (and Whisper's decoder steps) on the device against the CPU
 oracle, on the same synthetic GGUF and the same seeded log-mel input.
 
-Bars (BASELINE north_star): encoder outputs within relative L2 1e-2 — the kernels round GEMM operands
+Bars: encoder outputs within relative L2 1e-2 — the kernels round GEMM operands
 to f16 exactly as the oracle (wavo's CPU backend) does, so the remaining error comes from f32 summation
 order (~1e-4 after it moves a few f16 roundings) — and identical greedy token ids: CTC (src/gigaam/decoder.rs:135-151), TDT
 (src/parakeet/decoder.rs:158-191), and the argmax of every Whisper step.  Each token mismatch would

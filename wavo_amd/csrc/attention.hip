@@ -66,7 +66,8 @@ Split split_shape(int t, int heads, int hd, int batch, bool rel) {
 
 struct Args {
   const float *q, *qv;   // f32 queries (q or q + u) and q + v rows
-  float *o;
+  void *o;               // f32, or f16 with o16 (for the output projection, which rounds it)
+  int o16;
   int qs, os;            // row strides in floats (q/qv, o)
   long bq, bo;           // batch strides in floats
   const _Float16 *kh, *kl, *vh, *vl, *ph, *pl;
@@ -412,7 +413,7 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
   l += __shfl_xor(l, 32, 64);
   if (qi >= t) return;
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;  // a window with no valid key outputs zeros
-  float *ob = A.o + A.bo * b + (size_t)qi * A.os + hoff;
+  const size_t obase = A.bo * b + (size_t)qi * A.os + hoff;
 #pragma unroll
   for (int ot = 0; ot < OT; ot++) {
     const int d = 16 * ot + 4 * g;
@@ -422,7 +423,9 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
     r.y = (om[ot][1] + oc[ot][1] * LO_INV) * inv;
     r.z = (om[ot][2] + oc[ot][2] * LO_INV) * inv;
     r.w = (om[ot][3] + oc[ot][3] * LO_INV) * inv;
-    *(float4 *)(ob + d) = r;  // hd % 4 == 0: a quad is inside or past the head
+    // hd % 4 == 0: a quad is inside or past the head
+    if (A.o16) *(half4 *)((_Float16 *)A.o + obase + d) = half4{(_Float16)r.x, (_Float16)r.y, (_Float16)r.z, (_Float16)r.w};
+    else *(float4 *)((float *)A.o + obase + d) = r;
   }
 }
 
@@ -469,8 +472,8 @@ size_t attention_scratch_bytes(int t, int heads, int hd, int batch, int rel) {
   return split_shape(t, heads, hd, batch, rel != 0).bytes();
 }
 
-int launch_attention(wh_ctx *ctx, const float *qk, const float *v, const float *pos, float *o, int t, int heads,
-                     int hd, const int *valid_dev, int valid, int batch) {
+int launch_attention(wh_ctx *ctx, const float *qk, const float *v, const float *pos, void *o, int t, int heads,
+                     int hd, const int *valid_dev, int valid, int batch, int out16) {
   if (t <= 0 || heads <= 0 || hd <= 0 || hd > 128 || hd % 4 || batch <= 0 || !qk || !o)
     return wh_fail(ctx, WH_EARG, "attention: bad shape (t %d, heads %d, head_dim %d)", t, heads, hd);
   if (v && pos) return wh_fail(ctx, WH_EARG, "attention: relative positions take [q+u | k | v | q+v] rows");
@@ -484,6 +487,7 @@ int launch_attention(wh_ctx *ctx, const float *qk, const float *v, const float *
   a.valid = valid < 0 || valid > t ? t : valid;
   if (!valid_dev && a.valid == 0) return wh_fail(ctx, WH_EARG, "attention: no valid keys");
   a.o = o;
+  a.o16 = out16 != 0;
   a.os = ch;
   a.bo = (long)t * ch;
   a.q = qk;

@@ -184,9 +184,9 @@ __device__ __forceinline__ void dequant_b(const BRaw<WT> &s, int g, half8 f[4]) 
   }
 }
 
-template <int WT, int BM, int BN, bool ALIGNED, bool A16>
+template <int WT, int BM, int BN, bool ALIGNED, bool A16, bool OUT16>
 __global__ __launch_bounds__(256) void gemm_reg_kernel(const void *__restrict__ a, const uint8_t *__restrict__ w,
-                                                   const float *__restrict__ bias, float *__restrict__ c,
+                                                   const float *__restrict__ bias, void *__restrict__ c,
                                                    int m, int rows, int cols, int k, int dual, int ldc,
                                                    int epi, float alpha, size_t row_bytes) {
   __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDS_ROW];
@@ -247,10 +247,17 @@ __global__ __launch_bounds__(256) void gemm_reg_kernel(const void *__restrict__ 
       for (int v = 0; v < 16; v++) {
         int row = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         if (row >= m) continue;
-        float *cp = c + (size_t)row * ldc + col;
-        float x = acc[i][j][v];
-        *cp = epilogue(epi, alpha, x + bv, cp);
-        if (col < dual) cp[cols] = x + b2;
+        const size_t at = (size_t)row * ldc + col;
+        float x = col < rows ? acc[i][j][v] : 0.0f;
+        if constexpr (OUT16) {
+          _Float16 *cp = (_Float16 *)c + at;
+          *cp = (_Float16)epilogue(epi, alpha, x + bv, nullptr);
+          if (col < dual) cp[cols] = (_Float16)(x + b2);
+        } else {
+          float *cp = (float *)c + at;
+          *cp = epilogue(epi, alpha, x + bv, cp);
+          if (col < dual) cp[cols] = x + b2;
+        }
       }
     }
 }
@@ -617,8 +624,8 @@ int launch_lds(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int 
   }
 }
 
-template <int WT, bool ALIGNED, bool A16>
-int launch_t(wh_ctx *ctx, const void *a, const wh_linear *l, float *c, int m, int ldc, int epi, float alpha) {
+template <int WT, bool ALIGNED, bool A16, bool OUT16>
+int launch_t(wh_ctx *ctx, const void *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha) {
   // Tile: the largest whose grid still gives every CU a workgroup, else the smallest.
   const int cus = ctx->cus > 0 ? ctx->cus : 256;
   auto tiles = [&](int bm, int bn) { return (long)((l->cols + bn - 1) / bn) * ((m + bm - 1) / bm); };
@@ -631,32 +638,32 @@ int launch_t(wh_ctx *ctx, const void *a, const wh_linear *l, float *c, int m, in
   // back by the residual epilogues).
   static const char *tn = WT == WH_F32 ? "f32" : WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
   char name[64];
-  snprintf(name, sizeof name, "gemm_%s%s_%dx%d", tn, A16 ? "_a16" : "", bm, bn);
+  snprintf(name, sizeof name, "gemm_reg_%s%s_%dx%d", tn, A16 ? "_a16" : "", bm, bn);
   double width = l->cols + l->dual;
   double bytes = (double)l->rows * l->row_bytes + (A16 ? 2.0 : 4.0) * m * l->k +
-                 4.0 * m * width * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
+                 (OUT16 ? 2.0 : 4.0) * m * width * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
   ProfScope prof(ctx, name, 2.0 * m * l->rows * l->k, bytes);
   if (bm == 128)
-    gemm_reg_kernel<WT, 128, 128, ALIGNED, A16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
+    gemm_reg_kernel<WT, 128, 128, ALIGNED, A16, OUT16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
   else if (bn == 128)
-    gemm_reg_kernel<WT, 64, 128, ALIGNED, A16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
+    gemm_reg_kernel<WT, 64, 128, ALIGNED, A16, OUT16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
   else
-    gemm_reg_kernel<WT, 64, 64, ALIGNED, A16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
+    gemm_reg_kernel<WT, 64, 64, ALIGNED, A16, OUT16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
   return wh_launched(ctx, "gemm");
 }
 
-template <bool A16>
-int launch_typed(wh_ctx *ctx, const void *a, const wh_linear *l, float *c, int m, int ldc, int epi, float alpha) {
+template <bool A16, bool OUT16>
+int launch_typed(wh_ctx *ctx, const void *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha) {
   const bool aligned = l->k % 64 == 0;
   switch (l->type) {
-    case WH_F32: return launch_t<WH_F32, true, A16>(ctx, a, l, c, m, ldc, epi, alpha);
-    case WH_F16: return launch_t<WH_F16, true, A16>(ctx, a, l, c, m, ldc, epi, alpha);
+    case WH_F32: return launch_t<WH_F32, true, A16, OUT16>(ctx, a, l, c, m, ldc, epi, alpha);
+    case WH_F16: return launch_t<WH_F16, true, A16, OUT16>(ctx, a, l, c, m, ldc, epi, alpha);
     case WH_Q8_0:
-      return aligned ? launch_t<WH_Q8_0, true, A16>(ctx, a, l, c, m, ldc, epi, alpha)
-                     : launch_t<WH_Q8_0, false, A16>(ctx, a, l, c, m, ldc, epi, alpha);
+      return aligned ? launch_t<WH_Q8_0, true, A16, OUT16>(ctx, a, l, c, m, ldc, epi, alpha)
+                     : launch_t<WH_Q8_0, false, A16, OUT16>(ctx, a, l, c, m, ldc, epi, alpha);
     case WH_Q4_0:
-      return aligned ? launch_t<WH_Q4_0, true, A16>(ctx, a, l, c, m, ldc, epi, alpha)
-                     : launch_t<WH_Q4_0, false, A16>(ctx, a, l, c, m, ldc, epi, alpha);
+      return aligned ? launch_t<WH_Q4_0, true, A16, OUT16>(ctx, a, l, c, m, ldc, epi, alpha)
+                     : launch_t<WH_Q4_0, false, A16, OUT16>(ctx, a, l, c, m, ldc, epi, alpha);
   }
   return wh_fail(ctx, WH_EARG, "gemm: weight type %d", l->type);
 }
@@ -673,7 +680,7 @@ static int check(wh_ctx *ctx, const void *a, const wh_linear *l, const void *c, 
 int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int ldc, int epi, float alpha) {
   if (int rc = check(ctx, a, l, c, m, epi)) return rc;
   if (m == 0) return WH_OK;
-  if (!lds_path(l)) return launch_typed<false>(ctx, a, l, c, m, ldc, epi, alpha);
+  if (!lds_path(l)) return launch_typed<false, false>(ctx, a, l, c, m, ldc, epi, alpha);
   // The main kernel takes a in f16: round it once into scratch (followed by the split partials).
   const size_t n = (size_t)m * l->k, abytes = (n * 2 + 255) / 256 * 256;
   uint8_t *ws = (uint8_t *)wh_scratch(ctx, abytes + split_bytes(ctx, l, m));
@@ -689,6 +696,16 @@ int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m
   return launch_lds(ctx, a16, l, c, m, ldc, epi, alpha, false, (float *)(ws + abytes));
 }
 
+int launch_to_half(wh_ctx *ctx, const float *x, void *y, size_t n) {
+  if (n % 4 || (uintptr_t)x % 16 || (uintptr_t)y % 8) return wh_fail(ctx, WH_EARG, "to_half: n %% 4 == 0 and aligned buffers");
+  if (!n) return WH_OK;
+  ProfScope prof(ctx, "to_half", 0.0, 6.0 * n);
+  const size_t n4 = n / 4;
+  const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 4096);
+  to_half_kernel<<<blocks, 256, 0, ctx->stream>>>((const float4 *)x, (half4 *)y, n4);
+  return wh_launched(ctx, "to_half");
+}
+
 int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
                   int out16) {
   if (int rc = check(ctx, a16, l, c, m, epi)) return rc;
@@ -701,6 +718,6 @@ int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int
     if (pb && !(part = (float *)wh_scratch(ctx, pb))) return WH_EOOM;
     return launch_lds(ctx, (const _Float16 *)a16, l, c, m, ldc, epi, alpha, out16 != 0, part);
   }
-  if (out16) return wh_fail(ctx, WH_EARG, "gemm: f16 output needs a Q8_0/Q4_0/F16 weight with k %% 64 == 0");
-  return launch_typed<true>(ctx, a16, l, (float *)c, m, ldc, epi, alpha);
+  if (out16) return launch_typed<true, true>(ctx, a16, l, c, m, ldc, epi, alpha);
+  return launch_typed<true, false>(ctx, a16, l, c, m, ldc, epi, alpha);
 }

@@ -78,19 +78,22 @@ int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m
 // epilogues need f32 outputs.
 int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int ldc, int epi,
                   float alpha, int out16);
+// f32 → f16 (RNE) of n values (n % 4 == 0).
+int launch_to_half(wh_ctx *ctx, const float *x, void *y, size_t n);
 int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,
                 int offset);
 int launch_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, const uint32_t *ids,
                  int i, int offset);
-int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *b, float *y, int rows,
-                      int cols, const float *table, float *yr, int head_dim);
+// out16: y (and yr) as f16, for consumers that are GEMMs.
+int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *b, void *y, int rows,
+                      int cols, const float *table, void *yr, int head_dim, int out16 = 0);
 int launch_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int kernel, int stride,
                   int pad, int batch, long x_batch_stride, long col_batch_stride);
 int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb, int kernel,
-                    const float *g, const float *b, int layer_norm, float *y, int t, int ch,
-                    const int *valid_dev, int valid, int batch);
-int launch_attention(wh_ctx *ctx, const float *qk, const float *v, const float *pos, float *o, int t,
-                     int heads, int hd, const int *valid_dev, int valid, int batch);
+                    const float *g, const float *b, int layer_norm, void *y, int t, int ch,
+                    const int *valid_dev, int valid, int batch, int out16 = 0);
+int launch_attention(wh_ctx *ctx, const float *qk, const float *v, const float *pos, void *o, int t,
+                     int heads, int hd, const int *valid_dev, int valid, int batch, int out16 = 0);
 // Scratch bytes launch_attention uses for t frames × batch windows (rel: relative positions).
 size_t attention_scratch_bytes(int t, int heads, int hd, int batch, int rel);
 int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *b0, const float *w,

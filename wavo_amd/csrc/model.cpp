@@ -426,6 +426,8 @@ struct wh_model {
   // Arena (device activations), sized for `cap` encoder frames × `cap_batch` windows.
   int cap = 0, cap_batch = 0;
   float *x = nullptr, *y = nullptr, *h = nullptr, *qk = nullptr, *yr = nullptr, *pos = nullptr, *sub = nullptr;
+  void *pos16 = nullptr;            // Parakeet: the position table as f16 (the pos GEMM's input)
+  const void *pos16_cur = nullptr;  // its rows of this call
   int *valid_dev = nullptr;
   float *sub2 = nullptr;   // Parakeet conv3 output (the subsampling's second buffer)
   float *rope = nullptr;   // GigaAM rope table for `cap` frames
@@ -692,7 +694,7 @@ int parakeet_frames(int mel_frames) { return half_len(half_len(half_len(mel_fram
 int arena(wh_model *m, int frames, int batch) {
   if (frames <= m->cap && batch <= m->cap_batch) return WH_OK;
   int F = (std::max(frames, m->cap) + 63) / 64 * 64, B = std::max(batch, std::max(m->cap_batch, 1));
-  for (float *p : {m->x, m->y, m->h, m->qk, m->yr, m->pos, m->sub, m->sub2, m->rope})
+  for (float *p : {m->x, m->y, m->h, m->qk, m->yr, m->pos, m->sub, m->sub2, m->rope, (float *)m->pos16})
     if (p) {
       wh_free(m->ctx, p);
       for (auto &o : m->owned)
@@ -700,6 +702,7 @@ int arena(wh_model *m, int frames, int batch) {
     }
   if (m->valid_dev) wh_free(m->ctx, m->valid_dev);
   m->x = m->y = m->h = m->qk = m->yr = m->pos = m->sub = m->sub2 = m->rope = nullptr;
+  m->pos16 = nullptr;
   m->valid_dev = nullptr;
   const int d = m->d;
   const size_t rows = (size_t)F * B;
@@ -742,6 +745,9 @@ int arena(wh_model *m, int frames, int batch) {
     // pos_rows(t) rows from row F − t (src/parakeet/encoder.rs:93, :129-131).
     auto table = rel_positions(d, (long)F + 15, 2 * F + 15);
     CK(wh_write(m->ctx, m->pos, table.data(), table.size() * 4));
+    m->pos16 = dev_alloc(m, (table.size() + 1) / 2);
+    if (!m->pos16) return WH_EOOM;
+    CK(launch_to_half(m->ctx, m->pos, m->pos16, table.size()));
   } else if (m->arch == GIGAAM) {
     int hd = d / m->heads;
     auto t = rope_table(F, hd, m->theta);
@@ -755,34 +761,43 @@ int arena(wh_model *m, int frames, int batch) {
 }
 
 // Conformer Block::record (src/conformer.rs:232-265) over `batch` windows of t frames in x; the
-// block's output goes to y.  `valid_dev` (or none) masks keys and conv inputs per window.
+// block's output goes to y.  `valid_dev` (or none) masks keys and conv inputs per window.  The
+// residual stream x stays f32; every activation whose only consumer is a GEMM (the norms' outputs,
+// the first FFN projections, attention and the conv module) is written as f16, the rounding that
+// GEMM applies to its input anyway (src/cpu/gemm.rs:163-176), into f16 views of the arena buffers.
 int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int batch, const int *valid_dev) {
   wh_ctx *c = m->ctx;
   const int d = m->d, hd = d / m->heads, rows = t * batch;
-  CK(launch_layer_norm(c, x, k.norm_ff1.w, k.norm_ff1.b, y, rows, d, nullptr, nullptr, 0));
-  CK(launch_gemm(c, y, k.ff1[0], m->h, rows, k.ff1[0]->cols + k.ff1[0]->dual, WH_SILU, 0.0f));
-  CK(launch_gemm(c, m->h, k.ff1[1], x, rows, k.ff1[1]->cols + k.ff1[1]->dual, WH_RESIDUAL, 0.5f));
+  void *y16 = y, *h16 = m->h;
+  auto g16 = [&](const void *a, const wh_linear *l, void *out, int r, int epi, float alpha, int o16) {
+    return launch_gemm_h(c, a, l, out, r, l->cols + l->dual, epi, alpha, o16);
+  };
+  auto ln16 = [&](const Chan &n) { return launch_layer_norm(c, x, n.w, n.b, y16, rows, d, nullptr, nullptr, 0, 1); };
+  CK(ln16(k.norm_ff1));
+  CK(g16(y16, k.ff1[0], h16, rows, WH_SILU, 0.0f, 1));
+  CK(g16(h16, k.ff1[1], x, rows, WH_RESIDUAL, 0.5f, 0));
   if (!m->relative) {
-    CK(launch_layer_norm(c, x, k.norm_attn.w, k.norm_attn.b, y, rows, d, m->rope, m->yr, hd));
-    CK(launch_gemm(c, m->yr, k.qk, m->qk, rows, k.qk->cols + k.qk->dual, WH_BIAS, 0.0f));
-    CK(launch_gemm(c, y, k.v, m->h, rows, k.v->cols + k.v->dual, WH_BIAS, 0.0f));
-    CK(launch_attention(c, m->qk, m->h, nullptr, y, t, m->heads, hd, valid_dev, t, batch));
+    void *yr16 = m->yr;
+    CK(launch_layer_norm(c, x, k.norm_attn.w, k.norm_attn.b, y16, rows, d, m->rope, yr16, hd, 1));
+    CK(g16(yr16, k.qk, m->qk, rows, WH_BIAS, 0.0f, 0));
+    CK(g16(y16, k.v, m->h, rows, WH_BIAS, 0.0f, 0));
+    CK(launch_attention(c, m->qk, m->h, nullptr, y16, t, m->heads, hd, valid_dev, t, batch, 1));
   } else {
     const int pr = 2 * t + 15;
-    CK(launch_layer_norm(c, x, k.norm_attn.w, k.norm_attn.b, y, rows, d, nullptr, nullptr, 0));
-    CK(launch_gemm(c, y, k.qkv, m->qk, rows, k.qkv->cols + k.qkv->dual, WH_BIAS, 0.0f));
-    CK(launch_gemm(c, m->pos_cur, k.pos, m->yr, pr, k.pos->cols + k.pos->dual, WH_BIAS, 0.0f));
-    CK(launch_attention(c, m->qk, nullptr, m->yr, y, t, m->heads, hd, valid_dev, t, batch));
+    CK(ln16(k.norm_attn));
+    CK(g16(y16, k.qkv, m->qk, rows, WH_BIAS, 0.0f, 0));
+    CK(g16(m->pos16_cur, k.pos, m->yr, pr, WH_BIAS, 0.0f, 0));
+    CK(launch_attention(c, m->qk, nullptr, m->yr, y16, t, m->heads, hd, valid_dev, t, batch, 1));
   }
-  CK(launch_gemm(c, y, k.out, x, rows, k.out->cols + k.out->dual, WH_RESIDUAL, 1.0f));
-  CK(launch_layer_norm(c, x, k.norm_conv.w, k.norm_conv.b, y, rows, d, nullptr, nullptr, 0));
-  CK(launch_gemm(c, y, k.pw1, m->qk, rows, k.pw1->cols + k.pw1->dual, WH_BIAS, 0.0f));
-  CK(launch_conv_glu(c, m->qk, k.dw.w, k.dw.b, m->kernel, k.conv_norm.w, k.conv_norm.b, m->layer_norm_conv, y, t, d,
-                     valid_dev, t, batch));
-  CK(launch_gemm(c, y, k.pw2, x, rows, k.pw2->cols + k.pw2->dual, WH_RESIDUAL, 1.0f));
-  CK(launch_layer_norm(c, x, k.norm_ff2.w, k.norm_ff2.b, y, rows, d, nullptr, nullptr, 0));
-  CK(launch_gemm(c, y, k.ff2[0], m->h, rows, k.ff2[0]->cols + k.ff2[0]->dual, WH_SILU, 0.0f));
-  CK(launch_gemm(c, m->h, k.ff2[1], x, rows, k.ff2[1]->cols + k.ff2[1]->dual, WH_RESIDUAL, 0.5f));
+  CK(g16(y16, k.out, x, rows, WH_RESIDUAL, 1.0f, 0));
+  CK(ln16(k.norm_conv));
+  CK(g16(y16, k.pw1, m->qk, rows, WH_BIAS, 0.0f, 0));
+  CK(launch_conv_glu(c, m->qk, k.dw.w, k.dw.b, m->kernel, k.conv_norm.w, k.conv_norm.b, m->layer_norm_conv, y16, t, d,
+                     valid_dev, t, batch, 1));
+  CK(g16(y16, k.pw2, x, rows, WH_RESIDUAL, 1.0f, 0));
+  CK(ln16(k.norm_ff2));
+  CK(g16(y16, k.ff2[0], h16, rows, WH_SILU, 0.0f, 1));
+  CK(g16(h16, k.ff2[1], x, rows, WH_RESIDUAL, 0.5f, 0));
   // The block output is norm_out(x), not the residual stream.
   return launch_layer_norm(c, x, k.norm_out.w, k.norm_out.b, y, rows, d, nullptr, nullptr, 0);
 }
@@ -816,6 +831,7 @@ int parakeet_encode(wh_model *m, const float *mel, int batch, int mel_frames, co
   if (mel_frames < 3 || t < 1) return fail(m, "too few mel frames");
   CK(arena(m, t, batch));
   m->pos_cur = m->pos + (size_t)(m->cap - t) * d;
+  m->pos16_cur = (const _Float16 *)m->pos16 + (size_t)(m->cap - t) * d;
   wh_ctx *c = m->ctx;
   const int rows1 = 2 * t + 1;  // conv2's output rows from −1 on
   const size_t per = (size_t)rows1 * f2 * ch;
@@ -872,14 +888,16 @@ int whisper_encode(wh_model *m, const float *mel, int mel_frames, float *out) {
   CK(launch_im2col(c, m->h, m->qk, 2 * t, d, 3, 2, 1, 1, 0, 0));
   CK(wh_copy(c, m->x, m->enc_pos, (size_t)t * d * 4));
   CK(lin(m, m->qk, m->wconv1, m->x, t, WH_GELU_RESIDUAL));
+  // Pre-LN blocks; the GEMMs' inputs as f16 (see record_block).
+  void *y16 = m->y, *h16 = m->h;
   for (const WBlock &b : m->wblocks) {
-    CK(launch_layer_norm(c, m->x, b.norm_attn.w, b.norm_attn.b, m->y, t, d, nullptr, nullptr, 0));
-    CK(lin(m, m->y, b.qkv, m->qk, t, WH_BIAS));
-    CK(launch_attention(c, m->qk, nullptr, nullptr, m->y, t, m->heads, hd, nullptr, t, 1));
-    CK(lin(m, m->y, b.out, m->x, t, WH_RESIDUAL, 1.0f));
-    CK(launch_layer_norm(c, m->x, b.norm_ffn.w, b.norm_ffn.b, m->y, t, d, nullptr, nullptr, 0));
-    CK(lin(m, m->y, b.fc1, m->h, t, WH_GELU));
-    CK(lin(m, m->h, b.fc2, m->x, t, WH_RESIDUAL, 1.0f));
+    CK(launch_layer_norm(c, m->x, b.norm_attn.w, b.norm_attn.b, y16, t, d, nullptr, nullptr, 0, 1));
+    CK(launch_gemm_h(c, y16, b.qkv, m->qk, t, b.qkv->cols + b.qkv->dual, WH_BIAS, 0.0f, 0));
+    CK(launch_attention(c, m->qk, nullptr, nullptr, y16, t, m->heads, hd, nullptr, t, 1, 1));
+    CK(launch_gemm_h(c, y16, b.out, m->x, t, b.out->cols + b.out->dual, WH_RESIDUAL, 1.0f, 0));
+    CK(launch_layer_norm(c, m->x, b.norm_ffn.w, b.norm_ffn.b, y16, t, d, nullptr, nullptr, 0, 1));
+    CK(launch_gemm_h(c, y16, b.fc1, h16, t, b.fc1->cols + b.fc1->dual, WH_GELU, 0.0f, 1));
+    CK(launch_gemm_h(c, h16, b.fc2, m->x, t, b.fc2->cols + b.fc2->dual, WH_RESIDUAL, 1.0f, 0));
   }
   return launch_layer_norm(c, m->x, m->enc_norm.w, m->enc_norm.b, out, t, d, nullptr, nullptr, 0);
 }
@@ -1072,7 +1090,10 @@ int wh_model_encode_batch(wh_model *m, const float *mel, int batch, int mel_fram
 int wh_model_blocks(wh_model *m, float *x, int t, int layers) {
   if (!m || !x || t <= 0 || layers < 0 || layers > m->layers || m->arch == WHISPER) return WH_EARG;
   CK(arena(m, t, 1));
-  if (m->arch == PARAKEET) m->pos_cur = m->pos + (size_t)(m->cap - t) * m->d;
+  if (m->arch == PARAKEET) {
+    m->pos_cur = m->pos + (size_t)(m->cap - t) * m->d;
+    m->pos16_cur = (const _Float16 *)m->pos16 + (size_t)(m->cap - t) * m->d;
+  }
   CK(wh_copy(m->ctx, m->x, x, (size_t)t * m->d * 4));
   CK(record_blocks(m, t, 1, nullptr, layers));
   return wh_copy(m->ctx, x, m->x, (size_t)t * m->d * 4);

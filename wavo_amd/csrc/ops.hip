@@ -22,12 +22,20 @@ __device__ __forceinline__ float wave_max(float v) {
 
 constexpr int ROW_REGS = 32;  // row values per lane held in registers: rows up to 2048
 
+__device__ __forceinline__ void store4(float *p, float4 v) { *(float4 *)p = v; }
+__device__ __forceinline__ void store4(_Float16 *p, float4 v) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  *(h4 *)p = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+}
+
 // LayerNorm (eps 1e-5) of row `row`, one wavefront per row; with a table, the NEOX split-half RoPE
-// of each head into yr (ops.wgsl:44-95; src/cpu/ops.rs:68-110).
+// of each head into yr (ops.wgsl:44-95; src/cpu/ops.rs:68-110).  OT = float, or _Float16 when every
+// consumer of y (and yr) is a GEMM, which rounds its input to f16 anyway.
+template <typename OT>
 __global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict__ x, const float *__restrict__ g,
-                                                         const float *__restrict__ b, float *__restrict__ y,
+                                                         const float *__restrict__ b, OT *__restrict__ y,
                                                          int rows, int cols, const float *__restrict__ table,
-                                                         float *__restrict__ yr, int hd) {
+                                                         OT *__restrict__ yr, int hd) {
   extern __shared__ float srow[];  // 4 rows of cols (RoPE only)
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + w;
@@ -54,7 +62,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict
       }
     }
     const float rstd = rsqrtf(wave_sum(q) / (float)cols + 1e-5f);
-    float4 *yy = (float4 *)(y + (size_t)row * cols);
+    OT *yy = y + (size_t)row * cols;
     const float4 *g4 = (const float4 *)g, *b4 = (const float4 *)b;
 #pragma unroll
     for (int j = 0; j < ROW_REGS / 4; j++) {
@@ -65,7 +73,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict
         o.y = (v[j].y - mean) * rstd * gg.y + bb.y;
         o.z = (v[j].z - mean) * rstd * gg.z + bb.z;
         o.w = (v[j].w - mean) * rstd * gg.w + bb.w;
-        yy[i] = o;
+        store4(yy + 4 * i, o);
         if (table) *(float4 *)(sr + 4 * i) = o;
       }
     }
@@ -75,11 +83,11 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict
   if (!active) return;
   const int half = hd / 2;
   const float *tr = table + (size_t)row * hd;
-  float *out = yr + (size_t)row * cols;
+  OT *out = yr + (size_t)row * cols;
   for (int i = lane; i < cols; i += 64) {
     int d = i % hd, f = d % half;
     float c = tr[f], sn = tr[half + f];
-    out[i] = d < half ? sr[i] * c - sr[i + half] * sn : sr[i] * c + sr[i - half] * sn;
+    out[i] = (OT)(d < half ? sr[i] * c - sr[i + half] * sn : sr[i] * c + sr[i - half] * sn);
   }
 }
 
@@ -118,68 +126,116 @@ __global__ void im2col_kernel(const float *__restrict__ x, float *__restrict__ c
 
 // The Conformer conv module between the pointwise convs (ops.wgsl:121-164; src/cpu/ops.rs:137-182):
 // h [t][2ch] → GLU x·σ(gate) (zero from the window's valid frames on) → depthwise conv (odd kernel,
-// centred, w [ch][kernel]) + bias → LayerNorm or affine → SiLU.  A workgroup takes CF frames: it
-// computes the GLU of its frames and the kernel/2 frames either side once into LDS, then one
-// wavefront per frame runs the taps over LDS and the norm over its channels.  Frames are [batch][t];
-// the conv does not cross windows.
-constexpr int CF = 4;
+// centred, w [ch][kernel]) + bias → LayerNorm or affine → SiLU.  A workgroup takes CF consecutive
+// frames of one window with one thread per 4 channels: each thread slides over the CF + kernel − 1
+// frames its outputs need, keeping their GLU values and its 4·kernel taps in registers (the taps of
+// 4 channels are 4·kernel consecutive floats), so h is read once per workgroup plus the kernel − 1
+// frames of overlap.  The norm's row sums go through the wavefront shuffles and LDS.  Frames are
+// [batch][t]; the conv does not cross windows.  OT = float, or _Float16 for a consumer GEMM.
+constexpr int CF = 8;
+constexpr int CG_MAXK = 31;
 
+template <typename OT, int K>
 __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__ h, const float *__restrict__ w,
                                                        const float *__restrict__ wb, int kernel,
                                                        const float *__restrict__ g, const float *__restrict__ gb,
-                                                       int layer_norm, float *__restrict__ y, int t, int ch,
+                                                       int layer_norm, OT *__restrict__ y, int t, int ch,
                                                        const int *__restrict__ valid_dev, int valid) {
-  extern __shared__ float glu[];  // [CF + kernel − 1][ch]
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int SPAN = CF + K - 1;
+  __shared__ float red[2][4][CF];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const int seg = blockIdx.y, f0 = blockIdx.x * CF;
   const int lim = valid_dev ? min(valid_dev[seg], t) : min(valid, t);
-  const int pad = kernel / 2, span = CF + kernel - 1;
+  const int pad = K / 2;
+  const int c = 4 * tid;
+  const bool on = c < ch;
   const float *hs = h + (size_t)seg * t * 2 * ch;
-  for (int e = threadIdx.x; e < span * ch; e += 256) {
-    int r = e / ch, c = e % ch, src = f0 - pad + r;
-    float v = 0.0f;
-    if (src >= 0 && src < lim) {
-      const float *hr = hs + (size_t)src * 2 * ch;
-      v = hr[c] / (1.0f + __expf(-hr[ch + c]));
-    }
-    glu[e] = v;
-  }
-  __syncthreads();
-  const int i = f0 + wave;
-  if (i >= t) return;
-  float acc[16];
-  float s = 0.0f;
+  float4 acc[CF];
+  {
+    float4 tap[K];
+    const float4 bias = on ? *(const float4 *)(wb + c) : make_float4(0, 0, 0, 0);
+    if (on) {
+      // Taps of channels c..c+3: w[(c + q)·K + k] = 4·K consecutive floats from c·K.
+      const float *wc = w + (size_t)c * K;
 #pragma unroll
-  for (int j = 0; j < 16; j++) {
-    int c = lane + 64 * j;
-    float a = 0.0f;
-    if (c < ch) {
-      a = wb[c];
-      for (int k = 0; k < kernel; k++) a += w[c * kernel + k] * glu[(wave + k) * ch + c];
+      for (int k = 0; k < K; k++) tap[k] = make_float4(wc[k], wc[K + k], wc[2 * K + k], wc[3 * K + k]);
     }
-    acc[j] = a;
-    s += a;
+#pragma unroll
+    for (int i = 0; i < CF; i++) acc[i] = bias;
+#pragma unroll
+    for (int r = 0; r < SPAN; r++) {
+      const int src = f0 - pad + r;
+      float4 v = make_float4(0, 0, 0, 0);
+      if (on && src >= 0 && src < lim) {
+        const float4 x = *(const float4 *)(hs + (size_t)src * 2 * ch + c);
+        const float4 gt = *(const float4 *)(hs + (size_t)src * 2 * ch + ch + c);
+        v.x = x.x / (1.0f + __expf(-gt.x));
+        v.y = x.y / (1.0f + __expf(-gt.y));
+        v.z = x.z / (1.0f + __expf(-gt.z));
+        v.w = x.w / (1.0f + __expf(-gt.w));
+      }
+      // Output frame i takes tap k = r − i.
+#pragma unroll
+      for (int i = 0; i < CF; i++) {
+        const int k = r - i;
+        if (k >= 0 && k < K) {
+          acc[i].x += tap[k].x * v.x;
+          acc[i].y += tap[k].y * v.y;
+          acc[i].z += tap[k].z * v.z;
+          acc[i].w += tap[k].w * v.w;
+        }
+      }
+    }
   }
-  float mean = 0.0f, rstd = 1.0f;
+  float mean[CF], rstd[CF];
+#pragma unroll
+  for (int i = 0; i < CF; i++) mean[i] = 0.0f, rstd[i] = 1.0f;
   if (layer_norm) {
-    mean = wave_sum(s) / (float)ch;
-    float q = 0.0f;
+    // Mean, then the variance about it, over the ch channels of each frame.
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-      int c = lane + 64 * j;
-      float d = c < ch ? acc[j] - mean : 0.0f;
-      q += d * d;
+    for (int i = 0; i < CF; i++) {
+      const float s = on ? (acc[i].x + acc[i].y) + (acc[i].z + acc[i].w) : 0.0f;
+      const float ws = wave_sum(s);
+      if (lane == 0) red[0][wave][i] = ws;
     }
-    rstd = rsqrtf(wave_sum(q) / (float)ch + 1e-5f);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CF; i++) {
+      float s = 0.0f;
+      for (int q = 0; q < nw; q++) s += red[0][q][i];
+      mean[i] = s / (float)ch;
+      float qv = 0.0f;
+      if (on) {
+        const float dx = acc[i].x - mean[i], dy = acc[i].y - mean[i], dz = acc[i].z - mean[i], dw = acc[i].w - mean[i];
+        qv = (dx * dx + dy * dy) + (dz * dz + dw * dw);
+      }
+      const float ws = wave_sum(qv);
+      if (lane == 0) red[1][wave][i] = ws;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CF; i++) {
+      float s = 0.0f;
+      for (int q = 0; q < nw; q++) s += red[1][q][i];
+      rstd[i] = rsqrtf(s / (float)ch + 1e-5f);
+    }
   }
-  float *yy = y + ((size_t)seg * t + i) * ch;
+  if (!on) return;
+  const float4 gg = *(const float4 *)(g + c), bb = *(const float4 *)(gb + c);
 #pragma unroll
-  for (int j = 0; j < 16; j++) {
-    int c = lane + 64 * j;
-    if (c < ch) {
-      float v = (acc[j] - mean) * rstd * g[c] + gb[c];
-      yy[c] = v / (1.0f + __expf(-v));
-    }
+  for (int i = 0; i < CF; i++) {
+    const int f = f0 + i;
+    if (f >= t) break;
+    float4 v;
+    v.x = (acc[i].x - mean[i]) * rstd[i] * gg.x + bb.x;
+    v.y = (acc[i].y - mean[i]) * rstd[i] * gg.y + bb.y;
+    v.z = (acc[i].z - mean[i]) * rstd[i] * gg.z + bb.z;
+    v.w = (acc[i].w - mean[i]) * rstd[i] * gg.w + bb.w;
+    v.x = v.x / (1.0f + __expf(-v.x));
+    v.y = v.y / (1.0f + __expf(-v.y));
+    v.z = v.z / (1.0f + __expf(-v.z));
+    v.w = v.w / (1.0f + __expf(-v.w));
+    store4(y + ((size_t)seg * t + f) * ch + c, v);
   }
 }
 
@@ -302,21 +358,27 @@ __global__ void add_kernel(float *x, const float *a, size_t n) {
 
 }  // namespace
 
-int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *b, float *y, int rows,
-                      int cols, const float *table, float *yr, int hd) {
+int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *b, void *y, int rows,
+                      int cols, const float *table, void *yr, int hd, int out16) {
   if (rows < 0 || cols <= 0 || (rows && (!x || !g || !b || !y)))
     return wh_fail(ctx, WH_EARG, "layer_norm: bad arguments (%d x %d)", rows, cols);
   if (table && (!yr || hd <= 0 || hd % 2 || cols % hd))
     return wh_fail(ctx, WH_EARG, "layer_norm: rope needs cols %% head_dim == 0 and even head_dim");
   if (!rows) return WH_OK;
-  ProfScope prof(ctx, "layer_norm", 0.0, 4.0 * rows * cols * (table ? 3 : 2));
+  ProfScope prof(ctx, "layer_norm", 0.0, (double)rows * cols * (4 + (out16 ? 2 : 4) * (table ? 2 : 1)));
   if (cols <= ROW_REGS * 64 && cols % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 &&
       (uintptr_t)g % 16 == 0 && (uintptr_t)b % 16 == 0) {
     size_t lds = table ? (size_t)4 * cols * sizeof(float) : 0;
-    layer_norm_kernel<<<(rows + 3) / 4, 256, lds, ctx->stream>>>(x, g, b, y, rows, cols, table, yr, hd);
+    if (out16)
+      layer_norm_kernel<_Float16><<<(rows + 3) / 4, 256, lds, ctx->stream>>>(x, g, b, (_Float16 *)y, rows, cols, table,
+                                                                             (_Float16 *)yr, hd);
+    else
+      layer_norm_kernel<float><<<(rows + 3) / 4, 256, lds, ctx->stream>>>(x, g, b, (float *)y, rows, cols, table,
+                                                                          (float *)yr, hd);
   } else {
-    if (table) return wh_fail(ctx, WH_EARG, "layer_norm: rope rows need cols %% 4 == 0, at most %d", ROW_REGS * 64);
-    layer_norm_long<<<rows, 64, 0, ctx->stream>>>(x, g, b, y, cols);
+    if (table || out16)
+      return wh_fail(ctx, WH_EARG, "layer_norm: rope and f16 rows need cols %% 4 == 0, at most %d", ROW_REGS * 64);
+    layer_norm_long<<<rows, 64, 0, ctx->stream>>>(x, g, b, (float *)y, cols);
   }
   return wh_launched(ctx, "layer_norm");
 }
@@ -333,17 +395,39 @@ int launch_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int ke
   return wh_launched(ctx, "im2col");
 }
 
+template <typename OT>
+static void conv_glu_k(wh_ctx *ctx, dim3 grid, int threads, const float *h, const float *w, const float *wb, int kernel,
+                const float *g, const float *b, int layer_norm, OT *y, int t, int ch, const int *valid_dev, int valid) {
+#define CG(K)                                                                                                      \
+  case K:                                                                                                          \
+    conv_glu_kernel<OT, K><<<grid, threads, 0, ctx->stream>>>(h, w, wb, kernel, g, b, layer_norm, y, t, ch, valid_dev, \
+                                                              valid);                                              \
+    break;
+  switch (kernel) {
+    CG(1) CG(3) CG(5) CG(7) CG(9) CG(11) CG(13) CG(15) CG(17) CG(19) CG(21) CG(23) CG(25) CG(27) CG(29) CG(31)
+  }
+#undef CG
+}
+
 int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb, int kernel, const float *g,
-                    const float *b, int layer_norm, float *y, int t, int ch, const int *valid_dev, int valid,
-                    int batch) {
-  if (t <= 0 || ch <= 0 || ch > 1024 || kernel <= 0 || kernel % 2 == 0 || batch <= 0)
-    return wh_fail(ctx, WH_EARG, "conv_glu: bad shape (t %d, ch %d, kernel %d)", t, ch, kernel);
-  int frames = t * batch;
-  if ((size_t)(CF + kernel - 1) * ch * 4 > 160 * 1024) return wh_fail(ctx, WH_EARG, "conv_glu: kernel %d too large", kernel);
-  ProfScope prof(ctx, "conv_glu", 0.0, 12.0 * frames * ch);
+                    const float *b, int layer_norm, void *y, int t, int ch, const int *valid_dev, int valid,
+                    int batch, int out16) {
+  if (t <= 0 || ch <= 0 || ch > 1024 || ch % 4 || kernel <= 0 || kernel % 2 == 0 || kernel > CG_MAXK || batch <= 0)
+    return wh_fail(ctx, WH_EARG, "conv_glu: bad shape (t %d, ch %d, kernel %d): ch %% 4 == 0, ch <= 1024, odd kernel <= %d",
+                   t, ch, kernel, CG_MAXK);
+  if ((uintptr_t)h % 16 || (uintptr_t)w % 16 || (uintptr_t)wb % 16 || (uintptr_t)g % 16 || (uintptr_t)b % 16 ||
+      (uintptr_t)y % 16)
+    return wh_fail(ctx, WH_EARG, "conv_glu: buffers must be 16-byte aligned");
+  const int frames = t * batch;
+  ProfScope prof(ctx, "conv_glu", 0.0, (8.0 + (out16 ? 2.0 : 4.0)) * frames * ch);
   dim3 grid((t + CF - 1) / CF, batch);
-  conv_glu_kernel<<<grid, 64 * CF, (size_t)(CF + kernel - 1) * ch * 4, ctx->stream>>>(
-      h, w, wb, kernel, g, b, layer_norm, y, t, ch, valid_dev, valid < 0 ? t : valid);
+  const int threads = (ch / 4 + 63) / 64 * 64;
+  if (out16)
+    conv_glu_k<_Float16>(ctx, grid, threads, h, w, wb, kernel, g, b, layer_norm, (_Float16 *)y, t, ch, valid_dev,
+                         valid < 0 ? t : valid);
+  else
+    conv_glu_k<float>(ctx, grid, threads, h, w, wb, kernel, g, b, layer_norm, (float *)y, t, ch, valid_dev,
+                      valid < 0 ? t : valid);
   return wh_launched(ctx, "conv_glu");
 }
 

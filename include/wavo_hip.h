@@ -78,12 +78,17 @@ int wh_read(wh_ctx *ctx, void *host, const void *dptr, size_t bytes);
 int wh_sync(wh_ctx *ctx);
 /* The context's hipStream_t as an opaque pointer, for callers that time with HIP events. */
 void *wh_stream(wh_ctx *ctx);
-/* Per-launch profiling (no counterpart in the reference, whose timing lives in `wavo bench` and GPU
- * timestamp queries, docs/perf.md:54): with on != 0 every kernel launch gets HIP events on the
- * stream around it; wh_profile_read waits, then writes JSON text: per kernel variant its launches,
- * total milliseconds and algorithmic flops and bytes.  Turning it on or off clears the records. */
-int wh_profile(wh_ctx *ctx, int on);
+/* Profiling (no counterpart in the reference, whose timing lives in `wavo bench` and GPU timestamp
+ * queries, docs/perf.md:54).  mode 1: every kernel launch gets HIP events on the stream around it
+ * (each pair adds the event's own overhead, a few microseconds, to what it measures); mode 2: only
+ * the regions bracketed by wh_region.  wh_profile_read waits, then writes JSON text: per kernel
+ * variant or region name its count, total milliseconds and algorithmic flops and bytes.  Setting
+ * the mode clears the records. */
+int wh_profile(wh_ctx *ctx, int mode);
 int wh_profile_read(wh_ctx *ctx, char *out, size_t len);
+/* Begins (name != NULL) or ends (name == NULL, with the region's algorithmic flops and bytes) a
+ * timed region: HIP events on the stream around whatever is queued in between. */
+int wh_region(wh_ctx *ctx, const char *name, double flops, double bytes);
 
 /* -------------------------------------------------------------------------------- weights */
 
@@ -119,6 +124,12 @@ void wh_linear_free(wh_ctx *ctx, wh_linear *l);
  * epi(0); dual columns get acc + bias with no epilogue.  Residual modes read c. */
 int wh_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int epi,
             float alpha);
+/* wh_gemm with `a` already rounded to f16 (a16: m rows of k halves) and, with out16 != 0, f16
+ * outputs (not for the residual epilogues, which accumulate into f32): the form the graph drivers
+ * use between ops whose consumer is a GEMM.  No counterpart in the reference, whose GEMM reads f32
+ * and rounds it (gemm.wgsl:1-9). */
+int wh_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int epi,
+              float alpha, int out16);
 /* Pass::gemv (src/gpu/mod.rs:1461-1467): c[offset + j] = epi(a·W[j] + b[j]) for one row a, W not
  * rounded. */
 int wh_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,

@@ -41,12 +41,14 @@ SIGNATURES = {
     "wh_stream": (_vp, [_vp]),
     "wh_profile": (_i, [_vp, _i]),
     "wh_profile_read": (_i, [_vp, ctypes.c_char_p, _sz]),
+    "wh_region": (_i, [_vp, ctypes.c_char_p, ctypes.c_double, ctypes.c_double]),
     "wh_linear_new": (_i, [_vp, _vp, _i, _vp, _i, _i, ctypes.POINTER(_vp)]),
     "wh_linear_width": (_i, [_vp]),
     "wh_linear_k": (_i, [_vp]),
     "wh_linear_type": (_i, [_vp]),
     "wh_linear_free": (None, [_vp, _vp]),
     "wh_gemm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),
+    "wh_gemm_h": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _i]),
     "wh_gemv": (_i, [_vp, _vp, _vp, _vp, _i, _f, _i]),
     "wh_embed": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
     "wh_layer_norm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _i]),
@@ -181,8 +183,15 @@ class Gpu:
     def stream(self):
         return lib().wh_stream(self.h)
 
-    def profile(self, on):
-        self._check(lib().wh_profile(self.h, int(on)))
+    def profile(self, mode):
+        """0 off, 1 (or True) events around every launch, 2 named regions only (wh_region)."""
+        self._check(lib().wh_profile(self.h, int(mode)))
+
+    def region_begin(self, name):
+        self._check(lib().wh_region(self.h, name.encode(), 0.0, 0.0))
+
+    def region_end(self, flops=0.0, nbytes=0.0):
+        self._check(lib().wh_region(self.h, None, float(flops), float(nbytes)))
 
     def profile_read(self):
         """Per kernel variant: launches, total ms, algorithmic flops and bytes (profiled launches)."""
@@ -235,6 +244,10 @@ class Gpu:
     # -- Pass ops
     def gemm(self, a, l, c, m, epi, alpha=0.0):
         self._check(lib().wh_gemm(self.h, _p(a), l.h, _p(c), m, epi, alpha))
+
+    def gemm_h(self, a16, l, c, m, epi, alpha=0.0, out16=False):
+        """Pass::gemm with `a` already f16 (and f16 outputs with out16)."""
+        self._check(lib().wh_gemm_h(self.h, _p(a16), l.h, _p(c), int(m), int(epi), float(alpha), int(out16)))
 
     def gemv(self, a, l, c, epi, alpha=0.0, offset=0):
         self._check(lib().wh_gemv(self.h, _p(a), l.h, _p(c), epi, alpha, offset))

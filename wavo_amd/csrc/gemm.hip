@@ -280,6 +280,14 @@ __device__ __forceinline__ void dma4(const void *src, uint32_t lds) {
                : "memory");
 }
 __device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// The same from a wave-uniform base address (SGPRs) plus a per-lane 32-bit byte offset, so that a
+// loop moves the whole DMA by scalar adds.  `lds` must be wave-uniform (it goes to M0).
+__device__ __forceinline__ void dma16s(const void *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4s(const void *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
 
 // Two f16 values 1024 + byte0, 1024 + byte1 of x (bytes 0-1, or 2-3 with HI).
 template <bool HI>
@@ -329,175 +337,287 @@ struct LdsArgs {
   size_t row_bytes;
 };
 
+// s_waitcnt with vmcnt = N (0..63) and no wait on the other counters (gfx9 encoding: vmcnt bits
+// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // c tile BM × BN per workgroup of WM × WN wavefronts, each a (BM/WM) × (BN/WN) block of 32×32 MFMA
-// tiles, over the k range of split blockIdx.z (k / gridDim.z, a multiple of BK).  Two LDS stages
-// of BK-wide k steps: the DMA of step kt + 1 runs while the MFMAs work on step kt.  Stage layout:
-// a rows of BK/8 16-byte chunks (chunk c of row r at (c + r) % (BK/8), so the 8 lanes that read one
-// chunk column of 8 rows hit distinct banks), then W: F16 rows like a, or quantized rows of BK/64
-// block pairs (68 or 36 bytes each).  At substep s of block pair p, the lane of MFMA column n and k
-// half g takes k slots 64p + 32g + 8s .. + 8 — block 2p + g of its W row — and the a fragments the
-// same slots.
-template <int WT, int BM, int BN, int WM, int WN, int BK, bool SPLIT, bool OUT16>
+// tiles, over the k range of split blockIdx.z (k / gridDim.z, a multiple of 64).
+//
+// Pipeline.  The k loop moves in 64-wide steps through a ring of NS LDS stages that the LDS DMA
+// fills NS − 1 steps ahead (from scalar base addresses: a step costs the vector units nothing but
+// the dequantization).  At the top of step kt the wavefronts wait for stage kt + 1 and meet at one
+// barrier; then each issues the DMA of step kt + NS − 1 into the stage freed by step kt − 1, the LDS
+// reads of step kt + 1 into its second register set, and the dequantization and MFMAs of step kt
+// from the first — so LDS latency hides behind the matrix cores.  Each wavefront issues the same
+// number of DMA instructions per step (a wave without an instruction of its own repeats another
+// wave's: identical bytes to the same place), so a vmcnt immediate waits for exactly one step.
+//
+// Stage layout: a rows of 8 16-byte chunks, chunk c of row r at (c + r/2) % 8 — the 16 lanes that
+// LDS serves together read 16 rows and hit all 64 banks once — then W: F16 rows like a, or
+// quantized rows of one block pair (68 or 36 bytes, as stored).  At substep s, the lane of MFMA
+// column n and k half g takes k slots 32g + 8s .. + 8 — block g of its W row's pair — and the a
+// fragments the same slots.  With WM = 1 every W block of the tile is dequantized once.
+//
+// Epilogue.  The accumulators go through LDS (f32, rows padded so the two lane halves of a tile hit
+// distinct banks) and leave as 8 consecutive columns per lane: 16-byte loads of c for the residual
+// modes and 16-byte stores, with the bias, the epilogue, the dual columns and the padding columns
+// (epi(0 + bias), as the reference's zero rows give) applied on the way.
+template <int WT, int BM, int BN, int WM, int WN, int NSQ, bool SPLIT, bool OUT16>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
   static_assert(TM >= 1 && TN >= 1, "32×32 MFMA tiles per wave");
-  constexpr int PAIRS = BK / 64;
+  constexpr int BK = 64;
   constexpr int PAIR1 = WT == WH_Q8_0 ? 68 : WT == WH_Q4_0 ? 36 : 128;  // bytes of 64 weights
   constexpr bool WCH = WT == WH_F16;                                     // W moves in 16-byte chunks
-  constexpr int ACH = BK / 8;                                            // 16-byte chunks per a row
-  constexpr int A_BYTES = BM * BK * 2, W_BYTES = BN * PAIR1 * PAIRS, STAGE = A_BYTES + W_BYTES;
-  static_assert(STAGE % 16 == 0 && (WCH || W_BYTES % 256 == 0), "whole DMA instructions");
-  constexpr int NIA = BM * ACH / 64;                            // a: 16-byte DMA instructions per stage
-  constexpr int NIW = WCH ? BN * ACH / 64 : W_BYTES / 256;      // W: 16-byte or 4-byte ones
+  constexpr int A_BYTES = BM * BK * 2, W_BYTES = BN * PAIR1, STAGE = (A_BYTES + W_BYTES + 15) / 16 * 16;
+  constexpr int CROW = BN + 8;                                           // f32 per epilogue LDS row
+  constexpr int C_BYTES = BM * CROW * 4;
+  // NSQ stages asked for, as many as fit in the 160 KiB of LDS.
+  constexpr int NS = NSQ * STAGE + 16 <= 160 * 1024 ? NSQ : (160 * 1024 - 16) / STAGE;
+  static_assert(NS >= 3, "at least three stages");
+  static_assert(WCH || W_BYTES % 256 == 0, "whole DMA instructions");
+  constexpr int NIA = BM / 8;                                   // a: 16-byte DMA instructions per stage
+  constexpr int NIW = WCH ? BN / 8 : W_BYTES / 256;             // W: 16-byte or 4-byte ones
   constexpr int PA = (NIA + NW - 1) / NW, PW = (NIW + NW - 1) / NW;
+  constexpr int VM = (NS - 3) * (PA + PW);                      // DMA instructions of the later steps
+  static_assert(VM < 64, "vmcnt holds the DMA of NS - 3 steps");
   // (+16: the odd block of the last W row reads one dword past its row, unused)
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE + 16];
+  constexpr int LDS_BYTES = NS * STAGE + 16 > C_BYTES ? NS * STAGE + 16 : C_BYTES;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
   const int wm = (wave / WN) * (BM / WM), wn = (wave % WN) * (BN / WN);
   const int lrow = lane & 31, g = lane >> 5;
   const int m = P.m, k = P.k, rows = P.rows;
   const int nk = k / BK / gridDim.z, kz = blockIdx.z * nk;
 
-  // DMA sources of this lane at k step 0 (rows past m or rows are clamped: their products land
-  // in outputs that are discarded or zeroed).
-  const uint8_t *asrc[PA];
+  // Per-lane byte offsets of this wave's DMA instructions from the step's base addresses (rows past
+  // m or rows are clamped: their products land in outputs that are discarded or zeroed), and the
+  // instructions' LDS offsets in a stage.
+  uint32_t aoff[PA], alds[PA];
 #pragma unroll
   for (int i = 0; i < PA; i++) {
-    const int n = min(wave + NW * i, NIA - 1), r = (64 * n + lane) / ACH, lc = ((lane % ACH) - r) & (ACH - 1);
-    asrc[i] = (const uint8_t *)P.a + ((size_t)min(m0 + r, m - 1) * k + (size_t)kz * BK + 8 * lc) * 2;
+    const int n = (wave + NW * i) % NIA, r = 8 * n + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
+    aoff[i] = (uint32_t)(((size_t)min(m0 + r, m - 1) * k + 8 * lc) * 2);
+    alds[i] = 1024 * n;
   }
-  const uint8_t *wsrc[PW];
+  uint32_t woff[PW], wlds[PW];
 #pragma unroll
   for (int i = 0; i < PW; i++) {
-    const int n = min(wave + NW * i, NIW - 1);
+    const int n = (wave + NW * i) % NIW;
     if constexpr (WCH) {
-      const int r = (64 * n + lane) / ACH, lc = ((lane % ACH) - r) & (ACH - 1);
-      wsrc[i] = P.w + (size_t)min(n0 + r, rows - 1) * P.row_bytes + (size_t)kz * BK * 2 + 16 * lc;
+      const int r = 8 * n + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
+      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * lc);
+      wlds[i] = A_BYTES + 1024 * n;
     } else {
-      const int s = 64 * n + lane, r = s / (PAIRS * PAIR1 / 4), dwi = s % (PAIRS * PAIR1 / 4);
-      wsrc[i] = P.w + (size_t)min(n0 + r, rows - 1) * P.row_bytes + (size_t)kz * PAIRS * PAIR1 + 4 * dwi;
+      const int sidx = 64 * n + lane, r = sidx / (PAIR1 / 4), dwi = sidx % (PAIR1 / 4);
+      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 4 * dwi);
+      wlds[i] = A_BYTES + 256 * n;
     }
   }
+  const uint8_t *abase = (const uint8_t *)P.a + (size_t)kz * BK * 2;
+  const uint8_t *wbase = P.w + (size_t)kz * (WCH ? BK * 2 : PAIR1);
   const uint32_t lds0 = lds_addr(lds);
   auto issue = [&](int kt) {
-    const uint32_t st = lds0 + (kt & 1) * STAGE;
+    const uint32_t st = lds0 + (kt % NS) * STAGE;
+    const uint8_t *ab = abase + (size_t)kt * BK * 2, *wb = wbase + (size_t)kt * (WCH ? BK * 2 : PAIR1);
 #pragma unroll
-    for (int i = 0; i < PA; i++) {
-      const int n = wave + NW * i;
-      if (n < NIA) dma16(asrc[i] + (size_t)kt * BK * 2, st + 1024 * n);
-    }
+    for (int i = 0; i < PA; i++) dma16s(ab, aoff[i], st + alds[i]);
 #pragma unroll
     for (int i = 0; i < PW; i++) {
-      const int n = wave + NW * i;
-      if (n < NIW) {
-        if constexpr (WCH) dma16(wsrc[i] + (size_t)kt * BK * 2, st + A_BYTES + 1024 * n);
-        else dma4(wsrc[i] + (size_t)kt * PAIRS * PAIR1, st + A_BYTES + 256 * n);
-      }
+      if constexpr (WCH) dma16s(wb, woff[i], st + wlds[i]);
+      else dma4s(wb, woff[i], st + wlds[i]);
     }
   };
 
+  // One step's operands in registers: the a fragments of the 4 substeps and the W rows' data
+  // (quantized: the pair's dwords of the lane's block and its scale; F16: the fragments).
+  constexpr int ND = WT == WH_Q8_0 ? 9 : 5;
+  struct Regs {
+    half8 a[4][TM];
+    uint32_t dw[TN][WCH ? 1 : ND];
+    uint32_t sc[TN];
+    half8 b[WCH ? 4 : 1][TN];
+  };
+  // LDS half offsets of the lane's a rows and W rows within a stage (rotation r/2 applied per chunk).
+  int arow[TM], wrow[TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++) arow[i] = wm + 32 * i + lrow;
+#pragma unroll
+  for (int j = 0; j < TN; j++) wrow[j] = wn + 32 * j + lrow;
+  auto load = [&](Regs &R, int kt) {
+    const uint8_t *st = lds + (kt % NS) * STAGE;
+    const _Float16 *as = (const _Float16 *)st;
+    if constexpr (!WCH) {
+      constexpr int BLK = PAIR1 / 2;
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        // Even block: scale in the low half of dword 0, data from byte 2; odd block (bytes
+        // BLK..): scale in the high half of the dword before byte BLK + 2, where its data starts.
+        const uint32_t *row = (const uint32_t *)(st + A_BYTES) + wrow[j] * (PAIR1 / 4);
+        const uint32_t *p = row + (g ? (BLK + 2) / 4 : 0);
+        R.sc[j] = g ? row[(BLK + 2) / 4 - 1] : row[0];
+#pragma unroll
+        for (int i = 0; i < ND; i++) R.dw[j][i] = p[i];
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const int lc = 4 * g + s;
+#pragma unroll
+      for (int i = 0; i < TM; i++) R.a[s][i] = *(const half8 *)(as + arow[i] * BK + 8 * ((lc + (arow[i] >> 1)) & 7));
+      if constexpr (WCH)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+          R.b[s][j] = *(const half8 *)((const _Float16 *)(st + A_BYTES) + wrow[j] * BK + 8 * ((lc + (wrow[j] >> 1)) & 7));
+    }
+  };
   floatx16 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
     for (int j = 0; j < TN; j++) acc[i][j] = floatx16{};
-
-  if (nk > 0) issue(0);
-  for (int kt = 0; kt < nk; kt++) {
-    dma_wait();
-    __syncthreads();
-    if (kt + 1 < nk) issue(kt + 1);
-    const uint8_t *st = lds + (kt & 1) * STAGE;
-    const _Float16 *as = (const _Float16 *)st;
+  auto compute = [&](const Regs &R) {
+    half2 d2[TN];
+    const uint32_t sh = g ? 0u : 2u;
+    if constexpr (!WCH)
 #pragma unroll
-    for (int pp = 0; pp < PAIRS; pp++) {
-      // This pair's blocks of the wave's W rows (quantized): data dwords, shift and scale.
-      constexpr int ND = WT == WH_Q8_0 ? 9 : 5;
-      uint32_t dw[TN][ND];
-      half2 d2[TN];
-      const uint32_t sh = g ? 0u : 2u;
-      if constexpr (!WCH) {
-        constexpr int BLK = PAIR1 / 2;
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-          // Even block: scale in the low half of dword 0, data from byte 2; odd block (bytes
-          // BLK..): scale in the high half of the dword before byte BLK + 2, where its data starts.
-          const uint32_t *row = (const uint32_t *)(st + A_BYTES) + (wn + 32 * j + lrow) * (PAIRS * PAIR1 / 4) + pp * (PAIR1 / 4);
-          const uint32_t *p = row + (g ? (BLK + 2) / 4 : 0);
-          const uint32_t sc = g ? row[(BLK + 2) / 4 - 1] >> 16 : row[0] & 0xffffu;
-#pragma unroll
-          for (int i = 0; i < ND; i++) dw[j][i] = p[i];
-          const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)sc);
-          d2[j] = half2{d, d};
-        }
+      for (int j = 0; j < TN; j++) {
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(g ? R.sc[j] >> 16 : R.sc[j] & 0xffffu));
+        d2[j] = half2{d, d};
       }
 #pragma unroll
-      for (int s = 0; s < 4; s++) {
-        half8 af[TM], bf[TN];
-        const int lc = 8 * pp + 4 * g + s;
+    for (int s = 0; s < 4; s++) {
+      half8 bf[TN];
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-          if constexpr (WCH) {
-            const int r = wn + 32 * j + lrow;
-            bf[j] = *(const half8 *)((const _Float16 *)(st + A_BYTES) + r * BK + 8 * ((lc + r) & (ACH - 1)));
-          } else {
-            bf[j] = dequant_frag<WT>(dw[j], sh, d2[j], s);
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-          const int r = wm + 32 * i + lrow;
-          af[i] = *(const half8 *)(as + r * BK + 8 * ((lc + r) & (ACH - 1)));
-        }
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-          for (int j = 0; j < TN; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < TN; j++) {
+        if constexpr (WCH) bf[j] = R.b[s][j];
+        else bf[j] = dequant_frag<WT>(R.dw[j], sh, d2[j], s);
       }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(R.a[s][i], bf[j], acc[i][j], 0, 0, 0);
     }
+  };
+  // Top of step kt: stage kt + 1 (if any) has landed for every wavefront, and every wavefront is
+  // done with the stage of step kt − 1 (its registers were loaded during step kt − 2).
+  auto top = [&](int kt) {
+    if (kt + 1 < nk) {
+      if (kt + NS - 2 < nk) wait_vm<VM>();
+      else dma_wait();
+    }
+    __syncthreads();
+    if (kt + NS - 1 < nk) issue(kt + NS - 1);
+  };
+
+  Regs r0, r1;
+#pragma unroll
+  for (int s = 0; s < NS - 1; s++)
+    if (s < nk) issue(s);
+  static_assert((NS - 2) * (PA + PW) < 64, "vmcnt holds the DMA of NS - 2 steps");
+  if (nk > 0) {
+    if (nk - 1 >= NS - 2) wait_vm<(NS - 2) * (PA + PW)>();  // stages 1 .. NS - 2 may be in flight
+    else dma_wait();
+    __syncthreads();
+    load(r0, 0);
+  }
+  // Two steps per iteration so that the register sets alternate without copies.
+  for (int kt = 0; kt < nk; kt += 2) {
+    top(kt);
+    if (kt + 1 < nk) load(r1, kt + 1);
+    compute(r0);
+    if (kt + 1 >= nk) break;
+    top(kt + 1);
+    if (kt + 2 < nk) load(r0, kt + 2);
+    compute(r1);
   }
 
-  // D[i][j] of a 32×32 tile sits in lane j (mod 32), register v: i = 8·(v/4) + 4·(lane/32) + v%4.
-  // Columns past the real W rows (padding) get epi(0 + bias) as the reference's zero rows do.
+  // Epilogue through LDS: every DMA has landed (the last step waited for it) and the barrier below
+  // ends every wavefront's reads of the stages.
+  __syncthreads();
+  float *cl = (float *)lds;
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < TN; j++) {
-      const int col = n0 + wn + 32 * j + lrow;
-      if (col >= P.cols) continue;
-      if constexpr (SPLIT) {
-        float *cp = (float *)P.c + (size_t)blockIdx.z * m * P.cols + col;
+    for (int j = 0; j < TN; j++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-          const int row = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
-          if (row < m) cp[(size_t)row * P.cols] = acc[i][j][v];
-        }
-        continue;
-      }
-      const bool pad = col >= rows;
-      const float bv = P.bias[col];
-      const float b2 = col < P.dual ? P.bias[P.cols + col] : 0.0f;
+      for (int v = 0; v < 16; v++)
+        cl[(wm + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow] = acc[i][j][v];
+  __syncthreads();
+  constexpr int G8 = BN / 8;  // 8-column groups per row
+  for (int e = tid; e < BM * G8; e += 64 * NW) {
+    const int r = e / G8, c8 = 8 * (e % G8), row = m0 + r, col = n0 + c8;
+    if (row >= m || col >= P.cols) continue;  // cols % 32 == 0: a group is inside or past
+    const float4 x0 = *(const float4 *)(cl + r * CROW + c8), x1 = *(const float4 *)(cl + r * CROW + c8 + 4);
+    float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    if constexpr (SPLIT) {
+      float *cp = (float *)P.c + ((size_t)blockIdx.z * m + row) * P.cols + col;
+      *(float4 *)cp = x0;
+      *(float4 *)(cp + 4) = x1;
+      continue;
+    }
 #pragma unroll
-      for (int v = 0; v < 16; v++) {
-        const int row = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
-        if (row >= m) continue;
-        const float x = pad ? 0.0f : acc[i][j][v];
-        const size_t at = (size_t)row * P.ldc + col;
-        if constexpr (OUT16) {
-          _Float16 *cp = (_Float16 *)P.c + at;
-          *cp = (_Float16)epilogue(P.epi, P.alpha, x + bv, nullptr);
-          if (col < P.dual) cp[P.cols] = (_Float16)(x + b2);
-        } else {
-          float *cp = (float *)P.c + at;
-          *cp = epilogue(P.epi, P.alpha, x + bv, cp);
-          if (col < P.dual) cp[P.cols] = x + b2;
-        }
+    for (int q = 0; q < 8; q++)
+      if (col + q >= rows) x[q] = 0.0f;
+    const float4 b0 = *(const float4 *)(P.bias + col), b1 = *(const float4 *)(P.bias + col + 4);
+    const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const size_t at = (size_t)row * P.ldc + col;
+    float y[8];
+    if (!OUT16 && (P.epi == WH_RESIDUAL || P.epi == WH_GELU_RESIDUAL)) {
+      const float4 c0 = *(const float4 *)((const float *)P.c + at), c1 = *(const float4 *)((const float *)P.c + at + 4);
+      const float cc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      if (P.epi == WH_RESIDUAL)
+#pragma unroll
+        for (int q = 0; q < 8; q++) y[q] = cc[q] + P.alpha * (x[q] + bb[q]);
+      else
+#pragma unroll
+        for (int q = 0; q < 8; q++) y[q] = cc[q] + gelu(x[q] + bb[q]);
+    } else {
+      switch (P.epi) {
+#define EPI_CASE(E)                                                               \
+  case E:                                                                         \
+    _Pragma("unroll") for (int q = 0; q < 8; q++) y[q] = epilogue(E, 0.0f, x[q] + bb[q], nullptr); \
+    break;
+        EPI_CASE(WH_SILU)
+        EPI_CASE(WH_RELU)
+        EPI_CASE(WH_GELU)
+        EPI_CASE(WH_TANH)
+#undef EPI_CASE
+        default:
+#pragma unroll
+          for (int q = 0; q < 8; q++) y[q] = x[q] + bb[q];
       }
     }
+    const bool dual = col < P.dual;  // dual % 8 == 0 is not required: per column below
+    if constexpr (OUT16) {
+      half8 h;
+#pragma unroll
+      for (int q = 0; q < 8; q++) h[q] = (_Float16)y[q];
+      *(half8 *)((_Float16 *)P.c + at) = h;
+    } else {
+      *(float4 *)((float *)P.c + at) = make_float4(y[0], y[1], y[2], y[3]);
+      *(float4 *)((float *)P.c + at + 4) = make_float4(y[4], y[5], y[6], y[7]);
+    }
+    if (dual) {
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        if (col + q >= P.dual) break;
+        const float d = x[q] + P.bias[P.cols + col + q];
+        if constexpr (OUT16) ((_Float16 *)P.c)[at + P.cols + q] = (_Float16)d;
+        else ((float *)P.c)[at + P.cols + q] = d;
+      }
+    }
+  }
 }
 
 // Split-k finish: c = epi(Σ_z part[z] + bias) with the partial sums added in split order (the same
@@ -535,35 +655,32 @@ __global__ __launch_bounds__(256) void to_half_kernel(const float4 *__restrict__
 
 // Launch shapes of the LDS-DMA kernel (tile, wavefronts, k step, split).
 struct Plan {
-  int bm, bn, wm, wn, bk, split;
+  int bm, bn, wm, wn, ns, split;
 };
 
-// Chosen per GEMM shape from measurements on MI355X (one workgroup resident per CU at a time):
-// many output tiles → 128×128 tiles of 8 wavefronts; a few hundred → the same with 128-wide k steps;
-// fewer → 64×64 tiles of 4 wavefronts, and when even those leave CUs idle, k split 2 or 4 ways.
+// Chosen per GEMM shape from measurements on MI355X: many output tiles → 128×128 tiles of 8
+// wavefronts; fewer → 64×64 tiles of 4 wavefronts, and when even those leave CUs idle, k split 2
+// or 4 ways.  NS LDS stages of 64-wide k steps.
 Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
   const int cus = ctx->cus > 0 ? ctx->cus : 256;
   const long t128 = (long)((cols + 127) / 128) * ((m + 127) / 128), t64 = (long)((cols + 63) / 64) * ((m + 63) / 64);
-  Plan p{64, 64, 2, 2, 128, 1};
-  if (t128 >= 2L * cus) p = {128, 128, 2, 4, 64, 1};
-  else if (t128 >= cus / 2) p = {128, 128, 2, 4, 128, 1};
+  Plan p{64, 64, 2, 2, 4, 1};
+  if (t128 >= cus / 2) p = {128, 128, 2, 4, 4, 1};
   else if (t64 < cus)
-    while (p.split < 4 && t64 * p.split < 2L * cus && k % (2 * p.split * p.bk) == 0) p.split *= 2;
-  if (k % p.bk) p.bk = 64;
-  if (ctx->gemm_bm) {  // tuning override: the tile, with 8 wavefronts for 128×128
-    p.bm = ctx->gemm_bm, p.bn = ctx->gemm_bn, p.split = 1;
-    p.wm = 2, p.wn = p.bm == 128 && p.bn == 128 ? 4 : 2;
-    if (p.bm != p.bn) p.bk = 128;
-    if (k % p.bk) p.bm = p.bn = 64, p.bk = 64, p.wn = 2;
+    while (p.split < 4 && t64 * p.split < 2L * cus && k % (2 * p.split * 64) == 0) p.split *= 2;
+  if (ctx->gemm_plan[0]) {  // tuning override (WAVO_GEMM_PLAN): bm, bn, wm, wn, stages, split
+    const int *o = ctx->gemm_plan;
+    p = {o[0], o[1], o[2], o[3], o[4], o[5]};
+    if (k % (64 * p.split)) p.split = 1;
   }
   return p;
 }
 
-template <int WT, int BM, int BN, int WM, int WN, int BK>
+template <int WT, int BM, int BN, int WM, int WN, int NS>
 void lds_launch(wh_ctx *ctx, dim3 grid, const LdsArgs &a, bool split, bool out16) {
-  if (split) gemm_lds_kernel<WT, BM, BN, WM, WN, BK, true, false><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
-  else if (out16) gemm_lds_kernel<WT, BM, BN, WM, WN, BK, false, true><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
-  else gemm_lds_kernel<WT, BM, BN, WM, WN, BK, false, false><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
+  if (split) gemm_lds_kernel<WT, BM, BN, WM, WN, NS, true, false><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
+  else if (out16) gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, true><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
+  else gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, false><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
 }
 
 template <int WT>
@@ -576,19 +693,32 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
   dim3 grid((l->cols + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.split);
   static const char *tn = WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
   char name[64];
-  snprintf(name, sizeof name, "gemm_%s_%dx%d%s", tn, p.bm, p.bn, p.split > 1 ? (p.split == 2 ? "_k2" : "_k4") : "");
+  snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s", tn, p.bm, p.bn, p.wm, p.wn, p.ns,
+           p.split > 1 ? (p.split == 2 ? "_s2" : "_s4") : "");
   const double width = l->cols + l->dual;
   const double bytes = (double)l->rows * l->row_bytes + 2.0 * m * l->k +
                        (out16 ? 2.0 : 4.0) * m * width * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
   {
     ProfScope prof(ctx, name, 2.0 * m * l->rows * l->k, bytes);
     const bool sp = p.split > 1;
-    if (p.bm == 128 && p.bn == 128 && p.bk == 64) lds_launch<WT, 128, 128, 2, 4, 64>(ctx, grid, args, sp, out16);
-    else if (p.bm == 128 && p.bn == 128) lds_launch<WT, 128, 128, 2, 4, 128>(ctx, grid, args, sp, out16);
-    else if (p.bm == 64 && p.bn == 128) lds_launch<WT, 64, 128, 2, 2, 128>(ctx, grid, args, sp, out16);
-    else if (p.bm == 128) lds_launch<WT, 128, 64, 2, 2, 128>(ctx, grid, args, sp, out16);
-    else if (p.bk == 64) lds_launch<WT, 64, 64, 2, 2, 64>(ctx, grid, args, sp, out16);
-    else lds_launch<WT, 64, 64, 2, 2, 128>(ctx, grid, args, sp, out16);
+    bool ok = false;
+#define PLAN(BM, BN, WM, WN, NS)                                                           \
+  if (!ok && p.bm == BM && p.bn == BN && p.wm == WM && p.wn == WN && p.ns == NS) {          \
+    lds_launch<WT, BM, BN, WM, WN, NS>(ctx, grid, args, sp, out16);                         \
+    ok = true;                                                                               \
+  }
+    PLAN(128, 128, 2, 4, 4)
+    PLAN(128, 128, 1, 4, 4)
+    PLAN(128, 128, 1, 4, 6)
+    PLAN(128, 256, 1, 4, 4)
+    PLAN(128, 256, 1, 8, 4)
+    PLAN(64, 64, 2, 2, 4)
+    PLAN(64, 64, 2, 2, 8)
+    PLAN(64, 128, 1, 4, 6)
+    PLAN(128, 64, 1, 2, 4)
+    PLAN(64, 64, 1, 2, 6)
+#undef PLAN
+    if (!ok) return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages", p.bm, p.bn, p.wm, p.wn, p.ns);
     if (int rc = wh_launched(ctx, "gemm")) return rc;
   }
   if (p.split > 1) {
@@ -604,8 +734,11 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
   return WH_OK;
 }
 
-bool lds_path(const wh_linear *l) {
-  return l->k % 64 == 0 && (l->type == WH_Q8_0 || l->type == WH_Q4_0 || l->type == WH_F16) && l->row_bytes % 4 == 0;
+// The main kernel's conditions: 64-wide k steps over Q8_0 / Q4_0 / F16 rows, and an output whose
+// rows start on 16 bytes (its epilogue stores 8 columns at a time).
+bool lds_path(const wh_linear *l, const void *c, int ldc) {
+  return l->k % 64 == 0 && (l->type == WH_Q8_0 || l->type == WH_Q4_0 || l->type == WH_F16) && l->row_bytes % 4 == 0 &&
+         ldc % 8 == 0 && (uintptr_t)c % 16 == 0;
 }
 
 // Scratch bytes for the split-k partial sums of an m-row GEMM (0 when it does not split).
@@ -680,7 +813,7 @@ static int check(wh_ctx *ctx, const void *a, const wh_linear *l, const void *c, 
 int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int ldc, int epi, float alpha) {
   if (int rc = check(ctx, a, l, c, m, epi)) return rc;
   if (m == 0) return WH_OK;
-  if (!lds_path(l)) return launch_typed<false, false>(ctx, a, l, c, m, ldc, epi, alpha);
+  if (!lds_path(l, c, ldc)) return launch_typed<false, false>(ctx, a, l, c, m, ldc, epi, alpha);
   // The main kernel takes a in f16: round it once into scratch (followed by the split partials).
   const size_t n = (size_t)m * l->k, abytes = (n * 2 + 255) / 256 * 256;
   uint8_t *ws = (uint8_t *)wh_scratch(ctx, abytes + split_bytes(ctx, l, m));
@@ -712,7 +845,7 @@ int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int
   if (out16 && (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL))
     return wh_fail(ctx, WH_EARG, "gemm: residual epilogues accumulate into f32 outputs");
   if (m == 0) return WH_OK;
-  if (lds_path(l)) {
+  if (lds_path(l, c, ldc)) {
     const size_t pb = split_bytes(ctx, l, m);
     float *part = nullptr;
     if (pb && !(part = (float *)wh_scratch(ctx, pb))) return WH_EOOM;

@@ -21,13 +21,14 @@ struct wh_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   int cus = 0;
-  // GEMM tile override from WAVO_GEMM_TILE ("128x128", "64x128", "128x64", "64x64"; tuning sweeps
-  // only): 0 = chosen per shape.
-  int gemm_bm = 0, gemm_bn = 0;
+  // GEMM launch-plan override from WAVO_GEMM_PLAN ("bm,bn,wm,wn,bk,split"; tuning sweeps only):
+  // all zero = chosen per shape.
+  int gemm_plan[6] = {0, 0, 0, 0, 0, 0};
   std::string name;
   std::string error;
-  // Per-launch profiling (wh_profile): off by default.
-  bool prof = false;
+  // Profiling (wh_profile): 0 off (default), 1 events around every launch, 2 named regions only.
+  int prof = 0;
+  int open_region = -1;
   std::vector<hipEvent_t> events;
   size_t next_event = 0;
   std::vector<wh_prof_rec> recs;
@@ -92,8 +93,10 @@ int launch_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int ke
 int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb, int kernel,
                     const float *g, const float *b, int layer_norm, void *y, int t, int ch,
                     const int *valid_dev, int valid, int batch, int out16 = 0);
-int launch_attention(wh_ctx *ctx, const float *qk, const float *v, const float *pos, void *o, int t,
-                     int heads, int hd, const int *valid_dev, int valid, int batch, int out16 = 0);
+// qk / v / pos are f32 (in16 == 0) or f16; o is f32 or f16 (out16).
+int launch_attention(wh_ctx *ctx, const void *qk, const void *v, const void *pos, void *o, int t,
+                     int heads, int hd, const int *valid_dev, int valid, int batch, int out16 = 0,
+                     int in16 = 0);
 // Scratch bytes launch_attention uses for t frames × batch windows (rel: relative positions).
 size_t attention_scratch_bytes(int t, int heads, int hd, int batch, int rel);
 int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *b0, const float *w,

@@ -779,15 +779,15 @@ int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int bat
   if (!m->relative) {
     void *yr16 = m->yr;
     CK(launch_layer_norm(c, x, k.norm_attn.w, k.norm_attn.b, y16, rows, d, m->rope, yr16, hd, 1));
-    CK(g16(yr16, k.qk, m->qk, rows, WH_BIAS, 0.0f, 0));
-    CK(g16(y16, k.v, m->h, rows, WH_BIAS, 0.0f, 0));
-    CK(launch_attention(c, m->qk, m->h, nullptr, y16, t, m->heads, hd, valid_dev, t, batch, 1));
+    CK(g16(yr16, k.qk, m->qk, rows, WH_BIAS, 0.0f, 1));
+    CK(g16(y16, k.v, m->h, rows, WH_BIAS, 0.0f, 1));
+    CK(launch_attention(c, m->qk, m->h, nullptr, y16, t, m->heads, hd, valid_dev, t, batch, 1, 1));
   } else {
     const int pr = 2 * t + 15;
     CK(ln16(k.norm_attn));
-    CK(g16(y16, k.qkv, m->qk, rows, WH_BIAS, 0.0f, 0));
-    CK(g16(m->pos16_cur, k.pos, m->yr, pr, WH_BIAS, 0.0f, 0));
-    CK(launch_attention(c, m->qk, nullptr, m->yr, y16, t, m->heads, hd, valid_dev, t, batch, 1));
+    CK(g16(y16, k.qkv, m->qk, rows, WH_BIAS, 0.0f, 1));
+    CK(g16(m->pos16_cur, k.pos, m->yr, pr, WH_BIAS, 0.0f, 1));
+    CK(launch_attention(c, m->qk, nullptr, m->yr, y16, t, m->heads, hd, valid_dev, t, batch, 1, 1));
   }
   CK(g16(y16, k.out, x, rows, WH_RESIDUAL, 1.0f, 0));
   CK(ln16(k.norm_conv));
@@ -892,8 +892,8 @@ int whisper_encode(wh_model *m, const float *mel, int mel_frames, float *out) {
   void *y16 = m->y, *h16 = m->h;
   for (const WBlock &b : m->wblocks) {
     CK(launch_layer_norm(c, m->x, b.norm_attn.w, b.norm_attn.b, y16, t, d, nullptr, nullptr, 0, 1));
-    CK(launch_gemm_h(c, y16, b.qkv, m->qk, t, b.qkv->cols + b.qkv->dual, WH_BIAS, 0.0f, 0));
-    CK(launch_attention(c, m->qk, nullptr, nullptr, y16, t, m->heads, hd, nullptr, t, 1, 1));
+    CK(launch_gemm_h(c, y16, b.qkv, m->qk, t, b.qkv->cols + b.qkv->dual, WH_BIAS, 0.0f, 1));
+    CK(launch_attention(c, m->qk, nullptr, nullptr, y16, t, m->heads, hd, nullptr, t, 1, 1, 1));
     CK(launch_gemm_h(c, y16, b.out, m->x, t, b.out->cols + b.out->dual, WH_RESIDUAL, 1.0f, 0));
     CK(launch_layer_norm(c, m->x, b.norm_ffn.w, b.norm_ffn.b, y16, t, d, nullptr, nullptr, 0, 1));
     CK(launch_gemm_h(c, y16, b.fc1, h16, t, b.fc1->cols + b.fc1->dual, WH_GELU, 0.0f, 1));

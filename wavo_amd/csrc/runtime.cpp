@@ -40,7 +40,7 @@ static int prof_event(wh_ctx *ctx) {
 }
 
 ProfScope::ProfScope(wh_ctx *c, const char *kernel, double flops, double bytes) : ctx(c) {
-  if (!ctx || !ctx->prof) return;
+  if (!ctx || ctx->prof != 1) return;
   wh_prof_rec r;
   r.kernel = kernel;
   r.flops = flops;
@@ -107,10 +107,10 @@ int wh_open(int device_index, wh_ctx **out) {
   ctx->device = dev;
   ctx->cus = p.multiProcessorCount;
   ctx->name = p.name;
-  if (const char *t = getenv("WAVO_GEMM_TILE")) {
-    int bm = 0, bn = 0;
-    if (sscanf(t, "%dx%d", &bm, &bn) == 2 && (bm == 64 || bm == 128) && (bn == 64 || bn == 128))
-      ctx->gemm_bm = bm, ctx->gemm_bn = bn;
+  if (const char *t = getenv("WAVO_GEMM_PLAN")) {
+    int *o = ctx->gemm_plan;
+    if (sscanf(t, "%d,%d,%d,%d,%d,%d", &o[0], &o[1], &o[2], &o[3], &o[4], &o[5]) != 6 || o[5] < 1 || o[5] > 4)
+      for (int i = 0; i < 6; i++) o[i] = 0;
   }
   if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
     delete ctx;
@@ -207,13 +207,37 @@ int wh_read(wh_ctx *ctx, void *host, const void *dptr, size_t bytes) {
 
 void *wh_stream(wh_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 
-int wh_profile(wh_ctx *ctx, int on) {
-  if (!ctx) return WH_EARG;
+int wh_profile(wh_ctx *ctx, int mode) {
+  if (!ctx || mode < 0 || mode > 2) return WH_EARG;
   int rc = wh_sync(ctx);
   if (rc) return rc;
-  ctx->prof = on != 0;
+  ctx->prof = mode;
   ctx->recs.clear();
   ctx->next_event = 0;
+  ctx->open_region = -1;
+  return WH_OK;
+}
+
+int wh_region(wh_ctx *ctx, const char *name, double flops, double bytes) {
+  if (!ctx || !ctx->prof) return ctx ? WH_OK : WH_EARG;
+  if (name) {  // begin
+    if (ctx->open_region >= 0) return wh_fail(ctx, WH_EARG, "wh_region: a region is open");
+    wh_prof_rec r;
+    r.kernel = name;
+    r.ev0 = prof_event(ctx);
+    r.ev1 = prof_event(ctx);
+    if (r.ev0 < 0 || r.ev1 < 0) return wh_fail(ctx, WH_EGPU, "wh_region: event creation failed");
+    if (hipEventRecord(ctx->events[r.ev0], ctx->stream) != hipSuccess) return wh_fail(ctx, WH_EGPU, "wh_region: event record failed");
+    ctx->open_region = (int)ctx->recs.size();
+    ctx->recs.push_back(r);
+    return WH_OK;
+  }
+  if (ctx->open_region < 0) return wh_fail(ctx, WH_EARG, "wh_region: no open region");
+  wh_prof_rec &r = ctx->recs[ctx->open_region];
+  r.flops = flops;
+  r.bytes = bytes;
+  ctx->open_region = -1;
+  if (hipEventRecord(ctx->events[r.ev1], ctx->stream) != hipSuccess) return wh_fail(ctx, WH_EGPU, "wh_region: event record failed");
   return WH_OK;
 }
 
@@ -363,6 +387,11 @@ void wh_linear_free(wh_ctx *ctx, wh_linear *l) {
 int wh_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int epi, float alpha) {
   if (!ctx || !l) return WH_EARG;
   return launch_gemm(ctx, a, l, c, m, l->cols + l->dual, epi, alpha);
+}
+
+int wh_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int epi, float alpha, int out16) {
+  if (!ctx || !l) return WH_EARG;
+  return launch_gemm_h(ctx, a16, l, c, m, l->cols + l->dual, epi, alpha, out16);
 }
 
 int wh_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,

@@ -5,18 +5,30 @@ A step is one encoder call over 60 s of synthetic audio: the 128-bin log-mel (60
 HBM before the timed region) → 8× subsampling → 24 Conformer blocks (d 1024, 8 heads of 128, relative
 positions, FFN 4096, conv kernel 9) → the joint's encoder projection, all GEMM weights q8_0 (random
 N(0, 0.02), written as a GGUF file and loaded through the C ABI).  value = audio seconds per second
-of encoder time (RTFx), timed over --steps calls after --warmup.
+of encoder time (RTFx), timed over --steps calls after --warmup (HIP events on the library's stream
+around the whole timed region; the calls after the second replay a recorded HIP graph of the step).
 
-`roofline` is the dominant kernel of the step (by total time in a profiled step: HIP events around each
-launch on the library's stream), its algorithmic flops (2·M·N·K summed over its launches) over its
-measured time, against MI355X's dense fp16 MFMA peak.  `cpu_baseline` is the C parity oracle (the
-restated wavo CPU backend, portable f16-rounded arithmetic, AVX2+FMA, OpenMP) on the same model and
-mel, one full call, timed on this host.
+`roofline` is the dominant q8_0 GEMM of the step: the (kernel variant, call shape) with the most time
+in a profiled step.  Its average launch duration is measured by launching that exact configuration
+(same tile plan, m × n × k, epilogue and output type; random q8_0 weights of the same shape) 50 times
+back to back between two HIP events on the library's stream — events around every single launch would
+add their own few microseconds to each — and `achieved` = 2·m·n·k per launch over that duration, against
+MI355X's dense fp16 MFMA peak.  `traffic` is that launch's HBM bytes from rocprofv3 FETCH_SIZE /
+WRITE_SIZE passes (profiles/), when a summary for the same configuration is committed there.
+
+`gemv` is the Whisper-large-v3-turbo decoder's per-token matrix-vector products (q8_0; 4 layers of
+qkv 3840×1280, self_out / cross_q / cross_out 1280×1280, fc1 5120×1280, fc2 1280×5120, and the
+51866-row head), timed cold: two copies of the weights (2 × 168 MB, past the 256 MB Infinity Cache)
+alternate, and achieved bytes per second of the weights as stored is reported against HBM peak.
+
+`cpu_baseline` is the C parity oracle (the restated wavo CPU backend, portable f16-rounded arithmetic,
+AVX2+FMA, OpenMP) on the same model and mel, one full call, timed on this host.
 """
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -26,10 +38,130 @@ sys.path.insert(0, ROOT)
 METRIC = "encoder RTFx (audio s/s) at 1 MI355X; q8_0 GEMM % MFMA peak; GEMV % HBM BW"
 PEAK_F16 = 2500.0     # TFLOP/s, MI355X dense fp16 MFMA
 PEAK_HBM = 8000.0     # GB/s
+GEMM_NAME = re.compile(r"^gemm_(\w+?)_(\d+)x(\d+)_w(\d+)x(\d+)_n(\d+)(_s\d)? (\d+)x(\d+)x(\d+) e(\d+) (f16|f32) w(\d+)$")
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def time_region(gpu, fn, reps):
+    """Milliseconds per call of fn() over `reps` back-to-back calls between two events."""
+    gpu.profile(2)
+    gpu.region_begin("batch")
+    for _ in range(reps):
+        fn()
+    gpu.region_end()
+    ms = gpu.profile_read()[0]["ms"]
+    gpu.profile(0)
+    return ms / reps
+
+
+def gemm_replay(gpu, name, reps=50):
+    """Re-launches the GEMM configuration `name` (a profile record) back to back; returns us/launch."""
+    import numpy as np
+
+    import wavo_amd as wa
+    from wavo_amd import gguf
+
+    g = GEMM_NAME.match(name)
+    tn, bm, bn, wm, wn, ns, split, m, n, k, epi, out, width = g.groups()
+    wtype = {"q8_0": wa.Q8_0, "q4_0": wa.Q4_0, "f16": wa.F16}[tn]
+    rng = np.random.default_rng(5)
+    w = gguf.encode(rng.standard_normal(int(n) * int(k), dtype=np.float32) * np.float32(0.02), wtype)
+    f16 = out == "f16"
+    plan = f"{bm},{bn},{wm},{wn},{ns},{split[2:] if split else 1}"
+    os.environ["WAVO_GEMM_PLAN"] = plan  # the same launch plan as in the step
+    import wavo_amd
+
+    g2 = wavo_amd.Gpu(0)
+    os.environ.pop("WAVO_GEMM_PLAN")
+    lin2 = g2.linear([(w, wtype, int(k), int(n))], np.zeros(int(width), np.float32))
+    a2 = g2.upload(rng.standard_normal((int(m), int(k)), dtype=np.float32).astype(np.float16))
+    c2 = g2.buffer(int(m) * int(width))
+    run = lambda: g2.gemm_h(a2, lin2, c2, int(m), int(epi), 0.5, out16=f16)
+    for _ in range(5):
+        run()
+    g2.sync()
+    us = time_region(g2, run, reps) * 1e3
+    del lin2, a2, c2
+    g2.close()
+    return us, 2.0 * int(m) * int(n) * int(k)
+
+
+def gemv_cold(gpu):
+    """Whisper decoder GEMVs per token, q8_0, two weight copies alternating (cold)."""
+    import numpy as np
+
+    import wavo_amd as wa
+    from wavo_amd import gguf
+
+    d, ff, vocab, layers = 1280, 5120, 51866, 4
+    shapes = []
+    for _ in range(layers):
+        shapes += [(3 * d, d, wa.BIAS), (d, d, wa.RESIDUAL), (d, d, wa.BIAS), (d, d, wa.RESIDUAL),
+                   (ff, d, wa.GELU), (d, ff, wa.RESIDUAL)]
+    shapes.append((vocab, d, wa.BIAS))
+    rng = np.random.default_rng(9)
+    raw = {}
+    for (n, k, _) in set(shapes):
+        raw[(n, k)] = gguf.encode(rng.standard_normal(n * k, dtype=np.float32) * np.float32(0.02), wa.Q8_0)
+    copies = [[gpu.linear([(raw[(n, k)], wa.Q8_0, k, n)], np.zeros(n, np.float32)) for (n, k, _) in shapes]
+              for _ in range(2)]
+    x = gpu.upload(rng.standard_normal(ff, dtype=np.float32))
+    y = gpu.upload(np.zeros(vocab + 64, np.float32))
+    wbytes = sum(n * k // 32 * 34 for (n, k, _) in shapes)
+
+    def token(i):
+        for lin, (n, k, e) in zip(copies[i % 2], shapes):
+            gpu.gemv(x, lin, y, e, 1.0)
+
+    for i in range(4):
+        token(i)
+    gpu.sync()
+    reps = 20
+    state = {"i": 0}
+
+    def one():
+        token(state["i"])
+        state["i"] += 1
+
+    ms = time_region(gpu, one, reps)
+    # The head alone (70.6 MB), cold.
+    head = [c[-1] for c in copies]
+    st2 = {"i": 0}
+
+    def one_head():
+        gpu.gemv(x, head[st2["i"] % 2], y, wa.BIAS)
+        st2["i"] += 1
+
+    for _ in range(4):
+        one_head()
+    hms = time_region(gpu, one_head, 40)
+    hbytes = vocab * d // 32 * 34
+    out = {"workload": "whisper-large-v3-turbo decoder GEMVs per token, q8_0, cold (2 weight copies of 168 MB alternate)",
+           "launches_per_token": len(shapes), "us_per_token": round(ms * 1e3, 2), "weight_bytes": wbytes,
+           "achieved": round(wbytes / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM, "unit": "GB/s",
+           "frac": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM, 4),
+           "head": {"shape": f"{vocab}x{d}", "us": round(hms * 1e3, 2), "bytes": hbytes,
+                    "achieved": round(hbytes / (hms * 1e-3) / 1e9, 1),
+                    "frac": round(hbytes / (hms * 1e-3) / 1e9 / PEAK_HBM, 4)}}
+    del copies
+    return out
+
+
+def traffic_for(name):
+    """HBM bytes per launch for this GEMM configuration from a committed rocprofv3 summary, if any."""
+    path = os.path.join(ROOT, "profiles", "gemm_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic ") and name in line:
+            try:
+                return json.loads(line.split(" ", 1)[1].split(" | ", 1)[1])
+            except (ValueError, IndexError):
+                return None
+    return None
 
 
 def main():
@@ -39,6 +171,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seconds", type=float, default=60.0, help="audio per step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the decoder GEMV measurement")
+    ap.add_argument("--replay", action="store_true",
+                    help="only the dominant GEMM configuration's back-to-back launches (for rocprofv3 passes)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -58,7 +193,7 @@ def main():
     gpu = wa.Gpu(0)
     t0 = time.time()
     model = wa.Model(gpu, path)
-    log(f"loaded on {gpu.name} ({gpu.cus} CUs) in {time.time() - t0:.1f} s")
+    log(f"loaded on {gpu.name or 'gfx950'} ({gpu.cus} CUs) in {time.time() - t0:.1f} s")
     pcm = synth.audio(args.seconds, seed=1)
     mel = synth.parakeet_mel(pcm)
     mel_frames = mel.shape[0]
@@ -66,33 +201,42 @@ def main():
     melb = gpu.upload(mel)
     outb = gpu.buffer(frames * width)
 
-    for _ in range(args.warmup):
-        model.encode_device(melb, mel_frames, outb)
-    gpu.sync()
-    log(f"warmup done ({args.warmup} steps), timing {args.steps}")
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        model.encode_device(melb, mel_frames, outb)
-    gpu.sync()
-    dt = (time.perf_counter() - t0) / args.steps
-    rtfx = args.seconds / dt
-    log(f"{dt * 1e3:.3f} ms per step, RTFx {rtfx:.0f}")
+    if not args.replay:
+        for _ in range(args.warmup):
+            model.encode_device(melb, mel_frames, outb)
+        gpu.sync()
+        log(f"warmup done ({args.warmup} steps), timing {args.steps}")
+        t0 = time.perf_counter()
+        ms_ev = time_region(gpu, lambda: model.encode_device(melb, mel_frames, outb), args.steps)
+        wall = (time.perf_counter() - t0) / args.steps
+        dt = ms_ev * 1e-3
+        rtfx = args.seconds / dt
+        log(f"{dt * 1e3:.3f} ms per step (events; wall {wall * 1e3:.3f}), RTFx {rtfx:.0f}")
 
-    # One profiled step: per-kernel time and algorithmic work.
-    gpu.profile(True)
+    # One profiled step: per-kernel launches and algorithmic work (events around each launch).
+    gpu.profile(1)
     model.encode_device(melb, mel_frames, outb)
     prof = gpu.profile_read()
-    gpu.profile(False)
-    total_ms = sum(k["ms"] for k in prof)
-    by_family = {}
+    gpu.profile(0)
+    gemms = [k for k in prof if GEMM_NAME.match(k["kernel"])]
+    dom = max(gemms, key=lambda k: k["ms"])
+    us, flops = gemm_replay(gpu, dom["kernel"])
+    log(f"dominant GEMM {dom['kernel']}: {dom['launches']} launches per step, {us:.2f} us per launch back to back")
+    if args.replay:
+        print(json.dumps({"replayed": dom["kernel"], "us_per_launch": us}), flush=True)
+        gpu.close()
+        return
+
+    achieved = flops / (us * 1e-6) / 1e12
+    fam = {}
     for k in prof:
-        fam = k["kernel"].split("_")[0] if k["kernel"].startswith("gemm") else k["kernel"]
-        by_family[fam] = by_family.get(fam, 0.0) + k["ms"]
-    dom = max(prof, key=lambda k: k["ms"])
-    q8 = [k for k in prof if k["kernel"].startswith("gemm_q8_0")]
-    gemm_flops = sum(k["flops"] for k in q8)
-    gemm_ms = sum(k["ms"] for k in q8)
-    achieved = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
+        f = k["kernel"].split(" ")[0]
+        e = fam.setdefault(f, [0, 0.0])
+        e[0] += k["launches"]
+        e[1] += k["ms"]
+    q8 = [k for k in gemms if k["kernel"].startswith("gemm_q8_0")]
+    q8_flops = sum(k["flops"] for k in q8)
+    q8_ms = sum(k["ms"] for k in q8)
     roofline = {
         "bound": "mfma",
         "kernel": dom["kernel"],
@@ -100,16 +244,19 @@ def main():
         "peak": PEAK_F16,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_F16, 4),
-        "traffic": None,
+        "traffic": traffic_for(dom["kernel"]),
         "launches_per_step": dom["launches"],
-        "avg_launch_us": round(dom["ms"] * 1e3 / dom["launches"], 2),
-        "flops_per_launch": dom["flops"] / dom["launches"],
-        "all_q8_0_gemm": {"ms": round(gemm_ms, 4), "tflops": round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 2),
-                          "frac": round(gemm_flops / (gemm_ms * 1e-3) / 1e12 / PEAK_F16, 4)},
+        "avg_launch_us": round(us, 2),
+        "flops_per_launch": flops,
+        "timing": "50 back-to-back launches of this configuration between two HIP events on the library's stream",
+        "all_q8_0_gemm_profiled": {"launches": sum(k["launches"] for k in q8), "ms": round(q8_ms, 4),
+                                   "tflops_incl_event_overhead": round(q8_flops / (q8_ms * 1e-3) / 1e12, 2)},
     }
-    # The step's kernels, summed per family (ms per step), and what the launches leave out.
-    breakdown = {k: round(v, 4) for k, v in sorted(by_family.items(), key=lambda x: -x[1])}
-    breakdown["gaps"] = round(dt * 1e3 - total_ms, 4)
+    breakdown = {f: {"launches": n, "ms": round(ms, 4)} for f, (n, ms) in sorted(fam.items(), key=lambda x: -x[1][1])}
+
+    gemv = None if args.no_gemv else gemv_cold(gpu)
+    if gemv:
+        log(f"GEMV per token {gemv['us_per_token']} us, {gemv['achieved']} GB/s ({gemv['frac'] * 100:.1f}% of HBM)")
 
     cpu = None
     if not args.no_cpu:
@@ -145,10 +292,12 @@ def main():
                    "audio_s": args.seconds, "mel_frames": mel_frames, "encoder_frames": frames,
                    "layers": model.layers, "d_model": model.d, "weights": "q8_0"},
         "roofline": roofline,
+        "gemv": gemv,
         "cpu_baseline": cpu,
-        "breakdown_ms": breakdown,
+        "profiled_step_ms": breakdown,
     }
     print(json.dumps(out), flush=True)
+    model.free()
     gpu.close()
 
 

@@ -207,6 +207,12 @@ int wh_model_encode(wh_model *m, const float *mel_dev, int mel_frames, int valid
  * src/ane/mod.rs:463-466).  mel_dev [batch][mel_frames][mels] → out_dev [batch][frames][width]. */
 int wh_model_encode_batch(wh_model *m, const float *mel_dev, int batch, int mel_frames,
                           const int *valid, float *out_dev);
+/* Replay of repeated encoder calls (no counterpart in the reference, whose wgpu passes are recorded
+ * anew per call, src/gpu/mod.rs:906-1002).  With on != 0 (the default) the second wh_model_encode /
+ * wh_model_encode_batch call with the same arguments (same device buffers and sizes) is recorded
+ * into a HIP graph and later such calls replay it: the same kernels in the same order, without
+ * their host-side launch cost.  on == 0 drops the recordings and launches every call eagerly. */
+int wh_model_graphs(wh_model *m, int on);
 /* Conformer blocks only, over x_dev [t][d] in place (layers = how many of them). */
 int wh_model_blocks(wh_model *m, float *x_dev, int t, int layers);
 /* Greedy token ids of an encoder output on the host: CTC (GigaAM, src/gigaam/decoder.rs:135-151)

@@ -138,3 +138,32 @@ def test_gigaam_full_config(gpu):
     err = rel_l2(got, want)
     assert err < ENCODER_TOL, err
     check_ctc(m, full, want)
+
+
+@pytest.mark.parametrize("name", ["parakeet", "gigaam", "whisper"])
+def test_graph_replays_equal_eager_calls(gpu, name):
+    # The second call with the same buffers is recorded into a HIP graph and later ones replay it.
+    # Every replay, with the program's own eager work and synchronizations between them, must give
+    # the eager call's bytes exactly (the same kernels in the same order).
+    path = synth.model_path(name, small=True, directory=MODELS)
+    m = wa.Model(gpu, path)
+    mel = {"parakeet": synth.parakeet_mel, "gigaam": synth.gigaam_mel}.get(name, None)
+    if mel is None:
+        mel = synth.whisper_mel(synth.audio(2, 3), mels=80, frames=200)
+    else:
+        mel = mel(synth.audio(3, 3))
+    frames, width = m.frames(mel.shape[0])
+    melb, outb = gpu.upload(mel), gpu.buffer(frames * width)
+    m.graphs(False)
+    m.encode_device(melb, mel.shape[0], outb)
+    eager = gpu.read(outb, (frames, width)).copy()
+    m.graphs(True)
+    other = gpu.buffer(frames * width)
+    for call in range(4):  # eager, recorded, replay, replay
+        gpu.zero(outb)
+        m.encode_device(melb, mel.shape[0], outb)
+        got = gpu.read(outb, (frames, width))
+        assert np.array_equal(got, eager), f"call {call} differs from the eager result"
+        # Eager work of the program's own between the replays.
+        gpu.zero(other)
+        gpu.sync()

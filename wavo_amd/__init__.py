@@ -67,6 +67,7 @@ SIGNATURES = {
     "wh_model_frames": (_i, [_vp, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "wh_model_encode": (_i, [_vp, _vp, _i, _i, _vp]),
     "wh_model_encode_batch": (_i, [_vp, _vp, _i, _i, _vp, _vp]),
+    "wh_model_graphs": (_i, [_vp, _i]),
     "wh_model_blocks": (_i, [_vp, _vp, _i, _i]),
     "wh_model_greedy": (_i, [_vp, _vp, _i, _i, _vp, _i]),
     "wh_whisper_begin": (_i, [_vp, _vp, _i]),
@@ -172,6 +173,9 @@ class Gpu:
 
     def close(self):
         if self.h:
+            # Models hold device memory and recorded graphs of this context: free them first.
+            for m in list(getattr(self, "_models", ())):
+                m.free()
             lib().wh_close(self.h)
             self.h = None
 
@@ -300,15 +304,23 @@ class Model:
         h = _vp()
         gpu._check(lib().wh_model_load(gpu.h, path.encode(), ctypes.byref(h)))
         self.h = h.value
+        if not hasattr(gpu, "_models"):
+            import weakref
+
+            gpu._models = weakref.WeakSet()
+        gpu._models.add(self)
         vals = [_i() for _ in range(5)]
         lib().wh_model_info(self.h, *[ctypes.byref(v) for v in vals])
         arch, self.d, self.layers, self.mels, self.width = (v.value for v in vals)
         self.arch = self.ARCHS[arch]
 
-    def __del__(self):
-        if getattr(self, "h", None):
+    def free(self):
+        if getattr(self, "h", None) and self.gpu.h:
             lib().wh_model_free(self.h)
-            self.h = None
+        self.h = None
+
+    def __del__(self):
+        self.free()
 
     def frames(self, mel_frames):
         f, w = _i(), _i()
@@ -331,6 +343,10 @@ class Model:
     def encode_batch_device(self, mel_buf, batch, mel_frames, valid, out_buf):
         v = (ctypes.c_int * batch)(*valid)
         self.gpu._check(lib().wh_model_encode_batch(self.h, _p(mel_buf), batch, mel_frames, v, _p(out_buf)))
+
+    def graphs(self, on):
+        """Record repeated encoder calls into HIP graphs and replay them (on), or launch eagerly."""
+        self.gpu._check(lib().wh_model_graphs(self.h, int(on)))
 
     def blocks_device(self, x_buf, t, layers):
         self.gpu._check(lib().wh_model_blocks(self.h, _p(x_buf), t, layers))

@@ -692,9 +692,11 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
                l->row_bytes};
   dim3 grid((l->cols + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.split);
   static const char *tn = WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
-  char name[64];
-  snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s", tn, p.bm, p.bn, p.wm, p.wn, p.ns,
-           p.split > 1 ? (p.split == 2 ? "_s2" : "_s4") : "");
+  // Named by kernel variant and call shape: m x rows x k, epilogue, output type, row width.
+  char name[128];
+  snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s %dx%dx%d e%d %s w%d", tn, p.bm, p.bn, p.wm, p.wn, p.ns,
+           p.split > 1 ? (p.split == 2 ? "_s2" : "_s4") : "", m, l->rows, l->k, epi, out16 ? "f16" : "f32",
+           l->cols + l->dual);
   const double width = l->cols + l->dual;
   const double bytes = (double)l->rows * l->row_bytes + 2.0 * m * l->k +
                        (out16 ? 2.0 : 4.0) * m * width * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);

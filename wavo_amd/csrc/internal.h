@@ -36,6 +36,7 @@ struct wh_ctx {
   // operands): grown on demand, reused by every later call on this stream.
   void *scratch = nullptr;
   size_t scratch_bytes = 0;
+  long scratch_epoch = 0;  // incremented whenever scratch moves (recorded graphs hold its address)
 };
 
 // At least `bytes` of device scratch (256-byte aligned), or nullptr with ctx->error set.  Growing
@@ -108,4 +109,6 @@ int launch_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, 
 int launch_pack(wh_ctx *ctx, const float *x, int src, int stride, uint32_t *y, int rows, int d,
                 int cols, int col);
 int launch_zero(wh_ctx *ctx, void *dst, size_t bytes);
+// Device-to-device copy with a kernel (a graph node like any other launch).
+int launch_copy(wh_ctx *ctx, void *dst, const void *src, size_t bytes);
 int launch_add_rows(wh_ctx *ctx, float *x, const float *add, size_t n);

@@ -432,6 +432,16 @@ struct wh_model {
   float *sub2 = nullptr;   // Parakeet conv3 output (the subsampling's second buffer)
   float *rope = nullptr;   // GigaAM rope table for `cap` frames
   const float *pos_cur = nullptr;  // Parakeet: the positions of this call (rows from cap - t)
+  // Recorded encoder calls (HIP graphs), keyed by the call's arguments and the generations of the
+  // buffers they were recorded on; replayed instead of re-issuing their ~500 launches.
+  struct Graph {
+    std::vector<intptr_t> key;
+    hipGraphExec_t exec = nullptr;
+  };
+  std::vector<Graph> graphs;
+  std::vector<intptr_t> pending;  // the arguments of the last eager call
+  bool use_graph = true;
+  long epoch = 0;  // arena generation
   // Whisper decoding state.
   float *dx = nullptr, *dy = nullptr, *dqkv = nullptr, *dh = nullptr, *datt = nullptr, *dpart = nullptr,
         *dscratch = nullptr;
@@ -691,8 +701,16 @@ std::vector<float> rope_table(int frames, int hd, double theta) {
 int parakeet_frames(int mel_frames) { return half_len(half_len(half_len(mel_frames - 1))); }
 
 // Grows the arena to `frames` encoder frames × `batch` windows (rounded up to 64 frames).
+void drop_graphs(wh_model *m) {
+  for (auto &g : m->graphs) (void)hipGraphExecDestroy(g.exec);
+  m->graphs.clear();
+  m->pending.clear();
+}
+
 int arena(wh_model *m, int frames, int batch) {
   if (frames <= m->cap && batch <= m->cap_batch) return WH_OK;
+  drop_graphs(m);
+  m->epoch++;
   int F = (std::max(frames, m->cap) + 63) / 64 * 64, B = std::max(batch, std::max(m->cap_batch, 1));
   for (float *p : {m->x, m->y, m->h, m->qk, m->yr, m->pos, m->sub, m->sub2, m->rope, (float *)m->pos16})
     if (p) {
@@ -824,23 +842,27 @@ int lin(wh_model *m, const float *a, const wh_linear *l, float *c, int rows, int
 // masking as the reference (conv0/conv2 see the valid frames, conv5 the whole image).  Several
 // windows: each is subsampled as if alone (conv5 sees its own valid image rows), and its keys and
 // conv inputs past its own encoder frames are masked.
-int parakeet_encode(wh_model *m, const float *mel, int batch, int mel_frames, const int *valid, float *out) {
-  const int mels = m->mels, ch = m->ch, d = m->d;
+// The window's encoder frames for Parakeet, and for batched windows each window's valid ones.
+std::vector<int> parakeet_valid(int batch, int mel_frames, int t, const int *valid) {
+  std::vector<int> enc_valid(batch);
+  for (int b = 0; b < batch; b++) {
+    int v = std::min(std::max(valid[b], 1), mel_frames);
+    enc_valid[b] = batch == 1 ? t : std::min(t, parakeet_frames(std::max(v, 3)));
+  }
+  return enc_valid;
+}
+
+int parakeet_record(wh_model *m, const float *mel, int batch, int mel_frames, const int *valid, float *out) {
+  const int mels = m->mels, ch = m->ch;
   const int t2 = half_len(half_len(mel_frames)), f2 = half_len(half_len(mels));
   const int t = parakeet_frames(mel_frames), f = half_len(f2);
-  if (mel_frames < 3 || t < 1) return fail(m, "too few mel frames");
-  CK(arena(m, t, batch));
-  m->pos_cur = m->pos + (size_t)(m->cap - t) * d;
-  m->pos16_cur = (const _Float16 *)m->pos16 + (size_t)(m->cap - t) * d;
   wh_ctx *c = m->ctx;
   const int rows1 = 2 * t + 1;  // conv2's output rows from −1 on
   const size_t per = (size_t)rows1 * f2 * ch;
-  std::vector<int> enc_valid(batch);
   for (int b = 0; b < batch; b++) {
     int v = std::min(std::max(valid[b], 1), mel_frames);
     CK(launch_depthwise(c, mel + (size_t)b * mel_frames * mels, m->sc0.w, m->sc0.b, m->sc2.w, m->sc2.b,
                         m->sub + per * b, v, mels, ch, 0, rows1));
-    enc_valid[b] = batch == 1 ? t : std::min(t, parakeet_frames(std::max(v, 3)));
   }
   CK(lin(m, m->sub, m->conv3, m->sub2, rows1 * f2 * batch, WH_RELU));
   for (int b = 0; b < batch; b++) {
@@ -851,16 +873,82 @@ int parakeet_encode(wh_model *m, const float *mel, int batch, int mel_frames, co
   CK(lin(m, m->h, m->conv6, m->qk, t * f * batch, WH_RELU));
   CK(launch_flatten(c, m->qk, m->h, t * batch, f, ch));
   CK(lin(m, m->h, m->pre_out, m->x, t * batch, WH_BIAS));
-  const int *vd = nullptr;
-  if (batch > 1) {
-    hipError_t e = hipMemcpyAsync(m->valid_dev, enc_valid.data(), sizeof(int) * batch, hipMemcpyHostToDevice, c->stream);
-    if (e != hipSuccess) return wh_fail(c, WH_EGPU, "valid lengths: %s", hipGetErrorString(e));
-    e = hipStreamSynchronize(c->stream);
-    if (e != hipSuccess) return wh_fail(c, WH_EGPU, "valid lengths: %s", hipGetErrorString(e));
-    vd = m->valid_dev;
-  }
-  CK(record_blocks(m, t, batch, vd, m->layers));
+  CK(record_blocks(m, t, batch, batch > 1 ? m->valid_dev : nullptr, m->layers));
   return lin(m, m->x, m->joint_enc, out, t * batch, WH_BIAS);
+}
+
+// Runs `record` (a function queuing kernels only) for the call identified by `key`: eagerly the first
+// time, recorded into a HIP graph the second time, replayed from then on.  Buffers the graph names
+// must not move: the key carries the arena's and the scratch's generations.
+template <typename F>
+int run_recorded(wh_model *m, std::vector<intptr_t> key, F &&record) {
+  wh_ctx *c = m->ctx;
+  key.push_back(m->epoch);
+  key.push_back(c->scratch_epoch);
+  if (!m->use_graph || c->prof) return record();
+  for (auto &g : m->graphs)
+    if (g.key == key) {
+      hipError_t e = hipGraphLaunch(g.exec, c->stream);
+      if (e != hipSuccess) return wh_fail(c, WH_EGPU, "graph launch: %s", hipGetErrorString(e));
+      return WH_OK;
+    }
+  if (m->pending != key) {
+    m->pending = key;
+    return record();
+  }
+  hipGraph_t graph = nullptr;
+  if (hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    (void)hipGetLastError();
+    return record();
+  }
+  const int rc = record();
+  hipError_t e = hipStreamEndCapture(c->stream, &graph);
+  hipGraphExec_t exec = nullptr;
+  if (rc == WH_OK && e == hipSuccess && graph) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (graph) (void)hipGraphDestroy(graph);
+  if (rc != WH_OK) return rc;
+  if (e != hipSuccess || !exec) {  // recording failed: stay eager for this model
+    (void)hipGetLastError();
+    m->use_graph = false;
+    return record();
+  }
+  // Stale generations are never matched again: drop them, and keep at most 8 recordings.
+  for (size_t i = 0; i < m->graphs.size();)
+    if (m->graphs[i].key[m->graphs[i].key.size() - 2] != m->epoch ||
+        m->graphs[i].key.back() != c->scratch_epoch || m->graphs.size() >= 8) {
+      (void)hipGraphExecDestroy(m->graphs[i].exec);
+      m->graphs.erase(m->graphs.begin() + i);
+    } else {
+      i++;
+    }
+  m->graphs.push_back({key, exec});
+  e = hipGraphLaunch(exec, c->stream);
+  if (e != hipSuccess) return wh_fail(c, WH_EGPU, "graph launch: %s", hipGetErrorString(e));
+  return WH_OK;
+}
+
+// Parakeet Encoder::record (src/parakeet/encoder.rs:103-124) over `batch` windows of mel_frames
+// [batch][mel_frames][mels]; window b's first valid[b] mel frames are real.  One window: kestrel
+// masking as the reference (conv0/conv2 see the valid frames, conv5 the whole image).  Several
+// windows: each is subsampled as if alone (conv5 sees its own valid image rows), and its keys and
+// conv inputs past its own encoder frames are masked.
+int parakeet_encode(wh_model *m, const float *mel, int batch, int mel_frames, const int *valid, float *out) {
+  const int t = parakeet_frames(mel_frames), d = m->d;
+  if (mel_frames < 3 || t < 1) return fail(m, "too few mel frames");
+  CK(arena(m, t, batch));
+  m->pos_cur = m->pos + (size_t)(m->cap - t) * d;
+  m->pos16_cur = (const _Float16 *)m->pos16 + (size_t)(m->cap - t) * d;
+  wh_ctx *c = m->ctx;
+  if (batch > 1) {
+    // The windows' valid encoder frames, read by the kernels (uploaded before the recorded part).
+    const std::vector<int> enc_valid = parakeet_valid(batch, mel_frames, t, valid);
+    hipError_t e = hipMemcpyAsync(m->valid_dev, enc_valid.data(), sizeof(int) * batch, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return wh_fail(c, WH_EGPU, "valid lengths: %s", hipGetErrorString(e));
+  }
+  std::vector<intptr_t> key = {PARAKEET, (intptr_t)mel, (intptr_t)out, batch, mel_frames};
+  for (int b = 0; b < batch; b++) key.push_back(valid[b]);
+  return run_recorded(m, std::move(key), [&] { return parakeet_record(m, mel, batch, mel_frames, valid, out); });
 }
 
 // GigaAM Encoder::record (src/gigaam/encoder.rs:83-93).
@@ -869,12 +957,14 @@ int gigaam_encode(wh_model *m, const float *mel, int mel_frames, float *out) {
   if (mel_frames < 5) return fail(m, "too few mel frames");
   CK(arena(m, t1, 1));
   wh_ctx *c = m->ctx;
-  CK(launch_im2col(c, mel, m->h, mel_frames, m->mels, 5, 2, 2, 1, 0, 0));
-  CK(lin(m, m->h, m->conv0, m->qk, t1, WH_RELU));
-  CK(launch_im2col(c, m->qk, m->h, t1, d, 5, 2, 2, 1, 0, 0));
-  CK(lin(m, m->h, m->conv2, m->x, t, WH_RELU));
-  CK(record_blocks(m, t, 1, nullptr, m->layers));
-  return lin(m, m->x, m->head, out, t, WH_BIAS);
+  return run_recorded(m, {GIGAAM, (intptr_t)mel, (intptr_t)out, mel_frames}, [&] {
+    CK(launch_im2col(c, mel, m->h, mel_frames, m->mels, 5, 2, 2, 1, 0, 0));
+    CK(lin(m, m->h, m->conv0, m->qk, t1, WH_RELU));
+    CK(launch_im2col(c, m->qk, m->h, t1, d, 5, 2, 2, 1, 0, 0));
+    CK(lin(m, m->h, m->conv2, m->x, t, WH_RELU));
+    CK(record_blocks(m, t, 1, nullptr, m->layers));
+    return lin(m, m->x, m->head, out, t, WH_BIAS);
+  });
 }
 
 // Whisper Encoder::record (src/whisper/encoder.rs:67-74; transformer.rs:122-138) into out [t][d].
@@ -883,23 +973,25 @@ int whisper_encode(wh_model *m, const float *mel, int mel_frames, float *out) {
   if (mel_frames != 2 * t) return fail(m, "Whisper takes windows of " + std::to_string(2 * t) + " mel frames");
   CK(arena(m, t, 1));
   wh_ctx *c = m->ctx;
-  CK(launch_im2col(c, mel, m->qk, 2 * t, m->mels, 3, 1, 1, 1, 0, 0));
-  CK(lin(m, m->qk, m->wconv0, m->h, 2 * t, WH_GELU));
-  CK(launch_im2col(c, m->h, m->qk, 2 * t, d, 3, 2, 1, 1, 0, 0));
-  CK(wh_copy(c, m->x, m->enc_pos, (size_t)t * d * 4));
-  CK(lin(m, m->qk, m->wconv1, m->x, t, WH_GELU_RESIDUAL));
-  // Pre-LN blocks; the GEMMs' inputs as f16 (see record_block).
-  void *y16 = m->y, *h16 = m->h;
-  for (const WBlock &b : m->wblocks) {
-    CK(launch_layer_norm(c, m->x, b.norm_attn.w, b.norm_attn.b, y16, t, d, nullptr, nullptr, 0, 1));
-    CK(launch_gemm_h(c, y16, b.qkv, m->qk, t, b.qkv->cols + b.qkv->dual, WH_BIAS, 0.0f, 1));
-    CK(launch_attention(c, m->qk, nullptr, nullptr, y16, t, m->heads, hd, nullptr, t, 1, 1, 1));
-    CK(launch_gemm_h(c, y16, b.out, m->x, t, b.out->cols + b.out->dual, WH_RESIDUAL, 1.0f, 0));
-    CK(launch_layer_norm(c, m->x, b.norm_ffn.w, b.norm_ffn.b, y16, t, d, nullptr, nullptr, 0, 1));
-    CK(launch_gemm_h(c, y16, b.fc1, h16, t, b.fc1->cols + b.fc1->dual, WH_GELU, 0.0f, 1));
-    CK(launch_gemm_h(c, h16, b.fc2, m->x, t, b.fc2->cols + b.fc2->dual, WH_RESIDUAL, 1.0f, 0));
-  }
-  return launch_layer_norm(c, m->x, m->enc_norm.w, m->enc_norm.b, out, t, d, nullptr, nullptr, 0);
+  return run_recorded(m, {WHISPER, (intptr_t)mel, (intptr_t)out, mel_frames}, [&] {
+    CK(launch_im2col(c, mel, m->qk, 2 * t, m->mels, 3, 1, 1, 1, 0, 0));
+    CK(lin(m, m->qk, m->wconv0, m->h, 2 * t, WH_GELU));
+    CK(launch_im2col(c, m->h, m->qk, 2 * t, d, 3, 2, 1, 1, 0, 0));
+    CK(launch_copy(c, m->x, m->enc_pos, (size_t)t * d * 4));
+    CK(lin(m, m->qk, m->wconv1, m->x, t, WH_GELU_RESIDUAL));
+    // Pre-LN blocks; the GEMMs' inputs as f16 (see record_block).
+    void *y16 = m->y, *h16 = m->h;
+    for (const WBlock &b : m->wblocks) {
+      CK(launch_layer_norm(c, m->x, b.norm_attn.w, b.norm_attn.b, y16, t, d, nullptr, nullptr, 0, 1));
+      CK(launch_gemm_h(c, y16, b.qkv, m->qk, t, b.qkv->cols + b.qkv->dual, WH_BIAS, 0.0f, 1));
+      CK(launch_attention(c, m->qk, nullptr, nullptr, y16, t, m->heads, hd, nullptr, t, 1, 1, 1));
+      CK(launch_gemm_h(c, y16, b.out, m->x, t, b.out->cols + b.out->dual, WH_RESIDUAL, 1.0f, 0));
+      CK(launch_layer_norm(c, m->x, b.norm_ffn.w, b.norm_ffn.b, y16, t, d, nullptr, nullptr, 0, 1));
+      CK(launch_gemm_h(c, y16, b.fc1, h16, t, b.fc1->cols + b.fc1->dual, WH_GELU, 0.0f, 1));
+      CK(launch_gemm_h(c, h16, b.fc2, m->x, t, b.fc2->cols + b.fc2->dual, WH_RESIDUAL, 1.0f, 0));
+    }
+    return launch_layer_norm(c, m->x, m->enc_norm.w, m->enc_norm.b, out, t, d, nullptr, nullptr, 0);
+  });
 }
 
 // dot (src/cpu/mod.rs:20-43): 16 fused lanes summed pairwise, then the tail.
@@ -1029,6 +1121,8 @@ int wh_model_load(wh_ctx *ctx, const char *path, wh_model **out) {
 
 void wh_model_free(wh_model *m) {
   if (!m) return;
+  (void)hipStreamSynchronize(m->ctx->stream);
+  drop_graphs(m);
   for (float *p : m->owned)
     if (p) wh_free(m->ctx, p);
   if (m->valid_dev) wh_free(m->ctx, m->valid_dev);
@@ -1085,6 +1179,14 @@ int wh_model_encode_batch(wh_model *m, const float *mel, int batch, int mel_fram
   if (m->arch != PARAKEET) return wh_fail(m->ctx, WH_EARG, "batched windows are built for the Parakeet encoder");
   (void)hipSetDevice(m->ctx->device);
   return parakeet_encode(m, mel, batch, mel_frames, valid, out);
+}
+
+int wh_model_graphs(wh_model *m, int on) {
+  if (!m) return WH_EARG;
+  (void)hipStreamSynchronize(m->ctx->stream);
+  drop_graphs(m);
+  m->use_graph = on != 0;
+  return WH_OK;
 }
 
 int wh_model_blocks(wh_model *m, float *x, int t, int layers) {

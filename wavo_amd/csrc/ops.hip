@@ -4,6 +4,8 @@
 // src/gpu/ops.wgsl and src/gpu/spatial.wgsl (cited per kernel); the layout is one wavefront per row
 // (64 lanes over the channels, reductions by cross-lane shuffles) instead of a 256-thread
 // workgroup per row, so a row's data stays in registers and short rows keep every lane busy.
+#include <algorithm>
+
 #include "internal.h"
 
 namespace {
@@ -351,6 +353,14 @@ __global__ void zero_bytes_kernel(uint8_t *p, size_t bytes) {
   if (i < bytes) p[i] = 0;
 }
 
+__global__ void copy16_kernel(uint4 *__restrict__ y, const uint4 *__restrict__ x, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) y[i] = x[i];
+}
+
+__global__ void copy_bytes_kernel(uint8_t *__restrict__ y, const uint8_t *__restrict__ x, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) y[i] = x[i];
+}
+
 __global__ void add_kernel(float *x, const float *a, size_t n) {
   size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   for (; i < n; i += (size_t)gridDim.x * blockDim.x) x[i] += a[i];
@@ -475,6 +485,24 @@ int launch_zero(wh_ctx *ctx, void *dst, size_t bytes) {
     zero_bytes_kernel<<<(unsigned)((bytes + 255) / 256), 256, 0, ctx->stream>>>((uint8_t *)dst, bytes);
   }
   return wh_launched(ctx, "zero");
+}
+
+int launch_copy(wh_ctx *ctx, void *dst, const void *src, size_t bytes) {
+  if (!bytes) return WH_OK;
+  if (!dst || !src) return wh_fail(ctx, WH_EARG, "copy: NULL");
+  ProfScope prof(ctx, "copy", 0.0, 2.0 * bytes);
+  const size_t n16 = ((uintptr_t)dst % 16 == 0 && (uintptr_t)src % 16 == 0) ? bytes / 16 : 0;
+  if (n16) {
+    const size_t blocks = std::min<size_t>((n16 + 255) / 256, 8192);
+    copy16_kernel<<<(unsigned)blocks, 256, 0, ctx->stream>>>((uint4 *)dst, (const uint4 *)src, n16);
+  }
+  const size_t rest = bytes - 16 * n16;
+  if (rest) {
+    const size_t blocks = std::min<size_t>((rest + 255) / 256, 8192);
+    copy_bytes_kernel<<<(unsigned)blocks, 256, 0, ctx->stream>>>((uint8_t *)dst + 16 * n16, (const uint8_t *)src + 16 * n16,
+                                                                 rest);
+  }
+  return wh_launched(ctx, "copy");
 }
 
 int launch_add_rows(wh_ctx *ctx, float *x, const float *a, size_t n) {

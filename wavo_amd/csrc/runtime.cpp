@@ -71,6 +71,7 @@ void *wh_scratch(wh_ctx *ctx, size_t bytes) {
     return nullptr;
   }
   ctx->scratch_bytes = bytes;
+  ctx->scratch_epoch++;
   return ctx->scratch;
 }
 
@@ -177,9 +178,7 @@ int wh_write(wh_ctx *ctx, void *dst, const void *src, size_t bytes) {
 
 int wh_copy(wh_ctx *ctx, void *dst, const void *src, size_t bytes) {
   if (!ctx || (!bytes)) return ctx ? WH_OK : WH_EARG;
-  hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream);
-  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "copy of %zu bytes: %s", bytes, hipGetErrorString(e));
-  return WH_OK;
+  return launch_copy(ctx, dst, src, bytes);
 }
 
 int wh_zero(wh_ctx *ctx, void *dst, size_t bytes) {

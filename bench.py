@@ -172,8 +172,9 @@ def main():
     ap.add_argument("--seconds", type=float, default=60.0, help="audio per step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-gemv", action="store_true", help="skip the decoder GEMV measurement")
-    ap.add_argument("--replay", action="store_true",
-                    help="only the dominant GEMM configuration's back-to-back launches (for rocprofv3 passes)")
+    ap.add_argument("--replay", metavar="NAME", default=None,
+                    help="only the back-to-back launches of this GEMM configuration (a roofline.kernel value), "
+                         "for rocprofv3 passes over exactly those launches")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -186,6 +187,14 @@ def main():
 
     import wavo_amd as wa
     from wavo_amd import synth
+
+    if args.replay:
+        if not GEMM_NAME.match(args.replay):
+            sys.exit(f"--replay takes a GEMM configuration name like the bench line's roofline.kernel: {args.replay!r}")
+        us, flops = gemm_replay(None, args.replay)
+        print(json.dumps({"replayed": args.replay, "us_per_launch": round(us, 3),
+                          "tflops": round(flops / (us * 1e-6) / 1e12, 2)}), flush=True)
+        return
 
     t0 = time.time()
     path = synth.model_path("parakeet")
@@ -201,17 +210,16 @@ def main():
     melb = gpu.upload(mel)
     outb = gpu.buffer(frames * width)
 
-    if not args.replay:
-        for _ in range(args.warmup):
-            model.encode_device(melb, mel_frames, outb)
-        gpu.sync()
-        log(f"warmup done ({args.warmup} steps), timing {args.steps}")
-        t0 = time.perf_counter()
-        ms_ev = time_region(gpu, lambda: model.encode_device(melb, mel_frames, outb), args.steps)
-        wall = (time.perf_counter() - t0) / args.steps
-        dt = ms_ev * 1e-3
-        rtfx = args.seconds / dt
-        log(f"{dt * 1e3:.3f} ms per step (events; wall {wall * 1e3:.3f}), RTFx {rtfx:.0f}")
+    for _ in range(args.warmup):
+        model.encode_device(melb, mel_frames, outb)
+    gpu.sync()
+    log(f"warmup done ({args.warmup} steps), timing {args.steps}")
+    t0 = time.perf_counter()
+    ms_ev = time_region(gpu, lambda: model.encode_device(melb, mel_frames, outb), args.steps)
+    wall = (time.perf_counter() - t0) / args.steps
+    dt = ms_ev * 1e-3
+    rtfx = args.seconds / dt
+    log(f"{dt * 1e3:.3f} ms per step (events; wall {wall * 1e3:.3f}), RTFx {rtfx:.0f}")
 
     # One profiled step: per-kernel launches and algorithmic work (events around each launch).
     gpu.profile(1)
@@ -222,10 +230,6 @@ def main():
     dom = max(gemms, key=lambda k: k["ms"])
     us, flops = gemm_replay(gpu, dom["kernel"])
     log(f"dominant GEMM {dom['kernel']}: {dom['launches']} launches per step, {us:.2f} us per launch back to back")
-    if args.replay:
-        print(json.dumps({"replayed": dom["kernel"], "us_per_launch": us}), flush=True)
-        gpu.close()
-        return
 
     achieved = flops / (us * 1e-6) / 1e12
     fam = {}

@@ -159,7 +159,8 @@ int wh_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int kernel
 /* Pass::conv_glu (src/gpu/mod.rs:1535-1557): GLU of h [t][2ch], depthwise conv (odd kernel,
  * centred; taps dw_w [ch][kernel] + dw_b), LayerNorm (layer_norm != 0) or affine x·g + b, SiLU,
  * into y [t][ch].  `valid` (< t) zeroes the GLU output of frames >= valid first (a padded window's
- * frame mask, src/ane/conformer.rs:301-309); valid >= t is unmasked. */
+ * frame mask, src/ane/conformer.rs:301-309); valid >= t is unmasked.  ch % 4 == 0, ch <= 1024,
+ * kernel <= 31, 16-byte aligned buffers. */
 int wh_conv_glu(wh_ctx *ctx, const float *h, const float *dw_w, const float *dw_b, int kernel,
                 const float *g, const float *b, int layer_norm, float *y, int t, int ch,
                 int valid);
@@ -169,7 +170,8 @@ int wh_conv_glu(wh_ctx *ctx, const float *h, const float *dw_w, const float *dw_
  *   v == NULL, pos == NULL: qk [t][q | k | v]                          (Whisper)
  *   v == NULL, pos != NULL: qk [t][q + u | k | v | q + v], pos [2t + 15][heads·hd] (row r is
  *     position t + 15 − r); score (i, j) = ((q+u)_i·k_j + (q+v)_i·pos[j − i + t + 15]) / √hd.
- * `valid` (< t) masks keys >= valid (additive key mask, src/ane/mod.rs:463-466). */
+ * `valid` (< t) masks keys >= valid (additive key mask, src/ane/mod.rs:463-466).  The products
+ * use f16 operands with f32 accumulation and softmax, as the reference's f16 flash tier. */
 int wh_attention(wh_ctx *ctx, const float *qk, const float *v, const float *pos, float *o, int t,
                  int heads, int hd, int valid);
 /* Pass::depthwise (src/gpu/mod.rs:1603-1630): 3×3 stride-2 pad-1 depthwise conv + bias (w [9][ch])

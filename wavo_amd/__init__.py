@@ -224,6 +224,10 @@ class Gpu:
         self._check(lib().wh_read(self.h, out.ctypes.data, _p(buf) + offset_bytes, out.nbytes))
         return out
 
+    def copy(self, dst, src, nbytes):
+        """Device-to-device copy of nbytes with the library's copy kernel."""
+        self._check(lib().wh_copy(self.h, _p(dst), _p(src), int(nbytes)))
+
     def zero(self, buf, nbytes=None):
         self._check(lib().wh_zero(self.h, _p(buf), buf.nbytes if nbytes is None else nbytes))
 

@@ -179,6 +179,30 @@ def test_gemv_and_embed(gpu, wtype, k, n, cols):
     close(gpu.read(ob, (k,)), wrow + pos[k:] + padded[:k], what="embed")
 
 
+@pytest.mark.parametrize("wtype", [wa.Q8_0, wa.F16, wa.Q4_0])
+@pytest.mark.parametrize("n,k", [(1280, 1280), (3840, 1280), (5120, 1280), (1280, 5120), (51866, 1280), (37, 64)])
+def test_gemv_decoder_shapes(gpu, wtype, n, k):
+    # Whisper-large-v3-turbo's decoder GEMVs (per layer and the 51866-row head) through the streaming
+    # kernel: rows split across workgroups and stages, the last stage partial, padding columns.
+    w = np.random.default_rng(21).normal(0, 0.02, (n, k)).astype(np.float32)
+    raw = ox.quantize(w, wtype)
+    bias = rnd(n, 22)
+    l = gpu.linear([(raw, wtype, k, n)], bias)
+    ol = ox.Linear(wtype, k, [(raw, n)], bias)
+    a = rnd(k, 23)
+    ab = gpu.upload(a)
+    cols = l.width
+    c0 = rnd(cols + 1, 24)
+    for e, alpha in ((wa.BIAS, 0.0), (wa.RESIDUAL, 1.0), (wa.GELU, 0.0)):
+        cb = gpu.upload(c0)
+        gpu.gemv(ab, l, cb, e, alpha)
+        got = gpu.read(cb, c0.shape)
+        want = c0.copy()
+        want[:n] = ox.gemv(a, ol, e, alpha, c=c0[:n])
+        want[n:cols] = epi_zero(e, c0[n:cols])
+        close(got, want, what=f"gemv {n}x{k} type {wtype} epi {e}")
+
+
 @pytest.mark.parametrize("heads,hd", [(2, 40), (3, 36), (20, 64)])
 def test_attend_and_pack(gpu, heads, hd):
     keys = 4100

@@ -8,6 +8,8 @@
 // one 16-byte (F16/F32) or block-pair (Q8_0/Q4_0) item of a row per step, so the workgroup's loads
 // sweep the run's bytes in order; `a` sits in LDS.  Per block the int8 (or nibble) products are
 // summed in f32 and scaled once, as ggml's mul_mv (gemm.wgsl:244-262); W is not rounded to f16.
+#include <algorithm>
+
 #include "internal.h"
 
 namespace {
@@ -154,6 +156,208 @@ __global__ __launch_bounds__(256) void gemv_wave_kernel(const float *__restrict_
       *cp = epilogue(epi, alpha, s + bias[row], *cp);
     }
   }
+}
+
+// ------------------------------------------------------------------- streaming GEMV (k % 64 == 0)
+
+// LDS DMA from a wave-uniform base plus a per-lane byte offset (16 bytes or 4 bytes per lane) to LDS
+// lds + 16·lane (4·lane); counted by vmcnt.
+__device__ __forceinline__ void gv_dma16(const void *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void gv_dma4(const void *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ uint32_t gv_lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+template <int N>
+__device__ __forceinline__ void gv_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+struct GemvArgs {
+  const float *a;
+  const uint8_t *w;
+  const float *bias;
+  float *c;
+  int rows, k, epi, offset;
+  float alpha;
+  int row_bytes;
+  int rps;        // rows per stage
+  int stages;     // ceil(rows / rps)
+  int per_wg;     // stages per workgroup
+  size_t total;   // rows · row_bytes
+};
+
+constexpr int GV_NS = 3;       // LDS stages per workgroup (two in flight while one is used)
+constexpr int GV_STAGE = 16384;  // bytes per stage (whole DMA instructions of 1 KiB)
+
+// c[offset + j] = epi(a·W[j] + bias[j]) for rows j of W streamed from HBM: a workgroup takes a run
+// of stages, each `rps` consecutive rows (≤ 16 KiB, contiguous in HBM), and keeps GV_NS − 1 stages
+// in flight by LDS DMA (16-byte lanes when rows are 16-byte multiples, else 4-byte lanes), so the
+// chip holds tens of MB of loads in flight.  Each thread takes one 64-weight item (a Q8_0 or Q4_0
+// block pair, or 64 F16 weights) of one row of the stage from LDS, `a` from LDS, and sums the
+// products in f32 (per block Σ q·a, then × d, as gemm.wgsl:244-262); a row's items are summed in
+// order through LDS.  W is not rounded (Pass::gemv semantics).
+template <int WT, bool D16>
+__global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
+  constexpr int ITEM = WT == WH_Q8_0 ? 68 : WT == WH_Q4_0 ? 36 : 128;  // bytes of 64 weights
+  constexpr int LANE = D16 ? 16 : 4;                                   // bytes per lane per DMA
+  constexpr int NI = GV_STAGE / (64 * LANE);                           // DMA instructions per stage
+  constexpr int PER = NI / 4;                                          // per wave (4 waves)
+  constexpr int AS = 68;  // floats per item of a in LDS: 64 + 4, so items start 4 banks apart
+  static_assert(NI % 4 == 0 && (GV_NS - 2) * PER < 64, "vmcnt range");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t *st = smem;                                                  // GV_NS stages
+  const int items = P.k / 64;
+  float *as = (float *)(smem + GV_NS * GV_STAGE);                      // a: items × AS
+  float *part = as + items * AS;                                       // 256 partial sums
+  float *rsum = part + 256;                                            // the workgroup's row sums
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int s0 = blockIdx.x * P.per_wg, s1 = min(s0 + P.per_wg, P.stages);
+  const size_t stage_bytes = (size_t)P.rps * P.row_bytes;
+  const uint32_t lds0 = gv_lds_addr(st);
+  auto issue = [&](int s) {  // stage s of the matrix into ring slot (s - s0) % GV_NS
+    const uint8_t *base = P.w + (size_t)s * stage_bytes;
+    const size_t left = P.total - (size_t)s * stage_bytes;  // bytes from this stage's start to the end
+    const uint32_t slot = lds0 + ((s - s0) % GV_NS) * GV_STAGE;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+      const int n = wave + 4 * i;
+      // Bytes past the matrix end read its last chunk again (never used as a real row).
+      const uint32_t off = (uint32_t)min((size_t)(n * 64 + lane) * LANE, left - LANE);
+      if constexpr (D16) gv_dma16(base, off, slot + n * 64 * LANE);
+      else gv_dma4(base, off, slot + n * 64 * LANE);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < GV_NS - 1; i++)
+    if (s0 + i < s1) issue(s0 + i);
+  for (int i = tid; i < P.k; i += 256) as[(i >> 6) * AS + (i & 63)] = P.a[i];
+  const int row_l = tid / items, it = tid % items;
+  for (int s = s0; s < s1; s++) {
+    if (s + GV_NS - 2 < s1) gv_wait_vm<(GV_NS - 2) * PER>();
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // stage s landed everywhere; the slot of stage s − 1 and `part` are free
+    if (s + GV_NS - 1 < s1) issue(s + GV_NS - 1);
+    const int nrows = min(P.rps, P.rows - s * P.rps);
+    float sum = 0.0f;
+    if (row_l < nrows) {
+      const uint8_t *ip = st + ((s - s0) % GV_NS) * GV_STAGE + row_l * P.row_bytes + it * ITEM;
+      const float *x = as + AS * it;
+      if constexpr (WT == WH_F16) {
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          const uint4 v = *(const uint4 *)(ip + 16 * q);
+          const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+          const float4 x0 = *(const float4 *)(x + 8 * q), x1 = *(const float4 *)(x + 8 * q + 4);
+          const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+          for (int e = 0; e < 4; e++) sum += half_bits(u[e] & 0xffffu) * xs[2 * e] + half_bits(u[e] >> 16) * xs[2 * e + 1];
+        }
+      } else {
+        constexpr int DW = ITEM / 4;  // 17 or 9 dwords
+        const uint32_t *p = (const uint32_t *)ip;
+        uint32_t q[DW + 1];
+#pragma unroll
+        for (int i = 0; i < DW; i++) q[i] = p[i];
+        q[DW] = 0;
+        constexpr int S1 = ITEM / 8;  // block 1's scale sits in the high half of dword S1
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+          const float d = half_bits(b ? (q[S1] >> 16) : (q[0] & 0xffffu));
+          const float *xb = x + 32 * b;
+          float bs = 0.0f;
+          if constexpr (WT == WH_Q8_0) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+              const uint32_t v = b ? q[S1 + 1 + j] : __builtin_amdgcn_alignbyte(q[j + 1], q[j], 2);
+              const float4 xv = *(const float4 *)(xb + 4 * j);
+              bs += (float)(int8_t)(v) * xv.x + (float)(int8_t)(v >> 8) * xv.y + (float)(int8_t)(v >> 16) * xv.z +
+                    (float)(int8_t)(v >> 24) * xv.w;
+            }
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const uint32_t v = b ? q[S1 + 1 + j] : __builtin_amdgcn_alignbyte(q[j + 1], q[j], 2);
+              const float4 xl = *(const float4 *)(xb + 4 * j), xh = *(const float4 *)(xb + 16 + 4 * j);
+              bs += (float)((int)(v & 15u) - 8) * xl.x + (float)((int)((v >> 8) & 15u) - 8) * xl.y +
+                    (float)((int)((v >> 16) & 15u) - 8) * xl.z + (float)((int)((v >> 24) & 15u) - 8) * xl.w;
+              bs += (float)((int)((v >> 4) & 15u) - 8) * xh.x + (float)((int)((v >> 12) & 15u) - 8) * xh.y +
+                    (float)((int)((v >> 20) & 15u) - 8) * xh.z + (float)((int)((v >> 28) & 15u) - 8) * xh.w;
+            }
+          }
+          sum += bs * d;
+        }
+      }
+    }
+    part[tid] = sum;
+    __syncthreads();
+    if (tid < nrows) {
+      // The row's items in order, 4 at a time (items % 4 == 0 when k % 256 == 0; else a tail).
+      float acc = 0.0f;
+      const float *pr = part + tid * items;
+      int i = 0;
+      if ((items & 3) == 0) {
+#pragma unroll 4
+        for (; i < items; i += 4) {
+          const float4 v = *(const float4 *)(pr + i);
+          acc += ((v.x + v.y) + (v.z + v.w));
+        }
+      }
+      for (; i < items; i++) acc += pr[i];
+      rsum[(s - s0) * P.rps + tid] = acc;
+    }
+  }
+  // The epilogue of the workgroup's rows at once, off the streaming loop.
+  __syncthreads();
+  const int r0 = s0 * P.rps, r1 = min(s1 * P.rps, P.rows);
+  const bool res = P.epi == WH_RESIDUAL || P.epi == WH_GELU_RESIDUAL;
+  for (int row = r0 + tid; row < r1; row += 256) {
+    float *cp = P.c + P.offset + row;
+    *cp = epilogue(P.epi, P.alpha, rsum[row - r0] + P.bias[row], res ? *cp : 0.0f);
+  }
+}
+
+// Rows rows..cols (the padding columns) of a streamed GEMV: epi(0 + bias).
+__global__ void gemv_pad_kernel(const float *__restrict__ bias, float *__restrict__ c, int rows, int cols, int epi,
+                                float alpha, int offset) {
+  const int row = rows + blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= cols) return;
+  float *cp = c + offset + row;
+  *cp = epilogue(epi, alpha, bias[row], *cp);
+}
+
+template <int WT>
+int gemv_stream(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha, int offset) {
+  const int items = l->k / 64;
+  GemvArgs P{a, l->w, l->bias, c, l->rows, l->k, epi, offset, alpha, (int)l->row_bytes, 0, 0, 0, 0};
+  P.rps = std::min(256 / items, GV_STAGE / (int)l->row_bytes);
+  P.stages = (l->rows + P.rps - 1) / P.rps;
+  // Two workgroups per CU (48 KiB of stages each), each streaming a run of stages: measured on
+  // MI355X, 16 KiB stages three deep at two per CU stream the 70.5 MB head at 4.6 TB/s, against
+  // 3.2 TB/s for 20 KiB stages four deep at one per CU.
+  const int cus = ctx->cus > 0 ? ctx->cus : 256;
+  const int wgs = std::min(P.stages, 2 * cus);
+  P.per_wg = (P.stages + wgs - 1) / wgs;
+  const int grid = (P.stages + P.per_wg - 1) / P.per_wg;
+  P.total = (size_t)l->rows * l->row_bytes;
+  const size_t lds = (size_t)GV_NS * GV_STAGE + 4 * (size_t)items * 68 + 4 * 256 + 4 * (size_t)P.per_wg * P.rps;
+  if (lds > 160 * 1024) return 1;  // (positive: not an error) the caller takes the general kernel
+  static const char *tn = WT == WH_F16 ? "gemv_f16" : WT == WH_Q8_0 ? "gemv_q8_0" : "gemv_q4_0";
+  const double bytes = (double)P.total + 4.0 * l->k + 4.0 * l->cols * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
+  ProfScope prof(ctx, tn, 2.0 * l->rows * l->k, bytes);
+  if (l->row_bytes % 16 == 0)
+    gemv_stream_kernel<WT, true><<<grid, 256, lds, ctx->stream>>>(P);
+  else
+    gemv_stream_kernel<WT, false><<<grid, 256, lds, ctx->stream>>>(P);
+  if (l->cols > l->rows)
+    gemv_pad_kernel<<<(l->cols - l->rows + 255) / 256, 256, 0, ctx->stream>>>(l->bias, c, l->rows, l->cols, epi, alpha,
+                                                                             offset);
+  return wh_launched(ctx, "gemv");
 }
 
 template <int WT, bool PAIR>
@@ -310,6 +514,16 @@ int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int e
   if (!a || !c || offset < 0 || epi < WH_BIAS || epi > WH_TANH) return wh_fail(ctx, WH_EARG, "gemv: bad arguments");
   if ((size_t)l->k * 4 > 64 * 1024) return wh_fail(ctx, WH_EARG, "gemv: k %d too large", l->k);
   bool pair = l->k % 64 == 0;
+  // The streaming kernel: whole 64-weight items, at most 256 of them per row, rows 4-byte aligned.
+  if (pair && l->k / 64 <= 256 && l->row_bytes % 4 == 0 && (int)l->row_bytes <= GV_STAGE && l->rows > 0) {
+    int rc = 1;
+    switch (l->type) {
+      case WH_Q8_0: rc = gemv_stream<WH_Q8_0>(ctx, a, l, c, epi, alpha, offset); break;
+      case WH_Q4_0: rc = gemv_stream<WH_Q4_0>(ctx, a, l, c, epi, alpha, offset); break;
+      case WH_F16: rc = gemv_stream<WH_F16>(ctx, a, l, c, epi, alpha, offset); break;
+    }
+    if (rc != 1) return rc;
+  }
   switch (l->type) {
     case WH_F32: return gemv_t<WH_F32, false>(ctx, a, l, c, epi, alpha, offset);
     case WH_F16: return gemv_t<WH_F16, false>(ctx, a, l, c, epi, alpha, offset);

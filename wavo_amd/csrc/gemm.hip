@@ -543,7 +543,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   }
 
   // Epilogue through LDS: every DMA has landed (the last step waited for it) and the barrier below
-  // ends every wavefront's reads of the stages.
+  // ends every wavefront's reads of the stages.  A thread's 8-column group is the same on every row
+  // it stores (64·NW is a multiple of BN / 8), so its bias values are loaded once, before the barrier.
+  constexpr int G8 = BN / 8;  // 8-column groups per row
+  static_assert((64 * NW) % G8 == 0, "fixed column group per thread");
+  const int ecol = n0 + 8 * (tid % G8);
+  float bb[8] = {}, bd[8] = {};
+  if (!SPLIT && ecol < P.cols) {
+    const float4 b0 = *(const float4 *)(P.bias + ecol), b1 = *(const float4 *)(P.bias + ecol + 4);
+    bb[0] = b0.x, bb[1] = b0.y, bb[2] = b0.z, bb[3] = b0.w, bb[4] = b1.x, bb[5] = b1.y, bb[6] = b1.z, bb[7] = b1.w;
+#pragma unroll
+    for (int q = 0; q < 8; q++)
+      if (ecol + q < P.dual) bd[q] = P.bias[P.cols + ecol + q];
+  }
   __syncthreads();
   float *cl = (float *)lds;
 #pragma unroll
@@ -554,9 +566,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
       for (int v = 0; v < 16; v++)
         cl[(wm + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow] = acc[i][j][v];
   __syncthreads();
-  constexpr int G8 = BN / 8;  // 8-column groups per row
-  for (int e = tid; e < BM * G8; e += 64 * NW) {
-    const int r = e / G8, c8 = 8 * (e % G8), row = m0 + r, col = n0 + c8;
+  static_assert((BM * G8) % (64 * NW) == 0, "whole rounds of column groups");
+#pragma unroll
+  for (int it = 0; it < BM * G8 / (64 * NW); it++) {
+    const int e = tid + it * 64 * NW, r = e / G8, c8 = 8 * (e % G8), row = m0 + r, col = n0 + c8;
     if (row >= m || col >= P.cols) continue;  // cols % 32 == 0: a group is inside or past
     const float4 x0 = *(const float4 *)(cl + r * CROW + c8), x1 = *(const float4 *)(cl + r * CROW + c8 + 4);
     float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -569,8 +582,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
 #pragma unroll
     for (int q = 0; q < 8; q++)
       if (col + q >= rows) x[q] = 0.0f;
-    const float4 b0 = *(const float4 *)(P.bias + col), b1 = *(const float4 *)(P.bias + col + 4);
-    const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
     const size_t at = (size_t)row * P.ldc + col;
     float y[8];
     if (!OUT16 && (P.epi == WH_RESIDUAL || P.epi == WH_GELU_RESIDUAL)) {
@@ -612,7 +623,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
 #pragma unroll
       for (int q = 0; q < 8; q++) {
         if (col + q >= P.dual) break;
-        const float d = x[q] + P.bias[P.cols + col + q];
+        const float d = x[q] + bd[q];
         if constexpr (OUT16) ((_Float16 *)P.c)[at + P.cols + q] = (_Float16)d;
         else ((float *)P.c)[at + P.cols + q] = d;
       }
@@ -667,7 +678,10 @@ Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
   Plan p{64, 64, 2, 2, 4, 1};
   if (t128 >= cus / 2) p = {128, 128, 2, 4, 4, 1};
   else if (t64 < cus)
-    while (p.split < 4 && t64 * p.split < 2L * cus && k % (2 * p.split * 64) == 0) p.split *= 2;
+    // Split only while every split keeps at least 16 k steps: shorter ones spend more on the
+    // pipeline's fill and the partial sums than the extra workgroups win (k = 1024 runs faster whole).
+    while (p.split < 4 && t64 * p.split < 2L * cus && k % (2 * p.split * 64) == 0 && k / (2 * p.split * 64) >= 16)
+      p.split *= 2;
   if (ctx->gemm_plan[0]) {  // tuning override (WAVO_GEMM_PLAN): bm, bn, wm, wn, stages, split
     const int *o = ctx->gemm_plan;
     p = {o[0], o[1], o[2], o[3], o[4], o[5]};
@@ -719,6 +733,8 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     PLAN(64, 128, 1, 4, 6)
     PLAN(128, 64, 1, 2, 4)
     PLAN(64, 64, 1, 2, 6)
+    PLAN(128, 128, 2, 4, 3)
+    PLAN(64, 64, 2, 2, 3)
 #undef PLAN
     if (!ok) return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages", p.bm, p.bn, p.wm, p.wn, p.ns);
     if (int rc = wh_launched(ctx, "gemm")) return rc;

@@ -273,7 +273,8 @@ def test_attention(gpu, t, hd):
     close(gpu.read(ob, (t, d)), want, tol=ATT_TOL, what="qkv layout")
 
 
-@pytest.mark.parametrize("t,valid", [(37, 20), (100, 64), (100, 1)])
+# (300, …): keys split over two workgroups per query tile; valid 10 leaves the first split empty.
+@pytest.mark.parametrize("t,valid", [(37, 20), (100, 64), (100, 1), (300, 150), (300, 10)])
 def test_attention_masked(gpu, t, valid):
     heads, hd = 2, 64
     d = heads * hd
@@ -296,7 +297,8 @@ def relative_inputs(t, heads, hd, seed=17):
 
 
 @pytest.mark.parametrize("t,heads,hd,valid", [(5, 2, 40, None), (37, 2, 40, None), (100, 3, 128, None),
-                                               (750, 8, 128, None), (275, 16, 48, None), (100, 3, 128, 60)])
+                                               (750, 8, 128, None), (275, 16, 48, None), (100, 3, 128, 60),
+                                               (750, 8, 128, 400)])
 def test_relative_attention(gpu, t, heads, hd, valid):
     d = heads * hd
     qkv, pos, u, vb, rows = relative_inputs(t, heads, hd)

@@ -23,6 +23,7 @@
 // group and a block reads the groups of its own stage and the two before.  LDS rows are stored with
 // their 16-byte chunks rotated by the row index, so the 16 lanes that read one chunk column of 16
 // rows hit distinct banks.
+#include <algorithm>
 #include <type_traits>
 
 #include "internal.h"
@@ -77,6 +78,11 @@ struct Args {
   float scale;
   const int *valid_dev;
   int valid;
+  // Key split: nsplit > 1 workgroups share a query tile, each over its own run of key blocks, and
+  // write unnormalized partial outputs po [split][batch][t][heads·hd] and (max, sum) pairs pml
+  // [split][batch][heads][t] for combine_kernel.
+  int nsplit;
+  float *po, *pml;
 };
 
 __device__ __forceinline__ floatx4 mfma(half8 a, half8 b, floatx4 c) {
@@ -182,20 +188,16 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
   // Work item of this workgroup.  Workgroups go to the 8 XCDs round-robin by linear id; the items
   // are renumbered so that each XCD takes a contiguous run of (window, head, query tile) — the
   // query tiles of one head — and its L2 holds that head's operands.
-  int qt = blockIdx.x, head = blockIdx.y, b = blockIdx.z;
-  {
-    const int nq = gridDim.x, total = nq * gridDim.y * gridDim.z;
-    if (total % 8 == 0) {
-      const int lin = blockIdx.x + nq * (blockIdx.y + gridDim.y * blockIdx.z);
-      const int w = (lin % 8) * (total / 8) + lin / 8;
-      qt = w % nq;
-      head = (w / nq) % gridDim.y;
-      b = w / (nq * gridDim.y);
-    }
-  }
+  // Items are ordered query tile fastest, then key split, head and window.
+  const int nq = gridDim.x, ns = A.nsplit, total = nq * gridDim.y * gridDim.z;
+  int w = blockIdx.x + nq * (blockIdx.y + gridDim.y * blockIdx.z);
+  if (total % 8 == 0) w = (w % 8) * (total / 8) + w / 8;
+  const int qt = w % nq, split = (w / nq) % ns, head = (w / (nq * ns)) % A.heads, b = w / (nq * ns * A.heads);
   const int t = A.t, hd = A.hd;
   const int kv_len = A.valid_dev ? min(A.valid_dev[b], t) : min(A.valid, t);
-  const int nkb = (kv_len + KB - 1) / KB;
+  const int nkb_all = (kv_len + KB - 1) / KB;
+  // This workgroup's key blocks kb0 .. nkb − 1.
+  const int kb0 = nkb_all * split / ns, nkb = nkb_all * (split + 1) / ns;
   const int q0 = qt * 16 * QW;      // the workgroup's first query
   const int qi = q0 + 16 * wave + li;  // this lane's query
   const int hoff = head * hd;
@@ -242,11 +244,11 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
       dma16s(base, soff[i], st + sdst[i]);
     }
   };
-  // The two position groups before block 0's own (rows sb0 .. sb0 + 63) into the position parts of
-  // stages NS − 2 and NS − 1, as if blocks −2 and −1 had brought them.
-  auto issue_pre = [&](int grp) {  // grp = −2 or −1
-    const uint32_t st = lds0 + ((grp + NS) % NS) * STAGE;
-    const _Float16 *base = pp + (size_t)(sb0 + 32 * grp + 64) * DP;
+  // The two position groups before block kb0's own into the position parts of the stages of
+  // blocks kb0 − 2 and kb0 − 1, as if those blocks had brought them.
+  auto issue_pre = [&](int kbx) {  // kbx = kb0 − 2 or kb0 − 1 (≥ −2)
+    const uint32_t st = lds0 + ((kbx + NS) % NS) * STAGE;
+    const _Float16 *base = pp + (size_t)(sb0 + 32 * kbx + 64) * DP;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
       const int kind = __builtin_amdgcn_readfirstlane(skind[i]);
@@ -277,15 +279,15 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
   float m = -INFINITY, l = 0.0f;
   float *tw = tt + wave * 48 * 17;
 
-  if (nkb > 0) {
+  if (nkb > kb0) {
     if constexpr (REL) {
-      issue_pre(-2);
-      issue_pre(-1);
+      issue_pre(kb0 - 2);
+      issue_pre(kb0 - 1);
     }
-    issue(0);
-    if (nkb > 1) issue(1);
+    issue(kb0);
+    if (nkb > kb0 + 1) issue(kb0 + 1);
   }
-  for (int kb = 0; kb < nkb; kb++) {
+  for (int kb = kb0; kb < nkb; kb++) {
     // Stage kb has landed (stage kb + 1 may still be in flight); every wave is done with kb − 1.
     if (kb + 1 < nkb) wait_vm<PER>();
     else dma_wait();
@@ -385,6 +387,21 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
   l += __shfl_xor(l, 16, 64);
   l += __shfl_xor(l, 32, 64);
   if (qi >= t) return;
+  if (ns > 1) {  // partial output: unnormalized O, and (m, l) of this key run
+    const int batch = gridDim.z / ns;
+    const size_t prow = (((size_t)split * batch + b) * t + qi) * (size_t)A.heads * hd + hoff;
+#pragma unroll
+    for (int ot = 0; ot < OT; ot++) {
+      const int d = 16 * ot + 4 * g;
+      if (d >= hd) break;
+      *(float4 *)(A.po + prow + d) = make_float4(om[ot][0], om[ot][1], om[ot][2], om[ot][3]);
+    }
+    if (g == 0) {
+      float *ml = A.pml + 2 * ((((size_t)split * batch + b) * A.heads + head) * t + qi);
+      ml[0] = m, ml[1] = l;
+    }
+    return;
+  }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;  // a window with no valid key outputs zeros
   const size_t obase = A.bo * b + (size_t)qi * A.os + hoff;
 #pragma unroll
@@ -396,6 +413,53 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
     if (A.o16) *(half4 *)((_Float16 *)A.o + obase + d) = half4{(_Float16)r.x, (_Float16)r.y, (_Float16)r.z, (_Float16)r.w};
     else *(float4 *)((float *)A.o + obase + d) = r;
   }
+}
+
+// Key-split combine: o = Σ_s e^(m_s − M)·Õ_s / Σ_s e^(m_s − M)·l_s over the splits' unnormalized
+// outputs Õ_s and (max, sum) pairs, M = max_s m_s; zeros where no split saw a valid key.  One thread
+// per 4 dims.
+__global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ po, const float *__restrict__ pml, int ns,
+                                                      int batch, int t, int heads, int hd, void *__restrict__ o, int os,
+                                                      long bo, int o16) {
+  const int q4 = hd / 4;
+  const size_t n = (size_t)batch * t * heads * q4;
+  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256) {
+    const int d = 4 * (int)(e % q4);
+    const size_t r = e / q4;
+    const int head = (int)(r % heads), i = (int)((r / heads) % t), b = (int)(r / ((size_t)heads * t));
+    float mx = -INFINITY;
+    for (int sp = 0; sp < ns; sp++) mx = fmaxf(mx, pml[2 * ((((size_t)sp * batch + b) * heads + head) * t + i)]);
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float den = 0.0f;
+    if (mx != -INFINITY)
+      for (int sp = 0; sp < ns; sp++) {
+        const float *ml = pml + 2 * ((((size_t)sp * batch + b) * heads + head) * t + i);
+        const float w = __expf(ml[0] - mx);
+        den += w * ml[1];
+        const float4 x = *(const float4 *)(po + (((size_t)sp * batch + b) * t + i) * (size_t)heads * hd + head * hd + d);
+        acc.x += w * x.x, acc.y += w * x.y, acc.z += w * x.z, acc.w += w * x.w;
+      }
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    const float4 y = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    const size_t at = bo * b + (size_t)i * os + head * hd + d;
+    if (o16) *(half4 *)((_Float16 *)o + at) = half4{(_Float16)y.x, (_Float16)y.y, (_Float16)y.z, (_Float16)y.w};
+    else *(float4 *)((float *)o + at) = y;
+  }
+}
+
+// Key splits per query tile: enough workgroups for the CUs while every split keeps ≥ 4 key blocks.
+int kv_splits(const wh_ctx *ctx, int t, int heads, int batch) {
+  const int cus = ctx->cus > 0 ? ctx->cus : 256;
+  const long items = (long)((t + 16 * QW - 1) / (16 * QW)) * heads * batch;
+  const int nkb = (t + KB - 1) / KB;
+  int ns = 1;
+  while (ns < 4 && items * ns * 2 <= cus && nkb / (2 * ns) >= 4) ns *= 2;
+  return ns;
+}
+
+// Scratch bytes of the key-split partials (after the packed operands).
+size_t split_bytes(int ns, int t, int heads, int hd, int batch) {
+  return ns > 1 ? ((size_t)ns * batch * t * heads * hd * 4 + 255) / 256 * 256 + (size_t)ns * batch * heads * t * 8 : 0;
 }
 
 template <int DP, typename T>
@@ -414,13 +478,20 @@ int launch_flash(wh_ctx *ctx, const Args &a, int heads, int batch, int dp) {
   const double tt = (double)a.t * a.t * heads * a.hd * batch;
   const double bytes = 2.0 * batch * a.t * heads * a.hd * (REL ? 6 : 4) + (a.o16 ? 2.0 : 4.0) * batch * a.t * heads * a.hd;
   ProfScope prof(ctx, REL ? "attention_rel" : "attention", (REL ? 6.0 : 4.0) * tt, bytes);
-  const dim3 grid((a.t + 16 * QW - 1) / (16 * QW), heads, batch);
+  const dim3 grid((a.t + 16 * QW - 1) / (16 * QW), heads, batch * a.nsplit);
   switch (dp) {
     case 32: flash_kernel<1, REL><<<grid, 64 * QW, 0, ctx->stream>>>(a); break;
     case 64: flash_kernel<2, REL><<<grid, 64 * QW, 0, ctx->stream>>>(a); break;
     default: flash_kernel<4, REL><<<grid, 64 * QW, 0, ctx->stream>>>(a); break;
   }
-  return wh_launched(ctx, "attention");
+  if (int rc = wh_launched(ctx, "attention")) return rc;
+  if (a.nsplit > 1) {
+    const size_t n = (size_t)batch * a.t * heads * (a.hd / 4);
+    const int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
+    combine_kernel<<<blocks, 256, 0, ctx->stream>>>(a.po, a.pml, a.nsplit, batch, a.t, heads, a.hd, a.o, a.os, a.bo, a.o16);
+    return wh_launched(ctx, "attention combine");
+  }
+  return WH_OK;
 }
 
 template <typename T>
@@ -460,8 +531,13 @@ int attention_t(wh_ctx *ctx, const T *qk, const T *v, const T *pos, void *o, int
   // Queries: f16 rows read by the flash kernel directly (f32 input: converted first, after the
   // packed arrays in scratch).
   const size_t qbytes = std::is_same<T, float>::value ? ((size_t)batch * t * qs * 2 + 255) / 256 * 256 : 0;
-  uint8_t *ws = (uint8_t *)wh_scratch(ctx, sp.bytes() + qbytes);
+  a.nsplit = kv_splits(ctx, t, heads, batch);
+  uint8_t *ws = (uint8_t *)wh_scratch(ctx, sp.bytes() + qbytes + split_bytes(a.nsplit, t, heads, hd, batch));
   if (!ws) return WH_EOOM;
+  if (a.nsplit > 1) {
+    a.po = (float *)(ws + sp.bytes() + qbytes);
+    a.pml = a.po + ((size_t)a.nsplit * batch * t * heads * hd + 63) / 64 * 64;
+  }
   _Float16 *kp = (_Float16 *)ws, *vt = (_Float16 *)(ws + (sp.kv * 2 + 255) / 256 * 256);
   _Float16 *pp = (_Float16 *)(ws + 2 * ((sp.kv * 2 + 255) / 256 * 256));
   {
@@ -492,8 +568,8 @@ int attention_t(wh_ctx *ctx, const T *qk, const T *v, const T *pos, void *o, int
 
 }  // namespace
 
-size_t attention_scratch_bytes(int t, int heads, int hd, int batch, int rel) {
-  return pack_shape(t, heads, hd, batch, rel != 0).bytes();
+size_t attention_scratch_bytes(const wh_ctx *ctx, int t, int heads, int hd, int batch, int rel) {
+  return pack_shape(t, heads, hd, batch, rel != 0).bytes() + split_bytes(kv_splits(ctx, t, heads, batch), t, heads, hd, batch);
 }
 
 int launch_attention(wh_ctx *ctx, const void *qk, const void *v, const void *pos, void *o, int t, int heads,

@@ -98,8 +98,9 @@ int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb
 int launch_attention(wh_ctx *ctx, const void *qk, const void *v, const void *pos, void *o, int t,
                      int heads, int hd, const int *valid_dev, int valid, int batch, int out16 = 0,
                      int in16 = 0);
-// Scratch bytes launch_attention uses for t frames × batch windows (rel: relative positions).
-size_t attention_scratch_bytes(int t, int heads, int hd, int batch, int rel);
+// Scratch bytes launch_attention uses for t frames × batch windows (rel: relative positions) on
+// this context's device (its CU count sets the key splits).
+size_t attention_scratch_bytes(const wh_ctx *ctx, int t, int heads, int hd, int batch, int rel);
 int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *b0, const float *w,
                      const float *b, float *y, int t, int f, int ch, int t0, int rows);
 int launch_flatten(wh_ctx *ctx, const float *x, float *y, int t, int f, int ch);

@@ -756,7 +756,7 @@ int arena(wh_model *m, int frames, int batch) {
   if (!m->x || !m->y || !m->h || !m->qk || !m->yr || !m->pos || (sub && (!m->sub || !m->sub2)))
     return wh_fail(m->ctx, WH_EOOM, "arena of %d frames x %d windows: out of device memory", F, B);
   // Attention's split operands for the largest call, so that encoding allocates nothing.
-  if (!wh_scratch(m->ctx, attention_scratch_bytes(F, m->heads, d / m->heads, B, m->arch == PARAKEET)))
+  if (!wh_scratch(m->ctx, attention_scratch_bytes(m->ctx, F, m->heads, d / m->heads, B, m->arch == PARAKEET)))
     return WH_EOOM;
   if (m->arch == PARAKEET) {
     // The sinusoidal table for F frames stays on the device; a call over t frames reads its

@@ -140,6 +140,20 @@ def test_gigaam_full_config(gpu):
     check_ctc(m, full, want)
 
 
+def test_parakeet_full_config(gpu):
+    """the Parakeet-TDT-0.6B-v3 shape (24 layers, d 1024, FFN 4096), 60 s, q8_0 —
+    the FFN's k-split residual projections finish inside the following LayerNorm's kernel."""
+    path = synth.model_path("parakeet", directory=MODELS)
+    mel = synth.parakeet_mel(synth.audio(60, 0))
+    om = ox.Model(path)
+    want = om.encode(mel)
+    m = wa.Model(gpu, path)
+    got = m.encode(mel)[:, :want.shape[1]]
+    assert want.shape[0] == 750
+    err = rel_l2(got, want)
+    assert err < ENCODER_TOL, err
+
+
 @pytest.mark.parametrize("name", ["parakeet", "gigaam", "whisper"])
 def test_graph_replays_equal_eager_calls(gpu, name):
     # The second call with the same buffers is recorded into a HIP graph and later ones replay it.

@@ -699,9 +699,10 @@ void lds_launch(wh_ctx *ctx, dim3 grid, const LdsArgs &a, bool split, bool out16
 
 template <int WT>
 int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
-                 bool out16, float *part) {
+                 bool out16, float *part, int *splits) {
   Plan p = plan_for(ctx, m, l->cols, l->k);
   if (p.split > 1 && !part) p.split = 1;
+  if (splits) *splits = p.split;
   LdsArgs args{a, l->w, l->bias, p.split > 1 ? (void *)part : c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha,
                l->row_bytes};
   dim3 grid((l->cols + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.split);
@@ -739,7 +740,7 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     if (!ok) return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages", p.bm, p.bn, p.wm, p.wn, p.ns);
     if (int rc = wh_launched(ctx, "gemm")) return rc;
   }
-  if (p.split > 1) {
+  if (p.split > 1 && !splits) {
     ProfScope prof(ctx, "gemm_split_finish", 0.0, 4.0 * p.split * m * l->cols + 4.0 * m * width);
     const size_t n = (size_t)m * l->cols;
     const int blocks = (int)std::min<size_t>((n + 255) / 256, 8192);
@@ -765,13 +766,15 @@ size_t split_bytes(const wh_ctx *ctx, const wh_linear *l, int m) {
   return p.split > 1 ? (size_t)p.split * m * l->cols * 4 : 0;
 }
 
-// a16: f16 rows; part: scratch for split-k partial sums (or NULL: no split).
+// a16: f16 rows; part: scratch for split-k partial sums (or NULL: no split).  With `splits`, a split
+// GEMM stops after writing its partial sums (the caller finishes them) and *splits is the count
+// (1: c was written whole).
 int launch_lds(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
-               bool out16, float *part) {
+               bool out16, float *part, int *splits = nullptr) {
   switch (l->type) {
-    case WH_Q8_0: return launch_lds_t<WH_Q8_0>(ctx, a, l, c, m, ldc, epi, alpha, out16, part);
-    case WH_Q4_0: return launch_lds_t<WH_Q4_0>(ctx, a, l, c, m, ldc, epi, alpha, out16, part);
-    default: return launch_lds_t<WH_F16>(ctx, a, l, c, m, ldc, epi, alpha, out16, part);
+    case WH_Q8_0: return launch_lds_t<WH_Q8_0>(ctx, a, l, c, m, ldc, epi, alpha, out16, part, splits);
+    case WH_Q4_0: return launch_lds_t<WH_Q4_0>(ctx, a, l, c, m, ldc, epi, alpha, out16, part, splits);
+    default: return launch_lds_t<WH_F16>(ctx, a, l, c, m, ldc, epi, alpha, out16, part, splits);
   }
 }
 
@@ -871,4 +874,22 @@ int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int
   }
   if (out16) return launch_typed<true, true>(ctx, a16, l, c, m, ldc, epi, alpha);
   return launch_typed<true, false>(ctx, a16, l, c, m, ldc, epi, alpha);
+}
+
+int launch_gemm_h_ln(wh_ctx *ctx, const void *a16, const wh_linear *l, float *x, int m, float alpha, const float *g,
+                     const float *b, void *y, int out16) {
+  if (int rc = check(ctx, a16, l, x, m, WH_RESIDUAL)) return rc;
+  if (m == 0) return WH_OK;
+  const int cols = l->cols;
+  if (l->dual || !lds_path(l, x, cols)) {
+    if (int rc = launch_gemm_h(ctx, a16, l, x, m, cols, WH_RESIDUAL, alpha, 0)) return rc;
+    return launch_layer_norm(ctx, x, g, b, y, m, cols, nullptr, nullptr, 0, out16);
+  }
+  const size_t pb = split_bytes(ctx, l, m);
+  float *part = nullptr;
+  if (pb && !(part = (float *)wh_scratch(ctx, pb))) return WH_EOOM;
+  int splits = 1;
+  if (int rc = launch_lds(ctx, (const _Float16 *)a16, l, x, m, cols, WH_RESIDUAL, alpha, false, part, &splits)) return rc;
+  if (splits > 1) return launch_split_residual_ln(ctx, part, splits, l->bias, l->rows, alpha, x, g, b, y, m, cols, out16);
+  return launch_layer_norm(ctx, x, g, b, y, m, cols, nullptr, nullptr, 0, out16);
 }

@@ -793,8 +793,8 @@ int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int bat
   auto ln16 = [&](const Chan &n) { return launch_layer_norm(c, x, n.w, n.b, y16, rows, d, nullptr, nullptr, 0, 1); };
   CK(ln16(k.norm_ff1));
   CK(g16(y16, k.ff1[0], h16, rows, WH_SILU, 0.0f, 1));
-  CK(g16(h16, k.ff1[1], x, rows, WH_RESIDUAL, 0.5f, 0));
   if (!m->relative) {
+    CK(g16(h16, k.ff1[1], x, rows, WH_RESIDUAL, 0.5f, 0));
     void *yr16 = m->yr;
     CK(launch_layer_norm(c, x, k.norm_attn.w, k.norm_attn.b, y16, rows, d, m->rope, yr16, hd, 1));
     CK(g16(yr16, k.qk, m->qk, rows, WH_BIAS, 0.0f, 1));
@@ -802,7 +802,8 @@ int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int bat
     CK(launch_attention(c, m->qk, m->h, nullptr, y16, t, m->heads, hd, valid_dev, t, batch, 1, 1));
   } else {
     const int pr = 2 * t + 15;
-    CK(ln16(k.norm_attn));
+    // The FFN's residual projection and the attention norm (one kernel after a k-split GEMM).
+    CK(launch_gemm_h_ln(c, h16, k.ff1[1], x, rows, 0.5f, k.norm_attn.w, k.norm_attn.b, y16, 1));
     CK(g16(y16, k.qkv, m->qk, rows, WH_BIAS, 0.0f, 1));
     CK(g16(m->pos16_cur, k.pos, m->yr, pr, WH_BIAS, 0.0f, 1));
     CK(launch_attention(c, m->qk, nullptr, m->yr, y16, t, m->heads, hd, valid_dev, t, batch, 1, 1));
@@ -815,9 +816,8 @@ int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int bat
   CK(g16(y16, k.pw2, x, rows, WH_RESIDUAL, 1.0f, 0));
   CK(ln16(k.norm_ff2));
   CK(g16(y16, k.ff2[0], h16, rows, WH_SILU, 0.0f, 1));
-  CK(g16(h16, k.ff2[1], x, rows, WH_RESIDUAL, 0.5f, 0));
   // The block output is norm_out(x), not the residual stream.
-  return launch_layer_norm(c, x, k.norm_out.w, k.norm_out.b, y, rows, d, nullptr, nullptr, 0);
+  return launch_gemm_h_ln(c, h16, k.ff2[1], x, rows, 0.5f, k.norm_out.w, k.norm_out.b, y, 0);
 }
 
 }  // namespace

@@ -357,6 +357,81 @@ __global__ void copy16_kernel(uint4 *__restrict__ y, const uint4 *__restrict__ x
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) y[i] = x[i];
 }
 
+// The finish of a k-split GEMM with the residual epilogue, fused with the LayerNorm of its result:
+// x[row] += alpha·(Σ_z part[z][row] + bias) (the partial sums added in split order from 0, the W
+// padding columns ≥ wrows contributing epi(0 + bias) as the GEMM gives them), then y = LN(x[row])
+// with the arithmetic of layer_norm_kernel.  One wavefront per row.
+template <typename OT, int NSPLIT>
+__global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__restrict__ part, int splits,
+                                                                const float *__restrict__ bias, int wrows, float alpha,
+                                                                float *__restrict__ x, const float *__restrict__ g,
+                                                                const float *__restrict__ b, OT *__restrict__ y,
+                                                                int rows, int cols) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int row = blockIdx.x * 4 + w;
+  if (row >= rows) return;
+  const int q4 = cols / 4;
+  const size_t plane = (size_t)rows * cols;
+  float4 *xr = (float4 *)(x + (size_t)row * cols);
+  const float4 *pr = (const float4 *)(part + (size_t)row * cols), *b4 = (const float4 *)bias;
+  float4 v[ROW_REGS / 4];
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < ROW_REGS / 4; j++) {
+    const int i = lane + 64 * j;
+    v[j] = make_float4(0, 0, 0, 0);
+    if (i < q4) {
+      float4 acc = make_float4(0, 0, 0, 0);
+      if constexpr (NSPLIT > 0) {  // every partial load in flight at once
+        float4 p[NSPLIT];
+#pragma unroll
+        for (int z = 0; z < NSPLIT; z++) p[z] = pr[z * (plane / 4) + i];
+#pragma unroll
+        for (int z = 0; z < NSPLIT; z++) acc.x += p[z].x, acc.y += p[z].y, acc.z += p[z].z, acc.w += p[z].w;
+      } else {
+        for (int z = 0; z < splits; z++) {
+          const float4 p = pr[z * (plane / 4) + i];
+          acc.x += p.x, acc.y += p.y, acc.z += p.z, acc.w += p.w;
+        }
+      }
+      if (4 * i + 0 >= wrows) acc.x = 0.0f;
+      if (4 * i + 1 >= wrows) acc.y = 0.0f;
+      if (4 * i + 2 >= wrows) acc.z = 0.0f;
+      if (4 * i + 3 >= wrows) acc.w = 0.0f;
+      const float4 bb = b4[i], c = xr[i];
+      v[j] = make_float4(c.x + alpha * (acc.x + bb.x), c.y + alpha * (acc.y + bb.y), c.z + alpha * (acc.z + bb.z),
+                         c.w + alpha * (acc.w + bb.w));
+      xr[i] = v[j];
+      s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+    }
+  }
+  const float mean = wave_sum(s) / (float)cols;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < ROW_REGS / 4; j++) {
+    if (lane + 64 * j < q4) {
+      float dx = v[j].x - mean, dy = v[j].y - mean, dz = v[j].z - mean, dw = v[j].w - mean;
+      q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(q) / (float)cols + 1e-5f);
+  OT *yy = y + (size_t)row * cols;
+  const float4 *g4 = (const float4 *)g, *lb4 = (const float4 *)b;
+#pragma unroll
+  for (int j = 0; j < ROW_REGS / 4; j++) {
+    const int i = lane + 64 * j;
+    if (i < q4) {
+      const float4 gg = g4[i], bb = lb4[i];
+      float4 o;
+      o.x = (v[j].x - mean) * rstd * gg.x + bb.x;
+      o.y = (v[j].y - mean) * rstd * gg.y + bb.y;
+      o.z = (v[j].z - mean) * rstd * gg.z + bb.z;
+      o.w = (v[j].w - mean) * rstd * gg.w + bb.w;
+      store4(yy + 4 * i, o);
+    }
+  }
+}
+
 __global__ void copy_bytes_kernel(uint8_t *__restrict__ y, const uint8_t *__restrict__ x, size_t n) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) y[i] = x[i];
 }
@@ -391,6 +466,29 @@ int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *
     layer_norm_long<<<rows, 64, 0, ctx->stream>>>(x, g, b, (float *)y, cols);
   }
   return wh_launched(ctx, "layer_norm");
+}
+
+int launch_split_residual_ln(wh_ctx *ctx, const float *part, int splits, const float *bias, int wrows, float alpha,
+                             float *x, const float *g, const float *b, void *y, int rows, int cols, int out16) {
+  if (rows <= 0 || cols <= 0 || cols % 4 || cols > ROW_REGS * 64 || splits < 1 || !part || !bias || !x || !g || !b || !y ||
+      (uintptr_t)part % 16 || (uintptr_t)bias % 16 || (uintptr_t)x % 16 || (uintptr_t)g % 16 || (uintptr_t)b % 16 ||
+      (uintptr_t)y % 16)
+    return wh_fail(ctx, WH_EARG, "split_residual_ln: bad arguments (%d x %d, %d splits)", rows, cols, splits);
+  ProfScope prof(ctx, "split_residual_ln", 0.0, (double)rows * cols * (4.0 * splits + 8 + (out16 ? 2 : 4)));
+  const int grid = (rows + 3) / 4;
+#define SRL(OT, N) \
+  split_residual_ln_kernel<OT, N><<<grid, 256, 0, ctx->stream>>>(part, splits, bias, wrows, alpha, x, g, b, (OT *)y, rows, cols)
+  if (out16) {
+    if (splits == 2) SRL(_Float16, 2);
+    else if (splits == 4) SRL(_Float16, 4);
+    else SRL(_Float16, 0);
+  } else {
+    if (splits == 2) SRL(float, 2);
+    else if (splits == 4) SRL(float, 4);
+    else SRL(float, 0);
+  }
+#undef SRL
+  return wh_launched(ctx, "split_residual_ln");
 }
 
 int launch_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int kernel, int stride, int pad,

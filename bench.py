@@ -119,14 +119,25 @@ def gemv_cold(gpu):
     for i in range(4):
         token(i)
     gpu.sync()
+    # A token's GEMVs as one recorded pass per weight copy (Gpu::record), as a decoder step submits
+    # them: the time is the GPU's, not the launches' from Python.
+    passes = []
+    for i in range(2):
+        gpu.record_begin()
+        token(i)
+        passes.append(gpu.record_end())
+    for p in passes:
+        p.replay()
     reps = 20
     state = {"i": 0}
 
     def one():
-        token(state["i"])
+        passes[state["i"] % 2].replay()
         state["i"] += 1
 
     ms = time_region(gpu, one, reps)
+    for p in passes:
+        p.free()
     # The head alone (70.6 MB), cold.
     head = [c[-1] for c in copies]
     st2 = {"i": 0}
@@ -139,7 +150,8 @@ def gemv_cold(gpu):
         one_head()
     hms = time_region(gpu, one_head, 40)
     hbytes = vocab * d // 32 * 34
-    out = {"workload": "whisper-large-v3-turbo decoder GEMVs per token, q8_0, cold (2 weight copies of 168 MB alternate)",
+    out = {"workload": "whisper-large-v3-turbo decoder GEMVs per token, q8_0, cold (2 weight copies of 168 MB alternate), "
+                       "each token's 25 GEMVs replayed as one recorded pass",
            "launches_per_token": len(shapes), "us_per_token": round(ms * 1e3, 2), "weight_bytes": wbytes,
            "achieved": round(wbytes / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM, "unit": "GB/s",
            "frac": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM, 4),

@@ -90,6 +90,20 @@ int wh_profile_read(wh_ctx *ctx, char *out, size_t len);
  * timed region: HIP events on the stream around whatever is queued in between. */
 int wh_region(wh_ctx *ctx, const char *name, double flops, double bytes);
 
+/* ----------------------------------------------------------------------- recorded passes */
+
+/* Gpu::record / finish (src/gpu/mod.rs:922-943): the ops queued on ctx between wh_record_begin and
+ * wh_record_end are recorded, not run, into a pass (a HIP graph); wh_replay queues the whole pass
+ * again, with the buffers and arguments it was recorded with, as often as asked.  Nothing may
+ * allocate while recording: an op that would grow the context's scratch fails (run it once first),
+ * and wh_replay refuses a pass recorded before the scratch moved.  Profiling must be off.  Free a
+ * pass before its context. */
+typedef struct wh_pass wh_pass;
+int wh_record_begin(wh_ctx *ctx);
+int wh_record_end(wh_ctx *ctx, wh_pass **out);
+int wh_replay(wh_ctx *ctx, const wh_pass *pass);
+void wh_pass_free(wh_pass *pass);
+
 /* -------------------------------------------------------------------------------- weights */
 
 /* One GGUF weight tensor [rows][k] in its file bytes (ggml dims [k, rows], dims[0] contiguous:

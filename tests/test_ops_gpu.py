@@ -203,6 +203,46 @@ def test_gemv_decoder_shapes(gpu, wtype, n, k):
         close(got, want, what=f"gemv {n}x{k} type {wtype} epi {e}")
 
 
+def test_recorded_pass_replays(gpu):
+    # Gpu::record / finish: a recorded chain of ops (layer norm -> GEMV -> GEMV with the residual
+    # epilogue -> GEMM) replayed several times, with other work queued between the replays, gives
+    # the eager result every time, bit for bit; the pass's buffers are re-initialised before each
+    # replay so the residual reads the same input.
+    k, n, m = 1280, 1280, 40
+    w1 = ox.quantize(np.random.default_rng(31).normal(0, 0.02, (n, k)).astype(np.float32), wa.Q8_0)
+    w2 = ox.quantize(np.random.default_rng(32).normal(0, 0.02, (n, n)).astype(np.float32), wa.Q8_0)
+    l1 = gpu.linear([(w1, wa.Q8_0, k, n)], rnd(n, 33))
+    l2 = gpu.linear([(w2, wa.Q8_0, n, n)], rnd(n, 34))
+    x0, g, b, c0 = rnd(k, 35), rnd(k, 36), rnd(k, 37), rnd(n, 38)
+    a = rnd(m * k, 39).reshape(m, k)
+    xb, gb, bb, ab = gpu.upload(x0), gpu.upload(g), gpu.upload(b), gpu.upload(a)
+    yb, hb, cb, ob = gpu.buffer(k), gpu.buffer(n), gpu.buffer(n), gpu.buffer(m * n)
+
+    def ops():
+        gpu.layer_norm(xb, gb, bb, yb, 1, k)
+        gpu.gemv(yb, l1, hb, wa.GELU, 0.0)
+        gpu.gemv(hb, l2, cb, wa.RESIDUAL, 1.0)
+        gpu.gemm(ab, l1, ob, m, wa.SILU)
+
+    gpu.write(cb, c0)
+    ops()
+    want_c, want_o = gpu.read(cb, n), gpu.read(ob, (m, n))
+    gpu.record_begin()
+    ops()
+    p = gpu.record_end()
+    for i in range(3):
+        gpu.write(cb, c0)
+        gpu.zero(ob)
+        gpu.zero(hb)
+        p.replay()
+        assert np.array_equal(gpu.read(cb, n), want_c), i
+        assert np.array_equal(gpu.read(ob, (m, n)), want_o), i
+        gpu.gemv(yb, l2, hb, wa.BIAS, 0.0)  # unrelated work between replays
+    p.free()
+    with pytest.raises(wa.WavoError):
+        gpu.record_end()  # not recording
+
+
 @pytest.mark.parametrize("heads,hd", [(2, 40), (3, 36), (20, 64)])
 def test_attend_and_pack(gpu, heads, hd):
     keys = 4100

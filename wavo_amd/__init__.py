@@ -42,6 +42,10 @@ SIGNATURES = {
     "wh_profile": (_i, [_vp, _i]),
     "wh_profile_read": (_i, [_vp, ctypes.c_char_p, _sz]),
     "wh_region": (_i, [_vp, ctypes.c_char_p, ctypes.c_double, ctypes.c_double]),
+    "wh_record_begin": (_i, [_vp]),
+    "wh_record_end": (_i, [_vp, ctypes.POINTER(_vp)]),
+    "wh_replay": (_i, [_vp, _vp]),
+    "wh_pass_free": (None, [_vp]),
     "wh_linear_new": (_i, [_vp, _vp, _i, _vp, _i, _i, ctypes.POINTER(_vp)]),
     "wh_linear_width": (_i, [_vp]),
     "wh_linear_k": (_i, [_vp]),
@@ -157,6 +161,27 @@ def _p(x):
     return int(x)
 
 
+class Pass:
+    """A recorded pass (wh_record_end): replay() queues it again on its context's stream."""
+
+    def __init__(self, gpu, h):
+        self.gpu, self.h = gpu, h
+
+    def replay(self):
+        self.gpu._check(lib().wh_replay(self.gpu.h, self.h))
+
+    def free(self):
+        if self.h:
+            lib().wh_pass_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class Gpu:
     """The device (Gpu, src/gpu/mod.rs:211-577) with the Pass ops (:1394-1678) as methods."""
 
@@ -173,11 +198,29 @@ class Gpu:
 
     def close(self):
         if self.h:
-            # Models hold device memory and recorded graphs of this context: free them first.
+            # Models and recorded passes hold device memory and graphs of this context: free them first.
             for m in list(getattr(self, "_models", ())):
                 m.free()
+            for p in list(getattr(self, "_passes", ())):
+                p.free()
             lib().wh_close(self.h)
             self.h = None
+
+    # -- recorded passes (Gpu::record / finish)
+    def record_begin(self):
+        """Ops queued from here to record_end are recorded into a Pass instead of running."""
+        self._check(lib().wh_record_begin(self.h))
+
+    def record_end(self):
+        h = _vp()
+        self._check(lib().wh_record_end(self.h, ctypes.byref(h)))
+        p = Pass(self, h.value)
+        if not hasattr(self, "_passes"):
+            import weakref
+
+            self._passes = weakref.WeakSet()
+        self._passes.add(p)
+        return p
 
     def _check(self, rc):
         if rc:

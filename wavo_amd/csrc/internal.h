@@ -37,6 +37,7 @@ struct wh_ctx {
   void *scratch = nullptr;
   size_t scratch_bytes = 0;
   long scratch_epoch = 0;  // incremented whenever scratch moves (recorded graphs hold its address)
+  int recording = 0;       // between wh_record_begin and wh_record_end: the stream is being captured
 };
 
 // At least `bytes` of device scratch (256-byte aligned), or nullptr with ctx->error set.  Growing

@@ -59,6 +59,10 @@ ProfScope::~ProfScope() {
 
 void *wh_scratch(wh_ctx *ctx, size_t bytes) {
   if (bytes <= ctx->scratch_bytes) return ctx->scratch;
+  if (ctx->recording) {  // no allocation inside a capture: the op has to run once before recording
+    wh_fail(ctx, WH_EARG, "recording: an op needs %zu bytes of scratch (run it once before recording)", bytes);
+    return nullptr;
+  }
   hipError_t e = hipStreamSynchronize(ctx->stream);
   if (e == hipSuccess && ctx->scratch) e = hipFree(ctx->scratch);
   ctx->scratch = nullptr;
@@ -206,8 +210,76 @@ int wh_read(wh_ctx *ctx, void *host, const void *dptr, size_t bytes) {
 
 void *wh_stream(wh_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 
+// ------------------------------------------------------------------------------ recorded passes
+
+struct wh_pass {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  wh_ctx *ctx = nullptr;
+  long scratch_epoch = 0;
+};
+
+int wh_record_begin(wh_ctx *ctx) {
+  if (!ctx) return WH_EARG;
+  if (ctx->recording) return wh_fail(ctx, WH_EARG, "wh_record_begin: already recording");
+  if (ctx->prof) return wh_fail(ctx, WH_EARG, "wh_record_begin: profiling is on (its events are per launch)");
+  (void)hipSetDevice(ctx->device);
+  hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "wh_record_begin: %s", hipGetErrorString(e));
+  ctx->recording = 1;
+  return WH_OK;
+}
+
+int wh_record_end(wh_ctx *ctx, wh_pass **out) {
+  if (!ctx || !out) return WH_EARG;
+  *out = nullptr;
+  if (!ctx->recording) return wh_fail(ctx, WH_EARG, "wh_record_end: not recording");
+  ctx->recording = 0;
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+  if (e != hipSuccess || !graph) {
+    (void)hipGetLastError();
+    if (graph) (void)hipGraphDestroy(graph);
+    return wh_fail(ctx, WH_EGPU, "wh_record_end: capture failed (%s)", hipGetErrorString(e));
+  }
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipGraphDestroy(graph);
+    return wh_fail(ctx, WH_EGPU, "wh_record_end: %s", hipGetErrorString(e));
+  }
+  wh_pass *p = new wh_pass;
+  p->graph = graph;
+  p->exec = exec;
+  p->ctx = ctx;
+  p->scratch_epoch = ctx->scratch_epoch;
+  *out = p;
+  return WH_OK;
+}
+
+int wh_replay(wh_ctx *ctx, const wh_pass *p) {
+  if (!ctx || !p || p->ctx != ctx) return wh_fail(ctx, WH_EARG, "wh_replay: a pass of another context");
+  if (ctx->recording) return wh_fail(ctx, WH_EARG, "wh_replay: recording");
+  if (p->scratch_epoch != ctx->scratch_epoch)
+    return wh_fail(ctx, WH_EARG, "wh_replay: the context's scratch moved since the pass was recorded; record it again");
+  (void)hipSetDevice(ctx->device);
+  hipError_t e = hipGraphLaunch(p->exec, ctx->stream);
+  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "wh_replay: %s", hipGetErrorString(e));
+  return WH_OK;
+}
+
+void wh_pass_free(wh_pass *p) {
+  if (!p) return;
+  if (p->ctx) (void)hipStreamSynchronize(p->ctx->stream);
+  if (p->exec) (void)hipGraphExecDestroy(p->exec);
+  if (p->graph) (void)hipGraphDestroy(p->graph);
+  delete p;
+}
+
 int wh_profile(wh_ctx *ctx, int mode) {
   if (!ctx || mode < 0 || mode > 2) return WH_EARG;
+  if (ctx->recording) return wh_fail(ctx, WH_EARG, "wh_profile: recording");
   int rc = wh_sync(ctx);
   if (rc) return rc;
   ctx->prof = mode;

@@ -346,7 +346,7 @@ __device__ __forceinline__ void wait_vm() {
 }
 
 // c tile BM × BN per workgroup of WM × WN wavefronts, each a (BM/WM) × (BN/WN) block of 32×32 MFMA
-// tiles, over the k range of split blockIdx.z (k / gridDim.z, a multiple of 64).
+// tiles, over the k range of its split (k / gridDim.z, a multiple of 64).
 //
 // Pipeline.  The k loop moves in 64-wide steps through a ring of NS LDS stages that the LDS DMA
 // fills NS − 1 steps ahead (from scalar base addresses: a step costs the vector units nothing but
@@ -393,11 +393,27 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  // Tile order.  Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2.
+  // A grid that is resident at once (≤ 1024 workgroups: the small-m shapes) is renumbered so that an
+  // XCD takes a contiguous run of (split, column tile, row tile) — one k split and a band of column
+  // tiles over all row tiles — and fetches its share of a and W into its L2 once, instead of every
+  // XCD fetching all of a (measured: a third of the HBM/MALL traffic).  Larger grids keep the
+  // dispatch order, whose concurrently running workgroups on an XCD already share rows and columns.
+  int tx = blockIdx.x, ty = blockIdx.y, tz = blockIdx.z;
+  {
+    const int nx = gridDim.x, ny = gridDim.y, total = nx * ny * gridDim.z;
+    if (total % 8 == 0 && total <= 1024) {
+      const int lin = tx + nx * (ty + ny * tz), l = (lin % 8) * (total / 8) + lin / 8;
+      tz = l / (nx * ny);
+      tx = (l % (nx * ny)) / ny;
+      ty = l % ny;
+    }
+  }
+  const int n0 = tx * BN, m0 = ty * BM;
   const int wm = (wave / WN) * (BM / WM), wn = (wave % WN) * (BN / WN);
   const int lrow = lane & 31, g = lane >> 5;
   const int m = P.m, k = P.k, rows = P.rows;
-  const int nk = k / BK / gridDim.z, kz = blockIdx.z * nk;
+  const int nk = k / BK / gridDim.z, kz = tz * nk;
 
   // Per-lane byte offsets of this wave's DMA instructions from the step's base addresses (rows past
   // m or rows are clamped: their products land in outputs that are discarded or zeroed), and the
@@ -574,7 +590,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
     const float4 x0 = *(const float4 *)(cl + r * CROW + c8), x1 = *(const float4 *)(cl + r * CROW + c8 + 4);
     float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
     if constexpr (SPLIT) {
-      float *cp = (float *)P.c + ((size_t)blockIdx.z * m + row) * P.cols + col;
+      float *cp = (float *)P.c + ((size_t)tz * m + row) * P.cols + col;
       *(float4 *)cp = x0;
       *(float4 *)(cp + 4) = x1;
       continue;

@@ -22,6 +22,8 @@
 // LDS and W blocks loaded straight into registers.
 #include <algorithm>
 #include <cstdio>
+#include <type_traits>
+#include <utility>
 
 #include "internal.h"
 
@@ -345,23 +347,37 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// f(integral_constant<S>, kt0 + S) for S = I .. N − 1 while kt0 + S < nk: a loop body unrolled with
+// its step index known at compile time.
+template <int I, int N, class F>
+__device__ __forceinline__ void unrolled_steps(F &f, int kt0, int nk) {
+  if constexpr (I < N) {
+    if (kt0 + I < nk) {
+      f(std::integral_constant<int, I>{}, kt0 + I);
+      unrolled_steps<I + 1, N>(f, kt0, nk);
+    }
+  }
+}
+
 // c tile BM × BN per workgroup of WM × WN wavefronts, each a (BM/WM) × (BN/WN) block of 32×32 MFMA
-// tiles, over the k range of its split (k / gridDim.z, a multiple of 64).
+// tiles, over the k range of its split (the 64-wide k steps divided evenly over gridDim.z).
 //
 // Pipeline.  The k loop moves in 64-wide steps through a ring of NS LDS stages that the LDS DMA
-// fills NS − 1 steps ahead (from scalar base addresses: a step costs the vector units nothing but
-// the dequantization).  At the top of step kt the wavefronts wait for stage kt + 1 and meet at one
-// barrier; then each issues the DMA of step kt + NS − 1 into the stage freed by step kt − 1, the LDS
-// reads of step kt + 1 into its second register set, and the dequantization and MFMAs of step kt
-// from the first — so LDS latency hides behind the matrix cores.  Each wavefront issues the same
-// number of DMA instructions per step (a wave without an instruction of its own repeats another
-// wave's: identical bytes to the same place), so a vmcnt immediate waits for exactly one step.
+// fills NS − 1 steps ahead, from scalar base addresses (a step costs the vector units nothing but
+// the dequantization).  A step is 4 substeps of 16 k; each wave reads the a fragments of substep
+// s + 1 while the MFMAs of substep s run, and the W data of the next step after the one barrier of
+// the step, which sits after substep 2: there every wave has waited for the next stage's DMA and has
+// finished reading the stage of the previous step, so the DMA of step kt + NS − 1 goes into that
+// stage.  The loop is unrolled by the ring length so that every LDS offset is an immediate.  Each
+// wave issues the same number of DMA instructions per step (a wave without an instruction of its
+// own repeats another wave's: identical bytes to the same place), so a vmcnt immediate waits for
+// exactly one step.
 //
-// Stage layout: a rows of 8 16-byte chunks, chunk c of row r at (c + r/2) % 8 — the 16 lanes that
-// LDS serves together read 16 rows and hit all 64 banks once — then W: F16 rows like a, or
-// quantized rows of one block pair (68 or 36 bytes, as stored).  At substep s, the lane of MFMA
-// column n and k half g takes k slots 32g + 8s .. + 8 — block g of its W row's pair — and the a
-// fragments the same slots.  With WM = 1 every W block of the tile is dequantized once.
+// LDS layout: the a stages (rows of 8 16-byte chunks, chunk c of row r at (c + r/2) % 8 — the 16
+// lanes that LDS serves together read 16 rows and hit all 64 banks once), then the W stages: F16
+// rows like a, or quantized rows of one block pair (68 or 36 bytes, as stored).  At substep s, the
+// lane of MFMA column n and k half g takes k slots 32g + 8s .. + 8 — block g of its W row's pair —
+// and the a fragments the same slots.
 //
 // Epilogue.  The accumulators go through LDS (f32, rows padded so the two lane halves of a tile hit
 // distinct banks) and leave as 8 consecutive columns per lane: 16-byte loads of c for the residual
@@ -372,23 +388,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
   static_assert(TM >= 1 && TN >= 1, "32×32 MFMA tiles per wave");
-  constexpr int BK = 64;
-  constexpr int PAIR1 = WT == WH_Q8_0 ? 68 : WT == WH_Q4_0 ? 36 : 128;  // bytes of 64 weights
+  constexpr int PAIR1 = WT == WH_Q8_0 ? 68 : WT == WH_Q4_0 ? 36 : 128;  // W bytes of 64 weights
   constexpr bool WCH = WT == WH_F16;                                     // W moves in 16-byte chunks
-  constexpr int A_BYTES = BM * BK * 2, W_BYTES = BN * PAIR1, STAGE = (A_BYTES + W_BYTES + 15) / 16 * 16;
+  constexpr int A_ST = BM * 128, W_ST = BN * PAIR1, ST = A_ST + W_ST;
   constexpr int CROW = BN + 8;                                           // f32 per epilogue LDS row
   constexpr int C_BYTES = BM * CROW * 4;
   // NSQ stages asked for, as many as fit in the 160 KiB of LDS.
-  constexpr int NS = NSQ * STAGE + 16 <= 160 * 1024 ? NSQ : (160 * 1024 - 16) / STAGE;
+  constexpr int NS = NSQ * ST + 16 <= 160 * 1024 ? NSQ : (160 * 1024 - 16) / ST;
   static_assert(NS >= 3, "at least three stages");
-  static_assert(WCH || W_BYTES % 256 == 0, "whole DMA instructions");
-  constexpr int NIA = BM / 8;                                   // a: 16-byte DMA instructions per stage
-  constexpr int NIW = WCH ? BN / 8 : W_BYTES / 256;             // W: 16-byte or 4-byte ones
-  constexpr int PA = (NIA + NW - 1) / NW, PW = (NIW + NW - 1) / NW;
-  constexpr int VM = (NS - 3) * (PA + PW);                      // DMA instructions of the later steps
-  static_assert(VM < 64, "vmcnt holds the DMA of NS - 3 steps");
+  static_assert(WCH || W_ST % 256 == 0, "whole DMA instructions");
+  constexpr int W_RG = NS * A_ST;                               // the W stages follow the a stages
+  constexpr int NIA = A_ST / 1024;                              // a: 16-byte DMA instructions per stage
+  constexpr int NIW = WCH ? W_ST / 1024 : W_ST / 256;           // W: 16-byte or 4-byte ones
+  constexpr int PA = (NIA + NW - 1) / NW, PW = (NIW + NW - 1) / NW, PI = PA + PW;
+  static_assert((NS - 2) * PI < 64, "vmcnt holds the DMA of NS - 2 steps");
   // (+16: the odd block of the last W row reads one dword past its row, unused)
-  constexpr int LDS_BYTES = NS * STAGE + 16 > C_BYTES ? NS * STAGE + 16 : C_BYTES;
+  constexpr int LDS_BYTES = NS * ST + 16 > C_BYTES ? NS * ST + 16 : C_BYTES;
   __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -413,7 +428,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   const int wm = (wave / WN) * (BM / WM), wn = (wave % WN) * (BN / WN);
   const int lrow = lane & 31, g = lane >> 5;
   const int m = P.m, k = P.k, rows = P.rows;
-  const int nk = k / BK / gridDim.z, kz = tz * nk;
+  const int nkt = k / 64, kb = nkt * tz / (int)gridDim.z, nk = nkt * (tz + 1) / (int)gridDim.z - kb;
 
   // Per-lane byte offsets of this wave's DMA instructions from the step's base addresses (rows past
   // m or rows are clamped: their products land in outputs that are discarded or zeroed), and the
@@ -432,131 +447,119 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
     if constexpr (WCH) {
       const int r = 8 * n + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
       woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * lc);
-      wlds[i] = A_BYTES + 1024 * n;
+      wlds[i] = 1024 * n;
     } else {
       const int sidx = 64 * n + lane, r = sidx / (PAIR1 / 4), dwi = sidx % (PAIR1 / 4);
       woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 4 * dwi);
-      wlds[i] = A_BYTES + 256 * n;
+      wlds[i] = 256 * n;
     }
   }
-  const uint8_t *abase = (const uint8_t *)P.a + (size_t)kz * BK * 2;
-  const uint8_t *wbase = P.w + (size_t)kz * (WCH ? BK * 2 : PAIR1);
+  const uint8_t *abase = (const uint8_t *)P.a + (size_t)kb * 128;
+  const uint8_t *wbase = P.w + (size_t)kb * PAIR1;
   const uint32_t lds0 = lds_addr(lds);
-  auto issue = [&](int kt) {
-    const uint32_t st = lds0 + (kt % NS) * STAGE;
-    const uint8_t *ab = abase + (size_t)kt * BK * 2, *wb = wbase + (size_t)kt * (WCH ? BK * 2 : PAIR1);
+  auto issue = [&](int kt, int slot) {
+    const uint8_t *ab = abase + (size_t)kt * 128, *wb = wbase + (size_t)kt * PAIR1;
 #pragma unroll
-    for (int i = 0; i < PA; i++) dma16s(ab, aoff[i], st + alds[i]);
+    for (int i = 0; i < PA; i++) dma16s(ab, aoff[i], lds0 + slot * A_ST + alds[i]);
 #pragma unroll
     for (int i = 0; i < PW; i++) {
-      if constexpr (WCH) dma16s(wb, woff[i], st + wlds[i]);
-      else dma4s(wb, woff[i], st + wlds[i]);
+      if constexpr (WCH) dma16s(wb, woff[i], lds0 + W_RG + slot * W_ST + wlds[i]);
+      else dma4s(wb, woff[i], lds0 + W_RG + slot * W_ST + wlds[i]);
     }
   };
 
-  // One step's operands in registers: the a fragments of the 4 substeps and the W rows' data
-  // (quantized: the pair's dwords of the lane's block and its scale; F16: the fragments).
-  constexpr int ND = WT == WH_Q8_0 ? 9 : 5;
-  struct Regs {
-    half8 a[4][TM];
-    uint32_t dw[TN][WCH ? 1 : ND];
-    uint32_t sc[TN];
-    half8 b[WCH ? 4 : 1][TN];
+  // LDS read offsets of the lane: a chunk (4g + s) of row wm + lrow (+32i), rotated by row/2; the
+  // lane's W block (quantized: g = 0 reads dwords 0.. with the data from byte 2, g = 1 the dwords
+  // from byte BLK + 2 with the scale in the high half of the dword before); F16 chunks like a.
+  uint32_t a_off[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) a_off[s] = (wm + lrow) * 128 + 16 * ((4 * g + s + (lrow >> 1)) & 7);
+  constexpr int ND = WT == WH_Q8_0 ? 9 : WT == WH_Q4_0 ? 5 : 16;  // dwords per lane per W row and step
+  constexpr int BLK = PAIR1 / 2;
+  const uint32_t w_row = W_RG + (wn + lrow) * PAIR1;
+  const uint32_t w_dat = w_row + (g ? BLK + 2 : 0), w_sc = w_row + (g ? BLK - 2 : 0);
+  uint32_t wf_off[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) wf_off[s] = w_row + 16 * ((4 * g + s + (lrow >> 1)) & 7);
+
+  auto read_a = [&](half8 (&f)[TM], int slot, int s) {
+#pragma unroll
+    for (int i = 0; i < TM; i++) f[i] = *(const half8 *)(lds + a_off[s] + slot * A_ST + i * 4096);
   };
-  // LDS half offsets of the lane's a rows and W rows within a stage (rotation r/2 applied per chunk).
-  int arow[TM], wrow[TN];
+  auto read_w = [&](uint32_t (&w)[TN][ND], uint32_t (&sc)[TN], int slot) {
 #pragma unroll
-  for (int i = 0; i < TM; i++) arow[i] = wm + 32 * i + lrow;
+    for (int j = 0; j < TN; j++) {
+      if constexpr (WCH) {
 #pragma unroll
-  for (int j = 0; j < TN; j++) wrow[j] = wn + 32 * j + lrow;
-  auto load = [&](Regs &R, int kt) {
-    const uint8_t *st = lds + (kt % NS) * STAGE;
-    const _Float16 *as = (const _Float16 *)st;
-    if constexpr (!WCH) {
-      constexpr int BLK = PAIR1 / 2;
+        for (int s = 0; s < 4; s++) {
+          const uint4 x = *(const uint4 *)(lds + wf_off[s] + slot * W_ST + j * 32 * PAIR1);
+          w[j][4 * s] = x.x, w[j][4 * s + 1] = x.y, w[j][4 * s + 2] = x.z, w[j][4 * s + 3] = x.w;
+        }
+        sc[j] = 0;
+      } else {
+        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * PAIR1);
 #pragma unroll
-      for (int j = 0; j < TN; j++) {
-        // Even block: scale in the low half of dword 0, data from byte 2; odd block (bytes
-        // BLK..): scale in the high half of the dword before byte BLK + 2, where its data starts.
-        const uint32_t *row = (const uint32_t *)(st + A_BYTES) + wrow[j] * (PAIR1 / 4);
-        const uint32_t *p = row + (g ? (BLK + 2) / 4 : 0);
-        R.sc[j] = g ? row[(BLK + 2) / 4 - 1] : row[0];
-#pragma unroll
-        for (int i = 0; i < ND; i++) R.dw[j][i] = p[i];
+        for (int i = 0; i < ND; i++) w[j][i] = q[i];
+        sc[j] = *(const uint32_t *)(lds + w_sc + slot * W_ST + j * 32 * PAIR1);
       }
     }
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-      const int lc = 4 * g + s;
-#pragma unroll
-      for (int i = 0; i < TM; i++) R.a[s][i] = *(const half8 *)(as + arow[i] * BK + 8 * ((lc + (arow[i] >> 1)) & 7));
-      if constexpr (WCH)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-          R.b[s][j] = *(const half8 *)((const _Float16 *)(st + A_BYTES) + wrow[j] * BK + 8 * ((lc + (wrow[j] >> 1)) & 7));
-    }
   };
+
   floatx16 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
     for (int j = 0; j < TN; j++) acc[i][j] = floatx16{};
-  auto compute = [&](const Regs &R) {
-    half2 d2[TN];
-    const uint32_t sh = g ? 0u : 2u;
-    if constexpr (!WCH)
+  uint32_t wq[2][TN][ND], sc[2][TN];
+  half8 af[2][TM];
+  const uint32_t sh = g ? 0u : 2u;
+  // Substep s of a step: dequantize the lane's W fragment (quantized) and run the TM × TN MFMAs.
+  auto mma = [&](const half8 (&f)[TM], const uint32_t (&w)[TN][ND], const uint32_t (&scl)[TN], int s) {
 #pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(g ? R.sc[j] >> 16 : R.sc[j] & 0xffffu));
-        d2[j] = half2{d, d};
+    for (int j = 0; j < TN; j++) {
+      half8 b;
+      if constexpr (WCH) b = __builtin_bit_cast(half8, make_uint4(w[j][4 * s], w[j][4 * s + 1], w[j][4 * s + 2], w[j][4 * s + 3]));
+      else {
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(g ? scl[j] >> 16 : scl[j] & 0xffffu));
+        b = dequant_frag<WT>(w[j], sh, half2{d, d}, s);
       }
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-      half8 bf[TN];
-#pragma unroll
-      for (int j = 0; j < TN; j++) {
-        if constexpr (WCH) bf[j] = R.b[s][j];
-        else bf[j] = dequant_frag<WT>(R.dw[j], sh, d2[j], s);
-      }
-#pragma unroll
-      for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(R.a[s][i], bf[j], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < TM; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], b, acc[i][j], 0, 0, 0);
     }
-  };
-  // Top of step kt: stage kt + 1 (if any) has landed for every wavefront, and every wavefront is
-  // done with the stage of step kt − 1 (its registers were loaded during step kt − 2).
-  auto top = [&](int kt) {
-    if (kt + 1 < nk) {
-      if (kt + NS - 2 < nk) wait_vm<VM>();
-      else dma_wait();
-    }
-    __syncthreads();
-    if (kt + NS - 1 < nk) issue(kt + NS - 1);
   };
 
-  Regs r0, r1;
 #pragma unroll
   for (int s = 0; s < NS - 1; s++)
-    if (s < nk) issue(s);
-  static_assert((NS - 2) * (PA + PW) < 64, "vmcnt holds the DMA of NS - 2 steps");
+    if (s < nk) issue(s, s);
   if (nk > 0) {
-    if (nk - 1 >= NS - 2) wait_vm<(NS - 2) * (PA + PW)>();  // stages 1 .. NS - 2 may be in flight
+    if (nk - 1 >= NS - 2) wait_vm<(NS - 2) * PI>();  // stages 1 .. NS - 2 may be in flight
     else dma_wait();
     __syncthreads();
-    load(r0, 0);
+    read_w(wq[0], sc[0], 0);
+    read_a(af[0], 0, 0);
   }
-  // Two steps per iteration so that the register sets alternate without copies.
-  for (int kt = 0; kt < nk; kt += 2) {
-    top(kt);
-    if (kt + 1 < nk) load(r1, kt + 1);
-    compute(r0);
-    if (kt + 1 >= nk) break;
-    top(kt + 1);
-    if (kt + 2 < nk) load(r0, kt + 2);
-    compute(r1);
-  }
+  // Step kt (S = kt modulo the unroll: ring slot S % NS, register set S % 2).
+  auto step = [&](auto S_c, int kt) {
+    constexpr int S = decltype(S_c)::value, slot = S % NS, cur = S & 1;
+    read_a(af[1], slot, 1);
+    mma(af[0], wq[cur], sc[cur], 0);
+    read_a(af[0], slot, 2);
+    mma(af[1], wq[cur], sc[cur], 1);
+    read_a(af[1], slot, 3);
+    mma(af[0], wq[cur], sc[cur], 2);
+    if (kt + 1 < nk) {
+      // Stage kt + 1 has landed for every wave, and every wave is done with stage kt − 1.
+      if (kt + NS - 2 < nk) wait_vm<(NS - 3) * PI>();
+      else dma_wait();
+      __syncthreads();
+      if (kt + NS - 1 < nk) issue(kt + NS - 1, (slot + NS - 1) % NS);
+      read_w(wq[cur ^ 1], sc[cur ^ 1], (slot + 1) % NS);
+      read_a(af[0], (slot + 1) % NS, 0);
+    }
+    mma(af[1], wq[cur], sc[cur], 3);
+  };
+  constexpr int UNR = NS % 2 ? 2 * NS : NS;
+  for (int kt0 = 0; kt0 < nk; kt0 += UNR) unrolled_steps<0, UNR>(step, kt0, nk);
 
   // Epilogue through LDS: every DMA has landed (the last step waited for it) and the barrier below
   // ends every wavefront's reads of the stages.  A thread's 8-column group is the same on every row
@@ -685,9 +688,9 @@ struct Plan {
   int bm, bn, wm, wn, ns, split;
 };
 
-// Chosen per GEMM shape from measurements on MI355X: many output tiles → 128×128 tiles of 8
-// wavefronts; fewer → 64×64 tiles of 4 wavefronts, and when even those leave CUs idle, k split 2
-// or 4 ways.  NS LDS stages of 64-wide k steps.
+// Chosen per GEMM shape from measurements on MI355X (random operands, inside the encoder step):
+// many output tiles → 128×128 tiles of 8 wavefronts; fewer → 64×64 tiles of 4 wavefronts, and when
+// even those leave CUs idle, k split 2 or 4 ways.  Four LDS stages of 64-wide k steps.
 Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
   const int cus = ctx->cus > 0 ? ctx->cus : 256;
   const long t128 = (long)((cols + 127) / 128) * ((m + 127) / 128), t64 = (long)((cols + 63) / 64) * ((m + 63) / 64);

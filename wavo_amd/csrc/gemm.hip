@@ -695,7 +695,11 @@ Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
   const int cus = ctx->cus > 0 ? ctx->cus : 256;
   const long t128 = (long)((cols + 127) / 128) * ((m + 127) / 128), t64 = (long)((cols + 63) / 64) * ((m + 63) / 64);
   Plan p{64, 64, 2, 2, 4, 1};
-  if (t128 >= cus / 2) p = {128, 128, 2, 4, 4, 1};
+  // Grids of several workgroups per CU (batched windows, m ≈ 12000): three stages, so two
+  // workgroups share a CU (measured 187 against 221 µs at 12000×4096×1024); a single wave of
+  // workgroups (one 750-frame window) runs faster with four.
+  if (t128 >= 4L * cus) p = {128, 128, 2, 4, 3, 1};
+  else if (t128 >= cus / 2) p = {128, 128, 2, 4, 4, 1};
   else if (t64 < cus)
     // Split only while every split keeps at least 16 k steps: shorter ones spend more on the
     // pipeline's fill and the partial sums than the extra workgroups win (k = 1024 runs faster whole).

@@ -73,10 +73,12 @@ def test_gemm(gpu, wtype, k, n, cols):
 
 
 @pytest.mark.parametrize("wtype", [wa.Q8_0, wa.Q4_0, wa.F16])
-@pytest.mark.parametrize("m,n,k", [(2048, 4096, 256), (750, 4096, 1024), (750, 1024, 4096), (1515, 1024, 1024)])
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 256), (750, 4096, 1024), (750, 1024, 4096), (1515, 1024, 1024),
+                                   (4224, 4096, 192)])
 def test_gemm_large(gpu, wtype, m, n, k):
     # The tile plans of the main kernel at the encoder's shapes: 128×128 tiles of 8 wavefronts with
-    # 64- and 128-wide k steps, 64×64 tiles with k split 4 ways (partial sums finished in order).
+    # four LDS stages (one wave of workgroups) or three (4224 rows: several workgroups per CU, the
+    # batched-window plan), 64×64 tiles with k split 4 ways (partial sums finished in order).
     w = np.random.default_rng(1).normal(0, 0.02, (n, k)).astype(np.float32)
     raw = ox.quantize(w, wtype)
     bias = rnd(n, 2)

@@ -264,48 +264,54 @@ __global__ void depthwise_kernel(const float *__restrict__ x, const float *__res
 
 // conv0 (1 → ch, 3×3 s2 p1) + ReLU, never stored, then the depthwise conv2 + bias, into row
 // blockIdx.y of a chunk (output row 2·t0 − 1 + blockIdx.y; rows from ⌈t/4⌉ on zero, as masked)
-// (spatial.wgsl:50-107; src/parakeet/cpu.rs:103-152).  The 7×7 input patch goes to LDS first.
+// (spatial.wgsl:50-107; src/parakeet/cpu.rs:103-152).  A workgroup makes the whole output row, one
+// thread per channel: the row's 7 × (4·f2 + 3) input patch goes to LDS once and each thread keeps
+// its channel's 18 taps in registers across the f2 positions.
 __global__ void first_depthwise_kernel(const float *__restrict__ x, const float *__restrict__ w,
                                        const float *__restrict__ b, float *__restrict__ y,
                                        const float *__restrict__ w0, const float *__restrict__ b0, int t,
                                        int f, int ch, int t0) {
-  __shared__ float x7[49];
+  extern __shared__ float xs[];  // 7 rows × pw columns; column 4·fo + j is input column 4·fo + j − 3
   const int t1 = half_len(t), f1 = half_len(f), f2 = half_len(f1);
   const int r = 2 * t0 + blockIdx.y;  // output row + 1
-  const int fo = blockIdx.x;
-  const int lid = threadIdx.x;
-  if (lid < 49) {
-    int tm = 4 * r + lid / 7 - 7, fm = 4 * fo + lid % 7 - 3;
-    x7[lid] = (tm >= 0 && tm < t && fm >= 0 && fm < f) ? x[(size_t)tm * f + fm] : 0.0f;
+  const int pw = 4 * f2 + 3;
+  for (int e = threadIdx.x; e < 7 * pw; e += blockDim.x) {
+    const int tm = 4 * r + e / pw - 7, fm = e % pw - 3;
+    xs[e] = (tm >= 0 && tm < t && fm >= 0 && fm < f) ? x[(size_t)tm * f + fm] : 0.0f;
   }
   __syncthreads();
   const bool masked = r > half_len(t1);
-  for (int c = lid; c < ch; c += blockDim.x) {
-    float a[9];
+  for (int c = threadIdx.x; c < ch; c += blockDim.x) {
+    float a[9], wd[9];
 #pragma unroll
-    for (int q = 0; q < 9; q++) a[q] = w0[q * ch + c];
-    float acc = b[c];
-    for (int i = 0; i < 3; i++) {
-      int ti = 2 * r + i - 2;
-      for (int j = 0; j < 3; j++) {
-        int fi = 2 * fo + j;
-        if (ti >= 1 && ti <= t1 && fi >= 1 && fi <= f1) {
-          int o = 14 * i + 2 * j;
-          float v = b0[c];
-          v += a[0] * x7[o];
-          v += a[1] * x7[o + 1];
-          v += a[2] * x7[o + 2];
-          v += a[3] * x7[o + 7];
-          v += a[4] * x7[o + 8];
-          v += a[5] * x7[o + 9];
-          v += a[6] * x7[o + 14];
-          v += a[7] * x7[o + 15];
-          v += a[8] * x7[o + 16];
-          acc += w[(i * 3 + j) * ch + c] * fmaxf(v, 0.0f);
+    for (int q = 0; q < 9; q++) a[q] = w0[q * ch + c], wd[q] = w[q * ch + c];
+    const float bias0 = b0[c], bias = b[c];
+    for (int fo = 0; fo < f2; fo++) {
+      float acc = bias;
+#pragma unroll
+      for (int i = 0; i < 3; i++) {
+        const int ti = 2 * r + i - 2;
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+          const int fi = 2 * fo + j;
+          if (ti >= 1 && ti <= t1 && fi >= 1 && fi <= f1) {
+            const float *p = xs + 2 * i * pw + 4 * fo + 2 * j;
+            float v = bias0;
+            v += a[0] * p[0];
+            v += a[1] * p[1];
+            v += a[2] * p[2];
+            v += a[3] * p[pw];
+            v += a[4] * p[pw + 1];
+            v += a[5] * p[pw + 2];
+            v += a[6] * p[2 * pw];
+            v += a[7] * p[2 * pw + 1];
+            v += a[8] * p[2 * pw + 2];
+            acc += wd[i * 3 + j] * fmaxf(v, 0.0f);
+          }
         }
       }
+      y[((size_t)blockIdx.y * f2 + fo) * ch + c] = masked ? 0.0f : acc;
     }
-    y[((size_t)blockIdx.y * f2 + fo) * ch + c] = masked ? 0.0f : acc;
   }
 }
 
@@ -547,8 +553,9 @@ int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *
   ProfScope prof(ctx, w0 ? "first_depthwise" : "depthwise", 0.0,
                  4.0 * rows * half_len(w0 ? half_len(f) : f) * ch * (w0 ? 1 : 4));
   if (w0) {
-    dim3 grid(half_len(half_len(f)) , rows);
-    first_depthwise_kernel<<<grid, threads < 64 ? 64 : threads, 0, ctx->stream>>>(x, w, b, y, w0, b0, t, f, ch, t0);
+    const size_t lds = sizeof(float) * 7 * (4 * (size_t)half_len(half_len(f)) + 3);
+    if (lds > 64 * 1024) return wh_fail(ctx, WH_EARG, "depthwise: %d mel bins is more than one workgroup's patch holds", f);
+    first_depthwise_kernel<<<dim3(1, rows), threads < 64 ? 64 : threads, lds, ctx->stream>>>(x, w, b, y, w0, b0, t, f, ch, t0);
   } else {
     dim3 grid(half_len(f), rows);
     depthwise_kernel<<<grid, threads, 0, ctx->stream>>>(x, w, b, y, t, f, ch, t0);

@@ -377,9 +377,10 @@ int gemv_t(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, f
 // c[i] = W[ids[idx]][i] + pos[offset + i] + bias[i] (gemm.wgsl:309-327).
 __global__ void embed_kernel(const uint8_t *__restrict__ w, int type, size_t row_bytes, const float *__restrict__ pos,
                              const float *__restrict__ bias, float *__restrict__ c, const uint32_t *__restrict__ ids,
-                             int idx, int k, int offset) {
+                             int idx, int k, int offset, const int *__restrict__ dpos, int dstride) {
   int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= k) return;
+  if (dpos) offset = *dpos * dstride;
   const uint8_t *wr = w + (size_t)ids[idx] * row_bytes;
   float v;
   switch (type) {
@@ -410,7 +411,9 @@ constexpr int KEYS = 256;
 // Part (c, h): head h's query against keys c·KEYS.. (decode.wgsl:56-119).
 __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q, const uint32_t *__restrict__ kv,
                                                      float *__restrict__ part, int n, int hd, float scale,
-                                                     int cols, int heads) {
+                                                     int cols, int heads, const int *__restrict__ dn) {
+  if (dn) n = min(*dn + n, cols);
+  if ((int)blockIdx.x * KEYS >= n) return;  // a grid sized for the most keys: parts past n are unused
   __shared__ float qs[128];
   __shared__ float s[KEYS];
   __shared__ float red[8];
@@ -476,7 +479,9 @@ __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q
 }
 
 // Per head: the parts rescaled to their common maximum, summed and normalized (decode.wgsl:121-147).
-__global__ void combine_kernel(const float *__restrict__ part, float *__restrict__ o, int n, int hd) {
+__global__ void combine_kernel(const float *__restrict__ part, float *__restrict__ o, int n, int hd,
+                               const int *__restrict__ dn, int cols) {
+  if (dn) n = min(*dn + n, cols);
   const int parts = (n + KEYS - 1) / KEYS;
   const float *base = part + (size_t)blockIdx.x * parts * (hd + 2);
   float m = -INFINITY;
@@ -492,7 +497,8 @@ __global__ void combine_kernel(const float *__restrict__ part, float *__restrict
 
 // Rows of x (K then V, d floats each) into the f16 cache at positions col.. (decode.wgsl:148-173).
 __global__ void pack_kernel(const float *__restrict__ x, uint32_t *__restrict__ y, int n, int d, int cols, int col,
-                            int src, int stride) {
+                            int src, int stride, const int *__restrict__ dcol) {
+  if (dcol) col = *dcol;
   int i, j;
   if (n > 1) {
     i = blockIdx.y * 4 + threadIdx.x / 64;
@@ -502,7 +508,7 @@ __global__ void pack_kernel(const float *__restrict__ x, uint32_t *__restrict__ 
     j = 0;
   }
   const int half = d / 2;
-  if (i >= d || j >= n) return;
+  if (i >= d || j >= n || col + j >= cols) return;
   const float *p = x + src + (size_t)j * stride + 2 * i;
   size_t at = i < half ? (size_t)i * cols + col + j : (size_t)half * cols + (size_t)(col + j) * half + i - half;
   y[at] = h16(p[0]) | (h16(p[1]) << 16);
@@ -535,38 +541,56 @@ int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int e
   return wh_fail(ctx, WH_EARG, "gemv: weight type %d", l->type);
 }
 
+// A decoder step's token and position into device memory (ids[0], ids[1]), where a recorded step
+// reads them: a kernel argument, so the host neither copies nor waits.
+__global__ void step_args_kernel(uint32_t *ids, uint32_t token, uint32_t pos) {
+  if (threadIdx.x == 0) {
+    ids[0] = token;
+    ids[1] = pos;
+  }
+}
+
+int launch_step_args(wh_ctx *ctx, uint32_t *ids, int token, int pos) {
+  if (!ids || token < 0 || pos < 0) return wh_fail(ctx, WH_EARG, "step arguments: bad arguments");
+  step_args_kernel<<<1, 64, 0, ctx->stream>>>(ids, (uint32_t)token, (uint32_t)pos);
+  return wh_launched(ctx, "step_args");
+}
+
 int launch_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, const uint32_t *ids, int i,
-                 int offset) {
+                 int offset, const int *dpos, int dstride) {
   if (!pos || !c || !ids || i < 0 || offset < 0) return wh_fail(ctx, WH_EARG, "embed: bad arguments");
   ProfScope prof(ctx, "embed", 0.0, 12.0 * l->k);
   embed_kernel<<<(l->k + 255) / 256, 256, 0, ctx->stream>>>(l->w, l->type, l->row_bytes, pos, l->bias, c, ids, i,
-                                                            l->k, offset);
+                                                            l->k, offset, dpos, dstride);
   return wh_launched(ctx, "embed");
 }
 
 int launch_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, float *o, int n, int cols,
-                  int heads, int hd) {
+                  int heads, int hd, const int *dn) {
   if (n <= 0 || n > cols || heads <= 0 || hd <= 0 || hd > 128 || hd % 2 || !q || !kv || !part || !o)
     return wh_fail(ctx, WH_EARG, "attend: bad arguments (n %d, cols %d, hd %d)", n, cols, hd);
   float scale = 1.0f / sqrtf((float)hd);
-  dim3 grid((n + KEYS - 1) / KEYS, heads);
-  ProfScope prof(ctx, "attend", 4.0 * n * heads * hd, 2.0 * n * heads * hd * 2 + 4.0 * heads * hd);
-  attend_kernel<<<grid, 256, 0, ctx->stream>>>(q, kv, part, n, hd, scale, cols, heads);
+  // A key count in device memory: the grid covers the whole cache and parts past it return.
+  const int most = dn ? cols : n;
+  dim3 grid((most + KEYS - 1) / KEYS, heads);
+  ProfScope prof(ctx, "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
+  attend_kernel<<<grid, 256, 0, ctx->stream>>>(q, kv, part, n, hd, scale, cols, heads, dn);
   int rc = wh_launched(ctx, "attend");
   if (rc) return rc;
-  combine_kernel<<<heads, 64, 0, ctx->stream>>>(part, o, n, hd);
+  combine_kernel<<<heads, 64, 0, ctx->stream>>>(part, o, n, hd, dn, cols);
   return wh_launched(ctx, "combine");
 }
 
-int launch_pack(wh_ctx *ctx, const float *x, int src, int stride, uint32_t *y, int rows, int d, int cols, int col) {
+int launch_pack(wh_ctx *ctx, const float *x, int src, int stride, uint32_t *y, int rows, int d, int cols, int col,
+                const int *dcol) {
   if (rows <= 0 || d <= 0 || d % 2 || cols <= 0 || col < 0 || col + rows > cols || src < 0 || !x || !y)
     return wh_fail(ctx, WH_EARG, "pack: bad arguments");
   ProfScope prof(ctx, "pack", 0.0, 4.0 * rows * 2 * d + 2.0 * rows * 2 * d);
   if (rows == 1) {
-    pack_kernel<<<(d + 255) / 256, 256, 0, ctx->stream>>>(x, y, rows, d, cols, col, src, stride);
+    pack_kernel<<<(d + 255) / 256, 256, 0, ctx->stream>>>(x, y, rows, d, cols, col, src, stride, dcol);
   } else {
     dim3 grid((rows + 63) / 64, (d + 3) / 4);
-    pack_kernel<<<grid, 256, 0, ctx->stream>>>(x, y, rows, d, cols, col, src, stride);
+    pack_kernel<<<grid, 256, 0, ctx->stream>>>(x, y, rows, d, cols, col, src, stride, dcol);
   }
   return wh_launched(ctx, "pack");
 }

@@ -93,8 +93,10 @@ int launch_split_residual_ln(wh_ctx *ctx, const float *part, int splits, const f
 int launch_to_half(wh_ctx *ctx, const float *x, void *y, size_t n);
 int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,
                 int offset);
+// With dpos (device memory), the position offset is (*dpos)·dstride instead of `offset`: a recorded
+// decoder step reads its position from the device.
 int launch_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, const uint32_t *ids,
-                 int i, int offset);
+                 int i, int offset, const int *dpos = nullptr, int dstride = 0);
 // out16: y (and yr) as f16, for consumers that are GEMMs.
 int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *b, void *y, int rows,
                       int cols, const float *table, void *yr, int head_dim, int out16 = 0);
@@ -114,10 +116,14 @@ int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *
                      const float *b, float *y, int t, int f, int ch, int t0, int rows);
 int launch_flatten(wh_ctx *ctx, const float *x, float *y, int t, int f, int ch);
 int launch_argmax(wh_ctx *ctx, const float *x, uint32_t *out, int n);
+int launch_step_args(wh_ctx *ctx, uint32_t *ids, int token, int pos);
+// With dn (device memory), the key count is *dn + n (at most cols).
 int launch_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, float *o, int n,
-                  int cols, int heads, int hd);
+                  int cols, int heads, int hd, const int *dn = nullptr);
+// With dcol (device memory), the first cache column is *dcol instead of `col` (columns past the
+// cache are not written).
 int launch_pack(wh_ctx *ctx, const float *x, int src, int stride, uint32_t *y, int rows, int d,
-                int cols, int col);
+                int cols, int col, const int *dcol = nullptr);
 int launch_zero(wh_ctx *ctx, void *dst, size_t bytes);
 // Device-to-device copy with a kernel (a graph node like any other launch).
 int launch_copy(wh_ctx *ctx, void *dst, const void *src, size_t bytes);

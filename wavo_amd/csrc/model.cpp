@@ -361,6 +361,7 @@ class Loader {
 // ----------------------------------------------------------------------------------- model
 
 enum Arch { GIGAAM = 0, PARAKEET = 1, WHISPER = 2 };
+constexpr intptr_t WHISPER_STEP = 16;  // the recording key of a Whisper decoder step
 
 struct Block {
   Chan norm_ff1, norm_attn, norm_conv, norm_ff2, norm_out, conv_norm, dw;
@@ -1247,8 +1248,8 @@ int wh_whisper_begin(wh_model *m, const float *enc, int frames) {
     m->datt = dev_alloc(m, d);
     m->dpart = dev_alloc(m, wh_attend_len(std::max(m->frames, m->context), m->dec_heads, d / m->dec_heads));
     m->dscratch = dev_alloc(m, (size_t)m->frames * 2 * d);
-    float *ids = nullptr;
-    CK(wh_alloc(c, 1, &ids));
+    float *ids = nullptr;  // the step's token and position
+    CK(wh_alloc(c, 2, &ids));
     m->ids = (uint32_t *)ids;
     (void)vp;
     if (!m->dx || !m->dy || !m->dqkv || !m->dh || !m->datt || !m->dpart || !m->dscratch) return WH_EOOM;
@@ -1269,29 +1270,31 @@ int wh_whisper_step(wh_model *m, int token, int pos, float *logits) {
     return WH_EARG;
   const int d = m->d, heads = m->dec_heads, hd = d / heads;
   wh_ctx *c = m->ctx;
-  uint32_t tok = (uint32_t)token;
-  hipError_t e = hipMemcpyAsync(m->ids, &tok, 4, hipMemcpyHostToDevice, c->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-  if (e != hipSuccess) return wh_fail(c, WH_EGPU, "token: %s", hipGetErrorString(e));
+  // The token and position go to device memory; the step itself reads them there, so one recording
+  // serves every position.
+  CK(launch_step_args(c, m->ids, token, pos));
+  const int *dpos = (const int *)(m->ids + 1);
   // Decoder::record_step (src/transformer.rs:254-290).
-  CK(launch_embed(c, m->token_embd, m->dec_pos, m->dx, m->ids, 0, pos * d));
-  for (int i = 0; i < m->dec_layers; i++) {
-    const DLayer &l = m->dl[i];
-    CK(launch_layer_norm(c, m->dx, l.norm_self.w, l.norm_self.b, m->dy, 1, d, nullptr, nullptr, 0));
-    CK(launch_gemv(c, m->dy, l.qkv, m->dqkv, WH_BIAS, 0.0f, 0));
-    CK(launch_pack(c, m->dqkv, d, 0, m->own[i], 1, d, m->context, pos));
-    CK(launch_attend(c, m->dqkv, m->own[i], m->dpart, m->datt, pos + 1, m->context, heads, hd));
-    CK(launch_gemv(c, m->datt, l.self_out, m->dx, WH_RESIDUAL, 1.0f, 0));
-    CK(launch_layer_norm(c, m->dx, l.norm_cross.w, l.norm_cross.b, m->dy, 1, d, nullptr, nullptr, 0));
-    CK(launch_gemv(c, m->dy, l.cross_q, m->dqkv, WH_BIAS, 0.0f, 0));
-    CK(launch_attend(c, m->dqkv, m->cross[i], m->dpart, m->datt, m->cross_frames, m->cross_frames, heads, hd));
-    CK(launch_gemv(c, m->datt, l.cross_out, m->dx, WH_RESIDUAL, 1.0f, 0));
-    CK(launch_layer_norm(c, m->dx, l.norm_ffn.w, l.norm_ffn.b, m->dy, 1, d, nullptr, nullptr, 0));
-    CK(launch_gemv(c, m->dy, l.fc1, m->dh, WH_GELU, 0.0f, 0));
-    CK(launch_gemv(c, m->dh, l.fc2, m->dx, WH_RESIDUAL, 1.0f, 0));
-  }
-  CK(launch_layer_norm(c, m->dx, m->dec_norm.w, m->dec_norm.b, m->dy, 1, d, nullptr, nullptr, 0));
-  return launch_gemv(c, m->dy, m->token_embd, logits, WH_BIAS, 0.0f, 0);
+  return run_recorded(m, {WHISPER_STEP, (intptr_t)logits, m->cross_frames}, [&] {
+    CK(launch_embed(c, m->token_embd, m->dec_pos, m->dx, m->ids, 0, 0, dpos, d));
+    for (int i = 0; i < m->dec_layers; i++) {
+      const DLayer &l = m->dl[i];
+      CK(launch_layer_norm(c, m->dx, l.norm_self.w, l.norm_self.b, m->dy, 1, d, nullptr, nullptr, 0));
+      CK(launch_gemv(c, m->dy, l.qkv, m->dqkv, WH_BIAS, 0.0f, 0));
+      CK(launch_pack(c, m->dqkv, d, 0, m->own[i], 1, d, m->context, 0, dpos));
+      CK(launch_attend(c, m->dqkv, m->own[i], m->dpart, m->datt, 1, m->context, heads, hd, dpos));
+      CK(launch_gemv(c, m->datt, l.self_out, m->dx, WH_RESIDUAL, 1.0f, 0));
+      CK(launch_layer_norm(c, m->dx, l.norm_cross.w, l.norm_cross.b, m->dy, 1, d, nullptr, nullptr, 0));
+      CK(launch_gemv(c, m->dy, l.cross_q, m->dqkv, WH_BIAS, 0.0f, 0));
+      CK(launch_attend(c, m->dqkv, m->cross[i], m->dpart, m->datt, m->cross_frames, m->cross_frames, heads, hd));
+      CK(launch_gemv(c, m->datt, l.cross_out, m->dx, WH_RESIDUAL, 1.0f, 0));
+      CK(launch_layer_norm(c, m->dx, l.norm_ffn.w, l.norm_ffn.b, m->dy, 1, d, nullptr, nullptr, 0));
+      CK(launch_gemv(c, m->dy, l.fc1, m->dh, WH_GELU, 0.0f, 0));
+      CK(launch_gemv(c, m->dh, l.fc2, m->dx, WH_RESIDUAL, 1.0f, 0));
+    }
+    CK(launch_layer_norm(c, m->dx, m->dec_norm.w, m->dec_norm.b, m->dy, 1, d, nullptr, nullptr, 0));
+    return launch_gemv(c, m->dy, m->token_embd, logits, WH_BIAS, 0.0f, 0);
+  });
 }
 
 }  // extern "C"

@@ -297,6 +297,45 @@ __device__ __forceinline__ half2 magic_pair(uint32_t x) {
   return __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, x, HI ? 0x04030402u : 0x04010400u));
 }
 
+// Two int8 of x (bytes 0-1, or 2-3 with HI) as two f16 (exact: |q| ≤ 128), by sub-dword operand
+// selection of the conversion itself (SDWA: sign-extended byte in, one half of the result out).
+template <bool HI>
+__device__ __forceinline__ half2 i8_pair(uint32_t x) {
+  uint32_t r;
+  if constexpr (HI)
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+        : "=&v"(r) : "v"(x));
+  else
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1"
+        : "=&v"(r) : "v"(x));
+  return __builtin_bit_cast(half2, r);
+}
+
+// Q8_0 MFMA fragment of substep S: elements 16·(S % 2) + 8g .. + 8 of block S / 2 of the lane's W
+// row pair, f16(q·d) — the exact conversion of q, then one packed f16 multiply by the block scale.
+// w = the lane's dwords (read_w): for block 0 (data from byte 2 of the pair) three dwords per
+// substep holding the elements from byte 2, for block 1 (data from byte 36) two aligned dwords.
+template <int S>
+__device__ __forceinline__ half8 dequant_q8(const uint32_t *w, half2 d2) {
+  half2 p[4];
+  if constexpr (S < 2) {
+    const uint32_t *x = w + 3 * S;
+    p[0] = i8_pair<true>(x[0]), p[1] = i8_pair<false>(x[1]), p[2] = i8_pair<true>(x[1]), p[3] = i8_pair<false>(x[2]);
+  } else {
+    const uint32_t *x = w + 6 + 2 * (S - 2);
+    p[0] = i8_pair<false>(x[0]), p[1] = i8_pair<true>(x[0]), p[2] = i8_pair<false>(x[1]), p[3] = i8_pair<true>(x[1]);
+  }
+  half8 f;
+#pragma unroll
+  for (int h = 0; h < 4; h++) {
+    const half2 v = p[h] * d2;
+    f[2 * h] = v[0], f[2 * h + 1] = v[1];
+  }
+  return f;
+}
+
 // The MFMA fragment of substep s (elements 8s .. 8s + 7) of one block.  dw = the block's data
 // dwords as read from LDS at the lane's offset, `sh` = bytes of that offset before the data (2 for
 // the even block of a pair: data from byte 2; 0 for the odd one: data dword-aligned), d2 = the
@@ -468,25 +507,32 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
     }
   };
 
-  // LDS read offsets of the lane: a chunk (4g + s) of row wm + lrow (+32i), rotated by row/2; the
-  // lane's W block (quantized: g = 0 reads dwords 0.. with the data from byte 2, g = 1 the dwords
-  // from byte BLK + 2 with the scale in the high half of the dword before); F16 chunks like a.
+  // The lane's k chunk (of 8 in a step) at substep s.  Q8_0: 2s + g — block s/2 of the pair at
+  // every lane of a substep, so the bytes of a substep sit at the same place in every lane's dwords;
+  // Q4_0 and F16: 4g + s — block g.  a and W fragments take the same chunk.
+  constexpr bool Q8 = WT == WH_Q8_0;
+  auto chunk = [&](int s) { return Q8 ? 2 * s + g : 4 * g + s; };
+  // LDS read offsets of the lane: a chunk of row wm + lrow (+32i), rotated by row/2; the lane's W
+  // dwords (Q8_0: from byte 8g of its row pair, the scales in dwords 0 and 8 of the row; Q4_0:
+  // g = 0 reads dwords 0.. with the data from byte 2, g = 1 the dwords from byte BLK + 2 with the
+  // scale in the high half of the dword before); F16 chunks like a.
   uint32_t a_off[4];
 #pragma unroll
-  for (int s = 0; s < 4; s++) a_off[s] = (wm + lrow) * 128 + 16 * ((4 * g + s + (lrow >> 1)) & 7);
-  constexpr int ND = WT == WH_Q8_0 ? 9 : WT == WH_Q4_0 ? 5 : 16;  // dwords per lane per W row and step
+  for (int s = 0; s < 4; s++) a_off[s] = (wm + lrow) * 128 + 16 * ((chunk(s) + (lrow >> 1)) & 7);
+  constexpr int ND = Q8 ? 10 : WT == WH_Q4_0 ? 5 : 16;  // dwords per lane per W row and step
+  constexpr int NSC = Q8 ? 2 : 1;                       // scale dwords per lane per W row and step
   constexpr int BLK = PAIR1 / 2;
   const uint32_t w_row = W_RG + (wn + lrow) * PAIR1;
-  const uint32_t w_dat = w_row + (g ? BLK + 2 : 0), w_sc = w_row + (g ? BLK - 2 : 0);
+  const uint32_t w_dat = Q8 ? w_row + 8 * g : w_row + (g ? BLK + 2 : 0), w_sc = w_row + (g ? BLK - 2 : 0);
   uint32_t wf_off[4];
 #pragma unroll
-  for (int s = 0; s < 4; s++) wf_off[s] = w_row + 16 * ((4 * g + s + (lrow >> 1)) & 7);
+  for (int s = 0; s < 4; s++) wf_off[s] = w_row + 16 * ((chunk(s) + (lrow >> 1)) & 7);
 
   auto read_a = [&](half8 (&f)[TM], int slot, int s) {
 #pragma unroll
     for (int i = 0; i < TM; i++) f[i] = *(const half8 *)(lds + a_off[s] + slot * A_ST + i * 4096);
   };
-  auto read_w = [&](uint32_t (&w)[TN][ND], uint32_t (&sc)[TN], int slot) {
+  auto read_w = [&](uint32_t (&w)[TN][ND], uint32_t (&sc)[TN][NSC], int slot) {
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       if constexpr (WCH) {
@@ -495,12 +541,21 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
           const uint4 x = *(const uint4 *)(lds + wf_off[s] + slot * W_ST + j * 32 * PAIR1);
           w[j][4 * s] = x.x, w[j][4 * s + 1] = x.y, w[j][4 * s + 2] = x.z, w[j][4 * s + 3] = x.w;
         }
-        sc[j] = 0;
+        sc[j][0] = 0;
+      } else if constexpr (Q8) {
+        // Pair bytes 2 + 8g .. (block 0, substeps 0-1: dwords 0-2 and 4-6 from byte 8g) and
+        // 36 + 8g .. (block 1, substeps 2-3: dwords 9-10 and 13-14); the scales at bytes 0 and 34.
+        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * PAIR1);
+        constexpr int at[10] = {0, 1, 2, 4, 5, 6, 9, 10, 13, 14};
+#pragma unroll
+        for (int i = 0; i < 10; i++) w[j][i] = q[at[i]];
+        const uint32_t *r = (const uint32_t *)(lds + w_row + slot * W_ST + j * 32 * PAIR1);
+        sc[j][0] = r[0], sc[j][1] = r[8];
       } else {
         const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * PAIR1);
 #pragma unroll
         for (int i = 0; i < ND; i++) w[j][i] = q[i];
-        sc[j] = *(const uint32_t *)(lds + w_sc + slot * W_ST + j * 32 * PAIR1);
+        sc[j][0] = *(const uint32_t *)(lds + w_sc + slot * W_ST + j * 32 * PAIR1);
       }
     }
   };
@@ -510,17 +565,22 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   for (int i = 0; i < TM; i++)
 #pragma unroll
     for (int j = 0; j < TN; j++) acc[i][j] = floatx16{};
-  uint32_t wq[2][TN][ND], sc[2][TN];
+  uint32_t wq[2][TN][ND], sc[2][TN][NSC];
   half8 af[2][TM];
   const uint32_t sh = g ? 0u : 2u;
   // Substep s of a step: dequantize the lane's W fragment (quantized) and run the TM × TN MFMAs.
-  auto mma = [&](const half8 (&f)[TM], const uint32_t (&w)[TN][ND], const uint32_t (&scl)[TN], int s) {
+  auto mma = [&](const half8 (&f)[TM], const uint32_t (&w)[TN][ND], const uint32_t (&scl)[TN][NSC], auto s_c) {
+    constexpr int s = decltype(s_c)::value;
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       half8 b;
       if constexpr (WCH) b = __builtin_bit_cast(half8, make_uint4(w[j][4 * s], w[j][4 * s + 1], w[j][4 * s + 2], w[j][4 * s + 3]));
-      else {
-        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(g ? scl[j] >> 16 : scl[j] & 0xffffu));
+      else if constexpr (Q8) {
+        const half2 sv = __builtin_bit_cast(half2, scl[j][s >> 1]);  // block 0: low half; block 1: high
+        const _Float16 d = s < 2 ? sv[0] : sv[1];
+        b = dequant_q8<s>(w[j], half2{d, d});
+      } else {
+        const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(g ? scl[j][0] >> 16 : scl[j][0] & 0xffffu));
         b = dequant_frag<WT>(w[j], sh, half2{d, d}, s);
       }
 #pragma unroll
@@ -542,11 +602,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   auto step = [&](auto S_c, int kt) {
     constexpr int S = decltype(S_c)::value, slot = S % NS, cur = S & 1;
     read_a(af[1], slot, 1);
-    mma(af[0], wq[cur], sc[cur], 0);
+    mma(af[0], wq[cur], sc[cur], std::integral_constant<int, 0>{});
     read_a(af[0], slot, 2);
-    mma(af[1], wq[cur], sc[cur], 1);
+    mma(af[1], wq[cur], sc[cur], std::integral_constant<int, 1>{});
     read_a(af[1], slot, 3);
-    mma(af[0], wq[cur], sc[cur], 2);
+    mma(af[0], wq[cur], sc[cur], std::integral_constant<int, 2>{});
     if (kt + 1 < nk) {
       // Stage kt + 1 has landed for every wave, and every wave is done with stage kt − 1.
       if (kt + NS - 2 < nk) wait_vm<(NS - 3) * PI>();
@@ -556,7 +616,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
       read_w(wq[cur ^ 1], sc[cur ^ 1], (slot + 1) % NS);
       read_a(af[0], (slot + 1) % NS, 0);
     }
-    mma(af[1], wq[cur], sc[cur], 3);
+    mma(af[1], wq[cur], sc[cur], std::integral_constant<int, 3>{});
   };
   constexpr int UNR = NS % 2 ? 2 * NS : NS;
   for (int kt0 = 0; kt0 < nk; kt0 += UNR) unrolled_steps<0, UNR>(step, kt0, nk);

@@ -11,9 +11,9 @@
 // Two kernels per call.  pack_kernel writes K ([key][dim]), Vᵀ ([dim][key]) and the position rows as
 // f16 into the context's scratch, zero-padded to whole 32-key blocks and to a head dim of 32·NC, so
 // that the flash kernel's loads are whole aligned blocks.  flash_kernel gives each wavefront 16
-// queries and each workgroup 4 wavefronts (64 queries) that share the key blocks: a ring of 5 LDS
-// stages, each one key block's K and Vᵀ and 32 new position rows, filled by the LDS DMA of gfx950
-// two blocks ahead of the MFMAs, with one barrier per block.
+// queries and each workgroup 4 wavefronts (64 queries) that share the key blocks: two LDS stages of
+// K and Vᵀ and a ring of 32-row position groups, filled by the LDS DMA of gfx950 one block ahead of
+// the MFMAs, with one barrier per block; under 80 KiB of LDS, so that two workgroups share a CU.
 //
 // Layout in the flash kernel: a wavefront computes the transposed scores Sᵀ = K·Qᵀ and output
 // Oᵀ = Vᵀ·Pᵀ, so a query's softmax state lives in one lane column (lane % 16) of every MFMA result.
@@ -36,7 +36,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int KB = 32;  // keys per block
 constexpr int QW = 4;   // wavefronts (16 queries each) per workgroup
-constexpr int NS = 5;   // LDS stages: blocks kb − 2 .. kb + 2
+constexpr int PD = 1;   // key blocks whose DMA runs ahead of the MFMAs
+constexpr int TS = 20;  // floats per row of the band skew buffer: its writes and reads hit distinct banks
 
 // Scratch layout of one call: the packed operands, each array 256-byte aligned.
 struct Pack {
@@ -174,13 +175,17 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
   constexpr int CH = DP / 8;           // 16-byte chunks per K / position row (a power of 2)
   static_assert((CH & (CH - 1)) == 0, "chunk rotation masks");
   constexpr int OT = DP / 16;          // 16-dim output tiles
-  constexpr int KBYTES = KB * DP * 2;  // one block's K (and Vᵀ, and 32 position rows)
-  constexpr int STAGE = KBYTES * (REL ? 3 : 2);
-  // DMA instructions (1 KiB each) per stage and per wavefront (each issues the same count).
-  constexpr int NI = STAGE / 1024, PER = (NI + QW - 1) / QW;
-  static_assert(PER < 64, "vmcnt range");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[NS * STAGE];
-  __shared__ float tt[REL ? QW * 48 * 17 : 1];
+  constexpr int KBYTES = KB * DP * 2;  // one block's K, its Vᵀ, and one group of 32 position rows
+  // A block's band spans NG position groups: its own and the NG − 1 before.  Rings: NKV K/V stages
+  // (blocks kb .. kb + PD) and NP position groups (kb − NG + 1 .. kb + PD).
+  constexpr int NG = REL ? QW / 2 + 1 : 0;
+  constexpr int NKV = PD + 1, NP = REL ? NG + PD : 0;
+  constexpr int P_RG = NKV * 2 * KBYTES;  // the position ring follows the K/V ring
+  // DMA instructions (1 KiB each) per block and per wavefront (each issues the same count).
+  constexpr int NI = (REL ? 3 : 2) * KBYTES / 1024, PER = (NI + QW - 1) / QW;
+  static_assert(PER * PD < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[P_RG + (REL ? NP * KBYTES : 0)];
+  __shared__ float tt[REL ? QW * 48 * TS : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -204,71 +209,71 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
   const size_t kvoff = ((size_t)b * A.heads + head) * A.tk * DP;
   const _Float16 *kp = A.kp + kvoff, *vt = A.vt + kvoff;
   const _Float16 *pp = REL ? A.pp + (size_t)head * A.prows * DP : nullptr;
-  // Stored position row where key block kb's band starts (a multiple of 32).
-  const int sb0 = A.t - q0 - 48 + A.pfront;
+  // Stored position row where key block kb's band starts (a multiple of 32): the wave's band
+  // starts 16·(QW − 1 − wave) rows into it, so stored row sb0 + 32kb + 16(QW−1−wave) + jj − ii + 15
+  // is P[j − i + t + 15] (+ pfront) for key j = 32kb + jj and query i = q0 + 16·wave + ii.
+  const int sb0 = A.t - q0 - 16 * (QW - 1) + A.pfront;
 
   // Per lane and DMA instruction: byte offset of its 16 bytes from the block's base and the
-  // instruction's LDS offset in a stage.  A stage is [K: 32 rows of CH chunks][Vᵀ: DP rows of 4
-  // chunks][positions: 32 rows of CH chunks], K and position rows rotated by rot<CH>, Vᵀ rows by
-  // row / 4 (64-byte rows).
+  // instruction's LDS offset in its stage or group.  A K/V stage is [K: 32 rows of CH chunks]
+  // [Vᵀ: DP rows of 4 chunks], a group [positions: 32 rows of CH chunks]; K and position rows
+  // rotated by rot<CH>, Vᵀ rows by row / 4 (64-byte rows).
   uint32_t soff[PER], sdst[PER];
   int skind[PER];
 #pragma unroll
   for (int i = 0; i < PER; i++) {
-    const int n = (wave + QW * i) % NI, at = 1024 * n + 16 * lane;  // LDS byte in the stage
-    sdst[i] = 1024 * n;
+    const int n = (wave + QW * i) % NI, at = 1024 * n + 16 * lane;  // byte in the block's K|Vᵀ|positions
     if (at < KBYTES) {  // K row r, stored chunk position pc
       const int r = at / (DP * 2), pc = (at / 16) % CH, c = (pc - rot<CH>(r)) & (CH - 1);
       skind[i] = 0;
       soff[i] = (uint32_t)((r * DP + 8 * c) * 2);
+      sdst[i] = 1024 * n;
     } else if (at < 2 * KBYTES) {  // Vᵀ row d (keys j0 .. j0 + 31)
       const int x = at - KBYTES, d = x / 64, pc = (x / 16) % 4, c = (pc - (d >> 2)) & 3;
       skind[i] = 1;
       soff[i] = (uint32_t)(((size_t)d * A.tk + 8 * c) * 2);
+      sdst[i] = 1024 * n;
     } else {  // position row r of the group
       const int x = at - 2 * KBYTES, r = x / (DP * 2), pc = (x / 16) % CH, c = (pc - rot<CH>(r)) & (CH - 1);
       skind[i] = 2;
       soff[i] = (uint32_t)((r * DP + 8 * c) * 2);
+      sdst[i] = 1024 * n - 2 * KBYTES;
     }
   }
   // Instructions are whole-kind: KBYTES is a multiple of 1 KiB, so a wave-uniform kind per i.
   const uint32_t lds0 = lds_addr(lds);
-  auto issue = [&](int kb) {
-    const uint32_t st = lds0 + (kb % NS) * STAGE;
+  // Block kb's K and Vᵀ into K/V slot kvs and its position group (rows sb0 + 32(kb + NG − 1) ..)
+  // into group slot ps; pos_only: the group alone (the groups before the first block's).
+  auto issue = [&](int kb, int kvs, int ps, bool pos_only) {
     const _Float16 *kb_k = kp + (size_t)kb * KB * DP, *kb_v = vt + (size_t)kb * KB;
-    const _Float16 *kb_p = REL ? pp + (size_t)(sb0 + 32 * kb + 64) * DP : nullptr;
+    const _Float16 *kb_p = REL ? pp + (size_t)(sb0 + 32 * (kb + NG - 1)) * DP : nullptr;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
       const int kind = __builtin_amdgcn_readfirstlane(skind[i]);
-      const _Float16 *base = kind == 0 ? kb_k : kind == 1 ? kb_v : kb_p;
-      dma16s(base, soff[i], st + sdst[i]);
-    }
-  };
-  // The two position groups before block kb0's own into the position parts of the stages of
-  // blocks kb0 − 2 and kb0 − 1, as if those blocks had brought them.
-  auto issue_pre = [&](int kbx) {  // kbx = kb0 − 2 or kb0 − 1 (≥ −2)
-    const uint32_t st = lds0 + ((kbx + NS) % NS) * STAGE;
-    const _Float16 *base = pp + (size_t)(sb0 + 32 * kbx + 64) * DP;
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int kind = __builtin_amdgcn_readfirstlane(skind[i]);
-      if (kind == 2) dma16s(base, soff[i], st + sdst[i]);
+      if (kind == 2) dma16s(kb_p, soff[i], lds0 + P_RG + ps * KBYTES + sdst[i]);
+      else if (!pos_only) dma16s(kind == 0 ? kb_k : kb_v, soff[i], lds0 + kvs * 2 * KBYTES + sdst[i]);
     }
   };
 
   // The wave's queries (and (q + v) rows) as B fragments: lane (li, g) holds dims 32c + 8g ..+8.
   half8 qf[NC], wf[REL ? NC : 1];
   {
-    const _Float16 *qb = A.q + A.bq * b + hoff + (size_t)min(qi, t - 1) * A.qs;
-    const _Float16 *wb = REL ? A.qv + A.bq * b + hoff + (size_t)min(qi, t - 1) * A.qs : nullptr;
+    const size_t row = (size_t)min(qi, t - 1) * A.qs;
+    const _Float16 *qb = A.q + A.bq * b + hoff + row;
+    const _Float16 *wb = REL ? A.qv + A.bq * b + hoff + row : nullptr;
 #pragma unroll
     for (int c = 0; c < NC; c++) {
+      const int d = 32 * c + 8 * g;
+      if (qi < t && d + 8 <= hd) {  // rows and heads start on 16 bytes (hd % 4 == 0, aligned buffers)
+        qf[c] = *(const half8 *)(qb + d);
+        if constexpr (REL) wf[c] = *(const half8 *)(wb + d);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const int d = 32 * c + 8 * g + e;
-        const bool ok = qi < t && d < hd;
-        qf[c][e] = ok ? qb[d] : (_Float16)0.0f;
-        if constexpr (REL) wf[c][e] = ok ? wb[d] : (_Float16)0.0f;
+        for (int e = 0; e < 8; e++) {
+          const bool ok = qi < t && d + e < hd;
+          qf[c][e] = ok ? qb[d + e] : (_Float16)0.0f;
+          if constexpr (REL) wf[c][e] = ok ? wb[d + e] : (_Float16)0.0f;
+        }
       }
     }
   }
@@ -276,25 +281,28 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
   floatx4 om[OT];
 #pragma unroll
   for (int i = 0; i < OT; i++) om[i] = floatx4{};
+  // Softmax state in the log2 domain: scores s·scale·log2(e), running maximum m, row sum l.
+  const float sc2 = A.scale * 1.44269504088896341f;
   float m = -INFINITY, l = 0.0f;
-  float *tw = tt + wave * 48 * 17;
+  float *tw = tt + wave * 48 * TS;
 
   if (nkb > kb0) {
-    if constexpr (REL) {
-      issue_pre(kb0 - 2);
-      issue_pre(kb0 - 1);
-    }
-    issue(kb0);
-    if (nkb > kb0 + 1) issue(kb0 + 1);
+    if constexpr (REL)
+      for (int x = 0; x < NG - 1; x++) issue(kb0 - NG + 1 + x, 0, x, true);
+#pragma unroll
+    for (int x = 0; x < PD; x++)
+      if (kb0 + x < nkb) issue(kb0 + x, x, NG - 1 + x, false);
   }
+  int kvs = 0, ps0 = 0;  // K/V slot of block kb; group slot of its band's first group
   for (int kb = kb0; kb < nkb; kb++) {
-    // Stage kb has landed (stage kb + 1 may still be in flight); every wave is done with kb − 1.
-    if (kb + 1 < nkb) wait_vm<PER>();
+    // Block kb has landed (blocks after it may still be in flight); every wave is done with kb − 1,
+    // whose K/V slot and first band group take block kb + PD.
+    if (kb + PD - 1 < nkb) wait_vm<(PD - 1) * PER>();
     else dma_wait();
     __syncthreads();
-    if (kb + 2 < nkb) issue(kb + 2);
+    if (kb + PD < nkb) issue(kb + PD, kvs == 0 ? NKV - 1 : kvs - 1, REL ? (ps0 == 0 ? NP - 1 : ps0 - 1) : 0, false);
     const int j0 = kb * KB;
-    const _Float16 *kt = (const _Float16 *)(lds + (kb % NS) * STAGE);
+    const _Float16 *kt = (const _Float16 *)(lds + kvs * 2 * KBYTES);
     const _Float16 *vtl = kt + KB * DP;
 
     // Scores Sᵀ for the two 16-key tiles: lane holds keys 16·jt + 4g + v of query li.
@@ -313,23 +321,23 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
     }
 
     if constexpr (REL) {
-      // Band Tᵀ[r][i] = P[band row r]·(q+v)_i, r in 0..47 (r = jj − ii + 15); the wave's band starts
-      // 16·(QW − 1 − wave) rows into the block's (rows sb0 + 32kb ..: the groups of stages kb − 2,
-      // kb − 1 and kb).
+      // Band Tᵀ[r][i] = P[band row r]·(q+v)_i, r in 0..47 (r = jj − ii + 15): rows base + r of the
+      // block's band, whose 32-row groups are ring slots ps0 .. ps0 + NG − 1.
       const int base = 16 * (QW - 1 - wave);
 #pragma unroll
       for (int rt = 0; rt < 3; rt++) {
         floatx4 acc = floatx4{};
-        const int br = base + 16 * rt + li, grp = br >> 5, gr = br & 31;
-        const _Float16 *prow =
-            (const _Float16 *)(lds + ((kb - 2 + grp + NS) % NS) * STAGE + 2 * KBYTES) + gr * DP;
+        const int br0 = base + 16 * rt, grp = br0 >> 5;  // a 16-row tile lies in one group
+        const int slot = ps0 + grp >= NP ? ps0 + grp - NP : ps0 + grp;
+        const int gr = (br0 & 31) + li;
+        const _Float16 *prow = (const _Float16 *)(lds + P_RG + slot * KBYTES) + gr * DP;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
           const half8 a = *(const half8 *)(prow + 8 * ((4 * c + g + rot<CH>(gr)) & (CH - 1)));
           acc = mfma(a, wf[c], acc);
         }
 #pragma unroll
-        for (int v = 0; v < 4; v++) tw[(16 * rt + 4 * g + v) * 17 + li] = acc[v];
+        for (int v = 0; v < 4; v++) tw[(16 * rt + 4 * g + v) * TS + li] = acc[v];
       }
       // tw is the wave's own: its LDS writes complete before its reads, in order.
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -338,24 +346,29 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
 #pragma unroll
       for (int jt = 0; jt < 2; jt++)
 #pragma unroll
-        for (int v = 0; v < 4; v++) s[jt][v] += tw[(16 * jt + 4 * g + v - li + 15) * 17 + li];
+        for (int v = 0; v < 4; v++) s[jt][v] += tw[(16 * jt + 4 * g + v - li + 15) * TS + li];
       __builtin_amdgcn_wave_barrier();
     }
 
-    // Online softmax over this block (per query li: 8 scores per lane, 4 lanes).
-    float bm = -INFINITY;
+    // Online softmax over this block (per query li: 8 scores per lane, 4 lanes); keys past kv_len
+    // only in a window's last block.
+    if (j0 + KB <= kv_len) {
 #pragma unroll
-    for (int jt = 0; jt < 2; jt++)
+      for (int jt = 0; jt < 2; jt++)
 #pragma unroll
-      for (int v = 0; v < 4; v++) {
-        const int j = j0 + 16 * jt + 4 * g + v;
-        s[jt][v] = j < kv_len ? s[jt][v] * A.scale : -INFINITY;
-        bm = fmaxf(bm, s[jt][v]);
-      }
+        for (int v = 0; v < 4; v++) s[jt][v] *= sc2;
+    } else {
+#pragma unroll
+      for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) s[jt][v] = j0 + 16 * jt + 4 * g + v < kv_len ? s[jt][v] * sc2 : -INFINITY;
+    }
+    float bm = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
     bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
     bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
     const float mn = fmaxf(m, bm);
-    const float alpha = __expf(m - mn);
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);
     m = mn;
     half8 pf;
     float ps = 0.0f;
@@ -363,7 +376,7 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
     for (int jt = 0; jt < 2; jt++)
 #pragma unroll
       for (int v = 0; v < 4; v++) {
-        const float p = __expf(s[jt][v] - mn);
+        const float p = __builtin_amdgcn_exp2f(s[jt][v] - mn);
         ps += p;
         pf[4 * jt + v] = (_Float16)p;
       }
@@ -381,13 +394,15 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
       const half8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
       om[ot] = mfma(a, pf, om[ot]);
     }
+    kvs = kvs + 1 == NKV ? 0 : kvs + 1;
+    if constexpr (REL) ps0 = ps0 + 1 == NP ? 0 : ps0 + 1;
   }
 
   // The row sums over the 4 lanes of each query, then Oᵀ tile ot holds dims 16·ot + 4g + v.
   l += __shfl_xor(l, 16, 64);
   l += __shfl_xor(l, 32, 64);
   if (qi >= t) return;
-  if (ns > 1) {  // partial output: unnormalized O, and (m, l) of this key run
+  if (ns > 1) {  // partial output: unnormalized O, and (m, l) of this key run (m in natural-log units)
     const int batch = gridDim.z / ns;
     const size_t prow = (((size_t)split * batch + b) * t + qi) * (size_t)A.heads * hd + hoff;
 #pragma unroll
@@ -398,7 +413,7 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
     }
     if (g == 0) {
       float *ml = A.pml + 2 * ((((size_t)split * batch + b) * A.heads + head) * t + qi);
-      ml[0] = m, ml[1] = l;
+      ml[0] = m * 0.69314718055994531f, ml[1] = l;
     }
     return;
   }
@@ -447,13 +462,23 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
   }
 }
 
-// Key splits per query tile: enough workgroups for the CUs while every split keeps ≥ 4 key blocks.
-int kv_splits(const wh_ctx *ctx, int t, int heads, int batch) {
-  const int cus = ctx->cus > 0 ? ctx->cus : 256;
-  const long items = (long)((t + 16 * QW - 1) / (16 * QW)) * heads * batch;
+// LDS bytes of one flash workgroup (as flash_kernel declares them).
+int flash_lds(int dp, bool rel) {
+  const int kbytes = KB * dp * 2, ng = rel ? QW / 2 + 1 : 0;
+  return (PD + 1) * 2 * kbytes + (rel ? (ng + PD) * kbytes + QW * 48 * TS * 4 : 4);
+}
+
+// Key splits per query tile: workgroups for every slot the CUs hold at once (LDS-bound: two per CU
+// for 128-dim relative attention) while every split keeps ≥ 3 key blocks.
+int kv_splits(const wh_ctx *ctx, int t, int heads, int hd, int batch, bool rel) {
   const int nkb = (t + KB - 1) / KB;
+  if (ctx->attn_split > 0) return std::min(ctx->attn_split, std::max(nkb, 1));
+  const int cus = ctx->cus > 0 ? ctx->cus : 256;
+  const int dp = hd <= 32 ? 32 : hd <= 64 ? 64 : 128;
+  const long slots = (long)cus * std::max(1, std::min(2, 160 * 1024 / flash_lds(dp, rel)));
+  const long items = (long)((t + 16 * QW - 1) / (16 * QW)) * heads * batch;
   int ns = 1;
-  while (ns < 4 && items * ns * 2 <= cus && nkb / (2 * ns) >= 4) ns *= 2;
+  while (ns < 4 && items * ns * 2 <= slots && nkb / (2 * ns) >= 3) ns *= 2;
   return ns;
 }
 
@@ -531,7 +556,7 @@ int attention_t(wh_ctx *ctx, const T *qk, const T *v, const T *pos, void *o, int
   // Queries: f16 rows read by the flash kernel directly (f32 input: converted first, after the
   // packed arrays in scratch).
   const size_t qbytes = std::is_same<T, float>::value ? ((size_t)batch * t * qs * 2 + 255) / 256 * 256 : 0;
-  a.nsplit = kv_splits(ctx, t, heads, batch);
+  a.nsplit = kv_splits(ctx, t, heads, hd, batch, pos != nullptr);
   uint8_t *ws = (uint8_t *)wh_scratch(ctx, sp.bytes() + qbytes + split_bytes(a.nsplit, t, heads, hd, batch));
   if (!ws) return WH_EOOM;
   if (a.nsplit > 1) {
@@ -569,7 +594,8 @@ int attention_t(wh_ctx *ctx, const T *qk, const T *v, const T *pos, void *o, int
 }  // namespace
 
 size_t attention_scratch_bytes(const wh_ctx *ctx, int t, int heads, int hd, int batch, int rel) {
-  return pack_shape(t, heads, hd, batch, rel != 0).bytes() + split_bytes(kv_splits(ctx, t, heads, batch), t, heads, hd, batch);
+  return pack_shape(t, heads, hd, batch, rel != 0).bytes() +
+         split_bytes(kv_splits(ctx, t, heads, hd, batch, rel != 0), t, heads, hd, batch);
 }
 
 int launch_attention(wh_ctx *ctx, const void *qk, const void *v, const void *pos, void *o, int t, int heads,

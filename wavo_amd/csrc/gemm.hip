@@ -819,6 +819,7 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     PLAN(64, 64, 1, 2, 6)
     PLAN(128, 128, 2, 4, 3)
     PLAN(64, 64, 2, 2, 3)
+    PLAN(128, 128, 2, 2, 3)
 #undef PLAN
     if (!ok) return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages", p.bm, p.bn, p.wm, p.wn, p.ns);
     if (int rc = wh_launched(ctx, "gemm")) return rc;

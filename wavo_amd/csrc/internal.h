@@ -24,6 +24,8 @@ struct wh_ctx {
   // GEMM launch-plan override from WAVO_GEMM_PLAN ("bm,bn,wm,wn,bk,split"; tuning sweeps only):
   // all zero = chosen per shape.
   int gemm_plan[6] = {0, 0, 0, 0, 0, 0};
+  // Attention key-split override from WAVO_ATTN_SPLIT (tuning sweeps only): 0 = chosen per shape.
+  int attn_split = 0;
   std::string name;
   std::string error;
   // Profiling (wh_profile): 0 off (default), 1 events around every launch, 2 named regions only.

@@ -3,6 +3,7 @@
 // (:461-577), buffer/readback/upload/write (:675-750), upload_linear (:770-834), run/complete
 // (:906-1002).  One HIP stream per context replaces wgpu's queue; errors that wgpu reports through
 // callbacks (:508-512, :995-1000) surface here as HIP status codes at the next wh_sync/wh_read.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdlib>
 #include <cstdio>
@@ -117,6 +118,7 @@ int wh_open(int device_index, wh_ctx **out) {
     if (sscanf(t, "%d,%d,%d,%d,%d,%d", &o[0], &o[1], &o[2], &o[3], &o[4], &o[5]) != 6 || o[5] < 1 || o[5] > 4)
       for (int i = 0; i < 6; i++) o[i] = 0;
   }
+  if (const char *t = getenv("WAVO_ATTN_SPLIT")) ctx->attn_split = std::max(0, std::min(atoi(t), 64));
   if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
     delete ctx;
     return wh_fail(nullptr, WH_EGPU, "hipStreamCreate: %s", hipGetErrorString(e));

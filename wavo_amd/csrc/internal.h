@@ -86,11 +86,15 @@ int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int
 // x += alpha·(l(a16) + bias) followed by y = LayerNorm(x; g, b) (y f16 with out16): a GEMM with the
 // residual epilogue whose output row feeds a LayerNorm.  When the GEMM splits k, the split finish
 // and the norm run as one kernel (launch_split_residual_ln); otherwise the GEMM's own epilogue adds
-// the residual and the norm follows.  Needs l->cols == cols of x and no dual outputs.
+// the residual and the norm follows.  Needs l->cols == cols of x and no dual outputs.  keep_x = 0:
+// x is not needed afterwards (the fused kernel need not store it).  g2: a second LayerNorm of y (f32)
+// into y2 (f16) — the next block's first norm.
 int launch_gemm_h_ln(wh_ctx *ctx, const void *a16, const wh_linear *l, float *x, int m, float alpha, const float *g,
-                     const float *b, void *y, int out16);
+                     const float *b, void *y, int out16, int keep_x = 1, const float *g2 = nullptr,
+                     const float *b2 = nullptr, void *y2 = nullptr);
 int launch_split_residual_ln(wh_ctx *ctx, const float *part, int splits, const float *bias, int wrows, float alpha,
-                             float *x, const float *g, const float *b, void *y, int rows, int cols, int out16);
+                             float *x, const float *g, const float *b, void *y, int rows, int cols, int out16,
+                             int keep_x = 1, const float *g2 = nullptr, const float *b2 = nullptr, void *y2 = nullptr);
 // f32 → f16 (RNE) of n values (n % 4 == 0).
 int launch_to_half(wh_ctx *ctx, const float *x, void *y, size_t n);
 int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,

@@ -725,7 +725,9 @@ int arena(wh_model *m, int frames, int batch) {
   m->valid_dev = nullptr;
   const int d = m->d;
   const size_t rows = (size_t)F * B;
-  size_t hsz = rows * std::max(m->d_ff, d), qsz = rows * 4 * d, ysz = (size_t)(2 * F + 15 + 64) * d, sub = 0;
+  // yr: the projected positions (2F + 15 rows), rotary rows or the next block's first norm (f16).
+  size_t hsz = rows * std::max(m->d_ff, d), qsz = rows * 4 * d,
+         ysz = std::max((size_t)(2 * F + 15 + 64) * d, (rows * d + 1) / 2), sub = 0;
   if (m->arch == PARAKEET) {
     // The subsampling unchunked: conv2/conv3 outputs (2F + 1) rows of [MELS / 4][ch] per window, and
     // conv5's [F][MELS / 8][ch].
@@ -784,7 +786,11 @@ int arena(wh_model *m, int frames, int batch) {
 // residual stream x stays f32; every activation whose only consumer is a GEMM (the norms' outputs,
 // the first FFN projections, attention and the conv module) is written as f16, the rounding that
 // GEMM applies to its input anyway (src/cpu/gemm.rs:163-176), into f16 views of the arena buffers.
-int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int batch, const int *valid_dev) {
+// One block from x into y (y = norm_out(x), x is spent).  pre: the block's first norm (norm_ff1 of x)
+// is already in m->yr as f16 (the previous block's last kernel wrote it); next: the following
+// block's norm_ff1, which this block's last kernel then writes into m->yr.
+int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int batch, const int *valid_dev, bool pre,
+                 const Chan *next) {
   wh_ctx *c = m->ctx;
   const int d = m->d, hd = d / m->heads, rows = t * batch;
   void *y16 = y, *h16 = m->h;
@@ -792,8 +798,8 @@ int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int bat
     return launch_gemm_h(c, a, l, out, r, l->cols + l->dual, epi, alpha, o16);
   };
   auto ln16 = [&](const Chan &n) { return launch_layer_norm(c, x, n.w, n.b, y16, rows, d, nullptr, nullptr, 0, 1); };
-  CK(ln16(k.norm_ff1));
-  CK(g16(y16, k.ff1[0], h16, rows, WH_SILU, 0.0f, 1));
+  if (!pre) CK(ln16(k.norm_ff1));
+  CK(g16(pre ? (const void *)m->yr : y16, k.ff1[0], h16, rows, WH_SILU, 0.0f, 1));
   if (!m->relative) {
     CK(g16(h16, k.ff1[1], x, rows, WH_RESIDUAL, 0.5f, 0));
     void *yr16 = m->yr;
@@ -817,8 +823,9 @@ int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int bat
   CK(g16(y16, k.pw2, x, rows, WH_RESIDUAL, 1.0f, 0));
   CK(ln16(k.norm_ff2));
   CK(g16(y16, k.ff2[0], h16, rows, WH_SILU, 0.0f, 1));
-  // The block output is norm_out(x), not the residual stream.
-  return launch_gemm_h_ln(c, h16, k.ff2[1], x, rows, 0.5f, k.norm_out.w, k.norm_out.b, y, 0);
+  // The block output is norm_out(x), not the residual stream (x is not stored again).
+  return launch_gemm_h_ln(c, h16, k.ff2[1], x, rows, 0.5f, k.norm_out.w, k.norm_out.b, y, 0, 0,
+                          next ? next->w : nullptr, next ? next->b : nullptr, next ? m->yr : nullptr);
 }
 
 }  // namespace
@@ -828,7 +835,8 @@ namespace {
 // Conformer::record (src/conformer.rs:107-116): `layers` blocks from m->x, output in m->x.
 int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layers) {
   for (int i = 0; i < layers; i++) {
-    CK(record_block(m, m->blocks[i], m->x, m->y, t, batch, valid_dev));
+    const Chan *next = i + 1 < layers ? &m->blocks[i + 1].norm_ff1 : nullptr;
+    CK(record_block(m, m->blocks[i], m->x, m->y, t, batch, valid_dev, i > 0, next));
     std::swap(m->x, m->y);
   }
   return WH_OK;

@@ -372,7 +372,10 @@ __global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__r
                                                                 const float *__restrict__ bias, int wrows, float alpha,
                                                                 float *__restrict__ x, const float *__restrict__ g,
                                                                 const float *__restrict__ b, OT *__restrict__ y,
-                                                                int rows, int cols) {
+                                                                int rows, int cols, int keep_x,
+                                                                const float *__restrict__ g2,
+                                                                const float *__restrict__ b2,
+                                                                _Float16 *__restrict__ y2) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + w;
   if (row >= rows) return;
@@ -407,7 +410,7 @@ __global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__r
       const float4 bb = b4[i], c = xr[i];
       v[j] = make_float4(c.x + alpha * (acc.x + bb.x), c.y + alpha * (acc.y + bb.y), c.z + alpha * (acc.z + bb.z),
                          c.w + alpha * (acc.w + bb.w));
-      xr[i] = v[j];
+      if (keep_x) xr[i] = v[j];
       s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
     }
   }
@@ -434,6 +437,38 @@ __global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__r
       o.z = (v[j].z - mean) * rstd * gg.z + bb.z;
       o.w = (v[j].w - mean) * rstd * gg.w + bb.w;
       store4(yy + 4 * i, o);
+      v[j] = o;
+    }
+  }
+  if (!g2) return;
+  // A second LayerNorm of y (the next block's first norm) into y2, from the registers.
+  s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < ROW_REGS / 4; j++)
+    if (lane + 64 * j < q4) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  const float mean2 = wave_sum(s) / (float)cols;
+  q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < ROW_REGS / 4; j++) {
+    if (lane + 64 * j < q4) {
+      float dx = v[j].x - mean2, dy = v[j].y - mean2, dz = v[j].z - mean2, dw = v[j].w - mean2;
+      q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+    }
+  }
+  const float rstd2 = rsqrtf(wave_sum(q) / (float)cols + 1e-5f);
+  _Float16 *y2r = y2 + (size_t)row * cols;
+  const float4 *g24 = (const float4 *)g2, *b24 = (const float4 *)b2;
+#pragma unroll
+  for (int j = 0; j < ROW_REGS / 4; j++) {
+    const int i = lane + 64 * j;
+    if (i < q4) {
+      const float4 gg = g24[i], bb = b24[i];
+      float4 o;
+      o.x = (v[j].x - mean2) * rstd2 * gg.x + bb.x;
+      o.y = (v[j].y - mean2) * rstd2 * gg.y + bb.y;
+      o.z = (v[j].z - mean2) * rstd2 * gg.z + bb.z;
+      o.w = (v[j].w - mean2) * rstd2 * gg.w + bb.w;
+      store4(y2r + 4 * i, o);
     }
   }
 }
@@ -475,15 +510,18 @@ int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *
 }
 
 int launch_split_residual_ln(wh_ctx *ctx, const float *part, int splits, const float *bias, int wrows, float alpha,
-                             float *x, const float *g, const float *b, void *y, int rows, int cols, int out16) {
+                             float *x, const float *g, const float *b, void *y, int rows, int cols, int out16,
+                             int keep_x, const float *g2, const float *b2, void *y2) {
   if (rows <= 0 || cols <= 0 || cols % 4 || cols > ROW_REGS * 64 || splits < 1 || !part || !bias || !x || !g || !b || !y ||
       (uintptr_t)part % 16 || (uintptr_t)bias % 16 || (uintptr_t)x % 16 || (uintptr_t)g % 16 || (uintptr_t)b % 16 ||
-      (uintptr_t)y % 16)
+      (uintptr_t)y % 16 || (g2 && (!b2 || !y2 || (uintptr_t)g2 % 16 || (uintptr_t)b2 % 16 || (uintptr_t)y2 % 16)))
     return wh_fail(ctx, WH_EARG, "split_residual_ln: bad arguments (%d x %d, %d splits)", rows, cols, splits);
-  ProfScope prof(ctx, "split_residual_ln", 0.0, (double)rows * cols * (4.0 * splits + 8 + (out16 ? 2 : 4)));
+  ProfScope prof(ctx, "split_residual_ln", 0.0,
+                 (double)rows * cols * (4.0 * splits + (keep_x ? 8 : 4) + (out16 ? 2 : 4) + (g2 ? 2 : 0)));
   const int grid = (rows + 3) / 4;
-#define SRL(OT, N) \
-  split_residual_ln_kernel<OT, N><<<grid, 256, 0, ctx->stream>>>(part, splits, bias, wrows, alpha, x, g, b, (OT *)y, rows, cols)
+#define SRL(OT, N)                                                                                                  \
+  split_residual_ln_kernel<OT, N><<<grid, 256, 0, ctx->stream>>>(part, splits, bias, wrows, alpha, x, g, b, (OT *)y, \
+                                                                  rows, cols, keep_x, g2, b2, (_Float16 *)y2)
   if (out16) {
     if (splits == 2) SRL(_Float16, 2);
     else if (splits == 4) SRL(_Float16, 4);

@@ -119,12 +119,10 @@ __device__ __forceinline__ int rot(int row) {
 // K rows [batch][head][tk][DP] and Vᵀ [batch][head][DP][tk] as f16, zeros past t and hd.  One
 // workgroup per 32 keys of one head.  T = float or _Float16 input.
 template <int DP, typename T>
-__global__ __launch_bounds__(256) void pack_kv_kernel(const T *__restrict__ k, int ks, long kbs,
-                                                      const T *__restrict__ v, int vs, long vbs, int t, int heads,
-                                                      int hd, int tk, _Float16 *__restrict__ kp,
-                                                      _Float16 *__restrict__ vt) {
+__device__ __forceinline__ void pack_kv(const T *__restrict__ k, int ks, long kbs, const T *__restrict__ v, int vs,
+                                        long vbs, int t, int heads, int hd, int tk, _Float16 *__restrict__ kp,
+                                        _Float16 *__restrict__ vt, int j0, int head, int b) {
   __shared__ _Float16 tr[KB][DP + 2];
-  const int j0 = blockIdx.x * KB, head = blockIdx.y, b = blockIdx.z;
   const size_t off = ((size_t)b * heads + head) * tk * DP;
   for (int e = threadIdx.x; e < KB * DP / 4; e += 256) {
     const int key = e / (DP / 4), d = 4 * (e % (DP / 4)), j = j0 + key;
@@ -151,12 +149,11 @@ __global__ __launch_bounds__(256) void pack_kv_kernel(const T *__restrict__ k, i
 // Position rows [head][prows][DP] as f16: stored row sr holds position row sr − pfront of the
 // projected table (zeros outside 0 .. prow).  One workgroup per 32 stored rows of one head.
 template <int DP, typename T>
-__global__ __launch_bounds__(256) void pack_pos_kernel(const T *__restrict__ pos, int ps, int prow, int hd, int pfront,
-                                                       int prows, _Float16 *__restrict__ pp) {
-  const int head = blockIdx.y;
+__device__ __forceinline__ void pack_pos(const T *__restrict__ pos, int ps, int prow, int hd, int pfront, int prows,
+                                         _Float16 *__restrict__ pp, int x, int head) {
   const size_t off = (size_t)head * prows * DP;
   for (int e = threadIdx.x; e < 32 * DP / 4; e += 256) {
-    const int sr = blockIdx.x * 32 + e / (DP / 4), d = 4 * (e % (DP / 4)), r = sr - pfront;
+    const int sr = x * 32 + e / (DP / 4), d = 4 * (e % (DP / 4)), r = sr - pfront;
     half4 x = {};
     if (r >= 0 && r < prow && d < hd) {
       const T *pr = pos + (long)r * ps + head * hd + d;
@@ -165,6 +162,19 @@ __global__ __launch_bounds__(256) void pack_pos_kernel(const T *__restrict__ pos
     }
     *(half4 *)(pp + off + (size_t)sr * DP + d) = x;
   }
+}
+
+// Both packs in one launch: workgroups x < tk / KB pack K/Vᵀ (window z), the next prows / 32 (window
+// 0 only) the position rows.
+template <int DP, typename T>
+__global__ __launch_bounds__(256) void pack_kernel(const T *__restrict__ k, int ks, long kbs, const T *__restrict__ v,
+                                                   int vs, long vbs, int t, int heads, int hd, int tk,
+                                                   _Float16 *__restrict__ kp, _Float16 *__restrict__ vt,
+                                                   const T *__restrict__ pos, int ps, int prow, int pfront, int prows,
+                                                   _Float16 *__restrict__ pp) {
+  const int nkv = tk / KB;
+  if ((int)blockIdx.x < nkv) pack_kv<DP, T>(k, ks, kbs, v, vs, vbs, t, heads, hd, tk, kp, vt, blockIdx.x * KB, blockIdx.y, blockIdx.z);
+  else if (blockIdx.z == 0) pack_pos<DP, T>(pos, ps, prow, hd, pfront, prows, pp, blockIdx.x - nkv, blockIdx.y);
 }
 
 // ---------------------------------------------------------------------------------- flash kernel
@@ -490,11 +500,9 @@ size_t split_bytes(int ns, int t, int heads, int hd, int batch) {
 template <int DP, typename T>
 void launch_pack(wh_ctx *ctx, const Pack &sp, const T *k, int ks, long kbs, const T *v, int vs, long vbs, const T *pos,
                  int t, int heads, int hd, int batch, _Float16 *kp, _Float16 *vt, _Float16 *pp) {
-  pack_kv_kernel<DP, T><<<dim3(sp.tk / KB, heads, batch), 256, 0, ctx->stream>>>(k, ks, kbs, v, vs, vbs, t, heads, hd,
-                                                                                   sp.tk, kp, vt);
-  if (pos)
-    pack_pos_kernel<DP, T><<<dim3(sp.prows / 32, heads), 256, 0, ctx->stream>>>(pos, heads * hd, 2 * t + 15, hd,
-                                                                                 sp.pfront, sp.prows, pp);
+  const int gx = sp.tk / KB + (pos ? sp.prows / 32 : 0);
+  pack_kernel<DP, T><<<dim3(gx, heads, batch), 256, 0, ctx->stream>>>(k, ks, kbs, v, vs, vbs, t, heads, hd, sp.tk, kp, vt,
+                                                                       pos, heads * hd, 2 * t + 15, sp.pfront, sp.prows, pp);
 }
 
 template <bool REL>

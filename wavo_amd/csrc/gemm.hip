@@ -760,6 +760,11 @@ Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
   // workgroups (one 750-frame window) runs faster with four.
   if (t128 >= 4L * cus) p = {128, 128, 2, 4, 3, 1};
   else if (t128 >= cus / 2) p = {128, 128, 2, 4, 4, 1};
+  else if (t128 * 4 <= cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
+    // Long k over few tiles (the FFN's down projection, 750 × 1024 × 4096): 128×128 tiles split 4
+    // ways, one workgroup per CU, move half the bytes per MFMA of 64×64 ones (measured in the
+    // encoder step: 1.02 against 1.06 ms for its 48 launches).
+    p = {128, 128, 2, 4, 4, 4};
   else if (t64 < cus)
     // Split only while every split keeps at least 16 k steps: shorter ones spend more on the
     // pipeline's fill and the partial sums than the extra workgroups win (k = 1024 runs faster whole).
@@ -770,6 +775,11 @@ Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
     p = {o[0], o[1], o[2], o[3], o[4], o[5]};
     if (k % (64 * p.split)) p.split = 1;
   }
+  for (const auto &o : ctx->gemm_shape_plans)  // tuning override for one shape (WAVO_GEMM_SHAPE_PLANS)
+    if (o[0] == m && o[1] == cols && o[2] == k) {
+      p = {o[3], o[4], o[5], o[6], o[7], o[8]};
+      if (k % (64 * p.split)) p.split = 1;
+    }
   return p;
 }
 

@@ -6,6 +6,7 @@
 
 #include <cstdint>
 #include <string>
+#include <array>
 #include <vector>
 
 #include "../../include/wavo_hip.h"
@@ -24,6 +25,9 @@ struct wh_ctx {
   // GEMM launch-plan override from WAVO_GEMM_PLAN ("bm,bn,wm,wn,bk,split"; tuning sweeps only):
   // all zero = chosen per shape.
   int gemm_plan[6] = {0, 0, 0, 0, 0, 0};
+  // Per-shape overrides from WAVO_GEMM_SHAPE_PLANS ("m,cols,k:bm,bn,wm,wn,stages,split;…"; tuning
+  // sweeps inside a model's step only).
+  std::vector<std::array<int, 9>> gemm_shape_plans;
   // Attention key-split override from WAVO_ATTN_SPLIT (tuning sweeps only): 0 = chosen per shape.
   int attn_split = 0;
   std::string name;

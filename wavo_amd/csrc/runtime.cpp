@@ -119,6 +119,17 @@ int wh_open(int device_index, wh_ctx **out) {
       for (int i = 0; i < 6; i++) o[i] = 0;
   }
   if (const char *t = getenv("WAVO_ATTN_SPLIT")) ctx->attn_split = std::max(0, std::min(atoi(t), 64));
+  if (const char *t = getenv("WAVO_GEMM_SHAPE_PLANS")) {
+    for (const char *q = t; *q;) {
+      std::array<int, 9> o{};
+      if (sscanf(q, "%d,%d,%d:%d,%d,%d,%d,%d,%d", &o[0], &o[1], &o[2], &o[3], &o[4], &o[5], &o[6], &o[7], &o[8]) == 9 &&
+          o[8] >= 1 && o[8] <= 4)
+        ctx->gemm_shape_plans.push_back(o);
+      const char *n = strchr(q, ';');
+      if (!n) break;
+      q = n + 1;
+    }
+  }
   if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
     delete ctx;
     return wh_fail(nullptr, WH_EGPU, "hipStreamCreate: %s", hipGetErrorString(e));

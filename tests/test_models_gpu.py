@@ -126,6 +126,32 @@ def test_whisper_small(gpu):
         token = nxt
 
 
+def test_whisper_long_decode(gpu):
+    """300 recorded decoder steps (the step replays one graph, its position read on the device) past
+    the first 256-key part of the self-attention cache, each step's logits against the oracle's."""
+    path = synth.model_path("whisper_ctx", small=True, directory=MODELS)
+    cfg = synth.SMALL["whisper_ctx"]
+    om, m = ox.Model(path), wa.Model(gpu, path)
+    enc = np.random.default_rng(21).normal(0, 1, (cfg["frames"], cfg["d"])).astype(np.float32)
+    vocab = cfg["vocab"]
+    vp = vocab if vocab % 32 == 0 else (vocab + 63) // 64 * 64
+    eb, lb = gpu.upload(enc), gpu.buffer(vp)
+    om.whisper_begin(enc)
+    m.whisper_begin(eb, enc.shape[0])
+    tokens = np.random.default_rng(22).integers(0, vocab, 300)
+    worst = 0.0
+    for pos, token in enumerate(tokens):
+        wl = om.whisper_step(int(token), pos, vocab)
+        m.whisper_step(int(token), pos, lb)
+        gl = gpu.read(lb, (vp,))[:vocab]
+        worst = max(worst, rel_l2(gl, wl))
+        assert rel_l2(gl, wl) < ENCODER_TOL, (pos, rel_l2(gl, wl))
+        if int(np.argmax(gl)) != int(np.argmax(wl)):  # only a near tie, within the measured noise
+            noise = 4.0 * float(np.abs(gl - wl).max())
+            assert top2_gap(wl) < noise, f"step {pos}: argmax {np.argmax(gl)} vs {np.argmax(wl)}"
+    print(f"worst step rel L2 {worst:.2e}")
+
+
 def test_gigaam_full_config(gpu):
     """the GigaAM-v3 shape (16 layers, d 768, 16 heads of 48), 11 s, q8_0."""
     path = synth.model_path("gigaam", directory=MODELS)

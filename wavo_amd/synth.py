@@ -41,6 +41,9 @@ SMALL = {
                      joint=320, hidden=128, vocab=1025, durations=[0, 1, 2, 3, 4], lstm_layers=2),
     "whisper": dict(arch="whisper", layers=2, d=256, heads=4, d_ff=1024, dec_layers=2, dec_heads=4,
                     vocab=1000, mels=80, frames=100, context=64),
+    # A decoder context past one 256-key attend part (long decodes).
+    "whisper_ctx": dict(arch="whisper", layers=2, d=256, heads=4, d_ff=1024, dec_layers=2, dec_heads=4,
+                        vocab=1000, mels=80, frames=100, context=320),
 }
 
 

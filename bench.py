@@ -163,6 +163,43 @@ def gemv_cold(gpu):
     return out
 
 
+def decode_steps(gpu, tokens=224):
+    """Whisper-large-v3-turbo-shaped decoder steps (4 layers, d 1280, 20 heads, 51866-token head, cross
+    attention over 1500 encoder frames, q8_0), `tokens` steps back to back after one warm-up pass."""
+    import numpy as np
+
+    import wavo_amd as wa
+    from wavo_amd import synth
+
+    t0 = time.time()
+    path = synth.model_path("whisper")
+    m = wa.Model(gpu, path)
+    log(f"whisper model ready in {time.time() - t0:.1f} s")
+    cfg = synth.CONFIGS["whisper"]
+    frames, d, vocab = cfg["frames"], cfg["d"], cfg["vocab"]
+    enc = np.random.default_rng(3).normal(0, 1, (frames, d)).astype(np.float32)
+    eb = gpu.upload(enc)
+    lb = gpu.buffer(vocab if vocab % 32 == 0 else (vocab + 63) // 64 * 64)
+    m.whisper_begin(eb, frames)
+    ids = np.random.default_rng(4).integers(0, vocab, tokens)
+    for pos in range(8):  # the first two calls record the step; later ones replay it
+        m.whisper_step(int(ids[pos]), pos, lb)
+    gpu.sync()
+    m.whisper_begin(eb, frames)
+    state = {"pos": 0}
+
+    def one():
+        m.whisper_step(int(ids[state["pos"]]), state["pos"], lb)
+        state["pos"] += 1
+
+    ms = time_region(gpu, one, tokens)
+    m.free()
+    return {"workload": f"whisper-large-v3-turbo-shaped decoder step (4 layers, d {d}, {cfg['dec_heads']} heads, "
+                        f"{vocab}-token head, cross attention over {frames} frames, q8_0), {tokens} steps back to back "
+                        "(weights stay in the MALL between tokens), one recorded pass per step",
+            "us_per_token": round(ms * 1e3, 2), "tokens_per_s": round(1e3 / ms, 1)}
+
+
 def traffic_for(name):
     """HBM bytes per launch for this GEMM configuration from a committed rocprofv3 summary, if any."""
     path = os.path.join(ROOT, "profiles", "gemm_traffic.txt")
@@ -184,7 +221,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seconds", type=float, default=60.0, help="audio per step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-gemv", action="store_true", help="skip the decoder GEMV measurement")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the decoder GEMV and decoder step measurements")
     ap.add_argument("--replay", metavar="NAME", default=None,
                     help="only the back-to-back launches of this GEMM configuration (a roofline.kernel value), "
                          "for rocprofv3 passes over exactly those launches")
@@ -274,6 +311,8 @@ def main():
     gemv = None if args.no_gemv else gemv_cold(gpu)
     if gemv:
         log(f"GEMV per token {gemv['us_per_token']} us, {gemv['achieved']} GB/s ({gemv['frac'] * 100:.1f}% of HBM)")
+        gemv["decode_step"] = decode_steps(gpu)
+        log(f"decoder step {gemv['decode_step']['us_per_token']} us per token")
 
     cpu = None
     if not args.no_cpu:

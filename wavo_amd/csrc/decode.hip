@@ -182,7 +182,8 @@ struct GemvArgs {
   const uint8_t *w;
   const float *bias;
   float *c;
-  int rows, k, epi, offset;
+  int rows, cols, k, epi, offset;
+  const float *ln_g, *ln_b;  // non-null: the product takes LayerNorm(a; ln_g, ln_b)
   float alpha;
   int row_bytes;
   int rps;        // rows per stage
@@ -201,6 +202,12 @@ constexpr int GV_STAGE = 16384;  // bytes per stage (whole DMA instructions of 1
 // block pair, or 64 F16 weights) of one row of the stage from LDS, `a` from LDS, and sums the
 // products in f32 (per block Σ q·a, then × d, as gemm.wgsl:244-262); a row's items are summed in
 // order through LDS.  W is not rounded (Pass::gemv semantics).
+__device__ __forceinline__ float gv_wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
 template <int WT, bool D16>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
   constexpr int ITEM = WT == WH_Q8_0 ? 68 : WT == WH_Q4_0 ? 36 : 128;  // bytes of 64 weights
@@ -236,7 +243,34 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
 #pragma unroll
   for (int i = 0; i < GV_NS - 1; i++)
     if (s0 + i < s1) issue(s0 + i);
-  for (int i = tid; i < P.k; i += 256) as[(i >> 6) * AS + (i & 63)] = P.a[i];
+  if (P.ln_g) {
+    // The norm before this product, with layer_norm_kernel's arithmetic (one wave sums in the same
+    // order), so the normalized row equals the standalone kernel's bit for bit.
+    __shared__ float stat[2];
+    if (wave == 0) {
+      const float4 *a4 = (const float4 *)P.a;
+      const int q4 = P.k / 4;
+      float sm = 0.0f;
+      for (int i = lane; i < q4; i += 64) {
+        const float4 v = a4[i];
+        sm += (v.x + v.y) + (v.z + v.w);
+      }
+      const float mean = gv_wave_sum(sm) / (float)P.k;
+      float q = 0.0f;
+      for (int i = lane; i < q4; i += 64) {
+        const float4 v = a4[i];
+        const float dx = v.x - mean, dy = v.y - mean, dz = v.z - mean, dw = v.w - mean;
+        q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+      }
+      const float rstd = rsqrtf(gv_wave_sum(q) / (float)P.k + 1e-5f);
+      if (lane == 0) stat[0] = mean, stat[1] = rstd;
+    }
+    __syncthreads();
+    const float mean = stat[0], rstd = stat[1];
+    for (int i = tid; i < P.k; i += 256) as[(i >> 6) * AS + (i & 63)] = (P.a[i] - mean) * rstd * P.ln_g[i] + P.ln_b[i];
+  } else {
+    for (int i = tid; i < P.k; i += 256) as[(i >> 6) * AS + (i & 63)] = P.a[i];
+  }
   const int row_l = tid / items, it = tid % items;
   for (int s = s0; s < s1; s++) {
     if (s + GV_NS - 2 < s1) gv_wait_vm<(GV_NS - 2) * PER>();
@@ -320,21 +354,19 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
     float *cp = P.c + P.offset + row;
     *cp = epilogue(P.epi, P.alpha, rsum[row - r0] + P.bias[row], res ? *cp : 0.0f);
   }
-}
-
-// Rows rows..cols (the padding columns) of a streamed GEMV: epi(0 + bias).
-__global__ void gemv_pad_kernel(const float *__restrict__ bias, float *__restrict__ c, int rows, int cols, int epi,
-                                float alpha, int offset) {
-  const int row = rows + blockIdx.x * blockDim.x + threadIdx.x;
-  if (row >= cols) return;
-  float *cp = c + offset + row;
-  *cp = epilogue(epi, alpha, bias[row], *cp);
+  // Rows rows..cols (the padding rows of the linear): epi(0 + bias), by the first workgroup.
+  if (blockIdx.x == 0)
+    for (int row = P.rows + tid; row < P.cols; row += 256) {
+      float *cp = P.c + P.offset + row;
+      *cp = epilogue(P.epi, P.alpha, P.bias[row], res ? *cp : 0.0f);
+    }
 }
 
 template <int WT>
-int gemv_stream(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha, int offset) {
+int gemv_stream(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha, int offset,
+                const float *ln_g, const float *ln_b) {
   const int items = l->k / 64;
-  GemvArgs P{a, l->w, l->bias, c, l->rows, l->k, epi, offset, alpha, (int)l->row_bytes, 0, 0, 0, 0};
+  GemvArgs P{a, l->w, l->bias, c, l->rows, l->cols, l->k, epi, offset, ln_g, ln_b, alpha, (int)l->row_bytes, 0, 0, 0, 0};
   P.rps = std::min(256 / items, GV_STAGE / (int)l->row_bytes);
   P.stages = (l->rows + P.rps - 1) / P.rps;
   // Two workgroups per CU (48 KiB of stages each), each streaming a run of stages: measured on
@@ -354,9 +386,6 @@ int gemv_stream(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int e
     gemv_stream_kernel<WT, true><<<grid, 256, lds, ctx->stream>>>(P);
   else
     gemv_stream_kernel<WT, false><<<grid, 256, lds, ctx->stream>>>(P);
-  if (l->cols > l->rows)
-    gemv_pad_kernel<<<(l->cols - l->rows + 255) / 256, 256, 0, ctx->stream>>>(l->bias, c, l->rows, l->cols, epi, alpha,
-                                                                             offset);
   return wh_launched(ctx, "gemv");
 }
 
@@ -516,19 +545,26 @@ __global__ void pack_kernel(const float *__restrict__ x, uint32_t *__restrict__ 
 
 }  // namespace
 
-int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha, int offset) {
+int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha, int offset,
+                const float *ln_g, const float *ln_b, float *ln_y) {
   if (!a || !c || offset < 0 || epi < WH_BIAS || epi > WH_TANH) return wh_fail(ctx, WH_EARG, "gemv: bad arguments");
   if ((size_t)l->k * 4 > 64 * 1024) return wh_fail(ctx, WH_EARG, "gemv: k %d too large", l->k);
+  if (ln_g && (!ln_b || !ln_y || l->k % 4 || (uintptr_t)a % 16))
+    return wh_fail(ctx, WH_EARG, "gemv: the fused norm needs g, b, a row buffer, k %% 4 == 0 and an aligned a");
   bool pair = l->k % 64 == 0;
   // The streaming kernel: whole 64-weight items, at most 256 of them per row, rows 4-byte aligned.
   if (pair && l->k / 64 <= 256 && l->row_bytes % 4 == 0 && (int)l->row_bytes <= GV_STAGE && l->rows > 0) {
     int rc = 1;
     switch (l->type) {
-      case WH_Q8_0: rc = gemv_stream<WH_Q8_0>(ctx, a, l, c, epi, alpha, offset); break;
-      case WH_Q4_0: rc = gemv_stream<WH_Q4_0>(ctx, a, l, c, epi, alpha, offset); break;
-      case WH_F16: rc = gemv_stream<WH_F16>(ctx, a, l, c, epi, alpha, offset); break;
+      case WH_Q8_0: rc = gemv_stream<WH_Q8_0>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b); break;
+      case WH_Q4_0: rc = gemv_stream<WH_Q4_0>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b); break;
+      case WH_F16: rc = gemv_stream<WH_F16>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b); break;
     }
     if (rc != 1) return rc;
+  }
+  if (ln_g) {  // the general kernel takes the norm from its own launch
+    if (int rc = launch_layer_norm(ctx, a, ln_g, ln_b, ln_y, 1, l->k, nullptr, nullptr, 0)) return rc;
+    a = ln_y;
   }
   switch (l->type) {
     case WH_F32: return gemv_t<WH_F32, false>(ctx, a, l, c, epi, alpha, offset);

@@ -1285,23 +1285,20 @@ int wh_whisper_step(wh_model *m, int token, int pos, float *logits) {
   // Decoder::record_step (src/transformer.rs:254-290).
   return run_recorded(m, {WHISPER_STEP, (intptr_t)logits, m->cross_frames}, [&] {
     CK(launch_embed(c, m->token_embd, m->dec_pos, m->dx, m->ids, 0, 0, dpos, d));
+    // Each LayerNorm runs inside the GEMV that consumes it (its only reader).
     for (int i = 0; i < m->dec_layers; i++) {
       const DLayer &l = m->dl[i];
-      CK(launch_layer_norm(c, m->dx, l.norm_self.w, l.norm_self.b, m->dy, 1, d, nullptr, nullptr, 0));
-      CK(launch_gemv(c, m->dy, l.qkv, m->dqkv, WH_BIAS, 0.0f, 0));
+      CK(launch_gemv(c, m->dx, l.qkv, m->dqkv, WH_BIAS, 0.0f, 0, l.norm_self.w, l.norm_self.b, m->dy));
       CK(launch_pack(c, m->dqkv, d, 0, m->own[i], 1, d, m->context, 0, dpos));
       CK(launch_attend(c, m->dqkv, m->own[i], m->dpart, m->datt, 1, m->context, heads, hd, dpos));
       CK(launch_gemv(c, m->datt, l.self_out, m->dx, WH_RESIDUAL, 1.0f, 0));
-      CK(launch_layer_norm(c, m->dx, l.norm_cross.w, l.norm_cross.b, m->dy, 1, d, nullptr, nullptr, 0));
-      CK(launch_gemv(c, m->dy, l.cross_q, m->dqkv, WH_BIAS, 0.0f, 0));
+      CK(launch_gemv(c, m->dx, l.cross_q, m->dqkv, WH_BIAS, 0.0f, 0, l.norm_cross.w, l.norm_cross.b, m->dy));
       CK(launch_attend(c, m->dqkv, m->cross[i], m->dpart, m->datt, m->cross_frames, m->cross_frames, heads, hd));
       CK(launch_gemv(c, m->datt, l.cross_out, m->dx, WH_RESIDUAL, 1.0f, 0));
-      CK(launch_layer_norm(c, m->dx, l.norm_ffn.w, l.norm_ffn.b, m->dy, 1, d, nullptr, nullptr, 0));
-      CK(launch_gemv(c, m->dy, l.fc1, m->dh, WH_GELU, 0.0f, 0));
+      CK(launch_gemv(c, m->dx, l.fc1, m->dh, WH_GELU, 0.0f, 0, l.norm_ffn.w, l.norm_ffn.b, m->dy));
       CK(launch_gemv(c, m->dh, l.fc2, m->dx, WH_RESIDUAL, 1.0f, 0));
     }
-    CK(launch_layer_norm(c, m->dx, m->dec_norm.w, m->dec_norm.b, m->dy, 1, d, nullptr, nullptr, 0));
-    return launch_gemv(c, m->dy, m->token_embd, logits, WH_BIAS, 0.0f, 0);
+    return launch_gemv(c, m->dx, m->token_embd, logits, WH_BIAS, 0.0f, 0, m->dec_norm.w, m->dec_norm.b, m->dy);
   });
 }
 

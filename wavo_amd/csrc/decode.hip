@@ -524,6 +524,106 @@ __global__ void combine_kernel(const float *__restrict__ part, float *__restrict
   }
 }
 
+// One head's query against all its keys in one workgroup of 16 waves (no parts to merge afterwards):
+// key j is lane j % 64 of wave (j / 64) % 16 in round j / 1024, its score from the transposed K cache
+// (64 keys of a wave read 256 contiguous bytes per pair); the softmax over all keys; then the waves
+// take keys in turn for p·V (a key's value pairs are contiguous), summed over the waves through LDS.
+// The parts-and-merge arithmetic of decode.wgsl:56-147 regrouped: results differ by f32 rounding.
+constexpr int AT_WAVES = 16, AT_ROUNDS = 8;  // keys ≤ 16·64·8 = 8192
+__global__ __launch_bounds__(64 * AT_WAVES) void attend_one_kernel(const float *__restrict__ q,
+                                                                   const uint32_t *__restrict__ kv,
+                                                                   float *__restrict__ o, int n, int hd, float scale,
+                                                                   int cols, int heads, const int *__restrict__ dn) {
+  if (dn) n = min(*dn + n, cols);
+  __shared__ float qs[128];
+  __shared__ float p[64 * AT_WAVES * AT_ROUNDS];
+  __shared__ float red[2 * AT_WAVES];
+  __shared__ float2 ov[AT_WAVES][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pairs = hd / 2, h = blockIdx.x;
+  const size_t k0 = (size_t)h * pairs * cols;
+  const size_t v_stride = (size_t)heads * pairs;
+  const size_t v0 = v_stride * cols + (size_t)h * pairs;
+  for (int i = tid; i < hd; i += 64 * AT_WAVES) qs[i] = (float)(_Float16)q[h * hd + i];
+  __syncthreads();
+  // Scores of the thread's keys (unrolled over the rounds so every load is in flight at once).
+  float sc[AT_ROUNDS];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < AT_ROUNDS; r++) {
+    const int j = r * 64 * AT_WAVES + wave * 64 + lane;
+    sc[r] = -INFINITY;
+    if (j < n) {
+      float acc = 0.0f;
+      // 32 pairs' loads in flight at once (hd ≤ 64: one round trip per key).
+      for (int i0 = 0; i0 < pairs; i0 += 32) {
+        uint32_t u[32];
+#pragma unroll
+        for (int t = 0; t < 32; t++) u[t] = i0 + t < pairs ? kv[k0 + (size_t)(i0 + t) * cols + j] : 0u;
+#pragma unroll
+        for (int t = 0; t < 32; t++)
+          if (i0 + t < pairs) acc += qs[2 * (i0 + t)] * half_bits(u[t] & 0xffffu) + qs[2 * (i0 + t) + 1] * half_bits(u[t] >> 16);
+      }
+      sc[r] = acc * scale;
+      mx = fmaxf(mx, sc[r]);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int w = 1; w < AT_WAVES; w++) mx = fmaxf(mx, red[w]);
+  float l = 0.0f;
+#pragma unroll
+  for (int r = 0; r < AT_ROUNDS; r++) {
+    const int j = r * 64 * AT_WAVES + wave * 64 + lane;
+    if (j < n) {
+      const float e = __expf(sc[r] - mx);
+      p[j] = e;
+      l += e;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
+  if (lane == 0) red[AT_WAVES + wave] = l;
+  __syncthreads();  // p and the sums are complete
+  l = 0.0f;
+  for (int w = 0; w < AT_WAVES; w++) l += red[AT_WAVES + w];
+  // p·V: a wave takes `groups` keys at a time, one value pair per lane.
+  const int groups = 64 / pairs, c = lane % pairs, g = lane / pairs;
+  float2 acc = make_float2(0.0f, 0.0f);
+  if (g < groups) {
+    const int step = AT_WAVES * groups;
+    for (int j0 = wave * groups + g; j0 < n; j0 += 16 * step) {  // 16 keys' loads in flight at once
+      uint32_t u[16];
+#pragma unroll
+      for (int t = 0; t < 16; t++) u[t] = j0 + t * step < n ? kv[v0 + (size_t)(j0 + t * step) * v_stride + c] : 0u;
+#pragma unroll
+      for (int t = 0; t < 16; t++)
+        if (j0 + t * step < n) {
+          const float pj = p[j0 + t * step];
+          acc.x += pj * half_bits(u[t] & 0xffffu);
+          acc.y += pj * half_bits(u[t] >> 16);
+        }
+    }
+  }
+  // Sum over the wave's groups, then over the waves.
+  for (int gg = 1; gg < groups; gg++) {
+    const float ax = __shfl(acc.x, lane + gg * pairs, 64), ay = __shfl(acc.y, lane + gg * pairs, 64);
+    if (g == 0) acc.x += ax, acc.y += ay;
+  }
+  if (g == 0) ov[wave][c] = acc;
+  __syncthreads();
+  if (tid < pairs) {
+    float2 t = make_float2(0.0f, 0.0f);
+    for (int w = 0; w < AT_WAVES; w++) t.x += ov[w][tid].x, t.y += ov[w][tid].y;
+    const float inv = 1.0f / l;
+    o[h * hd + 2 * tid] = t.x * inv;
+    o[h * hd + 2 * tid + 1] = t.y * inv;
+  }
+}
+
 // Rows of x (K then V, d floats each) into the f16 cache at positions col.. (decode.wgsl:148-173).
 __global__ void pack_kernel(const float *__restrict__ x, uint32_t *__restrict__ y, int n, int d, int cols, int col,
                             int src, int stride, const int *__restrict__ dcol) {
@@ -608,6 +708,11 @@ int launch_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, 
   float scale = 1.0f / sqrtf((float)hd);
   // A key count in device memory: the grid covers the whole cache and parts past it return.
   const int most = dn ? cols : n;
+  if (most <= 64 * AT_WAVES * AT_ROUNDS) {  // every key in one workgroup per head: no merge launch
+    ProfScope prof(ctx, "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
+    attend_one_kernel<<<heads, 64 * AT_WAVES, 0, ctx->stream>>>(q, kv, o, n, hd, scale, cols, heads, dn);
+    return wh_launched(ctx, "attend");
+  }
   dim3 grid((most + KEYS - 1) / KEYS, heads);
   ProfScope prof(ctx, "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
   attend_kernel<<<grid, 256, 0, ctx->stream>>>(q, kv, part, n, hd, scale, cols, heads, dn);

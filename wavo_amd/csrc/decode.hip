@@ -243,33 +243,74 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
 #pragma unroll
   for (int i = 0; i < GV_NS - 1; i++)
     if (s0 + i < s1) issue(s0 + i);
-  if (P.ln_g) {
+  // `a` (and the norm's g, b) into LDS.  Every load of a thread is issued before any is used, so the
+  // prologue costs one round trip (with the first stages' DMA), not one per loop iteration.
+  const int q4 = P.k / 4;
+  const bool vec = ((uintptr_t)P.a % 16 == 0) && q4 <= 16 * 256;
+  __shared__ float stat[2];
+  if (P.ln_g && wave == 0) {
     // The norm before this product, with layer_norm_kernel's arithmetic (one wave sums in the same
-    // order), so the normalized row equals the standalone kernel's bit for bit.
-    __shared__ float stat[2];
-    if (wave == 0) {
-      const float4 *a4 = (const float4 *)P.a;
-      const int q4 = P.k / 4;
-      float sm = 0.0f;
+    // order, zeros past the row), so the normalized row equals the standalone kernel's bit for bit.
+    const float4 *a4 = (const float4 *)P.a;
+    float sm = 0.0f, q = 0.0f, mean;
+    if (q4 <= 16 * 64) {
+      float4 v[16];
+#pragma unroll
+      for (int t = 0; t < 16; t++) v[t] = lane + 64 * t < q4 ? a4[lane + 64 * t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+      for (int t = 0; t < 16; t++) sm += (v[t].x + v[t].y) + (v[t].z + v[t].w);
+      mean = gv_wave_sum(sm) / (float)P.k;
+#pragma unroll
+      for (int t = 0; t < 16; t++)
+        if (lane + 64 * t < q4) {
+          const float dx = v[t].x - mean, dy = v[t].y - mean, dz = v[t].z - mean, dw = v[t].w - mean;
+          q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
+        }
+    } else {
       for (int i = lane; i < q4; i += 64) {
         const float4 v = a4[i];
         sm += (v.x + v.y) + (v.z + v.w);
       }
-      const float mean = gv_wave_sum(sm) / (float)P.k;
-      float q = 0.0f;
+      mean = gv_wave_sum(sm) / (float)P.k;
       for (int i = lane; i < q4; i += 64) {
         const float4 v = a4[i];
         const float dx = v.x - mean, dy = v.y - mean, dz = v.z - mean, dw = v.w - mean;
         q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
       }
-      const float rstd = rsqrtf(gv_wave_sum(q) / (float)P.k + 1e-5f);
-      if (lane == 0) stat[0] = mean, stat[1] = rstd;
     }
-    __syncthreads();
-    const float mean = stat[0], rstd = stat[1];
-    for (int i = tid; i < P.k; i += 256) as[(i >> 6) * AS + (i & 63)] = (P.a[i] - mean) * rstd * P.ln_g[i] + P.ln_b[i];
+    const float rstd = rsqrtf(gv_wave_sum(q) / (float)P.k + 1e-5f);
+    if (lane == 0) stat[0] = mean, stat[1] = rstd;
+  }
+  if (vec) {
+    const float4 *a4 = (const float4 *)P.a;
+    float4 av[16], gv[16], bv[16];
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+      const int i = tid + 256 * t;
+      av[t] = i < q4 ? a4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (P.ln_g && i < q4) gv[t] = ((const float4 *)P.ln_g)[i], bv[t] = ((const float4 *)P.ln_b)[i];
+    }
+    if (P.ln_g) {
+      __syncthreads();  // the norm's statistics
+      const float mean = stat[0], rstd = stat[1];
+#pragma unroll
+      for (int t = 0; t < 16; t++) {
+        av[t].x = (av[t].x - mean) * rstd * gv[t].x + bv[t].x;
+        av[t].y = (av[t].y - mean) * rstd * gv[t].y + bv[t].y;
+        av[t].z = (av[t].z - mean) * rstd * gv[t].z + bv[t].z;
+        av[t].w = (av[t].w - mean) * rstd * gv[t].w + bv[t].w;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 16; t++) {
+      const int i = tid + 256 * t;  // float4 i: elements 4i .. 4i + 3 of item 4i / 64
+      if (i < q4) *(float4 *)(as + (i >> 4) * AS + 4 * (i & 15)) = av[t];
+    }
   } else {
-    for (int i = tid; i < P.k; i += 256) as[(i >> 6) * AS + (i & 63)] = P.a[i];
+    if (P.ln_g) __syncthreads();
+    const float mean = P.ln_g ? stat[0] : 0.0f, rstd = P.ln_g ? stat[1] : 1.0f;
+    for (int i = tid; i < P.k; i += 256)
+      as[(i >> 6) * AS + (i & 63)] = P.ln_g ? (P.a[i] - mean) * rstd * P.ln_g[i] + P.ln_b[i] : P.a[i];
   }
   const int row_l = tid / items, it = tid % items;
   for (int s = s0; s < s1; s++) {
@@ -649,7 +690,7 @@ int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int e
                 const float *ln_g, const float *ln_b, float *ln_y) {
   if (!a || !c || offset < 0 || epi < WH_BIAS || epi > WH_TANH) return wh_fail(ctx, WH_EARG, "gemv: bad arguments");
   if ((size_t)l->k * 4 > 64 * 1024) return wh_fail(ctx, WH_EARG, "gemv: k %d too large", l->k);
-  if (ln_g && (!ln_b || !ln_y || l->k % 4 || (uintptr_t)a % 16))
+  if (ln_g && (!ln_b || !ln_y || l->k % 4 || (uintptr_t)a % 16 || (uintptr_t)ln_g % 16 || (uintptr_t)ln_b % 16))
     return wh_fail(ctx, WH_EARG, "gemv: the fused norm needs g, b, a row buffer, k %% 4 == 0 and an aligned a");
   bool pair = l->k % 64 == 0;
   // The streaming kernel: whole 64-weight items, at most 256 of them per row, rows 4-byte aligned.

@@ -452,6 +452,36 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     const int d = 4 * (int)(e % q4);
     const size_t r = e / q4;
     const int head = (int)(r % heads), i = (int)((r / heads) % t), b = (int)(r / ((size_t)heads * t));
+    if (ns <= 4) {  // every split's loads in flight at once (the same sums in the same order)
+      float2 ml[4];
+      float4 x[4];
+#pragma unroll
+      for (int sp = 0; sp < 4; sp++)
+        if (sp < ns) {
+          ml[sp] = *(const float2 *)(pml + 2 * ((((size_t)sp * batch + b) * heads + head) * t + i));
+          x[sp] = *(const float4 *)(po + (((size_t)sp * batch + b) * t + i) * (size_t)heads * hd + head * hd + d);
+        }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int sp = 0; sp < 4; sp++)
+        if (sp < ns) mx = fmaxf(mx, ml[sp].x);
+      float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      float den = 0.0f;
+      if (mx != -INFINITY)
+#pragma unroll
+        for (int sp = 0; sp < 4; sp++)
+          if (sp < ns) {
+            const float w = __expf(ml[sp].x - mx);
+            den += w * ml[sp].y;
+            acc.x += w * x[sp].x, acc.y += w * x[sp].y, acc.z += w * x[sp].z, acc.w += w * x[sp].w;
+          }
+      const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+      const float4 y = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+      const size_t at = bo * b + (size_t)i * os + head * hd + d;
+      if (o16) *(half4 *)((_Float16 *)o + at) = half4{(_Float16)y.x, (_Float16)y.y, (_Float16)y.z, (_Float16)y.w};
+      else *(float4 *)((float *)o + at) = y;
+      continue;
+    }
     float mx = -INFINITY;
     for (int sp = 0; sp < ns; sp++) mx = fmaxf(mx, pml[2 * ((((size_t)sp * batch + b) * heads + head) * t + i)]);
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);

@@ -184,6 +184,7 @@ struct GemvArgs {
   float *c;
   int rows, cols, k, epi, offset;
   const float *ln_g, *ln_b;  // non-null: the product takes LayerNorm(a; ln_g, ln_b)
+  GemvPack pack;             // pack.cache non-null: outputs lo .. lo + 2d also into the cache column
   float alpha;
   int row_bytes;
   int rps;        // rows per stage
@@ -391,9 +392,18 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
   __syncthreads();
   const int r0 = s0 * P.rps, r1 = min(s1 * P.rps, P.rows);
   const bool res = P.epi == WH_RESIDUAL || P.epi == WH_GELU_RESIDUAL;
+  const int pcol = P.pack.dcol ? *P.pack.dcol : P.pack.col;
   for (int row = r0 + tid; row < r1; row += 256) {
     float *cp = P.c + P.offset + row;
-    *cp = epilogue(P.epi, P.alpha, rsum[row - r0] + P.bias[row], res ? *cp : 0.0f);
+    const float v = epilogue(P.epi, P.alpha, rsum[row - r0] + P.bias[row], res ? *cp : 0.0f);
+    *cp = v;
+    const int x = row - P.pack.lo;  // the cache's K then V values: pair x / 2, half x % 2 of launch_pack
+    if (P.pack.cache && x >= 0 && x < 2 * P.pack.d && pcol < P.pack.cols) {
+      const int pi = x >> 1, half = P.pack.d / 2;
+      const size_t word = pi < half ? (size_t)pi * P.pack.cols + pcol
+                                    : (size_t)half * P.pack.cols + (size_t)pcol * half + pi - half;
+      ((uint16_t *)P.pack.cache)[2 * word + (x & 1)] = __builtin_bit_cast(uint16_t, (_Float16)v);
+    }
   }
   // Rows rows..cols (the padding rows of the linear): epi(0 + bias), by the first workgroup.
   if (blockIdx.x == 0)
@@ -405,9 +415,10 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
 
 template <int WT>
 int gemv_stream(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha, int offset,
-                const float *ln_g, const float *ln_b) {
+                const float *ln_g, const float *ln_b, const GemvPack *pack) {
   const int items = l->k / 64;
-  GemvArgs P{a, l->w, l->bias, c, l->rows, l->cols, l->k, epi, offset, ln_g, ln_b, alpha, (int)l->row_bytes, 0, 0, 0, 0};
+  GemvArgs P{a, l->w, l->bias, c, l->rows, l->cols, l->k, epi, offset, ln_g, ln_b,
+             pack ? *pack : GemvPack{}, alpha, (int)l->row_bytes, 0, 0, 0, 0};
   P.rps = std::min(256 / items, GV_STAGE / (int)l->row_bytes);
   P.stages = (l->rows + P.rps - 1) / P.rps;
   // Two workgroups per CU (48 KiB of stages each), each streaming a run of stages: measured on
@@ -687,7 +698,10 @@ __global__ void pack_kernel(const float *__restrict__ x, uint32_t *__restrict__ 
 }  // namespace
 
 int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha, int offset,
-                const float *ln_g, const float *ln_b, float *ln_y) {
+                const float *ln_g, const float *ln_b, float *ln_y, const GemvPack *pack) {
+  if (pack && (!pack->cache || pack->d <= 0 || pack->d % 2 || pack->lo < 0 || pack->lo + 2 * pack->d > l->rows ||
+               pack->cols <= 0 || pack->col < 0 || pack->col >= pack->cols))
+    return wh_fail(ctx, WH_EARG, "gemv: bad cache column");
   if (!a || !c || offset < 0 || epi < WH_BIAS || epi > WH_TANH) return wh_fail(ctx, WH_EARG, "gemv: bad arguments");
   if ((size_t)l->k * 4 > 64 * 1024) return wh_fail(ctx, WH_EARG, "gemv: k %d too large", l->k);
   if (ln_g && (!ln_b || !ln_y || l->k % 4 || (uintptr_t)a % 16 || (uintptr_t)ln_g % 16 || (uintptr_t)ln_b % 16))
@@ -697,11 +711,15 @@ int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int e
   if (pair && l->k / 64 <= 256 && l->row_bytes % 4 == 0 && (int)l->row_bytes <= GV_STAGE && l->rows > 0) {
     int rc = 1;
     switch (l->type) {
-      case WH_Q8_0: rc = gemv_stream<WH_Q8_0>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b); break;
-      case WH_Q4_0: rc = gemv_stream<WH_Q4_0>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b); break;
-      case WH_F16: rc = gemv_stream<WH_F16>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b); break;
+      case WH_Q8_0: rc = gemv_stream<WH_Q8_0>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b, pack); break;
+      case WH_Q4_0: rc = gemv_stream<WH_Q4_0>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b, pack); break;
+      case WH_F16: rc = gemv_stream<WH_F16>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b, pack); break;
     }
     if (rc != 1) return rc;
+  }
+  if (pack) {  // the general kernel, then the cache column by its own launch
+    if (int rc = launch_gemv(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b, ln_y, nullptr)) return rc;
+    return launch_pack(ctx, c + offset, pack->lo, 0, pack->cache, 1, pack->d, pack->cols, pack->col, pack->dcol);
   }
   if (ln_g) {  // the general kernel takes the norm from its own launch
     if (int rc = launch_layer_norm(ctx, a, ln_g, ln_b, ln_y, 1, l->k, nullptr, nullptr, 0)) return rc;

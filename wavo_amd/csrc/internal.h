@@ -101,10 +101,19 @@ int launch_split_residual_ln(wh_ctx *ctx, const float *part, int splits, const f
                              int keep_x = 1, const float *g2 = nullptr, const float *b2 = nullptr, void *y2 = nullptr);
 // f32 → f16 (RNE) of n values (n % 4 == 0).
 int launch_to_half(wh_ctx *ctx, const float *x, void *y, size_t n);
+// A decoder cache column written by a GEMV as well: outputs lo .. lo + 2d (a K row then a V row of d
+// values) go, as f16, to column col (or *dcol) of `cache` (cols positions; launch_pack's layout).
+struct GemvPack {
+  uint32_t *cache;
+  int lo, d, cols, col;
+  const int *dcol;
+};
 // With ln_g: the product takes LayerNorm(a; ln_g, ln_b) (one row of k): inside the streaming kernel,
-// or written to ln_y (k floats) by its own launch before the general kernel.
+// or written to ln_y (k floats) by its own launch before the general kernel.  With pack: see GemvPack
+// (inside the streaming kernel, or by launch_pack after the general one).
 int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,
-                int offset, const float *ln_g = nullptr, const float *ln_b = nullptr, float *ln_y = nullptr);
+                int offset, const float *ln_g = nullptr, const float *ln_b = nullptr, float *ln_y = nullptr,
+                const GemvPack *pack = nullptr);
 // With dpos (device memory), the position offset is (*dpos)·dstride instead of `offset`: a recorded
 // decoder step reads its position from the device.
 int launch_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, const uint32_t *ids,

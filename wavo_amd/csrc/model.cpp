@@ -1288,8 +1288,9 @@ int wh_whisper_step(wh_model *m, int token, int pos, float *logits) {
     // Each LayerNorm runs inside the GEMV that consumes it (its only reader).
     for (int i = 0; i < m->dec_layers; i++) {
       const DLayer &l = m->dl[i];
-      CK(launch_gemv(c, m->dx, l.qkv, m->dqkv, WH_BIAS, 0.0f, 0, l.norm_self.w, l.norm_self.b, m->dy));
-      CK(launch_pack(c, m->dqkv, d, 0, m->own[i], 1, d, m->context, 0, dpos));
+      // q, k, v, with k and v also written into the self-attention cache's column (Decoder::pack).
+      const GemvPack kv{m->own[i], d, d, m->context, 0, dpos};
+      CK(launch_gemv(c, m->dx, l.qkv, m->dqkv, WH_BIAS, 0.0f, 0, l.norm_self.w, l.norm_self.b, m->dy, &kv));
       CK(launch_attend(c, m->dqkv, m->own[i], m->dpart, m->datt, 1, m->context, heads, hd, dpos));
       CK(launch_gemv(c, m->datt, l.self_out, m->dx, WH_RESIDUAL, 1.0f, 0));
       CK(launch_gemv(c, m->dx, l.cross_q, m->dqkv, WH_BIAS, 0.0f, 0, l.norm_cross.w, l.norm_cross.b, m->dy));

@@ -13,7 +13,8 @@ in a profiled step.  Its average launch duration is measured by launching that e
 (same tile plan, m × n × k, epilogue and output type; random q8_0 weights of the same shape) 50 times
 back to back between two HIP events on the library's stream — events around every single launch would
 add their own few microseconds to each — and `achieved` = 2·m·n·k per launch over that duration, against
-MI355X's dense fp16 MFMA peak.  `traffic` is that launch's HBM bytes from rocprofv3 FETCH_SIZE /
+MI355X's dense fp16 MFMA peak.  A k-split configuration is timed as its GEMM kernel alone, as in the step
+(where the next kernel, fused with the LayerNorm, adds the partial sums).  `traffic` is that launch's HBM bytes from rocprofv3 FETCH_SIZE /
 WRITE_SIZE passes (profiles/), when a summary for the same configuration is committed there.
 
 `gemv` is the Whisper-large-v3-turbo decoder's per-token matrix-vector products (q8_0; 4 layers of
@@ -72,10 +73,14 @@ def gemm_replay(gpu, name, reps=50):
     f16 = out == "f16"
     plan = f"{bm},{bn},{wm},{wn},{ns},{split[2:] if split else 1}"
     os.environ["WAVO_GEMM_PLAN"] = plan  # the same launch plan as in the step
+    # A split GEMM's kernel alone, as it runs in the step (where the following fused LayerNorm kernel
+    # adds the partial sums); a C-ABI call would add its own finishing kernel.
+    os.environ["WAVO_GEMM_KERNEL_ONLY"] = "1"
     import wavo_amd
 
     g2 = wavo_amd.Gpu(0)
     os.environ.pop("WAVO_GEMM_PLAN")
+    os.environ.pop("WAVO_GEMM_KERNEL_ONLY")
     lin2 = g2.linear([(w, wtype, int(k), int(n))], np.zeros(int(width), np.float32))
     a2 = g2.upload(rng.standard_normal((int(m), int(k)), dtype=np.float32).astype(np.float16))
     c2 = g2.buffer(int(m) * int(width))

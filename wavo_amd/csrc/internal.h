@@ -25,6 +25,10 @@ struct wh_ctx {
   // GEMM launch-plan override from WAVO_GEMM_PLAN ("bm,bn,wm,wn,bk,split"; tuning sweeps only):
   // all zero = chosen per shape.
   int gemm_plan[6] = {0, 0, 0, 0, 0, 0};
+  // WAVO_GEMM_KERNEL_ONLY (measurement only): a split GEMM call stops after the GEMM kernel, leaving
+  // its partial sums unfinished, so that the kernel can be timed alone as it runs inside a model step
+  // (where the next kernel finishes the sums).
+  int gemm_kernel_only = 0;
   // Per-shape overrides from WAVO_GEMM_SHAPE_PLANS ("m,cols,k:bm,bn,wm,wn,stages,split;…"; tuning
   // sweeps inside a model's step only).
   std::vector<std::array<int, 9>> gemm_shape_plans;

@@ -119,6 +119,7 @@ int wh_open(int device_index, wh_ctx **out) {
       for (int i = 0; i < 6; i++) o[i] = 0;
   }
   if (const char *t = getenv("WAVO_ATTN_SPLIT")) ctx->attn_split = std::max(0, std::min(atoi(t), 64));
+  if (const char *t = getenv("WAVO_GEMM_KERNEL_ONLY")) ctx->gemm_kernel_only = atoi(t) != 0;
   if (const char *t = getenv("WAVO_GEMM_SHAPE_PLANS")) {
     for (const char *q = t; *q;) {
       std::array<int, 9> o{};

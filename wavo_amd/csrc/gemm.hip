@@ -759,12 +759,22 @@ Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
   // workgroups share a CU (measured 187 against 221 µs at 12000×4096×1024); a single wave of
   // workgroups (one 750-frame window) runs faster with four.
   if (t128 >= 4L * cus) p = {128, 128, 2, 4, 3, 1};
+  else if (t128 > cus && (t128 <= 2L * cus || k >= 4096))
+    // More tiles than CUs (a 1500-frame window's wide projections, 16 windows' long-k ones): 4-wave
+    // workgroups in three stages, two per CU, take them in one round or fewer (measured in the
+    // encoder: Whisper's fc1 1.31 against 1.43 ms per call, 16 × 60 s FFN down 8.0 against 8.6; the
+    // 16 windows' 1024 × 1024 projections stay with 8-wave workgroups, 3.13 against 3.22).
+    p = {128, 128, 2, 2, 3, 1};
   else if (t128 >= cus / 2) p = {128, 128, 2, 4, 4, 1};
   else if (t128 * 4 <= cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
     // Long k over few tiles (the FFN's down projection, 750 × 1024 × 4096): 128×128 tiles split 4
     // ways, one workgroup per CU, move half the bytes per MFMA of 64×64 ones (measured in the
     // encoder step: 1.02 against 1.06 ms for its 48 launches).
     p = {128, 128, 2, 4, 4, 4};
+  else if (t128 * 4 <= 2L * cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
+    // The same with up to two workgroups per CU (Whisper's fc2, 1500 × 1280 × 5120: 1.18 + its
+    // finish against 1.82 ms per call for 64×64 tiles whole).
+    p = {128, 128, 2, 2, 3, 4};
   else if (t64 < cus)
     // Split only while every split keeps at least 16 k steps: shorter ones spend more on the
     // pipeline's fill and the partial sums than the extra workgroups win (k = 1024 runs faster whole).

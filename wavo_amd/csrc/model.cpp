@@ -988,18 +988,24 @@ int whisper_encode(wh_model *m, const float *mel, int mel_frames, float *out) {
     CK(launch_im2col(c, m->h, m->qk, 2 * t, d, 3, 2, 1, 1, 0, 0));
     CK(launch_copy(c, m->x, m->enc_pos, (size_t)t * d * 4));
     CK(lin(m, m->qk, m->wconv1, m->x, t, WH_GELU_RESIDUAL));
-    // Pre-LN blocks; the GEMMs' inputs as f16 (see record_block).
+    // Pre-LN blocks; the GEMMs' inputs as f16 (see record_block).  Each residual projection runs with
+    // the norm that follows it (a k-split GEMM's finish, the residual add and the norm in one kernel):
+    // the attention output's with norm_ffn, the FFN's with the next block's norm_attn or, last, the
+    // encoder's final norm into `out`.
     void *y16 = m->y, *h16 = m->h;
-    for (const WBlock &b : m->wblocks) {
-      CK(launch_layer_norm(c, m->x, b.norm_attn.w, b.norm_attn.b, y16, t, d, nullptr, nullptr, 0, 1));
+    if (m->wblocks.empty()) return launch_layer_norm(c, m->x, m->enc_norm.w, m->enc_norm.b, out, t, d, nullptr, nullptr, 0);
+    CK(launch_layer_norm(c, m->x, m->wblocks[0].norm_attn.w, m->wblocks[0].norm_attn.b, y16, t, d, nullptr, nullptr, 0, 1));
+    for (size_t i = 0; i < m->wblocks.size(); i++) {
+      const WBlock &b = m->wblocks[i];
       CK(launch_gemm_h(c, y16, b.qkv, m->qk, t, b.qkv->cols + b.qkv->dual, WH_BIAS, 0.0f, 1));
       CK(launch_attention(c, m->qk, nullptr, nullptr, y16, t, m->heads, hd, nullptr, t, 1, 1, 1));
-      CK(launch_gemm_h(c, y16, b.out, m->x, t, b.out->cols + b.out->dual, WH_RESIDUAL, 1.0f, 0));
-      CK(launch_layer_norm(c, m->x, b.norm_ffn.w, b.norm_ffn.b, y16, t, d, nullptr, nullptr, 0, 1));
+      CK(launch_gemm_h_ln(c, y16, b.out, m->x, t, 1.0f, b.norm_ffn.w, b.norm_ffn.b, y16, 1));
       CK(launch_gemm_h(c, y16, b.fc1, h16, t, b.fc1->cols + b.fc1->dual, WH_GELU, 0.0f, 1));
-      CK(launch_gemm_h(c, h16, b.fc2, m->x, t, b.fc2->cols + b.fc2->dual, WH_RESIDUAL, 1.0f, 0));
+      const bool last = i + 1 == m->wblocks.size();
+      const Chan &nn = last ? m->enc_norm : m->wblocks[i + 1].norm_attn;
+      CK(launch_gemm_h_ln(c, h16, b.fc2, m->x, t, 1.0f, nn.w, nn.b, last ? (void *)out : y16, last ? 0 : 1));
     }
-    return launch_layer_norm(c, m->x, m->enc_norm.w, m->enc_norm.b, out, t, d, nullptr, nullptr, 0);
+    return WH_OK;
   });
 }
 

@@ -93,6 +93,25 @@ def test_gemm_large(gpu, wtype, m, n, k):
               what=f"type {wtype} {m}x{n}x{k} epi {e}")
 
 
+@pytest.mark.parametrize("m,n,k", [(1500, 5120, 1280), (1500, 1280, 5120)])
+def test_gemm_more_tiles_than_cus(gpu, m, n, k):
+    # The 1500-frame plans: 128×128 tiles of 4 wavefronts, three stages, two workgroups per CU
+    # (1500 × 5120: 480 tiles), and the same split 4 ways over k (1500 × 1280 × 5120).
+    w = np.random.default_rng(1).normal(0, 0.02, (n, k)).astype(np.float32)
+    raw = ox.quantize(w, wa.Q8_0)
+    bias = rnd(n, 2)
+    l = gpu.linear([(raw, wa.Q8_0, k, n)], bias)
+    ol = ox.Linear(wa.Q8_0, k, [(raw, n)], bias)
+    a = rnd(m * k, 3).reshape(m, k)
+    ab, cb = gpu.upload(a), gpu.upload(rnd(m * n, 4).reshape(m, n))
+    c0 = gpu.read(cb, (m, n))
+    for e in (wa.GELU, wa.RESIDUAL):
+        gpu.gemm(ab, l, cb, m, e, 1.0)
+        want = ox.gemm(a, ol, m, e, 1.0, c0)
+        close(gpu.read(cb, (m, n)), want, tol=2e-5 * max(1.0, float(np.abs(want).max())), what=f"{m}x{n}x{k} epi {e}")
+        c0 = gpu.read(cb, (m, n))
+
+
 def test_gemm_padded_k(gpu):
     # k = 40 is padded to 64 by Gpu::conv; input rows are 64 wide with zeros after 40 (from im2col).
     n, k, m = 64, 40, 37

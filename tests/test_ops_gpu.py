@@ -282,6 +282,23 @@ def test_attend_and_pack(gpu, heads, hd):
         close(gpu.read(ob, (d,)), ox.attend(q, cpu, keys, n, heads, hd), what=f"attend n {n}")
 
 
+def test_attend_long_cache(gpu):
+    # More keys than one workgroup per head takes (8192): 256-key parts merged by a second kernel.
+    heads, hd, keys = 2, 64, 9000
+    d = heads * hd
+    kv = rnd(keys * 2 * d, 17).reshape(keys, 2 * d)
+    q = rnd(d, 18)
+    cpu = kv.reshape(keys, 2 * heads, hd).transpose(1, 0, 2).astype(np.float16).astype(np.float32)
+    xb, qb = gpu.upload(kv), gpu.upload(q)
+    cache = gpu.buffer(keys * d)
+    part = gpu.buffer(gpu.attend_len(keys, heads, hd))
+    ob = gpu.buffer(d)
+    gpu.pack(xb, 0, 2 * d, cache, keys, d, keys, 0)
+    for n in (8192, 8193, keys):
+        gpu.attend(qb, cache, part, ob, n, keys, heads, hd)
+        close(gpu.read(ob, (d,)), ox.attend(q, cpu, keys, n, heads, hd), what=f"attend n {n}")
+
+
 def test_pack_layout(gpu):
     # Rows of K then V (d = 6) from x[3..], 13 floats apart, into a cache of 7 positions.
     x = rnd(3 + 13 * 2, 7)

@@ -759,11 +759,17 @@ Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
   // workgroups share a CU (measured 187 against 221 µs at 12000×4096×1024); a single wave of
   // workgroups (one 750-frame window) runs faster with four.
   if (t128 >= 4L * cus) p = {128, 128, 2, 4, 3, 1};
+  else if (t128 > cus && t128 <= 2L * cus && k < 4096)
+    // Between one and two 128×128 tiles per CU (a 1500-frame window's wide projections): 256×128
+    // tiles of 8 wavefronts with 64×64 wave tiles, one per CU, read each a fragment for twice the
+    // columns (measured in the Whisper encoder: 6.05 against 6.16 ms per call, fc1 1.28 against
+    // 1.35 ms, than 4-wave 128×128 tiles two per CU; at m = 12000 they are slower).
+    p = {256, 128, 4, 2, 3, 1};
   else if (t128 > cus && (t128 <= 2L * cus || k >= 4096))
-    // More tiles than CUs (a 1500-frame window's wide projections, 16 windows' long-k ones): 4-wave
-    // workgroups in three stages, two per CU, take them in one round or fewer (measured in the
-    // encoder: Whisper's fc1 1.31 against 1.43 ms per call, 16 × 60 s FFN down 8.0 against 8.6; the
-    // 16 windows' 1024 × 1024 projections stay with 8-wave workgroups, 3.13 against 3.22).
+    // More tiles than CUs with a long k (16 windows' FFN down projection): 4-wave workgroups in
+    // three stages, two per CU, take them in one round or fewer (measured in the encoder: 16 × 60 s
+    // FFN down 8.0 against 8.6 ms per call; the 16 windows' 1024 × 1024 projections stay with 8-wave
+    // workgroups, 3.13 against 3.22).
     p = {128, 128, 2, 2, 3, 1};
   else if (t128 >= cus / 2) p = {128, 128, 2, 4, 4, 1};
   else if (t128 * 4 <= cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
@@ -840,6 +846,7 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     PLAN(128, 128, 2, 4, 3)
     PLAN(64, 64, 2, 2, 3)
     PLAN(128, 128, 2, 2, 3)
+    PLAN(256, 128, 4, 2, 3)
 #undef PLAN
     if (!ok) return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages", p.bm, p.bn, p.wm, p.wn, p.ns);
     if (int rc = wh_launched(ctx, "gemm")) return rc;

@@ -387,6 +387,26 @@ def test_relative_attention(gpu, t, heads, hd, valid):
     close(gpu.read(ob, (t, d)), want, tol=ATT_TOL)
 
 
+@pytest.mark.parametrize("valid", [None, 400])
+def test_relative_attention_many_splits(monkeypatch, valid):
+    """Key blocks split 8 ways (more than the merge's group of four: its running-maximum rescale, and
+    splits past the valid keys that contribute nothing), through a context opened with the tuning
+    override."""
+    t, heads, hd = 750, 8, 128
+    monkeypatch.setenv("WAVO_ATTN_SPLIT", "8")
+    g = wa.Gpu(0)
+    try:
+        d = heads * hd
+        qkv, pos, u, vb, rows = relative_inputs(t, heads, hd, seed=23)
+        v = -1 if valid is None else valid
+        want = ox.relative_attention(qkv, pos, u, vb, t, heads, hd, v)
+        qb, pb, ob = g.upload(rows), g.upload(pos), g.buffer(t * d)
+        g.attention(qb, None, pb, ob, t, heads, hd, v)
+        close(g.read(ob, (t, d)), want, tol=ATT_TOL)
+    finally:
+        g.close()
+
+
 @pytest.mark.parametrize("valid_drop", [0, 1])
 def test_subsampling(gpu, valid_drop):
     t, f, ch = 29, 11, 5

@@ -452,48 +452,36 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     const int d = 4 * (int)(e % q4);
     const size_t r = e / q4;
     const int head = (int)(r % heads), i = (int)((r / heads) % t), b = (int)(r / ((size_t)heads * t));
-    if (ns <= 4) {  // every split's loads in flight at once (the same sums in the same order)
+    // Splits in groups of four, each group's loads in flight at once; a running maximum rescales
+    // the sums when a later group raises it (one group: the plain two-pass merge, same order).
+    float mx = -INFINITY, den = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s0 = 0; s0 < ns; s0 += 4) {
       float2 ml[4];
       float4 x[4];
 #pragma unroll
-      for (int sp = 0; sp < 4; sp++)
-        if (sp < ns) {
-          ml[sp] = *(const float2 *)(pml + 2 * ((((size_t)sp * batch + b) * heads + head) * t + i));
-          x[sp] = *(const float4 *)(po + (((size_t)sp * batch + b) * t + i) * (size_t)heads * hd + head * hd + d);
+      for (int q = 0; q < 4; q++)
+        if (s0 + q < ns) {
+          const size_t sp = s0 + q;
+          ml[q] = *(const float2 *)(pml + 2 * (((sp * batch + b) * heads + head) * t + i));
+          x[q] = *(const float4 *)(po + ((sp * batch + b) * t + i) * (size_t)heads * hd + head * hd + d);
         }
-      float mx = -INFINITY;
+      float cm = mx;
 #pragma unroll
-      for (int sp = 0; sp < 4; sp++)
-        if (sp < ns) mx = fmaxf(mx, ml[sp].x);
-      float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      float den = 0.0f;
-      if (mx != -INFINITY)
+      for (int q = 0; q < 4; q++)
+        if (s0 + q < ns) cm = fmaxf(cm, ml[q].x);
+      if (cm == -INFINITY) continue;  // no split so far saw a valid key
+      const float rs = __expf(mx - cm);
+      den *= rs, acc.x *= rs, acc.y *= rs, acc.z *= rs, acc.w *= rs;
 #pragma unroll
-        for (int sp = 0; sp < 4; sp++)
-          if (sp < ns) {
-            const float w = __expf(ml[sp].x - mx);
-            den += w * ml[sp].y;
-            acc.x += w * x[sp].x, acc.y += w * x[sp].y, acc.z += w * x[sp].z, acc.w += w * x[sp].w;
-          }
-      const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-      const float4 y = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
-      const size_t at = bo * b + (size_t)i * os + head * hd + d;
-      if (o16) *(half4 *)((_Float16 *)o + at) = half4{(_Float16)y.x, (_Float16)y.y, (_Float16)y.z, (_Float16)y.w};
-      else *(float4 *)((float *)o + at) = y;
-      continue;
+      for (int q = 0; q < 4; q++)
+        if (s0 + q < ns) {
+          const float w = __expf(ml[q].x - cm);
+          den += w * ml[q].y;
+          acc.x += w * x[q].x, acc.y += w * x[q].y, acc.z += w * x[q].z, acc.w += w * x[q].w;
+        }
+      mx = cm;
     }
-    float mx = -INFINITY;
-    for (int sp = 0; sp < ns; sp++) mx = fmaxf(mx, pml[2 * ((((size_t)sp * batch + b) * heads + head) * t + i)]);
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float den = 0.0f;
-    if (mx != -INFINITY)
-      for (int sp = 0; sp < ns; sp++) {
-        const float *ml = pml + 2 * ((((size_t)sp * batch + b) * heads + head) * t + i);
-        const float w = __expf(ml[0] - mx);
-        den += w * ml[1];
-        const float4 x = *(const float4 *)(po + (((size_t)sp * batch + b) * t + i) * (size_t)heads * hd + head * hd + d);
-        acc.x += w * x.x, acc.y += w * x.y, acc.z += w * x.z, acc.w += w * x.w;
-      }
     const float inv = den > 0.0f ? 1.0f / den : 0.0f;
     const float4 y = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
     const size_t at = bo * b + (size_t)i * os + head * hd + d;

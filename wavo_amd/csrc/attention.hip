@@ -517,10 +517,10 @@ size_t split_bytes(int ns, int t, int heads, int hd, int batch) {
 
 template <int DP, typename T>
 void launch_pack(wh_ctx *ctx, const Pack &sp, const T *k, int ks, long kbs, const T *v, int vs, long vbs, const T *pos,
-                 int t, int heads, int hd, int batch, _Float16 *kp, _Float16 *vt, _Float16 *pp) {
+                 int ps, int t, int heads, int hd, int batch, _Float16 *kp, _Float16 *vt, _Float16 *pp) {
   const int gx = sp.tk / KB + (pos ? sp.prows / 32 : 0);
   pack_kernel<DP, T><<<dim3(gx, heads, batch), 256, 0, ctx->stream>>>(k, ks, kbs, v, vs, vbs, t, heads, hd, sp.tk, kp, vt,
-                                                                       pos, heads * hd, 2 * t + 15, sp.pfront, sp.prows, pp);
+                                                                       pos, ps, 2 * t + 15, sp.pfront, sp.prows, pp);
 }
 
 template <bool REL>
@@ -546,7 +546,7 @@ int launch_flash(wh_ctx *ctx, const Args &a, int heads, int batch, int dp) {
 }
 
 template <typename T>
-int attention_t(wh_ctx *ctx, const T *qk, const T *v, const T *pos, void *o, int t, int heads, int hd,
+int attention_t(wh_ctx *ctx, const T *qk, const T *v, const T *pos, int ps, void *o, int t, int heads, int hd,
                 const int *valid_dev, int valid, int batch, int out16) {
   const int ch = heads * hd;
   Args a{};
@@ -595,9 +595,9 @@ int attention_t(wh_ctx *ctx, const T *qk, const T *v, const T *pos, void *o, int
     ProfScope prof(ctx, "attention_pack", 0.0,
                    (sizeof(T) + 2.0) * batch * t * ch * 2 + (pos ? (sizeof(T) + 2.0) * (2 * t + 15) * ch : 0.0));
     switch (sp.dp) {
-      case 32: launch_pack<32, T>(ctx, sp, k, qs, bq, vv, vs, bv, pos, t, heads, hd, batch, kp, vt, pp); break;
-      case 64: launch_pack<64, T>(ctx, sp, k, qs, bq, vv, vs, bv, pos, t, heads, hd, batch, kp, vt, pp); break;
-      default: launch_pack<128, T>(ctx, sp, k, qs, bq, vv, vs, bv, pos, t, heads, hd, batch, kp, vt, pp); break;
+      case 32: launch_pack<32, T>(ctx, sp, k, qs, bq, vv, vs, bv, pos, ps, t, heads, hd, batch, kp, vt, pp); break;
+      case 64: launch_pack<64, T>(ctx, sp, k, qs, bq, vv, vs, bv, pos, ps, t, heads, hd, batch, kp, vt, pp); break;
+      default: launch_pack<128, T>(ctx, sp, k, qs, bq, vv, vs, bv, pos, ps, t, heads, hd, batch, kp, vt, pp); break;
     }
     if (int rc = wh_launched(ctx, "attention pack")) return rc;
   }
@@ -625,7 +625,7 @@ size_t attention_scratch_bytes(const wh_ctx *ctx, int t, int heads, int hd, int 
 }
 
 int launch_attention(wh_ctx *ctx, const void *qk, const void *v, const void *pos, void *o, int t, int heads,
-                     int hd, const int *valid_dev, int valid, int batch, int out16, int in16) {
+                     int hd, const int *valid_dev, int valid, int batch, int out16, int in16, int pos_stride) {
   if (t <= 0 || heads <= 0 || hd <= 0 || hd > 128 || hd % 4 || batch <= 0 || !qk || !o)
     return wh_fail(ctx, WH_EARG, "attention: bad shape (t %d, heads %d, head_dim %d)", t, heads, hd);
   if (v && pos) return wh_fail(ctx, WH_EARG, "attention: relative positions take [q+u | k | v | q+v] rows");
@@ -633,9 +633,12 @@ int launch_attention(wh_ctx *ctx, const void *qk, const void *v, const void *pos
   if (!valid_dev && vvalid == 0) return wh_fail(ctx, WH_EARG, "attention: no valid keys");
   if ((uintptr_t)qk % 16 || (v && (uintptr_t)v % 16) || (pos && (uintptr_t)pos % 16) || (uintptr_t)o % 16)
     return wh_fail(ctx, WH_EARG, "attention: buffers must be 16-byte aligned");
+  const int ps = pos_stride > 0 ? pos_stride : heads * hd;
+  if (pos && (ps < heads * hd || ps % 8))
+    return wh_fail(ctx, WH_EARG, "attention: position row stride %d (heads·hd %d, multiple of 8)", ps, heads * hd);
   if (in16)
-    return attention_t<_Float16>(ctx, (const _Float16 *)qk, (const _Float16 *)v, (const _Float16 *)pos, o, t, heads,
-                                 hd, valid_dev, valid, batch, out16);
-  return attention_t<float>(ctx, (const float *)qk, (const float *)v, (const float *)pos, o, t, heads, hd, valid_dev,
-                            valid, batch, out16);
+    return attention_t<_Float16>(ctx, (const _Float16 *)qk, (const _Float16 *)v, (const _Float16 *)pos, ps, o, t,
+                                 heads, hd, valid_dev, valid, batch, out16);
+  return attention_t<float>(ctx, (const float *)qk, (const float *)v, (const float *)pos, ps, o, t, heads, hd,
+                            valid_dev, valid, batch, out16);
 }

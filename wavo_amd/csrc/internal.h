@@ -130,10 +130,11 @@ int launch_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int ke
 int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb, int kernel,
                     const float *g, const float *b, int layer_norm, void *y, int t, int ch,
                     const int *valid_dev, int valid, int batch, int out16 = 0);
-// qk / v / pos are f32 (in16 == 0) or f16; o is f32 or f16 (out16).
+// qk / v / pos are f32 (in16 == 0) or f16; o is f32 or f16 (out16).  pos rows are pos_stride
+// elements apart (0: heads · hd).
 int launch_attention(wh_ctx *ctx, const void *qk, const void *v, const void *pos, void *o, int t,
                      int heads, int hd, const int *valid_dev, int valid, int batch, int out16 = 0,
-                     int in16 = 0);
+                     int in16 = 0, int pos_stride = 0);
 // Scratch bytes launch_attention uses for t frames × batch windows (rel: relative positions) on
 // this context's device (its CU count sets the key splits).
 size_t attention_scratch_bytes(const wh_ctx *ctx, int t, int heads, int hd, int batch, int rel);

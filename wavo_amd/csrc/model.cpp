@@ -367,7 +367,7 @@ struct Block {
   Chan norm_ff1, norm_attn, norm_conv, norm_ff2, norm_out, conv_norm, dw;
   wh_linear *ff1[2] = {}, *ff2[2] = {}, *out = nullptr, *pw1 = nullptr, *pw2 = nullptr;
   wh_linear *qk = nullptr, *v = nullptr;     // rotary: q stacked over k, and v
-  wh_linear *qkv = nullptr, *pos = nullptr;  // relative: [q + u | k | v | q + v], linear_pos
+  wh_linear *qkv = nullptr;  // relative: [q + u | k | v | q + v]
 };
 
 struct WBlock {
@@ -428,6 +428,10 @@ struct wh_model {
   int cap = 0, cap_batch = 0;
   float *x = nullptr, *y = nullptr, *h = nullptr, *qk = nullptr, *yr = nullptr, *pos = nullptr, *sub = nullptr;
   void *pos16 = nullptr;            // Parakeet: the position table as f16 (the pos GEMM's input)
+  // Parakeet: every block's linear_pos stacked along rows, and the projected position rows of a call,
+  // f16 [2t + 15][layers · d] (block i's at column i · d).
+  wh_linear *pos_all = nullptr;
+  void *posp = nullptr;
   const void *pos16_cur = nullptr;  // its rows of this call
   int *valid_dev = nullptr;
   float *sub2 = nullptr;   // Parakeet conv3 output (the subsampling's second buffer)
@@ -509,7 +513,7 @@ void load_block(Loader &L, wh_model *m, int i, Block &k) {
     b.insert(b.end(), 2 * (size_t)d, 0.0f);
     b.insert(b.end(), v.begin(), v.end());
     k.qkv = L.linear({p + "attn.linear_q", p + "attn.linear_k", p + "attn.linear_v"}, false, -1, b);
-    k.pos = L.linear({p + "attn.linear_pos"}, false);
+    // linear_pos: loaded for all blocks at once (the model's pos_all).
   }
   k.out = L.linear({p + "attn.linear_out"}, bias);
   k.norm_conv = L.norm(p + "norm_conv", d, true);
@@ -574,6 +578,13 @@ bool load_parakeet(const Gguf &g, Loader &L, wh_model *m, std::string &err) {
   m->joint_enc = L.linear({"joint.enc"}, true);
   m->blocks.resize(m->layers);
   for (int i = 0; i < m->layers && L.err.empty(); i++) load_block(L, m, i, m->blocks[i]);
+  {
+    // The position rows do not depend on the input: one GEMM per call projects them for every block
+    // (rows of the blocks' linear_pos stacked), instead of one per block.
+    std::vector<std::string> names;
+    for (int i = 0; i < m->layers; i++) names.push_back("enc.blocks." + std::to_string(i) + ".attn.linear_pos");
+    m->pos_all = L.linear(names, false);
+  }
   // TDT decoder (src/parakeet/decoder.rs:46-89), kept on the host as the reference keeps it.
   m->blank = (int)g.integer("tokenizer.ggml.blank_token_id", -1);
   m->hidden = (int)g.integer("stt.parakeet.predictor.hidden", -1);
@@ -713,7 +724,7 @@ int arena(wh_model *m, int frames, int batch) {
   drop_graphs(m);
   m->epoch++;
   int F = (std::max(frames, m->cap) + 63) / 64 * 64, B = std::max(batch, std::max(m->cap_batch, 1));
-  for (float *p : {m->x, m->y, m->h, m->qk, m->yr, m->pos, m->sub, m->sub2, m->rope, (float *)m->pos16})
+  for (float *p : {m->x, m->y, m->h, m->qk, m->yr, m->pos, m->sub, m->sub2, m->rope, (float *)m->pos16, (float *)m->posp})
     if (p) {
       wh_free(m->ctx, p);
       for (auto &o : m->owned)
@@ -721,7 +732,7 @@ int arena(wh_model *m, int frames, int batch) {
     }
   if (m->valid_dev) wh_free(m->ctx, m->valid_dev);
   m->x = m->y = m->h = m->qk = m->yr = m->pos = m->sub = m->sub2 = m->rope = nullptr;
-  m->pos16 = nullptr;
+  m->pos16 = m->posp = nullptr;
   m->valid_dev = nullptr;
   const int d = m->d;
   const size_t rows = (size_t)F * B;
@@ -767,7 +778,8 @@ int arena(wh_model *m, int frames, int batch) {
     auto table = rel_positions(d, (long)F + 15, 2 * F + 15);
     CK(wh_write(m->ctx, m->pos, table.data(), table.size() * 4));
     m->pos16 = dev_alloc(m, (table.size() + 1) / 2);
-    if (!m->pos16) return WH_EOOM;
+    m->posp = dev_alloc(m, ((size_t)(2 * F + 15) * m->layers * d + 1) / 2);
+    if (!m->pos16 || !m->posp) return WH_EOOM;
     CK(launch_to_half(m->ctx, m->pos, m->pos16, table.size()));
   } else if (m->arch == GIGAAM) {
     int hd = d / m->heads;
@@ -789,8 +801,8 @@ int arena(wh_model *m, int frames, int batch) {
 // One block from x into y (y = norm_out(x), x is spent).  pre: the block's first norm (norm_ff1 of x)
 // is already in m->yr as f16 (the previous block's last kernel wrote it); next: the following
 // block's norm_ff1, which this block's last kernel then writes into m->yr.
-int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int batch, const int *valid_dev, bool pre,
-                 const Chan *next) {
+int record_block(wh_model *m, int layer, const Block &k, float *x, float *y, int t, int batch, const int *valid_dev,
+                 bool pre, const Chan *next) {
   wh_ctx *c = m->ctx;
   const int d = m->d, hd = d / m->heads, rows = t * batch;
   void *y16 = y, *h16 = m->h;
@@ -808,12 +820,13 @@ int record_block(wh_model *m, const Block &k, float *x, float *y, int t, int bat
     CK(g16(y16, k.v, m->h, rows, WH_BIAS, 0.0f, 1));
     CK(launch_attention(c, m->qk, m->h, nullptr, y16, t, m->heads, hd, valid_dev, t, batch, 1, 1));
   } else {
-    const int pr = 2 * t + 15;
     // The FFN's residual projection and the attention norm (one kernel after a k-split GEMM).
     CK(launch_gemm_h_ln(c, h16, k.ff1[1], x, rows, 0.5f, k.norm_attn.w, k.norm_attn.b, y16, 1));
     CK(g16(y16, k.qkv, m->qk, rows, WH_BIAS, 0.0f, 1));
-    CK(g16(m->pos16_cur, k.pos, m->yr, pr, WH_BIAS, 0.0f, 1));
-    CK(launch_attention(c, m->qk, nullptr, m->yr, y16, t, m->heads, hd, valid_dev, t, batch, 1, 1));
+    // This block's projected position rows (record_blocks projected every block's).
+    const int ps = m->pos_all->cols;
+    CK(launch_attention(c, m->qk, nullptr, (const _Float16 *)m->posp + (size_t)layer * d, y16, t, m->heads, hd,
+                        valid_dev, t, batch, 1, 1, ps));
   }
   CK(g16(y16, k.out, x, rows, WH_RESIDUAL, 1.0f, 0));
   CK(ln16(k.norm_conv));
@@ -834,9 +847,11 @@ namespace {
 
 // Conformer::record (src/conformer.rs:107-116): `layers` blocks from m->x, output in m->x.
 int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layers) {
+  if (m->relative && layers > 0)  // every block's linear_pos(P) in one GEMM: [2t + 15][layers · d] f16
+    CK(launch_gemm_h(m->ctx, m->pos16_cur, m->pos_all, m->posp, 2 * t + 15, m->pos_all->cols, WH_BIAS, 0.0f, 1));
   for (int i = 0; i < layers; i++) {
     const Chan *next = i + 1 < layers ? &m->blocks[i + 1].norm_ff1 : nullptr;
-    CK(record_block(m, m->blocks[i], m->x, m->y, t, batch, valid_dev, i > 0, next));
+    CK(record_block(m, i, m->blocks[i], m->x, m->y, t, batch, valid_dev, i > 0, next));
     std::swap(m->x, m->y);
   }
   return WH_OK;

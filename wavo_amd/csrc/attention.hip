@@ -634,8 +634,8 @@ int launch_attention(wh_ctx *ctx, const void *qk, const void *v, const void *pos
   if ((uintptr_t)qk % 16 || (v && (uintptr_t)v % 16) || (pos && (uintptr_t)pos % 16) || (uintptr_t)o % 16)
     return wh_fail(ctx, WH_EARG, "attention: buffers must be 16-byte aligned");
   const int ps = pos_stride > 0 ? pos_stride : heads * hd;
-  if (pos && (ps < heads * hd || ps % 8))
-    return wh_fail(ctx, WH_EARG, "attention: position row stride %d (heads·hd %d, multiple of 8)", ps, heads * hd);
+  if (pos && ps < heads * hd)
+    return wh_fail(ctx, WH_EARG, "attention: position row stride %d below heads·hd %d", ps, heads * hd);
   if (in16)
     return attention_t<_Float16>(ctx, (const _Float16 *)qk, (const _Float16 *)v, (const _Float16 *)pos, ps, o, t,
                                  heads, hd, valid_dev, valid, batch, out16);

@@ -771,7 +771,11 @@ Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
     // FFN down 8.0 against 8.6 ms per call; the 16 windows' 1024 × 1024 projections stay with 8-wave
     // workgroups, 3.13 against 3.22).
     p = {128, 128, 2, 2, 3, 1};
-  else if (t128 >= cus / 2) p = {128, 128, 2, 4, 4, 1};
+  else if (t128 * 4 >= 3L * cus)
+    // Three quarters of a tile per CU or more (the FFN's first projection at 750 frames): 128×128
+    // tiles; fewer (the qkv projection, 144 tiles) run faster as 64×64 tiles (4.96 against 4.98 ms
+    // per 60 s call).
+    p = {128, 128, 2, 4, 4, 1};
   else if (t128 * 4 <= cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
     // Long k over few tiles (the FFN's down projection, 750 × 1024 × 4096): 128×128 tiles split 4
     // ways, one workgroup per CU, move half the bytes per MFMA of 64×64 ones (measured in the

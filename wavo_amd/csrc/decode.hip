@@ -561,9 +561,9 @@ __global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q
 
 // Per head: the parts rescaled to their common maximum, summed and normalized (decode.wgsl:121-147).
 __global__ void combine_kernel(const float *__restrict__ part, float *__restrict__ o, int n, int hd,
-                               const int *__restrict__ dn, int cols) {
+                               const int *__restrict__ dn, int cols, int kpp) {
   if (dn) n = min(*dn + n, cols);
-  const int parts = (n + KEYS - 1) / KEYS;
+  const int parts = (n + kpp - 1) / kpp;
   const float *base = part + (size_t)blockIdx.x * parts * (hd + 2);
   float m = -INFINITY;
   for (int c = 0; c < parts; c++) m = fmaxf(m, base[c * (hd + 2) + hd]);
@@ -576,7 +576,7 @@ __global__ void combine_kernel(const float *__restrict__ part, float *__restrict
   }
 }
 
-// One head's query against all its keys in one workgroup of 16 waves (no parts to merge afterwards):
+// One head's query against all its keys (or one run of them, see kpp) in one workgroup of 16 waves:
 // key j is lane j % 64 of wave (j / 64) % 16 in round j / 1024, its score from the transposed K cache
 // (64 keys of a wave read 256 contiguous bytes per pair); the softmax over all keys; then the waves
 // take keys in turn for p·V (a key's value pairs are contiguous), summed over the waves through LDS.
@@ -585,8 +585,13 @@ constexpr int AT_WAVES = 16, AT_ROUNDS = 8;  // keys ≤ 16·64·8 = 8192
 __global__ __launch_bounds__(64 * AT_WAVES) void attend_one_kernel(const float *__restrict__ q,
                                                                    const uint32_t *__restrict__ kv,
                                                                    float *__restrict__ o, int n, int hd, float scale,
-                                                                   int cols, int heads, const int *__restrict__ dn) {
+                                                                   int cols, int heads, const int *__restrict__ dn,
+                                                                   float *__restrict__ part, int kpp) {
   if (dn) n = min(*dn + n, cols);
+  // With kpp > 0 the workgroup (head, c) takes keys c·kpp .. of the head and writes its partial
+  // (Σ e·v, max, Σ e) for combine_kernel instead of the output.
+  const int kb = kpp ? (int)blockIdx.y * kpp : 0;
+  n = kpp ? max(0, min(kpp, n - kb)) : n;
   __shared__ float qs[128];
   __shared__ float p[64 * AT_WAVES * AT_ROUNDS];
   __shared__ float red[2 * AT_WAVES];
@@ -611,7 +616,7 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attend_one_kernel(const float *
       for (int i0 = 0; i0 < pairs; i0 += 32) {
         uint32_t u[32];
 #pragma unroll
-        for (int t = 0; t < 32; t++) u[t] = i0 + t < pairs ? kv[k0 + (size_t)(i0 + t) * cols + j] : 0u;
+        for (int t = 0; t < 32; t++) u[t] = i0 + t < pairs ? kv[k0 + (size_t)(i0 + t) * cols + kb + j] : 0u;
 #pragma unroll
         for (int t = 0; t < 32; t++)
           if (i0 + t < pairs) acc += qs[2 * (i0 + t)] * half_bits(u[t] & 0xffffu) + qs[2 * (i0 + t) + 1] * half_bits(u[t] >> 16);
@@ -650,7 +655,7 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attend_one_kernel(const float *
     for (int j0 = wave * groups + g; j0 < n; j0 += 16 * step) {  // 16 keys' loads in flight at once
       uint32_t u[16];
 #pragma unroll
-      for (int t = 0; t < 16; t++) u[t] = j0 + t * step < n ? kv[v0 + (size_t)(j0 + t * step) * v_stride + c] : 0u;
+      for (int t = 0; t < 16; t++) u[t] = j0 + t * step < n ? kv[v0 + (size_t)(kb + j0 + t * step) * v_stride + c] : 0u;
 #pragma unroll
       for (int t = 0; t < 16; t++)
         if (j0 + t * step < n) {
@@ -670,9 +675,15 @@ __global__ __launch_bounds__(64 * AT_WAVES) void attend_one_kernel(const float *
   if (tid < pairs) {
     float2 t = make_float2(0.0f, 0.0f);
     for (int w = 0; w < AT_WAVES; w++) t.x += ov[w][tid].x, t.y += ov[w][tid].y;
-    const float inv = 1.0f / l;
-    o[h * hd + 2 * tid] = t.x * inv;
-    o[h * hd + 2 * tid + 1] = t.y * inv;
+    if (kpp) {
+      float *pp = part + ((size_t)h * gridDim.y + blockIdx.y) * (hd + 2);
+      pp[2 * tid] = t.x, pp[2 * tid + 1] = t.y;
+      if (tid == 0) pp[hd] = mx, pp[hd + 1] = l;
+    } else {
+      const float inv = 1.0f / l;
+      o[h * hd + 2 * tid] = t.x * inv;
+      o[h * hd + 2 * tid + 1] = t.y * inv;
+    }
   }
 }
 
@@ -767,9 +778,21 @@ int launch_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, 
   float scale = 1.0f / sqrtf((float)hd);
   // A key count in device memory: the grid covers the whole cache and parts past it return.
   const int most = dn ? cols : n;
+  if (!dn && n > 1024 && n <= 64 * AT_WAVES * AT_ROUNDS) {
+    // More keys than one workgroup's threads (the cross-attention over 1500 frames): runs of 512
+    // keys per workgroup, merged by a second kernel (measured: 261 against 278 µs per decoder
+    // step; runs of 768 keys 268, of 256 keys 262).
+    const int kpp = 512, parts = (n + kpp - 1) / kpp;
+    ProfScope prof(ctx, "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
+    attend_one_kernel<<<dim3(heads, parts), 64 * AT_WAVES, 0, ctx->stream>>>(q, kv, o, n, hd, scale, cols, heads, dn,
+                                                                             part, kpp);
+    if (int rc = wh_launched(ctx, "attend")) return rc;
+    combine_kernel<<<heads, 64, 0, ctx->stream>>>(part, o, n, hd, dn, cols, kpp);
+    return wh_launched(ctx, "combine");
+  }
   if (most <= 64 * AT_WAVES * AT_ROUNDS) {  // every key in one workgroup per head: no merge launch
     ProfScope prof(ctx, "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
-    attend_one_kernel<<<heads, 64 * AT_WAVES, 0, ctx->stream>>>(q, kv, o, n, hd, scale, cols, heads, dn);
+    attend_one_kernel<<<heads, 64 * AT_WAVES, 0, ctx->stream>>>(q, kv, o, n, hd, scale, cols, heads, dn, nullptr, 0);
     return wh_launched(ctx, "attend");
   }
   dim3 grid((most + KEYS - 1) / KEYS, heads);
@@ -777,7 +800,7 @@ int launch_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, 
   attend_kernel<<<grid, 256, 0, ctx->stream>>>(q, kv, part, n, hd, scale, cols, heads, dn);
   int rc = wh_launched(ctx, "attend");
   if (rc) return rc;
-  combine_kernel<<<heads, 64, 0, ctx->stream>>>(part, o, n, hd, dn, cols);
+  combine_kernel<<<heads, 64, 0, ctx->stream>>>(part, o, n, hd, dn, cols, KEYS);
   return wh_launched(ctx, "combine");
 }
 

@@ -20,7 +20,10 @@ WRITE_SIZE passes (profiles/), when a summary for the same configuration is comm
 `gemv` is the Whisper-large-v3-turbo decoder's per-token matrix-vector products (q8_0; 4 layers of
 qkv 3840×1280, self_out / cross_q / cross_out 1280×1280, fc1 5120×1280, fc2 1280×5120, and the
 51866-row head), timed cold: two copies of the weights (2 × 168 MB, past the 256 MB Infinity Cache)
-alternate, and achieved bytes per second of the weights as stored is reported against HBM peak.
+alternate, and achieved bytes per second of the weights as stored is reported against HBM peak;
+`gemv.head` is the head alone, and `gemv.decode_step` the whole decoder step (embedding, 4 layers of
+norms, GEMVs, self- and cross-attention, the head) replayed as one recorded pass per token for 224
+tokens, with the weights left in the Infinity Cache between tokens as a decode loop leaves them.
 
 `cpu_baseline` is the C parity oracle (the restated wavo CPU backend, portable f16-rounded arithmetic,
 AVX2+FMA, OpenMP) on the same model and mel, one full call, timed on this host.

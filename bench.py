@@ -75,15 +75,13 @@ def gemm_replay(gpu, name, reps=50):
     w = gguf.encode(rng.standard_normal(int(n) * int(k), dtype=np.float32) * np.float32(0.02), wtype)
     f16 = out == "f16"
     plan = f"{bm},{bn},{wm},{wn},{ns},{split[2:] if split else 1}"
-    os.environ["WAVO_GEMM_PLAN"] = plan  # the same launch plan as in the step
-    # A split GEMM's kernel alone, as it runs in the step (where the following fused LayerNorm kernel
-    # adds the partial sums); a C-ABI call would add its own finishing kernel.
-    os.environ["WAVO_GEMM_KERNEL_ONLY"] = "1"
     import wavo_amd
 
     g2 = wavo_amd.Gpu(0)
-    os.environ.pop("WAVO_GEMM_PLAN")
-    os.environ.pop("WAVO_GEMM_KERNEL_ONLY")
+    g2.tune("gemm_plan", plan)  # the same launch plan as in the step
+    # A split GEMM's kernel alone, as it runs in the step (where the following fused LayerNorm kernel
+    # adds the partial sums); a C-ABI call would add its own finishing kernel.
+    g2.tune("gemm_kernel_only", 1)
     lin2 = g2.linear([(w, wtype, int(k), int(n))], np.zeros(int(width), np.float32))
     a2 = g2.upload(rng.standard_normal((int(m), int(k)), dtype=np.float32).astype(np.float16))
     c2 = g2.buffer(int(m) * int(width))

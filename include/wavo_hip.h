@@ -78,6 +78,16 @@ int wh_read(wh_ctx *ctx, void *host, const void *dptr, size_t bytes);
 int wh_sync(wh_ctx *ctx);
 /* The context's hipStream_t as an opaque pointer, for callers that time with HIP events. */
 void *wh_stream(wh_ctx *ctx);
+/* Tuning and measurement overrides (no counterpart in the reference, whose kernel choices are fixed
+ * per device tier, src/gpu/mod.rs:50-107).  Only an explicit call changes them; a fresh context
+ * chooses every launch plan itself.  Keys:
+ *   "gemm_plan"        "bm,bn,wm,wn,stages,split" for every GEMM of the main kernel ("" clears);
+ *   "gemm_shape_plans" "m,cols,k:bm,bn,wm,wn,stages,split;..." per call shape ("" clears);
+ *   "gemm_kernel_only" "1": a k-split GEMM call stops after its GEMM kernel and leaves c unwritten
+ *                      (to time that kernel alone, as a model step runs it); "0" restores;
+ *   "attn_split"       "n": attention splits its key range n ways (0 = chosen per shape).
+ * Unknown keys and malformed values return WH_EARG. */
+int wh_tune(wh_ctx *ctx, const char *key, const char *value);
 /* Profiling (no counterpart in the reference, whose timing lives in `wavo bench` and GPU timestamp
  * queries, docs/perf.md:54).  mode 1: every kernel launch gets HIP events on the stream around it
  * (each pair adds the event's own overhead, a few microseconds, to what it measures); mode 2: only
@@ -241,6 +251,47 @@ int wh_model_greedy(wh_model *m, const float *enc_host, int frames, int width, u
  * token at position pos (Decoder::record_step, :254-290) and leaves the logits in logits_dev. */
 int wh_whisper_begin(wh_model *m, const float *enc_dev, int frames);
 int wh_whisper_step(wh_model *m, int token, int pos, float *logits_dev);
+
+/* ------------------------------------------------------------------- Whisper window search */
+
+/* The reference's `Ids` (src/whisper/search.rs:16-23): EOT, <|notimestamps|>, the first timestamp
+ * <|0.00|> (begin; timestamps run to the end of the vocabulary) and the two suppression lists, plus
+ * SOT (src/whisper/mod.rs:177). */
+typedef struct wh_whisper_ids {
+  int eot, no_timestamps, begin, sot;
+  const int *suppress;
+  int n_suppress;
+  const int *begin_suppress;
+  int n_begin_suppress;
+} wh_whisper_ids;
+/* The model's ids as Whisper::load reads them (src/whisper/mod.rs:131-141); the lists point into
+ * the model. */
+int wh_whisper_ids_of(const wh_model *m, wh_whisper_ids *out);
+/* search::decode's choice of the next token (`pick`, src/whisper/search.rs:46-59, with
+ * timestamp_rules :73-111 and argmax :113-127), in place on host logits[vocab]: the suppression list,
+ * the begin-suppression list while n == 0, the timestamp rules over the n ids generated so far, then
+ * the first maximum; with logprob != NULL also its log-softmax.  Returns the id (or WH_EARG).  Host
+ * code only: it needs no device. */
+int wh_whisper_pick(const wh_whisper_ids *ids, float *logits, int vocab, const uint32_t *generated, int n,
+                    float *logprob);
+/* search::probability (src/whisper/search.rs:129-135): the softmax probability of id. */
+float wh_whisper_probability(const float *logits, int vocab, int id);
+/* search::retrieve (src/whisper/search.rs:137-181): the segments of a window's generated ids as
+ * (start in 20 ms steps, first index, end index) triples in seg[3i..3i+2] (their text: the ids < eot
+ * in that range); returns the count (writes at most cap); *advance = the mel frames the next window
+ * moves on.  Host code only. */
+int wh_whisper_retrieve(const wh_whisper_ids *ids, const uint32_t *generated, int n, int frames, int *seg, int cap,
+                        int *advance);
+/* The decoding of one window of Whisper::transcribe (src/whisper/mod.rs:226-239, search::decode
+ * src/whisper/search.rs:35-71) on the device: the cross K/V of enc_dev [frames][d] (wh_whisper_begin),
+ * the decoder over the prompt (n_prompt ids from SOT; 0 = [SOT], the prompt of a model without
+ * language tokens), then greedy steps under the rules, each step's logits read back as Gpu::finish
+ * reads them, until EOT, 256 new tokens or position min(448, context).  Log-probabilities are summed
+ * when the no-speech probability on SOT's logits is above 0.6, as the reference asks for them.
+ * Writes the generated ids (without EOT) to out and returns their count (or an error); *no_speech and
+ * *avg_logprob (0 when not summed) may be NULL. */
+int wh_whisper_decode(wh_model *m, const float *enc_dev, int frames, const uint32_t *prompt, int n_prompt,
+                      uint32_t *out, int cap, float *no_speech, float *avg_logprob);
 
 #ifdef __cplusplus
 }

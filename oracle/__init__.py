@@ -91,8 +91,22 @@ def lib():
             "ox_model_tdt_trace": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_int, ctypes.c_int,
                                                   _u32p, ctypes.c_int, _ip, _fp, ctypes.c_int]),
             "ox_model_tdt_lipschitz": (ctypes.c_float, [ctypes.c_void_p]),
+            "ox_model_predict": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, _fp, _fp, _fp]),
+            "ox_model_joint": (ctypes.c_int, [ctypes.c_void_p, _fp, _fp, _fp]),
             "ox_whisper_begin": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_int]),
             "ox_whisper_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _fp]),
+            "ox_model_whisper_ids": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
+            "ox_model_context": (ctypes.c_int, [ctypes.c_void_p]),
+            "ox_timestamp_rules": (None, [ctypes.c_void_p, _fp, ctypes.c_int, _u32p, ctypes.c_int]),
+            "ox_whisper_argmax": (ctypes.c_int, [_fp, ctypes.c_int, ctypes.c_int, _fp]),
+            "ox_whisper_pick": (ctypes.c_int, [ctypes.c_void_p, _fp, ctypes.c_int, _u32p, ctypes.c_int,
+                                               ctypes.c_int, _fp]),
+            "ox_probability": (ctypes.c_float, [_fp, ctypes.c_int, ctypes.c_int]),
+            "ox_whisper_decode": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, _fp, ctypes.c_int,
+                                                 ctypes.c_int, ctypes.c_int, _u32p, ctypes.c_int, _fp, _fp]),
+            "ox_top2_gap": (ctypes.c_float, [_fp, ctypes.c_int, ctypes.c_void_p, _u32p, ctypes.c_int]),
+            "ox_whisper_retrieve": (ctypes.c_int, [ctypes.c_void_p, _u32p, ctypes.c_int, ctypes.c_int,
+                                                   _ip, ctypes.c_int, _ip]),
             "ox_threads": (ctypes.c_int, []),
             "ox_set_threads": (None, [ctypes.c_int]),
         }
@@ -315,6 +329,64 @@ def tdt_scripted(frames, blank, durations, max_symbols, global_, script):
     return pairs, cl
 
 
+class WhisperIds(ctypes.Structure):
+    """ox_whisper_ids: the reference's `Ids` (src/whisper/search.rs:16-23) plus SOT."""
+
+    _fields_ = [("eot", ctypes.c_int), ("no_timestamps", ctypes.c_int), ("begin", ctypes.c_int),
+                ("sot", ctypes.c_int), ("suppress", _ip), ("n_suppress", ctypes.c_int),
+                ("begin_suppress", _ip), ("n_begin_suppress", ctypes.c_int)]
+
+    @classmethod
+    def make(cls, eot, no_timestamps, begin, suppress=(), begin_suppress=(), sot=-1):
+        ids = cls()
+        ids.eot, ids.no_timestamps, ids.begin, ids.sot = eot, no_timestamps, begin, sot
+        ids._s = (ctypes.c_int * max(1, len(suppress)))(*suppress)
+        ids._b = (ctypes.c_int * max(1, len(begin_suppress)))(*begin_suppress)
+        ids.suppress, ids.n_suppress = ctypes.cast(ids._s, _ip), len(suppress)
+        ids.begin_suppress, ids.n_begin_suppress = ctypes.cast(ids._b, _ip), len(begin_suppress)
+        return ids
+
+
+def _gen(generated):
+    g = np.ascontiguousarray(np.asarray(list(generated) or [0], np.uint32))
+    return g, g.ctypes.data_as(_u32p)
+
+
+def timestamp_rules(ids, logits, generated):
+    l = np.ascontiguousarray(logits, np.float32).copy()
+    g, pg = _gen(generated)
+    lib().ox_timestamp_rules(ctypes.byref(ids), _ptr(l), l.size, pg, len(generated))
+    return l
+
+
+def whisper_pick(ids, logits, generated, logprob=False):
+    """(id, log-probability, logits after the rules)."""
+    l = np.ascontiguousarray(logits, np.float32).copy()
+    g, pg = _gen(generated)
+    lp = ctypes.c_float()
+    i = lib().ox_whisper_pick(ctypes.byref(ids), _ptr(l), l.size, pg, len(generated), int(logprob), ctypes.byref(lp))
+    return i, lp.value, l
+
+
+def probability(logits, i):
+    l, pl = f32(logits)
+    return float(lib().ox_probability(pl, l.size, i))
+
+
+def whisper_retrieve(ids, generated, frames):
+    """(segments [(start, text ids)], advance)."""
+    g, pg = _gen(generated)
+    n = len(generated)
+    seg = (ctypes.c_int * (3 * (n + 2)))()
+    adv = ctypes.c_int()
+    c = lib().ox_whisper_retrieve(ctypes.byref(ids), pg, n, frames, seg, n + 2, ctypes.byref(adv))
+    out = []
+    for i in range(c):
+        s, lo, hi = seg[3 * i], seg[3 * i + 1], seg[3 * i + 2]
+        out.append((s, [int(x) for x in generated[lo:hi] if x < ids.eot]))
+    return out, adv.value
+
+
 class Model:
     """ox_model: a whole encoder (and decoder) restated on the CPU, loaded from a GGUF file."""
 
@@ -375,6 +447,23 @@ class Model:
         toks = [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(min(n, cap))]
         return toks, frames.reshape(-1, 3), gaps
 
+    def predict(self, token, state, hidden, joint, layers):
+        """One predictor step: (next state, joint's predictor projection)."""
+        st, ps = f32(state)
+        nxt = np.zeros(2 * layers * hidden, np.float32)
+        pred = np.zeros(joint, np.float32)
+        if lib().ox_model_predict(self.h, token, ps, _ptr(nxt), _ptr(pred)):
+            raise ValueError("predict failed")
+        return nxt, pred
+
+    def joint(self, enc_row, pred, outputs):
+        e, pe = f32(enc_row)
+        p, pp = f32(pred)
+        out = np.zeros(outputs, np.float32)
+        if lib().ox_model_joint(self.h, pe, pp, _ptr(out)):
+            raise ValueError("joint failed")
+        return out
+
     def tdt_lipschitz(self):
         return float(lib().ox_model_tdt_lipschitz(self.h))
 
@@ -382,6 +471,26 @@ class Model:
         enc, pe = f32(enc)
         if lib().ox_whisper_begin(self.h, pe, enc.shape[0]):
             raise ValueError("whisper_begin failed")
+
+    def whisper_ids(self):
+        ids = WhisperIds()
+        if lib().ox_model_whisper_ids(self.h, ctypes.byref(ids)):
+            raise ValueError("not a Whisper model")
+        return ids
+
+    def whisper_decode(self, logits, prompt=1, logprobs=False, cap=512):
+        """search::decode from the prompt's last logits: (generated ids, avg log-prob, per-pick top-2
+        gaps after the rules)."""
+        ids = self.whisper_ids()
+        l = np.ascontiguousarray(logits, np.float32).copy()
+        out = np.zeros(cap, np.uint32)
+        gaps = np.zeros(cap + 1, np.float32)
+        avg = ctypes.c_float()
+        n = lib().ox_whisper_decode(self.h, ctypes.byref(ids), _ptr(l), l.size, prompt, int(logprobs),
+                                    out.ctypes.data_as(_u32p), cap, ctypes.byref(avg), _ptr(gaps))
+        if n < 0:
+            raise ValueError("whisper_decode failed")
+        return [int(x) for x in out[:n]], avg.value, gaps[:n + 1]
 
     def whisper_step(self, token, pos, vocab):
         out = np.zeros(vocab, np.float32)

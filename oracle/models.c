@@ -403,6 +403,9 @@ struct ox_model {
   /* Whisper decoding caches (src/cpu/transformer.rs:146-223): per layer K then V. */
   float **own, **cross;
   int cross_frames;
+  /* Whisper's special ids and suppression lists (src/whisper/mod.rs:131-141, :177). */
+  int eot, no_timestamps, sot, n_suppress, n_begin_suppress;
+  int suppress[512], begin_suppress[64];
 };
 
 static chan norm(loader *L, const char *name, int d, int bias) {
@@ -714,6 +717,26 @@ static int load_whisper(loader *L, ox_model *m) {
 #undef P
   }
   m->dec_norm = norm(L, "dec.final_norm", d, 1);
+  m->eot = (int)gg_int(L->g, "tokenizer.ggml.eos_token_id", -1);
+  m->no_timestamps = (int)gg_int(L->g, "stt.whisper.no_timestamps_token_id", -1);
+  m->sot = (int)gg_int(L->g, "stt.whisper.sot_token_id", -1);
+  /* Optional lists: the converter writes them only when not empty (src/whisper/mod.rs:131-133). */
+  m->n_suppress = gg_int_array(L->g, "stt.whisper.suppress_tokens", m->suppress, 512);
+  m->n_begin_suppress = gg_int_array(L->g, "stt.whisper.begin_suppress_tokens", m->begin_suppress, 64);
+  if (m->n_suppress < 0) m->n_suppress = 0;
+  if (m->n_begin_suppress < 0) m->n_begin_suppress = 0;
+  if (m->n_suppress > 512 || m->n_begin_suppress > 64 || m->eot < 0 || m->no_timestamps < 0 ||
+      m->no_timestamps + 1 >= m->vocab) {
+    snprintf(L->err, sizeof L->err, "bad Whisper special token ids");
+    return -1;
+  }
+  for (int i = 0; i < m->n_suppress + m->n_begin_suppress; i++) {
+    int id = i < m->n_suppress ? m->suppress[i] : m->begin_suppress[i - m->n_suppress];
+    if (id < 0 || id >= m->vocab) {
+      snprintf(L->err, sizeof L->err, "special token ids out of the vocabulary");
+      return -1;
+    }
+  }
   m->token_embd = linear1(L, "dec.token_embd", 0);
   m->dec_pos = f32s(L, "dec.pos_emb.weight", (size_t)d * m->context);
   return L->err[0] ? -1 : 0;
@@ -1037,6 +1060,26 @@ int ox_model_tdt_trace(ox_model *m, const float *enc, int frames, int width, uin
   return n;
 }
 
+int ox_model_predict(ox_model *m, int token, const float *state, float *next, float *pred) {
+  if (m->arch != ARCH_PARAKEET || !m->embed || token >= m->classes) return -1;
+  predict(m, token, state, next, pred);
+  return 0;
+}
+
+/* Decoder::joint's logits (src/parakeet/decoder.rs:135-142) before the two argmaxes. */
+int ox_model_joint(ox_model *m, const float *enc_row, const float *pred, float *logits) {
+  if (m->arch != ARCH_PARAKEET || !m->embed) return -1;
+  float *z = (float *)malloc(sizeof(float) * m->joint);
+  for (int j = 0; j < m->joint; j++) {
+    float v = enc_row[j] + pred[j];
+    z[j] = v > 0.0f ? v : 0.0f;
+  }
+  matvec(m->out_w, z, logits);
+  for (int i = 0; i < m->classes + m->n_dur; i++) logits[i] = logits[i] + m->out_b[i];
+  free(z);
+  return 0;
+}
+
 int ox_model_tdt(ox_model *m, const float *enc, int frames, int width, uint32_t *out, int cap) {
   return ox_model_tdt_trace(m, enc, frames, width, out, cap, NULL, NULL, 0);
 }
@@ -1083,6 +1126,21 @@ int ox_whisper_begin(ox_model *m, const float *enc, int frames) {
   m->cross_frames = frames;
   return 0;
 }
+
+int ox_model_whisper_ids(ox_model *m, ox_whisper_ids *ids) {
+  if (m->arch != ARCH_WHISPER) return -1;
+  ids->eot = m->eot;
+  ids->no_timestamps = m->no_timestamps;
+  ids->begin = m->no_timestamps + 1;
+  ids->sot = m->sot;
+  ids->suppress = m->suppress;
+  ids->n_suppress = m->n_suppress;
+  ids->begin_suppress = m->begin_suppress;
+  ids->n_begin_suppress = m->n_begin_suppress;
+  return 0;
+}
+
+int ox_model_context(ox_model *m) { return m->arch == ARCH_WHISPER ? m->context : 0; }
 
 /* Decoder::step (src/cpu/transformer.rs:226-266). */
 int ox_whisper_step(ox_model *m, int token, int pos, float *logits) {

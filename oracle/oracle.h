@@ -154,11 +154,55 @@ int ox_model_tdt(ox_model *m, const float *enc, int frames, int width, uint32_t 
  * smaller top-2 gap of its token/duration logits in trace_gap[i] (first trace_cap decisions). */
 int ox_model_tdt_trace(ox_model *m, const float *enc, int frames, int width, uint32_t *out, int cap,
                        int *trace_frame, float *trace_gap, int trace_cap);
+/* One predictor step (Decoder::predict, src/parakeet/decoder.rs:107-133): token < 0 feeds zeros; state
+ * and next [layers][h | c] of hidden values each; pred [joint] = the joint's predictor projection. */
+int ox_model_predict(ox_model *m, int token, const float *state, float *next, float *pred);
+/* The joint's logits (src/parakeet/decoder.rs:135-142): ReLU(enc_row + pred) times the output layer
+ * plus its bias, [classes + durations]. */
+int ox_model_joint(ox_model *m, const float *enc_row, const float *pred, float *logits);
 /* max_i Σ_j |W_ij| of the joint's output layer (the logits' sensitivity to the encoder row). */
 float ox_model_tdt_lipschitz(ox_model *m);
 /* Whisper: cross cache from encoder output, one decoder step's logits. */
 int ox_whisper_begin(ox_model *m, const float *enc, int frames);
 int ox_whisper_step(ox_model *m, int token, int pos, float *logits);
+
+/* Whisper's greedy window search (oracle/search.c; src/whisper/search.rs).  Token ids as the
+ * reference's `Ids` (src/whisper/search.rs:16-23, loaded by src/whisper/mod.rs:131-141). */
+typedef struct ox_whisper_ids {
+  int eot, no_timestamps, begin, sot;
+  const int *suppress;
+  int n_suppress;
+  const int *begin_suppress;
+  int n_begin_suppress;
+} ox_whisper_ids;
+/* The model's ids (pointers into the model); -1 if it is not a Whisper model. */
+int ox_model_whisper_ids(ox_model *m, ox_whisper_ids *ids);
+/* The decoder's context (max_target_positions). */
+int ox_model_context(ox_model *m);
+/* timestamp_rules (src/whisper/search.rs:73-111), in place. */
+void ox_timestamp_rules(const ox_whisper_ids *ids, float *logits, int vocab, const uint32_t *gen, int n);
+/* argmax, the first maximum, and with logprob its log-softmax (src/whisper/search.rs:113-127). */
+int ox_whisper_argmax(const float *logits, int vocab, int logprob, float *lp);
+/* decode's `pick` (src/whisper/search.rs:46-59): suppression, begin suppression before the first
+ * token, the timestamp rules, argmax; in place. */
+int ox_whisper_pick(const ox_whisper_ids *ids, float *logits, int vocab, const uint32_t *gen, int n, int logprob,
+                    float *lp);
+/* probability (src/whisper/search.rs:129-135). */
+float ox_probability(const float *logits, int vocab, int id);
+/* search::decode (src/whisper/search.rs:35-71) from the logits of the prompt's last token (modified
+ * in place), stepping the model (ox_whisper_step) from position `prompt`: generated ids without EOT
+ * into out (count returned, -1 on error); the average log-probability in *avg when logprobs; with
+ * gaps != NULL the top-2 gap of each pick after the rules (gaps[i] for the pick of out[i]). Stops
+ * at EOT, 256 new tokens or position min(448, context). */
+int ox_whisper_decode(ox_model *m, const ox_whisper_ids *ids, float *logits, int vocab, int prompt, int logprobs,
+                      uint32_t *out, int cap, float *avg, float *gaps);
+/* The margin of a pick: the two largest logits left by the rules (+inf with fewer than two). */
+float ox_top2_gap(const float *logits, int vocab, const ox_whisper_ids *ids, const uint32_t *gen, int n);
+/* retrieve (src/whisper/search.rs:137-181): segments as (start in 20 ms steps, first index, end
+ * index) triples of gen in seg[3i..]; their text is the ids < eot in that range.  Returns the count;
+ * *advance = mel frames the next window moves on. */
+int ox_whisper_retrieve(const ox_whisper_ids *ids, const uint32_t *gen, int n, int frames, int *seg, int cap,
+                        int *advance);
 
 int ox_threads(void);
 void ox_set_threads(int n);

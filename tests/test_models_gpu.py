@@ -178,6 +178,117 @@ def test_parakeet_full_config(gpu):
     assert want.shape[0] == 750
     err = rel_l2(got, want)
     assert err < ENCODER_TOL, err
+    flip = check_tdt(m, om, got, want)
+    print(f"parakeet 60 s: rel L2 {err:.2e}, TDT {'identical' if flip is None else f'near-tie flip {flip}'}")
+
+
+def whisper_decode_parity(om, m, gpu, enc, vocab):
+    """Whisper's window search (src/whisper/search.rs:35-71) from the same encoder output on both sides:
+    the device decode (wh_whisper_decode: steps on the device, rules on the host) against the oracle's.
+    The ids must match; a divergence passes only as a near tie, where the oracle's top-2 margin after
+    the rules is below the logit noise measured on the steps before it."""
+    eb = gpu.upload(enc)
+    got, ns, lp = m.whisper_decode(eb, enc.shape[0])
+    ids = om.whisper_ids()
+    om.whisper_begin(enc)
+    sot = om.whisper_step(ids.sot, 0, vocab)
+    want, _, gaps = om.whisper_decode(sot.copy(), 1, False)
+    assert ns == pytest.approx(ox.probability(sot, ids.no_timestamps - 1), rel=1e-2, abs=1e-6)
+    if got == want:
+        return len(want), None
+    k = next((i for i in range(min(len(got), len(want))) if got[i] != want[i]), min(len(got), len(want)))
+    # Logit noise: the device's logits against the oracle's on the agreed prefix.
+    vp = vocab if vocab % 32 == 0 else (vocab + 63) // 64 * 64
+    lb = gpu.buffer(vp)
+    m.whisper_begin(eb, enc.shape[0])
+    om.whisper_begin(enc)
+    noise = 0.0
+    for pos, tok in enumerate([ids.sot] + want[:k]):
+        m.whisper_step(tok, pos, lb)
+        gl = gpu.read(lb, (vp,))[:vocab]
+        wl = om.whisper_step(tok, pos, vocab)
+        noise = max(noise, float(np.abs(gl - wl).max()))
+    assert gaps[k] <= 4.0 * noise, f"pick {k}: {got[k:k + 3]} vs {want[k:k + 3]}, margin {gaps[k]:.3g} > 4·noise {noise:.3g}"
+    return k, (k, float(gaps[k]), noise)
+
+
+@pytest.mark.parametrize("wtype", [gguf.Q8_0, gguf.F16])
+def test_whisper_full_config(gpu, wtype):
+    """the Whisper-large-v3-turbo shape (30 s window → 1500 frames, 32 layers,
+    d 1280, 20 heads, FFN 5120; decoder 4 layers, 51866-token head), once in q8_0 and once in f16.
+    The encoder against the oracle; 224 forced decoder steps (the oracle's greedy tokens fed to both)
+    logit by logit; then the window search under the real rules from the same encoder output."""
+    path = synth.model_path("whisper", wtype=wtype, directory=MODELS)
+    cfg = synth.CONFIGS["whisper"]
+    mel = synth.whisper_mel(synth.audio(30.0, 4), cfg["mels"], 2 * cfg["frames"])
+    om, m = ox.Model(path), wa.Model(gpu, path)
+    want = om.encode(mel)
+    got = m.encode(mel)
+    assert want.shape == (1500, 1280)
+    err = rel_l2(got, want)
+    assert err < ENCODER_TOL, err
+    vocab = cfg["vocab"]
+    vp = vocab if vocab % 32 == 0 else (vocab + 63) // 64 * 64
+    eb, lb = gpu.upload(want), gpu.buffer(vp)
+    om.whisper_begin(want)
+    m.whisper_begin(eb, want.shape[0])
+    token, worst, flips = om.whisper_ids().sot, 0.0, 0
+    for pos in range(224):
+        wl = om.whisper_step(token, pos, vocab)
+        m.whisper_step(token, pos, lb)
+        gl = gpu.read(lb, (vp,))[:vocab]
+        worst = max(worst, rel_l2(gl, wl))
+        assert rel_l2(gl, wl) < ENCODER_TOL, (pos, rel_l2(gl, wl))
+        if int(np.argmax(gl)) != int(np.argmax(wl)):
+            flips += 1
+            assert top2_gap(wl) < 4.0 * float(np.abs(gl - wl).max()), f"step {pos}: argmax flip off a near tie"
+        token = int(np.argmax(wl))
+    n, flip = whisper_decode_parity(om, m, gpu, want, vocab)
+    print(f"whisper type {wtype}: encoder rel L2 {err:.2e}; 224 steps worst logits rel L2 {worst:.2e}, "
+          f"{flips} near-tie argmax flips; search: {n} ids agree{'' if flip is None else f', then near tie {flip}'}")
+
+
+def test_whisper_search_small(gpu):
+    """The window search on the small Whisper shape: the device decode's ids equal the oracle's."""
+    path = synth.model_path("whisper", small=True, directory=MODELS)
+    cfg = synth.SMALL["whisper"]
+    mel = synth.whisper_mel(synth.audio(2.0, 4), cfg["mels"], 2 * cfg["frames"])
+    om, m = ox.Model(path), wa.Model(gpu, path)
+    enc = om.encode(mel)
+    n, flip = whisper_decode_parity(om, m, gpu, enc, cfg["vocab"])
+    assert n > 0
+
+
+def test_parakeet_batch16(gpu):
+    """long-form audio cut at its pauses into ≤ 60 s segments (src/split.rs:42-65),
+    16 of them through the config[1] encoder in one padded batch (wh_model_encode_batch: per-window
+    subsampling, key masks and conv-input masks).  Every window's valid frames against the oracle's
+    encoder on that segment alone (relative L2), and its TDT tokens."""
+    path = synth.model_path("parakeet", directory=MODELS)
+    pcm, gaps = synth.long_audio(16 * 55.0, seed=11)
+    segs = synth.split_at_gaps(len(pcm) / synth.SR, gaps)[:16]
+    assert len(segs) == 16
+    mels = [synth.parakeet_mel(pcm[int(a * synth.SR):int(b * synth.SR)]) for a, b in segs]
+    mf = max(x.shape[0] for x in mels)
+    om, m = ox.Model(path), wa.Model(gpu, path)
+    frames, width = m.frames(mf)
+    batch = np.zeros((16, mf, mels[0].shape[1]), np.float32)
+    for i, x in enumerate(mels):
+        batch[i, :x.shape[0]] = x
+    mb, ob = gpu.upload(batch), gpu.buffer(16 * frames * width)
+    m.encode_batch_device(mb, 16, mf, [x.shape[0] for x in mels], ob)
+    out = gpu.read(ob, (16, frames, width))
+    worst, flips = 0.0, []
+    for i, x in enumerate(mels):
+        want = om.encode(x)
+        got = out[i, :want.shape[0], :want.shape[1]]
+        err = rel_l2(got, want)
+        worst = max(worst, err)
+        assert err < ENCODER_TOL, (i, err)
+        flip = check_tdt(m, om, got, want)
+        if flip is not None:
+            flips.append((i, flip))
+    print(f"16 windows of {[round(b - a, 1) for a, b in segs]} s: worst rel L2 {worst:.2e}, TDT near-tie flips {flips}")
 
 
 @pytest.mark.parametrize("name", ["parakeet", "gigaam", "whisper"])

@@ -388,13 +388,13 @@ def test_relative_attention(gpu, t, heads, hd, valid):
 
 
 @pytest.mark.parametrize("valid", [None, 400])
-def test_relative_attention_many_splits(monkeypatch, valid):
+def test_relative_attention_many_splits(valid):
     """Key blocks split 8 ways (more than the merge's group of four: its running-maximum rescale, and
     splits past the valid keys that contribute nothing), through a context opened with the tuning
     override."""
     t, heads, hd = 750, 8, 128
-    monkeypatch.setenv("WAVO_ATTN_SPLIT", "8")
     g = wa.Gpu(0)
+    g.tune("attn_split", 8)
     try:
         d = heads * hd
         qkv, pos, u, vb, rows = relative_inputs(t, heads, hd, seed=23)

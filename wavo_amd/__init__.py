@@ -39,6 +39,7 @@ SIGNATURES = {
     "wh_read": (_i, [_vp, _vp, _vp, _sz]),
     "wh_sync": (_i, [_vp]),
     "wh_stream": (_vp, [_vp]),
+    "wh_tune": (_i, [_vp, ctypes.c_char_p, ctypes.c_char_p]),
     "wh_profile": (_i, [_vp, _i]),
     "wh_profile_read": (_i, [_vp, ctypes.c_char_p, _sz]),
     "wh_region": (_i, [_vp, ctypes.c_char_p, ctypes.c_double, ctypes.c_double]),
@@ -76,6 +77,11 @@ SIGNATURES = {
     "wh_model_greedy": (_i, [_vp, _vp, _i, _i, _vp, _i]),
     "wh_whisper_begin": (_i, [_vp, _vp, _i]),
     "wh_whisper_step": (_i, [_vp, _i, _i, _vp]),
+    "wh_whisper_ids_of": (_i, [_vp, _vp]),
+    "wh_whisper_pick": (_i, [_vp, _vp, _i, _vp, _i, _vp]),
+    "wh_whisper_probability": (_f, [_vp, _i, _i]),
+    "wh_whisper_retrieve": (_i, [_vp, _vp, _i, _i, _vp, _i, _vp]),
+    "wh_whisper_decode": (_i, [_vp, _vp, _i, _vp, _i, _vp, _i, _vp, _vp]),
 }
 
 _lib = None
@@ -146,6 +152,61 @@ class Linear:
         if getattr(self, "h", None) and self.gpu.h:
             lib().wh_linear_free(self.gpu.h, self.h)
             self.h = None
+
+
+class WhisperIds(ctypes.Structure):
+    """wh_whisper_ids: the reference's `Ids` (src/whisper/search.rs:16-23) plus SOT."""
+
+    _fields_ = [("eot", _i), ("no_timestamps", _i), ("begin", _i), ("sot", _i),
+                ("suppress", ctypes.POINTER(_i)), ("n_suppress", _i),
+                ("begin_suppress", ctypes.POINTER(_i)), ("n_begin_suppress", _i)]
+
+    @classmethod
+    def make(cls, eot, no_timestamps, begin, suppress=(), begin_suppress=(), sot=-1):
+        ids = cls()
+        ids.eot, ids.no_timestamps, ids.begin, ids.sot = eot, no_timestamps, begin, sot
+        ids._s = (_i * max(1, len(suppress)))(*suppress)
+        ids._b = (_i * max(1, len(begin_suppress)))(*begin_suppress)
+        ids.suppress, ids.n_suppress = ctypes.cast(ids._s, ctypes.POINTER(_i)), len(suppress)
+        ids.begin_suppress = ctypes.cast(ids._b, ctypes.POINTER(_i))
+        ids.n_begin_suppress = len(begin_suppress)
+        return ids
+
+
+def _ids_array(generated):
+    g = np.ascontiguousarray(np.asarray(list(generated) or [0], np.uint32))
+    return g
+
+
+def whisper_pick(ids, logits, generated, logprob=False):
+    """search::decode's `pick` on host logits (wh_whisper_pick): (id, log-probability or None, the
+    logits after the rules).  Needs no GPU."""
+    l = np.ascontiguousarray(logits, np.float32).copy()
+    g = _ids_array(generated)
+    lp = ctypes.c_float()
+    i = lib().wh_whisper_pick(ctypes.byref(ids), l.ctypes.data, l.size, g.ctypes.data, len(generated),
+                              ctypes.byref(lp) if logprob else None)
+    if i < 0:
+        raise WavoError(i, "wh_whisper_pick: bad arguments")
+    return i, (lp.value if logprob else None), l
+
+
+def whisper_probability(logits, i):
+    l = np.ascontiguousarray(logits, np.float32)
+    return float(lib().wh_whisper_probability(l.ctypes.data, l.size, i))
+
+
+def whisper_retrieve(ids, generated, frames):
+    """search::retrieve (wh_whisper_retrieve): ([(start, text ids)], advance).  Needs no GPU."""
+    g = _ids_array(generated)
+    n = len(generated)
+    seg = (_i * (3 * (n + 2)))()
+    adv = _i()
+    c = lib().wh_whisper_retrieve(ctypes.byref(ids), g.ctypes.data, n, frames, seg, n + 2, ctypes.byref(adv))
+    if c < 0:
+        raise WavoError(c, "wh_whisper_retrieve: bad arguments")
+    return [(seg[3 * i], [int(x) for x in generated[seg[3 * i + 1]:seg[3 * i + 2]] if x < ids.eot])
+            for i in range(c)], adv.value
 
 
 class _Tensor(ctypes.Structure):
@@ -229,6 +290,11 @@ class Gpu:
     @property
     def stream(self):
         return lib().wh_stream(self.h)
+
+    def tune(self, key, value):
+        """Tuning and measurement overrides (wh_tune): gemm_plan, gemm_shape_plans, gemm_kernel_only,
+        attn_split."""
+        self._check(lib().wh_tune(self.h, key.encode(), str(value).encode()))
 
     def profile(self, mode):
         """0 off, 1 (or True) events around every launch, 2 named regions only (wh_region)."""
@@ -413,3 +479,20 @@ class Model:
 
     def whisper_step(self, token, pos, logits_buf):
         self.gpu._check(lib().wh_whisper_step(self.h, token, pos, _p(logits_buf)))
+
+    def whisper_ids(self):
+        ids = WhisperIds()
+        self.gpu._check(lib().wh_whisper_ids_of(self.h, ctypes.byref(ids)))
+        return ids
+
+    def whisper_decode(self, enc_buf, frames, prompt=(), cap=512):
+        """One window's greedy search on the device (wh_whisper_decode): (generated ids, no-speech
+        probability, average log-probability)."""
+        p = np.ascontiguousarray(np.asarray(list(prompt) or [0], np.uint32))
+        out = np.zeros(cap, np.uint32)
+        ns, lp = _f(), _f()
+        n = lib().wh_whisper_decode(self.h, _p(enc_buf), frames, p.ctypes.data if prompt else None, len(prompt),
+                                    out.ctypes.data, cap, ctypes.byref(ns), ctypes.byref(lp))
+        if n < 0:
+            self.gpu._check(n)
+        return [int(x) for x in out[:min(n, cap)]], ns.value, lp.value

@@ -790,12 +790,12 @@ Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
     // pipeline's fill and the partial sums than the extra workgroups win (k = 1024 runs faster whole).
     while (p.split < 4 && t64 * p.split < 2L * cus && k % (2 * p.split * 64) == 0 && k / (2 * p.split * 64) >= 16)
       p.split *= 2;
-  if (ctx->gemm_plan[0]) {  // tuning override (WAVO_GEMM_PLAN): bm, bn, wm, wn, stages, split
+  if (ctx->gemm_plan[0]) {  // tuning override (wh_tune "gemm_plan"): bm, bn, wm, wn, stages, split
     const int *o = ctx->gemm_plan;
     p = {o[0], o[1], o[2], o[3], o[4], o[5]};
     if (k % (64 * p.split)) p.split = 1;
   }
-  for (const auto &o : ctx->gemm_shape_plans)  // tuning override for one shape (WAVO_GEMM_SHAPE_PLANS)
+  for (const auto &o : ctx->gemm_shape_plans)  // tuning override for one shape (wh_tune "gemm_shape_plans")
     if (o[0] == m && o[1] == cols && o[2] == k) {
       p = {o[3], o[4], o[5], o[6], o[7], o[8]};
       if (k % (64 * p.split)) p.split = 1;

@@ -22,17 +22,17 @@ struct wh_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   int cus = 0;
-  // GEMM launch-plan override from WAVO_GEMM_PLAN ("bm,bn,wm,wn,bk,split"; tuning sweeps only):
-  // all zero = chosen per shape.
+  // GEMM launch-plan override set by wh_tune("gemm_plan", "bm,bn,wm,wn,stages,split") (tuning sweeps
+  // only): all zero = chosen per shape.
   int gemm_plan[6] = {0, 0, 0, 0, 0, 0};
-  // WAVO_GEMM_KERNEL_ONLY (measurement only): a split GEMM call stops after the GEMM kernel, leaving
+  // wh_tune("gemm_kernel_only", "1") (measurement only): a split GEMM call stops after the GEMM kernel, leaving
   // its partial sums unfinished, so that the kernel can be timed alone as it runs inside a model step
   // (where the next kernel finishes the sums).
   int gemm_kernel_only = 0;
-  // Per-shape overrides from WAVO_GEMM_SHAPE_PLANS ("m,cols,k:bm,bn,wm,wn,stages,split;…"; tuning
+  // Per-shape overrides set by wh_tune("gemm_shape_plans", "m,cols,k:bm,bn,wm,wn,stages,split;…"); tuning
   // sweeps inside a model's step only).
   std::vector<std::array<int, 9>> gemm_shape_plans;
-  // Attention key-split override from WAVO_ATTN_SPLIT (tuning sweeps only): 0 = chosen per shape.
+  // Attention key-split override set by wh_tune("attn_split", "n") (tuning sweeps only): 0 = chosen per shape.
   int attn_split = 0;
   std::string name;
   std::string error;

@@ -453,6 +453,11 @@ struct wh_model {
   uint32_t *ids = nullptr;
   std::vector<uint32_t *> own, cross;
   int cross_frames = 0;
+  // Whisper's special ids and suppression lists (src/whisper/mod.rs:131-141, :177), and the device
+  // logits of the window search's steps.
+  int eot = -1, no_timestamps = -1, sot = -1;
+  std::vector<int> suppress, begin_suppress;
+  float *dlogits = nullptr;
 };
 
 namespace {
@@ -679,6 +684,19 @@ bool load_whisper(const Gguf &g, Loader &L, wh_model *m, std::string &err) {
     l.fc2 = L.linear({p + "ffn.fc2"}, true);
   }
   m->dec_norm = L.norm("dec.final_norm", d, true);
+  m->eot = (int)g.integer("tokenizer.ggml.eos_token_id", -1);
+  m->no_timestamps = (int)g.integer("stt.whisper.no_timestamps_token_id", -1);
+  m->sot = (int)g.integer("stt.whisper.sot_token_id", -1);
+  // The converter writes a suppress list only when it is not empty (src/whisper/mod.rs:131-133).
+  for (long v : g.ints("stt.whisper.suppress_tokens")) m->suppress.push_back((int)v);
+  for (long v : g.ints("stt.whisper.begin_suppress_tokens")) m->begin_suppress.push_back((int)v);
+  {
+    bool ok = m->eot >= 0 && m->eot < m->vocab && m->no_timestamps >= 0 && m->no_timestamps + 1 < m->vocab &&
+              m->sot >= 0 && m->sot < m->vocab;
+    for (int id : m->suppress) ok = ok && id >= 0 && id < m->vocab;
+    for (int id : m->begin_suppress) ok = ok && id >= 0 && id < m->vocab;
+    if (!ok) return err = "special token ids out of the vocabulary", false;
+  }
   m->token_embd = L.linear({"dec.token_embd"}, false);
   m->dec_pos = L.upload(L.f32s("dec.pos_emb.weight", (size_t)d * m->context));
   return L.err.empty();
@@ -1322,6 +1340,78 @@ int wh_whisper_step(wh_model *m, int token, int pos, float *logits) {
     }
     return launch_gemv(c, m->dx, m->token_embd, logits, WH_BIAS, 0.0f, 0, m->dec_norm.w, m->dec_norm.b, m->dy);
   });
+}
+
+
+int wh_whisper_ids_of(const wh_model *m, wh_whisper_ids *out) {
+  if (!m || !out || m->arch != WHISPER) return WH_EARG;
+  out->eot = m->eot;
+  out->no_timestamps = m->no_timestamps;
+  out->begin = m->no_timestamps + 1;
+  out->sot = m->sot;
+  out->suppress = m->suppress.data();
+  out->n_suppress = (int)m->suppress.size();
+  out->begin_suppress = m->begin_suppress.data();
+  out->n_begin_suppress = (int)m->begin_suppress.size();
+  return WH_OK;
+}
+
+int wh_whisper_decode(wh_model *m, const float *enc, int frames, const uint32_t *prompt, int n_prompt, uint32_t *out,
+                      int cap, float *no_speech, float *avg_logprob) {
+  if (!m || m->arch != WHISPER || !enc || frames <= 0 || n_prompt < 0 || (n_prompt && !prompt) || cap < 0 ||
+      (cap && !out))
+    return WH_EARG;
+  if (n_prompt && (int)prompt[0] != m->sot) return wh_fail(m->ctx, WH_EARG, "wh_whisper_decode: the prompt starts with SOT");
+  for (int i = 0; i < n_prompt; i++)
+    if ((int)prompt[i] >= m->vocab) return wh_fail(m->ctx, WH_EARG, "wh_whisper_decode: prompt id out of the vocabulary");
+  constexpr int MAX_NEW = 256, CONTEXT = 448;  // src/whisper/search.rs:10-11
+  constexpr float NO_SPEECH = 0.6f;            // src/whisper/mod.rs:31
+  wh_ctx *c = m->ctx;
+  (void)hipSetDevice(c->device);
+  const int vocab = m->vocab, vp = vocab % 32 == 0 ? vocab : (vocab + 63) / 64 * 64;
+  if (!m->dlogits && !(m->dlogits = dev_alloc(m, (size_t)vp))) return WH_EOOM;
+  CK(wh_whisper_begin(m, enc, frames));
+  const uint32_t sot_only = (uint32_t)m->sot;
+  const uint32_t *pr = n_prompt ? prompt : &sot_only;
+  const int np = n_prompt ? n_prompt : 1;
+  if (np > std::min(CONTEXT, m->context)) return wh_fail(c, WH_EARG, "wh_whisper_decode: prompt longer than the context");
+  std::vector<float> logits((size_t)vocab);
+  auto step = [&](uint32_t token, int pos) {
+    CK(wh_whisper_step(m, (int)token, pos, m->dlogits));
+    return wh_read(c, logits.data(), m->dlogits, sizeof(float) * (size_t)vocab);
+  };
+  // Whisper::window: the decoder on SOT at position 0; its logits give the no-speech probability
+  // (src/whisper/mod.rs:226-227), then the rest of the prompt (:235).
+  CK(step(pr[0], 0));
+  const float ns = wh_whisper_probability(logits.data(), vocab, m->no_timestamps - 1);
+  if (no_speech) *no_speech = ns;
+  for (int i = 1; i < np; i++) CK(step(pr[i], i));
+  const bool logprobs = ns > NO_SPEECH;
+  wh_whisper_ids ids;
+  CK(wh_whisper_ids_of(m, &ids));
+  const int limit = std::min(CONTEXT, m->context);
+  std::vector<uint32_t> gen;
+  double sum = 0.0;
+  int picks = 0;
+  float lp = 0.0f;
+  auto pick = [&]() {
+    const int id = wh_whisper_pick(&ids, logits.data(), vocab, gen.data(), (int)gen.size(), logprobs ? &lp : nullptr);
+    sum += logprobs ? lp : 0.0f;
+    picks++;
+    return id;
+  };
+  int next = pick();
+  if (next < 0) return wh_fail(c, WH_EARG, "wh_whisper_decode: bad token ids");
+  for (int pos = np; pos < np + MAX_NEW; pos++) {
+    if (next == m->eot) break;
+    gen.push_back((uint32_t)next);
+    if (pos + 1 > limit) break;
+    CK(step((uint32_t)next, pos));
+    next = pick();
+  }
+  if (avg_logprob) *avg_logprob = logprobs ? (float)(sum / picks) : 0.0f;
+  for (size_t i = 0; i < gen.size() && (int)i < cap; i++) out[i] = gen[i];
+  return (int)gen.size();
 }
 
 }  // extern "C"

@@ -113,24 +113,6 @@ int wh_open(int device_index, wh_ctx **out) {
   ctx->device = dev;
   ctx->cus = p.multiProcessorCount;
   ctx->name = p.name;
-  if (const char *t = getenv("WAVO_GEMM_PLAN")) {
-    int *o = ctx->gemm_plan;
-    if (sscanf(t, "%d,%d,%d,%d,%d,%d", &o[0], &o[1], &o[2], &o[3], &o[4], &o[5]) != 6 || o[5] < 1 || o[5] > 4)
-      for (int i = 0; i < 6; i++) o[i] = 0;
-  }
-  if (const char *t = getenv("WAVO_ATTN_SPLIT")) ctx->attn_split = std::max(0, std::min(atoi(t), 64));
-  if (const char *t = getenv("WAVO_GEMM_KERNEL_ONLY")) ctx->gemm_kernel_only = atoi(t) != 0;
-  if (const char *t = getenv("WAVO_GEMM_SHAPE_PLANS")) {
-    for (const char *q = t; *q;) {
-      std::array<int, 9> o{};
-      if (sscanf(q, "%d,%d,%d:%d,%d,%d,%d,%d,%d", &o[0], &o[1], &o[2], &o[3], &o[4], &o[5], &o[6], &o[7], &o[8]) == 9 &&
-          o[8] >= 1 && o[8] <= 4)
-        ctx->gemm_shape_plans.push_back(o);
-      const char *n = strchr(q, ';');
-      if (!n) break;
-      q = n + 1;
-    }
-  }
   if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
     delete ctx;
     return wh_fail(nullptr, WH_EGPU, "hipStreamCreate: %s", hipGetErrorString(e));
@@ -223,6 +205,36 @@ int wh_read(wh_ctx *ctx, void *host, const void *dptr, size_t bytes) {
 }
 
 void *wh_stream(wh_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int wh_tune(wh_ctx *ctx, const char *key, const char *value) {
+  if (!ctx || !key) return WH_EARG;
+  const char *v = value ? value : "";
+  if (!strcmp(key, "gemm_plan")) {
+    int o[6] = {0, 0, 0, 0, 0, 0};
+    if (*v && (sscanf(v, "%d,%d,%d,%d,%d,%d", &o[0], &o[1], &o[2], &o[3], &o[4], &o[5]) != 6 || o[5] < 1 || o[5] > 4))
+      return wh_fail(ctx, WH_EARG, "wh_tune gemm_plan: \"bm,bn,wm,wn,stages,split\" (split 1..4) or \"\"");
+    memcpy(ctx->gemm_plan, o, sizeof o);
+  } else if (!strcmp(key, "gemm_shape_plans")) {
+    ctx->gemm_shape_plans.clear();
+    for (const char *q = v; *q;) {
+      std::array<int, 9> o{};
+      if (sscanf(q, "%d,%d,%d:%d,%d,%d,%d,%d,%d", &o[0], &o[1], &o[2], &o[3], &o[4], &o[5], &o[6], &o[7], &o[8]) != 9 ||
+          o[8] < 1 || o[8] > 4)
+        return wh_fail(ctx, WH_EARG, "wh_tune gemm_shape_plans: \"m,cols,k:bm,bn,wm,wn,stages,split;...\"");
+      ctx->gemm_shape_plans.push_back(o);
+      const char *n = strchr(q, ';');
+      if (!n) break;
+      q = n + 1;
+    }
+  } else if (!strcmp(key, "gemm_kernel_only")) {
+    ctx->gemm_kernel_only = atoi(v) != 0;
+  } else if (!strcmp(key, "attn_split")) {
+    ctx->attn_split = std::max(0, std::min(atoi(v), 64));
+  } else {
+    return wh_fail(ctx, WH_EARG, "wh_tune: unknown key \"%s\"", key);
+  }
+  return WH_OK;
+}
 
 // ------------------------------------------------------------------------------ recorded passes
 

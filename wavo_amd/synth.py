@@ -53,10 +53,15 @@ def _rng(seed, name):
 
 
 class _Builder:
-    def __init__(self, seed, wtype):
+    def __init__(self, seed, wtype, perturb=False):
         self.w = gguf.Writer()
         self.seed = seed
         self.wtype = wtype
+        # perturb: norms, BatchNorm statistics and position biases away from their identity values
+        # (gain 1 + N(0, 0.2), shift N(0, 0.2), BN mean N(0, 0.2) and var U(0.5, 1.5), u/v N(0, 0.3),
+        # LSTM gate biases N(0, 1): gates that differ, not all near one half),
+        # so that a check of the composition sees which parameter goes where.
+        self.perturb = perturb
 
     def normal(self, name, n, std=0.02):
         return (_rng(self.seed, name).standard_normal(n, dtype=np.float32) * np.float32(std)).astype(np.float32)
@@ -78,9 +83,10 @@ class _Builder:
             self.f32(name + ".bias", [dims[-1]], self.normal(name + ".bias", dims[-1]))
 
     def norm(self, name, d, bias=True):
-        self.f32(name + ".weight", [d], np.ones(d, np.float32))
+        g = 1.0 + self.normal(name + ".weight", d, 0.2) if self.perturb else np.ones(d, np.float32)
+        self.f32(name + ".weight", [d], g)
         if bias:
-            self.f32(name + ".bias", [d], np.zeros(d, np.float32))
+            self.f32(name + ".bias", [d], self.normal(name + ".bias", d, 0.2) if self.perturb else np.zeros(d, np.float32))
 
 
 def _conformer_blocks(b, c, arch):
@@ -97,7 +103,8 @@ def _conformer_blocks(b, c, arch):
         if arch == "parakeet":
             b.linear(p + "attn.linear_pos", [d, d], False)
             for n in ("u", "v"):
-                b.f32(p + f"attn.pos_bias_{n}", [d // heads, heads], b.normal(p + f"attn.pos_bias_{n}", d))
+                b.f32(p + f"attn.pos_bias_{n}", [d // heads, heads],
+                      b.normal(p + f"attn.pos_bias_{n}", d, 0.3 if b.perturb else 0.02))
         b.norm(p + "norm_conv", d)
         b.linear(p + "conv.pointwise1", [1, d, 2 * d], bias)
         b.f32(p + "conv.depthwise.weight", [k, 1, d], b.normal(p + "conv.depthwise.weight", k * d))
@@ -106,10 +113,17 @@ def _conformer_blocks(b, c, arch):
         if arch == "gigaam":
             b.norm(p + "conv.ln", d)
         else:
-            b.f32(p + "conv.bn.weight", [d], np.ones(d))
-            b.f32(p + "conv.bn.bias", [d], np.zeros(d))
-            b.f32(p + "conv.bn.running_mean", [d], np.zeros(d))
-            b.f32(p + "conv.bn.running_var", [d], np.ones(d))
+            if b.perturb:
+                b.f32(p + "conv.bn.weight", [d], 1.0 + b.normal(p + "conv.bn.weight", d, 0.2))
+                b.f32(p + "conv.bn.bias", [d], b.normal(p + "conv.bn.bias", d, 0.2))
+                b.f32(p + "conv.bn.running_mean", [d], b.normal(p + "conv.bn.running_mean", d, 0.2))
+                b.f32(p + "conv.bn.running_var", [d],
+                      _rng(b.seed, p + "conv.bn.running_var").uniform(0.5, 1.5, d).astype(np.float32))
+            else:
+                b.f32(p + "conv.bn.weight", [d], np.ones(d))
+                b.f32(p + "conv.bn.bias", [d], np.zeros(d))
+                b.f32(p + "conv.bn.running_mean", [d], np.zeros(d))
+                b.f32(p + "conv.bn.running_var", [d], np.ones(d))
         b.linear(p + "conv.pointwise2", [1, d, d], bias)
         b.norm(p + "norm_ff2", d)
         b.linear(p + "ff2.linear1", [d, f], bias)
@@ -211,7 +225,7 @@ def build_parakeet(c, b):
         for n in ("Wx", "Wh"):
             name = f"pred.lstm.{l}.{n}"
             b.w.tensor(name, [hidden, 4 * hidden], b.wtype, gguf.encode(b.normal(name, 4 * hidden * hidden), b.wtype))
-        b.f32(f"pred.lstm.{l}.bias", [4 * hidden], b.normal(f"pred.lstm.{l}.bias", 4 * hidden))
+        b.f32(f"pred.lstm.{l}.bias", [4 * hidden], b.normal(f"pred.lstm.{l}.bias", 4 * hidden, 1.0 if b.perturb else 0.02))
     b.linear("joint.pred", [hidden, joint])
     b.linear("joint.out", [joint, vocab + len(c["durations"])])
 
@@ -254,6 +268,11 @@ def build_whisper(c, b):
     w.u32("stt.whisper.sot_token_id", eot + 1)
     w.u32("stt.whisper.transcribe_token_id", eot + 102)
     w.u32("stt.whisper.no_timestamps_token_id", eot + 107)
+    # Suppression lists as large-v3 carries them: ~90 text ids (seeded here), and the begin list
+    # [" ", EOT] (src/whisper/mod.rs:131-141 reads both).
+    rng = _rng(b.seed, "suppress_tokens")
+    w.i32s("stt.whisper.suppress_tokens", sorted(int(x) for x in rng.choice(eot, 88, replace=False)))
+    w.i32s("stt.whisper.begin_suppress_tokens", [220 % eot, eot])
     w.bool("stt.capability.lang_detect", False)
     w.strs("tokenizer.ggml.tokens", [f"t{i}" for i in range(vocab)])
     b.linear("enc.conv.0", [3, c["mels"], d])
@@ -290,10 +309,10 @@ def build_whisper(c, b):
     b.f32("dec.pos_emb.weight", [d, c["context"]], b.normal("dec.pos_emb.weight", d * c["context"]))
 
 
-def write_model(path, config, seed=0, wtype=gguf.Q8_0):
+def write_model(path, config, seed=0, wtype=gguf.Q8_0, perturb=False):
     """Writes a synthetic GGUF for `config` (a CONFIGS/SMALL entry or a dict) and returns the path."""
     c = dict(config)
-    b = _Builder(seed, wtype)
+    b = _Builder(seed, wtype, perturb)
     {"gigaam": build_gigaam, "parakeet": build_parakeet, "whisper": build_whisper}[c["arch"]](c, b)
     tmp = path + ".tmp"
     b.w.write(tmp)
@@ -301,14 +320,14 @@ def write_model(path, config, seed=0, wtype=gguf.Q8_0):
     return path
 
 
-def model_path(name, small=False, seed=0, wtype=gguf.Q8_0, directory=None):
+def model_path(name, small=False, seed=0, wtype=gguf.Q8_0, directory=None, perturb=False):
     """A cached synthetic model file under `directory` (default /tmp/wavo_models)."""
     directory = directory or os.environ.get("WAVO_MODELS", "/tmp/wavo_models")
     os.makedirs(directory, exist_ok=True)
-    tag = f"{name}{'-small' if small else ''}-s{seed}-t{wtype}.gguf"
+    tag = f"{name}{'-small' if small else ''}-s{seed}-t{wtype}{'-p' if perturb else ''}.gguf"
     path = os.path.join(directory, tag)
     if not os.path.exists(path):
-        write_model(path, (SMALL if small else CONFIGS)[name], seed, wtype)
+        write_model(path, (SMALL if small else CONFIGS)[name], seed, wtype, perturb)
     return path
 
 

@@ -154,6 +154,15 @@ int wh_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, in
  * and rounds it (gemm.wgsl:1-9). */
 int wh_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int epi,
               float alpha, int out16);
+/* wh_gemm that allocates nothing: no counterpart in the reference.  For callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The same kernels and results as wh_gemm; the f16 copy of `a` and the split-k partial sums go to a
+ * fixed workspace of wh_gemm_noalloc_limit() bytes (32 MiB) that each device holds for the life of
+ * the process, instead of the context's growable scratch.  A call whose workspace would exceed it
+ * returns WH_EARG without launching.  Calls on one device share the workspace: calls that overlap
+ * on a device (other streams or contexts) race.  Not while per-launch profiling (wh_profile 1) is on. */
+int wh_gemm_noalloc(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int epi, float alpha);
+size_t wh_gemm_noalloc_limit(void);
 /* Pass::gemv (src/gpu/mod.rs:1461-1467): c[offset + j] = epi(a·W[j] + b[j]) for one row a, W not
  * rounded. */
 int wh_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,

@@ -54,6 +54,8 @@ SIGNATURES = {
     "wh_linear_free": (None, [_vp, _vp]),
     "wh_gemm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),
     "wh_gemm_h": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f, _i]),
+    "wh_gemm_noalloc": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),
+    "wh_gemm_noalloc_limit": (_sz, []),
     "wh_gemv": (_i, [_vp, _vp, _vp, _vp, _i, _f, _i]),
     "wh_embed": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
     "wh_layer_norm": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _i]),

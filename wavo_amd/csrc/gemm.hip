@@ -22,6 +22,7 @@
 // LDS and W blocks loaded straight into registers.
 #include <algorithm>
 #include <cstdio>
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -946,14 +947,13 @@ static int check(wh_ctx *ctx, const void *a, const wh_linear *l, const void *c, 
   return WH_OK;
 }
 
-int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int ldc, int epi, float alpha) {
-  if (int rc = check(ctx, a, l, c, m, epi)) return rc;
-  if (m == 0) return WH_OK;
-  if (!lds_path(l, c, ldc)) return launch_typed<false, false>(ctx, a, l, c, m, ldc, epi, alpha);
-  // The main kernel takes a in f16: round it once into scratch (followed by the split partials).
-  const size_t n = (size_t)m * l->k, abytes = (n * 2 + 255) / 256 * 256;
-  uint8_t *ws = (uint8_t *)wh_scratch(ctx, abytes + split_bytes(ctx, l, m));
-  if (!ws) return WH_EOOM;
+// Workspace of an f32-input GEMM on the main kernel: the f16 copy of `a`, then the split-k partial sums.
+static size_t f32_gemm_abytes(const wh_linear *l, int m) { return ((size_t)m * l->k * 2 + 255) / 256 * 256; }
+
+// The f32-input GEMM on the main kernel with its workspace at ws (f32_gemm_abytes + split_bytes).
+static int gemm_f32_ws(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int ldc, int epi, float alpha,
+                       uint8_t *ws) {
+  const size_t n = (size_t)m * l->k, abytes = f32_gemm_abytes(l, m);
   _Float16 *a16 = (_Float16 *)ws;
   {
     ProfScope prof(ctx, "to_half", 0.0, 6.0 * n);
@@ -963,6 +963,69 @@ int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m
     if (int rc = wh_launched(ctx, "gemm: rounding a")) return rc;
   }
   return launch_lds(ctx, a16, l, c, m, ldc, epi, alpha, false, (float *)(ws + abytes));
+}
+
+int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int ldc, int epi, float alpha) {
+  if (int rc = check(ctx, a, l, c, m, epi)) return rc;
+  if (m == 0) return WH_OK;
+  if (!lds_path(l, c, ldc)) return launch_typed<false, false>(ctx, a, l, c, m, ldc, epi, alpha);
+  // The main kernel takes a in f16: round it once into scratch (followed by the split partials).
+  uint8_t *ws = (uint8_t *)wh_scratch(ctx, f32_gemm_abytes(l, m) + split_bytes(ctx, l, m));
+  if (!ws) return WH_EOOM;
+  return gemm_f32_ws(ctx, a, l, c, m, ldc, epi, alpha, ws);
+}
+
+// ------------------------------------------------------------------ the GEMM that allocates nothing
+// wh_gemm_noalloc's workspace (the f16 copy of `a` and the split-k partial sums): a file-scope device
+// array, which every device the library runs on holds until the process ends.  In host code its name
+// is not a device address: the address comes from hipGetSymbolAddress, once per device with that
+// device current (gemm_noalloc_init, from wh_open), and only that address is used.  Every call on a
+// device shares the array, so calls that overlap on one device (other streams or contexts) race; a
+// call writes all of the workspace it reads (the rounded `a` and every split's partial plane), so
+// nothing in it has to start at zero.
+constexpr size_t NOALLOC_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
+
+int gemm_noalloc_init(wh_ctx *ctx) {
+  constexpr int MAX_DEVICES = 64;
+  static std::mutex mu;
+  static void *addr[MAX_DEVICES] = {};
+  static hipError_t err[MAX_DEVICES] = {};
+  std::lock_guard<std::mutex> lock(mu);
+  ctx->noalloc = nullptr;
+  if (ctx->device < 0 || ctx->device >= MAX_DEVICES) return WH_EGPU;
+  if (!addr[ctx->device] && err[ctx->device] == hipSuccess) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      (void)hipGetLastError();
+      err[ctx->device] = e != hipSuccess ? e : hipErrorInvalidSymbol;
+    } else {
+      addr[ctx->device] = p;
+    }
+  }
+  ctx->noalloc = addr[ctx->device];
+  ctx->noalloc_error = ctx->noalloc ? hipSuccess : err[ctx->device];
+  return ctx->noalloc ? WH_OK : WH_EGPU;
+}
+
+size_t wh_gemm_noalloc_limit(void) { return NOALLOC_BYTES; }
+
+int wh_gemm_noalloc(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int epi, float alpha) {
+  if (!ctx || !l) return WH_EARG;
+  if (int rc = check(ctx, a, l, c, m, epi)) return rc;
+  if (!ctx->noalloc)
+    return wh_fail(ctx, WH_EGPU, "wh_gemm_noalloc: no workspace address on device %d (%s)", ctx->device,
+                   hipGetErrorString(ctx->noalloc_error));
+  if (ctx->prof == 1) return wh_fail(ctx, WH_EARG, "wh_gemm_noalloc: per-launch profiling creates events; turn it off");
+  if (m == 0) return WH_OK;
+  const int ldc = l->cols + l->dual;
+  if (!lds_path(l, c, ldc)) return launch_typed<false, false>(ctx, a, l, c, m, ldc, epi, alpha);  // no workspace
+  const size_t need = f32_gemm_abytes(l, m) + split_bytes(ctx, l, m);
+  if (need > NOALLOC_BYTES)
+    return wh_fail(ctx, WH_EARG, "wh_gemm_noalloc: %d x %d x %d needs %zu bytes of workspace, more than its %zu", m,
+                   l->rows, l->k, need, NOALLOC_BYTES);
+  return gemm_f32_ws(ctx, a, l, c, m, ldc, epi, alpha, (uint8_t *)ctx->noalloc);
 }
 
 int launch_to_half(wh_ctx *ctx, const float *x, void *y, size_t n) {

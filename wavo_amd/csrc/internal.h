@@ -48,7 +48,14 @@ struct wh_ctx {
   size_t scratch_bytes = 0;
   long scratch_epoch = 0;  // incremented whenever scratch moves (recorded graphs hold its address)
   int recording = 0;       // between wh_record_begin and wh_record_end: the stream is being captured
+  // The device address of wh_gemm_noalloc's file-scope workspace on this device (nullptr if the
+  // lookup failed, with its error).
+  void *noalloc = nullptr;
+  hipError_t noalloc_error = hipSuccess;
 };
+
+// Looks up the device address of wh_gemm_noalloc's workspace on ctx's device (current), once per device.
+int gemm_noalloc_init(wh_ctx *ctx);
 
 // At least `bytes` of device scratch (256-byte aligned), or nullptr with ctx->error set.  Growing
 // it drains the stream first; a caller that must not allocate reserves the size up front.

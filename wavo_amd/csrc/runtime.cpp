@@ -117,6 +117,9 @@ int wh_open(int device_index, wh_ctx **out) {
     delete ctx;
     return wh_fail(nullptr, WH_EGPU, "hipStreamCreate: %s", hipGetErrorString(e));
   }
+  // The workspace address of wh_gemm_noalloc on this device; a failed lookup only disables that
+  // entry point (it reports the error), every other one works without it.
+  (void)gemm_noalloc_init(ctx);
   *out = ctx;
   return WH_OK;
 }

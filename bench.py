@@ -4,35 +4,43 @@
 A step is one encoder call over 60 s of synthetic audio: the 128-bin log-mel (6001 frames, resident in
 HBM before the timed region) → 8× subsampling → 24 Conformer blocks (d 1024, 8 heads of 128, relative
 positions, FFN 4096, conv kernel 9) → the joint's encoder projection, all GEMM weights q8_0 (random
-N(0, 0.02), written as a GGUF file and loaded through the C ABI).  value = audio seconds per second
-of encoder time (RTFx), timed over --steps calls after --warmup (HIP events on the library's stream
-around the whole timed region; the calls after the second replay a recorded HIP graph of the step).
+N(0, 0.02), written as a GGUF file and loaded through the C ABI).  After --warmup untimed calls, each
+of the --steps timed calls is bracketed by HIP events on the library's stream (the calls after the
+second replay a recorded HIP graph of the step); `ms_per_step` is their median and `value` = audio
+seconds ÷ that median (RTFx).  `host_io` is the same call timed on the host from the mel's upload
+(host → HBM) to the output's read-back (HBM → host), PCIe included; it is reported beside `value`,
+never as it.  `host_frontend_ms` (the numpy log-mel of the synthetic audio) and `tdt_decode_ms` (the
+TDT greedy decode on the host, as the reference runs it) are separate.
 
-`roofline` is the dominant q8_0 GEMM of the step: the (kernel variant, call shape) with the most time
-in a profiled step.  Its average launch duration is measured by launching that exact configuration
-(same tile plan, m × n × k, epilogue and output type; random q8_0 weights of the same shape) 50 times
-back to back between two HIP events on the library's stream — events around every single launch would
-add their own few microseconds to each — and `achieved` = 2·m·n·k per launch over that duration, against
-MI355X's dense fp16 MFMA peak.  A k-split configuration is timed as its GEMM kernel alone, as in the step
-(where the next kernel, fused with the LayerNorm, adds the partial sums).  `traffic` is that launch's HBM bytes from rocprofv3 FETCH_SIZE /
-WRITE_SIZE passes (profiles/), when a summary for the same configuration is committed there.
+Per-kernel figures come from one more call with per-launch profiling: each launch carries HIP start
+and stop events that the runtime stamps at the kernel's own start and end (hipExtLaunchKernel), on
+the stream the kernels run on; per kernel variant the launches, the average duration and the
+algorithmic work per launch give achieved TFLOP/s (matrix-core kernels: GEMMs, attention) or GB/s
+(the rest) and their fraction of MI355X's peak (dense f16 MFMA 2.5 PFLOP/s, HBM 8 TB/s).  That call
+runs the same kernels eagerly (a graph replay cannot carry the events).  `roofline` is the q8_0 GEMM
+variant with the most time in the step; `kernels` lists every variant.  `traffic` is its HBM bytes
+per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/gemm_traffic.txt).
+`hbm_copy` is the measured ceiling: the library's copy kernel over 1 GiB.
 
 `gemv` is the Whisper-large-v3-turbo decoder's per-token matrix-vector products (q8_0; 4 layers of
 qkv 3840×1280, self_out / cross_q / cross_out 1280×1280, fc1 5120×1280, fc2 1280×5120, and the
-51866-row head), timed cold: two copies of the weights (2 × 168 MB, past the 256 MB Infinity Cache)
-alternate, and achieved bytes per second of the weights as stored is reported against HBM peak;
-`gemv.head` is the head alone, and `gemv.decode_step` the whole decoder step (embedding, 4 layers of
-norms, GEMVs, self- and cross-attention, the head) replayed as one recorded pass per token for 224
-tokens, with the weights left in the Infinity Cache between tokens as a decode loop leaves them.
+51866-row head), cold: two copies of the weights (2 × 168 MB, past the 256 MB Infinity Cache)
+alternate; the recorded pass of a token timed whole, and every launch kernel-stamped; `gemv.head` is
+the head alone, and `gemv.decode_step` the whole decoder step replayed as one recorded pass per
+token for 224 tokens.
 
-`cpu_baseline` is the C parity oracle (the restated wavo CPU backend, portable f16-rounded arithmetic,
-AVX2+FMA, OpenMP) on the same model and mel, one full call, timed on this host.
+`cpu_baseline` is the C parity oracle (the restated wavo CPU backend: portable f16-rounded GEMM,
+AVX2+FMA, OpenMP) on the same model, on this host: the median of 3 warm 60 s calls on all threads, and
+one 10 s call on 1 thread.  `load` times wh_model_load of the GGUF (page cache warm: the file was just
+written).
 """
 
 import argparse
 import json
 import os
 import re
+import statistics
+import subprocess
 import sys
 import time
 
@@ -43,6 +51,7 @@ METRIC = "encoder RTFx (audio s/s) at 1 MI355X; q8_0 GEMM % MFMA peak; GEMV % HB
 PEAK_F16 = 2500.0     # TFLOP/s, MI355X dense fp16 MFMA
 PEAK_HBM = 8000.0     # GB/s
 GEMM_NAME = re.compile(r"^gemm_(\w+?)_(\d+)x(\d+)_w(\d+)x(\d+)_n(\d+)(_s\d)? (\d+)x(\d+)x(\d+) e(\d+) (f16|f32) w(\d+)$")
+MFMA_KERNELS = ("attention", "attention_rel")
 
 
 def log(msg):
@@ -61,7 +70,43 @@ def time_region(gpu, fn, reps):
     return ms / reps
 
 
-def gemm_replay(gpu, name, reps=50):
+def time_each(gpu, fn, reps):
+    """Milliseconds of each of `reps` calls of fn(), each between its own pair of events."""
+    gpu.profile(2)
+    for i in range(reps):
+        gpu.region_begin(f"call{i}")
+        fn()
+        gpu.region_end()
+    recs = gpu.profile_read()
+    gpu.profile(0)
+    return [r["ms"] for r in recs]
+
+
+def profiled(gpu, fn):
+    """Per kernel variant of one call of fn(): launches, total ms (kernel-stamped), flops, bytes."""
+    gpu.profile(1)
+    fn()
+    recs = gpu.profile_read()
+    gpu.profile(0)
+    return recs
+
+
+def kernel_roofline(rec):
+    """Achieved rate of a profiled kernel variant against its roof."""
+    us = rec["ms"] * 1e3 / rec["launches"]
+    mfma = rec["flops"] > 0 and (GEMM_NAME.match(rec["kernel"]) or rec["kernel"] in MFMA_KERNELS)
+    if mfma:
+        per = rec["flops"] / rec["launches"]
+        achieved = per / (us * 1e-6) / 1e12
+        return {"bound": "mfma", "launches": rec["launches"], "avg_us": round(us, 3), "flops_per_launch": per,
+                "achieved": round(achieved, 2), "peak": PEAK_F16, "unit": "TFLOP/s", "frac": round(achieved / PEAK_F16, 4)}
+    per = rec["bytes"] / rec["launches"]
+    achieved = per / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "launches": rec["launches"], "avg_us": round(us, 3), "bytes_per_launch": per,
+            "achieved": round(achieved, 1), "peak": PEAK_HBM, "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4)}
+
+
+def gemm_replay(name, reps=50):
     """Re-launches the GEMM configuration `name` (a profile record) back to back; returns us/launch."""
     import numpy as np
 
@@ -74,11 +119,8 @@ def gemm_replay(gpu, name, reps=50):
     rng = np.random.default_rng(5)
     w = gguf.encode(rng.standard_normal(int(n) * int(k), dtype=np.float32) * np.float32(0.02), wtype)
     f16 = out == "f16"
-    plan = f"{bm},{bn},{wm},{wn},{ns},{split[2:] if split else 1}"
-    import wavo_amd
-
-    g2 = wavo_amd.Gpu(0)
-    g2.tune("gemm_plan", plan)  # the same launch plan as in the step
+    g2 = wa.Gpu(0)
+    g2.tune("gemm_plan", f"{bm},{bn},{wm},{wn},{ns},{split[2:] if split else 1}")  # the plan of the step
     # A split GEMM's kernel alone, as it runs in the step (where the following fused LayerNorm kernel
     # adds the partial sums); a C-ABI call would add its own finishing kernel.
     g2.tune("gemm_kernel_only", 1)
@@ -93,6 +135,21 @@ def gemm_replay(gpu, name, reps=50):
     del lin2, a2, c2
     g2.close()
     return us, 2.0 * int(m) * int(n) * int(k)
+
+
+def hbm_copy(gpu, nbytes=1 << 30):
+    """The library's copy kernel over `nbytes` (device to device): read + write bytes per second."""
+    a, b = gpu.buffer(nbytes // 4), gpu.buffer(nbytes // 4)
+    gpu.zero(a)
+    for _ in range(3):
+        gpu.copy(b, a, nbytes)
+    recs = profiled(gpu, lambda: [gpu.copy(b, a, nbytes) for _ in range(10)])
+    r = next(x for x in recs if x["kernel"] == "copy")
+    us = r["ms"] * 1e3 / r["launches"]
+    a.free(), b.free()
+    rate = 2 * nbytes / (us * 1e-6) / 1e9
+    return {"bytes_per_launch": 2 * nbytes, "avg_us": round(us, 2), "achieved": round(rate, 1),
+            "peak": PEAK_HBM, "unit": "GB/s", "frac": round(rate / PEAK_HBM, 4)}
 
 
 def gemv_cold(gpu):
@@ -144,27 +201,24 @@ def gemv_cold(gpu):
     ms = time_region(gpu, one, reps)
     for p in passes:
         p.free()
-    # The head alone (70.6 MB), cold: one launch per call (a one-node recorded pass costs more to
-    # launch than the kernel runs).
-    head = [c[-1] for c in copies]
-    st2 = {"i": 0}
-
-    def one_head():
-        gpu.gemv(x, head[st2["i"] % 2], y, wa.BIAS)
-        st2["i"] += 1
-
-    for _ in range(4):
-        one_head()
-    hms = time_region(gpu, one_head, 40)
+    # Kernel time of the same GEMVs, stamped per launch (cold, alternating copies).
+    recs = profiled(gpu, lambda: [token(i) for i in range(8)])
+    kern_ms = sum(r["ms"] for r in recs) / 8
+    head = [r for r in recs if r["kernel"].startswith("gemv") and f" {vocab}x" in r["kernel"]]
     hbytes = vocab * d // 32 * 34
     out = {"workload": "whisper-large-v3-turbo decoder GEMVs per token, q8_0, cold (2 weight copies of 168 MB alternate), "
                        "each token's 25 GEMVs replayed as one recorded pass",
            "launches_per_token": len(shapes), "us_per_token": round(ms * 1e3, 2), "weight_bytes": wbytes,
            "achieved": round(wbytes / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM, "unit": "GB/s",
            "frac": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM, 4),
-           "head": {"shape": f"{vocab}x{d}", "us": round(hms * 1e3, 2), "bytes": hbytes,
-                    "achieved": round(hbytes / (hms * 1e-3) / 1e9, 1),
-                    "frac": round(hbytes / (hms * 1e-3) / 1e9 / PEAK_HBM, 4)}}
+           "kernel_us_per_token": round(kern_ms * 1e3, 2),
+           "kernel_frac": round(wbytes / (kern_ms * 1e-3) / 1e9 / PEAK_HBM, 4),
+           "per_kernel": {r["kernel"]: kernel_roofline(r) for r in recs}}
+    if head:
+        us = head[0]["ms"] * 1e3 / head[0]["launches"]
+        out["head"] = {"shape": f"{vocab}x{d}", "us": round(us, 2), "bytes": hbytes,
+                       "achieved": round(hbytes / (us * 1e-6) / 1e9, 1),
+                       "frac": round(hbytes / (us * 1e-6) / 1e9 / PEAK_HBM, 4)}
     del copies
     return out
 
@@ -220,6 +274,54 @@ def traffic_for(name):
     return None
 
 
+def host_cpu():
+    """nproc, the CPU model and the oracle's SIMD path on this host."""
+    model = ""
+    try:
+        for line in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "model": model,
+            "simd": "AVX2+FMA (oracle built -march=x86-64-v3)"}
+
+
+def cpu_baseline(path, mel, seconds, gpu_out):
+    import numpy as np
+
+    import oracle
+    from wavo_amd import synth
+
+    om = oracle.Model(path)
+    threads = oracle.lib().ox_threads()
+    log(f"CPU baseline: oracle on {threads} threads")
+    times = []
+    want = None
+    for i in range(4):  # one warm-up, then 3 timed
+        t0 = time.perf_counter()
+        want = om.encode(mel)
+        if i:
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    err = float(np.linalg.norm(gpu_out - want) / np.linalg.norm(want))
+    # One thread over a 10 s clip (a bounded sample of the same workload).
+    short = synth.parakeet_mel(synth.audio(10.0, seed=1))
+    oracle.lib().ox_set_threads(1)
+    t0 = time.perf_counter()
+    om.encode(short)
+    one = time.perf_counter() - t0
+    oracle.lib().ox_set_threads(threads)
+    log(f"CPU {med:.2f} s median on {threads} threads, {one:.2f} s for 10 s on 1 thread; rel L2 {err:.2e}")
+    return {"value": round(seconds / med, 3), "unit": "audio s/s", "cores": threads, "kind": "port",
+            "seconds_median": round(med, 3), "calls": len(times),
+            "one_thread": {"value": round(10.0 / one, 3), "unit": "audio s/s", "seconds": round(one, 3),
+                           "sample": "one 10 s call"},
+            "host": host_cpu(),
+            "sample": f"median of 3 warm encoder calls on the same {seconds:.0f} s mel and model (after one warm-up), "
+                      f"all threads; the restated wavo CPU backend (portable f16-rounded GEMM); GPU-vs-CPU rel L2 {err:.2e}"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -238,6 +340,8 @@ def main():
               "Segments of long audio shard across GPUs with no exchange step; run one process per GPU.",
               file=sys.stderr)
         sys.exit(2)
+    if args.warmup < 2 or args.steps < 10:
+        log("note: the measurement protocol is a median of >= 10 calls after >= 2 warm-ups")
 
     import numpy as np
 
@@ -247,7 +351,7 @@ def main():
     if args.replay:
         if not GEMM_NAME.match(args.replay):
             sys.exit(f"--replay takes a GEMM configuration name like the bench line's roofline.kernel: {args.replay!r}")
-        us, flops = gemm_replay(None, args.replay)
+        us, flops = gemm_replay(args.replay)
         print(json.dumps({"replayed": args.replay, "us_per_launch": round(us, 3),
                           "tflops": round(flops / (us * 1e-6) / 1e12, 2)}), flush=True)
         return
@@ -256,86 +360,99 @@ def main():
     path = synth.model_path("parakeet")
     log(f"model {path} ready in {time.time() - t0:.1f} s")
     gpu = wa.Gpu(0)
-    t0 = time.time()
+    t0 = time.perf_counter()
     model = wa.Model(gpu, path)
-    log(f"loaded on {gpu.name or 'gfx950'} ({gpu.cus} CUs) in {time.time() - t0:.1f} s")
+    load_s = time.perf_counter() - t0
+    log(f"loaded on {gpu.name or 'gfx950'} ({gpu.cus} CUs) in {load_s:.2f} s")
     pcm = synth.audio(args.seconds, seed=1)
-    mel = synth.parakeet_mel(pcm)
+    fe = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        mel = synth.parakeet_mel(pcm)
+        fe.append(time.perf_counter() - t0)
     mel_frames = mel.shape[0]
     frames, width = model.frames(mel_frames)
     melb = gpu.upload(mel)
     outb = gpu.buffer(frames * width)
+    step = lambda: model.encode_device(melb, mel_frames, outb)
 
     for _ in range(args.warmup):
-        model.encode_device(melb, mel_frames, outb)
+        step()
     gpu.sync()
     log(f"warmup done ({args.warmup} steps), timing {args.steps}")
     t0 = time.perf_counter()
-    ms_ev = time_region(gpu, lambda: model.encode_device(melb, mel_frames, outb), args.steps)
+    per = time_each(gpu, step, args.steps)
     wall = (time.perf_counter() - t0) / args.steps
-    dt = ms_ev * 1e-3
-    rtfx = args.seconds / dt
-    log(f"{dt * 1e3:.3f} ms per step (events; wall {wall * 1e3:.3f}), RTFx {rtfx:.0f}")
+    med = statistics.median(per)
+    rtfx = args.seconds / (med * 1e-3)
+    log(f"{med:.3f} ms per step (median of {len(per)}; mean {statistics.mean(per):.3f}, min {min(per):.3f}; "
+        f"host wall {wall * 1e3:.3f}), RTFx {rtfx:.0f}")
 
-    # One profiled step: per-kernel launches and algorithmic work (events around each launch).
-    gpu.profile(1)
-    model.encode_device(melb, mel_frames, outb)
-    prof = gpu.profile_read()
-    gpu.profile(0)
-    gemms = [k for k in prof if GEMM_NAME.match(k["kernel"])]
-    dom = max(gemms, key=lambda k: k["ms"])
-    us, flops = gemm_replay(gpu, dom["kernel"])
-    log(f"dominant GEMM {dom['kernel']}: {dom['launches']} launches per step, {us:.2f} us per launch back to back")
+    # The same call from host memory to host memory: mel upload, encoder, output read-back.
+    host = np.empty((frames, width), np.float32)
+    io = []
+    for i in range(12):
+        t0 = time.perf_counter()
+        gpu.write(melb, mel)
+        step()
+        host[:] = gpu.read(outb, (frames, width))
+        if i >= 2:
+            io.append(time.perf_counter() - t0)
+    io_med = statistics.median(io)
+    dec = []
+    tokens = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        tokens = model.greedy(host)
+        dec.append(time.perf_counter() - t0)
 
-    achieved = flops / (us * 1e-6) / 1e12
-    fam = {}
-    for k in prof:
-        f = k["kernel"].split(" ")[0]
-        e = fam.setdefault(f, [0, 0.0])
-        e[0] += k["launches"]
-        e[1] += k["ms"]
-    q8 = [k for k in gemms if k["kernel"].startswith("gemm_q8_0")]
-    q8_flops = sum(k["flops"] for k in q8)
-    q8_ms = sum(k["ms"] for k in q8)
+    # One call with every launch stamped: per-kernel in-step durations.
+    prof = profiled(gpu, step)
+    kern = {r["kernel"]: kernel_roofline(r) for r in prof}
+    gemms = [r for r in prof if GEMM_NAME.match(r["kernel"]) and r["kernel"].startswith("gemm_q8_0")]
+    dom = max(gemms, key=lambda r: r["ms"])
+    rl = kernel_roofline(dom)
+    replay_us, _ = gemm_replay(dom["kernel"])
+    log(f"dominant GEMM {dom['kernel']}: {dom['launches']} launches, {rl['avg_us']:.2f} us in the step "
+        f"({rl['frac'] * 100:.1f}% of f16 peak); {replay_us:.2f} us back to back")
+    q8_flops = sum(r["flops"] for r in gemms)
+    q8_ms = sum(r["ms"] for r in gemms)
     roofline = {
         "bound": "mfma",
         "kernel": dom["kernel"],
-        "achieved": round(achieved, 2),
+        "achieved": rl["achieved"],
         "peak": PEAK_F16,
         "unit": "TFLOP/s",
-        "frac": round(achieved / PEAK_F16, 4),
+        "frac": rl["frac"],
         "traffic": traffic_for(dom["kernel"]),
         "launches_per_step": dom["launches"],
-        "avg_launch_us": round(us, 2),
-        "flops_per_launch": flops,
-        "timing": "50 back-to-back launches of this configuration between two HIP events on the library's stream",
-        "all_q8_0_gemm_profiled": {"launches": sum(k["launches"] for k in q8), "ms": round(q8_ms, 4),
-                                   "tflops_incl_event_overhead": round(q8_flops / (q8_ms * 1e-3) / 1e12, 2)},
+        "avg_launch_us": rl["avg_us"],
+        "flops_per_launch": rl["flops_per_launch"],
+        "timing": "kernel-stamped HIP events (hipExtLaunchKernel start/stop) on every launch of one step",
+        "back_to_back_us": round(replay_us, 2),
+        "all_q8_0_gemms": {"launches": sum(r["launches"] for r in gemms), "ms": round(q8_ms, 4),
+                           "tflops": round(q8_flops / (q8_ms * 1e-3) / 1e12, 2),
+                           "frac": round(q8_flops / (q8_ms * 1e-3) / 1e12 / PEAK_F16, 4)},
     }
+    fam = {}
+    for r in prof:
+        f = r["kernel"].split(" ")[0]
+        e = fam.setdefault(f, [0, 0.0])
+        e[0] += r["launches"]
+        e[1] += r["ms"]
     breakdown = {f: {"launches": n, "ms": round(ms, 4)} for f, (n, ms) in sorted(fam.items(), key=lambda x: -x[1][1])}
+    log(f"kernel time in the profiled step {sum(r['ms'] for r in prof):.3f} ms")
+    copy = hbm_copy(gpu)
+    log(f"HBM copy ceiling {copy['achieved']} GB/s")
 
     gemv = None if args.no_gemv else gemv_cold(gpu)
     if gemv:
-        log(f"GEMV per token {gemv['us_per_token']} us, {gemv['achieved']} GB/s ({gemv['frac'] * 100:.1f}% of HBM)")
+        log(f"GEMV per token {gemv['us_per_token']} us, {gemv['achieved']} GB/s ({gemv['frac'] * 100:.1f}% of HBM); "
+            f"kernels {gemv['kernel_frac'] * 100:.1f}%; head {gemv.get('head', {}).get('frac', 0) * 100:.1f}%")
         gemv["decode_step"] = decode_steps(gpu)
         log(f"decoder step {gemv['decode_step']['us_per_token']} us per token")
 
-    cpu = None
-    if not args.no_cpu:
-        import oracle
-
-        om = oracle.Model(path)
-        log(f"CPU baseline: oracle on {oracle.lib().ox_threads()} threads")
-        t0 = time.perf_counter()
-        want = om.encode(mel)
-        cdt = time.perf_counter() - t0
-        got = gpu.read(outb, (frames, width))
-        err = float(np.linalg.norm(got - want) / np.linalg.norm(want))
-        cpu = {"value": round(args.seconds / cdt, 3), "unit": "audio s/s", "cores": oracle.lib().ox_threads(),
-               "kind": "port", "seconds": round(cdt, 3),
-               "sample": f"one full encoder call on the same {args.seconds:.0f} s mel and model (restated wavo CPU "
-                         f"backend, portable f16-rounded GEMM, AVX2+FMA, OpenMP); GPU-vs-CPU rel L2 {err:.2e}"}
-        log(f"CPU {cdt:.2f} s, rel L2 {err:.2e}")
+    cpu = None if args.no_cpu else cpu_baseline(path, mel, args.seconds, host)
 
     out = {
         "metric": METRIC,
@@ -344,7 +461,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(dt * 1e3, 4),
+        "ms_per_step": round(med, 4),
+        "ms_per_step_mean": round(statistics.mean(per), 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -354,6 +472,14 @@ def main():
                    "audio_s": args.seconds, "mel_frames": mel_frames, "encoder_frames": frames,
                    "layers": model.layers, "d_model": model.d, "weights": "q8_0"},
         "roofline": roofline,
+        "kernels": kern,
+        "hbm_copy": copy,
+        "host_io": {"ms_median": round(io_med * 1e3, 3), "rtfx": round(args.seconds / io_med, 1),
+                    "what": "mel upload (pageable host memory) + encoder call + output read-back, host clock"},
+        "host_frontend_ms": round(statistics.median(fe) * 1e3, 2),
+        "tdt_decode_ms": round(statistics.median(dec) * 1e3, 2),
+        "tdt_tokens": len(tokens),
+        "load": {"seconds": round(load_s, 3), "what": "wh_model_load of the GGUF, page cache warm"},
         "gemv": gemv,
         "cpu_baseline": cpu,
         "profiled_step_ms": breakdown,

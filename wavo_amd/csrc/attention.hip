@@ -519,7 +519,7 @@ template <int DP, typename T>
 void launch_pack(wh_ctx *ctx, const Pack &sp, const T *k, int ks, long kbs, const T *v, int vs, long vbs, const T *pos,
                  int ps, int t, int heads, int hd, int batch, _Float16 *kp, _Float16 *vt, _Float16 *pp) {
   const int gx = sp.tk / KB + (pos ? sp.prows / 32 : 0);
-  pack_kernel<DP, T><<<dim3(gx, heads, batch), 256, 0, ctx->stream>>>(k, ks, kbs, v, vs, vbs, t, heads, hd, sp.tk, kp, vt,
+  wh_launch(ctx, pack_kernel<DP, T>, dim3(gx, heads, batch), 256, 0, k, ks, kbs, v, vs, vbs, t, heads, hd, sp.tk, kp, vt,
                                                                        pos, ps, 2 * t + 15, sp.pfront, sp.prows, pp);
 }
 
@@ -531,15 +531,17 @@ int launch_flash(wh_ctx *ctx, const Args &a, int heads, int batch, int dp) {
   ProfScope prof(ctx, REL ? "attention_rel" : "attention", (REL ? 6.0 : 4.0) * tt, bytes);
   const dim3 grid((a.t + 16 * QW - 1) / (16 * QW), heads, batch * a.nsplit);
   switch (dp) {
-    case 32: flash_kernel<1, REL><<<grid, 64 * QW, 0, ctx->stream>>>(a); break;
-    case 64: flash_kernel<2, REL><<<grid, 64 * QW, 0, ctx->stream>>>(a); break;
-    default: flash_kernel<4, REL><<<grid, 64 * QW, 0, ctx->stream>>>(a); break;
+    case 32: wh_launch(ctx, flash_kernel<1, REL>, grid, 64 * QW, 0, a); break;
+    case 64: wh_launch(ctx, flash_kernel<2, REL>, grid, 64 * QW, 0, a); break;
+    default: wh_launch(ctx, flash_kernel<4, REL>, grid, 64 * QW, 0, a); break;
   }
   if (int rc = wh_launched(ctx, "attention")) return rc;
   if (a.nsplit > 1) {
     const size_t n = (size_t)batch * a.t * heads * (a.hd / 4);
     const int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
-    combine_kernel<<<blocks, 256, 0, ctx->stream>>>(a.po, a.pml, a.nsplit, batch, a.t, heads, a.hd, a.o, a.os, a.bo, a.o16);
+    ProfScope pc(ctx, "attention_combine", 0.0, 4.0 * a.nsplit * batch * a.t * heads * (a.hd + 2.0) +
+                                                    (a.o16 ? 2.0 : 4.0) * batch * a.t * heads * a.hd);
+    wh_launch(ctx, combine_kernel, blocks, 256, 0, a.po, a.pml, a.nsplit, batch, a.t, heads, a.hd, a.o, a.os, a.bo, a.o16);
     return wh_launched(ctx, "attention combine");
   }
   return WH_OK;

@@ -10,6 +10,8 @@
 // summed in f32 and scaled once, as ggml's mul_mv (gemm.wgsl:244-262); W is not rounded to f16.
 #include <algorithm>
 
+#include <cstdio>
+
 #include "internal.h"
 
 namespace {
@@ -431,13 +433,15 @@ int gemv_stream(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int e
   P.total = (size_t)l->rows * l->row_bytes;
   const size_t lds = (size_t)GV_NS * GV_STAGE + 4 * (size_t)items * 68 + 4 * 256 + 4 * (size_t)P.per_wg * P.rps;
   if (lds > 160 * 1024) return 1;  // (positive: not an error) the caller takes the general kernel
-  static const char *tn = WT == WH_F16 ? "gemv_f16" : WT == WH_Q8_0 ? "gemv_q8_0" : "gemv_q4_0";
+  // Named by type and shape (rows x k): the profile tells the decoder's GEMVs apart.
+  char tn[64];
+  snprintf(tn, sizeof tn, "gemv_%s %dx%d", WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0", l->rows, l->k);
   const double bytes = (double)P.total + 4.0 * l->k + 4.0 * l->cols * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
   ProfScope prof(ctx, tn, 2.0 * l->rows * l->k, bytes);
   if (l->row_bytes % 16 == 0)
-    gemv_stream_kernel<WT, true><<<grid, 256, lds, ctx->stream>>>(P);
+    wh_launch(ctx, gemv_stream_kernel<WT, true>, grid, 256, lds, P);
   else
-    gemv_stream_kernel<WT, false><<<grid, 256, lds, ctx->stream>>>(P);
+    wh_launch(ctx, gemv_stream_kernel<WT, false>, grid, 256, lds, P);
   return wh_launched(ctx, "gemv");
 }
 
@@ -446,11 +450,13 @@ int gemv_t(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, f
   int waves = (l->cols + 1) / 2;
   int grid = (waves + 3) / 4;
   size_t lds = sizeof(float) * (size_t)l->k;
-  static const char *tn = WT == WH_F32 ? "gemv_f32" : WT == WH_F16 ? "gemv_f16" : WT == WH_Q8_0 ? "gemv_q8_0" : "gemv_q4_0";
+  char tn[64];
+  snprintf(tn, sizeof tn, "gemv_%s %dx%d", WT == WH_F32 ? "f32" : WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0",
+           l->rows, l->k);
   // Algorithmic bytes: W as stored + a + c (+ c read by the residual epilogues).
   double bytes = (double)l->rows * l->row_bytes + 4.0 * l->k + 4.0 * l->cols * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
   ProfScope prof(ctx, tn, 2.0 * l->rows * l->k, bytes);
-  gemv_wave_kernel<WT, PAIR><<<grid, 256, lds, ctx->stream>>>(a, l->w, l->bias, c, l->rows, l->cols, l->k,
+  wh_launch(ctx, gemv_wave_kernel<WT, PAIR>, grid, 256, lds, a, l->w, l->bias, c, l->rows, l->cols, l->k,
                                                               l->row_bytes, epi, alpha, offset);
   return wh_launched(ctx, "gemv");
 }
@@ -758,7 +764,7 @@ __global__ void step_args_kernel(uint32_t *ids, uint32_t token, uint32_t pos) {
 
 int launch_step_args(wh_ctx *ctx, uint32_t *ids, int token, int pos) {
   if (!ids || token < 0 || pos < 0) return wh_fail(ctx, WH_EARG, "step arguments: bad arguments");
-  step_args_kernel<<<1, 64, 0, ctx->stream>>>(ids, (uint32_t)token, (uint32_t)pos);
+  wh_launch(ctx, step_args_kernel, 1, 64, 0, ids, (uint32_t)token, (uint32_t)pos);
   return wh_launched(ctx, "step_args");
 }
 
@@ -766,7 +772,7 @@ int launch_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, co
                  int offset, const int *dpos, int dstride) {
   if (!pos || !c || !ids || i < 0 || offset < 0) return wh_fail(ctx, WH_EARG, "embed: bad arguments");
   ProfScope prof(ctx, "embed", 0.0, 12.0 * l->k);
-  embed_kernel<<<(l->k + 255) / 256, 256, 0, ctx->stream>>>(l->w, l->type, l->row_bytes, pos, l->bias, c, ids, i,
+  wh_launch(ctx, embed_kernel, (l->k + 255) / 256, 256, 0, l->w, l->type, l->row_bytes, pos, l->bias, c, ids, i,
                                                             l->k, offset, dpos, dstride);
   return wh_launched(ctx, "embed");
 }
@@ -784,23 +790,25 @@ int launch_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, 
     // step; runs of 768 keys 268, of 256 keys 262).
     const int kpp = 512, parts = (n + kpp - 1) / kpp;
     ProfScope prof(ctx, "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
-    attend_one_kernel<<<dim3(heads, parts), 64 * AT_WAVES, 0, ctx->stream>>>(q, kv, o, n, hd, scale, cols, heads, dn,
+    wh_launch(ctx, attend_one_kernel, dim3(heads, parts), 64 * AT_WAVES, 0, q, kv, o, n, hd, scale, cols, heads, dn,
                                                                              part, kpp);
     if (int rc = wh_launched(ctx, "attend")) return rc;
-    combine_kernel<<<heads, 64, 0, ctx->stream>>>(part, o, n, hd, dn, cols, kpp);
+    ProfScope pc(ctx, "attend_combine", 0.0, 4.0 * parts * heads * (hd + 2.0) + 4.0 * heads * hd);
+    wh_launch(ctx, combine_kernel, heads, 64, 0, part, o, n, hd, dn, cols, kpp);
     return wh_launched(ctx, "combine");
   }
   if (most <= 64 * AT_WAVES * AT_ROUNDS) {  // every key in one workgroup per head: no merge launch
     ProfScope prof(ctx, "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
-    attend_one_kernel<<<heads, 64 * AT_WAVES, 0, ctx->stream>>>(q, kv, o, n, hd, scale, cols, heads, dn, nullptr, 0);
+    wh_launch(ctx, attend_one_kernel, heads, 64 * AT_WAVES, 0, q, kv, o, n, hd, scale, cols, heads, dn, nullptr, 0);
     return wh_launched(ctx, "attend");
   }
   dim3 grid((most + KEYS - 1) / KEYS, heads);
   ProfScope prof(ctx, "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
-  attend_kernel<<<grid, 256, 0, ctx->stream>>>(q, kv, part, n, hd, scale, cols, heads, dn);
+  wh_launch(ctx, attend_kernel, grid, 256, 0, q, kv, part, n, hd, scale, cols, heads, dn);
   int rc = wh_launched(ctx, "attend");
   if (rc) return rc;
-  combine_kernel<<<heads, 64, 0, ctx->stream>>>(part, o, n, hd, dn, cols, KEYS);
+  ProfScope pc(ctx, "attend_combine", 0.0, 4.0 * grid.x * heads * (hd + 2.0) + 4.0 * heads * hd);
+  wh_launch(ctx, combine_kernel, heads, 64, 0, part, o, n, hd, dn, cols, KEYS);
   return wh_launched(ctx, "combine");
 }
 
@@ -810,10 +818,10 @@ int launch_pack(wh_ctx *ctx, const float *x, int src, int stride, uint32_t *y, i
     return wh_fail(ctx, WH_EARG, "pack: bad arguments");
   ProfScope prof(ctx, "pack", 0.0, 4.0 * rows * 2 * d + 2.0 * rows * 2 * d);
   if (rows == 1) {
-    pack_kernel<<<(d + 255) / 256, 256, 0, ctx->stream>>>(x, y, rows, d, cols, col, src, stride, dcol);
+    wh_launch(ctx, pack_kernel, (d + 255) / 256, 256, 0, x, y, rows, d, cols, col, src, stride, dcol);
   } else {
     dim3 grid((rows + 63) / 64, (d + 3) / 4);
-    pack_kernel<<<grid, 256, 0, ctx->stream>>>(x, y, rows, d, cols, col, src, stride, dcol);
+    wh_launch(ctx, pack_kernel, grid, 256, 0, x, y, rows, d, cols, col, src, stride, dcol);
   }
   return wh_launched(ctx, "pack");
 }

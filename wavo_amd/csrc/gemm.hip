@@ -399,6 +399,81 @@ __device__ __forceinline__ void unrolled_steps(F &f, int kt0, int nk) {
   }
 }
 
+// The epilogue's store of a BM × BN tile whose f32 sums sit in LDS (cl, rows of `crow` floats): NT
+// threads take 8 consecutive columns each (16-byte loads of c for the residual modes, 16-byte stores),
+// applying the bias (bb, loaded by the caller for the thread's fixed column group), the epilogue, the
+// dual columns (bd) and the padding columns (epi(0 + bias), as the reference's zero rows give); a
+// split GEMM stores its plain partial sums into plane tz instead.
+template <int BM, int BN, int NT, bool SPLIT, bool OUT16>
+__device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, int crow, int tid, int m0, int n0,
+                                             int tz, const float (&bb)[8], const float (&bd)[8]) {
+  constexpr int G8 = BN / 8;
+  const int m = P.m, rows = P.rows;
+  static_assert((BM * G8) % NT == 0, "whole rounds of column groups");
+#pragma unroll
+  for (int it = 0; it < BM * G8 / NT; it++) {
+    const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0 + r, col = n0 + c8;
+    if (row >= m || col >= P.cols) continue;  // cols % 32 == 0: a group is inside or past
+    const float4 x0 = *(const float4 *)(cl + r * crow + c8), x1 = *(const float4 *)(cl + r * crow + c8 + 4);
+    float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    if constexpr (SPLIT) {
+      float *cp = (float *)P.c + ((size_t)tz * m + row) * P.cols + col;
+      *(float4 *)cp = x0;
+      *(float4 *)(cp + 4) = x1;
+      continue;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; q++)
+      if (col + q >= rows) x[q] = 0.0f;
+    const size_t at = (size_t)row * P.ldc + col;
+    float y[8];
+    if (!OUT16 && (P.epi == WH_RESIDUAL || P.epi == WH_GELU_RESIDUAL)) {
+      const float4 c0 = *(const float4 *)((const float *)P.c + at), c1 = *(const float4 *)((const float *)P.c + at + 4);
+      const float cc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      if (P.epi == WH_RESIDUAL)
+#pragma unroll
+        for (int q = 0; q < 8; q++) y[q] = cc[q] + P.alpha * (x[q] + bb[q]);
+      else
+#pragma unroll
+        for (int q = 0; q < 8; q++) y[q] = cc[q] + gelu(x[q] + bb[q]);
+    } else {
+      switch (P.epi) {
+#define EPI_CASE(E)                                                               \
+  case E:                                                                         \
+    _Pragma("unroll") for (int q = 0; q < 8; q++) y[q] = epilogue(E, 0.0f, x[q] + bb[q], nullptr); \
+    break;
+        EPI_CASE(WH_SILU)
+        EPI_CASE(WH_RELU)
+        EPI_CASE(WH_GELU)
+        EPI_CASE(WH_TANH)
+#undef EPI_CASE
+        default:
+#pragma unroll
+          for (int q = 0; q < 8; q++) y[q] = x[q] + bb[q];
+      }
+    }
+    const bool dual = col < P.dual;  // dual % 8 == 0 is not required: per column below
+    if constexpr (OUT16) {
+      half8 h;
+#pragma unroll
+      for (int q = 0; q < 8; q++) h[q] = (_Float16)y[q];
+      *(half8 *)((_Float16 *)P.c + at) = h;
+    } else {
+      *(float4 *)((float *)P.c + at) = make_float4(y[0], y[1], y[2], y[3]);
+      *(float4 *)((float *)P.c + at + 4) = make_float4(y[4], y[5], y[6], y[7]);
+    }
+    if (dual) {
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        if (col + q >= P.dual) break;
+        const float d = x[q] + bd[q];
+        if constexpr (OUT16) ((_Float16 *)P.c)[at + P.cols + q] = (_Float16)d;
+        else ((float *)P.c)[at + P.cols + q] = d;
+      }
+    }
+  }
+}
+
 // c tile BM × BN per workgroup of WM × WN wavefronts, each a (BM/WM) × (BN/WN) block of 32×32 MFMA
 // tiles, over the k range of its split (the 64-wide k steps divided evenly over gridDim.z).
 //
@@ -646,69 +721,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
       for (int v = 0; v < 16; v++)
         cl[(wm + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow] = acc[i][j][v];
   __syncthreads();
-  static_assert((BM * G8) % (64 * NW) == 0, "whole rounds of column groups");
-#pragma unroll
-  for (int it = 0; it < BM * G8 / (64 * NW); it++) {
-    const int e = tid + it * 64 * NW, r = e / G8, c8 = 8 * (e % G8), row = m0 + r, col = n0 + c8;
-    if (row >= m || col >= P.cols) continue;  // cols % 32 == 0: a group is inside or past
-    const float4 x0 = *(const float4 *)(cl + r * CROW + c8), x1 = *(const float4 *)(cl + r * CROW + c8 + 4);
-    float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-    if constexpr (SPLIT) {
-      float *cp = (float *)P.c + ((size_t)tz * m + row) * P.cols + col;
-      *(float4 *)cp = x0;
-      *(float4 *)(cp + 4) = x1;
-      continue;
-    }
-#pragma unroll
-    for (int q = 0; q < 8; q++)
-      if (col + q >= rows) x[q] = 0.0f;
-    const size_t at = (size_t)row * P.ldc + col;
-    float y[8];
-    if (!OUT16 && (P.epi == WH_RESIDUAL || P.epi == WH_GELU_RESIDUAL)) {
-      const float4 c0 = *(const float4 *)((const float *)P.c + at), c1 = *(const float4 *)((const float *)P.c + at + 4);
-      const float cc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-      if (P.epi == WH_RESIDUAL)
-#pragma unroll
-        for (int q = 0; q < 8; q++) y[q] = cc[q] + P.alpha * (x[q] + bb[q]);
-      else
-#pragma unroll
-        for (int q = 0; q < 8; q++) y[q] = cc[q] + gelu(x[q] + bb[q]);
-    } else {
-      switch (P.epi) {
-#define EPI_CASE(E)                                                               \
-  case E:                                                                         \
-    _Pragma("unroll") for (int q = 0; q < 8; q++) y[q] = epilogue(E, 0.0f, x[q] + bb[q], nullptr); \
-    break;
-        EPI_CASE(WH_SILU)
-        EPI_CASE(WH_RELU)
-        EPI_CASE(WH_GELU)
-        EPI_CASE(WH_TANH)
-#undef EPI_CASE
-        default:
-#pragma unroll
-          for (int q = 0; q < 8; q++) y[q] = x[q] + bb[q];
-      }
-    }
-    const bool dual = col < P.dual;  // dual % 8 == 0 is not required: per column below
-    if constexpr (OUT16) {
-      half8 h;
-#pragma unroll
-      for (int q = 0; q < 8; q++) h[q] = (_Float16)y[q];
-      *(half8 *)((_Float16 *)P.c + at) = h;
-    } else {
-      *(float4 *)((float *)P.c + at) = make_float4(y[0], y[1], y[2], y[3]);
-      *(float4 *)((float *)P.c + at + 4) = make_float4(y[4], y[5], y[6], y[7]);
-    }
-    if (dual) {
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        if (col + q >= P.dual) break;
-        const float d = x[q] + bd[q];
-        if constexpr (OUT16) ((_Float16 *)P.c)[at + P.cols + q] = (_Float16)d;
-        else ((float *)P.c)[at + P.cols + q] = d;
-      }
-    }
-  }
+  store_c_tile<BM, BN, 64 * NW, SPLIT, OUT16>(P, cl, CROW, tid, m0, n0, tz, bb, bd);
 }
 
 // Split-k finish: c = epi(Σ_z part[z] + bias) with the partial sums added in split order (the same
@@ -806,9 +819,9 @@ Plan plan_for(const wh_ctx *ctx, int m, int cols, int k) {
 
 template <int WT, int BM, int BN, int WM, int WN, int NS>
 void lds_launch(wh_ctx *ctx, dim3 grid, const LdsArgs &a, bool split, bool out16) {
-  if (split) gemm_lds_kernel<WT, BM, BN, WM, WN, NS, true, false><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
-  else if (out16) gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, true><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
-  else gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, false><<<grid, 64 * WM * WN, 0, ctx->stream>>>(a);
+  if (split) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, true, false>, grid, 64 * WM * WN, 0, a);
+  else if (out16) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, true>, grid, 64 * WM * WN, 0, a);
+  else wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, false>, grid, 64 * WM * WN, 0, a);
 }
 
 template <int WT>
@@ -861,9 +874,9 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     const size_t n = (size_t)m * l->cols;
     const int blocks = (int)std::min<size_t>((n + 255) / 256, 8192);
     if (out16)
-      split_finish_kernel<true><<<blocks, 256, 0, ctx->stream>>>(part, p.split, l->bias, c, m, l->rows, l->cols, l->dual, ldc, epi, alpha);
+      wh_launch(ctx, split_finish_kernel<true>, blocks, 256, 0, part, p.split, l->bias, c, m, l->rows, l->cols, l->dual, ldc, epi, alpha);
     else
-      split_finish_kernel<false><<<blocks, 256, 0, ctx->stream>>>(part, p.split, l->bias, c, m, l->rows, l->cols, l->dual, ldc, epi, alpha);
+      wh_launch(ctx, split_finish_kernel<false>, blocks, 256, 0, part, p.split, l->bias, c, m, l->rows, l->cols, l->dual, ldc, epi, alpha);
     return wh_launched(ctx, "gemm split finish");
   }
   return WH_OK;
@@ -903,7 +916,6 @@ int launch_t(wh_ctx *ctx, const void *a, const wh_linear *l, void *c, int m, int
   if (tiles(128, 128) >= cus) bm = 128, bn = 128;
   else if (tiles(64, 128) >= cus) bm = 64, bn = 128;
   dim3 grid((l->cols + bn - 1) / bn, (m + bm - 1) / bm);
-  hipStream_t s = ctx->stream;
   // Algorithmic work: 2·m·rows·k flops over the real rows; bytes of W as stored, a, c (and c read
   // back by the residual epilogues).
   static const char *tn = WT == WH_F32 ? "f32" : WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
@@ -914,11 +926,11 @@ int launch_t(wh_ctx *ctx, const void *a, const wh_linear *l, void *c, int m, int
                  (OUT16 ? 2.0 : 4.0) * m * width * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
   ProfScope prof(ctx, name, 2.0 * m * l->rows * l->k, bytes);
   if (bm == 128)
-    gemm_reg_kernel<WT, 128, 128, ALIGNED, A16, OUT16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
+    wh_launch(ctx, gemm_reg_kernel<WT, 128, 128, ALIGNED, A16, OUT16>, grid, 256, 0, a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
   else if (bn == 128)
-    gemm_reg_kernel<WT, 64, 128, ALIGNED, A16, OUT16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
+    wh_launch(ctx, gemm_reg_kernel<WT, 64, 128, ALIGNED, A16, OUT16>, grid, 256, 0, a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
   else
-    gemm_reg_kernel<WT, 64, 64, ALIGNED, A16, OUT16><<<grid, 256, 0, s>>>(a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
+    wh_launch(ctx, gemm_reg_kernel<WT, 64, 64, ALIGNED, A16, OUT16>, grid, 256, 0, a, l->w, l->bias, c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha, l->row_bytes);
   return wh_launched(ctx, "gemm");
 }
 
@@ -959,7 +971,7 @@ static int gemm_f32_ws(wh_ctx *ctx, const float *a, const wh_linear *l, float *c
     ProfScope prof(ctx, "to_half", 0.0, 6.0 * n);
     const size_t n4 = n / 4;
     const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 4096);
-    to_half_kernel<<<blocks, 256, 0, ctx->stream>>>((const float4 *)a, (half4 *)a16, n4);
+    wh_launch(ctx, to_half_kernel, blocks, 256, 0, (const float4 *)a, (half4 *)a16, n4);
     if (int rc = wh_launched(ctx, "gemm: rounding a")) return rc;
   }
   return launch_lds(ctx, a16, l, c, m, ldc, epi, alpha, false, (float *)(ws + abytes));
@@ -1034,7 +1046,7 @@ int launch_to_half(wh_ctx *ctx, const float *x, void *y, size_t n) {
   ProfScope prof(ctx, "to_half", 0.0, 6.0 * n);
   const size_t n4 = n / 4;
   const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 4096);
-  to_half_kernel<<<blocks, 256, 0, ctx->stream>>>((const float4 *)x, (half4 *)y, n4);
+  wh_launch(ctx, to_half_kernel, blocks, 256, 0, (const float4 *)x, (half4 *)y, n4);
   return wh_launched(ctx, "to_half");
 }
 

@@ -2,6 +2,7 @@
 // the C ABI (include/wavo_hip.h) and the graph drivers call.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -11,11 +12,14 @@
 
 #include "../../include/wavo_hip.h"
 
-// One profiled launch: HIP events on the context's stream around it, and its algorithmic work.
+// One profiled launch (or named region) and its algorithmic work: a start and a stop event.  A launch's
+// events are stamped by the runtime at the kernel's own start and end (hipExtLaunchKernel); a region's
+// are recorded on the stream around whatever is queued in between.  `used` = the events were queued.
 struct wh_prof_rec {
   std::string kernel;
   double flops = 0, bytes = 0;
   int ev0 = -1, ev1 = -1;
+  bool used = false;
 };
 
 struct wh_ctx {
@@ -39,6 +43,7 @@ struct wh_ctx {
   // Profiling (wh_profile): 0 off (default), 1 events around every launch, 2 named regions only.
   int prof = 0;
   int open_region = -1;
+  int prof_pending = -1;  // mode 1: the record whose events the next wh_launch carries
   std::vector<hipEvent_t> events;
   size_t next_event = 0;
   std::vector<wh_prof_rec> recs;
@@ -61,13 +66,32 @@ int gemm_noalloc_init(wh_ctx *ctx);
 // it drains the stream first; a caller that must not allocate reserves the size up front.
 void *wh_scratch(wh_ctx *ctx, size_t bytes);
 
-// Profiling scope of one launch: records an event before and after it when profiling is on.
+// Profiling scope of one launch: with per-launch profiling on (wh_profile 1) it reserves a record with
+// a start/stop event pair, which the next wh_launch inside the scope carries; a scope left without a
+// launch drops its record.
 struct ProfScope {
   ProfScope(wh_ctx *ctx, const char *kernel, double flops, double bytes);
   ~ProfScope();
   wh_ctx *ctx;
   int rec = -1;
 };
+
+// The event pair of the pending profiled launch (nullptr when none), which the call clears.
+void wh_prof_take(wh_ctx *ctx, hipEvent_t *start, hipEvent_t *stop);
+
+// Queues kernel<<<grid, block, shm, ctx->stream>>>(args...).  Under a ProfScope with per-launch
+// profiling on, the launch goes through hipExtLaunchKernelGGL with the scope's events, which the
+// runtime stamps at the kernel's own start and end (no marker packets around it).
+template <typename F, typename... Args>
+inline void wh_launch(wh_ctx *ctx, F kernel, dim3 grid, dim3 block, size_t shm, Args... args) {
+  if (ctx->prof == 1 && ctx->prof_pending >= 0) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    wh_prof_take(ctx, &e0, &e1);
+    hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)shm, ctx->stream, e0, e1, 0u, args...);
+    return;
+  }
+  kernel<<<grid, block, shm, ctx->stream>>>(args...);
+}
 
 // A linear layer on the device (src/gpu/mod.rs:390-413): W [rows][k] in its GGUF bytes, rows
 // contiguous; the bias padded to `cols + dual`.

@@ -359,8 +359,20 @@ __global__ void zero_bytes_kernel(uint8_t *p, size_t bytes) {
   if (i < bytes) p[i] = 0;
 }
 
-__global__ void copy16_kernel(uint4 *__restrict__ y, const uint4 *__restrict__ x, size_t n) {
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) y[i] = x[i];
+// 16-byte copy: each thread moves four 16-byte pieces per round (a workgroup's 16 KiB in flight
+// before any store), streaming past the caches (non-temporal loads and stores).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void copy16_kernel(u32x4 *__restrict__ y, const u32x4 *__restrict__ x, size_t n) {
+  constexpr int U = 4;
+  for (size_t i = (size_t)blockIdx.x * 256 * U + threadIdx.x; i < n; i += (size_t)gridDim.x * 256 * U) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      if (i + 256 * u < n) v[u] = __builtin_nontemporal_load(x + i + 256 * u);
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      if (i + 256 * u < n) __builtin_nontemporal_store(v[u], y + i + 256 * u);
+  }
 }
 
 // The finish of a k-split GEMM with the residual epilogue, fused with the LayerNorm of its result:
@@ -496,15 +508,15 @@ int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *
       (uintptr_t)g % 16 == 0 && (uintptr_t)b % 16 == 0) {
     size_t lds = table ? (size_t)4 * cols * sizeof(float) : 0;
     if (out16)
-      layer_norm_kernel<_Float16><<<(rows + 3) / 4, 256, lds, ctx->stream>>>(x, g, b, (_Float16 *)y, rows, cols, table,
+      wh_launch(ctx, layer_norm_kernel<_Float16>, (rows + 3) / 4, 256, lds, x, g, b, (_Float16 *)y, rows, cols, table,
                                                                              (_Float16 *)yr, hd);
     else
-      layer_norm_kernel<float><<<(rows + 3) / 4, 256, lds, ctx->stream>>>(x, g, b, (float *)y, rows, cols, table,
+      wh_launch(ctx, layer_norm_kernel<float>, (rows + 3) / 4, 256, lds, x, g, b, (float *)y, rows, cols, table,
                                                                           (float *)yr, hd);
   } else {
     if (table || out16)
       return wh_fail(ctx, WH_EARG, "layer_norm: rope and f16 rows need cols %% 4 == 0, at most %d", ROW_REGS * 64);
-    layer_norm_long<<<rows, 64, 0, ctx->stream>>>(x, g, b, (float *)y, cols);
+    wh_launch(ctx, layer_norm_long, rows, 64, 0, x, g, b, (float *)y, cols);
   }
   return wh_launched(ctx, "layer_norm");
 }
@@ -520,7 +532,7 @@ int launch_split_residual_ln(wh_ctx *ctx, const float *part, int splits, const f
                  (double)rows * cols * (4.0 * splits + (keep_x ? 8 : 4) + (out16 ? 2 : 4) + (g2 ? 2 : 0)));
   const int grid = (rows + 3) / 4;
 #define SRL(OT, N)                                                                                                  \
-  split_residual_ln_kernel<OT, N><<<grid, 256, 0, ctx->stream>>>(part, splits, bias, wrows, alpha, x, g, b, (OT *)y, \
+  wh_launch(ctx, split_residual_ln_kernel<OT, N>, grid, 256, 0, part, splits, bias, wrows, alpha, x, g, b, (OT *)y, \
                                                                   rows, cols, keep_x, g2, b2, (_Float16 *)y2)
   if (out16) {
     if (splits == 2) SRL(_Float16, 2);
@@ -543,7 +555,7 @@ int launch_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int ke
   int width = (ch * kernel + 31) / 32 * 32;
   dim3 grid((width + 255) / 256, rows, batch);
   ProfScope prof(ctx, "im2col", 0.0, 4.0 * batch * ((double)rows * width + (double)t * ch));
-  im2col_kernel<<<grid, 256, 0, ctx->stream>>>(x, col, t, ch, kernel, stride, pad, rows, width, xs, cs);
+  wh_launch(ctx, im2col_kernel, grid, 256, 0, x, col, t, ch, kernel, stride, pad, rows, width, xs, cs);
   return wh_launched(ctx, "im2col");
 }
 
@@ -552,7 +564,7 @@ static void conv_glu_k(wh_ctx *ctx, dim3 grid, int threads, const float *h, cons
                 const float *g, const float *b, int layer_norm, OT *y, int t, int ch, const int *valid_dev, int valid) {
 #define CG(K)                                                                                                      \
   case K:                                                                                                          \
-    conv_glu_kernel<OT, K><<<grid, threads, 0, ctx->stream>>>(h, w, wb, kernel, g, b, layer_norm, y, t, ch, valid_dev, \
+    wh_launch(ctx, conv_glu_kernel<OT, K>, grid, threads, 0, h, w, wb, kernel, g, b, layer_norm, y, t, ch, valid_dev, \
                                                               valid);                                              \
     break;
   switch (kernel) {
@@ -593,10 +605,10 @@ int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *
   if (w0) {
     const size_t lds = sizeof(float) * 7 * (4 * (size_t)half_len(half_len(f)) + 3);
     if (lds > 64 * 1024) return wh_fail(ctx, WH_EARG, "depthwise: %d mel bins is more than one workgroup's patch holds", f);
-    first_depthwise_kernel<<<dim3(1, rows), threads < 64 ? 64 : threads, lds, ctx->stream>>>(x, w, b, y, w0, b0, t, f, ch, t0);
+    wh_launch(ctx, first_depthwise_kernel, dim3(1, rows), threads < 64 ? 64 : threads, lds, x, w, b, y, w0, b0, t, f, ch, t0);
   } else {
     dim3 grid(half_len(f), rows);
-    depthwise_kernel<<<grid, threads, 0, ctx->stream>>>(x, w, b, y, t, f, ch, t0);
+    wh_launch(ctx, depthwise_kernel, grid, threads, 0, x, w, b, y, t, f, ch, t0);
   }
   return wh_launched(ctx, "depthwise");
 }
@@ -605,13 +617,13 @@ int launch_flatten(wh_ctx *ctx, const float *x, float *y, int t, int f, int ch) 
   if (t < 0 || f <= 0 || ch <= 0) return wh_fail(ctx, WH_EARG, "flatten: bad shape");
   if (!t) return WH_OK;
   ProfScope prof(ctx, "flatten", 0.0, 8.0 * t * f * ch);
-  flatten_kernel<<<t, 256, 0, ctx->stream>>>(x, y, f, ch);
+  wh_launch(ctx, flatten_kernel, t, 256, 0, x, y, f, ch);
   return wh_launched(ctx, "flatten");
 }
 
 int launch_argmax(wh_ctx *ctx, const float *x, uint32_t *out, int n) {
   if (n < 0 || !out) return wh_fail(ctx, WH_EARG, "argmax: bad arguments");
-  argmax_kernel<<<1, 256, 0, ctx->stream>>>(x, out, n);
+  wh_launch(ctx, argmax_kernel, 1, 256, 0, x, out, n);
   return wh_launched(ctx, "argmax");
 }
 
@@ -621,11 +633,11 @@ int launch_zero(wh_ctx *ctx, void *dst, size_t bytes) {
   size_t words = bytes / 4;
   if ((uintptr_t)dst % 4 == 0 && words) {
     size_t blocks = (words + 255) / 256;
-    zero_kernel<<<(unsigned)(blocks > 65535 ? 65535 : blocks), 256, 0, ctx->stream>>>((uint32_t *)dst, words);
+    wh_launch(ctx, zero_kernel, (unsigned)(blocks > 65535 ? 65535 : blocks), 256, 0, (uint32_t *)dst, words);
     if (bytes % 4)
-      zero_bytes_kernel<<<1, 4, 0, ctx->stream>>>((uint8_t *)dst + words * 4, bytes % 4);
+      wh_launch(ctx, zero_bytes_kernel, 1, 4, 0, (uint8_t *)dst + words * 4, bytes % 4);
   } else {
-    zero_bytes_kernel<<<(unsigned)((bytes + 255) / 256), 256, 0, ctx->stream>>>((uint8_t *)dst, bytes);
+    wh_launch(ctx, zero_bytes_kernel, (unsigned)((bytes + 255) / 256), 256, 0, (uint8_t *)dst, bytes);
   }
   return wh_launched(ctx, "zero");
 }
@@ -636,13 +648,13 @@ int launch_copy(wh_ctx *ctx, void *dst, const void *src, size_t bytes) {
   ProfScope prof(ctx, "copy", 0.0, 2.0 * bytes);
   const size_t n16 = ((uintptr_t)dst % 16 == 0 && (uintptr_t)src % 16 == 0) ? bytes / 16 : 0;
   if (n16) {
-    const size_t blocks = std::min<size_t>((n16 + 255) / 256, 8192);
-    copy16_kernel<<<(unsigned)blocks, 256, 0, ctx->stream>>>((uint4 *)dst, (const uint4 *)src, n16);
+    const size_t blocks = std::min<size_t>((n16 + 1023) / 1024, 16384);
+    wh_launch(ctx, copy16_kernel, (unsigned)blocks, 256, 0, (u32x4 *)dst, (const u32x4 *)src, n16);
   }
   const size_t rest = bytes - 16 * n16;
   if (rest) {
     const size_t blocks = std::min<size_t>((rest + 255) / 256, 8192);
-    copy_bytes_kernel<<<(unsigned)blocks, 256, 0, ctx->stream>>>((uint8_t *)dst + 16 * n16, (const uint8_t *)src + 16 * n16,
+    wh_launch(ctx, copy_bytes_kernel, (unsigned)blocks, 256, 0, (uint8_t *)dst + 16 * n16, (const uint8_t *)src + 16 * n16,
                                                                  rest);
   }
   return wh_launched(ctx, "copy");
@@ -651,6 +663,6 @@ int launch_copy(wh_ctx *ctx, void *dst, const void *src, size_t bytes) {
 int launch_add_rows(wh_ctx *ctx, float *x, const float *a, size_t n) {
   if (!n) return WH_OK;
   size_t blocks = (n + 255) / 256;
-  add_kernel<<<(unsigned)(blocks > 65535 ? 65535 : blocks), 256, 0, ctx->stream>>>(x, a, n);
+  wh_launch(ctx, add_kernel, (unsigned)(blocks > 65535 ? 65535 : blocks), 256, 0, x, a, n);
   return wh_launched(ctx, "add");
 }

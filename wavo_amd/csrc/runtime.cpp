@@ -49,13 +49,23 @@ ProfScope::ProfScope(wh_ctx *c, const char *kernel, double flops, double bytes) 
   r.ev0 = prof_event(ctx);
   r.ev1 = prof_event(ctx);
   if (r.ev0 < 0 || r.ev1 < 0) return;
-  (void)hipEventRecord(ctx->events[r.ev0], ctx->stream);
   rec = (int)ctx->recs.size();
   ctx->recs.push_back(r);
+  ctx->prof_pending = rec;
 }
 
 ProfScope::~ProfScope() {
-  if (rec >= 0) (void)hipEventRecord(ctx->events[ctx->recs[rec].ev1], ctx->stream);
+  if (rec >= 0 && ctx->prof_pending == rec) ctx->prof_pending = -1;  // no launch took the events
+}
+
+void wh_prof_take(wh_ctx *ctx, hipEvent_t *start, hipEvent_t *stop) {
+  *start = *stop = nullptr;
+  if (ctx->prof_pending < 0) return;
+  wh_prof_rec &r = ctx->recs[ctx->prof_pending];
+  *start = ctx->events[r.ev0];
+  *stop = ctx->events[r.ev1];
+  r.used = true;
+  ctx->prof_pending = -1;
 }
 
 void *wh_scratch(wh_ctx *ctx, size_t bytes) {
@@ -315,6 +325,7 @@ int wh_profile(wh_ctx *ctx, int mode) {
   ctx->recs.clear();
   ctx->next_event = 0;
   ctx->open_region = -1;
+  ctx->prof_pending = -1;
   return WH_OK;
 }
 
@@ -328,6 +339,7 @@ int wh_region(wh_ctx *ctx, const char *name, double flops, double bytes) {
     r.ev1 = prof_event(ctx);
     if (r.ev0 < 0 || r.ev1 < 0) return wh_fail(ctx, WH_EGPU, "wh_region: event creation failed");
     if (hipEventRecord(ctx->events[r.ev0], ctx->stream) != hipSuccess) return wh_fail(ctx, WH_EGPU, "wh_region: event record failed");
+    r.used = true;
     ctx->open_region = (int)ctx->recs.size();
     ctx->recs.push_back(r);
     return WH_OK;
@@ -350,6 +362,7 @@ int wh_profile_read(wh_ctx *ctx, char *out, size_t len) {
   std::vector<double> ms, fl, by;
   std::vector<long> n;
   for (const wh_prof_rec &r : ctx->recs) {
+    if (!r.used) continue;
     float t = 0.0f;
     if (hipEventElapsedTime(&t, ctx->events[r.ev0], ctx->events[r.ev1]) != hipSuccess) t = 0.0f;
     size_t i = 0;

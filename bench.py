@@ -10,7 +10,9 @@ second replay a recorded HIP graph of the step); `ms_per_step` is their median a
 seconds ÷ that median (RTFx).  `host_io` is the same call timed on the host from the mel's upload
 (host → HBM) to the output's read-back (HBM → host), PCIe included; it is reported beside `value`,
 never as it.  `host_frontend_ms` (the numpy log-mel of the synthetic audio) and `tdt_decode_ms` (the
-TDT greedy decode on the host, as the reference runs it) are separate.
+TDT greedy decode on the host, as the reference runs it) are separate; `tdt_device` is the same decode
+on the device over the resident encoder output (wh_model_greedy_device, host clock, median of 5 calls
+after 2), with whether its tokens equal the host decode's.
 
 Per-kernel figures come from one more call with per-launch profiling: each launch carries HIP start
 and stop events that the runtime stamps at the kernel's own start and end (hipExtLaunchKernel), on
@@ -406,6 +408,17 @@ def main():
         tokens = model.greedy(host)
         dec.append(time.perf_counter() - t0)
 
+    # The same decode on the device, over the encoder output still in HBM.
+    ddec = []
+    dtokens = []
+    for i in range(7):
+        t0 = time.perf_counter()
+        dtokens = model.greedy_device(outb, frames, width)
+        if i >= 2:
+            ddec.append(time.perf_counter() - t0)
+    log(f"TDT decode: host {statistics.median(dec) * 1e3:.1f} ms, device {statistics.median(ddec) * 1e3:.2f} ms "
+        f"({len(dtokens)} tokens, {'equal' if dtokens == tokens else 'different'})")
+
     # One call with every launch stamped: per-kernel in-step durations.
     prof = profiled(gpu, step)
     kern = {r["kernel"]: kernel_roofline(r) for r in prof}
@@ -479,6 +492,9 @@ def main():
         "host_frontend_ms": round(statistics.median(fe) * 1e3, 2),
         "tdt_decode_ms": round(statistics.median(dec) * 1e3, 2),
         "tdt_tokens": len(tokens),
+        "tdt_device": {"ms_median": round(statistics.median(ddec) * 1e3, 3), "tokens": len(dtokens),
+                       "equal_to_host": dtokens == tokens,
+                       "what": "wh_model_greedy_device over the resident encoder output, host clock"},
         "load": {"seconds": round(load_s, 3), "what": "wh_model_load of the GGUF, page cache warm"},
         "gemv": gemv,
         "cpu_baseline": cpu,

@@ -255,6 +255,14 @@ int wh_model_blocks(wh_model *m, float *x_dev, int t, int layers);
  * returns the count or a negative error. */
 int wh_model_greedy(wh_model *m, const float *enc_host, int frames, int width, uint32_t *out,
                     int cap);
+/* The same decoders over an encoder output in device memory, run on the device; replaces the
+ * encoder readback plus host decode of Model::transcribe (src/parakeet/mod.rs:135-141,
+ * src/gigaam/mod.rs:144-152).  CTC: per-frame first-maximum argmax and the collapse.  TDT: the
+ * joint, decision and LSTM predictor with the loop's state in device memory (runs of decisions
+ * recorded and replayed; the host reads the state between runs).  Same results as wh_model_greedy
+ * up to float rounding of the decoder's products (ties of near-equal logits may differ). */
+int wh_model_greedy_device(wh_model *m, const float *enc_dev, int frames, int width, uint32_t *out,
+                           int cap);
 /* Whisper decoding on the device: wh_whisper_begin computes every layer's cross-attention K/V from
  * the encoder output (Decoder::record_cross, src/transformer.rs:243-248); wh_whisper_step runs one
  * token at position pos (Decoder::record_step, :254-290) and leaves the logits in logits_dev. */

@@ -439,13 +439,14 @@ class Model:
         cap = 16384
         out = np.zeros(2 * cap, np.uint32)
         frames = np.zeros(3 * 4 * cap, np.int32)
-        gaps = np.zeros(4 * cap, np.float32)
+        gaps = np.full(4 * cap, -1.0, np.float32)  # a gap is >= 0: the decisions are the leading run
         n = lib().ox_model_tdt_trace(self.h, pe, enc.shape[0], enc.shape[1], out.ctypes.data_as(_u32p), cap,
                                      frames.ctypes.data_as(_ip), _ptr(gaps), 4 * cap)
         if n < 0:
             raise ValueError("tdt failed")
         toks = [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(min(n, cap))]
-        return toks, frames.reshape(-1, 3), gaps
+        d = int(np.argmax(gaps < 0)) if (gaps < 0).any() else len(gaps)
+        return toks, frames.reshape(-1, 3)[:d], gaps[:d]
 
     def predict(self, token, state, hidden, joint, layers):
         """One predictor step: (next state, joint's predictor projection)."""

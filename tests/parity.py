@@ -53,3 +53,37 @@ def tdt_parity(om, got, want):
     gap = float(gw[k])
     assert gap <= bound, f"decision {k} (frame {frame}) flipped with gap {gap:.3g} > bound {bound:.3g}"
     return (k, frame, gap, bound), tg, tw
+
+
+# Relative tie bound of the device TDT decoder: both sides compute the joint and the predictor in f32,
+# summing in different orders, so their logits differ by about 1e-6 of the output layer's Lipschitz
+# bound times |z|; a flipped decision needs an oracle top-2 gap of that order.
+TDT_TIE_REL = 1e-4
+
+
+def tdt_device_parity(om, tokens, enc):
+    """The device TDT decoder's (token, frame) list against the oracle's on the same encoder output.
+    Identical, or else the first flipped decision is a near tie: it lies after the oracle's decision
+    that emitted the last shared token (the lists agree up to it) and at a frame no later than either
+    list's first differing entry, and some oracle decision in that window has a top-2 gap of at most
+    TDT_TIE_REL times the joint output layer's Lipschitz bound.  Returns None or (index, frame,
+    smallest gap in the window, bound)."""
+    want, trace, gaps = om.tdt_trace(enc)
+    if tokens == want:
+        return None
+    n = min(len(tokens), len(want))
+    i = next((k for k in range(n) if tokens[k] != want[k]), n)
+    frame = min(lst[i][1] for lst in (tokens, want) if i < len(lst))
+    # The oracle's decision that emitted want[i - 1]: emissions are the decisions whose (token,
+    # frame) is the next list entry (a blank is never in the list).
+    start, j = 0, 0
+    for k in range(len(trace)):
+        if j < i and (int(trace[k][1]), int(trace[k][0])) == want[j]:
+            j += 1
+            start = k + 1
+    window = [k for k in range(start, len(trace)) if trace[k][0] <= frame]
+    assert window, f"token {i} (frame {frame}) differs with no oracle decision where it could have flipped"
+    gap = float(min(gaps[k] for k in window))
+    bound = TDT_TIE_REL * om.tdt_lipschitz()
+    assert gap <= bound, f"token {i} (frame {frame}) differs; smallest gap in decisions {start}.. is {gap:.3g} > bound {bound:.3g}"
+    return i, frame, gap, bound

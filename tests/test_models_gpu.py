@@ -15,7 +15,7 @@ import pytest
 
 import oracle as ox
 import wavo_amd as wa
-from parity import ctc_parity, tdt_parity, top2_gap
+from parity import ctc_parity, tdt_device_parity, tdt_parity, top2_gap
 from wavo_amd import gguf, synth
 
 pytestmark = pytest.mark.gpu
@@ -34,11 +34,13 @@ ENCODER_TOL = 1e-2
 
 
 def check_ctc(m, full, want):
-    """The product's CTC on the device output equals the oracle's CTC on the same logits; against the
-    oracle's encoder output only provable near-tie frames may differ."""
+    """The product's CTC on the device output equals the oracle's CTC on the same logits, on the host
+    and on the device; against the oracle's encoder output only provable near-tie frames may differ."""
     classes = want.shape[1]
     got = full[:, :classes]
     assert m.greedy(full) == ox.ctc(got, classes - 1)
+    fb = m.gpu.upload(np.ascontiguousarray(full))
+    assert m.greedy_device(fb, full.shape[0], full.shape[1]) == ox.ctc(got, classes - 1)
     flips = ctc_parity(got, want, classes)
     if not flips:
         assert m.greedy(full) == ox.ctc(want, classes - 1)
@@ -46,7 +48,12 @@ def check_ctc(m, full, want):
 
 
 def check_tdt(m, om, got, want):
+    """TDT on the device output: the host decoder equals the oracle's, the device decoder
+    (wh_model_greedy_device) too up to f32 near-ties; then the device output against the oracle's."""
     assert m.greedy(got) == om.tdt(got), "the product's TDT decoder differs from the oracle's"
+    gb = m.gpu.upload(np.ascontiguousarray(got))
+    dev_flip = tdt_device_parity(om, m.greedy_device(gb, got.shape[0], got.shape[1]), got)
+    assert dev_flip is None or dev_flip[2] <= dev_flip[3]
     flip, tg, tw = tdt_parity(om, got, want)
     if flip is None:
         assert tg == tw

@@ -77,6 +77,7 @@ SIGNATURES = {
     "wh_model_graphs": (_i, [_vp, _i]),
     "wh_model_blocks": (_i, [_vp, _vp, _i, _i]),
     "wh_model_greedy": (_i, [_vp, _vp, _i, _i, _vp, _i]),
+    "wh_model_greedy_device": (_i, [_vp, _vp, _i, _i, _vp, _i]),
     "wh_whisper_begin": (_i, [_vp, _vp, _i]),
     "wh_whisper_step": (_i, [_vp, _i, _i, _vp]),
     "wh_whisper_ids_of": (_i, [_vp, _vp]),
@@ -472,6 +473,16 @@ class Model:
         cap = 4 * enc.shape[0] + 16
         out = np.zeros(2 * cap, np.uint32)
         n = lib().wh_model_greedy(self.h, enc.ctypes.data, enc.shape[0], enc.shape[1], out.ctypes.data, cap)
+        if n < 0:
+            self.gpu._check(n)
+        return [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(min(n, cap))]
+
+    def greedy_device(self, enc_buf, frames, width, cap=None):
+        """The same greedy decoders run on the device over an encoder output in device memory
+        (wh_model_greedy_device)."""
+        cap = 4 * frames + 16 if cap is None else cap
+        out = np.zeros(2 * max(cap, 1), np.uint32)
+        n = lib().wh_model_greedy_device(self.h, _p(enc_buf), frames, width, out.ctypes.data, cap)
         if n < 0:
             self.gpu._check(n)
         return [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(min(n, cap))]

@@ -146,9 +146,11 @@ struct GemvPack {
 // With ln_g: the product takes LayerNorm(a; ln_g, ln_b) (one row of k): inside the streaming kernel,
 // or written to ln_y (k floats) by its own launch before the general kernel.  With pack: see GemvPack
 // (inside the streaming kernel, or by launch_pack after the general one).
+// With skip (device memory), the launch does nothing while *skip != 0: a recorded sequence switches
+// its GEMVs on and off from the device (not with a fused norm or cache column).
 int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,
                 int offset, const float *ln_g = nullptr, const float *ln_b = nullptr, float *ln_y = nullptr,
-                const GemvPack *pack = nullptr);
+                const GemvPack *pack = nullptr, const int *skip = nullptr);
 // With dpos (device memory), the position offset is (*dpos)·dstride instead of `offset`: a recorded
 // decoder step reads its position from the device.
 int launch_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, const uint32_t *ids,
@@ -185,3 +187,32 @@ int launch_zero(wh_ctx *ctx, void *dst, size_t bytes);
 // Device-to-device copy with a kernel (a graph node like any other launch).
 int launch_copy(wh_ctx *ctx, void *dst, const void *src, size_t bytes);
 int launch_add_rows(wh_ctx *ctx, float *x, const float *add, size_t n);
+
+// ---- greedy decoding on the device (greedy.hip) ----
+// The TDT loop's state (src/parakeet/decoder.rs:158-191), in device memory: the call's encoder output
+// and (token, frame) list too, so a recorded decision serves every call.
+struct TdtState {
+  int t, symbols, left, count, token, done, idle, decisions;
+  int frames, width, cap, pad;
+  const float *enc;
+  uint32_t *out;
+};
+// The decoder's constants (src/parakeet/decoder.rs:46-89).
+struct TdtConfig {
+  int classes, ndur, blank, max_symbols, global;
+  int durations[16];
+};
+int launch_tdt_init(wh_ctx *ctx, TdtState *st, const TdtState &init);
+// z = ReLU(enc[t] + pred) (joint values); nothing once done.
+int launch_tdt_joint_in(wh_ctx *ctx, const float *pred, float *z, int joint, const TdtState *st);
+// x = table row of the last emitted token (n values); nothing while idle.
+int launch_tdt_embed(wh_ctx *ctx, const float *table, int n, float *x, const TdtState *st);
+// One decision on logits [classes + durations]; nothing once done.
+int launch_tdt_decide(wh_ctx *ctx, const float *logits, TdtState *st, const TdtConfig &cfg);
+// One LSTM layer's cell over its gates (4n) into h, c (n each) in place; nothing while *idle != 0.
+int launch_tdt_cell(wh_ctx *ctx, const float *gates, float *h, float *c, int n, const int *idle);
+// Greedy CTC (src/gigaam/decoder.rs:135-151) over `frames` rows of `width` logits (the first
+// `classes` columns): ids (frames ints) is scratch; up to cap (token, frame) pairs into out, the
+// count into *count (all device memory).
+int launch_ctc(wh_ctx *ctx, const float *logits, int frames, int width, int classes, int blank, int *ids,
+               uint32_t *out, int cap, int *count);

@@ -18,6 +18,8 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -346,6 +348,42 @@ class Loader {
     return l;
   }
 
+  // One linear layer from weight tensors joined along k: row r is [names[0] row r | names[1] row r |
+  // ...] (the LSTM's [Wx | Wh] over [x | h]).  Same type and rows; whole 32-weight blocks each.
+  wh_linear *joined(const std::vector<std::string> &names, const std::vector<float> &bias) {
+    if (!err.empty()) return nullptr;
+    std::vector<const Tensor *> ts;
+    std::vector<size_t> rb;
+    int k = 0, rows = -1, type = -1;
+    for (const std::string &name : names) {
+      const Tensor *t = need(name);
+      if (!t) return nullptr;
+      const int ki = (int)t->dims[0], ri = (int)(t->count() / t->dims[0]);
+      if ((type >= 0 && t->type != type) || (rows >= 0 && ri != rows) || ki % 32) {
+        fail(name + ": joined weights differ in type or rows, or k is not a multiple of 32");
+        return nullptr;
+      }
+      type = t->type, rows = ri, k += ki;
+      ts.push_back(t);
+      rb.push_back(wh_type_bytes(type, (size_t)ki));
+    }
+    size_t row_bytes = 0;
+    for (size_t b : rb) row_bytes += b;
+    std::vector<uint8_t> host(row_bytes * rows);
+    for (int r = 0; r < rows; r++) {
+      uint8_t *dst = host.data() + (size_t)r * row_bytes;
+      for (size_t i = 0; i < ts.size(); dst += rb[i], i++) memcpy(dst, ts[i]->data + (size_t)r * rb[i], rb[i]);
+    }
+    wh_tensor w{host.data(), type, k, rows};
+    wh_linear *l = nullptr;
+    if (wh_linear_new(ctx_, &w, 1, bias.data(), (int)bias.size(), 0, &l)) {
+      fail(names[0] + ": " + ctx_->error);
+      return nullptr;
+    }
+    linears.push_back(l);
+    return l;
+  }
+
   void fail(const std::string &m) {
     if (err.empty()) err = m;
   }
@@ -362,6 +400,8 @@ class Loader {
 
 enum Arch { GIGAAM = 0, PARAKEET = 1, WHISPER = 2 };
 constexpr intptr_t WHISPER_STEP = 16;  // the recording key of a Whisper decoder step
+constexpr intptr_t TDT_CHUNK = 17;     // the recording key of a run of TDT decisions
+constexpr int TDT_DECISIONS = 32;      // decisions per recorded run (the host looks at the state between runs)
 
 struct Block {
   Chan norm_ff1, norm_attn, norm_conv, norm_ff2, norm_out, conv_norm, dw;
@@ -417,6 +457,18 @@ struct wh_model {
   std::vector<HostMat> wx, wh;
   std::vector<std::vector<float>> lstm_b;
   std::vector<float> pred_b, out_b;
+  // The same decoder on the device (greedy.hip): [Wx | Wh] per LSTM layer with its bias, the joint's
+  // projections, the embedding table in f32; the loop's buffers [h slots (layers + 1)·hidden | c
+  // layers·hidden | gates | pred | z | logits], its state and (token, frame) list.
+  std::vector<wh_linear *> tdt_lstm;
+  wh_linear *tdt_pred = nullptr, *tdt_out = nullptr;
+  float *tdt_embed = nullptr, *tdt_buf = nullptr;
+  TdtState *tdt_st = nullptr;
+  uint32_t *tdt_list = nullptr;
+  int tdt_list_cap = 0;
+  // Greedy CTC on the device: [ids (frames) | count | pairs], sized for ctc_cap frames.
+  int *ctc_buf = nullptr;
+  int ctc_cap = 0;
   // Whisper
   int frames = 1500, dec_layers = 0, dec_heads = 0, dec_ff = 0, vocab = 0, context = 0;
   wh_linear *wconv0 = nullptr, *wconv1 = nullptr, *token_embd = nullptr;
@@ -611,6 +663,16 @@ bool load_parakeet(const Gguf &g, Loader &L, wh_model *m, std::string &err) {
     m->pred_b = L.f32s("joint.pred.bias", m->joint);
     m->out_w = host_mat(L, "joint.out.weight");
     m->out_b = L.f32s("joint.out.bias", (size_t)(m->classes + m->durations.size()));
+    // The device copy; the joined LSTM layers need whole blocks of the hidden size.
+    if (m->hidden % 32 == 0 && m->embed_h.k == m->hidden && m->durations.size() <= 16) {
+      for (int l = 0; l < m->lstm_layers; l++) {
+        std::string p = "pred.lstm." + std::to_string(l);
+        m->tdt_lstm.push_back(L.joined({p + ".Wx", p + ".Wh"}, m->lstm_b[l]));
+      }
+      m->tdt_pred = L.linear({"joint.pred"}, true);
+      m->tdt_out = L.linear({"joint.out"}, true);
+      m->tdt_embed = L.upload(m->embed_h.w);
+    }
   }
   return L.err.empty();
 }
@@ -1136,6 +1198,143 @@ int tdt_greedy(const wh_model *m, const float *enc, int frames, int width, uint3
   return count;
 }
 
+// ---- greedy decoding on the device
+
+// Offsets (floats) of the TDT loop's buffers in tdt_buf; each part starts on a 64-float boundary.
+struct TdtBufs {
+  float *h, *c, *gates, *pred, *z, *logits;
+  size_t total;
+};
+
+TdtBufs tdt_bufs(const wh_model *m, float *base) {
+  auto up = [](size_t n) { return (n + 63) / 64 * 64; };
+  const size_t n = m->hidden, L = m->lstm_layers;
+  size_t at = 0;
+  TdtBufs b;
+  b.h = base + at, at += up((L + 1) * n);
+  b.c = base + at, at += up(L * n);
+  b.gates = base + at, at += up(wh_linear_width(m->tdt_lstm[0]));
+  b.pred = base + at, at += up(wh_linear_width(m->tdt_pred));
+  b.z = base + at, at += up(m->joint);
+  b.logits = base + at, at += up(wh_linear_width(m->tdt_out));
+  b.total = at;
+  return b;
+}
+
+TdtConfig tdt_config(const wh_model *m) {
+  TdtConfig cfg{};
+  cfg.classes = m->classes;
+  cfg.ndur = (int)m->durations.size();
+  cfg.blank = m->blank;
+  cfg.max_symbols = m->max_symbols;
+  cfg.global = m->global;
+  for (int i = 0; i < cfg.ndur; i++) cfg.durations[i] = m->durations[i];
+  return cfg;
+}
+
+// Decoder::predict (src/parakeet/decoder.rs:111-133) on the device: per LSTM layer one GEMV of
+// [Wx | Wh] over the slots [x | h] (slot 0 holds the token's embedding, slot l + 1 layer l's h) and
+// the cell, then the joint's predictor projection.  With idle, every launch is switched by it.
+int tdt_predict(wh_model *m, const TdtBufs &b, const int *idle) {
+  wh_ctx *c = m->ctx;
+  const int n = m->hidden;
+  for (int l = 0; l < m->lstm_layers; l++) {
+    CK(launch_gemv(c, b.h + (size_t)l * n, m->tdt_lstm[l], b.gates, WH_BIAS, 1.0f, 0, nullptr, nullptr, nullptr,
+                   nullptr, idle));
+    CK(launch_tdt_cell(c, b.gates, b.h + (size_t)(l + 1) * n, b.c + (size_t)l * n, n, idle));
+  }
+  return launch_gemv(c, b.h + (size_t)m->lstm_layers * n, m->tdt_pred, b.pred, WH_BIAS, 1.0f, 0, nullptr, nullptr,
+                     nullptr, nullptr, idle);
+}
+
+// `count` decisions of the TDT loop (src/parakeet/decoder.rs:158-191): the joint on the current frame
+// (Decoder::joint, :135-149), the decision, and the predictor on an emitted token.
+int tdt_decisions(wh_model *m, int count) {
+  wh_ctx *c = m->ctx;
+  const TdtBufs b = tdt_bufs(m, m->tdt_buf);
+  const TdtConfig cfg = tdt_config(m);
+  for (int i = 0; i < count; i++) {
+    CK(launch_tdt_joint_in(c, b.pred, b.z, m->joint, m->tdt_st));
+    CK(launch_gemv(c, b.z, m->tdt_out, b.logits, WH_BIAS, 1.0f, 0, nullptr, nullptr, nullptr, nullptr,
+                   &m->tdt_st->done));
+    CK(launch_tdt_decide(c, b.logits, m->tdt_st, cfg));
+    CK(launch_tdt_embed(c, m->tdt_embed, m->hidden, b.h, m->tdt_st));
+    CK(tdt_predict(m, b, &m->tdt_st->idle));
+  }
+  return WH_OK;
+}
+
+// Decoder::decode (src/parakeet/decoder.rs:91-103) over an encoder output in device memory.
+int tdt_greedy_device(wh_model *m, const float *enc, int frames, int width, uint32_t *out, int cap) {
+  wh_ctx *c = m->ctx;
+  if (m->tdt_lstm.empty() || !m->tdt_pred || !m->tdt_out || !m->tdt_embed)
+    return wh_fail(c, WH_EARG, "model has no device TDT decoder");
+  if (width < m->joint) return wh_fail(c, WH_EARG, "encoder width %d is below the joint's %d", width, m->joint);
+  if (frames == 0) return 0;
+  if (!m->tdt_buf) {
+    CK(wh_alloc(c, tdt_bufs(m, nullptr).total, &m->tdt_buf));
+    float *st = nullptr;
+    CK(wh_alloc(c, (sizeof(TdtState) + 3) / 4, &st));
+    m->tdt_st = (TdtState *)st;
+  }
+  // At most max_symbols decisions per frame (and the global budget is as many), so no more tokens.
+  const long most = (long)frames * m->max_symbols;
+  if (most > INT_MAX / 2) return wh_fail(c, WH_EARG, "tdt: %d frames is too many", frames);
+  const int need = (int)std::max(1L, std::min((long)cap, most));
+  if (need > m->tdt_list_cap) {
+    if (m->tdt_list) CK(wh_free(c, m->tdt_list));
+    m->tdt_list = nullptr, m->tdt_list_cap = 0;
+    float *p = nullptr;
+    CK(wh_alloc(c, (size_t)2 * need, &p));
+    m->tdt_list = (uint32_t *)p, m->tdt_list_cap = need;
+  }
+  TdtState init{};
+  init.left = m->global ? (int)most : -1;
+  init.idle = 1;
+  init.frames = frames;
+  init.width = width;
+  init.cap = need;
+  init.enc = enc;
+  init.out = m->tdt_list;
+  CK(launch_tdt_init(c, m->tdt_st, init));
+  // The first predict(None): a zero input and state.
+  const TdtBufs b = tdt_bufs(m, m->tdt_buf);
+  CK(launch_zero(c, b.h, (size_t)(b.gates - b.h) * 4));
+  CK(tdt_predict(m, b, nullptr));
+  TdtState s{};
+  for (;;) {
+    CK(run_recorded(m, {TDT_CHUNK}, [&] { return tdt_decisions(m, TDT_DECISIONS); }));
+    CK(wh_read(c, &s, m->tdt_st, sizeof s));
+    if (s.done) break;
+    if (s.decisions > most) return wh_fail(c, WH_EGPU, "tdt: %d decisions without reaching the end", s.decisions);
+  }
+  const int k = std::min(s.count, cap);
+  if (k > 0) CK(wh_read(c, out, m->tdt_list, (size_t)k * 8));
+  return s.count;
+}
+
+// Greedy CTC (src/gigaam/decoder.rs:135-151) over logits in device memory.
+int ctc_greedy_device(wh_model *m, const float *logits, int frames, int width, uint32_t *out, int cap) {
+  wh_ctx *c = m->ctx;
+  if (width < m->outputs || m->outputs <= 0) return WH_EARG;
+  if (frames == 0) return 0;
+  if (frames > m->ctc_cap) {
+    if (m->ctc_buf) CK(wh_free(c, m->ctc_buf));
+    m->ctc_buf = nullptr, m->ctc_cap = 0;
+    float *p = nullptr;
+    CK(wh_alloc(c, (size_t)3 * frames + 1, &p));
+    m->ctc_buf = (int *)p, m->ctc_cap = frames;
+  }
+  int *ids = m->ctc_buf, *count = ids + frames;
+  uint32_t *pairs = (uint32_t *)(count + 1);
+  CK(launch_ctc(c, logits, frames, width, m->outputs, m->blank, ids, pairs, frames, count));
+  int n = 0;
+  CK(wh_read(c, &n, count, 4));
+  const int k = std::min(n, cap);
+  if (k > 0) CK(wh_read(c, out, pairs, (size_t)k * 8));
+  return n;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1178,6 +1377,8 @@ void wh_model_free(wh_model *m) {
   for (uint32_t *p : m->own) wh_free(m->ctx, p);
   for (uint32_t *p : m->cross) wh_free(m->ctx, p);
   if (m->ids) wh_free(m->ctx, m->ids);
+  for (void *p : {(void *)m->tdt_buf, (void *)m->tdt_st, (void *)m->tdt_list, (void *)m->ctc_buf})
+    if (p) wh_free(m->ctx, p);
   delete m;
 }
 
@@ -1273,6 +1474,14 @@ int wh_model_greedy(wh_model *m, const float *enc, int frames, int width, uint32
     return tdt_greedy(m, enc, frames, width, out, cap);
   }
   return wh_fail(m->ctx, WH_EARG, "Whisper decodes through wh_whisper_step");
+}
+
+int wh_model_greedy_device(wh_model *m, const float *enc_dev, int frames, int width, uint32_t *out, int cap) {
+  if (!m || !enc_dev || frames < 0 || width <= 0 || !out || cap < 0) return WH_EARG;
+  (void)hipSetDevice(m->ctx->device);
+  if (m->arch == GIGAAM) return ctc_greedy_device(m, enc_dev, frames, width, out, cap);
+  if (m->arch == PARAKEET) return tdt_greedy_device(m, enc_dev, frames, width, out, cap);
+  return wh_fail(m->ctx, WH_EARG, "Whisper decodes through wh_whisper_decode");
 }
 
 int wh_whisper_begin(wh_model *m, const float *enc, int frames) {

@@ -203,7 +203,9 @@ def build_parakeet(c, b):
     w.u32("stt.parakeet.predictor.n_layers", c["lstm_layers"])
     w.u32("stt.parakeet.predictor.vocab", vocab)
     w.i32s("stt.parakeet.tdt.durations", c["durations"])
-    w.u32("stt.parakeet.tdt.max_symbols", 10)
+    w.u32("stt.parakeet.tdt.max_symbols", c.get("max_symbols", 10))
+    if "symbol_budget" in c:
+        w.str("stt.parakeet.tdt.symbol_budget", c["symbol_budget"])
     _vocab(w, vocab, True)
     w.u32("tokenizer.ggml.unknown_token_id", 0)
     w.u32("tokenizer.ggml.blank_token_id", vocab - 1)
@@ -227,7 +229,12 @@ def build_parakeet(c, b):
             b.w.tensor(name, [hidden, 4 * hidden], b.wtype, gguf.encode(b.normal(name, 4 * hidden * hidden), b.wtype))
         b.f32(f"pred.lstm.{l}.bias", [4 * hidden], b.normal(f"pred.lstm.{l}.bias", 4 * hidden, 1.0 if b.perturb else 0.02))
     b.linear("joint.pred", [hidden, joint])
-    b.linear("joint.out", [joint, vocab + len(c["durations"])])
+    # blank_bias: added to the blank's output bias (a decoder that emits blanks often).
+    outs = vocab + len(c["durations"])
+    b.linear("joint.out", [joint, outs], False)
+    ob = b.normal("joint.out.bias", outs)
+    ob[vocab - 1] += np.float32(c.get("blank_bias", 0.0))
+    b.f32("joint.out.bias", [outs], ob)
 
 
 def sinusoids(length, channels, max_timescale=10000.0):

@@ -139,6 +139,30 @@ def gemm_replay(name, reps=50):
     return us, 2.0 * int(m) * int(n) * int(k)
 
 
+def attention_replay(reps=50, t=750, heads=8, hd=128):
+    """The Parakeet block's relative-position attention (t 750, 8 heads of 128) through the C ABI,
+    back to back: packing, the flash kernel and the key-split merge; returns us per call and the
+    flash kernel's flops (4·H·T²·hd + 2·H·T²·hd for the position band)."""
+    import numpy as np
+
+    import wavo_amd as wa
+
+    d = heads * hd
+    rng = np.random.default_rng(3)
+    g2 = wa.Gpu(0)
+    qb = g2.upload(rng.standard_normal((t, 4 * d), dtype=np.float32))
+    pb = g2.upload(rng.standard_normal((2 * t + 15, d), dtype=np.float32))
+    ob = g2.buffer(t * d)
+    run = lambda: g2.attention(qb, None, pb, ob, t, heads, hd, -1)
+    for _ in range(5):
+        run()
+    g2.sync()
+    us = time_region(g2, run, reps) * 1e3
+    del qb, pb, ob
+    g2.close()
+    return us, 6.0 * heads * t * t * hd
+
+
 def hbm_copy(gpu, nbytes=1 << 30):
     """The library's copy kernel over `nbytes` (device to device): read + write bytes per second."""
     a, b = gpu.buffer(nbytes // 4), gpu.buffer(nbytes // 4)
@@ -334,7 +358,8 @@ def main():
     ap.add_argument("--no-gemv", action="store_true", help="skip the decoder GEMV and decoder step measurements")
     ap.add_argument("--replay", metavar="NAME", default=None,
                     help="only the back-to-back launches of this GEMM configuration (a roofline.kernel value), "
-                         "for rocprofv3 passes over exactly those launches")
+                         "or 'attention_rel' for the Parakeet attention call, for rocprofv3 passes over exactly "
+                         "those launches")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -350,6 +375,11 @@ def main():
     import wavo_amd as wa
     from wavo_amd import synth
 
+    if args.replay == "attention_rel":
+        us, flops = attention_replay()
+        print(json.dumps({"replayed": args.replay, "us_per_call": round(us, 3),
+                          "tflops": round(flops / (us * 1e-6) / 1e12, 2)}), flush=True)
+        return
     if args.replay:
         if not GEMM_NAME.match(args.replay):
             sys.exit(f"--replay takes a GEMM configuration name like the bench line's roofline.kernel: {args.replay!r}")

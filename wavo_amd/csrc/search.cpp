@@ -14,7 +14,7 @@
 #include <cmath>
 #include <vector>
 
-#include "internal.h"
+#include "../../include/wavo_hip.h"
 
 namespace {
 

@@ -57,7 +57,36 @@ struct wh_ctx {
   // lookup failed, with its error).
   void *noalloc = nullptr;
   hipError_t noalloc_error = hipSuccess;
+  // Staged uploads (stage_upload): a second stream for host-to-device copies, a ring of pinned host
+  // buffers (allocated at the first upload), per slot the event of its last copy, and the fill of
+  // the current slot.
+  hipStream_t upload = nullptr;
+  static constexpr int STAGE_SLOTS = 4;
+  void *pinned[STAGE_SLOTS] = {};
+  hipEvent_t pinned_done[STAGE_SLOTS] = {};
+  bool pinned_used[STAGE_SLOTS] = {};
+  int pinned_slot = 0;
+  size_t pinned_fill = 0;
+  hipEvent_t upload_fence = nullptr;
 };
+
+// A file whose mapping [base, base + size) a staged upload reads with pread instead of through the
+// mapping: no page faults, the kernel copies from the page cache (or the disk) into pinned memory.
+struct StageFile {
+  int fd;
+  const uint8_t *base;
+  size_t size;
+};
+// Copies `bytes` of host memory (read from `file` where they lie in its mapping) into pinned staging
+// and queues their copy to `dst` on the context's upload stream; returns once `src` may be reused.
+int stage_upload(wh_ctx *ctx, void *dst, const void *src, size_t bytes, const StageFile *file = nullptr);
+// Work queued on ctx->stream after this call waits for every staged upload so far.
+int stage_fence(wh_ctx *ctx);
+// Waits for every staged upload and reports their errors.
+int stage_wait(wh_ctx *ctx);
+// wh_linear_new with the weights read through `file` where they lie in its mapping.
+int linear_new(wh_ctx *ctx, const wh_tensor *ws, int count, const float *bias, int n_bias, int pad_k,
+               wh_linear **out, const StageFile *file);
 
 // Looks up the device address of wh_gemm_noalloc's workspace on ctx's device (current), once per device.
 int gemm_noalloc_init(wh_ctx *ctx);

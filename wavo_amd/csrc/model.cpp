@@ -54,16 +54,20 @@ class Gguf {
  public:
   ~Gguf() {
     if (map_) munmap(map_, len_);
+    if (fd_ >= 0) ::close(fd_);
   }
+
+  // The mapping as a source of staged uploads: weight bytes are read with pread into pinned memory.
+  StageFile file() const { return StageFile{fd_, map_, len_}; }
 
   bool open(const char *path, std::string &err) {
     int fd = ::open(path, O_RDONLY);
     if (fd < 0) return err = std::string("cannot open ") + path, false;
+    fd_ = fd;
     struct stat st;
     fstat(fd, &st);
     len_ = (size_t)st.st_size;
     void *m = mmap(nullptr, len_, PROT_READ, MAP_PRIVATE, fd, 0);
-    ::close(fd);
     if (m == MAP_FAILED) return err = "cannot map the file", false;
     map_ = (uint8_t *)m;
     p_ = map_;
@@ -207,6 +211,7 @@ class Gguf {
 
   uint8_t *map_ = nullptr;
   size_t len_ = 0;
+  int fd_ = -1;
   const uint8_t *p_ = nullptr, *end_ = nullptr;
   bool bad_ = false;
   std::map<std::string, Value> kv_;
@@ -305,7 +310,7 @@ class Loader {
       return nullptr;
     }
     owned.push_back(p);
-    if (!v.empty() && wh_write(ctx_, p, v.data(), v.size() * 4)) fail(ctx_->error);
+    if (!v.empty() && stage_upload(ctx_, p, v.data(), v.size() * 4)) fail(ctx_->error);
     return p;
   }
 
@@ -340,7 +345,9 @@ class Loader {
     }
     const std::vector<float> &bb = override_bias.empty() ? b : override_bias;
     wh_linear *l = nullptr;
-    if (wh_linear_new(ctx_, ws.data(), (int)ws.size(), bb.empty() ? nullptr : bb.data(), (int)bb.size(), pad_k, &l)) {
+    const StageFile file = g_.file();
+    if (linear_new(ctx_, ws.data(), (int)ws.size(), bb.empty() ? nullptr : bb.data(), (int)bb.size(), pad_k, &l,
+                   &file)) {
       fail(names[0] + ": " + ctx_->error);
       return nullptr;
     }
@@ -376,7 +383,7 @@ class Loader {
     }
     wh_tensor w{host.data(), type, k, rows};
     wh_linear *l = nullptr;
-    if (wh_linear_new(ctx_, &w, 1, bias.data(), (int)bias.size(), 0, &l)) {
+    if (linear_new(ctx_, &w, 1, bias.data(), (int)bias.size(), 0, &l, nullptr)) {
       fail(names[0] + ": " + ctx_->error);
       return nullptr;
     }
@@ -1357,6 +1364,8 @@ int wh_model_load(wh_ctx *ctx, const char *path, wh_model **out) {
   else ok = false, err = "unsupported general.architecture \"" + arch + "\"";
   m->owned = L.owned;
   m->linears = L.linears;
+  // Every staged upload done (and its errors seen) before the model is handed out.
+  if (ok && L.err.empty() && (stage_fence(ctx) || stage_wait(ctx))) L.fail(ctx->error);
   if (!ok || !L.err.empty()) {
     std::string msg = err.empty() ? L.err : err;
     wh_model_free(m.release());

@@ -3,11 +3,14 @@
 // (:461-577), buffer/readback/upload/write (:675-750), upload_linear (:770-834), run/complete
 // (:906-1002).  One HIP stream per context replaces wgpu's queue; errors that wgpu reports through
 // callbacks (:508-512, :995-1000) surface here as HIP status codes at the next wh_sync/wh_read.
+#include <unistd.h>
+
 #include <algorithm>
 #include <cstdarg>
 #include <cstdlib>
 #include <cstdio>
 #include <cstring>
+#include <thread>
 #include <vector>
 
 #include "internal.h"
@@ -138,11 +141,124 @@ void wh_close(wh_ctx *ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->upload) {
+    (void)hipStreamSynchronize(ctx->upload);
+    for (int i = 0; i < wh_ctx::STAGE_SLOTS; i++) {
+      if (ctx->pinned[i]) (void)hipHostFree(ctx->pinned[i]);
+      if (ctx->pinned_done[i]) (void)hipEventDestroy(ctx->pinned_done[i]);
+    }
+    if (ctx->upload_fence) (void)hipEventDestroy(ctx->upload_fence);
+    (void)hipStreamDestroy(ctx->upload);
+  }
   for (hipEvent_t e : ctx->events) (void)hipEventDestroy(e);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------ staged uploads
+// Weights reach the device through a ring of pinned host buffers and a second stream: the host fills
+// one slot (memcpy, or pread from the model file: no page faults on its mapping) while the DMA
+// engine drains the others, and several host threads fill a large piece together.  Small pieces
+// share a slot (each copy is queued at once; the slot's event marks its last copy).
+
+constexpr size_t STAGE_BYTES = (size_t)16 << 20;
+constexpr size_t STAGE_SPLIT = (size_t)2 << 20;  // pieces at least this large are filled by threads
+constexpr int STAGE_THREADS = 8;
+
+static int stage_init(wh_ctx *ctx) {
+  if (ctx->upload) return WH_OK;
+  hipError_t e = hipStreamCreateWithFlags(&ctx->upload, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->upload_fence, hipEventDisableTiming);
+  for (int i = 0; i < wh_ctx::STAGE_SLOTS && e == hipSuccess; i++) {
+    e = hipHostMalloc(&ctx->pinned[i], STAGE_BYTES, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->pinned_done[i], hipEventDisableTiming);
+  }
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return wh_fail(ctx, e == hipErrorOutOfMemory ? WH_EOOM : WH_EGPU, "upload staging: %s", hipGetErrorString(e));
+  }
+  return WH_OK;
+}
+
+// dst[0..n) = src[0..n), read from the file where src lies in its mapping.
+static bool fill_part(uint8_t *dst, const uint8_t *src, size_t n, const StageFile *f) {
+  if (f && src >= f->base && src + n <= f->base + f->size) {
+    off_t at = (off_t)(src - f->base);
+    while (n) {
+      ssize_t r = pread(f->fd, dst, n, at);
+      if (r <= 0) return false;
+      dst += r, at += r, n -= (size_t)r;
+    }
+    return true;
+  }
+  memcpy(dst, src, n);
+  return true;
+}
+
+static bool fill(uint8_t *dst, const uint8_t *src, size_t n, const StageFile *f) {
+  if (n < STAGE_SPLIT) return fill_part(dst, src, n, f);
+  const int parts = STAGE_THREADS;
+  const size_t per = (n / parts + 4095) / 4096 * 4096;
+  bool ok[STAGE_THREADS];
+  std::vector<std::thread> th;
+  for (int i = 0; i < parts; i++) {
+    const size_t lo = std::min(n, i * per), hi = std::min(n, lo + per);
+    ok[i] = true;
+    if (hi > lo) th.emplace_back([&, i, lo, hi] { ok[i] = fill_part(dst + lo, src + lo, hi - lo, f); });
+  }
+  for (auto &t : th) t.join();
+  for (int i = 0; i < parts; i++)
+    if (!ok[i]) return false;
+  return true;
+}
+
+int stage_upload(wh_ctx *ctx, void *dst, const void *src, size_t bytes, const StageFile *file) {
+  if (!bytes) return WH_OK;
+  if (int rc = stage_init(ctx)) return rc;
+  const uint8_t *s = (const uint8_t *)src;
+  uint8_t *d = (uint8_t *)dst;
+  for (size_t off = 0; off < bytes;) {
+    const size_t n = std::min(STAGE_BYTES, bytes - off);
+    if (ctx->pinned_fill + n > STAGE_BYTES) {  // the next slot, once its last copy is done
+      ctx->pinned_slot = (ctx->pinned_slot + 1) % wh_ctx::STAGE_SLOTS;
+      ctx->pinned_fill = 0;
+    }
+    const int k = ctx->pinned_slot;
+    if (ctx->pinned_fill == 0 && ctx->pinned_used[k]) {
+      hipError_t e = hipEventSynchronize(ctx->pinned_done[k]);
+      if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "upload: %s", hipGetErrorString(e));
+    }
+    uint8_t *p = (uint8_t *)ctx->pinned[k] + ctx->pinned_fill;
+    if (!fill(p, s + off, n, file)) return wh_fail(ctx, WH_EARG, "upload: reading the model file failed");
+    hipError_t e = hipMemcpyAsync(d + off, p, n, hipMemcpyHostToDevice, ctx->upload);
+    if (e == hipSuccess) e = hipEventRecord(ctx->pinned_done[k], ctx->upload);
+    if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "upload: %s", hipGetErrorString(e));
+    ctx->pinned_used[k] = true;
+    ctx->pinned_fill += (n + 255) / 256 * 256;
+    off += n;
+  }
+  return WH_OK;
+}
+
+int stage_fence(wh_ctx *ctx) {
+  if (!ctx->upload) return WH_OK;
+  hipError_t e = hipEventRecord(ctx->upload_fence, ctx->upload);
+  if (e == hipSuccess) e = hipStreamWaitEvent(ctx->stream, ctx->upload_fence, 0);
+  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "upload fence: %s", hipGetErrorString(e));
+  return WH_OK;
+}
+
+int stage_wait(wh_ctx *ctx) {
+  if (!ctx->upload) return WH_OK;
+  hipError_t e = hipStreamSynchronize(ctx->upload);
+  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "upload: %s", hipGetErrorString(e));
+  return WH_OK;
+}
+
+extern "C" {
 
 const char *wh_last_error(const wh_ctx *ctx) {
   return ctx ? ctx->error.c_str() : g_open_error.c_str();
@@ -174,6 +290,7 @@ int wh_free(wh_ctx *ctx, void *dptr) {
   if (!ctx) return WH_EARG;
   if (!dptr) return WH_OK;
   (void)hipSetDevice(ctx->device);
+  if (ctx->upload) (void)hipStreamSynchronize(ctx->upload);  // no staged copy into it still queued
   hipError_t e = hipFree(dptr);
   if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "hipFree: %s", hipGetErrorString(e));
   return WH_OK;
@@ -389,7 +506,15 @@ int wh_profile_read(wh_ctx *ctx, char *out, size_t len) {
 
 int wh_linear_new(wh_ctx *ctx, const wh_tensor *ws, int count, const float *bias, int n_bias,
                   int pad_k, wh_linear **out) {
+  return linear_new(ctx, ws, count, bias, n_bias, pad_k, out, nullptr);
+}
+
+}  // extern "C"
+
+int linear_new(wh_ctx *ctx, const wh_tensor *ws, int count, const float *bias, int n_bias, int pad_k,
+               wh_linear **out, const StageFile *file) {
   if (!ctx || !ws || count <= 0 || !out || n_bias < 0) return wh_fail(ctx, WH_EARG, "wh_linear_new: bad arguments");
+  if (ctx->recording) return wh_fail(ctx, WH_EARG, "wh_linear_new: weights cannot be created while recording");
   *out = nullptr;
   int type = ws[0].type, k = ws[0].k, rows = 0;
   for (int i = 0; i < count; i++) {
@@ -457,31 +582,37 @@ int wh_linear_new(wh_ctx *ctx, const wh_tensor *ws, int count, const float *bias
     wh_linear_free(ctx, l);
     return rc;
   }
-  if (!host.empty()) {
-    e = hipMemcpy(l->w, host.data(), wbytes, hipMemcpyHostToDevice);
-  } else {
-    size_t at = 0;
-    for (int i = 0; i < count && e == hipSuccess; i++) {
-      size_t b = l->row_bytes * ws[i].rows;
-      e = hipMemcpy(l->w + at, ws[i].data, b, hipMemcpyHostToDevice);
-      at += b;
-    }
-  }
-  if (e == hipSuccess) e = hipMemset(l->w + wbytes, 0, 256);
+  // The weights and the bias through the staged uploads; the 256 bytes of slack are zeros.
   std::vector<float> pb((size_t)(n > cols + dual ? n : cols + dual), 0.0f);
   if (n_bias) {
     memcpy(pb.data(), bias, sizeof(float) * rows);
     if (dual) memcpy(pb.data() + cols, bias + rows, sizeof(float) * dual);
   }
-  if (e == hipSuccess) e = hipMemcpy(l->bias, pb.data(), sizeof(float) * pb.size(), hipMemcpyHostToDevice);
-  if (e != hipSuccess) {
-    int rc = wh_fail(ctx, WH_EGPU, "weight upload: %s", hipGetErrorString(e));
+  static const uint8_t zeros[256] = {};
+  int rc = WH_OK;
+  if (!host.empty()) {
+    rc = stage_upload(ctx, l->w, host.data(), wbytes);
+  } else {
+    size_t at = 0;
+    for (int i = 0; i < count && rc == WH_OK; i++) {
+      size_t b = l->row_bytes * ws[i].rows;
+      rc = stage_upload(ctx, l->w + at, ws[i].data, b, file);
+      at += b;
+    }
+  }
+  if (rc == WH_OK) rc = stage_upload(ctx, l->w + wbytes, zeros, sizeof zeros);
+  if (rc == WH_OK) rc = stage_upload(ctx, l->bias, pb.data(), sizeof(float) * pb.size());
+  if (rc == WH_OK) rc = stage_fence(ctx);
+  if (rc != WH_OK) {
+    (void)stage_wait(ctx);
     wh_linear_free(ctx, l);
     return rc;
   }
   *out = l;
   return WH_OK;
 }
+
+extern "C" {
 
 int wh_linear_width(const wh_linear *l) { return l ? l->cols + l->dual : 0; }
 int wh_linear_k(const wh_linear *l) { return l ? l->k : 0; }
@@ -490,6 +621,7 @@ int wh_linear_type(const wh_linear *l) { return l ? l->type : -1; }
 void wh_linear_free(wh_ctx *ctx, wh_linear *l) {
   if (!l) return;
   if (ctx) (void)hipSetDevice(ctx->device);
+  if (ctx && ctx->upload) (void)hipStreamSynchronize(ctx->upload);  // no copy into it still queued
   if (l->w) (void)hipFree(l->w);
   if (l->bias) (void)hipFree(l->bias);
   delete l;

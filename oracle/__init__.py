@@ -107,6 +107,14 @@ def lib():
             "ox_top2_gap": (ctypes.c_float, [_fp, ctypes.c_int, ctypes.c_void_p, _u32p, ctypes.c_int]),
             "ox_whisper_retrieve": (ctypes.c_int, [ctypes.c_void_p, _u32p, ctypes.c_int, ctypes.c_int,
                                                    _ip, ctypes.c_int, _ip]),
+            "ox_fft": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+            "ox_fft_tables": (ctypes.c_int, [ctypes.c_int, _ip, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.c_void_p, _ip, _ip]),
+            "ox_parakeet_filterbank": (None, [_fp]),
+            "ox_parakeet_log_mel": (ctypes.c_int, [_fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _fp]),
+            "ox_parakeet_mel": (ctypes.c_int, [_fp, ctypes.c_int, _fp]),
+            "ox_gigaam_mel": (ctypes.c_int, [_fp, ctypes.c_int, _fp, _fp, ctypes.c_int, _fp]),
+            "ox_whisper_mel": (ctypes.c_int, [_fp, ctypes.c_int, _fp, _fp, ctypes.c_int, _fp]),
             "ox_threads": (ctypes.c_int, []),
             "ox_set_threads": (None, [ctypes.c_int]),
         }
@@ -304,6 +312,63 @@ def flatten(x, t, f, ch):
     y = np.zeros((t, f * ch), np.float32)
     lib().ox_flatten(px, _ptr(y), t, f, ch)
     return y
+
+
+def fft(x, f64=True):
+    """Fft::forward (src/fft.rs:72-104) of real x: (re, im) in float64 or float32."""
+    dt = np.float64 if f64 else np.float32
+    x = np.ascontiguousarray(x, dt)
+    re, im = np.zeros(len(x), dt), np.zeros(len(x), dt)
+    lib().ox_fft(len(x), int(f64), x.ctypes.data, re.ctypes.data, im.ctypes.data)
+    return re, im
+
+
+def parakeet_filterbank():
+    out = np.zeros((128, 257), np.float32)
+    lib().ox_parakeet_filterbank(_ptr(out))
+    return out
+
+
+def parakeet_log_mel(pcm, t0, t1):
+    """Frontend::log_mel (src/parakeet/frontend.rs:74-108): frames [t0, t1) of the whole pcm."""
+    pcm, pp = f32(pcm)
+    out = np.zeros((max(t1 - t0, 0), 128), np.float32)
+    if lib().ox_parakeet_log_mel(pp, len(pcm), t0, t1, _ptr(out)) < 0:
+        raise ValueError("bad frame range")
+    return out
+
+
+def parakeet_mel(pcm):
+    """Frontend::compute (src/parakeet/frontend.rs:52-72): [len / 160 + 1][128], empty below 3 frames."""
+    pcm, pp = f32(pcm)
+    n = lib().ox_parakeet_mel(pp, len(pcm), None)
+    out = np.zeros((n, 128), np.float32)
+    if n:
+        lib().ox_parakeet_mel(pp, len(pcm), _ptr(out))
+    return out
+
+
+def gigaam_mel(pcm, window, filters):
+    """Frontend::compute (src/gigaam/frontend.rs:50-71) with the GGUF's window and filterbank [mels][161]."""
+    pcm, pp = f32(pcm)
+    w, pw = f32(window)
+    f, pf = f32(filters)
+    n = lib().ox_gigaam_mel(pp, len(pcm), pw, pf, f.shape[0], None)
+    out = np.zeros((n, f.shape[0]), np.float32)
+    if n:
+        lib().ox_gigaam_mel(pp, len(pcm), pw, pf, f.shape[0], _ptr(out))
+    return out
+
+
+def whisper_mel(pcm, window, filters):
+    """Frontend::compute (src/whisper/frontend.rs:45-85) with the GGUF's window and filterbank [mels][201]."""
+    pcm, pp = f32(pcm)
+    w, pw = f32(window)
+    f, pf = f32(filters)
+    n = lib().ox_whisper_mel(pp, len(pcm), pw, pf, f.shape[0], None)
+    out = np.zeros((n, f.shape[0]), np.float32)
+    lib().ox_whisper_mel(pp, len(pcm), pw, pf, f.shape[0], _ptr(out))
+    return out
 
 
 def ctc(logits, blank):

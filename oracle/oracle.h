@@ -207,6 +207,24 @@ int ox_whisper_retrieve(const ox_whisper_ids *ids, const uint32_t *gen, int n, i
 int ox_threads(void);
 void ox_set_threads(int n);
 
+/* --- log-mel frontends (oracle/frontend.c) ------------------------------------------------------ */
+/* Fft::forward (src/fft.rs:72-104) of n real values: f64 (f64 != 0) or f32 arrays. */
+int ox_fft(int n, int f64, const void *x, void *re, void *im);
+/* Fft::new's tables (src/fft.rs:47-70): perm [n], leaf cos/sin [leaf][leaf], per stage the twiddles
+ * [stages][n / 2]; any pointer may be NULL. */
+int ox_fft_tables(int n, int *perm, double *leaf_cos, double *leaf_sin, double *tw_cos, double *tw_sin,
+                  int *leaf, int *stages);
+/* Parakeet (src/parakeet/frontend.rs): the Slaney filterbank [128][257]; log_mel of frames [t0, t1);
+ * compute: [samples / 160 + 1][128] normalized (returns the frame count, 0 below 3 frames; out NULL
+ * returns the count only). */
+void ox_parakeet_filterbank(float *out);
+int ox_parakeet_log_mel(const float *pcm, int samples, int t0, int t1, float *out);
+int ox_parakeet_mel(const float *pcm, int samples, float *out);
+/* GigaAM (src/gigaam/frontend.rs) and Whisper (src/whisper/frontend.rs) with the GGUF's window and
+ * filterbank [mels][n_fft / 2 + 1]; out NULL returns the frame count only. */
+int ox_gigaam_mel(const float *pcm, int samples, const float *window, const float *filters, int mels, float *out);
+int ox_whisper_mel(const float *pcm, int samples, const float *window, const float *filters, int mels, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -166,6 +166,10 @@ def build_gigaam(c, b):
     w.u32("stt.frontend.num_mels", c["mels"])
     _vocab(w, c["classes"], True)
     w.u32("tokenizer.ggml.blank_token_id", c["classes"] - 1)
+    # The frontend's tables as the converter stores them (src/gigaam/frontend.rs:28-45): periodic Hann
+    # of 320 and an HTK filterbank [mels][161].
+    b.f32("frontend.window", [320], hann_periodic(320))
+    b.f32("frontend.mel_filterbank", [161, c["mels"]], htk_filters(SR, 320, c["mels"]))
     d, m = c["d"], c["mels"]
     b.linear("enc.pre_encode.conv.0", [5, m, d])
     b.linear("enc.pre_encode.conv.2", [5, d, d])
@@ -268,6 +272,10 @@ def build_whisper(c, b):
     w.u32("stt.whisper.decoder.vocab_size", c["vocab"])
     w.u32("stt.whisper.decoder.max_target_positions", c["context"])
     w.u32("stt.whisper.encoder.num_mel_bins", c["mels"])
+    # The frontend's tables (src/whisper/frontend.rs:29-41): periodic Hann of 400 and a Slaney
+    # filterbank [mels][201].
+    b.f32("frontend.window", [400], hann_periodic(400))
+    b.f32("frontend.mel_filterbank", [201, c["mels"]], _mel_filters(SR, 400, c["mels"]).astype(np.float32))
     # Special ids as large-v3's layout: EOT 50257, SOT 50258, …, no-timestamps 50364, <|0.00|> 50365.
     vocab = c["vocab"]
     eot = min(50257, vocab - 110)
@@ -331,7 +339,8 @@ def model_path(name, small=False, seed=0, wtype=gguf.Q8_0, directory=None, pertu
     """A cached synthetic model file under `directory` (default /tmp/wavo_models)."""
     directory = directory or os.environ.get("WAVO_MODELS", "/tmp/wavo_models")
     os.makedirs(directory, exist_ok=True)
-    tag = f"{name}{'-small' if small else ''}-s{seed}-t{wtype}{'-p' if perturb else ''}.gguf"
+    # v2: the files carry the frontend's tables (GigaAM, Whisper).
+    tag = f"{name}{'-small' if small else ''}-s{seed}-t{wtype}{'-p' if perturb else ''}-v2.gguf"
     path = os.path.join(directory, tag)
     if not os.path.exists(path):
         write_model(path, (SMALL if small else CONFIGS)[name], seed, wtype, perturb)
@@ -384,6 +393,25 @@ def split_at_gaps(seconds, gaps, limit=60.0):
         start = end
     segs.append((start, seconds))
     return segs
+
+
+def hann_periodic(n):
+    """0.5 − 0.5·cos(2πi/n), i < n (torch.hann_window(n, periodic=True))."""
+    return (0.5 - 0.5 * np.cos(2.0 * np.pi * np.arange(n) / n)).astype(np.float32)
+
+
+def htk_filters(sr, n_fft, mels, fmin=0.0, fmax=None):
+    """HTK-scale triangular filterbank without area normalization [mels][n_fft/2 + 1]
+    (torchaudio's melscale_fbanks with mel_scale="htk", norm=None)."""
+    fmax = fmax or sr / 2
+    freqs = np.linspace(0.0, sr / 2, n_fft // 2 + 1)
+    mel = lambda f: 2595.0 * np.log10(1.0 + f / 700.0)
+    pts = 700.0 * (10.0 ** (np.linspace(mel(fmin), mel(fmax), mels + 2) / 2595.0) - 1.0)
+    diff = pts[1:] - pts[:-1]
+    slopes = pts[None, :] - freqs[:, None]
+    down = -slopes[:, :-2] / diff[:-1]
+    up = slopes[:, 2:] / diff[1:]
+    return np.maximum(0.0, np.minimum(down, up)).T.astype(np.float32)
 
 
 def _mel_filters(sr, n_fft, mels, fmin=0.0, fmax=None):

@@ -12,7 +12,9 @@ seconds ÷ that median (RTFx).  `host_io` is the same call timed on the host fro
 never as it.  `host_frontend_ms` (the numpy log-mel of the synthetic audio) and `tdt_decode_ms` (the
 TDT greedy decode on the host, as the reference runs it) are separate; `tdt_device` is the same decode
 on the device over the resident encoder output (wh_model_greedy_device, host clock, median of 5 calls
-after 2), with whether its tokens equal the host decode's.
+after 2), with whether its tokens equal the host decode's.  `audio_to_tokens` is the whole path on the
+device from 16 kHz PCM: the upload, the reference's Parakeet frontend (wh_model_mel), the encoder and
+the TDT decode, host clock (the step's `value` starts from a resident mel and stays the metric).
 
 Per-kernel figures come from one more call with per-launch profiling: each launch carries HIP start
 and stop events that the runtime stamps at the kernel's own start and end (hipExtLaunchKernel), on
@@ -476,6 +478,29 @@ def main():
     log(f"TDT decode: host {statistics.median(dec) * 1e3:.1f} ms, device {statistics.median(ddec) * 1e3:.2f} ms "
         f"({len(dtokens)} tokens, {'equal' if dtokens == tokens else 'different'})")
 
+    # Audio to tokens on the device: the PCM upload, the reference's Parakeet frontend (wh_model_mel,
+    # into the same mel buffer the step reads), the encoder and the TDT decode; host clock.
+    pcm_b = gpu.upload(pcm)
+    assert model.mel_frames(len(pcm)) == mel_frames
+
+    def audio_to_tokens():
+        gpu.write(pcm_b, pcm)
+        model.mel_device(pcm_b, len(pcm), melb)
+        model.encode_device(melb, mel_frames, outb)
+        return model.greedy_device(outb, frames, width)
+
+    e2e = []
+    for i in range(9):
+        t0 = time.perf_counter()
+        e2e_tokens = audio_to_tokens()
+        if i >= 2:
+            e2e.append(time.perf_counter() - t0)
+    mel_prof = profiled(gpu, lambda: model.mel_device(pcm_b, len(pcm), melb))
+    mel_us = sum(r["ms"] for r in mel_prof) * 1e3
+    e2e_med = statistics.median(e2e)
+    log(f"audio to tokens on the device: {e2e_med * 1e3:.2f} ms ({args.seconds / e2e_med:.0f}x real time), "
+        f"frontend {mel_us:.1f} us, {len(e2e_tokens)} tokens")
+
     # One call with every launch stamped: per-kernel in-step durations.
     prof = profiled(gpu, step)
     kern = {r["kernel"]: kernel_roofline(r) for r in prof}
@@ -552,6 +577,11 @@ def main():
         "tdt_device": {"ms_median": round(statistics.median(ddec) * 1e3, 3), "tokens": len(dtokens),
                        "equal_to_host": dtokens == tokens,
                        "what": "wh_model_greedy_device over the resident encoder output, host clock"},
+        "audio_to_tokens": {"ms_median": round(e2e_med * 1e3, 3), "rtfx": round(args.seconds / e2e_med, 1),
+                            "tokens": len(e2e_tokens), "frontend_us": round(mel_us, 2),
+                            "frontend_kernels": {r["kernel"]: round(r["ms"] * 1e3, 2) for r in mel_prof},
+                            "what": "PCM upload (pageable) + the Parakeet log-mel frontend (wh_model_mel) + encoder + "
+                                    "TDT decode on the device + tokens read back, host clock, median of 7 after 2"},
         "load": load,
         "gemv": gemv,
         "cpu_baseline": cpu,

@@ -85,7 +85,9 @@ void *wh_stream(wh_ctx *ctx);
  *   "gemm_shape_plans" "m,cols,k:bm,bn,wm,wn,stages,split;..." per call shape ("" clears);
  *   "gemm_kernel_only" "1": a k-split GEMM call stops after its GEMM kernel and leaves c unwritten
  *                      (to time that kernel alone, as a model step runs it); "0" restores;
- *   "attn_split"       "n": attention splits its key range n ways (0 = chosen per shape).
+ *   "attn_split"       "n": attention splits its key range n ways (0 = chosen per shape);
+ *   "mel_raw"          "1": wh_model_mel writes each filter's sum before the logarithm, without the
+ *                      normalization or scaling (to check the transforms bit for bit); "0" restores.
  * Unknown keys and malformed values return WH_EARG. */
 int wh_tune(wh_ctx *ctx, const char *key, const char *value);
 /* Profiling (no counterpart in the reference, whose timing lives in `wavo bench` and GPU timestamp
@@ -263,6 +265,15 @@ int wh_model_greedy(wh_model *m, const float *enc_host, int frames, int width, u
  * up to float rounding of the decoder's products (ties of near-equal logits may differ). */
 int wh_model_greedy_device(wh_model *m, const float *enc_dev, int frames, int width, uint32_t *out,
                            int cap);
+/* The family's log-mel frontend, Frontend::compute (src/parakeet/frontend.rs:52-72,
+ * src/gigaam/frontend.rs:50-71, src/whisper/frontend.rs:45-85), on the device: pcm_dev holds
+ * `samples` 16 kHz samples; writes the features [frames][mels] to mel_dev and their count to *frames
+ * (mel_dev NULL: the count only).  Parakeet: samples / 160 + 1 frames (0 below 3), normalized;
+ * GigaAM: full 320-sample frames; Whisper: 3000 frames for up to 30 s, else samples / 160.  GigaAM and
+ * Whisper take the window and filterbank the model file holds.  The transforms use the reference's
+ * operation order and tables, so the spectra are bit-identical; the logarithms are the device's
+ * (within an ulp of the host's). */
+int wh_model_mel(wh_model *m, const float *pcm_dev, int samples, float *mel_dev, int *frames);
 /* Whisper decoding on the device: wh_whisper_begin computes every layer's cross-attention K/V from
  * the encoder output (Decoder::record_cross, src/transformer.rs:243-248); wh_whisper_step runs one
  * token at position pos (Decoder::record_step, :254-290) and leaves the logits in logits_dev. */

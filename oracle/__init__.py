@@ -111,6 +111,7 @@ def lib():
             "ox_fft_tables": (ctypes.c_int, [ctypes.c_int, _ip, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                              ctypes.c_void_p, _ip, _ip]),
             "ox_parakeet_filterbank": (None, [_fp]),
+            "ox_mel_raw": (None, [ctypes.c_int]),
             "ox_parakeet_log_mel": (ctypes.c_int, [_fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _fp]),
             "ox_parakeet_mel": (ctypes.c_int, [_fp, ctypes.c_int, _fp]),
             "ox_gigaam_mel": (ctypes.c_int, [_fp, ctypes.c_int, _fp, _fp, ctypes.c_int, _fp]),
@@ -321,6 +322,11 @@ def fft(x, f64=True):
     re, im = np.zeros(len(x), dt), np.zeros(len(x), dt)
     lib().ox_fft(len(x), int(f64), x.ctypes.data, re.ctypes.data, im.ctypes.data)
     return re, im
+
+
+def mel_raw(on):
+    """on: the frontends return each filter's sum before the logarithm (no normalization or scale)."""
+    lib().ox_mel_raw(int(on))
 
 
 def parakeet_filterbank():

@@ -17,6 +17,12 @@
 
 #include "oracle.h"
 
+/* With g_raw set, the frontends write each filter's sum (the value the logarithm would take, before
+ * Parakeet's epsilon, GigaAM's clamp or Whisper's floor; 0 for Whisper's silent frames) and skip the
+ * normalization or scaling: the check of the transform and filter arithmetic bit for bit. */
+static int g_raw = 0;
+void ox_mel_raw(int on) { g_raw = on; }
+
 /* ------------------------------------------------------------------------------------------ FFT */
 
 /* The transform's tables for n = leaf · 2^stages (src/fft.rs:47-70). */
@@ -232,7 +238,7 @@ int ox_parakeet_log_mel(const float *pcm, int samples, int t0, int t1, float *ou
     for (int m = 0; m < PK_MELS; m++) {
       float e = 0.0f;
       for (int k = lo[m]; k < hi[m]; k++) e = fmaf(filters[m * PK_BINS + k], power[k], e);
-      out[t * PK_MELS + m] = logf(e + 1.0f / (float)(1 << 24));
+      out[t * PK_MELS + m] = g_raw ? e : logf(e + 1.0f / (float)(1 << 24));
     }
   }
   free(padded);
@@ -247,6 +253,7 @@ int ox_parakeet_mel(const float *pcm, int samples, float *out) {
   if (frames < 3) return 0;
   if (!out) return frames;
   ox_parakeet_log_mel(pcm, samples, 0, frames, out);
+  if (g_raw) return frames;
   const int n = frames - 1;
   for (int m = 0; m < PK_MELS; m++) {
     double mean = 0.0, var = 0.0;
@@ -299,6 +306,10 @@ int ox_gigaam_mel(const float *pcm, int samples, const float *window, const floa
     for (int k = 0; k < GA_BINS; k++) power[k] = buf[k] * buf[k] + buf[GA_FFT + k] * buf[GA_FFT + k];
     for (int m = 0; m < mels; m++) {
       float v = ox_dot(filters + m * GA_BINS + lo[m], power + lo[m], (size_t)(hi[m] - lo[m]));
+      if (g_raw) {
+        out[t * mels + m] = v;
+        continue;
+      }
       v = v < 1e-9f ? 1e-9f : v > 1e9f ? 1e9f : v;
       out[t * mels + m] = logf(v);
     }
@@ -353,7 +364,7 @@ int ox_whisper_mel(const float *pcm, int samples, const float *window, const flo
     int zero = 1;
     for (int i = 0; i < WS_FFT; i++) zero &= x[i] == 0.0f;
     if (zero) {
-      for (int m = 0; m < mels; m++) out[(size_t)t * mels + m] = silent;
+      for (int m = 0; m < mels; m++) out[(size_t)t * mels + m] = g_raw ? 0.0f : silent;
       continue;
     }
     for (int i = 0; i < WS_FFT; i++) frame[i] = x[i] * window[i];
@@ -369,8 +380,13 @@ int ox_whisper_mel(const float *pcm, int samples, const float *window, const flo
       for (int g = glo[m]; g < ghi[m]; g++) sum += ((W(4 * g) + W(4 * g + 1)) + W(4 * g + 2)) + W(4 * g + 3);
       sum += W(WS_BINS - 1);
 #undef W
-      out[(size_t)t * mels + m] = (float)log10(sum > 1e-10 ? sum : 1e-10);
+      out[(size_t)t * mels + m] = g_raw ? (float)sum : (float)log10(sum > 1e-10 ? sum : 1e-10);
     }
+  }
+  if (g_raw) {
+    fft_plan_free(&p);
+    free(padded), free(glo), free(ghi);
+    return frames;
   }
   float mx = -INFINITY;
   for (size_t i = 0; i < (size_t)frames * mels; i++) mx = out[i] > mx ? out[i] : mx;

@@ -224,6 +224,9 @@ int ox_parakeet_mel(const float *pcm, int samples, float *out);
  * filterbank [mels][n_fft / 2 + 1]; out NULL returns the frame count only. */
 int ox_gigaam_mel(const float *pcm, int samples, const float *window, const float *filters, int mels, float *out);
 int ox_whisper_mel(const float *pcm, int samples, const float *window, const float *filters, int mels, float *out);
+/* on != 0: the frontends write each filter's sum before the logarithm and skip the normalization or
+ * scaling (Whisper's silent frames 0). */
+void ox_mel_raw(int on);
 
 #ifdef __cplusplus
 }

@@ -78,6 +78,7 @@ SIGNATURES = {
     "wh_model_blocks": (_i, [_vp, _vp, _i, _i]),
     "wh_model_greedy": (_i, [_vp, _vp, _i, _i, _vp, _i]),
     "wh_model_greedy_device": (_i, [_vp, _vp, _i, _i, _vp, _i]),
+    "wh_model_mel": (_i, [_vp, _vp, _i, _vp, ctypes.POINTER(_i)]),
     "wh_whisper_begin": (_i, [_vp, _vp, _i]),
     "wh_whisper_step": (_i, [_vp, _i, _i, _vp]),
     "wh_whisper_ids_of": (_i, [_vp, _vp]),
@@ -476,6 +477,27 @@ class Model:
         if n < 0:
             self.gpu._check(n)
         return [(int(out[2 * i]), int(out[2 * i + 1])) for i in range(min(n, cap))]
+
+    def mel_frames(self, samples):
+        f = _i()
+        self.gpu._check(lib().wh_model_mel(self.h, None, samples, None, ctypes.byref(f)))
+        return f.value
+
+    def mel_device(self, pcm_buf, samples, mel_buf):
+        """The family's log-mel frontend on the device (wh_model_mel): returns the frame count."""
+        f = _i()
+        self.gpu._check(lib().wh_model_mel(self.h, _p(pcm_buf), samples, _p(mel_buf), ctypes.byref(f)))
+        return f.value
+
+    def mel(self, pcm):
+        """Log-mel features [frames][mels] of host audio, computed on the device."""
+        pcm = np.ascontiguousarray(pcm, np.float32)
+        frames = self.mel_frames(len(pcm))
+        if frames == 0:
+            return np.zeros((0, self.mels), np.float32)
+        pb, mb = self.gpu.upload(pcm if len(pcm) else np.zeros(1, np.float32)), self.gpu.buffer(frames * self.mels)
+        self.mel_device(pb, len(pcm), mb)
+        return self.gpu.read(mb, (frames, self.mels))
 
     def greedy_device(self, enc_buf, frames, width, cap=None):
         """The same greedy decoders run on the device over an encoder output in device memory

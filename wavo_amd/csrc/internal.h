@@ -38,6 +38,8 @@ struct wh_ctx {
   std::vector<std::array<int, 9>> gemm_shape_plans;
   // Attention key-split override set by wh_tune("attn_split", "n") (tuning sweeps only): 0 = chosen per shape.
   int attn_split = 0;
+  // wh_tune("mel_raw", "1") (checks only): the frontends write each filter's sum before the logarithm.
+  int mel_raw = 0;
   std::string name;
   std::string error;
   // Profiling (wh_profile): 0 off (default), 1 events around every launch, 2 named regions only.
@@ -245,3 +247,21 @@ int launch_tdt_cell(wh_ctx *ctx, const float *gates, float *h, float *c, int n, 
 // count into *count (all device memory).
 int launch_ctc(wh_ctx *ctx, const float *logits, int frames, int width, int classes, int blank, int *ids,
                uint32_t *out, int cap, int *count);
+
+// ---- the log-mel frontends on the device (frontend.hip) ----
+// One call's arguments: the audio, the transform's tables (as the element type: double for
+// Parakeet, float otherwise), the window, the filterbank [mels][n_fft / 2 + 1] and per filter its
+// span (Parakeet: nonzero bins; GigaAM: bins widened to 16; Whisper: 4-bin groups), the output.
+struct MelArgs {
+  const float *pcm;
+  int samples, len, hop, mels, leaf, stages;
+  const int *perm;
+  const void *leaf_cos, *leaf_sin, *tw_cos, *tw_sin, *window;
+  const float *filters;
+  const int *span;
+  float *out;
+  float silent;  // Whisper: the value of a frame of zeros
+  int raw;       // write each filter's sum before the logarithm; no normalization or scale
+};
+// kind 0 Parakeet, 1 GigaAM, 2 Whisper; `frames` frames into a.out; scratch: one float (Whisper).
+int launch_mel(wh_ctx *ctx, const MelArgs &a, int kind, int frames, float *scratch);

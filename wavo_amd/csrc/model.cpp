@@ -476,6 +476,17 @@ struct wh_model {
   // Greedy CTC on the device: [ids (frames) | count | pairs], sized for ctc_cap frames.
   int *ctc_buf = nullptr;
   int ctc_cap = 0;
+  // The log-mel frontend: GigaAM's and Whisper's window and filterbank [mels][n_fft / 2 + 1] from the
+  // GGUF (empty when the file has none), and the device plan built at the first wh_model_mel.
+  std::vector<float> fe_window, fe_filters;
+  struct MelDev {
+    bool ready = false;
+    int kind = 0, n = 0, mels = 0, leaf = 0, stages = 0;
+    float silent = 0.0f;
+    uint8_t *buf = nullptr;  // every table and the scratch float in one allocation
+    MelArgs args{};
+    float *scratch = nullptr;
+  } mel;
   // Whisper
   int frames = 1500, dec_layers = 0, dec_heads = 0, dec_ff = 0, vocab = 0, context = 0;
   wh_linear *wconv0 = nullptr, *wconv1 = nullptr, *token_embd = nullptr;
@@ -690,6 +701,10 @@ bool load_gigaam(const Gguf &g, Loader &L, wh_model *m, std::string &err) {
   m->relative = false;
   if (!conformer_config(g, m, "gigaam", err)) return false;
   m->mels = (int)g.integer("stt.frontend.num_mels", -1);
+  if (g.tensor("frontend.window") && g.tensor("frontend.mel_filterbank") && m->mels > 0) {
+    m->fe_window = L.f32s("frontend.window", 320);
+    m->fe_filters = L.f32s("frontend.mel_filterbank", (size_t)161 * m->mels);
+  }
   m->theta = (double)g.integer("stt.gigaam.encoder.pos_emb_max_len", 5000);
   m->conv0 = L.linear({"enc.pre_encode.conv.0"}, true);
   m->conv2 = L.linear({"enc.pre_encode.conv.2"}, true);
@@ -722,6 +737,10 @@ bool load_whisper(const Gguf &g, Loader &L, wh_model *m, std::string &err) {
       return err = "unsupported shape: d_model " + std::to_string(d) + ", " + std::to_string(heads) + " heads", false;
   }
   if (m->frames <= 0 || m->mels <= 0 || m->vocab <= 0 || m->context <= 0) return err = "bad Whisper metadata", false;
+  if (g.tensor("frontend.window") && g.tensor("frontend.mel_filterbank")) {
+    m->fe_window = L.f32s("frontend.window", 400);
+    m->fe_filters = L.f32s("frontend.mel_filterbank", (size_t)201 * m->mels);
+  }
   m->wconv0 = L.linear({"enc.conv.0"}, true, -1, {}, 1);
   m->wconv1 = L.linear({"enc.conv.1"}, true, -1, {}, 1);
   m->enc_pos = L.upload(L.f32s("enc.pos_emb.weight", (size_t)d * m->frames));
@@ -1342,6 +1361,175 @@ int ctc_greedy_device(wh_model *m, const float *logits, int frames, int width, u
   return n;
 }
 
+// ---- the log-mel frontend on the device
+
+// Fft::new's tables (src/fft.rs:47-70): the input permutation, the leaves' cos and sin [j][k] and per
+// radix-2 stage the twiddle of each output i < n / 2, from cos and sin of 2πi/n in f64.
+void fft_tables(int n, std::vector<int> &perm, std::vector<double> &lc, std::vector<double> &ls,
+                std::vector<double> &tc, std::vector<double> &ts, int &leaf, int &stages) {
+  leaf = n;
+  while (leaf % 2 == 0) leaf /= 2;
+  const int blocks = n / leaf;
+  std::vector<int> starts{0};
+  while ((int)starts.size() < blocks) {
+    std::vector<int> next;
+    for (int s : starts) next.push_back(2 * s);
+    for (int s : starts) next.push_back(2 * s + 1);
+    starts.swap(next);
+  }
+  perm.resize(n);
+  for (int i = 0; i < n; i++) perm[i] = starts[i % blocks] + i / blocks * blocks;
+  auto trig = [n](long i, double &c, double &s) {
+    const double phase = 6.283185307179586 * (double)i / (double)n;
+    c = std::cos(phase), s = std::sin(phase);
+  };
+  lc.resize((size_t)leaf * leaf), ls.resize((size_t)leaf * leaf);
+  for (int i = 0; i < leaf * leaf; i++) trig((long)(i / leaf) * (i % leaf) * blocks % n, lc[i], ls[i]);
+  stages = 0;
+  tc.clear(), ts.clear();
+  for (int size = 2 * leaf; size <= n; size *= 2, stages++)
+    for (int i = 0; i < n / 2; i++) {
+      double c, s;
+      trig((long)(i / (n / size)) * (n / size), c, s);
+      tc.push_back(c), ts.push_back(s);
+    }
+}
+
+// Parakeet's symmetric Hann(400) centred in 512 and Slaney filterbank [128][257] (src/parakeet/
+// frontend.rs:31-40, :113-141), in f64 and rounded to f32 as the reference builds them.
+void parakeet_tables(std::vector<double> &window, std::vector<float> &filters) {
+  window.assign(512, 0.0);
+  for (int i = 0; i < 512; i++) {
+    const int k = i - 56;
+    if (k >= 0 && k < 400) window[i] = 0.5 - 0.5 * std::cos(2.0 * 3.141592653589793 * (double)k / 399.0);
+  }
+  const double fsp = 200.0 / 3.0, min_log_hz = 1000.0, min_log_mel = min_log_hz / fsp;
+  const double log_step = std::log(6.4) / 27.0;
+  const double mel_max = min_log_mel + std::log(8000.0 / min_log_hz) / log_step;
+  double hz[130];
+  for (int m = 0; m < 130; m++) {
+    const double mel = mel_max * (double)m / 129.0;
+    hz[m] = mel < min_log_mel ? mel * fsp : min_log_hz * std::exp(log_step * (mel - min_log_mel));
+  }
+  filters.assign((size_t)128 * 257, 0.0f);
+  for (int m = 0; m < 128; m++) {
+    const double enorm = 2.0 / (hz[m + 2] - hz[m]);
+    for (int k = 0; k < 257; k++) {
+      const double f = 16000.0 * (double)k / 512.0;
+      const double lower = (f - hz[m]) / (hz[m + 1] - hz[m]), upper = (hz[m + 2] - f) / (hz[m + 2] - hz[m + 1]);
+      double v = std::min(lower, upper);
+      v = v > 0.0 ? v : 0.0;
+      filters[(size_t)m * 257 + k] = (float)(v * enorm);
+    }
+  }
+}
+
+// Per filter, the range its sum covers: Parakeet the nonzero bins (src/parakeet/frontend.rs:41-47),
+// GigaAM those widened to dot's 16-bin chunks (src/gigaam/frontend.rs:31-38), Whisper the 4-bin
+// groups below the last bin (src/whisper/frontend.rs:34-39).
+std::vector<int> mel_spans(const std::vector<float> &filters, int mels, int bins, int kind) {
+  std::vector<int> span(2 * (size_t)mels);
+  for (int m = 0; m < mels; m++) {
+    const float *f = filters.data() + (size_t)m * bins;
+    int first = -1, last = -1;
+    for (int k = 0; k < bins; k++)
+      if (f[k] != 0.0f) {
+        if (first < 0) first = k;
+        last = k;
+      }
+    int lo, hi;
+    if (kind == 0) {
+      lo = first < 0 ? 0 : first;
+      hi = last < 0 ? lo : last + 1;
+    } else if (kind == 1) {
+      lo = (first < 0 ? 0 : first) / 16 * 16;
+      hi = last < 0 ? 0 : last + 1;
+      hi = hi > bins / 16 * 16 ? bins : (hi + 15) / 16 * 16;
+      hi = std::max(hi, lo);
+    } else {
+      lo = (first < 0 ? 0 : first) / 4;
+      hi = last < 0 ? 0 : last / 4 + 1;
+      hi = std::min(std::max(hi, lo), (bins - 1) / 4);
+    }
+    span[2 * m] = lo, span[2 * m + 1] = hi;
+  }
+  return span;
+}
+
+int mel_frames(const wh_model *m, int samples) {
+  switch (m->arch) {
+    case PARAKEET: return samples / 160 + 1 >= 3 ? samples / 160 + 1 : 0;
+    case GIGAAM: return samples >= 320 ? (samples - 320) / 160 + 1 : 0;
+    default: return std::max(samples, 480000) / 160;
+  }
+}
+
+// The device tables of the model's frontend, in one allocation.
+int mel_plan(wh_model *m) {
+  auto &d = m->mel;
+  if (d.ready) return WH_OK;
+  wh_ctx *c = m->ctx;
+  const int kind = m->arch == PARAKEET ? 0 : m->arch == GIGAAM ? 1 : 2;
+  const int n = kind == 0 ? 512 : kind == 1 ? 320 : 400, bins = n / 2 + 1;
+  std::vector<double> window;
+  std::vector<float> filters;
+  int mels = m->mels;
+  if (kind == 0) {
+    if (mels != 128) return wh_fail(c, WH_EARG, "the Parakeet frontend makes 128 bins; the model takes %d", mels);
+    parakeet_tables(window, filters);
+  } else {
+    if (m->fe_window.size() != (size_t)n || m->fe_filters.size() != (size_t)bins * mels)
+      return wh_fail(c, WH_EARG, "the model file has no frontend.window / frontend.mel_filterbank");
+    window.assign(m->fe_window.begin(), m->fe_window.end());
+    filters = m->fe_filters;
+  }
+  std::vector<int> perm;
+  std::vector<double> lc, ls, tc, ts;
+  int leaf = 0, stages = 0;
+  fft_tables(n, perm, lc, ls, tc, ts, leaf, stages);
+  const std::vector<int> span = mel_spans(filters, mels, bins, kind);
+  // Layout: perm | leaf cos | leaf sin | twiddle cos | twiddle sin | window | filters | spans | scratch.
+  const size_t es = kind == 0 ? 8 : 4;
+  std::vector<size_t> sizes = {4 * perm.size(), es * lc.size(), es * ls.size(), es * tc.size(), es * ts.size(),
+                               es * window.size(), 4 * filters.size(), 4 * span.size(), 256};
+  std::vector<size_t> at;
+  size_t total = 0;
+  for (size_t b : sizes) at.push_back(total), total += (b + 255) / 256 * 256;
+  std::vector<uint8_t> host(total, 0);
+  auto put_t = [&](size_t off, const std::vector<double> &v) {
+    for (size_t i = 0; i < v.size(); i++) {
+      if (kind == 0) memcpy(host.data() + off + 8 * i, &v[i], 8);
+      else {
+        const float f = (float)v[i];
+        memcpy(host.data() + off + 4 * i, &f, 4);
+      }
+    }
+  };
+  memcpy(host.data() + at[0], perm.data(), sizes[0]);
+  put_t(at[1], lc), put_t(at[2], ls), put_t(at[3], tc), put_t(at[4], ts);
+  if (kind == 0) put_t(at[5], window);
+  else memcpy(host.data() + at[5], m->fe_window.data(), 4 * m->fe_window.size());  // the GGUF's f32 window
+  memcpy(host.data() + at[6], filters.data(), sizes[6]);
+  memcpy(host.data() + at[7], span.data(), sizes[7]);
+  float *buf = nullptr;
+  CK(wh_alloc(c, (total + 3) / 4, &buf));
+  d.buf = (uint8_t *)buf;
+  CK(wh_write(c, d.buf, host.data(), total));
+  MelArgs &a = d.args;
+  a.perm = (const int *)(d.buf + at[0]);
+  a.leaf_cos = d.buf + at[1], a.leaf_sin = d.buf + at[2];
+  a.tw_cos = d.buf + at[3], a.tw_sin = d.buf + at[4];
+  a.window = d.buf + at[5];
+  a.filters = (const float *)(d.buf + at[6]);
+  a.span = (const int *)(d.buf + at[7]);
+  a.hop = 160, a.mels = mels, a.leaf = leaf, a.stages = stages;
+  a.silent = (float)std::log10(1e-10);
+  d.scratch = (float *)(d.buf + at[8]);
+  d.kind = kind, d.n = n, d.mels = mels, d.leaf = leaf, d.stages = stages;
+  d.ready = true;
+  return WH_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1386,7 +1574,7 @@ void wh_model_free(wh_model *m) {
   for (uint32_t *p : m->own) wh_free(m->ctx, p);
   for (uint32_t *p : m->cross) wh_free(m->ctx, p);
   if (m->ids) wh_free(m->ctx, m->ids);
-  for (void *p : {(void *)m->tdt_buf, (void *)m->tdt_st, (void *)m->tdt_list, (void *)m->ctc_buf})
+  for (void *p : {(void *)m->tdt_buf, (void *)m->tdt_st, (void *)m->tdt_list, (void *)m->ctc_buf, (void *)m->mel.buf})
     if (p) wh_free(m->ctx, p);
   delete m;
 }
@@ -1483,6 +1671,23 @@ int wh_model_greedy(wh_model *m, const float *enc, int frames, int width, uint32
     return tdt_greedy(m, enc, frames, width, out, cap);
   }
   return wh_fail(m->ctx, WH_EARG, "Whisper decodes through wh_whisper_step");
+}
+
+int wh_model_mel(wh_model *m, const float *pcm_dev, int samples, float *mel_dev, int *frames) {
+  if (!m || samples < 0 || !frames) return WH_EARG;
+  const int f = mel_frames(m, samples);
+  *frames = f;
+  if (!mel_dev || f == 0) return WH_OK;
+  if (!pcm_dev) return wh_fail(m->ctx, WH_EARG, "wh_model_mel: no audio");
+  (void)hipSetDevice(m->ctx->device);
+  CK(mel_plan(m));
+  MelArgs a = m->mel.args;
+  a.pcm = pcm_dev;
+  a.samples = samples;
+  a.len = std::max(samples, 480000);
+  a.out = mel_dev;
+  a.raw = m->ctx->mel_raw;
+  return launch_mel(m->ctx, a, m->mel.kind, f, m->mel.scratch);
 }
 
 int wh_model_greedy_device(wh_model *m, const float *enc_dev, int frames, int width, uint32_t *out, int cap) {

@@ -360,6 +360,8 @@ int wh_tune(wh_ctx *ctx, const char *key, const char *value) {
     ctx->gemm_kernel_only = atoi(v) != 0;
   } else if (!strcmp(key, "attn_split")) {
     ctx->attn_split = std::max(0, std::min(atoi(v), 64));
+  } else if (!strcmp(key, "mel_raw")) {
+    ctx->mel_raw = atoi(v) != 0;
   } else {
     return wh_fail(ctx, WH_EARG, "wh_tune: unknown key \"%s\"", key);
   }

@@ -33,6 +33,10 @@ alternate; the recorded pass of a token timed whole, and every launch kernel-sta
 the head alone, and `gemv.decode_step` the whole decoder step replayed as one recorded pass per
 token for 224 tokens.
 
+`other_configs` times the encoder call of BASELINE's other configurations: configs[0] (GigaAM-v3 shape,
+11 s), configs[2] (Whisper-large-v3-turbo encoder, one 30 s window) and configs[3] (Parakeet over 16
+windows of ≤ 60 s cut at pauses, one padded batch).
+
 `cpu_baseline` is the C parity oracle (the restated wavo CPU backend: portable f16-rounded GEMM,
 AVX2+FMA, OpenMP) on the same model, on this host: the median of 3 warm 60 s calls on all threads, and
 one 10 s call on 1 thread.  `load` times wh_model_load of the GGUF with the file dropped from the page
@@ -279,6 +283,61 @@ def gemv_cold(gpu):
     return out
 
 
+def other_configs(gpu, model, reps=10):
+    """The encoder call of BASELINE's other configurations on this GPU, HIP events around each call,
+    median of `reps` after 3 warm-ups: configs[0] GigaAM-v3 shape (11 s, 275 frames), configs[2]
+    Whisper-large-v3-turbo encoder (one 30 s window, 1500 frames) and configs[3] Parakeet over 16 windows
+    of ≤ 60 s cut at pauses in one padded batch (wh_model_encode_batch)."""
+    import numpy as np
+
+    import wavo_amd as wa
+    from wavo_amd import synth
+
+    out = {}
+
+    def timed(step):
+        for _ in range(3):
+            step()
+        gpu.sync()
+        return statistics.median(time_each(gpu, step, reps))
+
+    # configs[3]: the long-form batch.
+    pcm, gaps = synth.long_audio(16 * 55.0, seed=11)
+    segs = synth.split_at_gaps(len(pcm) / synth.SR, gaps)[:16]
+    mels = [synth.parakeet_mel(pcm[int(a * synth.SR):int(b * synth.SR)]) for a, b in segs]
+    mf = max(x.shape[0] for x in mels)
+    frames, width = model.frames(mf)
+    batch = np.zeros((16, mf, mels[0].shape[1]), np.float32)
+    for i, x in enumerate(mels):
+        batch[i, :x.shape[0]] = x
+    mb, ob = gpu.upload(batch), gpu.buffer(16 * frames * width)
+    valid = [x.shape[0] for x in mels]
+    audio = sum(b - a for a, b in segs)
+    ms = timed(lambda: model.encode_batch_device(mb, 16, mf, valid, ob))
+    out["C3_parakeet_16_windows"] = {"ms": round(ms, 3), "audio_s": round(audio, 1), "rtfx": round(audio / (ms * 1e-3), 1)}
+    del mb, ob
+    # configs[0]: GigaAM.
+    m0 = wa.Model(gpu, synth.model_path("gigaam"))
+    mel0 = synth.gigaam_mel(synth.audio(11.0, seed=1))
+    f0, w0 = m0.frames(mel0.shape[0])
+    mb, ob = gpu.upload(mel0), gpu.buffer(f0 * w0)
+    ms = timed(lambda: m0.encode_device(mb, mel0.shape[0], ob))
+    out["C0_gigaam_11s"] = {"ms": round(ms, 3), "encoder_frames": f0, "rtfx": round(11.0 / (ms * 1e-3), 1)}
+    m0.free()
+    del mb, ob
+    # configs[2]: the Whisper encoder over one 30 s window.
+    m2 = wa.Model(gpu, synth.model_path("whisper"))
+    mel2 = synth.whisper_mel(synth.audio(30.0, seed=2))
+    f2, w2 = m2.frames(mel2.shape[0])
+    mb, ob = gpu.upload(mel2), gpu.buffer(f2 * w2)
+    ms = timed(lambda: m2.encode_device(mb, mel2.shape[0], ob))
+    out["C2_whisper_encoder_30s"] = {"ms": round(ms, 3), "encoder_frames": f2, "rtfx": round(30.0 / (ms * 1e-3), 1)}
+    m2.free()
+    out["what"] = ("encoder calls of BASELINE configs[0], [2], [3] on synthetic q8_0 models, mel resident, HIP events "
+                   f"around each call, median of {reps} after 3 warm-ups")
+    return out
+
+
 def decode_steps(gpu, tokens=224):
     """Whisper-large-v3-turbo-shaped decoder steps (4 layers, d 1280, 20 heads, 51866-token head, cross
     attention over 1500 encoder frames, q8_0), `tokens` steps back to back after one warm-up pass."""
@@ -386,6 +445,7 @@ def main():
     ap.add_argument("--seconds", type=float, default=60.0, help="audio per step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-gemv", action="store_true", help="skip the decoder GEMV and decoder step measurements")
+    ap.add_argument("--no-configs", action="store_true", help="skip the encoder timings of the other BASELINE configs")
     ap.add_argument("--replay", metavar="NAME", default=None,
                     help="only the back-to-back launches of this GEMM configuration (a roofline.kernel value), "
                          "or 'attention_rel' for the Parakeet attention call, for rocprofv3 passes over exactly "
@@ -547,6 +607,10 @@ def main():
         gemv["decode_step"] = decode_steps(gpu)
         log(f"decoder step {gemv['decode_step']['us_per_token']} us per token")
 
+    others = None if args.no_configs else other_configs(gpu, model)
+    if others:
+        log(f"other configs: {others}")
+
     cpu = None if args.no_cpu else cpu_baseline(path, mel, args.seconds, host)
 
     out = {
@@ -584,6 +648,7 @@ def main():
                                     "TDT decode on the device + tokens read back, host clock, median of 7 after 2"},
         "load": load,
         "gemv": gemv,
+        "other_configs": others,
         "cpu_baseline": cpu,
         "profiled_step_ms": breakdown,
     }

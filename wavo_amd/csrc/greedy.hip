@@ -4,12 +4,16 @@
 // pairs come back.
 //
 // TDT: the loop's control state lives in device memory (TdtState), so one decision is a fixed
-// sequence of launches that a caller records once and replays until the state says done: the joint
-// input z = ReLU(enc[t] + pred) (tdt_joint_in_kernel), the joint's output layer (a GEMV), the
-// decision (tdt_decide_kernel: both first-maximum argmaxes and the reference's frame / symbol-budget
-// rules), then the predictor on the emitted token (the embedding row, per LSTM layer the gate GEMVs
-// and tdt_cell_kernel, the joint's predictor projection), whose launches a device-side flag switches
-// off when the decision emitted nothing or the loop is done.
+// sequence of three launches that a caller records once and replays until the state says done.
+// tdt_joint_kernel builds z = ReLU(enc[t] + pred) in LDS and takes its share of the output layer's
+// rows, keeping the first maximum of its token rows and of its duration rows; tdt_step_kernel
+// reduces those in every workgroup to the same decision (workgroup 0 applies the frame / symbol
+// rules to the next state and appends the emission) and, after an emission, runs the first LSTM
+// layer on the token's embedding row, a wavefront per cell (its four gate rows of [Wx | Wh], the
+// gates and the cell); tdt_pred_kernel projects the last layer's h for the joint and makes the next
+// state current.  Further LSTM layers take one launch each.  The decoder's weights (the C1 shape:
+// 9.5 MB) stay in the L2 caches between decisions, so each product is a wavefront per row reading
+// the blocks as stored.
 #include <cfloat>
 
 #include "internal.h"
@@ -44,86 +48,418 @@ __device__ __forceinline__ void wg_argmax(const float *__restrict__ x, int n, fl
   __syncthreads();
 }
 
-// z[j] = max(enc[t·width + j] + pred[j], 0) for the current frame t (Decoder::joint's input,
-// src/parakeet/decoder.rs:135-142).
-__global__ __launch_bounds__(256) void tdt_joint_in_kernel(const float *__restrict__ pred, float *__restrict__ z,
-                                                           int joint, const TdtState *__restrict__ st) {
-  if (st->done) return;
-  const float *e = st->enc + (size_t)st->t * st->width;
-  for (int j = threadIdx.x; j < joint; j += 256) z[j] = fmaxf(e[j] + pred[j], 0.0f);
-}
+__device__ __forceinline__ float half_to_f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
-// The predictor's input: the embedding row of the last emitted token (Decoder::predict,
-// src/parakeet/decoder.rs:111-114).
-__global__ __launch_bounds__(256) void tdt_embed_kernel(const float *__restrict__ table, int n, float *__restrict__ x,
-                                                        const TdtState *__restrict__ st) {
-  if (st->idle) return;
-  const float *row = table + (size_t)st->token * n;
-  for (int j = threadIdx.x; j < n; j += 256) x[j] = row[j];
-}
+// 16 weights of a row as the file stores them (half of a 32-weight block: weights 16·hb .. 16·hb + 15),
+// loaded into registers first and multiplied with x (in LDS) later, so that a wavefront issues every
+// load of its rows before it waits for any.  Q8_0 / Q4_0: the block's scale and the 16 bytes (Q4_0: the
+// block's 16 bytes, whose low or high nibbles are these weights), as 2-byte words (blocks start on 2
+// bytes); F16: 32 bytes; F32: 64 bytes.
+template <int WT>
+struct Half {
+  static constexpr int R = WT == WH_F32 ? 16 : WT == WH_F16 ? 8 : 9;
+  uint32_t r[R];
 
-// One decision of the TDT greedy loop (src/parakeet/decoder.rs:158-191) on the joint's logits
-// [classes + durations]: the token and duration argmaxes (first maximum), the emission, and the
-// frame / symbol-budget update.  One workgroup.
-__global__ __launch_bounds__(256) void tdt_decide_kernel(const float *__restrict__ logits, TdtState *__restrict__ st,
-                                                         TdtConfig cfg) {
-  __shared__ float sv[4];
-  __shared__ int si[4];
-  if (st->done) return;
-  float v;
-  int token, di;
-  wg_argmax(logits, cfg.classes, sv, si, v, token);
-  wg_argmax(logits + cfg.classes, cfg.ndur, sv, si, v, di);
-  if (threadIdx.x != 0) return;
-  const int t = st->t, dur = cfg.durations[di];
-  const bool emit = token != cfg.blank;
-  if (emit) {
-    if (st->count < st->cap) {
-      st->out[2 * st->count] = (uint32_t)token;
-      st->out[2 * st->count + 1] = (uint32_t)t;
+  __device__ __forceinline__ void load(const uint8_t *__restrict__ row, int hb) {
+    if constexpr (WT == WH_F32 || WT == WH_F16) {
+      const uint4 *p = (const uint4 *)(row + (size_t)hb * R * 4);
+#pragma unroll
+      for (int i = 0; i < R / 4; i++) {
+        const uint4 v = p[i];
+        r[4 * i] = v.x, r[4 * i + 1] = v.y, r[4 * i + 2] = v.z, r[4 * i + 3] = v.w;
+      }
+    } else {
+      const uint16_t *u = (const uint16_t *)(row + (size_t)(hb >> 1) * (WT == WH_Q8_0 ? 34 : 18));
+      r[0] = u[0];
+      const int off = WT == WH_Q8_0 ? 1 + 8 * (hb & 1) : 1;
+#pragma unroll
+      for (int e = 0; e < 8; e++) r[1 + e] = u[off + e];
     }
-    st->count++;
-    st->token = token;
   }
-  int nt = t;
-  if (cfg.global) {
-    st->left--;
-    nt = t + (token == cfg.blank ? max(dur, 1) : dur);
-  } else {
-    nt = t + dur;
-    int symbols = st->symbols + 1;
-    if (dur != 0) {
-      symbols = 0;
-    } else if (symbols >= cfg.max_symbols || token == cfg.blank) {
-      nt++;
-      symbols = 0;
+
+  __device__ __forceinline__ float dot(int hb, const float *x) const {
+    const float *xv = x + 16 * hb;
+    float s = 0.0f;
+    if constexpr (WT == WH_F32) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) s += __builtin_bit_cast(float, r[e]) * xv[e];
+      return s;
+    } else if constexpr (WT == WH_F16) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) s += half_to_f(r[e] & 0xffffu) * xv[2 * e] + half_to_f(r[e] >> 16) * xv[2 * e + 1];
+      return s;
+    } else if constexpr (WT == WH_Q8_0) {
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        s += (float)(int8_t)(r[1 + e] & 0xffu) * xv[2 * e] + (float)(int8_t)(r[1 + e] >> 8) * xv[2 * e + 1];
+      return s * half_to_f(r[0]);
+    } else {
+      const int sh = 4 * (hb & 1);
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        s += (float)((int)((r[1 + e] >> sh) & 15u) - 8) * xv[2 * e] +
+             (float)((int)((r[1 + e] >> (8 + sh)) & 15u) - 8) * xv[2 * e + 1];
+      return s * half_to_f(r[0]);
     }
-    st->symbols = symbols;
   }
-  st->t = nt;
-  st->decisions++;
-  const int done = nt >= st->frames || (cfg.global && st->left <= 0);
-  st->done = done;
-  st->idle = (!emit || done) ? 1 : 0;
+};
+
+// Rows per wavefront in the joint's and the predictor's products.
+template <int WT>
+constexpr int rows_per_wave() { return WT == WH_F32 ? 4 : 8; }
+
+// Sums each of the N = 2^m values of every lane over the wavefront with 6 + N − 2 shuffles instead of
+// 6·N: each exchange halves the values a lane holds (a lane keeps half, its partner the other half),
+// then the single value is summed over the lanes that hold the same one.  Afterwards lane 64·v/N..
+// holds value v's sum (lanes with bit 5 − j of the lane index set hold the upper half at step j).
+template <int N>
+__device__ __forceinline__ float wave_sums(float (&v)[N]) {
+  const int lane = threadIdx.x & 63;
+  float cur[N];
+#pragma unroll
+  for (int i = 0; i < N; i++) cur[i] = v[i];
+  int n = N;
+#pragma unroll
+  for (int o = 32; n > 1; o >>= 1) {
+    const bool up = lane & o;
+    n >>= 1;
+#pragma unroll
+    for (int i = 0; i < N / 2; i++)
+      if (i < n) {
+        const float keep = up ? cur[n + i] : cur[i], send = up ? cur[i] : cur[n + i];
+        cur[i] = keep + __shfl_xor(send, o, 64);
+      }
+  }
+  float s = cur[0];
+  // The lanes that share this value: those equal in the bits used above.
+#pragma unroll
+  for (int o = 64 / N / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  return s;
 }
 
-// One LSTM layer's cell (Decoder::predict, src/parakeet/decoder.rs:115-128): the gates [i | f | g | o]
-// (one GEMV of [Wx | Wh] over [x | h] with the bias), c' = σ(f)·c + σ(i)·tanh(g), h' = σ(o)·tanh(c'),
-// in place.
-__global__ __launch_bounds__(256) void tdt_cell_kernel(const float *__restrict__ gates, float *__restrict__ h,
-                                                       float *__restrict__ c, int n, const int *__restrict__ idle) {
-  if (idle && *idle) return;
-  for (int k = blockIdx.x * 256 + threadIdx.x; k < n; k += gridDim.x * 256) {
-    const float ig = gates[k], fg = gates[n + k], gg = gates[2 * n + k], og = gates[3 * n + k];
-    const float si = 1.0f / (1.0f + expf(-ig)), sf = 1.0f / (1.0f + expf(-fg)), so = 1.0f / (1.0f + expf(-og));
-    const float cc = sf * c[k] + si * tanhf(gg);
-    c[k] = cc;
-    h[k] = so * tanhf(cc);
+// RW consecutive rows from r0 (those below `rows`) of a layer with k ≤ 1024 inputs, held by one
+// wavefront: load() issues every weight and bias load (from addresses clamped into the layer, so that
+// no load sits behind a branch and the wavefront waits once), finish() multiplies with x in LDS and
+// sums; lane 64·i/RW gets row i's value (plus bias).
+template <int WT, int RW>
+struct Rows {
+  Half<WT> h[RW];
+  float b;
+  int r0, rows, k;
+
+  __device__ __forceinline__ void load(const uint8_t *__restrict__ w, size_t rb, const float *__restrict__ bias,
+                                       int first, int nrows, int kk) {
+    r0 = first, rows = nrows, k = kk;
+    const int lane = threadIdx.x & 63, hb = min(lane, k / 16 - 1);
+#pragma unroll
+    for (int i = 0; i < RW; i++) h[i].load(w + (size_t)min(r0 + i, rows - 1) * rb, hb);
+    b = bias[min(r0 + lane * RW / 64, rows - 1)];
+  }
+
+  // The value of row r0 + lane·RW/64 (0 past the rows).
+  __device__ __forceinline__ float finish(const float *x) const {
+    const int lane = threadIdx.x & 63, hb = min(lane, k / 16 - 1);
+    const bool on = lane < k / 16;
+    float v[RW];
+#pragma unroll
+    for (int i = 0; i < RW; i++) v[i] = on && r0 + i < rows ? h[i].dot(hb, x) : 0.0f;
+    return wave_sums<RW>(v) + b;
+  }
+};
+
+// Stages n ≤ 256·P values into LDS: every load into registers first (one round trip), then the stores.
+template <int P, typename F>
+__device__ __forceinline__ void stage(float *dst, int n, F value) {
+  float v[P];
+#pragma unroll
+  for (int i = 0; i < P; i++) v[i] = value(min((int)threadIdx.x + 256 * i, n - 1));  // clamped: no branch
+#pragma unroll
+  for (int i = 0; i < P; i++) {
+    const int j = threadIdx.x + 256 * i;
+    if (j < n) dst[j] = v[i];
   }
 }
 
-__global__ void tdt_init_kernel(TdtState *st, TdtState init) {
-  if (threadIdx.x == 0) *st = init;
+__device__ __forceinline__ float sigm(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+// One TDT decision, first part (Decoder::joint, src/parakeet/decoder.rs:135-149): the joint's input
+// z = ReLU(enc[t] + pred) (made by the previous decision's last kernel) in LDS, this workgroup's rows
+// of the output layer (RW per wavefront), and the first maximum of its token rows and of its duration
+// rows into part[blockIdx.x] (value, index, value, index; index −1 when it has none).
+template <int WT>
+__global__ __launch_bounds__(256) void tdt_joint_kernel(TdtArgs a) {
+  constexpr int RW = rows_per_wave<WT>();
+  extern __shared__ float z[];
+  __shared__ float bv[2][4];
+  __shared__ int bi[2][4];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // The weights and z (written by the previous decision's last kernel) in one round trip.
+  const int r0 = (blockIdx.x * 4 + wave) * RW;
+  Rows<WT, RW> rows;
+  rows.load(a.out_w, a.out_rb, a.out_b, r0, a.out_rows, a.joint);
+  const float *zg = a.z;
+  stage<4>(z, a.joint, [&](int j) { return zg[j]; });
+  if (a.st->done) return;
+  __syncthreads();
+  // Row r0 + i's value is in lane 64·i/RW: the first maximum over those lanes, in row order.
+  const float val = rows.finish(z);
+  const int r = r0 + lane * RW / 64;
+  const bool mine = lane % (64 / RW) == 0 && r < a.out_rows;
+  float tv = -FLT_MAX, dv = -FLT_MAX;
+  int ti = -1, di = -1;
+  if (mine) {
+    if (r < a.cfg.classes) tv = val, ti = r;
+    else dv = val, di = r - a.cfg.classes;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float otv = __shfl_xor(tv, o, 64), odv = __shfl_xor(dv, o, 64);
+    const int oti = __shfl_xor(ti, o, 64), odi = __shfl_xor(di, o, 64);
+    if (oti >= 0 && (ti < 0 || better(otv, oti, tv, ti))) tv = otv, ti = oti;
+    if (odi >= 0 && (di < 0 || better(odv, odi, dv, di))) dv = odv, di = odi;
+  }
+  if (lane == 0) bv[0][wave] = tv, bi[0][wave] = ti, bv[1][wave] = dv, bi[1][wave] = di;
+  __syncthreads();
+  if (tid == 0) {
+    float out[4];
+    for (int k = 0; k < 2; k++) {
+      float bvv = -FLT_MAX;
+      int bii = -1;
+      for (int w = 0; w < 4; w++)
+        if (bi[k][w] >= 0 && (bii < 0 || better(bv[k][w], bi[k][w], bvv, bii))) bvv = bv[k][w], bii = bi[k][w];
+      out[2 * k] = bvv, out[2 * k + 1] = (float)bii;
+    }
+    *(float4 *)(a.part + 4 * blockIdx.x) = float4{out[0], out[1], out[2], out[3]};
+  }
+}
+
+// One LSTM layer's cell k (one per wavefront) over [x | h_old] (2n ≤ 2048 values in LDS): the four gate
+// rows k, n + k, 2n + k, 3n + k of the joined [Wx | Wh] with the bias, c' = σ(f)·c + σ(i)·tanh(g),
+// h' = σ(o)·tanh(c').
+template <int WT>
+struct Cell {
+  Half<WT> h[4][2];
+  float b[4], cold;
+  int k, hbs;
+
+  // Every load of this wavefront's cell (weights, biases, its c) before it waits for anything, from
+  // addresses clamped into the layer (no load behind a branch).
+  __device__ __forceinline__ void load(const TdtArgs &a, int layer) {
+    const int n = a.n, lane = threadIdx.x & 63;
+    hbs = 2 * n / 16;
+    k = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int kk = min(k, n - 1);
+    const uint8_t *w = a.lstm_w[layer];
+    const float *bias = a.lstm_b[layer];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      b[g] = bias[g * n + kk];
+      const uint8_t *row = w + (size_t)(g * n + kk) * a.lstm_rb;
+#pragma unroll
+      for (int i = 0; i < 2; i++) h[g][i].load(row, min(lane + 64 * i, hbs - 1));
+    }
+    cold = a.c[(size_t)layer * n + kk];
+  }
+
+  __device__ __forceinline__ void finish(const TdtArgs &a, int layer, const float *xin, float *h_new) const {
+    const int n = a.n, lane = threadIdx.x & 63;
+    float acc[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+        if (lane + 64 * i < hbs) s += h[g][i].dot(lane + 64 * i, xin);
+      acc[g] = s;
+    }
+    // Gate g's sum lands in lanes 16g..16g + 15: lane 0 gathers all four.
+    const float own = wave_sums<4>(acc);
+    float gate[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) gate[g] = __shfl(own, 16 * g, 64) + b[g];
+    if (lane == 0 && k < n) {
+      const float cc = sigm(gate[1]) * cold + sigm(gate[0]) * tanhf(gate[2]);
+      a.c[(size_t)layer * n + k] = cc;
+      h_new[k] = sigm(gate[3]) * tanhf(cc);
+    }
+  }
+};
+
+// One TDT decision, second part: every workgroup reduces the joint's partial maxima to the same
+// decision (the token and duration argmaxes, src/parakeet/decoder.rs:158-191) and workgroup 0 writes
+// the next state and appends the emission; then, after an emission, the first LSTM layer over the
+// token's embedding row (Decoder::predict, :107-133).  INIT: the first predict(None): no decision,
+// a zero input.
+template <int WT, bool INIT>
+__global__ __launch_bounds__(256) void tdt_step_kernel(TdtArgs a) {
+  extern __shared__ float xin[];
+  __shared__ float sv[2][4];
+  __shared__ int si[2][4];
+  const int tid = threadIdx.x, n = a.n;
+  // The cell's weights and the old h do not depend on the decision: their loads go out first.
+  Cell<WT> cell;
+  cell.load(a, 0);
+  float hv[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int j = tid + 256 * i;
+    hv[i] = a.h_old[min(j, n - 1)];
+  }
+  int token = 0;
+  if constexpr (!INIT) {
+    const TdtState *st = a.st;
+    if (st->done) return;
+    // The parts' first maxima (token rows, duration rows): every part loaded first.
+    float4 q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int p = tid + 256 * i;
+      q[i] = *(const float4 *)(a.part + 4 * min(p, a.parts - 1));  // clamped: no branch
+      if (p >= a.parts) q[i] = float4{0.0f, -1.0f, 0.0f, -1.0f};
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      float v = -FLT_MAX;
+      int i = -1;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float pv = k ? q[j].z : q[j].x;
+        const int pi = (int)(k ? q[j].w : q[j].y);
+        if (pi >= 0 && (i < 0 || better(pv, pi, v, i))) v = pv, i = pi;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o, 64);
+        const int oi = __shfl_xor(i, o, 64);
+        if (oi >= 0 && (i < 0 || better(ov, oi, v, i))) v = ov, i = oi;
+      }
+      if ((tid & 63) == 0) sv[k][tid >> 6] = v, si[k][tid >> 6] = i;
+    }
+    __syncthreads();
+    int dec[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      float bvv = -FLT_MAX;
+      int bii = -1;
+      for (int w = 0; w < 4; w++)
+        if (si[k][w] >= 0 && (bii < 0 || better(sv[k][w], si[k][w], bvv, bii))) bvv = sv[k][w], bii = si[k][w];
+      dec[k] = bii;
+    }
+    token = dec[0];
+    const int dur = a.cfg.durations[dec[1]], t = st->t;
+    const bool emit = token != a.cfg.blank;
+    int nt = t, symbols = st->symbols, left = st->left;
+    if (a.cfg.global) {
+      left--;
+      nt = t + (token == a.cfg.blank ? max(dur, 1) : dur);
+    } else {
+      nt = t + dur;
+      symbols++;
+      if (dur != 0) {
+        symbols = 0;
+      } else if (symbols >= a.cfg.max_symbols || token == a.cfg.blank) {
+        nt++;
+        symbols = 0;
+      }
+    }
+    const int done = nt >= st->frames || (a.cfg.global && left <= 0);
+    const int idle = (!emit || done) ? 1 : 0;
+    // The next frame's encoder row, for the next joint input: each workgroup its slice.
+    if (!done) {
+      const float *e = st->enc + (size_t)nt * st->width;
+      for (int j = blockIdx.x * 256 + tid; j < a.joint; j += gridDim.x * 256) a.erow[j] = e[j];
+    }
+    if (blockIdx.x == 0 && tid == 0) {
+      TdtState nx = *st;
+      if (emit) {
+        if (nx.count < nx.cap) {
+          nx.out[2 * nx.count] = (uint32_t)token;
+          nx.out[2 * nx.count + 1] = (uint32_t)t;
+        }
+        nx.count++;
+        nx.token = token;
+      }
+      nx.t = nt, nx.symbols = symbols, nx.left = left, nx.decisions++;
+      nx.done = done, nx.idle = idle;
+      *a.nx = nx;
+    }
+    if (idle) return;
+  }
+  if constexpr (INIT) {  // the first frame's encoder row
+    const float *e = a.st->enc;
+    for (int j = blockIdx.x * 256 + tid; j < a.joint; j += gridDim.x * 256) a.erow[j] = e[j];
+  }
+  // Layer 0's input [embedding row of the token | h]: the first predict has a zero input.
+  const float *row = a.embed + (size_t)token * n;
+  stage<4>(xin, n, [&](int j) { return INIT ? 0.0f : row[j]; });
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int j = tid + 256 * i;
+    if (j < n) xin[n + j] = hv[i];
+  }
+  __syncthreads();
+  cell.finish(a, 0, xin, a.h_new);
+}
+
+// LSTM layer l ≥ 1 over [layer l − 1's new h | its own h]; nothing while idle.
+template <int WT>
+__global__ __launch_bounds__(256) void tdt_layer_kernel(TdtArgs a, int layer) {
+  extern __shared__ float xin[];
+  Cell<WT> cell;
+  cell.load(a, layer);
+  if (a.nx->idle) return;
+  const int n = a.n;
+  const float *x = a.h_new + (size_t)(layer - 1) * n, *h = a.h_old + (size_t)layer * n;
+  stage<8>(xin, 2 * n, [&](int j) { return j < n ? x[j] : h[j - n]; });
+  __syncthreads();
+  cell.finish(a, layer, xin, a.h_new + (size_t)layer * n);
+}
+
+// One TDT decision, last part: after an emission the joint's predictor projection of the last layer's
+// new h (Decoder::predict's pred, src/parakeet/decoder.rs:129-133), RW rows per wavefront, and the new
+// h as the old; then the next decision's joint input z = ReLU(enc[t] + pred) from the encoder row the
+// step kernel copied, and the next state becomes the current one.
+template <int WT>
+__global__ __launch_bounds__(256) void tdt_pred_kernel(TdtArgs a) {
+  constexpr int RW = rows_per_wave<WT>();
+  extern __shared__ float hin[];
+  const TdtState *nx = a.nx;
+  const int n = a.n, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // Everything this kernel reads goes out before the wait for the state: the weights, the new h,
+  // and for this wavefront's rows the next encoder row and the current projection.
+  const int r0 = (blockIdx.x * 4 + wave) * RW, r = r0 + lane * RW / 64, rc = min(r, a.joint - 1);
+  Rows<WT, RW> rows;
+  rows.load(a.pred_w, a.pred_rb, a.pred_b, r0, a.joint, n);
+  const float *h = a.h_new + (size_t)(a.layers - 1) * n;
+  float hv[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) hv[i] = h[min(tid + 256 * i, n - 1)];
+  const float erow = a.erow[rc];
+  float pv = a.pred[rc];
+  const bool mine = lane % (64 / RW) == 0 && r < a.joint;
+  if (!nx->idle) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int j = tid + 256 * i;
+      if (j < n) hin[j] = hv[i];
+    }
+    __syncthreads();
+    pv = rows.finish(hin);
+    if (mine) a.pred[r] = pv;
+    for (int j = blockIdx.x * 256 + tid; j < a.layers * n; j += gridDim.x * 256) a.h_old[j] = a.h_new[j];
+  }
+  // The next decision's joint input (src/parakeet/decoder.rs:135-142).
+  if (mine && !nx->done) a.z[r] = fmaxf(erow + pv, 0.0f);
+  if (blockIdx.x == 0 && tid == 0) *a.st = *nx;
+}
+
+__global__ void tdt_init_kernel(TdtState *st, TdtState *nx, TdtState init) {
+  if (threadIdx.x == 0) {
+    *st = init;
+    TdtState next = init;
+    next.idle = 0;  // the first predict runs
+    *nx = next;
+  }
 }
 
 // Greedy CTC, step 1: the first maximum of each frame's first `classes` logits.
@@ -165,36 +501,61 @@ __global__ __launch_bounds__(256) void ctc_collapse_kernel(const int *__restrict
 
 }  // namespace
 
-int launch_tdt_init(wh_ctx *ctx, TdtState *st, const TdtState &init) {
-  wh_launch(ctx, tdt_init_kernel, 1, 64, 0, st, init);
+int launch_tdt_init(wh_ctx *ctx, TdtState *st, TdtState *nx, const TdtState &init) {
+  wh_launch(ctx, tdt_init_kernel, 1, 64, 0, st, nx, init);
   return wh_launched(ctx, "tdt init");
 }
 
-int launch_tdt_joint_in(wh_ctx *ctx, const float *pred, float *z, int joint, const TdtState *st) {
-  ProfScope prof(ctx, "tdt_joint_in", 0.0, 12.0 * joint);
-  wh_launch(ctx, tdt_joint_in_kernel, 1, 256, 0, pred, z, joint, st);
-  return wh_launched(ctx, "tdt joint input");
+template <int WT>
+static int tdt_launch_t(wh_ctx *ctx, const TdtArgs &a, int what) {
+  const int cells = (a.n + 3) / 4;
+  switch (what) {
+    case TDT_JOINT: {
+      ProfScope prof(ctx, "tdt_joint", 2.0 * a.out_rows * a.joint, (double)a.out_rb * a.out_rows + 8.0 * a.joint);
+      wh_launch(ctx, tdt_joint_kernel<WT>, a.parts, 256, (size_t)4 * a.joint, a);
+      return wh_launched(ctx, "tdt joint");
+    }
+    case TDT_STEP:
+    case TDT_INIT: {
+      ProfScope prof(ctx, what == TDT_INIT ? "tdt_init_step" : "tdt_step", 16.0 * a.n * a.n,
+                     (double)a.lstm_rb * 4 * a.n + 16.0 * a.parts);
+      if (what == TDT_INIT) wh_launch(ctx, tdt_step_kernel<WT, true>, cells, 256, (size_t)8 * a.n, a);
+      else wh_launch(ctx, tdt_step_kernel<WT, false>, cells, 256, (size_t)8 * a.n, a);
+      if (int rc = wh_launched(ctx, "tdt step")) return rc;
+      for (int l = 1; l < a.layers; l++) {
+        ProfScope pl(ctx, "tdt_layer", 16.0 * a.n * a.n, (double)a.lstm_rb * 4 * a.n);
+        wh_launch(ctx, tdt_layer_kernel<WT>, cells, 256, (size_t)8 * a.n, a, l);
+        if (int rc = wh_launched(ctx, "tdt layer")) return rc;
+      }
+      return WH_OK;
+    }
+    default: {
+      ProfScope prof(ctx, "tdt_pred", 2.0 * a.joint * a.n, (double)a.pred_rb * a.joint);
+      const int rows = 4 * rows_per_wave<WT>();
+      wh_launch(ctx, tdt_pred_kernel<WT>, (a.joint + rows - 1) / rows, 256, (size_t)4 * a.n, a);
+      return wh_launched(ctx, "tdt pred");
+    }
+  }
 }
 
-int launch_tdt_embed(wh_ctx *ctx, const float *table, int n, float *x, const TdtState *st) {
-  ProfScope prof(ctx, "tdt_embed", 0.0, 8.0 * n);
-  wh_launch(ctx, tdt_embed_kernel, 1, 256, 0, table, n, x, st);
-  return wh_launched(ctx, "tdt embed");
+int tdt_parts(int type, int out_rows) {
+  const int rows = 4 * (type == WH_F32 ? rows_per_wave<WH_F32>() : rows_per_wave<WH_Q8_0>());
+  return (out_rows + rows - 1) / rows;
 }
 
-int launch_tdt_decide(wh_ctx *ctx, const float *logits, TdtState *st, const TdtConfig &cfg) {
-  if (cfg.classes <= 0 || cfg.ndur <= 0 || cfg.ndur > 16 || cfg.blank < 0 || cfg.blank >= cfg.classes ||
-      cfg.max_symbols <= 0)
+int launch_tdt(wh_ctx *ctx, const TdtArgs &a, int what) {
+  const TdtConfig &c = a.cfg;
+  if (c.classes <= 0 || c.ndur <= 0 || c.ndur > 16 || c.blank < 0 || c.blank >= c.classes || c.max_symbols <= 0 ||
+      a.n <= 0 || a.n % 16 || a.n > 1024 || a.joint <= 0 || a.joint % 16 || a.joint > 1024 || a.layers < 1 ||
+      a.layers > 4 || a.parts != tdt_parts(a.type, a.out_rows) || a.parts > 1024 || a.out_rows != c.classes + c.ndur)
     return wh_fail(ctx, WH_EARG, "tdt: bad decoder configuration");
-  ProfScope prof(ctx, "tdt_decide", 0.0, 4.0 * (cfg.classes + cfg.ndur));
-  wh_launch(ctx, tdt_decide_kernel, 1, 256, 0, logits, st, cfg);
-  return wh_launched(ctx, "tdt decide");
-}
-
-int launch_tdt_cell(wh_ctx *ctx, const float *gates, float *h, float *c, int n, const int *idle) {
-  ProfScope prof(ctx, "tdt_cell", 0.0, 28.0 * n);
-  wh_launch(ctx, tdt_cell_kernel, (n + 255) / 256, 256, 0, gates, h, c, n, idle);
-  return wh_launched(ctx, "tdt cell");
+  switch (a.type) {
+    case WH_F32: return tdt_launch_t<WH_F32>(ctx, a, what);
+    case WH_F16: return tdt_launch_t<WH_F16>(ctx, a, what);
+    case WH_Q8_0: return tdt_launch_t<WH_Q8_0>(ctx, a, what);
+    case WH_Q4_0: return tdt_launch_t<WH_Q4_0>(ctx, a, what);
+  }
+  return wh_fail(ctx, WH_EARG, "tdt: weight type %d", a.type);
 }
 
 int launch_ctc(wh_ctx *ctx, const float *logits, int frames, int width, int classes, int blank, int *ids,

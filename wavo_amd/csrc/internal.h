@@ -233,15 +233,30 @@ struct TdtConfig {
   int classes, ndur, blank, max_symbols, global;
   int durations[16];
 };
-int launch_tdt_init(wh_ctx *ctx, TdtState *st, const TdtState &init);
-// z = ReLU(enc[t] + pred) (joint values); nothing once done.
-int launch_tdt_joint_in(wh_ctx *ctx, const float *pred, float *z, int joint, const TdtState *st);
-// x = table row of the last emitted token (n values); nothing while idle.
-int launch_tdt_embed(wh_ctx *ctx, const float *table, int n, float *x, const TdtState *st);
-// One decision on logits [classes + durations]; nothing once done.
-int launch_tdt_decide(wh_ctx *ctx, const float *logits, TdtState *st, const TdtConfig &cfg);
-// One LSTM layer's cell over its gates (4n) into h, c (n each) in place; nothing while *idle != 0.
-int launch_tdt_cell(wh_ctx *ctx, const float *gates, float *h, float *c, int n, const int *idle);
+// The fused decision's arguments: the decoder's weights as stored (one type for all), the state
+// records (current and next), the LSTM state [layers][n] (old and new h, c), the joint's predictor
+// projection, and the joint's per-workgroup partial maxima [parts][4].
+struct TdtArgs {
+  const uint8_t *out_w, *pred_w;
+  const uint8_t *lstm_w[4];
+  const float *out_b, *pred_b;
+  const float *lstm_b[4];
+  size_t out_rb, pred_rb, lstm_rb;
+  int type, n, joint, layers, out_rows, parts;
+  const float *embed;  // [classes][n] f32
+  TdtState *st, *nx;
+  float *h_old, *h_new, *c, *pred, *part;
+  float *erow, *z;  // the next frame's encoder row [joint], the next joint input [joint]
+  TdtConfig cfg;
+};
+enum { TDT_JOINT = 0, TDT_STEP = 1, TDT_PRED = 2, TDT_INIT = 3 };
+// Both state records from `init` (the next one not idle: the first predict runs).
+int launch_tdt_init(wh_ctx *ctx, TdtState *st, TdtState *nx, const TdtState &init);
+// One part of a decision (TDT_JOINT, TDT_STEP with the further LSTM layers, TDT_PRED), or the first
+// predict(None) (TDT_INIT, then TDT_PRED).
+int launch_tdt(wh_ctx *ctx, const TdtArgs &a, int what);
+// The joint's workgroups (and partial maxima) for `out_rows` output rows of weight type `type`.
+int tdt_parts(int type, int out_rows);
 // Greedy CTC (src/gigaam/decoder.rs:135-151) over `frames` rows of `width` logits (the first
 // `classes` columns): ids (frames ints) is scratch; up to cap (token, frame) pairs into out, the
 // count into *count (all device memory).

@@ -465,12 +465,10 @@ struct wh_model {
   std::vector<std::vector<float>> lstm_b;
   std::vector<float> pred_b, out_b;
   // The same decoder on the device (greedy.hip): [Wx | Wh] per LSTM layer with its bias, the joint's
-  // projections, the embedding table in f32; the loop's buffers [h slots (layers + 1)·hidden | c
-  // layers·hidden | gates | pred | z | logits], its state and (token, frame) list.
+  // projections, the embedding table in f32; the loop's buffers (tdt_bufs) and (token, frame) list.
   std::vector<wh_linear *> tdt_lstm;
   wh_linear *tdt_pred = nullptr, *tdt_out = nullptr;
   float *tdt_embed = nullptr, *tdt_buf = nullptr;
-  TdtState *tdt_st = nullptr;
   uint32_t *tdt_list = nullptr;
   int tdt_list_cap = 0;
   // Greedy CTC on the device: [ids (frames) | count | pairs], sized for ctc_cap frames.
@@ -1226,23 +1224,31 @@ int tdt_greedy(const wh_model *m, const float *enc, int frames, int width, uint3
 
 // ---- greedy decoding on the device
 
-// Offsets (floats) of the TDT loop's buffers in tdt_buf; each part starts on a 64-float boundary.
+// The TDT loop's device buffers in tdt_buf: [h_old | h_new | c] ([layers][hidden] each), the joint's
+// predictor projection, the next frame's encoder row and the next joint input ([joint] each), the
+// joint's partial maxima [parts][4], and the two state records; each part on a 64-float boundary.
+constexpr int TDT_PARTS = 1024;  // the most the joint's launch may have (32768 output rows)
+
 struct TdtBufs {
-  float *h, *c, *gates, *pred, *z, *logits;
-  size_t total;
+  float *h_old, *h_new, *c, *pred, *erow, *z, *part;
+  TdtState *st, *nx;
+  size_t total;  // floats
 };
 
 TdtBufs tdt_bufs(const wh_model *m, float *base) {
   auto up = [](size_t n) { return (n + 63) / 64 * 64; };
-  const size_t n = m->hidden, L = m->lstm_layers;
+  const size_t ln = (size_t)m->lstm_layers * m->hidden, sw = up((sizeof(TdtState) + 3) / 4);
   size_t at = 0;
   TdtBufs b;
-  b.h = base + at, at += up((L + 1) * n);
-  b.c = base + at, at += up(L * n);
-  b.gates = base + at, at += up(wh_linear_width(m->tdt_lstm[0]));
-  b.pred = base + at, at += up(wh_linear_width(m->tdt_pred));
+  b.h_old = base + at, at += up(ln);
+  b.h_new = base + at, at += up(ln);
+  b.c = base + at, at += up(ln);
+  b.pred = base + at, at += up(m->joint);
+  b.erow = base + at, at += up(m->joint);
   b.z = base + at, at += up(m->joint);
-  b.logits = base + at, at += up(wh_linear_width(m->tdt_out));
+  b.part = base + at, at += up((size_t)4 * TDT_PARTS);
+  b.st = (TdtState *)(base + at), at += sw;
+  b.nx = (TdtState *)(base + at), at += sw;
   b.total = at;
   return b;
 }
@@ -1258,34 +1264,33 @@ TdtConfig tdt_config(const wh_model *m) {
   return cfg;
 }
 
-// Decoder::predict (src/parakeet/decoder.rs:111-133) on the device: per LSTM layer one GEMV of
-// [Wx | Wh] over the slots [x | h] (slot 0 holds the token's embedding, slot l + 1 layer l's h) and
-// the cell, then the joint's predictor projection.  With idle, every launch is switched by it.
-int tdt_predict(wh_model *m, const TdtBufs &b, const int *idle) {
-  wh_ctx *c = m->ctx;
-  const int n = m->hidden;
-  for (int l = 0; l < m->lstm_layers; l++) {
-    CK(launch_gemv(c, b.h + (size_t)l * n, m->tdt_lstm[l], b.gates, WH_BIAS, 1.0f, 0, nullptr, nullptr, nullptr,
-                   nullptr, idle));
-    CK(launch_tdt_cell(c, b.gates, b.h + (size_t)(l + 1) * n, b.c + (size_t)l * n, n, idle));
-  }
-  return launch_gemv(c, b.h + (size_t)m->lstm_layers * n, m->tdt_pred, b.pred, WH_BIAS, 1.0f, 0, nullptr, nullptr,
-                     nullptr, nullptr, idle);
+TdtArgs tdt_args(const wh_model *m) {
+  const TdtBufs b = tdt_bufs(m, m->tdt_buf);
+  TdtArgs a{};
+  a.out_w = m->tdt_out->w, a.out_b = m->tdt_out->bias, a.out_rb = m->tdt_out->row_bytes;
+  a.pred_w = m->tdt_pred->w, a.pred_b = m->tdt_pred->bias, a.pred_rb = m->tdt_pred->row_bytes;
+  for (int l = 0; l < m->lstm_layers; l++) a.lstm_w[l] = m->tdt_lstm[l]->w, a.lstm_b[l] = m->tdt_lstm[l]->bias;
+  a.lstm_rb = m->tdt_lstm[0]->row_bytes;
+  a.type = m->tdt_out->type;
+  a.n = m->hidden, a.joint = m->joint, a.layers = m->lstm_layers;
+  a.out_rows = m->tdt_out->rows;
+  a.parts = tdt_parts(a.type, a.out_rows);
+  a.embed = m->tdt_embed;
+  a.st = b.st, a.nx = b.nx;
+  a.h_old = b.h_old, a.h_new = b.h_new, a.c = b.c, a.pred = b.pred, a.part = b.part;
+  a.erow = b.erow, a.z = b.z;
+  a.cfg = tdt_config(m);
+  return a;
 }
 
-// `count` decisions of the TDT loop (src/parakeet/decoder.rs:158-191): the joint on the current frame
-// (Decoder::joint, :135-149), the decision, and the predictor on an emitted token.
+// `count` decisions of the TDT loop (src/parakeet/decoder.rs:158-191), three launches each (and one
+// per further LSTM layer).
 int tdt_decisions(wh_model *m, int count) {
-  wh_ctx *c = m->ctx;
-  const TdtBufs b = tdt_bufs(m, m->tdt_buf);
-  const TdtConfig cfg = tdt_config(m);
+  const TdtArgs a = tdt_args(m);
   for (int i = 0; i < count; i++) {
-    CK(launch_tdt_joint_in(c, b.pred, b.z, m->joint, m->tdt_st));
-    CK(launch_gemv(c, b.z, m->tdt_out, b.logits, WH_BIAS, 1.0f, 0, nullptr, nullptr, nullptr, nullptr,
-                   &m->tdt_st->done));
-    CK(launch_tdt_decide(c, b.logits, m->tdt_st, cfg));
-    CK(launch_tdt_embed(c, m->tdt_embed, m->hidden, b.h, m->tdt_st));
-    CK(tdt_predict(m, b, &m->tdt_st->idle));
+    CK(launch_tdt(m->ctx, a, TDT_JOINT));
+    CK(launch_tdt(m->ctx, a, TDT_STEP));
+    CK(launch_tdt(m->ctx, a, TDT_PRED));
   }
   return WH_OK;
 }
@@ -1296,13 +1301,15 @@ int tdt_greedy_device(wh_model *m, const float *enc, int frames, int width, uint
   if (m->tdt_lstm.empty() || !m->tdt_pred || !m->tdt_out || !m->tdt_embed)
     return wh_fail(c, WH_EARG, "model has no device TDT decoder");
   if (width < m->joint) return wh_fail(c, WH_EARG, "encoder width %d is below the joint's %d", width, m->joint);
+  if (m->lstm_layers > 4) return wh_fail(c, WH_EARG, "tdt: %d LSTM layers (the device decoder takes up to 4)", m->lstm_layers);
+  for (const wh_linear *l : m->tdt_lstm)
+    if (l->type != m->tdt_out->type || l->row_bytes != m->tdt_lstm[0]->row_bytes)
+      return wh_fail(c, WH_EARG, "tdt: the decoder's weights differ in type");
+  if (m->tdt_pred->type != m->tdt_out->type) return wh_fail(c, WH_EARG, "tdt: the decoder's weights differ in type");
+  if (tdt_parts(m->tdt_out->type, m->tdt_out->rows) > TDT_PARTS || m->hidden > 1024 || m->joint > 1024)
+    return wh_fail(c, WH_EARG, "tdt: the decoder is larger than the device decoder takes");
   if (frames == 0) return 0;
-  if (!m->tdt_buf) {
-    CK(wh_alloc(c, tdt_bufs(m, nullptr).total, &m->tdt_buf));
-    float *st = nullptr;
-    CK(wh_alloc(c, (sizeof(TdtState) + 3) / 4, &st));
-    m->tdt_st = (TdtState *)st;
-  }
+  if (!m->tdt_buf) CK(wh_alloc(c, tdt_bufs(m, nullptr).total, &m->tdt_buf));
   // At most max_symbols decisions per frame (and the global budget is as many), so no more tokens.
   const long most = (long)frames * m->max_symbols;
   if (most > INT_MAX / 2) return wh_fail(c, WH_EARG, "tdt: %d frames is too many", frames);
@@ -1314,6 +1321,7 @@ int tdt_greedy_device(wh_model *m, const float *enc, int frames, int width, uint
     CK(wh_alloc(c, (size_t)2 * need, &p));
     m->tdt_list = (uint32_t *)p, m->tdt_list_cap = need;
   }
+  const TdtArgs a = tdt_args(m);
   TdtState init{};
   init.left = m->global ? (int)most : -1;
   init.idle = 1;
@@ -1322,15 +1330,15 @@ int tdt_greedy_device(wh_model *m, const float *enc, int frames, int width, uint
   init.cap = need;
   init.enc = enc;
   init.out = m->tdt_list;
-  CK(launch_tdt_init(c, m->tdt_st, init));
+  CK(launch_tdt_init(c, a.st, a.nx, init));
   // The first predict(None): a zero input and state.
-  const TdtBufs b = tdt_bufs(m, m->tdt_buf);
-  CK(launch_zero(c, b.h, (size_t)(b.gates - b.h) * 4));
-  CK(tdt_predict(m, b, nullptr));
+  CK(launch_zero(c, a.h_old, (size_t)(a.pred - a.h_old) * 4));
+  CK(launch_tdt(c, a, TDT_INIT));
+  CK(launch_tdt(c, a, TDT_PRED));
   TdtState s{};
   for (;;) {
     CK(run_recorded(m, {TDT_CHUNK}, [&] { return tdt_decisions(m, TDT_DECISIONS); }));
-    CK(wh_read(c, &s, m->tdt_st, sizeof s));
+    CK(wh_read(c, &s, a.st, sizeof s));
     if (s.done) break;
     if (s.decisions > most) return wh_fail(c, WH_EGPU, "tdt: %d decisions without reaching the end", s.decisions);
   }
@@ -1574,7 +1582,7 @@ void wh_model_free(wh_model *m) {
   for (uint32_t *p : m->own) wh_free(m->ctx, p);
   for (uint32_t *p : m->cross) wh_free(m->ctx, p);
   if (m->ids) wh_free(m->ctx, m->ids);
-  for (void *p : {(void *)m->tdt_buf, (void *)m->tdt_st, (void *)m->tdt_list, (void *)m->ctc_buf, (void *)m->mel.buf})
+  for (void *p : {(void *)m->tdt_buf, (void *)m->tdt_list, (void *)m->ctc_buf, (void *)m->mel.buf})
     if (p) wh_free(m->ctx, p);
   delete m;
 }

@@ -133,8 +133,7 @@ template <int WT, bool PAIR>
 __global__ __launch_bounds__(256) void gemv_wave_kernel(const float *__restrict__ a, const uint8_t *__restrict__ w,
                                                         const float *__restrict__ bias, float *__restrict__ c,
                                                         int rows, int cols, int k, size_t row_bytes, int epi,
-                                                        float alpha, int offset, const int *__restrict__ skip) {
-  if (skip && *skip) return;  // a recorded launch that its device-side flag switches off
+                                                        float alpha, int offset) {
   extern __shared__ float as[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int i = tid; i < k; i += 256) as[i] = a[i];
@@ -194,7 +193,6 @@ struct GemvArgs {
   int stages;     // ceil(rows / rps)
   int per_wg;     // stages per workgroup
   size_t total;   // rows · row_bytes
-  const int *skip;  // non-null: the launch does nothing while *skip != 0 (a device-side switch)
 };
 
 constexpr int GV_NS = 3;       // LDS stages per workgroup (two in flight while one is used)
@@ -221,7 +219,6 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
   constexpr int PER = NI / 4;                                          // per wave (4 waves)
   constexpr int AS = 68;  // floats per item of a in LDS: 64 + 4, so items start 4 banks apart
   static_assert(NI % 4 == 0 && (GV_NS - 2) * PER < 64, "vmcnt range");
-  if (P.skip && *P.skip) return;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t *st = smem;                                                  // GV_NS stages
   const int items = P.k / 64;
@@ -420,10 +417,10 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
 
 template <int WT>
 int gemv_stream(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha, int offset,
-                const float *ln_g, const float *ln_b, const GemvPack *pack, const int *skip) {
+                const float *ln_g, const float *ln_b, const GemvPack *pack) {
   const int items = l->k / 64;
   GemvArgs P{a, l->w, l->bias, c, l->rows, l->cols, l->k, epi, offset, ln_g, ln_b,
-             pack ? *pack : GemvPack{}, alpha, (int)l->row_bytes, 0, 0, 0, 0, skip};
+             pack ? *pack : GemvPack{}, alpha, (int)l->row_bytes, 0, 0, 0, 0};
   P.rps = std::min(256 / items, GV_STAGE / (int)l->row_bytes);
   P.stages = (l->rows + P.rps - 1) / P.rps;
   // Two workgroups per CU (48 KiB of stages each), each streaming a run of stages: measured on
@@ -449,8 +446,7 @@ int gemv_stream(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int e
 }
 
 template <int WT, bool PAIR>
-int gemv_t(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha, int offset,
-           const int *skip) {
+int gemv_t(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha, int offset) {
   int waves = (l->cols + 1) / 2;
   int grid = (waves + 3) / 4;
   size_t lds = sizeof(float) * (size_t)l->k;
@@ -461,7 +457,7 @@ int gemv_t(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, f
   double bytes = (double)l->rows * l->row_bytes + 4.0 * l->k + 4.0 * l->cols * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
   ProfScope prof(ctx, tn, 2.0 * l->rows * l->k, bytes);
   wh_launch(ctx, gemv_wave_kernel<WT, PAIR>, grid, 256, lds, a, l->w, l->bias, c, l->rows, l->cols, l->k,
-                                                              l->row_bytes, epi, alpha, offset, skip);
+                                                              l->row_bytes, epi, alpha, offset);
   return wh_launched(ctx, "gemv");
 }
 
@@ -719,8 +715,7 @@ __global__ void pack_kernel(const float *__restrict__ x, uint32_t *__restrict__ 
 }  // namespace
 
 int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha, int offset,
-                const float *ln_g, const float *ln_b, float *ln_y, const GemvPack *pack, const int *skip) {
-  if (skip && (pack || ln_g)) return wh_fail(ctx, WH_EARG, "gemv: a switched launch takes no fused norm or cache column");
+                const float *ln_g, const float *ln_b, float *ln_y, const GemvPack *pack) {
   if (pack && (!pack->cache || pack->d <= 0 || pack->d % 2 || pack->lo < 0 || pack->lo + 2 * pack->d > l->rows ||
                pack->cols <= 0 || pack->col < 0 || pack->col >= pack->cols))
     return wh_fail(ctx, WH_EARG, "gemv: bad cache column");
@@ -733,9 +728,9 @@ int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int e
   if (pair && l->k / 64 <= 256 && l->row_bytes % 4 == 0 && (int)l->row_bytes <= GV_STAGE && l->rows > 0) {
     int rc = 1;
     switch (l->type) {
-      case WH_Q8_0: rc = gemv_stream<WH_Q8_0>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b, pack, skip); break;
-      case WH_Q4_0: rc = gemv_stream<WH_Q4_0>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b, pack, skip); break;
-      case WH_F16: rc = gemv_stream<WH_F16>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b, pack, skip); break;
+      case WH_Q8_0: rc = gemv_stream<WH_Q8_0>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b, pack); break;
+      case WH_Q4_0: rc = gemv_stream<WH_Q4_0>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b, pack); break;
+      case WH_F16: rc = gemv_stream<WH_F16>(ctx, a, l, c, epi, alpha, offset, ln_g, ln_b, pack); break;
     }
     if (rc != 1) return rc;
   }
@@ -748,12 +743,12 @@ int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int e
     a = ln_y;
   }
   switch (l->type) {
-    case WH_F32: return gemv_t<WH_F32, false>(ctx, a, l, c, epi, alpha, offset, skip);
-    case WH_F16: return gemv_t<WH_F16, false>(ctx, a, l, c, epi, alpha, offset, skip);
-    case WH_Q8_0: return pair ? gemv_t<WH_Q8_0, true>(ctx, a, l, c, epi, alpha, offset, skip)
-                              : gemv_t<WH_Q8_0, false>(ctx, a, l, c, epi, alpha, offset, skip);
-    case WH_Q4_0: return pair ? gemv_t<WH_Q4_0, true>(ctx, a, l, c, epi, alpha, offset, skip)
-                              : gemv_t<WH_Q4_0, false>(ctx, a, l, c, epi, alpha, offset, skip);
+    case WH_F32: return gemv_t<WH_F32, false>(ctx, a, l, c, epi, alpha, offset);
+    case WH_F16: return gemv_t<WH_F16, false>(ctx, a, l, c, epi, alpha, offset);
+    case WH_Q8_0: return pair ? gemv_t<WH_Q8_0, true>(ctx, a, l, c, epi, alpha, offset)
+                              : gemv_t<WH_Q8_0, false>(ctx, a, l, c, epi, alpha, offset);
+    case WH_Q4_0: return pair ? gemv_t<WH_Q4_0, true>(ctx, a, l, c, epi, alpha, offset)
+                              : gemv_t<WH_Q4_0, false>(ctx, a, l, c, epi, alpha, offset);
   }
   return wh_fail(ctx, WH_EARG, "gemv: weight type %d", l->type);
 }

@@ -69,11 +69,24 @@ struct Half {
         r[4 * i] = v.x, r[4 * i + 1] = v.y, r[4 * i + 2] = v.z, r[4 * i + 3] = v.w;
       }
     } else {
-      const uint16_t *u = (const uint16_t *)(row + (size_t)(hb >> 1) * (WT == WH_Q8_0 ? 34 : 18));
-      r[0] = u[0];
-      const int off = WT == WH_Q8_0 ? 1 + 8 * (hb & 1) : 1;
+      // Aligned dword loads (blocks start on 2 bytes; wide loads at 2 bytes past a dword are split by
+      // the hardware): the dword holding the scale, and the 5 dwords covering these 16 weights'
+      // bytes, whose 2-byte words start at bit 0 or 16 of the first (a select, not an indexed register).
+      const size_t at = (size_t)(hb >> 1) * (WT == WH_Q8_0 ? 34 : 18);
+      const size_t data = at + 2 + (WT == WH_Q8_0 ? 16 * (hb & 1) : 0);
+      const uint32_t sc = *(const uint32_t *)(row + (at & ~(size_t)3));
+      const uint32_t *p = (const uint32_t *)(row + (data & ~(size_t)3));
+      uint32_t d[5];
 #pragma unroll
-      for (int e = 0; e < 8; e++) r[1 + e] = u[off + e];
+      for (int i = 0; i < 5; i++) d[i] = p[i];
+      r[0] = (sc >> ((at & 3) * 8)) & 0xffffu;
+      const bool odd = data & 3;  // the words start at bit 16
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const uint32_t even = (d[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        const uint32_t shifted = (d[(e + 1) >> 1] >> (16 * ((e + 1) & 1))) & 0xffffu;
+        r[1 + e] = odd ? shifted : even;
+      }
     }
   }
 

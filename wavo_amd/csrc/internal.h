@@ -177,11 +177,9 @@ struct GemvPack {
 // With ln_g: the product takes LayerNorm(a; ln_g, ln_b) (one row of k): inside the streaming kernel,
 // or written to ln_y (k floats) by its own launch before the general kernel.  With pack: see GemvPack
 // (inside the streaming kernel, or by launch_pack after the general one).
-// With skip (device memory), the launch does nothing while *skip != 0: a recorded sequence switches
-// its GEMVs on and off from the device (not with a fused norm or cache column).
 int launch_gemv(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int epi, float alpha,
                 int offset, const float *ln_g = nullptr, const float *ln_b = nullptr, float *ln_y = nullptr,
-                const GemvPack *pack = nullptr, const int *skip = nullptr);
+                const GemvPack *pack = nullptr);
 // With dpos (device memory), the position offset is (*dpos)·dstride instead of `offset`: a recorded
 // decoder step reads its position from the device.
 int launch_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, const uint32_t *ids,

@@ -368,11 +368,33 @@ def decode_steps(gpu, tokens=224):
         state["pos"] += 1
 
     ms = time_region(gpu, one, tokens)
+    # One window's search (wh_whisper_decode over the same encoder output, SOT prompt): picks on the
+    # device against every step's logits read back and picked on the host; host clock, median of 5
+    # after 2 warm-ups.
+    window = {}
+    for mode in ("device", "host"):
+        gpu.tune("whisper_host", int(mode == "host"))
+        times = []
+        for i in range(7):
+            t0 = time.perf_counter()
+            got = m.whisper_decode(eb, frames)[0]
+            if i >= 2:
+                times.append(time.perf_counter() - t0)
+        window[mode] = (statistics.median(times) * 1e3, got)
+    gpu.tune("whisper_host", 0)
     m.free()
+    n = len(window["device"][1])
+    search = {"ids": n, "equal": window["device"][1] == window["host"][1],
+              "device_ms": round(window["device"][0], 3), "host_ms": round(window["host"][0], 3),
+              "device_us_per_id": round(window["device"][0] * 1e3 / max(n, 1), 2),
+              "host_us_per_id": round(window["host"][0] * 1e3 / max(n, 1), 2),
+              "what": "wh_whisper_decode of one 1500-frame window from SOT (cross K/V, steps, picks; the random "
+                      "model runs to the 256-id budget), host clock, median of 5 after 2 warm-ups; host = every "
+                      "step's logits read back and picked by wh_whisper_pick"}
     return {"workload": f"whisper-large-v3-turbo-shaped decoder step (4 layers, d {d}, {cfg['dec_heads']} heads, "
                         f"{vocab}-token head, cross attention over {frames} frames, q8_0), {tokens} steps back to back "
                         "(weights stay in the MALL between tokens), one recorded pass per step",
-            "us_per_token": round(ms * 1e3, 2), "tokens_per_s": round(1e3 / ms, 1)}
+            "us_per_token": round(ms * 1e3, 2), "tokens_per_s": round(1e3 / ms, 1), "window_search": search}
 
 
 def traffic_for(name):
@@ -605,7 +627,10 @@ def main():
         log(f"GEMV per token {gemv['us_per_token']} us, {gemv['achieved']} GB/s ({gemv['frac'] * 100:.1f}% of HBM); "
             f"kernels {gemv['kernel_frac'] * 100:.1f}%; head {gemv.get('head', {}).get('frac', 0) * 100:.1f}%")
         gemv["decode_step"] = decode_steps(gpu)
-        log(f"decoder step {gemv['decode_step']['us_per_token']} us per token")
+        ws = gemv["decode_step"]["window_search"]
+        log(f"decoder step {gemv['decode_step']['us_per_token']} us per token; window search {ws['ids']} ids: device "
+            f"{ws['device_ms']} ms ({ws['device_us_per_id']} us/id), host picks {ws['host_ms']} ms "
+            f"({ws['host_us_per_id']} us/id), {'equal' if ws['equal'] else 'different'}")
 
     others = None if args.no_configs else other_configs(gpu, model)
     if others:

@@ -87,7 +87,13 @@ void *wh_stream(wh_ctx *ctx);
  *                      (to time that kernel alone, as a model step runs it); "0" restores;
  *   "attn_split"       "n": attention splits its key range n ways (0 = chosen per shape);
  *   "mel_raw"          "1": wh_model_mel writes each filter's sum before the logarithm, without the
- *                      normalization or scaling (to check the transforms bit for bit); "0" restores.
+ *                      normalization or scaling (to check the transforms bit for bit); "0" restores;
+ *   "whisper_host"     "1": wh_whisper_decode reads every step's logits back and picks on the host
+ *                      (wh_whisper_pick), the check of its device search; "0" restores;
+ *   "whisper_logprobs" "1": wh_whisper_decode sums the log-probabilities whatever the no-speech
+ *                      probability (to check them); "0" restores;
+ *   "attend_merge"     "1": wh_attend merges its 256-key parts in the launch's last workgroup (the
+ *                      path of a decoder step's self-attention) instead of a second kernel; "0" restores.
  * Unknown keys and malformed values return WH_EARG. */
 int wh_tune(wh_ctx *ctx, const char *key, const char *value);
 /* Profiling (no counterpart in the reference, whose timing lives in `wavo bench` and GPU timestamp
@@ -313,9 +319,12 @@ int wh_whisper_retrieve(const wh_whisper_ids *ids, const uint32_t *generated, in
 /* The decoding of one window of Whisper::transcribe (src/whisper/mod.rs:226-239, search::decode
  * src/whisper/search.rs:35-71) on the device: the cross K/V of enc_dev [frames][d] (wh_whisper_begin),
  * the decoder over the prompt (n_prompt ids from SOT; 0 = [SOT], the prompt of a model without
- * language tokens), then greedy steps under the rules, each step's logits read back as Gpu::finish
- * reads them, until EOT, 256 new tokens or position min(448, context).  Log-probabilities are summed
- * when the no-speech probability on SOT's logits is above 0.6, as the reference asks for them.
+ * language tokens), then greedy steps under the rules until EOT, 256 new tokens or position
+ * min(448, context).  The search runs on the device: each pick (suppression, timestamp rules, first
+ * argmax, log-softmax) is a kernel over the step's logits that also writes the next step's token and
+ * position, and recorded runs of 8 (step, pick) pairs replay with one small read of the search's
+ * state between runs (the reference reads every step's logits back, Gpu::finish).  Log-probabilities
+ * are summed when the no-speech probability on SOT's logits is above 0.6, as the reference asks for them.
  * Writes the generated ids (without EOT) to out and returns their count (or an error); *no_speech and
  * *avg_logprob (0 when not summed) may be NULL. */
 int wh_whisper_decode(wh_model *m, const float *enc_dev, int frames, const uint32_t *prompt, int n_prompt,

@@ -264,8 +264,11 @@ def test_recorded_pass_replays(gpu):
         gpu.record_end()  # not recording
 
 
-@pytest.mark.parametrize("heads,hd", [(2, 40), (3, 36), (20, 64)])
-def test_attend_and_pack(gpu, heads, hd):
+@pytest.mark.parametrize("merge", [False, True])
+@pytest.mark.parametrize("heads,hd", [(2, 40), (3, 36), (20, 64), (2, 100), (4, 128)])
+def test_attend_and_pack(gpu, heads, hd, merge):
+    """Parts of 256 keys merged by a second kernel, or (merge) by the launch's last part to finish,
+    through the head's counter: 1 to 17 parts in a row on one set of counters."""
     keys = 4100
     d = heads * hd
     kv = rnd(keys * 2 * d, 7).reshape(keys, 2 * d)
@@ -277,13 +280,18 @@ def test_attend_and_pack(gpu, heads, hd):
     part = gpu.buffer(gpu.attend_len(keys, heads, hd))
     ob = gpu.buffer(d)
     gpu.pack(xb, 0, 2 * d, cache, keys, d, keys, 0)
-    for n in (1, 37, 256, 257, 1500, 2049, keys):
-        gpu.attend(qb, cache, part, ob, n, keys, heads, hd)
-        close(gpu.read(ob, (d,)), ox.attend(q, cpu, keys, n, heads, hd), what=f"attend n {n}")
+    gpu.tune("attend_merge", int(merge))
+    try:
+        for n in (1, 37, 256, 257, 1500, 2049, keys, 300):
+            gpu.attend(qb, cache, part, ob, n, keys, heads, hd)
+            close(gpu.read(ob, (d,)), ox.attend(q, cpu, keys, n, heads, hd), what=f"attend n {n}")
+    finally:
+        gpu.tune("attend_merge", 0)
 
 
-def test_attend_long_cache(gpu):
-    # More keys than one workgroup per head takes (8192): 256-key parts merged by a second kernel.
+@pytest.mark.parametrize("merge", [False, True])
+def test_attend_long_cache(gpu, merge):
+    # 32 to 36 parts of 256 keys per head.
     heads, hd, keys = 2, 64, 9000
     d = heads * hd
     kv = rnd(keys * 2 * d, 17).reshape(keys, 2 * d)
@@ -294,9 +302,13 @@ def test_attend_long_cache(gpu):
     part = gpu.buffer(gpu.attend_len(keys, heads, hd))
     ob = gpu.buffer(d)
     gpu.pack(xb, 0, 2 * d, cache, keys, d, keys, 0)
-    for n in (8192, 8193, keys):
-        gpu.attend(qb, cache, part, ob, n, keys, heads, hd)
-        close(gpu.read(ob, (d,)), ox.attend(q, cpu, keys, n, heads, hd), what=f"attend n {n}")
+    gpu.tune("attend_merge", int(merge))
+    try:
+        for n in (8192, 8193, keys):
+            gpu.attend(qb, cache, part, ob, n, keys, heads, hd)
+            close(gpu.read(ob, (d,)), ox.attend(q, cpu, keys, n, heads, hd), what=f"attend n {n}")
+    finally:
+        gpu.tune("attend_merge", 0)
 
 
 def test_pack_layout(gpu):

@@ -1,7 +1,7 @@
 // Decoder kernels for one token: the HBM-bound GEMV over GGUF weight bytes (Pass::gemv,
 // src/gpu/mod.rs:1461-1467; gemm.wgsl:244-307), the embedding row (Pass::embed, :1469-1482;
 // gemm.wgsl:309-327), attention of one query per head over an f16 K/V cache split into parts of
-// 256 keys and their merge (Pass::attend, :1484-1505; decode.wgsl:56-147), and packing f32 rows
+// 256 keys and their merge, in one launch (Pass::attend, :1484-1505; decode.wgsl:56-147), and packing f32 rows
 // into that cache (Pass::pack, :1507-1523; decode.wgsl:148-173).
 //
 // The GEMV streams W once: a workgroup takes a run of whole rows, contiguous in HBM, and each thread
@@ -493,83 +493,123 @@ __global__ void embed_kernel(const uint8_t *__restrict__ w, int type, size_t row
 // reference's WGSL, here they become ±inf (the cache is f16 storage).
 __device__ __forceinline__ uint32_t h16(float x) { return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x); }
 
-constexpr int KEYS = 256;
+constexpr int KEYS = 256;  // keys per workgroup, one per thread (the parts of attend_len)
 
-// Part (c, h): head h's query against keys c·KEYS.. (decode.wgsl:56-119).
-__global__ __launch_bounds__(256) void attend_kernel(const float *__restrict__ q, const uint32_t *__restrict__ kv,
-                                                     float *__restrict__ part, int n, int hd, float scale,
-                                                     int cols, int heads, const int *__restrict__ dn) {
+// Part (c, h): head h's query against keys c·KEYS .. (c+1)·KEYS − 1 (decode.wgsl:56-119).
+//
+// Every load is issued at the start: thread t's key K (all its pairs: K is transposed per head, so a
+// wave's 64 keys read 256 contiguous bytes per pair) and, for p·V, the value pair t % pairs of every
+// (KEYS / pairs)-th key from t / pairs on (a key's pairs are contiguous); then q.  Scores, the
+// softmax over the part and p·V follow from registers and LDS.  A head of one part writes its output;
+// otherwise each part writes (Σ e·v, max, Σ e) for the merge (decode.wgsl:121-147): by combine_kernel
+// when the key count is known at launch (a second launch costs less than the fences below), or with
+// MERGE by whichever of the head's parts finishes last, for a count in device memory (a recorded
+// decoder step, mostly one part: no second launch and no fence then).  There wave 0, which wrote the
+// part, makes it visible device-wide (release fence: the XCDs' L2s are written back) and counts it
+// done on the head's counter; the part that completes the count (acquire fence) merges and puts the
+// counter back to 0 for the next launch.  No workgroup waits on another.
+template <int P, bool MERGE>  // P: pairs per head, at most
+__global__ __launch_bounds__(KEYS) void attend_kernel(const float *__restrict__ q, const uint32_t *__restrict__ kv,
+                                                      float *__restrict__ part, float *__restrict__ o,
+                                                      int *__restrict__ count, int n, int hd, float scale, int cols,
+                                                      int heads, const int *__restrict__ dn) {
   if (dn) n = min(*dn + n, cols);
-  if ((int)blockIdx.x * KEYS >= n) return;  // a grid sized for the most keys: parts past n are unused
-  __shared__ float qs[128];
-  __shared__ float s[KEYS];
-  __shared__ float red[8];
-  __shared__ float2 rv[256];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int pairs = hd / 2, h = blockIdx.y;
-  const size_t k0 = (size_t)h * pairs * cols;
-  const size_t v_stride = (size_t)heads * pairs;
-  const size_t v0 = v_stride * cols + (size_t)h * pairs;
-  for (int i = tid; i < hd; i += 256) qs[i] = (float)(_Float16)q[h * hd + i];
-  __syncthreads();
   const int j0 = blockIdx.x * KEYS;
+  if (j0 >= n) return;  // a grid sized for the most keys: parts past n are unused
+  __shared__ float qs[2 * P];
+  __shared__ float p[KEYS];
+  __shared__ float red[8];
+  __shared__ float2 rv[KEYS];
+  __shared__ int last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pairs = hd / 2, h = blockIdx.y, parts = (n + KEYS - 1) / KEYS;
   const int cnt = min(n - j0, KEYS);
-  float x = -INFINITY;
-  if (tid < cnt) {
-    float acc = 0.0f;
-    for (int i = 0; i < pairs; i++) {
-      uint32_t u = kv[k0 + (size_t)i * cols + j0 + tid];
-      acc += qs[2 * i] * half_bits(u & 0xffffu) + qs[2 * i + 1] * half_bits(u >> 16);
-    }
-    x = acc * scale;
-  }
+  const size_t v_stride = (size_t)heads * pairs;
+  // K of key j0 + tid (clamped into the part; its score is dropped below).
+  const uint32_t *kp = kv + (size_t)h * pairs * cols + j0 + min(tid, cnt - 1);
+  uint32_t ku[P];
+#pragma unroll
+  for (int i = 0; i < P; i++) ku[i] = kp[(size_t)min(i, pairs - 1) * cols];
+  // V: pair c of keys g, g + groups, … of the part (key j is (j % groups, j / groups): j / groups < P
+  // since groups ≥ KEYS / P; clamped into the part, weighted 0 past cnt).
+  const int groups = KEYS / pairs, c = tid % pairs, g = tid / pairs;
+  const uint32_t *vp = kv + v_stride * cols + (size_t)h * pairs + c;
+  uint32_t vu[P];
+#pragma unroll
+  for (int t = 0; t < P; t++) vu[t] = vp[(size_t)(j0 + min(g + groups * t, cnt - 1)) * v_stride];
+  for (int i = tid; i < hd; i += KEYS) qs[i] = (float)(_Float16)q[h * hd + i];
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < P; i++)
+    if (i < pairs) acc += qs[2 * i] * half_bits(ku[i] & 0xffffu) + qs[2 * i + 1] * half_bits(ku[i] >> 16);
+  const float x = tid < cnt ? acc * scale : -INFINITY;
   float m = x;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
   if (lane == 0) red[wave] = m;
   __syncthreads();
   m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  float e = tid < cnt ? __expf(x - m) : 0.0f;
-  s[tid] = e;
+  const float e = tid < cnt ? __expf(x - m) : 0.0f;
+  p[tid] = e;
   float l = e;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+  for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
   if (lane == 0) red[4 + wave] = l;
   __syncthreads();
   l = red[4] + red[5] + red[6] + red[7];
-  const int groups = 256 / pairs;
-  const int c = tid % pairs, g = tid / pairs;
-  float2 o = make_float2(0.0f, 0.0f);
+  float2 ov = make_float2(0.0f, 0.0f);
   if (g < groups)
-    for (int j = g; j < cnt; j += groups) {
-      uint32_t u = kv[v0 + (size_t)(j0 + j) * v_stride + c];
-      o.x += s[j] * half_bits(u & 0xffffu);
-      o.y += s[j] * half_bits(u >> 16);
+#pragma unroll
+    for (int t = 0; t < P; t++) {
+      const int j = g + groups * t;
+      if (j < cnt) {
+        ov.x += p[j] * half_bits(vu[t] & 0xffffu);
+        ov.y += p[j] * half_bits(vu[t] >> 16);
+      }
     }
-  rv[tid] = o;
+  rv[tid] = ov;
   __syncthreads();
-  const int nparts = (n + KEYS - 1) / KEYS;
-  float *pp = part + ((size_t)h * nparts + blockIdx.x) * (hd + 2);
-  if (tid < pairs) {
-    float2 t = make_float2(0.0f, 0.0f);
-    for (int k = 0; k < groups; k++) {
-      t.x += rv[k * pairs + tid].x;
-      t.y += rv[k * pairs + tid].y;
+  float2 sum = make_float2(0.0f, 0.0f);
+  if (tid < pairs)
+    for (int k = 0; k < groups; k++) sum.x += rv[k * pairs + tid].x, sum.y += rv[k * pairs + tid].y;
+  if (parts == 1) {
+    if (tid < pairs) {
+      const float inv = 1.0f / l;
+      o[h * hd + 2 * tid] = sum.x * inv;
+      o[h * hd + 2 * tid + 1] = sum.y * inv;
     }
-    pp[2 * tid] = t.x;
-    pp[2 * tid + 1] = t.y;
+    return;
   }
-  if (tid == 0) {
-    pp[hd] = m;
-    pp[hd + 1] = l;
+  float *pp = part + ((size_t)h * parts + blockIdx.x) * (hd + 2);
+  if (tid < pairs) pp[2 * tid] = sum.x, pp[2 * tid + 1] = sum.y;  // wave 0 (pairs ≤ 64)
+  if (tid == 0) pp[hd] = m, pp[hd + 1] = l;
+  if (!MERGE) return;
+  if (wave == 0) {
+    __threadfence();
+    if (tid == 0) last = atomicAdd(&count[h], 1) == parts - 1;
   }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  // The merge: every part rescaled to the common maximum.
+  const float *base = part + (size_t)h * parts * (hd + 2);
+  float mx = -INFINITY;
+  for (int k = 0; k < parts; k++) mx = fmaxf(mx, base[k * (hd + 2) + hd]);
+  float lt = 0.0f;
+  for (int k = 0; k < parts; k++) lt += __expf(base[k * (hd + 2) + hd] - mx) * base[k * (hd + 2) + hd + 1];
+  if (tid < hd) {
+    float r = 0.0f;
+    for (int k = 0; k < parts; k++) r += __expf(base[k * (hd + 2) + hd] - mx) * base[k * (hd + 2) + tid];
+    o[h * hd + tid] = r / lt;
+  }
+  if (tid == 0) count[h] = 0;
 }
 
-// Per head: the parts rescaled to their common maximum, summed and normalized (decode.wgsl:121-147).
-__global__ void combine_kernel(const float *__restrict__ part, float *__restrict__ o, int n, int hd,
-                               const int *__restrict__ dn, int cols, int kpp) {
-  if (dn) n = min(*dn + n, cols);
-  const int parts = (n + kpp - 1) / kpp;
+// Per head, the parts of attend_kernel rescaled to their common maximum, summed and normalized
+// (decode.wgsl:121-147).
+__global__ void combine_kernel(const float *__restrict__ part, float *__restrict__ o, int n, int hd) {
+  const int parts = (n + KEYS - 1) / KEYS;
   const float *base = part + (size_t)blockIdx.x * parts * (hd + 2);
   float m = -INFINITY;
   for (int c = 0; c < parts; c++) m = fmaxf(m, base[c * (hd + 2) + hd]);
@@ -579,117 +619,6 @@ __global__ void combine_kernel(const float *__restrict__ part, float *__restrict
     float acc = 0.0f;
     for (int c = 0; c < parts; c++) acc += __expf(base[c * (hd + 2) + hd] - m) * base[c * (hd + 2) + i];
     o[blockIdx.x * hd + i] = acc / l;
-  }
-}
-
-// One head's query against all its keys (or one run of them, see kpp) in one workgroup of 16 waves:
-// key j is lane j % 64 of wave (j / 64) % 16 in round j / 1024, its score from the transposed K cache
-// (64 keys of a wave read 256 contiguous bytes per pair); the softmax over all keys; then the waves
-// take keys in turn for p·V (a key's value pairs are contiguous), summed over the waves through LDS.
-// The parts-and-merge arithmetic of decode.wgsl:56-147 regrouped: results differ by f32 rounding.
-constexpr int AT_WAVES = 16, AT_ROUNDS = 8;  // keys ≤ 16·64·8 = 8192
-__global__ __launch_bounds__(64 * AT_WAVES) void attend_one_kernel(const float *__restrict__ q,
-                                                                   const uint32_t *__restrict__ kv,
-                                                                   float *__restrict__ o, int n, int hd, float scale,
-                                                                   int cols, int heads, const int *__restrict__ dn,
-                                                                   float *__restrict__ part, int kpp) {
-  if (dn) n = min(*dn + n, cols);
-  // With kpp > 0 the workgroup (head, c) takes keys c·kpp .. of the head and writes its partial
-  // (Σ e·v, max, Σ e) for combine_kernel instead of the output.
-  const int kb = kpp ? (int)blockIdx.y * kpp : 0;
-  n = kpp ? max(0, min(kpp, n - kb)) : n;
-  __shared__ float qs[128];
-  __shared__ float p[64 * AT_WAVES * AT_ROUNDS];
-  __shared__ float red[2 * AT_WAVES];
-  __shared__ float2 ov[AT_WAVES][64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int pairs = hd / 2, h = blockIdx.x;
-  const size_t k0 = (size_t)h * pairs * cols;
-  const size_t v_stride = (size_t)heads * pairs;
-  const size_t v0 = v_stride * cols + (size_t)h * pairs;
-  for (int i = tid; i < hd; i += 64 * AT_WAVES) qs[i] = (float)(_Float16)q[h * hd + i];
-  __syncthreads();
-  // Scores of the thread's keys (unrolled over the rounds so every load is in flight at once).
-  float sc[AT_ROUNDS];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int r = 0; r < AT_ROUNDS; r++) {
-    const int j = r * 64 * AT_WAVES + wave * 64 + lane;
-    sc[r] = -INFINITY;
-    if (j < n) {
-      float acc = 0.0f;
-      // 32 pairs' loads in flight at once (hd ≤ 64: one round trip per key).
-      for (int i0 = 0; i0 < pairs; i0 += 32) {
-        uint32_t u[32];
-#pragma unroll
-        for (int t = 0; t < 32; t++) u[t] = i0 + t < pairs ? kv[k0 + (size_t)(i0 + t) * cols + kb + j] : 0u;
-#pragma unroll
-        for (int t = 0; t < 32; t++)
-          if (i0 + t < pairs) acc += qs[2 * (i0 + t)] * half_bits(u[t] & 0xffffu) + qs[2 * (i0 + t) + 1] * half_bits(u[t] >> 16);
-      }
-      sc[r] = acc * scale;
-      mx = fmaxf(mx, sc[r]);
-    }
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  mx = red[0];
-  for (int w = 1; w < AT_WAVES; w++) mx = fmaxf(mx, red[w]);
-  float l = 0.0f;
-#pragma unroll
-  for (int r = 0; r < AT_ROUNDS; r++) {
-    const int j = r * 64 * AT_WAVES + wave * 64 + lane;
-    if (j < n) {
-      const float e = __expf(sc[r] - mx);
-      p[j] = e;
-      l += e;
-    }
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
-  if (lane == 0) red[AT_WAVES + wave] = l;
-  __syncthreads();  // p and the sums are complete
-  l = 0.0f;
-  for (int w = 0; w < AT_WAVES; w++) l += red[AT_WAVES + w];
-  // p·V: a wave takes `groups` keys at a time, one value pair per lane.
-  const int groups = 64 / pairs, c = lane % pairs, g = lane / pairs;
-  float2 acc = make_float2(0.0f, 0.0f);
-  if (g < groups) {
-    const int step = AT_WAVES * groups;
-    for (int j0 = wave * groups + g; j0 < n; j0 += 16 * step) {  // 16 keys' loads in flight at once
-      uint32_t u[16];
-#pragma unroll
-      for (int t = 0; t < 16; t++) u[t] = j0 + t * step < n ? kv[v0 + (size_t)(kb + j0 + t * step) * v_stride + c] : 0u;
-#pragma unroll
-      for (int t = 0; t < 16; t++)
-        if (j0 + t * step < n) {
-          const float pj = p[j0 + t * step];
-          acc.x += pj * half_bits(u[t] & 0xffffu);
-          acc.y += pj * half_bits(u[t] >> 16);
-        }
-    }
-  }
-  // Sum over the wave's groups, then over the waves.
-  for (int gg = 1; gg < groups; gg++) {
-    const float ax = __shfl(acc.x, lane + gg * pairs, 64), ay = __shfl(acc.y, lane + gg * pairs, 64);
-    if (g == 0) acc.x += ax, acc.y += ay;
-  }
-  if (g == 0) ov[wave][c] = acc;
-  __syncthreads();
-  if (tid < pairs) {
-    float2 t = make_float2(0.0f, 0.0f);
-    for (int w = 0; w < AT_WAVES; w++) t.x += ov[w][tid].x, t.y += ov[w][tid].y;
-    if (kpp) {
-      float *pp = part + ((size_t)h * gridDim.y + blockIdx.y) * (hd + 2);
-      pp[2 * tid] = t.x, pp[2 * tid + 1] = t.y;
-      if (tid == 0) pp[hd] = mx, pp[hd + 1] = l;
-    } else {
-      const float inv = 1.0f / l;
-      o[h * hd + 2 * tid] = t.x * inv;
-      o[h * hd + 2 * tid + 1] = t.y * inv;
-    }
   }
 }
 
@@ -779,36 +708,30 @@ int launch_embed(wh_ctx *ctx, const wh_linear *l, const float *pos, float *c, co
 
 int launch_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, float *o, int n, int cols,
                   int heads, int hd, const int *dn) {
-  if (n <= 0 || n > cols || heads <= 0 || hd <= 0 || hd > 128 || hd % 2 || !q || !kv || !part || !o)
-    return wh_fail(ctx, WH_EARG, "attend: bad arguments (n %d, cols %d, hd %d)", n, cols, hd);
-  float scale = 1.0f / sqrtf((float)hd);
+  if (n <= 0 || n > cols || heads <= 0 || heads > ATTEND_HEADS || hd <= 0 || hd > 128 || hd % 2 || !q || !kv || !part ||
+      !o)
+    return wh_fail(ctx, WH_EARG, "attend: bad arguments (n %d, cols %d, heads %d, hd %d)", n, cols, heads, hd);
+  if (!ctx->attend_count) return wh_fail(ctx, WH_EGPU, "attend: the context has no part counters");
+  const float scale = 1.0f / sqrtf((float)hd);
   // A key count in device memory: the grid covers the whole cache and parts past it return.
   const int most = dn ? cols : n;
-  if (!dn && n > 1024 && n <= 64 * AT_WAVES * AT_ROUNDS) {
-    // More keys than one workgroup's threads (the cross-attention over 1500 frames): runs of 512
-    // keys per workgroup, merged by a second kernel (measured: 261 against 278 µs per decoder
-    // step; runs of 768 keys 268, of 256 keys 262).
-    const int kpp = 512, parts = (n + kpp - 1) / kpp;
-    ProfScope prof(ctx, "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
-    wh_launch(ctx, attend_one_kernel, dim3(heads, parts), 64 * AT_WAVES, 0, q, kv, o, n, hd, scale, cols, heads, dn,
-                                                                             part, kpp);
-    if (int rc = wh_launched(ctx, "attend")) return rc;
-    ProfScope pc(ctx, "attend_combine", 0.0, 4.0 * parts * heads * (hd + 2.0) + 4.0 * heads * hd);
-    wh_launch(ctx, combine_kernel, heads, 64, 0, part, o, n, hd, dn, cols, kpp);
-    return wh_launched(ctx, "combine");
-  }
-  if (most <= 64 * AT_WAVES * AT_ROUNDS) {  // every key in one workgroup per head: no merge launch
-    ProfScope prof(ctx, "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
-    wh_launch(ctx, attend_one_kernel, heads, 64 * AT_WAVES, 0, q, kv, o, n, hd, scale, cols, heads, dn, nullptr, 0);
+  const dim3 grid((most + KEYS - 1) / KEYS, heads);
+  int *count = ctx->attend_count;
+  ProfScope prof(ctx, dn ? "attend_self" : "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
+  if (dn || most <= KEYS || ctx->attend_merge) {  // one launch: one part, or the merge by the last part
+    if (hd <= 64)
+      wh_launch(ctx, (attend_kernel<32, true>), grid, KEYS, 0, q, kv, part, o, count, n, hd, scale, cols, heads, dn);
+    else
+      wh_launch(ctx, (attend_kernel<64, true>), grid, KEYS, 0, q, kv, part, o, count, n, hd, scale, cols, heads, dn);
     return wh_launched(ctx, "attend");
   }
-  dim3 grid((most + KEYS - 1) / KEYS, heads);
-  ProfScope prof(ctx, "attend", 4.0 * most * heads * hd, 2.0 * most * heads * hd * 2 + 4.0 * heads * hd);
-  wh_launch(ctx, attend_kernel, grid, 256, 0, q, kv, part, n, hd, scale, cols, heads, dn);
-  int rc = wh_launched(ctx, "attend");
-  if (rc) return rc;
+  if (hd <= 64)
+    wh_launch(ctx, (attend_kernel<32, false>), grid, KEYS, 0, q, kv, part, o, count, n, hd, scale, cols, heads, dn);
+  else
+    wh_launch(ctx, (attend_kernel<64, false>), grid, KEYS, 0, q, kv, part, o, count, n, hd, scale, cols, heads, dn);
+  if (int rc = wh_launched(ctx, "attend")) return rc;
   ProfScope pc(ctx, "attend_combine", 0.0, 4.0 * grid.x * heads * (hd + 2.0) + 4.0 * heads * hd);
-  wh_launch(ctx, combine_kernel, heads, 64, 0, part, o, n, hd, dn, cols, KEYS);
+  wh_launch(ctx, combine_kernel, heads, 64, 0, part, o, n, hd);
   return wh_launched(ctx, "combine");
 }
 

@@ -584,3 +584,214 @@ int launch_ctc(wh_ctx *ctx, const float *logits, int frames, int width, int clas
   wh_launch(ctx, ctc_collapse_kernel, 1, 256, 0, ids, frames, blank, out, cap, count);
   return wh_launched(ctx, "ctc collapse");
 }
+
+// ------------------------------------------------------------------------- Whisper's window search
+// search::decode's pick (src/whisper/search.rs:46-127) on the device in two launches, then the loop's
+// bookkeeping (src/whisper/search.rs:35-71): the picked id appended, the next step's token and
+// position written where the recorded step reads them.
+//
+//   whisper_rules_kernel: 1024 ids per workgroup (a float4 of logits and a word of suppression bits
+//     per thread).  The rules only set logits to −∞, so they apply per id: the suppression lists (a
+//     per-id mask), then the timestamp rules as id ranges.  Each workgroup writes its partial: the
+//     maxima of its timestamps, its text and its finite logits, the first maximum over all its ids
+//     and over its timestamps, and the f64 sums of exp(v − its maximum) over its timestamps and
+//     (with log-probabilities) over all its finite logits.
+//   whisper_pick_kernel: one wave merges the partials (sums rescaled to the common maximum): the
+//     timestamps' mass against the best text, the first maximum (over the timestamps when the mass
+//     wins), its log-softmax, and the bookkeeping.
+//
+// The host sums exp(v − max) in id order against the global maximum; here each term is taken against
+// its workgroup's maximum and the sums are rescaled, which changes only the rounding.
+
+namespace {
+
+constexpr int WR_THREADS = 256, WR_IDS = 4 * WR_THREADS, WP_PARTS = 64;  // vocabularies up to 65536 ids
+
+__device__ __forceinline__ float lane4(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
+
+// (value, id) pairs: the greater value, the lower id among equals (the first maximum).
+__device__ __forceinline__ void first_max(float &v, int &i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) v = ov, i = oi;
+}
+
+// The state's view of the rules: which ids die.
+struct Rules {
+  int ts_lo, ts_hi, text_floor, no_ts, begin;
+  uint32_t mbits;
+};
+
+__device__ __forceinline__ Rules rules_of(const WhisperPickArgs &a, int n, int lts, int g1, int g2) {
+  const int begin = a.begin, vocab = a.vocab;
+  const bool last = n > 0 && g1 >= begin, pen = n < 2 || g2 >= begin, n0 = n == 0;
+  Rules r;
+  // A text id dies below text_floor (every text id before the first pick, the ids below EOT after a
+  // lone timestamp); a timestamp outside [ts_lo, ts_hi): timestamps never decrease (ids below the last
+  // one, or below it + 1 when it closed a pair), none after a pair, none past MAX_INITIAL first.
+  r.ts_lo = lts < 0 ? begin : min(last && !pen ? lts : lts + 1, vocab);
+  r.ts_hi = last && pen ? begin : n0 ? min(begin + a.max_initial + 1, vocab) : vocab;
+  r.text_floor = n0 ? begin : last && !pen ? a.eot : 0;
+  r.mbits = n0 ? 0x03030303u : 0x01010101u;  // suppressed; suppressed at the first pick
+  r.no_ts = a.no_ts;
+  r.begin = begin;
+  return r;
+}
+
+template <int N>
+__device__ __forceinline__ void block_max(float (&v)[N], float *red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+    for (int t = 0; t < N; t++) v[t] = fmaxf(v[t], __shfl_xor(v[t], o, 64));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0)
+#pragma unroll
+    for (int t = 0; t < N; t++) red[4 * t + (threadIdx.x >> 6)] = v[t];
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < N; t++) v[t] = fmaxf(fmaxf(red[4 * t], red[4 * t + 1]), fmaxf(red[4 * t + 2], red[4 * t + 3]));
+}
+
+__global__ __launch_bounds__(WR_THREADS) void whisper_rules_kernel(WhisperPickArgs a) {
+  __shared__ float redf[4 * 4];
+  __shared__ double redd[2 * 4];
+  __shared__ float redv[2 * 4];
+  __shared__ int redi[2 * 4];
+  const int tid = threadIdx.x, vocab = a.vocab, quads = (vocab + 3) / 4;
+  const int q = min((int)blockIdx.x * WR_THREADS + tid, quads - 1);  // clamped: ids past vocab die below
+  const float4 lg = reinterpret_cast<const float4 *>(a.logits)[q];
+  const uint32_t mk = reinterpret_cast<const uint32_t *>(a.mask)[q];
+  const WhisperState *st = a.st;
+  const int done = st->done, n = st->n, lts = st->last_ts, logprobs = st->logprobs;
+  const int g1 = (int)a.gen[max(n - 1, 0)], g2 = (int)a.gen[max(n - 2, 0)];
+  if (done) return;
+  const Rules r = rules_of(a, n, lts, g1, g2);
+  const int i0 = 4 * ((int)blockIdx.x * WR_THREADS + tid);
+  float v[4];
+  // mx: the maxima of the timestamps, the text and the finite logits.
+  float mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+  float bv = -INFINITY, tv = -INFINITY;  // first maxima over all ids and over the timestamps
+  int bi = i0, ti = INT_MAX;
+  const uint32_t m = mk & r.mbits;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int i = i0 + e;
+    const bool ts = i >= r.begin;
+    const bool kill = ((m >> (8 * e)) & 0xffu) != 0 || i == r.no_ts || i < r.text_floor || (ts && i < r.ts_lo) ||
+                      i >= r.ts_hi || i >= vocab;
+    v[e] = kill ? -INFINITY : lane4(lg, e);
+    if (ts) mx[0] = fmaxf(mx[0], v[e]);
+    else mx[1] = fmaxf(mx[1], v[e]);
+    if (isfinite(v[e])) mx[2] = fmaxf(mx[2], v[e]);
+    if (v[e] > bv) bv = v[e], bi = i;
+    if (ts && i < vocab && (ti == INT_MAX || v[e] > tv)) tv = v[e], ti = i;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    first_max(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+    first_max(tv, ti, __shfl_xor(tv, o, 64), __shfl_xor(ti, o, 64));
+  }
+  if ((tid & 63) == 0) redv[tid >> 6] = bv, redi[tid >> 6] = bi, redv[4 + (tid >> 6)] = tv, redi[4 + (tid >> 6)] = ti;
+  block_max(mx, redf);
+  // The sums against this workgroup's maxima.
+  double s[2] = {0.0, 0.0};
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    if (i0 + e >= r.begin && isfinite(v[e])) s[0] += exp((double)(v[e] - mx[0]));
+    if (logprobs && isfinite(v[e])) s[1] += exp((double)(v[e] - mx[2]));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s[0] += __shfl_xor(s[0], o, 64), s[1] += __shfl_xor(s[1], o, 64);
+  if ((tid & 63) == 0) redd[tid >> 6] = s[0], redd[4 + (tid >> 6)] = s[1];
+  __syncthreads();
+  if (tid != 0) return;
+  WhisperPart p;
+  p.s_ts = redd[0] + redd[1] + redd[2] + redd[3];
+  p.s_all = redd[4] + redd[5] + redd[6] + redd[7];
+  p.tmax = mx[0], p.text = mx[1], p.fmax = mx[2];
+  p.best_v = redv[0], p.best_i = redi[0], p.ts_v = redv[4], p.ts_i = redi[4];
+  for (int w = 1; w < 4; w++) first_max(p.best_v, p.best_i, redv[w], redi[w]), first_max(p.ts_v, p.ts_i, redv[4 + w], redi[4 + w]);
+  a.part[blockIdx.x] = p;
+}
+
+__global__ __launch_bounds__(64) void whisper_pick_kernel(WhisperPickArgs a, int parts) {
+  const int lane = threadIdx.x;
+  WhisperState *st = a.st;
+  const WhisperPart p = a.part[min(lane, parts - 1)];
+  if (st->done) return;
+  const bool mine = lane < parts;
+  // The common maxima, then the sums rescaled to them.
+  float tmax = mine ? p.tmax : -INFINITY, text = mine ? p.text : -INFINITY, fmx = mine ? p.fmax : -INFINITY;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    tmax = fmaxf(tmax, __shfl_xor(tmax, o, 64));
+    text = fmaxf(text, __shfl_xor(text, o, 64));
+    fmx = fmaxf(fmx, __shfl_xor(fmx, o, 64));
+  }
+  double s_ts = mine && isfinite(p.tmax) ? p.s_ts * exp((double)p.tmax - (double)tmax) : 0.0;
+  double s_all = mine && isfinite(p.fmax) ? p.s_all * exp((double)p.fmax - (double)fmx) : 0.0;
+  float bv = mine ? p.best_v : -INFINITY, tv = mine ? p.ts_v : -INFINITY;
+  int bi = mine ? p.best_i : INT_MAX, ti = mine ? p.ts_i : INT_MAX;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    s_ts += __shfl_xor(s_ts, o, 64);
+    s_all += __shfl_xor(s_all, o, 64);
+    first_max(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+    first_max(tv, ti, __shfl_xor(tv, o, 64), __shfl_xor(ti, o, 64));
+  }
+  if (lane != 0) return;
+  // The timestamps' total probability against the best text token (src/whisper/search.rs:99-110);
+  // when it wins, the text dies and the first maximum is over the timestamps.
+  float mass = -INFINITY;
+  if (isfinite(tmax) && s_ts > 0.0) mass = tmax + (float)log(s_ts);
+  const bool no_text = mass > text;
+  const int best = no_text ? ti : bi;
+  const float best_v = no_text ? tv : bv;
+  float lp = 0.0f;
+  if (st->logprobs) lp = no_text ? best_v - (tmax + (float)log(s_ts)) : best_v - (fmx + (float)log(s_all));
+  // The loop (src/whisper/search.rs:35-71): every pick counts; the id is kept unless it is EOT or the
+  // window's new-token budget is spent, and a step follows unless the context is full.
+  const int n = st->n, pos = st->pos;
+  st->picks++;
+  st->sum += (double)lp;
+  if (pos >= st->np + st->max_new || best == a.eot) {
+    st->done = 1;
+    return;
+  }
+  a.gen[n] = (uint32_t)best;
+  st->n = n + 1;
+  if (best >= a.begin) st->last_ts = best;
+  if (pos + 1 > st->limit) {
+    st->done = 1;
+    return;
+  }
+  a.ids[0] = (uint32_t)best;
+  a.ids[1] = (uint32_t)pos;
+  st->pos = pos + 1;
+}
+
+}  // namespace
+
+__global__ void whisper_init_kernel(WhisperState *st, WhisperState init) {
+  if (threadIdx.x == 0) *st = init;
+}
+
+int launch_whisper_init(wh_ctx *ctx, WhisperState *st, const WhisperState &init) {
+  wh_launch(ctx, whisper_init_kernel, 1, 64, 0, st, init);
+  return wh_launched(ctx, "whisper init");
+}
+
+int launch_whisper_pick(wh_ctx *ctx, const WhisperPickArgs &a) {
+  // The logits and the mask are read in whole quads of ids (both buffers are padded to them).
+  const int parts = (a.vocab + WR_IDS - 1) / WR_IDS;
+  if (a.vocab <= 0 || parts > WP_PARTS || a.begin <= 0 || a.begin > a.vocab || a.eot < 0 || a.eot >= a.vocab ||
+      ((uintptr_t)a.logits | (uintptr_t)a.mask) % 16 || !a.part)
+    return wh_fail(ctx, WH_EARG, "whisper pick: bad ids, vocabulary above %d or unaligned buffers", WP_PARTS * WR_IDS);
+  {
+    ProfScope prof(ctx, "whisper_rules", 0.0, 5.0 * a.vocab);
+    wh_launch(ctx, whisper_rules_kernel, parts, WR_THREADS, 0, a);
+    if (int rc = wh_launched(ctx, "whisper rules")) return rc;
+  }
+  ProfScope prof(ctx, "whisper_pick", 0.0, (double)sizeof(WhisperPart) * parts);
+  wh_launch(ctx, whisper_pick_kernel, 1, 64, 0, a, parts);
+  return wh_launched(ctx, "whisper pick");
+}

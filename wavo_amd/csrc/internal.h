@@ -22,10 +22,14 @@ struct wh_prof_rec {
   bool used = false;
 };
 
+constexpr int ATTEND_HEADS = 1024;  // heads of one attend launch, at most
+
 struct wh_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   int cus = 0;
+  // Per head, the parts of an attend launch done so far (0 between launches: the last part resets it).
+  int *attend_count = nullptr;
   // GEMM launch-plan override set by wh_tune("gemm_plan", "bm,bn,wm,wn,stages,split") (tuning sweeps
   // only): all zero = chosen per shape.
   int gemm_plan[6] = {0, 0, 0, 0, 0, 0};
@@ -40,6 +44,14 @@ struct wh_ctx {
   int attn_split = 0;
   // wh_tune("mel_raw", "1") (checks only): the frontends write each filter's sum before the logarithm.
   int mel_raw = 0;
+  // wh_tune("whisper_host", "1") (checks only): wh_whisper_decode picks each token on the host.
+  int whisper_host = 0;
+  // wh_tune("whisper_logprobs", "1") (checks only): the window search sums the picks' log-probabilities
+  // whatever the no-speech probability.
+  int whisper_logprobs = 0;
+  // wh_tune("attend_merge", "1") (checks only): attention over a key count known at launch merges its
+  // parts in its last workgroup, as for a count in device memory, instead of a second kernel.
+  int attend_merge = 0;
   std::string name;
   std::string error;
   // Profiling (wh_profile): 0 off (default), 1 events around every launch, 2 named regions only.
@@ -278,3 +290,27 @@ struct MelArgs {
 };
 // kind 0 Parakeet, 1 GigaAM, 2 Whisper; `frames` frames into a.out; scratch: one float (Whisper).
 int launch_mel(wh_ctx *ctx, const MelArgs &a, int kind, int frames, float *scratch);
+
+// Whisper's window search on the device (greedy.hip): the loop's state, and one pick's arguments
+// (the suppression lists as a per-id mask: bit 0 suppress, bit 1 suppress before the first token).
+struct WhisperState {
+  int n, pos, done, picks, np, limit, max_new, logprobs, last_ts, pad;
+  double sum;
+};
+// One workgroup's share of a pick (greedy.hip): sums of exp(v − its maxima), the maxima, the first
+// maxima over all its ids and over its timestamps.
+struct WhisperPart {
+  double s_ts, s_all;
+  float tmax, text, fmax, best_v, ts_v;
+  int best_i, ts_i, pad;
+};
+struct WhisperPickArgs {
+  const float *logits;
+  int vocab, eot, no_ts, begin, max_initial;
+  const uint8_t *mask;
+  WhisperState *st;
+  uint32_t *gen, *ids;
+  WhisperPart *part;  // a partial per 1024 ids
+};
+int launch_whisper_init(wh_ctx *ctx, WhisperState *st, const WhisperState &init);
+int launch_whisper_pick(wh_ctx *ctx, const WhisperPickArgs &a);

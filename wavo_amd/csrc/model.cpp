@@ -409,6 +409,9 @@ enum Arch { GIGAAM = 0, PARAKEET = 1, WHISPER = 2 };
 constexpr intptr_t WHISPER_STEP = 16;  // the recording key of a Whisper decoder step
 constexpr intptr_t TDT_CHUNK = 17;     // the recording key of a run of TDT decisions
 constexpr int TDT_DECISIONS = 32;      // decisions per recorded run (the host looks at the state between runs)
+constexpr intptr_t WHISPER_LOOP = 18;  // the recording key of a run of Whisper (step, pick) pairs
+constexpr int WHISPER_PICKS = 8;       // (step, pick) pairs per recorded run
+constexpr int WHISPER_MAX_NEW = 256, WHISPER_CONTEXT = 448;  // src/whisper/search.rs:10-11
 
 struct Block {
   Chan norm_ff1, norm_attn, norm_conv, norm_ff2, norm_out, conv_norm, dw;
@@ -526,6 +529,8 @@ struct wh_model {
   int eot = -1, no_timestamps = -1, sot = -1;
   std::vector<int> suppress, begin_suppress;
   float *dlogits = nullptr;
+  // The device window search: [WhisperState | generated ids (WHISPER_MAX_NEW) | partials | suppression mask].
+  float *wsearch = nullptr;
 };
 
 namespace {
@@ -1538,6 +1543,93 @@ int mel_plan(wh_model *m) {
   return WH_OK;
 }
 
+// Decoder::record_step (src/transformer.rs:254-290) for the token and position held at m->ids[0..1]:
+// kernels only, so that a recording replays it for every position.
+int whisper_step_kernels(wh_model *m, float *logits) {
+  const int d = m->d, heads = m->dec_heads, hd = d / heads;
+  wh_ctx *c = m->ctx;
+  const int *dpos = (const int *)(m->ids + 1);
+  CK(launch_embed(c, m->token_embd, m->dec_pos, m->dx, m->ids, 0, 0, dpos, d));
+  // Each LayerNorm runs inside the GEMV that consumes it (its only reader).
+  for (int i = 0; i < m->dec_layers; i++) {
+    const DLayer &l = m->dl[i];
+    // q, k, v, with k and v also written into the self-attention cache's column (Decoder::pack).
+    const GemvPack kv{m->own[i], d, d, m->context, 0, dpos};
+    CK(launch_gemv(c, m->dx, l.qkv, m->dqkv, WH_BIAS, 0.0f, 0, l.norm_self.w, l.norm_self.b, m->dy, &kv));
+    CK(launch_attend(c, m->dqkv, m->own[i], m->dpart, m->datt, 1, m->context, heads, hd, dpos));
+    CK(launch_gemv(c, m->datt, l.self_out, m->dx, WH_RESIDUAL, 1.0f, 0));
+    CK(launch_gemv(c, m->dx, l.cross_q, m->dqkv, WH_BIAS, 0.0f, 0, l.norm_cross.w, l.norm_cross.b, m->dy));
+    CK(launch_attend(c, m->dqkv, m->cross[i], m->dpart, m->datt, m->cross_frames, m->cross_frames, heads, hd));
+    CK(launch_gemv(c, m->datt, l.cross_out, m->dx, WH_RESIDUAL, 1.0f, 0));
+    CK(launch_gemv(c, m->dx, l.fc1, m->dh, WH_GELU, 0.0f, 0, l.norm_ffn.w, l.norm_ffn.b, m->dy));
+    CK(launch_gemv(c, m->dh, l.fc2, m->dx, WH_RESIDUAL, 1.0f, 0));
+  }
+  return launch_gemv(c, m->dx, m->token_embd, logits, WH_BIAS, 0.0f, 0, m->dec_norm.w, m->dec_norm.b, m->dy);
+}
+
+// The window search's loop (src/whisper/search.rs:35-71) on the device, from the logits of the
+// prompt's last step in m->dlogits: a pick, then recorded runs of WHISPER_PICKS (step, pick) pairs
+// until the state says done.  A pair after the end repeats the last step on the same token and
+// position (same cache column, same values) and its pick returns at once.  Returns the number of
+// ids picked, the first `cap` of them in `out`, and the mean log-probability when `logprobs`.
+int whisper_search_device(wh_model *m, int np, int limit, bool logprobs, uint32_t *out, int cap, float *avg) {
+  wh_ctx *c = m->ctx;
+  const int vocab = m->vocab;
+  // [state | generated ids | a partial per 1024 ids (64) | suppression mask, padded to whole quads]
+  constexpr size_t state = 16, parts = 64 * sizeof(WhisperPart) / 4;
+  static_assert(sizeof(WhisperState) <= state * 4 && sizeof(WhisperPart) % 8 == 0, "search buffer slots");
+  const size_t mask = ((size_t)vocab + 3) / 4, at_mask = state + WHISPER_MAX_NEW + parts;
+  if (!m->wsearch) {
+    float *p = dev_alloc(m, at_mask + mask);
+    if (!p) return WH_EOOM;
+    // Bit 0: suppressed (src/whisper/search.rs:47-49); bit 1: suppressed at the window's first pick (:50-54).
+    std::vector<uint8_t> bits((size_t)mask * 4, 0);
+    for (int id : m->suppress) bits[id] |= 1;
+    for (int id : m->begin_suppress) bits[id] |= 2;
+    CK(wh_write(c, p + at_mask, bits.data(), bits.size()));
+    m->wsearch = p;
+  }
+  WhisperPickArgs a{};
+  a.logits = m->dlogits;
+  a.vocab = vocab;
+  a.eot = m->eot;
+  a.no_ts = m->no_timestamps;
+  a.begin = m->no_timestamps + 1;
+  a.max_initial = 50;  // src/whisper/search.rs:13
+  a.mask = (const uint8_t *)(m->wsearch + at_mask);
+  a.st = (WhisperState *)m->wsearch;
+  a.gen = (uint32_t *)(m->wsearch + state);
+  a.part = (WhisperPart *)(m->wsearch + state + WHISPER_MAX_NEW);
+  a.ids = m->ids;
+  WhisperState init{};
+  init.pos = np;
+  init.np = np;
+  init.limit = limit;
+  init.max_new = WHISPER_MAX_NEW;
+  init.logprobs = logprobs;
+  init.last_ts = -1;
+  CK(launch_whisper_init(c, a.st, init));
+  CK(launch_whisper_pick(c, a));
+  WhisperState s{};
+  CK(wh_read(c, &s, a.st, sizeof s));
+  for (int runs = 0; !s.done; runs++) {
+    if (runs > WHISPER_MAX_NEW / WHISPER_PICKS + 1) return wh_fail(c, WH_EGPU, "whisper search: no end after %d picks", s.picks);
+    CK(run_recorded(m, {WHISPER_LOOP, (intptr_t)m->dlogits, m->cross_frames}, [&] {
+      for (int i = 0; i < WHISPER_PICKS; i++) {
+        CK(whisper_step_kernels(m, m->dlogits));
+        CK(launch_whisper_pick(c, a));
+      }
+      return WH_OK;
+    }));
+    CK(wh_read(c, &s, a.st, sizeof s));
+  }
+  if (s.n < 0 || s.n > WHISPER_MAX_NEW || s.picks <= 0) return wh_fail(c, WH_EGPU, "whisper search: bad state");
+  const int k = std::min(s.n, cap);
+  if (k > 0) CK(wh_read(c, out, a.gen, (size_t)k * 4));
+  if (avg) *avg = logprobs ? (float)(s.sum / s.picks) : 0.0f;
+  return s.n;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1746,31 +1838,10 @@ int wh_whisper_step(wh_model *m, int token, int pos, float *logits) {
   if (!m || m->arch != WHISPER || !logits || m->own.empty() || pos < 0 || pos >= m->context || token < 0 ||
       token >= m->vocab)
     return WH_EARG;
-  const int d = m->d, heads = m->dec_heads, hd = d / heads;
-  wh_ctx *c = m->ctx;
   // The token and position go to device memory; the step itself reads them there, so one recording
   // serves every position.
-  CK(launch_step_args(c, m->ids, token, pos));
-  const int *dpos = (const int *)(m->ids + 1);
-  // Decoder::record_step (src/transformer.rs:254-290).
-  return run_recorded(m, {WHISPER_STEP, (intptr_t)logits, m->cross_frames}, [&] {
-    CK(launch_embed(c, m->token_embd, m->dec_pos, m->dx, m->ids, 0, 0, dpos, d));
-    // Each LayerNorm runs inside the GEMV that consumes it (its only reader).
-    for (int i = 0; i < m->dec_layers; i++) {
-      const DLayer &l = m->dl[i];
-      // q, k, v, with k and v also written into the self-attention cache's column (Decoder::pack).
-      const GemvPack kv{m->own[i], d, d, m->context, 0, dpos};
-      CK(launch_gemv(c, m->dx, l.qkv, m->dqkv, WH_BIAS, 0.0f, 0, l.norm_self.w, l.norm_self.b, m->dy, &kv));
-      CK(launch_attend(c, m->dqkv, m->own[i], m->dpart, m->datt, 1, m->context, heads, hd, dpos));
-      CK(launch_gemv(c, m->datt, l.self_out, m->dx, WH_RESIDUAL, 1.0f, 0));
-      CK(launch_gemv(c, m->dx, l.cross_q, m->dqkv, WH_BIAS, 0.0f, 0, l.norm_cross.w, l.norm_cross.b, m->dy));
-      CK(launch_attend(c, m->dqkv, m->cross[i], m->dpart, m->datt, m->cross_frames, m->cross_frames, heads, hd));
-      CK(launch_gemv(c, m->datt, l.cross_out, m->dx, WH_RESIDUAL, 1.0f, 0));
-      CK(launch_gemv(c, m->dx, l.fc1, m->dh, WH_GELU, 0.0f, 0, l.norm_ffn.w, l.norm_ffn.b, m->dy));
-      CK(launch_gemv(c, m->dh, l.fc2, m->dx, WH_RESIDUAL, 1.0f, 0));
-    }
-    return launch_gemv(c, m->dx, m->token_embd, logits, WH_BIAS, 0.0f, 0, m->dec_norm.w, m->dec_norm.b, m->dy);
-  });
+  CK(launch_step_args(m->ctx, m->ids, token, pos));
+  return run_recorded(m, {WHISPER_STEP, (intptr_t)logits, m->cross_frames}, [&] { return whisper_step_kernels(m, logits); });
 }
 
 
@@ -1795,8 +1866,7 @@ int wh_whisper_decode(wh_model *m, const float *enc, int frames, const uint32_t 
   if (n_prompt && (int)prompt[0] != m->sot) return wh_fail(m->ctx, WH_EARG, "wh_whisper_decode: the prompt starts with SOT");
   for (int i = 0; i < n_prompt; i++)
     if ((int)prompt[i] >= m->vocab) return wh_fail(m->ctx, WH_EARG, "wh_whisper_decode: prompt id out of the vocabulary");
-  constexpr int MAX_NEW = 256, CONTEXT = 448;  // src/whisper/search.rs:10-11
-  constexpr float NO_SPEECH = 0.6f;            // src/whisper/mod.rs:31
+  constexpr float NO_SPEECH = 0.6f;  // src/whisper/mod.rs:31
   wh_ctx *c = m->ctx;
   (void)hipSetDevice(c->device);
   const int vocab = m->vocab, vp = vocab % 32 == 0 ? vocab : (vocab + 63) / 64 * 64;
@@ -1805,22 +1875,22 @@ int wh_whisper_decode(wh_model *m, const float *enc, int frames, const uint32_t 
   const uint32_t sot_only = (uint32_t)m->sot;
   const uint32_t *pr = n_prompt ? prompt : &sot_only;
   const int np = n_prompt ? n_prompt : 1;
-  if (np > std::min(CONTEXT, m->context)) return wh_fail(c, WH_EARG, "wh_whisper_decode: prompt longer than the context");
+  const int limit = std::min(WHISPER_CONTEXT, m->context);
+  if (np > limit) return wh_fail(c, WH_EARG, "wh_whisper_decode: prompt longer than the context");
   std::vector<float> logits((size_t)vocab);
-  auto step = [&](uint32_t token, int pos) {
-    CK(wh_whisper_step(m, (int)token, pos, m->dlogits));
-    return wh_read(c, logits.data(), m->dlogits, sizeof(float) * (size_t)vocab);
-  };
   // Whisper::window: the decoder on SOT at position 0; its logits give the no-speech probability
   // (src/whisper/mod.rs:226-227), then the rest of the prompt (:235).
-  CK(step(pr[0], 0));
+  CK(wh_whisper_step(m, (int)pr[0], 0, m->dlogits));
+  CK(wh_read(c, logits.data(), m->dlogits, sizeof(float) * (size_t)vocab));
   const float ns = wh_whisper_probability(logits.data(), vocab, m->no_timestamps - 1);
   if (no_speech) *no_speech = ns;
-  for (int i = 1; i < np; i++) CK(step(pr[i], i));
-  const bool logprobs = ns > NO_SPEECH;
+  for (int i = 1; i < np; i++) CK(wh_whisper_step(m, (int)pr[i], i, m->dlogits));
+  const bool logprobs = ns > NO_SPEECH || c->whisper_logprobs;
+  if (!c->whisper_host) return whisper_search_device(m, np, limit, logprobs, out, cap, avg_logprob);
+  // The same loop with each pick on the host (wh_whisper_pick), one read of the logits per step.
+  if (np > 1) CK(wh_read(c, logits.data(), m->dlogits, sizeof(float) * (size_t)vocab));
   wh_whisper_ids ids;
   CK(wh_whisper_ids_of(m, &ids));
-  const int limit = std::min(CONTEXT, m->context);
   std::vector<uint32_t> gen;
   double sum = 0.0;
   int picks = 0;
@@ -1833,11 +1903,12 @@ int wh_whisper_decode(wh_model *m, const float *enc, int frames, const uint32_t 
   };
   int next = pick();
   if (next < 0) return wh_fail(c, WH_EARG, "wh_whisper_decode: bad token ids");
-  for (int pos = np; pos < np + MAX_NEW; pos++) {
+  for (int pos = np; pos < np + WHISPER_MAX_NEW; pos++) {
     if (next == m->eot) break;
     gen.push_back((uint32_t)next);
     if (pos + 1 > limit) break;
-    CK(step((uint32_t)next, pos));
+    CK(wh_whisper_step(m, (int)next, pos, m->dlogits));
+    CK(wh_read(c, logits.data(), m->dlogits, sizeof(float) * (size_t)vocab));
     next = pick();
   }
   if (avg_logprob) *avg_logprob = logprobs ? (float)(sum / picks) : 0.0f;

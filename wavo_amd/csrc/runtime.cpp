@@ -130,6 +130,13 @@ int wh_open(int device_index, wh_ctx **out) {
     delete ctx;
     return wh_fail(nullptr, WH_EGPU, "hipStreamCreate: %s", hipGetErrorString(e));
   }
+  if ((e = hipMalloc((void **)&ctx->attend_count, sizeof(int) * ATTEND_HEADS)) != hipSuccess ||
+      (e = hipMemset(ctx->attend_count, 0, sizeof(int) * ATTEND_HEADS)) != hipSuccess) {
+    if (ctx->attend_count) (void)hipFree(ctx->attend_count);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return wh_fail(nullptr, WH_EGPU, "attend counters: %s", hipGetErrorString(e));
+  }
   // The workspace address of wh_gemm_noalloc on this device; a failed lookup only disables that
   // entry point (it reports the error), every other one works without it.
   (void)gemm_noalloc_init(ctx);
@@ -152,6 +159,7 @@ void wh_close(wh_ctx *ctx) {
   }
   for (hipEvent_t e : ctx->events) (void)hipEventDestroy(e);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->attend_count) (void)hipFree(ctx->attend_count);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
 }
@@ -362,6 +370,12 @@ int wh_tune(wh_ctx *ctx, const char *key, const char *value) {
     ctx->attn_split = std::max(0, std::min(atoi(v), 64));
   } else if (!strcmp(key, "mel_raw")) {
     ctx->mel_raw = atoi(v) != 0;
+  } else if (!strcmp(key, "whisper_host")) {
+    ctx->whisper_host = atoi(v) != 0;
+  } else if (!strcmp(key, "whisper_logprobs")) {
+    ctx->whisper_logprobs = atoi(v) != 0;
+  } else if (!strcmp(key, "attend_merge")) {
+    ctx->attend_merge = atoi(v) != 0;
   } else {
     return wh_fail(ctx, WH_EARG, "wh_tune: unknown key \"%s\"", key);
   }

@@ -69,11 +69,15 @@ class _Builder:
     def f32(self, name, dims, values):
         self.w.tensor(name, dims, gguf.F32, np.ascontiguousarray(values, np.float32).tobytes())
 
-    def linear(self, name, dims, bias=True):
-        """A GEMM weight in the model's type (ggml dims, last = outputs), with a N(0, 0.02) bias."""
+    def linear(self, name, dims, bias=True, row_scale=None):
+        """A GEMM weight in the model's type (ggml dims, last = outputs), with a N(0, 0.02) bias;
+        row_scale (row, factor) multiplies one output row."""
         n = int(np.prod(dims))
         w = self.normal(name + ".weight", n)
         k = int(np.prod(dims[:-1]))
+        if row_scale is not None:
+            r, f = row_scale
+            w[r * k:(r + 1) * k] *= np.float32(f)
         wt = self.wtype if k % 32 == 0 else gguf.F32
         # Quantize in pieces of 16M values to bound the temporary memory.
         step = 1 << 24
@@ -320,7 +324,8 @@ def build_whisper(c, b):
         b.linear(p + "ffn.fc1", [d, c["d_ff"]])
         b.linear(p + "ffn.fc2", [c["d_ff"], d])
     b.norm("dec.final_norm", d)
-    b.linear("dec.token_embd", [d, vocab], False)
+    # eot_scale: EOT's embedding row (the tied head's EOT logit) scaled, so that a window ends on EOT.
+    b.linear("dec.token_embd", [d, vocab], False, (eot, c["eot_scale"]) if "eot_scale" in c else None)
     b.f32("dec.pos_emb.weight", [d, c["context"]], b.normal("dec.pos_emb.weight", d * c["context"]))
 
 

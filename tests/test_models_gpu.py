@@ -85,6 +85,23 @@ def test_parakeet_small(gpu, wtype):
     check_tdt(m, om, got, want)
 
 
+@pytest.mark.parametrize("small,seconds", [(True, 3.0), (False, 60.0), (False, 7.3)])
+def test_parakeet_attention_reads_in_place(gpu, small, seconds):
+    """One window's attention reads K and the position rows where the projections wrote them, and Vᵀ
+    from the qkv projection's epilogue (no packing launch).  The operands are the same f16 values as
+    after packing, so the encoder output equals the packed path's (wh_tune attn_pack) bit for bit."""
+    m = wa.Model(gpu, synth.model_path("parakeet", small=small, directory=MODELS))
+    mel = synth.parakeet_mel(synth.audio(seconds, seed=9))
+    direct = m.encode(mel)
+    gpu.tune("attn_pack", 1)
+    try:
+        packed = m.encode(mel)
+    finally:
+        gpu.tune("attn_pack", 0)
+    assert direct.shape == packed.shape
+    assert np.array_equal(direct, packed), float(np.abs(direct - packed).max())
+
+
 def test_parakeet_kestrel_valid(gpu):
     # The kestrel length masking: the last mel frame is padding (src/parakeet/mod.rs:140-141).
     path = synth.model_path("parakeet", small=True, directory=MODELS)

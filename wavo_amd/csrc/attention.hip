@@ -621,6 +621,49 @@ int attention_t(wh_ctx *ctx, const T *qk, const T *v, const T *pos, int ps, void
 
 }  // namespace
 
+void attention_layout(int t, int heads, int hd, int rel, int *tk, int *pfront, int *prows) {
+  const Pack sp = pack_shape(t, heads, hd, 1, rel != 0);
+  *tk = sp.tk, *pfront = sp.pfront, *prows = sp.prows;
+}
+
+// Attention over one window whose operands the projections already wrote in the packed layout
+// (launch_gemm_h_heads): K [head][tk][hd], Vᵀ [head][hd][tk] and, with relative positions, the
+// position rows [head][prows][hd] from row pfront; queries (and q + v rows) read from `q` rows of
+// qs halves.  No packing launch.  Head dims of 32, 64 or 128.
+int launch_attention_packed(wh_ctx *ctx, const _Float16 *q, int qs, const _Float16 *qv, const _Float16 *kp,
+                            const _Float16 *vt, const _Float16 *pp, void *o, int t, int heads, int hd, int out16) {
+  if (t <= 0 || heads <= 0 || (hd != 32 && hd != 64 && hd != 128) || !q || !kp || !vt || !o || qs < heads * hd)
+    return wh_fail(ctx, WH_EARG, "attention: bad packed call (t %d, heads %d, head_dim %d)", t, heads, hd);
+  if ((uintptr_t)q % 16 || (qv && (uintptr_t)qv % 16) || (uintptr_t)kp % 16 || (uintptr_t)vt % 16 ||
+      (pp && (uintptr_t)pp % 16) || (uintptr_t)o % 16 || qs % 8)
+    return wh_fail(ctx, WH_EARG, "attention: buffers must be 16-byte aligned");
+  const bool rel = pp != nullptr;
+  if (rel != (qv != nullptr)) return wh_fail(ctx, WH_EARG, "attention: relative positions take q + v rows");
+  const int ch = heads * hd;
+  Args a{};
+  a.t = t;
+  a.hd = hd;
+  a.heads = heads;
+  a.scale = 1.0f / sqrtf((float)hd);
+  a.valid = t;
+  a.o = o;
+  a.o16 = out16 != 0;
+  a.os = ch;
+  a.bo = (long)t * ch;
+  a.q = q, a.qv = qv, a.qs = qs, a.bq = (long)t * qs;
+  a.kp = kp, a.vt = vt, a.pp = pp;
+  const Pack sp = pack_shape(t, heads, hd, 1, rel);
+  a.tk = sp.tk, a.pfront = sp.pfront, a.prows = sp.prows;
+  a.nsplit = kv_splits(ctx, t, heads, hd, 1, rel);
+  if (a.nsplit > 1) {
+    uint8_t *ws = (uint8_t *)wh_scratch(ctx, split_bytes(a.nsplit, t, heads, hd, 1));
+    if (!ws) return WH_EOOM;
+    a.po = (float *)ws;
+    a.pml = a.po + ((size_t)a.nsplit * t * heads * hd + 63) / 64 * 64;
+  }
+  return rel ? launch_flash<true>(ctx, a, heads, 1, hd) : launch_flash<false>(ctx, a, heads, 1, hd);
+}
+
 size_t attention_scratch_bytes(const wh_ctx *ctx, int t, int heads, int hd, int batch, int rel) {
   return pack_shape(t, heads, hd, batch, rel != 0).bytes() +
          split_bytes(kv_splits(ctx, t, heads, hd, batch, rel != 0), t, heads, hd, batch);

@@ -377,6 +377,8 @@ struct LdsArgs {
   int m, rows, cols, k, dual, ldc, epi;
   float alpha;
   size_t row_bytes;
+  HeadsOut ho[2];  // column ranges written in attention's packed layout instead of into c (f16 outputs)
+  int nho;
 };
 
 // s_waitcnt with vmcnt = N (0..63) and no wait on the other counters (gfx9 encoding: vmcnt bits
@@ -410,6 +412,46 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
   constexpr int G8 = BN / 8;
   const int m = P.m, rows = P.rows;
   static_assert((BM * G8) % NT == 0, "whole rounds of column groups");
+  if constexpr (OUT16 && !SPLIT) {
+    // A tile inside a packed range (the host keeps each range on whole tiles): f16 rows per head or,
+    // transposed, 8 rows of one column per store; the epilogue as below (no residual, no dual).
+    for (int o = 0; o < P.nho; o++) {
+      const HeadsOut &h = P.ho[o];
+      if (n0 < h.col0 || n0 >= h.col0 + h.cols) continue;
+      if (h.tr) {
+#pragma unroll
+        for (int it = 0; it < BM * G8 / NT; it++) {
+          const int e = tid + it * NT, c = e % BN, r0 = 8 * (e / BN), row0 = m0 + r0, col = n0 + c;
+          if (row0 >= h.rs || col >= P.cols) continue;
+          const float b = P.bias[col];
+          half8 y;
+#pragma unroll
+          for (int q = 0; q < 8; q++)
+            y[q] = (_Float16)(row0 + q < m ? epilogue(P.epi, 0.0f, cl[(r0 + q) * crow + c] + b, nullptr) : 0.0f);
+          *(half8 *)(h.dst + (size_t)(col - h.col0) * h.rs + row0) = y;  // head j, dim i: row j·hd + i
+        }
+      } else {
+#pragma unroll
+        for (int it = 0; it < BM * G8 / NT; it++) {
+          const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0 + r, col = n0 + c8;
+          if (row + h.r0 >= h.rs || col >= P.cols) continue;
+          half8 y;
+          if (row < m) {
+            const float4 x0 = *(const float4 *)(cl + r * crow + c8), x1 = *(const float4 *)(cl + r * crow + c8 + 4);
+            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int q = 0; q < 8; q++) y[q] = (_Float16)epilogue(P.epi, 0.0f, x[q] + bb[q], nullptr);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 8; q++) y[q] = (_Float16)0.0f;
+          }
+          const int v = col - h.col0;  // 8 columns of one head (hd % 8 == 0)
+          *(half8 *)(h.dst + ((size_t)(v / h.hd) * h.rs + h.r0 + row) * h.hd + v % h.hd) = y;
+        }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int it = 0; it < BM * G8 / NT; it++) {
     const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0 + r, col = n0 + c8;
@@ -826,12 +868,21 @@ void lds_launch(wh_ctx *ctx, dim3 grid, const LdsArgs &a, bool split, bool out16
 
 template <int WT>
 int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
-                 bool out16, float *part, int *splits) {
+                 bool out16, float *part, int *splits, const HeadsOut *ho, int nho) {
   Plan p = plan_for(ctx, m, l->cols, l->k);
-  if (p.split > 1 && !part) p.split = 1;
+  if ((p.split > 1 && !part) || nho) p.split = 1;  // packed ranges are written by the tiles' own epilogue
   if (splits) *splits = p.split;
   LdsArgs args{a, l->w, l->bias, p.split > 1 ? (void *)part : c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha,
-               l->row_bytes};
+               l->row_bytes, {}, nho};
+  if (nho < 0 || nho > 2) return wh_fail(ctx, WH_EARG, "gemm: %d packed ranges", nho);
+  for (int i = 0; i < nho; i++) {
+    const HeadsOut &h = ho[i];
+    // Whole tiles, inside the real columns, no dual columns; 16-byte stores.
+    if (!out16 || h.col0 % p.bn || h.cols % p.bn || h.col0 + h.cols > l->rows || h.col0 < l->dual || h.hd % 8 ||
+        h.cols % h.hd || (uintptr_t)h.dst % 16 || h.r0 < 0 || (h.tr ? h.r0 || h.rs % 8 || h.rs < m : h.rs < h.r0 + m))
+      return wh_fail(ctx, WH_EARG, "gemm: packed output %d off the %d-column tiles or its layout", i, p.bn);
+    args.ho[i] = h;
+  }
   dim3 grid((l->cols + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.split);
   static const char *tn = WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
   // Named by kernel variant and call shape: m x rows x k, epilogue, output type, row width.
@@ -899,11 +950,11 @@ size_t split_bytes(const wh_ctx *ctx, const wh_linear *l, int m) {
 // GEMM stops after writing its partial sums (the caller finishes them) and *splits is the count
 // (1: c was written whole).
 int launch_lds(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
-               bool out16, float *part, int *splits = nullptr) {
+               bool out16, float *part, int *splits = nullptr, const HeadsOut *ho = nullptr, int nho = 0) {
   switch (l->type) {
-    case WH_Q8_0: return launch_lds_t<WH_Q8_0>(ctx, a, l, c, m, ldc, epi, alpha, out16, part, splits);
-    case WH_Q4_0: return launch_lds_t<WH_Q4_0>(ctx, a, l, c, m, ldc, epi, alpha, out16, part, splits);
-    default: return launch_lds_t<WH_F16>(ctx, a, l, c, m, ldc, epi, alpha, out16, part, splits);
+    case WH_Q8_0: return launch_lds_t<WH_Q8_0>(ctx, a, l, c, m, ldc, epi, alpha, out16, part, splits, ho, nho);
+    case WH_Q4_0: return launch_lds_t<WH_Q4_0>(ctx, a, l, c, m, ldc, epi, alpha, out16, part, splits, ho, nho);
+    default: return launch_lds_t<WH_F16>(ctx, a, l, c, m, ldc, epi, alpha, out16, part, splits, ho, nho);
   }
 }
 
@@ -1064,6 +1115,17 @@ int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int
   }
   if (out16) return launch_typed<true, true>(ctx, a16, l, c, m, ldc, epi, alpha);
   return launch_typed<true, false>(ctx, a16, l, c, m, ldc, epi, alpha);
+}
+
+int launch_gemm_h_heads(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int ldc, int epi,
+                        const HeadsOut *outs, int n) {
+  if (int rc = check(ctx, a16, l, c, m, epi)) return rc;
+  if (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL) return wh_fail(ctx, WH_EARG, "gemm: packed output with a residual epilogue");
+  if (!lds_path(l, c, ldc) || !outs || n <= 0) return wh_fail(ctx, WH_EARG, "gemm: packed output needs the main kernel");
+  for (int i = 0; i < n; i++)
+    if (!outs[i].dst || outs[i].hd <= 0) return wh_fail(ctx, WH_EARG, "gemm: packed output %d", i);
+  if (m == 0) return WH_OK;
+  return launch_lds(ctx, (const _Float16 *)a16, l, c, m, ldc, epi, 0.0f, true, nullptr, nullptr, outs, n);
 }
 
 int launch_gemm_h_ln(wh_ctx *ctx, const void *a16, const wh_linear *l, float *x, int m, float alpha, const float *g,

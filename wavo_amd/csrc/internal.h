@@ -52,6 +52,9 @@ struct wh_ctx {
   // wh_tune("attend_merge", "1") (checks only): attention over a key count known at launch merges its
   // parts in its last workgroup, as for a count in device memory, instead of a second kernel.
   int attend_merge = 0;
+  // wh_tune("attn_pack", "1") (checks only): the encoder's attention packs K, Vᵀ and the position rows
+  // in a launch of its own, as for padded batches, instead of reading them where they were written.
+  int attn_pack = 0;
   std::string name;
   std::string error;
   // Profiling (wh_profile): 0 off (default), 1 events around every launch, 2 named regions only.
@@ -171,6 +174,17 @@ int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int
 // the residual and the norm follows.  Needs l->cols == cols of x and no dual outputs.  keep_x = 0:
 // x is not needed afterwards (the fused kernel need not store it).  g2: a second LayerNorm of y (f32)
 // into y2 (f16) — the next block's first norm.
+// A GEMM whose columns col0 .. col0 + cols − 1, heads of hd, go to dst in attention's packed layout
+// instead of into c: rows per head (tr false: [head][rs][hd], this call's rows from row r0, rows m ..
+// rs − r0 − 1 as zeros where tiles reach them) or transposed (tr: [head][hd][rs], r0 = 0, zeros for
+// rows m .. rs − 1).
+struct HeadsOut {
+  _Float16 *dst;
+  int col0, cols, hd, rs, r0;
+  bool tr;
+};
+int launch_gemm_h_heads(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int ldc, int epi,
+                        const HeadsOut *outs, int n);
 int launch_gemm_h_ln(wh_ctx *ctx, const void *a16, const wh_linear *l, float *x, int m, float alpha, const float *g,
                      const float *b, void *y, int out16, int keep_x = 1, const float *g2 = nullptr,
                      const float *b2 = nullptr, void *y2 = nullptr);
@@ -206,6 +220,10 @@ int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb
                     const int *valid_dev, int valid, int batch, int out16 = 0);
 // qk / v / pos are f32 (in16 == 0) or f16; o is f32 or f16 (out16).  pos rows are pos_stride
 // elements apart (0: heads · hd).
+// The packed attention operands' shape for one window of t keys (relative: with position rows).
+void attention_layout(int t, int heads, int hd, int rel, int *tk, int *pfront, int *prows);
+int launch_attention_packed(wh_ctx *ctx, const _Float16 *q, int qs, const _Float16 *qv, const _Float16 *kp,
+                            const _Float16 *vt, const _Float16 *pp, void *o, int t, int heads, int hd, int out16);
 int launch_attention(wh_ctx *ctx, const void *qk, const void *v, const void *pos, void *o, int t,
                      int heads, int hd, const int *valid_dev, int valid, int batch, int out16 = 0,
                      int in16 = 0, int pos_stride = 0);

@@ -506,6 +506,9 @@ struct wh_model {
   const void *pos16_cur = nullptr;  // its rows of this call
   int *valid_dev = nullptr;
   float *sub2 = nullptr;   // Parakeet conv3 output (the subsampling's second buffer)
+  // Parakeet: every block's position rows in attention's packed layout for one window,
+  // [layer · head][prows][hd] f16, zero where no call writes.
+  _Float16 *ppk = nullptr;
   float *rope = nullptr;   // GigaAM rope table for `cap` frames
   const float *pos_cur = nullptr;  // Parakeet: the positions of this call (rows from cap - t)
   // Recorded encoder calls (HIP graphs), keyed by the call's arguments and the generations of the
@@ -833,7 +836,8 @@ int arena(wh_model *m, int frames, int batch) {
   drop_graphs(m);
   m->epoch++;
   int F = (std::max(frames, m->cap) + 63) / 64 * 64, B = std::max(batch, std::max(m->cap_batch, 1));
-  for (float *p : {m->x, m->y, m->h, m->qk, m->yr, m->pos, m->sub, m->sub2, m->rope, (float *)m->pos16, (float *)m->posp})
+  for (float *p : {m->x, m->y, m->h, m->qk, m->yr, m->pos, m->sub, m->sub2, m->rope, (float *)m->pos16, (float *)m->posp,
+                   (float *)m->ppk})
     if (p) {
       wh_free(m->ctx, p);
       for (auto &o : m->owned)
@@ -841,7 +845,7 @@ int arena(wh_model *m, int frames, int batch) {
     }
   if (m->valid_dev) wh_free(m->ctx, m->valid_dev);
   m->x = m->y = m->h = m->qk = m->yr = m->pos = m->sub = m->sub2 = m->rope = nullptr;
-  m->pos16 = m->posp = nullptr;
+  m->pos16 = m->posp = m->ppk = nullptr;
   m->valid_dev = nullptr;
   const int d = m->d;
   const size_t rows = (size_t)F * B;
@@ -889,6 +893,15 @@ int arena(wh_model *m, int frames, int batch) {
     m->pos16 = dev_alloc(m, (table.size() + 1) / 2);
     m->posp = dev_alloc(m, ((size_t)(2 * F + 15) * m->layers * d + 1) / 2);
     if (!m->pos16 || !m->posp) return WH_EOOM;
+    const int hd = d / m->heads;
+    if (hd == 32 || hd == 64 || hd == 128) {
+      int most = 0, tk, pfront, prows;
+      for (int t = 1; t <= F; t++) attention_layout(t, m->heads, hd, 1, &tk, &pfront, &prows), most = std::max(most, prows);
+      const size_t n = (size_t)m->layers * d * most;  // halves
+      m->ppk = (_Float16 *)dev_alloc(m, (n + 1) / 2);
+      if (!m->ppk) return WH_EOOM;
+      CK(launch_zero(m->ctx, m->ppk, n * 2));  // a fill kernel on the context's stream
+    }
     CK(launch_to_half(m->ctx, m->pos, m->pos16, table.size()));
   } else if (m->arch == GIGAAM) {
     int hd = d / m->heads;
@@ -910,6 +923,13 @@ int arena(wh_model *m, int frames, int batch) {
 // One block from x into y (y = norm_out(x), x is spent).  pre: the block's first norm (norm_ff1 of x)
 // is already in m->yr as f16 (the previous block's last kernel wrote it); next: the following
 // block's norm_ff1, which this block's last kernel then writes into m->yr.
+// Whether a Parakeet call's attention takes its operands packed by the projections themselves: one
+// window (padded batches pack per call), head dims the packed layout holds unpadded.
+bool packed_attention(const wh_model *m, int batch, const int *valid_dev) {
+  const int hd = m->d / m->heads;
+  return m->relative && m->ppk && batch == 1 && !valid_dev && (hd == 32 || hd == 64 || hd == 128) && !m->ctx->attn_pack;
+}
+
 int record_block(wh_model *m, int layer, const Block &k, float *x, float *y, int t, int batch, const int *valid_dev,
                  bool pre, const Chan *next) {
   wh_ctx *c = m->ctx;
@@ -931,11 +951,23 @@ int record_block(wh_model *m, int layer, const Block &k, float *x, float *y, int
   } else {
     // The FFN's residual projection and the attention norm (one kernel after a k-split GEMM).
     CK(launch_gemm_h_ln(c, h16, k.ff1[1], x, rows, 0.5f, k.norm_attn.w, k.norm_attn.b, y16, 1));
-    CK(g16(y16, k.qkv, m->qk, rows, WH_BIAS, 0.0f, 1));
     // This block's projected position rows (record_blocks projected every block's).
     const int ps = m->pos_all->cols;
-    CK(launch_attention(c, m->qk, nullptr, (const _Float16 *)m->posp + (size_t)layer * d, y16, t, m->heads, hd,
-                        valid_dev, t, batch, 1, 1, ps));
+    const _Float16 *pos = (const _Float16 *)m->posp + (size_t)layer * d;
+    if (packed_attention(m, batch, valid_dev)) {
+      // One window: the projection writes K and Vᵀ in attention's packed layout (after its f16 rows
+      // in qk) and record_blocks wrote every block's position rows packed: no packing launch.
+      int tk, pfront, prows;
+      attention_layout(t, m->heads, hd, 1, &tk, &pfront, &prows);
+      _Float16 *q16 = (_Float16 *)m->qk, *kp = q16 + (size_t)m->cap * 4 * d, *vt = kp + (size_t)m->cap * d;
+      const HeadsOut outs[2] = {{kp, d, d, hd, tk, 0, false}, {vt, 2 * d, d, hd, tk, 0, true}};
+      CK(launch_gemm_h_heads(c, y16, k.qkv, m->qk, rows, k.qkv->cols + k.qkv->dual, WH_BIAS, outs, 2));
+      CK(launch_attention_packed(c, q16, 4 * d, q16 + 3 * d, kp, vt, m->ppk + (size_t)layer * d * prows, y16, t,
+                                 m->heads, hd, 1));
+    } else {
+      CK(g16(y16, k.qkv, m->qk, rows, WH_BIAS, 0.0f, 1));
+      CK(launch_attention(c, m->qk, nullptr, pos, y16, t, m->heads, hd, valid_dev, t, batch, 1, 1, ps));
+    }
   }
   CK(g16(y16, k.out, x, rows, WH_RESIDUAL, 1.0f, 0));
   CK(ln16(k.norm_conv));
@@ -956,8 +988,19 @@ namespace {
 
 // Conformer::record (src/conformer.rs:107-116): `layers` blocks from m->x, output in m->x.
 int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layers) {
-  if (m->relative && layers > 0)  // every block's linear_pos(P) in one GEMM: [2t + 15][layers · d] f16
-    CK(launch_gemm_h(m->ctx, m->pos16_cur, m->pos_all, m->posp, 2 * t + 15, m->pos_all->cols, WH_BIAS, 0.0f, 1));
+  if (m->relative && layers > 0) {  // every block's linear_pos(P) in one GEMM: [2t + 15][layers · d] f16
+    if (packed_attention(m, batch, valid_dev)) {
+      // One window: written as attention's packed position rows, [layer · head][prows][hd] from row
+      // pfront (the rows around them stay zero from the arena's allocation).
+      const int hd = m->d / m->heads;
+      int tk, pfront, prows;
+      attention_layout(t, m->heads, hd, 1, &tk, &pfront, &prows);
+      const HeadsOut out{m->ppk, 0, layers * m->d, hd, prows, pfront, false};
+      CK(launch_gemm_h_heads(m->ctx, m->pos16_cur, m->pos_all, m->posp, 2 * t + 15, m->pos_all->cols, WH_BIAS, &out, 1));
+    } else {
+      CK(launch_gemm_h(m->ctx, m->pos16_cur, m->pos_all, m->posp, 2 * t + 15, m->pos_all->cols, WH_BIAS, 0.0f, 1));
+    }
+  }
   for (int i = 0; i < layers; i++) {
     const Chan *next = i + 1 < layers ? &m->blocks[i + 1].norm_ff1 : nullptr;
     CK(record_block(m, i, m->blocks[i], m->x, m->y, t, batch, valid_dev, i > 0, next));

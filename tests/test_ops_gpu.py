@@ -146,13 +146,19 @@ def test_layer_norm_and_rope(gpu):
     close(gpu.read(out, (cols,)), y[0], what="layer_norm_row")
     gpu.layer_norm(xb, gb, bb, out, rows, cols, tb, outr, hd)
     close(gpu.read(outr, (rows, cols)), yr, what="rope")
-    # Whisper's d = 1280 and a long row past the register path.
-    for cols in (1280, 5000):
-        x = rnd(3 * cols, 9).reshape(3, cols)
+    # The models' widths (GigaAM 768, Parakeet 1024, Whisper 1280: kernels specialized to the width),
+    # with RoPE at 1024, and a long row past the register path.
+    for cols in (768, 1024, 1280, 5000):
+        x = rnd(5 * cols, 9).reshape(5, cols)
         g, b = rnd(cols, 10), rnd(cols, 11)
-        xb, gb, bb, out = gpu.upload(x), gpu.upload(g), gpu.upload(b), gpu.buffer(3 * cols)
-        gpu.layer_norm(xb, gb, bb, out, 3, cols)
-        close(gpu.read(out, (3, cols)), ox.layer_norm(x, g, b), what=f"cols {cols}")
+        xb, gb, bb, out = gpu.upload(x), gpu.upload(g), gpu.upload(b), gpu.buffer(5 * cols)
+        gpu.layer_norm(xb, gb, bb, out, 5, cols)
+        close(gpu.read(out, (5, cols)), ox.layer_norm(x, g, b), what=f"cols {cols}")
+        if cols == 1024:
+            table = rnd(5 * 128, 12).reshape(5, 128)
+            tb, outr = gpu.upload(table), gpu.buffer(5 * cols)
+            gpu.layer_norm(xb, gb, bb, out, 5, cols, tb, outr, 128)
+            close(gpu.read(outr, (5, cols)), ox.layer_norm(x, g, b, table, 128)[1], what="rope 1024")
 
 
 @pytest.mark.parametrize("t_in,ch,conv", [(37, 20, (5, 2, 2)), (37, 20, (3, 1, 1)), (37, 20, (3, 2, 1)),

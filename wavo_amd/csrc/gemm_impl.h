@@ -1,0 +1,902 @@
+// The GEMM kernels and their launch templates, shared by gemm.hip and the per-weight-type
+// translation units gemm_lds_{q8_0,q4_0,f16}.hip (each instantiates the LDS-DMA kernel for one
+// weight type, so that the three compile in parallel).  The kernels are described in gemm.hip.
+#pragma once
+#include <algorithm>
+#include <cstdio>
+#include <mutex>
+#include <type_traits>
+#include <utility>
+#include "internal.h"
+
+// Launch shapes of the LDS-DMA kernel (tile, wavefronts, k step, split).
+struct GemmPlan {
+  int bm, bn, wm, wn, ns, split;
+  int var = 0;  // kernel variant bits: 1 DMA spread over the substeps, 2 16-byte DMA of quantized rows
+};
+
+// The launch plan of an m × cols × k GEMM (gemm.hip).
+GemmPlan gemm_plan_for(const wh_ctx *ctx, int m, int cols, int k);
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BK = 64;       // k per stage: two quantized blocks
+constexpr int LDS_ROW = 72;  // halves per LDS row (144 B: 16-byte aligned rows, banks staggered)
+
+__device__ __forceinline__ float gelu(float x) {
+  // Abramowitz–Stegun 7.1.26 erf, as gemm.wgsl:65-70 and src/cpu/ops.rs:33-40.
+  float z = fabsf(0.70710678118654752440f * x);
+  float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * z);  // 1 ulp, against ~10 instructions of IEEE division
+  float e = 1.0f - (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
+                     0.254829592f) * t * __expf(-z * z);
+  float s = x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : 0.0f);
+  return 0.5f * x * (1.0f + s * e);
+}
+
+__device__ __forceinline__ float epilogue(int epi, float alpha, float v, const float *c) {
+  switch (epi) {
+    case WH_SILU: return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+    case WH_RELU: return fmaxf(v, 0.0f);
+    case WH_RESIDUAL: return *c + alpha * v;
+    case WH_GELU: return gelu(v);
+    case WH_GELU_RESIDUAL: return *c + gelu(v);
+    case WH_TANH: return tanhf(fminf(fmaxf(v, -10.0f), 10.0f));
+    default: return v;
+  }
+}
+
+__device__ __forceinline__ float half_bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+// A operand staging: the BM×64 tile of `a` for one k step, f32 (rounded to f16 when stored to
+// LDS) or already f16.
+template <int BM, bool A16>
+struct AStage {
+  static constexpr int N = A16 ? BM * 64 / 8 / 256 : BM * 64 / 4 / 256;  // 16-byte loads per thread
+  uint4 v[N];
+};
+
+template <int BM, bool A16>
+__device__ __forceinline__ void load_a(AStage<BM, A16> &s, const void *__restrict__ a, int m, int k, int m0, int k0,
+                                       int tid) {
+  constexpr int PER_ROW = A16 ? 8 : 16;  // 16-byte pieces per 64-wide row
+  constexpr int EL = A16 ? 8 : 4;
+#pragma unroll
+  for (int p = 0; p < AStage<BM, A16>::N; p++) {
+    int f = tid + 256 * p, r = f / PER_ROW, q = f % PER_ROW;
+    int row = m0 + r, col = k0 + EL * q;
+    const uint8_t *src = (const uint8_t *)a + ((size_t)row * k + col) * (A16 ? 2 : 4);
+    s.v[p] = (row < m && col < k) ? *(const uint4 *)src : make_uint4(0, 0, 0, 0);
+  }
+}
+
+template <int BM, bool A16>
+__device__ __forceinline__ void store_a(const AStage<BM, A16> &s, _Float16 *As, int tid) {
+#pragma unroll
+  for (int p = 0; p < AStage<BM, A16>::N; p++) {
+    int f = tid + 256 * p;
+    if constexpr (A16) {
+      int r = f >> 3, q = f & 7;
+      *(uint4 *)(As + r * LDS_ROW + 8 * q) = s.v[p];
+    } else {
+      int r = f >> 4, q = f & 15;
+      float4 x = __builtin_bit_cast(float4, s.v[p]);
+      half4 h = {(_Float16)x.x, (_Float16)x.y, (_Float16)x.z, (_Float16)x.w};
+      *(half4 *)(As + r * LDS_ROW + 4 * q) = h;
+    }
+  }
+}
+
+// B operand: each lane of a wave holds, per 32-row MFMA tile j of the wave's W rows, row
+// n = n0 + wn + 32j + lane%32 and the k half g = lane/32 of the 64-wide step — for Q8_0/Q4_0 exactly
+// one GGUF block.  The MFMA's k slots of lane group g at substep s are then k = 32g + 8s..+8 of the
+// step, and the A fragments are read with the same permutation, so the products pair up as in
+// Σ_k a[m][k]·W[n][k].
+template <int WT>
+struct BRaw {
+  static constexpr int D = WT == WH_Q8_0 ? 9 : WT == WH_Q4_0 ? 5 : WT == WH_F16 ? 16 : 32;  // dwords
+  uint32_t d[D];
+};
+
+template <int WT, bool ALIGNED>
+__device__ __forceinline__ void load_b(BRaw<WT> &s, const uint8_t *__restrict__ w, int rows, int k,
+                                       size_t row_bytes, int n, int k0, int g) {
+  const int blk = (k0 >> 5) + g;  // the lane's 32-wide k block
+  const bool ok = n < rows && blk < (k >> 5);
+  const uint8_t *base = w + (size_t)n * row_bytes;
+  if constexpr (WT == WH_F16 || WT == WH_F32) {
+    const uint4 *p = (const uint4 *)(base + (size_t)blk * 32 * (WT == WH_F16 ? 2 : 4));
+#pragma unroll
+    for (int i = 0; i < BRaw<WT>::D / 4; i++) {
+      uint4 v = ok ? p[i] : make_uint4(0, 0, 0, 0);
+      s.d[4 * i] = v.x, s.d[4 * i + 1] = v.y, s.d[4 * i + 2] = v.z, s.d[4 * i + 3] = v.w;
+    }
+  } else {
+    constexpr int BLK = WT == WH_Q8_0 ? 34 : 18;
+    if (ALIGNED) {
+      // k % 64 == 0: block pairs are 4-byte aligned; block g starts at byte g·BLK of its pair, so
+      // block 1 is read from byte BLK − 2 (its scale is then the high half of the first dword).
+      const uint32_t *p = (const uint32_t *)(base + (size_t)(k0 >> 6) * 2 * BLK + (g ? BLK - 2 : 0));
+#pragma unroll
+      for (int i = 0; i < BRaw<WT>::D; i++) s.d[i] = ok ? p[i] : 0u;
+    } else {
+      constexpr int HW = BLK / 2;
+      const uint16_t *p = (const uint16_t *)(base + (size_t)blk * BLK);
+#pragma unroll
+      for (int j = 0; j < BRaw<WT>::D; j++) {
+        uint32_t lo = ok && 2 * j < HW ? p[2 * j] : 0u, hi = ok && 2 * j + 1 < HW ? p[2 * j + 1] : 0u;
+        s.d[j] = lo | (hi << 16);
+      }
+    }
+  }
+}
+
+// The lane's block as 4 MFMA fragments of 8 halves: f16(q·d) (Q8_0/Q4_0), f16(w) (F32), or as stored.
+template <int WT, bool ALIGNED>
+__device__ __forceinline__ void dequant_b(const BRaw<WT> &s, int g, half8 f[4]) {
+  if constexpr (WT == WH_F16) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint4 v = make_uint4(s.d[4 * q], s.d[4 * q + 1], s.d[4 * q + 2], s.d[4 * q + 3]);
+      f[q] = __builtin_bit_cast(half8, v);
+    }
+  } else if constexpr (WT == WH_F32) {
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) f[q][e] = (_Float16)__builtin_bit_cast(float, s.d[8 * q + e]);
+  } else {
+    // Scale in the low half of d[0] (data from byte 2), or for an aligned odd block in the high
+    // half (data dword-aligned from d[1]).
+    const bool odd = ALIGNED && g;
+    const float d = half_bits(odd ? (s.d[0] >> 16) : (s.d[0] & 0xffffu));
+    constexpr int NDW = WT == WH_Q8_0 ? 8 : 4;
+    uint32_t dw[NDW];
+#pragma unroll
+    for (int i = 0; i < NDW; i++) dw[i] = odd ? s.d[i + 1] : __builtin_amdgcn_alignbyte(s.d[i + 1], s.d[i], 2);
+    if constexpr (WT == WH_Q8_0) {
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) f[q][e] = (_Float16)((float)(int8_t)(dw[2 * q + e / 4] >> (8 * (e & 3))) * d);
+    } else {
+      // ggml block_q4_0: element i < 16 is the low nibble of byte i, 16 + i the high one.
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int i = 8 * q + e, byte = i & 15;
+          const uint32_t v = (dw[byte >> 2] >> (8 * (byte & 3))) & 0xffu;
+          f[q][e] = (_Float16)((float)((int)(i < 16 ? (v & 15u) : (v >> 4)) - 8) * d);
+        }
+    }
+  }
+}
+
+template <int WT, int BM, int BN, bool ALIGNED, bool A16, bool OUT16>
+__global__ __launch_bounds__(256) void gemm_reg_kernel(const void *__restrict__ a, const uint8_t *__restrict__ w,
+                                                   const float *__restrict__ bias, void *__restrict__ c,
+                                                   int m, int rows, int cols, int k, int dual, int ldc,
+                                                   int epi, float alpha, size_t row_bytes) {
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * LDS_ROW];
+  constexpr int TM = BM / 64, TN = BN / 64;  // 32×32 MFMA tiles per wave (2×2 waves)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+  const int lrow = lane & 31, g = lane >> 5;
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) acc[i][j] = floatx16{};
+
+  AStage<BM, A16> as;
+  BRaw<WT> bs[TN];
+  load_a<BM, A16>(as, a, m, k, m0, 0, tid);
+#pragma unroll
+  for (int j = 0; j < TN; j++) load_b<WT, ALIGNED>(bs[j], w, rows, k, row_bytes, n0 + wn + 32 * j + lrow, 0, g);
+  store_a<BM, A16>(as, As[0], tid);
+  __syncthreads();
+  int buf = 0;
+  for (int k0 = 0; k0 < k; k0 += BK) {
+    half8 bf[TN][4];
+#pragma unroll
+    for (int j = 0; j < TN; j++) dequant_b<WT, ALIGNED>(bs[j], g, bf[j]);
+    const bool more = k0 + BK < k;
+    if (more) {
+      load_a<BM, A16>(as, a, m, k, m0, k0 + BK, tid);
+#pragma unroll
+      for (int j = 0; j < TN; j++) load_b<WT, ALIGNED>(bs[j], w, rows, k, row_bytes, n0 + wn + 32 * j + lrow, k0 + BK, g);
+    }
+    const _Float16 *at = As[buf];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      half8 af[TM];
+#pragma unroll
+      for (int i = 0; i < TM; i++) af[i] = *(const half8 *)(at + (wm + 32 * i + lrow) * LDS_ROW + 32 * g + 8 * s);
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j][s], acc[i][j], 0, 0, 0);
+    }
+    if (more) store_a<BM, A16>(as, As[buf ^ 1], tid);
+    __syncthreads();
+    buf ^= 1;
+  }
+  // D[i][j] of a 32×32 tile sits in lane j (mod 32), register v: i = 8·(v/4) + 4·(lane/32) + v%4.
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      int col = n0 + wn + 32 * j + lrow;
+      if (col >= cols) continue;
+      float bv = bias[col];
+      float b2 = col < dual ? bias[cols + col] : 0.0f;
+#pragma unroll
+      for (int v = 0; v < 16; v++) {
+        int row = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (row >= m) continue;
+        const size_t at = (size_t)row * ldc + col;
+        float x = col < rows ? acc[i][j][v] : 0.0f;
+        if constexpr (OUT16) {
+          _Float16 *cp = (_Float16 *)c + at;
+          *cp = (_Float16)epilogue(epi, alpha, x + bv, nullptr);
+          if (col < dual) cp[cols] = (_Float16)(x + b2);
+        } else {
+          float *cp = (float *)c + at;
+          *cp = epilogue(epi, alpha, x + bv, cp);
+          if (col < dual) cp[cols] = x + b2;
+        }
+      }
+    }
+}
+
+
+// ------------------------------------------------------------------------------------ LDS-DMA path
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// LDS DMA (counted by vmcnt): each lane copies 16 (dma16) or 4 (dma4) bytes at `src` to LDS byte
+// lds + 16·lane (4·lane); `lds` is wave-uniform.
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+__device__ __forceinline__ void dma4(const void *src, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// The same from a wave-uniform base address (SGPRs) plus a per-lane 32-bit byte offset, so that a
+// loop moves the whole DMA by scalar adds.  `lds` must be wave-uniform (it goes to M0).
+__device__ __forceinline__ void dma16s(const void *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4s(const void *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+
+// Two f16 values 1024 + byte0, 1024 + byte1 of x (bytes 0-1, or 2-3 with HI).
+template <bool HI>
+__device__ __forceinline__ half2 magic_pair(uint32_t x) {
+  return __builtin_bit_cast(half2, __builtin_amdgcn_perm(0x64646464u, x, HI ? 0x04030402u : 0x04010400u));
+}
+
+// Two int8 of x (bytes 0-1, or 2-3 with HI) as two f16 (exact: |q| ≤ 128), by sub-dword operand
+// selection of the conversion itself (SDWA: sign-extended byte in, one half of the result out).
+template <bool HI>
+__device__ __forceinline__ half2 i8_pair(uint32_t x) {
+  uint32_t r;
+  if constexpr (HI)
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+        : "=&v"(r) : "v"(x));
+  else
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1"
+        : "=&v"(r) : "v"(x));
+  return __builtin_bit_cast(half2, r);
+}
+
+// Q8_0 MFMA fragment of substep S: elements 16·(S % 2) + 8g .. + 8 of block S / 2 of the lane's W
+// row pair, f16(q·d) — the exact conversion of q, then one packed f16 multiply by the block scale.
+// w = the lane's dwords (read_w): for block 0 (data from byte 2 of the pair) three dwords per
+// substep holding the elements from byte 2, for block 1 (data from byte 36) two aligned dwords.
+template <int S>
+__device__ __forceinline__ half8 dequant_q8(const uint32_t *w, half2 d2) {
+  half2 p[4];
+  if constexpr (S < 2) {
+    const uint32_t *x = w + 3 * S;
+    p[0] = i8_pair<true>(x[0]), p[1] = i8_pair<false>(x[1]), p[2] = i8_pair<true>(x[1]), p[3] = i8_pair<false>(x[2]);
+  } else {
+    const uint32_t *x = w + 6 + 2 * (S - 2);
+    p[0] = i8_pair<false>(x[0]), p[1] = i8_pair<true>(x[0]), p[2] = i8_pair<false>(x[1]), p[3] = i8_pair<true>(x[1]);
+  }
+  half8 f;
+#pragma unroll
+  for (int h = 0; h < 4; h++) {
+    const half2 v = p[h] * d2;
+    f[2 * h] = v[0], f[2 * h + 1] = v[1];
+  }
+  return f;
+}
+
+// The MFMA fragment of substep s (elements 8s .. 8s + 7) of one block.  dw = the block's data
+// dwords as read from LDS at the lane's offset, `sh` = bytes of that offset before the data (2 for
+// the even block of a pair: data from byte 2; 0 for the odd one: data dword-aligned), d2 = the
+// block's scale twice.
+template <int WT>
+__device__ __forceinline__ half8 dequant_frag(const uint32_t *dw, uint32_t sh, half2 d2, int s) {
+  half8 f;
+  if constexpr (WT == WH_Q8_0) {
+    const half2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};  // 1024 + 128
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const uint32_t x = __builtin_amdgcn_alignbyte(dw[2 * s + h + 1], dw[2 * s + h], sh) ^ 0x80808080u;
+      const half2 p0 = (magic_pair<false>(x) - bias) * d2, p1 = (magic_pair<true>(x) - bias) * d2;
+      f[4 * h] = p0[0], f[4 * h + 1] = p0[1], f[4 * h + 2] = p1[0], f[4 * h + 3] = p1[1];
+    }
+  } else {
+    // ggml block_q4_0: element i < 16 is the low nibble of byte i, 16 + i the high one; value
+    // (nibble − 8)·d.  Substeps 0-1 take low nibbles of bytes 0-15, substeps 2-3 high ones.
+    const half2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};  // 1024 + 8
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int q = 2 * (s & 1) + h;
+      const uint32_t x = __builtin_amdgcn_alignbyte(dw[q + 1], dw[q], sh);
+      const uint32_t nib = s < 2 ? x & 0x0f0f0f0fu : (x >> 4) & 0x0f0f0f0fu;
+      const half2 p0 = (magic_pair<false>(nib) - bias) * d2, p1 = (magic_pair<true>(nib) - bias) * d2;
+      f[4 * h] = p0[0], f[4 * h + 1] = p0[1], f[4 * h + 2] = p1[0], f[4 * h + 3] = p1[1];
+    }
+  }
+  return f;
+}
+
+// Work of one gemm_lds_kernel launch.
+struct LdsArgs {
+  const _Float16 *a;
+  const uint8_t *w;
+  const float *bias;
+  void *c;          // output, or f32 partial sums [split][m][cols] with SPLIT
+  int m, rows, cols, k, dual, ldc, epi;
+  float alpha;
+  size_t row_bytes;
+  HeadsOut ho[2];  // column ranges written in attention's packed layout instead of into c (f16 outputs)
+  int nho;
+};
+
+// s_waitcnt with vmcnt = N (0..63) and no wait on the other counters (gfx9 encoding: vmcnt bits
+// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// f(integral_constant<S>, kt0 + S) for S = I .. N − 1 while kt0 + S < nk: a loop body unrolled with
+// its step index known at compile time.
+template <int I, int N, class F>
+__device__ __forceinline__ void unrolled_steps(F &f, int kt0, int nk) {
+  if constexpr (I < N) {
+    if (kt0 + I < nk) {
+      f(std::integral_constant<int, I>{}, kt0 + I);
+      unrolled_steps<I + 1, N>(f, kt0, nk);
+    }
+  }
+}
+
+// The epilogue's store of a BM × BN tile whose f32 sums sit in LDS (cl, rows of `crow` floats): NT
+// threads take 8 consecutive columns each (16-byte loads of c for the residual modes, 16-byte stores),
+// applying the bias (bb, loaded by the caller for the thread's fixed column group), the epilogue, the
+// dual columns (bd) and the padding columns (epi(0 + bias), as the reference's zero rows give); a
+// split GEMM stores its plain partial sums into plane tz instead.
+template <int BM, int BN, int NT, bool SPLIT, bool OUT16>
+__device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, int crow, int tid, int m0, int n0,
+                                             int tz, const float (&bb)[8], const float (&bd)[8]) {
+  constexpr int G8 = BN / 8;
+  const int m = P.m, rows = P.rows;
+  static_assert((BM * G8) % NT == 0, "whole rounds of column groups");
+  if constexpr (OUT16 && !SPLIT) {
+    // A tile inside a packed range (the host keeps each range on whole tiles): f16 rows per head or,
+    // transposed, 8 rows of one column per store; the epilogue as below (no residual, no dual).
+    for (int o = 0; o < P.nho; o++) {
+      const HeadsOut &h = P.ho[o];
+      if (n0 < h.col0 || n0 >= h.col0 + h.cols) continue;
+      if (h.tr) {
+#pragma unroll
+        for (int it = 0; it < BM * G8 / NT; it++) {
+          const int e = tid + it * NT, c = e % BN, r0 = 8 * (e / BN), row0 = m0 + r0, col = n0 + c;
+          if (row0 >= h.rs || col >= P.cols) continue;
+          const float b = P.bias[col];
+          half8 y;
+#pragma unroll
+          for (int q = 0; q < 8; q++)
+            y[q] = (_Float16)(row0 + q < m ? epilogue(P.epi, 0.0f, cl[(r0 + q) * crow + c] + b, nullptr) : 0.0f);
+          *(half8 *)(h.dst + (size_t)(col - h.col0) * h.rs + row0) = y;  // head j, dim i: row j·hd + i
+        }
+      } else {
+#pragma unroll
+        for (int it = 0; it < BM * G8 / NT; it++) {
+          const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0 + r, col = n0 + c8;
+          if (row + h.r0 >= h.rs || col >= P.cols) continue;
+          half8 y;
+          if (row < m) {
+            const float4 x0 = *(const float4 *)(cl + r * crow + c8), x1 = *(const float4 *)(cl + r * crow + c8 + 4);
+            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int q = 0; q < 8; q++) y[q] = (_Float16)epilogue(P.epi, 0.0f, x[q] + bb[q], nullptr);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 8; q++) y[q] = (_Float16)0.0f;
+          }
+          const int v = col - h.col0;  // 8 columns of one head (hd % 8 == 0)
+          *(half8 *)(h.dst + ((size_t)(v / h.hd) * h.rs + h.r0 + row) * h.hd + v % h.hd) = y;
+        }
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < BM * G8 / NT; it++) {
+    const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0 + r, col = n0 + c8;
+    if (row >= m || col >= P.cols) continue;  // cols % 32 == 0: a group is inside or past
+    const float4 x0 = *(const float4 *)(cl + r * crow + c8), x1 = *(const float4 *)(cl + r * crow + c8 + 4);
+    float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+    if constexpr (SPLIT) {
+      float *cp = (float *)P.c + ((size_t)tz * m + row) * P.cols + col;
+      *(float4 *)cp = x0;
+      *(float4 *)(cp + 4) = x1;
+      continue;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; q++)
+      if (col + q >= rows) x[q] = 0.0f;
+    const size_t at = (size_t)row * P.ldc + col;
+    float y[8];
+    if (!OUT16 && (P.epi == WH_RESIDUAL || P.epi == WH_GELU_RESIDUAL)) {
+      const float4 c0 = *(const float4 *)((const float *)P.c + at), c1 = *(const float4 *)((const float *)P.c + at + 4);
+      const float cc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      if (P.epi == WH_RESIDUAL)
+#pragma unroll
+        for (int q = 0; q < 8; q++) y[q] = cc[q] + P.alpha * (x[q] + bb[q]);
+      else
+#pragma unroll
+        for (int q = 0; q < 8; q++) y[q] = cc[q] + gelu(x[q] + bb[q]);
+    } else {
+      switch (P.epi) {
+#define EPI_CASE(E)                                                               \
+  case E:                                                                         \
+    _Pragma("unroll") for (int q = 0; q < 8; q++) y[q] = epilogue(E, 0.0f, x[q] + bb[q], nullptr); \
+    break;
+        EPI_CASE(WH_SILU)
+        EPI_CASE(WH_RELU)
+        EPI_CASE(WH_GELU)
+        EPI_CASE(WH_TANH)
+#undef EPI_CASE
+        default:
+#pragma unroll
+          for (int q = 0; q < 8; q++) y[q] = x[q] + bb[q];
+      }
+    }
+    const bool dual = col < P.dual;  // dual % 8 == 0 is not required: per column below
+    if constexpr (OUT16) {
+      half8 h;
+#pragma unroll
+      for (int q = 0; q < 8; q++) h[q] = (_Float16)y[q];
+      *(half8 *)((_Float16 *)P.c + at) = h;
+    } else {
+      *(float4 *)((float *)P.c + at) = make_float4(y[0], y[1], y[2], y[3]);
+      *(float4 *)((float *)P.c + at + 4) = make_float4(y[4], y[5], y[6], y[7]);
+    }
+    if (dual) {
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        if (col + q >= P.dual) break;
+        const float d = x[q] + bd[q];
+        if constexpr (OUT16) ((_Float16 *)P.c)[at + P.cols + q] = (_Float16)d;
+        else ((float *)P.c)[at + P.cols + q] = d;
+      }
+    }
+  }
+}
+
+// c tile BM × BN per workgroup of WM × WN wavefronts, each a (BM/WM) × (BN/WN) block of 32×32 MFMA
+// tiles, over the k range of its split (the 64-wide k steps divided evenly over gridDim.z).
+//
+// Pipeline.  The k loop moves in 64-wide steps through a ring of NS LDS stages that the LDS DMA
+// fills NS − 1 steps ahead, from scalar base addresses (a step costs the vector units nothing but
+// the dequantization).  A step is 4 substeps of 16 k; each wave reads the a fragments of substep
+// s + 1 while the MFMAs of substep s run, and the W data of the next step after the one barrier of
+// the step, which sits after substep 2: there every wave has waited for the next stage's DMA and has
+// finished reading the stage of the previous step, so the DMA of step kt + NS − 1 goes into that
+// stage.  The loop is unrolled by the ring length so that every LDS offset is an immediate.  Each
+// wave issues the same number of DMA instructions per step (a wave without an instruction of its
+// own repeats another wave's: identical bytes to the same place), so a vmcnt immediate waits for
+// exactly one step.
+//
+// LDS layout: the a stages (rows of 8 16-byte chunks, chunk c of row r at (c + r/2) % 8 — the 16
+// lanes that LDS serves together read 16 rows and hit all 64 banks once), then the W stages: F16
+// rows like a, or quantized rows of one block pair (68 or 36 bytes, as stored).  At substep s, the
+// lane of MFMA column n and k half g takes k slots 32g + 8s .. + 8 — block g of its W row's pair —
+// and the a fragments the same slots.
+//
+// Epilogue.  The accumulators go through LDS (f32, rows padded so the two lane halves of a tile hit
+// distinct banks) and leave as 8 consecutive columns per lane: 16-byte loads of c for the residual
+// modes and 16-byte stores, with the bias, the epilogue, the dual columns and the padding columns
+// (epi(0 + bias), as the reference's zero rows give) applied on the way.
+template <int WT, int BM, int BN, int WM, int WN, int NSQ, bool SPLIT, bool OUT16, int VAR>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+  static_assert(TM >= 1 && TN >= 1, "32×32 MFMA tiles per wave");
+  constexpr int PAIR1 = WT == WH_Q8_0 ? 68 : WT == WH_Q4_0 ? 36 : 128;  // W bytes of 64 weights
+  constexpr bool WCH = WT == WH_F16;                                     // W moves in 16-byte chunks
+  // VAR bit 0: the DMA of a step spread over the substeps; bit 1: quantized rows moved by 16-byte
+  // DMA into LDS rows padded to 16 bytes (WROW), the last chunk of a row read from 16 bytes before
+  // the row's end (its bytes past WROW − 16 land 12 bytes further on).
+  constexpr bool SPREAD = VAR & 1, W16 = (VAR & 2) && !WCH;
+  constexpr int WROW = W16 ? (PAIR1 + 15) / 16 * 16 : PAIR1, WSH = WROW - PAIR1;
+  constexpr int A_ST = BM * 128, W_ST = BN * WROW, ST = A_ST + W_ST;
+  constexpr int CROW = BN + 8;                                           // f32 per epilogue LDS row
+  constexpr int C_BYTES = BM * CROW * 4;
+  // NSQ stages asked for, as many as fit in the 160 KiB of LDS.
+  constexpr int NS = NSQ * ST + 16 <= 160 * 1024 ? NSQ : (160 * 1024 - 16) / ST;
+  static_assert(NS >= 3, "at least three stages");
+  static_assert((WCH || W16) ? W_ST % 1024 == 0 : W_ST % 256 == 0, "whole DMA instructions");
+  constexpr int W_RG = NS * A_ST;                               // the W stages follow the a stages
+  constexpr int NIA = A_ST / 1024;                              // a: 16-byte DMA instructions per stage
+  constexpr int NIW = (WCH || W16) ? W_ST / 1024 : W_ST / 256;  // W: 16-byte or 4-byte ones
+  constexpr int PA = (NIA + NW - 1) / NW, PW = (NIW + NW - 1) / NW, PI = PA + PW;
+  static_assert((NS - 2) * PI < 64, "vmcnt holds the DMA of NS - 2 steps");
+  // (+16: the odd block of the last W row reads one dword past its row, unused)
+  constexpr int LDS_BYTES = NS * ST + 16 > C_BYTES ? NS * ST + 16 : C_BYTES;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Tile order.  Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2.
+  // The grid is renumbered so that an XCD takes a contiguous run of (split, row tile, column tile):
+  // one k split and a band of row tiles over all column tiles, in order, so that the workgroups
+  // running at once on an XCD share their rows of a and the XCDs do not all fetch the same a
+  // (measured against the dispatch order and against bands of column tiles: Parakeet 60 s
+  // 5.02 against 5.18 and 5.12 ms per call, 16 windows 30.9 against 31.9 ms).
+  int tx = blockIdx.x, ty = blockIdx.y, tz = blockIdx.z;
+  {
+    const int nx = gridDim.x, ny = gridDim.y, total = nx * ny * gridDim.z;
+    if (total % 8 == 0) {
+      const int lin = tx + nx * (ty + ny * tz), l = (lin % 8) * (total / 8) + lin / 8;
+      tz = l / (nx * ny);
+      ty = (l % (nx * ny)) / nx;
+      tx = l % nx;
+    }
+  }
+  const int n0 = tx * BN, m0 = ty * BM;
+  const int wm = (wave / WN) * (BM / WM), wn = (wave % WN) * (BN / WN);
+  const int lrow = lane & 31, g = lane >> 5;
+  const int m = P.m, k = P.k, rows = P.rows;
+  const int nkt = k / 64, kb = nkt * tz / (int)gridDim.z, nk = nkt * (tz + 1) / (int)gridDim.z - kb;
+
+  // Per-lane byte offsets of this wave's DMA instructions from the step's base addresses (rows past
+  // m or rows are clamped: their products land in outputs that are discarded or zeroed), and the
+  // instructions' LDS offsets in a stage.
+  uint32_t aoff[PA], alds[PA];
+#pragma unroll
+  for (int i = 0; i < PA; i++) {
+    const int n = (wave + NW * i) % NIA, r = 8 * n + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
+    aoff[i] = (uint32_t)(((size_t)min(m0 + r, m - 1) * k + 8 * lc) * 2);
+    alds[i] = 1024 * n;
+  }
+  uint32_t woff[PW], wlds[PW];
+#pragma unroll
+  for (int i = 0; i < PW; i++) {
+    const int n = (wave + NW * i) % NIW;
+    if constexpr (WCH) {
+      const int r = 8 * n + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
+      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * lc);
+      wlds[i] = 1024 * n;
+    } else if constexpr (W16) {
+      constexpr int CH = WROW / 16;  // chunks per row
+      const int ci = 64 * n + lane, r = ci / CH, c = ci % CH;
+      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + (c < CH - 1 ? 16 * c : PAIR1 - 16));
+      wlds[i] = 1024 * n;
+    } else {
+      const int sidx = 64 * n + lane, r = sidx / (PAIR1 / 4), dwi = sidx % (PAIR1 / 4);
+      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 4 * dwi);
+      wlds[i] = 256 * n;
+    }
+  }
+  const uint8_t *abase = (const uint8_t *)P.a + (size_t)kb * 128;
+  const uint8_t *wbase = P.w + (size_t)kb * PAIR1;
+  const uint32_t lds0 = lds_addr(lds);
+  // The wave's DMA instructions of step kt into ring slot `slot`: all of them (part < 0), or those
+  // whose index (a instructions first) is `part` modulo 4.
+  auto issue = [&](int kt, int slot, int part = -1) {
+    const uint8_t *ab = abase + (size_t)kt * 128, *wb = wbase + (size_t)kt * PAIR1;
+#pragma unroll
+    for (int i = 0; i < PA; i++)
+      if (part < 0 || i % 4 == part) dma16s(ab, aoff[i], lds0 + slot * A_ST + alds[i]);
+#pragma unroll
+    for (int i = 0; i < PW; i++) {
+      if (part >= 0 && (PA + i) % 4 != part) continue;
+      if constexpr (WCH || W16) dma16s(wb, woff[i], lds0 + W_RG + slot * W_ST + wlds[i]);
+      else dma4s(wb, woff[i], lds0 + W_RG + slot * W_ST + wlds[i]);
+    }
+  };
+
+  // The lane's k chunk (of 8 in a step) at substep s.  Q8_0: 2s + g — block s/2 of the pair at
+  // every lane of a substep, so the bytes of a substep sit at the same place in every lane's dwords;
+  // Q4_0 and F16: 4g + s — block g.  a and W fragments take the same chunk.
+  constexpr bool Q8 = WT == WH_Q8_0;
+  auto chunk = [&](int s) { return Q8 ? 2 * s + g : 4 * g + s; };
+  // LDS read offsets of the lane: a chunk of row wm + lrow (+32i), rotated by row/2; the lane's W
+  // dwords (Q8_0: from byte 8g of its row pair, the scales in dwords 0 and 8 of the row; Q4_0:
+  // g = 0 reads dwords 0.. with the data from byte 2, g = 1 the dwords from byte BLK + 2 with the
+  // scale in the high half of the dword before); F16 chunks like a.
+  uint32_t a_off[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) a_off[s] = (wm + lrow) * 128 + 16 * ((chunk(s) + (lrow >> 1)) & 7);
+  constexpr int ND = Q8 ? 10 : WT == WH_Q4_0 ? 5 : 16;  // dwords per lane per W row and step
+  constexpr int NSC = Q8 ? 2 : 1;                       // scale dwords per lane per W row and step
+  constexpr int BLK = PAIR1 / 2;
+  const uint32_t w_row = W_RG + (wn + lrow) * WROW;
+  const uint32_t w_dat = Q8 ? w_row + 8 * g : w_row + (g ? BLK + 2 : 0), w_sc = w_row + (g ? BLK - 2 : 0);
+  uint32_t wf_off[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) wf_off[s] = w_row + 16 * ((chunk(s) + (lrow >> 1)) & 7);
+
+  auto read_a = [&](half8 (&f)[TM], int slot, int s) {
+#pragma unroll
+    for (int i = 0; i < TM; i++) f[i] = *(const half8 *)(lds + a_off[s] + slot * A_ST + i * 4096);
+  };
+  auto read_w = [&](uint32_t (&w)[TN][ND], uint32_t (&sc)[TN][NSC], int slot) {
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      if constexpr (WCH) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+          const uint4 x = *(const uint4 *)(lds + wf_off[s] + slot * W_ST + j * 32 * WROW);
+          w[j][4 * s] = x.x, w[j][4 * s + 1] = x.y, w[j][4 * s + 2] = x.z, w[j][4 * s + 3] = x.w;
+        }
+        sc[j][0] = 0;
+      } else if constexpr (Q8) {
+        // Pair bytes 2 + 8g .. (block 0, substeps 0-1: dwords 0-2 and 4-6 from byte 8g) and
+        // 36 + 8g .. (block 1, substeps 2-3: dwords 9-10 and 13-14); the scales at bytes 0 and 34.
+        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * WROW);
+        constexpr int at[10] = {0, 1, 2, 4, 5, 6, 9, 10, 13, 14};
+#pragma unroll
+        for (int i = 0; i < 9; i++) w[j][i] = q[at[i]];
+        // Byte 56 + 8g: for g = 1 past byte 64 (W16: moved by WSH).
+        w[j][9] = *(const uint32_t *)(lds + w_dat + (W16 && g ? WSH : 0) + 56 + slot * W_ST + j * 32 * WROW);
+        const uint32_t *r = (const uint32_t *)(lds + w_row + slot * W_ST + j * 32 * WROW);
+        sc[j][0] = r[0], sc[j][1] = r[8];
+      } else {
+        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * WROW);
+#pragma unroll
+        for (int i = 0; i < ND; i++) w[j][i] = q[i];
+        if constexpr (W16)  // g = 1: dwords 3-4 start at byte 32 (moved by WSH)
+          w[j][3] = *(const uint32_t *)(lds + w_dat + (g ? WSH : 0) + 12 + slot * W_ST + j * 32 * WROW),
+          w[j][4] = *(const uint32_t *)(lds + w_dat + (g ? WSH : 0) + 16 + slot * W_ST + j * 32 * WROW);
+        sc[j][0] = *(const uint32_t *)(lds + w_sc + slot * W_ST + j * 32 * WROW);
+      }
+    }
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) acc[i][j] = floatx16{};
+  const uint32_t sh = g ? 0u : 2u;
+  // The MFMA operand of W column block j at substep s: f16 chunks as read (F16), or the lane's
+  // quantized dwords dequantized (f16(q·d)).
+  auto wfrag = [&](const uint32_t (&w)[TN][ND], const uint32_t (&scl)[TN][NSC], int j, auto s_c) -> half8 {
+    constexpr int s = decltype(s_c)::value;
+    if constexpr (WCH) return __builtin_bit_cast(half8, make_uint4(w[j][4 * s], w[j][4 * s + 1], w[j][4 * s + 2], w[j][4 * s + 3]));
+    else if constexpr (Q8) {
+      const half2 sv = __builtin_bit_cast(half2, scl[j][s >> 1]);  // block 0: low half; block 1: high
+      const _Float16 d = s < 2 ? sv[0] : sv[1];
+      return dequant_q8<s>(w[j], half2{d, d});
+    } else {
+      const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(g ? scl[j][0] >> 16 : scl[j][0] & 0xffffu));
+      return dequant_frag<WT>(w[j], sh, half2{d, d}, s);
+    }
+  };
+#pragma unroll
+  for (int s = 0; s < NS - 1; s++)
+    if (s < nk) issue(s, s);
+  {
+    uint32_t wq[2][TN][ND], sc[2][TN][NSC];
+    half8 af[2][TM];
+    // Substep s of a step: dequantize the lane's W fragment (quantized) and run the TM × TN MFMAs.
+    auto mma = [&](const half8 (&f)[TM], const uint32_t (&w)[TN][ND], const uint32_t (&scl)[TN][NSC], auto s_c) {
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const half8 b = wfrag(w, scl, j, s_c);
+#pragma unroll
+        for (int i = 0; i < TM; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], b, acc[i][j], 0, 0, 0);
+      }
+    };
+    if (nk > 0) {
+      if (nk - 1 >= NS - 2) wait_vm<(NS - 2) * PI>();  // stages 1 .. NS - 2 may be in flight
+      else dma_wait();
+      __syncthreads();
+      read_w(wq[0], sc[0], 0);
+      read_a(af[0], 0, 0);
+    }
+    // Step kt (S = kt modulo the unroll: ring slot S % NS, register set S % 2).
+    auto step = [&](auto S_c, int kt) {
+      constexpr int S = decltype(S_c)::value, slot = S % NS, cur = S & 1;
+      // SPREAD: the DMA of step kt + NS − 2 (begun after the previous step's barrier) continues
+      // between the substeps, so that the 8 waves do not queue all their DMA at once.
+      const bool pend = SPREAD && kt >= 1 && kt + NS - 2 < nk;
+      constexpr int pslot = (S + NS - 2) % NS;
+      if (pend) issue(kt + NS - 2, pslot, 1);
+      read_a(af[1], slot, 1);
+      mma(af[0], wq[cur], sc[cur], std::integral_constant<int, 0>{});
+      if (pend) issue(kt + NS - 2, pslot, 2);
+      read_a(af[0], slot, 2);
+      mma(af[1], wq[cur], sc[cur], std::integral_constant<int, 1>{});
+      if (pend) issue(kt + NS - 2, pslot, 3);
+      read_a(af[1], slot, 3);
+      mma(af[0], wq[cur], sc[cur], std::integral_constant<int, 2>{});
+      if (kt + 1 < nk) {
+        // Stage kt + 1 has landed for every wave, and every wave is done with stage kt − 1.
+        if (kt + NS - 2 < nk) wait_vm<(NS - 3) * PI>();
+        else dma_wait();
+        __syncthreads();
+        if (kt + NS - 1 < nk) issue(kt + NS - 1, (slot + NS - 1) % NS, SPREAD ? 0 : -1);
+        read_w(wq[cur ^ 1], sc[cur ^ 1], (slot + 1) % NS);
+        read_a(af[0], (slot + 1) % NS, 0);
+      }
+      mma(af[1], wq[cur], sc[cur], std::integral_constant<int, 3>{});
+    };
+    constexpr int UNR = NS % 2 ? 2 * NS : NS;
+    for (int kt0 = 0; kt0 < nk; kt0 += UNR) unrolled_steps<0, UNR>(step, kt0, nk);
+  }
+
+  // Epilogue through LDS: every DMA has landed (the last step waited for it) and the barrier below
+  // ends every wavefront's reads of the stages.  A thread's 8-column group is the same on every row
+  // it stores (64·NW is a multiple of BN / 8), so its bias values are loaded once, before the barrier.
+  constexpr int G8 = BN / 8;  // 8-column groups per row
+  static_assert((64 * NW) % G8 == 0, "fixed column group per thread");
+  const int ecol = n0 + 8 * (tid % G8);
+  float bb[8] = {}, bd[8] = {};
+  if (!SPLIT && ecol < P.cols) {
+    const float4 b0 = *(const float4 *)(P.bias + ecol), b1 = *(const float4 *)(P.bias + ecol + 4);
+    bb[0] = b0.x, bb[1] = b0.y, bb[2] = b0.z, bb[3] = b0.w, bb[4] = b1.x, bb[5] = b1.y, bb[6] = b1.z, bb[7] = b1.w;
+#pragma unroll
+    for (int q = 0; q < 8; q++)
+      if (ecol + q < P.dual) bd[q] = P.bias[P.cols + ecol + q];
+  }
+  __syncthreads();
+  float *cl = (float *)lds;
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int v = 0; v < 16; v++)
+        cl[(wm + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow] = acc[i][j][v];
+  __syncthreads();
+  store_c_tile<BM, BN, 64 * NW, SPLIT, OUT16>(P, cl, CROW, tid, m0, n0, tz, bb, bd);
+}
+
+// Split-k finish: c = epi(Σ_z part[z] + bias) with the partial sums added in split order (the same
+// result on every run), dual outputs and padding columns as in the kernel above.
+template <bool OUT16>
+__global__ __launch_bounds__(256) void split_finish_kernel(const float *__restrict__ part, int splits, const float *__restrict__ bias,
+                                                           void *__restrict__ c, int m, int rows, int cols, int dual,
+                                                           int ldc, int epi, float alpha) {
+  const size_t n = (size_t)m * cols, plane = n;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const int row = (int)(i / cols), col = (int)(i % cols);
+    float x = 0.0f;
+    for (int z = 0; z < splits; z++) x += part[z * plane + i];
+    if (col >= rows) x = 0.0f;
+    const size_t at = (size_t)row * ldc + col;
+    if constexpr (OUT16) {
+      _Float16 *cp = (_Float16 *)c + at;
+      *cp = (_Float16)epilogue(epi, alpha, x + bias[col], nullptr);
+      if (col < dual) cp[cols] = (_Float16)(x + bias[cols + col]);
+    } else {
+      float *cp = (float *)c + at;
+      *cp = epilogue(epi, alpha, x + bias[col], cp);
+      if (col < dual) cp[cols] = x + bias[cols + col];
+    }
+  }
+}
+
+template <int WT, int BM, int BN, int WM, int WN, int NS, int VAR>
+void lds_launch(wh_ctx *ctx, dim3 grid, const LdsArgs &a, bool split, bool out16) {
+  if (split) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, true, false, VAR>, grid, 64 * WM * WN, 0, a);
+  else if (out16) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, true, VAR>, grid, 64 * WM * WN, 0, a);
+  else wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, false, VAR>, grid, 64 * WM * WN, 0, a);
+}
+
+template <int WT>
+int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
+                 bool out16, float *part, int *splits, const HeadsOut *ho, int nho) {
+  GemmPlan p = gemm_plan_for(ctx, m, l->cols, l->k);
+  if ((p.split > 1 && !part) || nho) p.split = 1;  // packed ranges are written by the tiles' own epilogue
+  if (splits) *splits = p.split;
+  LdsArgs args{a, l->w, l->bias, p.split > 1 ? (void *)part : c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha,
+               l->row_bytes, {}, nho};
+  if (nho < 0 || nho > 2) return wh_fail(ctx, WH_EARG, "gemm: %d packed ranges", nho);
+  for (int i = 0; i < nho; i++) {
+    const HeadsOut &h = ho[i];
+    // Whole tiles, inside the real columns, no dual columns; 16-byte stores.
+    if (!out16 || h.col0 % p.bn || h.cols % p.bn || h.col0 + h.cols > l->rows || h.col0 < l->dual || h.hd % 8 ||
+        h.cols % h.hd || (uintptr_t)h.dst % 16 || h.r0 < 0 || (h.tr ? h.r0 || h.rs % 8 || h.rs < m : h.rs < h.r0 + m))
+      return wh_fail(ctx, WH_EARG, "gemm: packed output %d off the %d-column tiles or its layout", i, p.bn);
+    args.ho[i] = h;
+  }
+  dim3 grid((l->cols + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.split);
+  static const char *tn = WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
+  // Named by kernel variant and call shape: m x rows x k, epilogue, output type, row width.
+  char name[128];
+  snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s%s %dx%dx%d e%d %s w%d", tn, p.bm, p.bn, p.wm, p.wn, p.ns,
+           p.split > 1 ? (p.split == 2 ? "_s2" : "_s4") : "", p.var ? (p.var == 1 ? "_v1" : p.var == 2 ? "_v2" : "_v3") : "", m, l->rows, l->k, epi,
+           out16 ? "f16" : "f32", l->cols + l->dual);
+  const double width = l->cols + l->dual;
+  const double bytes = (double)l->rows * l->row_bytes + 2.0 * m * l->k +
+                       (out16 ? 2.0 : 4.0) * m * width * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
+  {
+    ProfScope prof(ctx, name, 2.0 * m * l->rows * l->k, bytes);
+    const bool sp = p.split > 1;
+    bool ok = false;
+#define PLAN(BM, BN, WM, WN, NS)                                                           \
+  if (!ok && p.bm == BM && p.bn == BN && p.wm == WM && p.wn == WN && p.ns == NS) {          \
+    if constexpr (WT == WH_Q8_0) {                                                          \
+      if (p.var == 1) lds_launch<WT, BM, BN, WM, WN, NS, 1>(ctx, grid, args, sp, out16);    \
+      else if (p.var == 2) lds_launch<WT, BM, BN, WM, WN, NS, 2>(ctx, grid, args, sp, out16); \
+      else if (p.var == 3) lds_launch<WT, BM, BN, WM, WN, NS, 3>(ctx, grid, args, sp, out16); \
+      else lds_launch<WT, BM, BN, WM, WN, NS, 0>(ctx, grid, args, sp, out16);               \
+    } else lds_launch<WT, BM, BN, WM, WN, NS, 0>(ctx, grid, args, sp, out16);               \
+    ok = true;                                                                               \
+  }
+    PLAN(128, 128, 2, 4, 4)
+    PLAN(128, 128, 1, 4, 4)
+    PLAN(128, 128, 1, 4, 6)
+    PLAN(128, 256, 1, 4, 4)
+    PLAN(128, 256, 1, 8, 4)
+    PLAN(64, 64, 2, 2, 4)
+    PLAN(64, 64, 2, 2, 8)
+    PLAN(64, 128, 1, 4, 6)
+    PLAN(128, 64, 1, 2, 4)
+    PLAN(64, 64, 1, 2, 6)
+    PLAN(128, 128, 2, 4, 3)
+    PLAN(64, 64, 2, 2, 3)
+    PLAN(128, 128, 2, 2, 3)
+    PLAN(256, 128, 4, 2, 3)
+#undef PLAN
+    if (!ok) return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages", p.bm, p.bn, p.wm, p.wn, p.ns);
+    if (int rc = wh_launched(ctx, "gemm")) return rc;
+  }
+  if (p.split > 1 && !splits && !ctx->gemm_kernel_only) {
+    ProfScope prof(ctx, "gemm_split_finish", 0.0, 4.0 * p.split * m * l->cols + 4.0 * m * width);
+    const size_t n = (size_t)m * l->cols;
+    const int blocks = (int)std::min<size_t>((n + 255) / 256, 8192);
+    if (out16)
+      wh_launch(ctx, split_finish_kernel<true>, blocks, 256, 0, part, p.split, l->bias, c, m, l->rows, l->cols, l->dual, ldc, epi, alpha);
+    else
+      wh_launch(ctx, split_finish_kernel<false>, blocks, 256, 0, part, p.split, l->bias, c, m, l->rows, l->cols, l->dual, ldc, epi, alpha);
+    return wh_launched(ctx, "gemm split finish");
+  }
+  return WH_OK;
+}
+
+}  // namespace
+
+// The LDS-DMA GEMM for one weight type (gemm_lds_<type>.hip); arguments as launch_lds in gemm.hip.
+int gemm_lds_q8_0(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
+                bool out16, float *part, int *splits, const HeadsOut *ho, int nho);
+int gemm_lds_q4_0(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
+                bool out16, float *part, int *splits, const HeadsOut *ho, int nho);
+int gemm_lds_f16(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
+                bool out16, float *part, int *splits, const HeadsOut *ho, int nho);

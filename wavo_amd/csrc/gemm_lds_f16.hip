@@ -1,0 +1,7 @@
+// The LDS-DMA GEMM kernels instantiated for f16 weights (kernels and plans: gemm.hip, gemm_impl.h).
+#include "gemm_impl.h"
+
+int gemm_lds_f16(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
+                bool out16, float *part, int *splits, const HeadsOut *ho, int nho) {
+  return launch_lds_t<WH_F16>(ctx, a, l, c, m, ldc, epi, alpha, out16, part, splits, ho, nho);
+}

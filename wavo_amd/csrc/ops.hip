@@ -32,13 +32,17 @@ __device__ __forceinline__ void store4(_Float16 *p, float4 v) {
 
 // LayerNorm (eps 1e-5) of row `row`, one wavefront per row; with a table, the NEOX split-half RoPE
 // of each head into yr (ops.wgsl:44-95; src/cpu/ops.rs:68-110).  OT = float, or _Float16 when every
-// consumer of y (and yr) is a GEMM, which rounds its input to f16 anyway.
-template <typename OT>
+// consumer of y (and yr) is a GEMM, which rounds its input to f16 anyway.  NJ: float4 groups per lane
+// when cols == 256·NJ (the models' widths), else 0 (any cols ≤ ROW_REGS·64).  Every load of the row
+// and of the norm's weights is issued before the first use, so the wave waits for one memory round
+// trip (a loop that loads and then stores waits once per iteration).
+template <typename OT, int NJ>
 __global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict__ x, const float *__restrict__ g,
                                                          const float *__restrict__ b, OT *__restrict__ y,
                                                          int rows, int cols, const float *__restrict__ table,
                                                          OT *__restrict__ yr, int hd) {
   extern __shared__ float srow[];  // 4 rows of cols (RoPE only)
+  constexpr int J = NJ ? NJ : ROW_REGS / 4;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + w;
   const bool active = row < rows;
@@ -46,35 +50,39 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *__restrict
   const int q4 = cols / 4;  // float4 per row (cols % 4 == 0)
   if (active) {
     const float4 *xr = (const float4 *)(x + (size_t)row * cols);
-    float4 v[ROW_REGS / 4];
+    const float4 *g4 = (const float4 *)g, *b4 = (const float4 *)b;
+    float4 v[J], gg[J], bb[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int i = lane + 64 * j;
+      const bool in = NJ || i < q4;
+      v[j] = in ? xr[i] : make_float4(0, 0, 0, 0);
+      gg[j] = in ? g4[i] : make_float4(0, 0, 0, 0);
+      bb[j] = in ? b4[i] : make_float4(0, 0, 0, 0);
+    }
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < ROW_REGS / 4; j++) {
-      int i = lane + 64 * j;
-      v[j] = i < q4 ? xr[i] : make_float4(0, 0, 0, 0);
-      s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-    }
+    for (int j = 0; j < J; j++) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
     const float mean = wave_sum(s) / (float)cols;
     float q = 0.0f;
 #pragma unroll
-    for (int j = 0; j < ROW_REGS / 4; j++) {
-      if (lane + 64 * j < q4) {
+    for (int j = 0; j < J; j++) {
+      if (NJ || lane + 64 * j < q4) {
         float dx = v[j].x - mean, dy = v[j].y - mean, dz = v[j].z - mean, dw = v[j].w - mean;
         q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
       }
     }
     const float rstd = rsqrtf(wave_sum(q) / (float)cols + 1e-5f);
     OT *yy = y + (size_t)row * cols;
-    const float4 *g4 = (const float4 *)g, *b4 = (const float4 *)b;
 #pragma unroll
-    for (int j = 0; j < ROW_REGS / 4; j++) {
-      int i = lane + 64 * j;
-      if (i < q4) {
-        float4 gg = g4[i], bb = b4[i], o;
-        o.x = (v[j].x - mean) * rstd * gg.x + bb.x;
-        o.y = (v[j].y - mean) * rstd * gg.y + bb.y;
-        o.z = (v[j].z - mean) * rstd * gg.z + bb.z;
-        o.w = (v[j].w - mean) * rstd * gg.w + bb.w;
+    for (int j = 0; j < J; j++) {
+      const int i = lane + 64 * j;
+      if (NJ || i < q4) {
+        float4 o;
+        o.x = (v[j].x - mean) * rstd * gg[j].x + bb[j].x;
+        o.y = (v[j].y - mean) * rstd * gg[j].y + bb[j].y;
+        o.z = (v[j].z - mean) * rstd * gg[j].z + bb[j].z;
+        o.w = (v[j].w - mean) * rstd * gg[j].w + bb[j].w;
         store4(yy + 4 * i, o);
         if (table) *(float4 *)(sr + 4 * i) = o;
       }
@@ -378,8 +386,9 @@ __global__ __launch_bounds__(256) void copy16_kernel(u32x4 *__restrict__ y, cons
 // The finish of a k-split GEMM with the residual epilogue, fused with the LayerNorm of its result:
 // x[row] += alpha·(Σ_z part[z][row] + bias) (the partial sums added in split order from 0, the W
 // padding columns ≥ wrows contributing epi(0 + bias) as the GEMM gives them), then y = LN(x[row])
-// with the arithmetic of layer_norm_kernel.  One wavefront per row.
-template <typename OT, int NSPLIT>
+// with the arithmetic of layer_norm_kernel.  One wavefront per row; NJ as in layer_norm_kernel, and
+// every load (partial sums, bias, x, the norms' weights) issued before the first use.
+template <typename OT, int NSPLIT, int NJ>
 __global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__restrict__ part, int splits,
                                                                 const float *__restrict__ bias, int wrows, float alpha,
                                                                 float *__restrict__ x, const float *__restrict__ g,
@@ -388,6 +397,7 @@ __global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__r
                                                                 const float *__restrict__ g2,
                                                                 const float *__restrict__ b2,
                                                                 _Float16 *__restrict__ y2) {
+  constexpr int J = NJ ? NJ : ROW_REGS / 4;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + w;
   if (row >= rows) return;
@@ -395,60 +405,93 @@ __global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__r
   const size_t plane = (size_t)rows * cols;
   float4 *xr = (float4 *)(x + (size_t)row * cols);
   const float4 *pr = (const float4 *)(part + (size_t)row * cols), *b4 = (const float4 *)bias;
-  float4 v[ROW_REGS / 4];
-  float s = 0.0f;
+  const float4 *g4 = (const float4 *)g, *lb4 = (const float4 *)b;
+  const float4 *g24 = (const float4 *)g2, *b24 = (const float4 *)b2;
+  const float4 z4 = make_float4(0, 0, 0, 0);
+  auto in = [&](int j) { return NJ || lane + 64 * j < q4; };
+  float4 v[J], gg[J], bb[J], gg2[J], bb2[J];
+  if constexpr (NSPLIT > 0) {
+    float4 p[NSPLIT][J], bi[J], c[J];
 #pragma unroll
-  for (int j = 0; j < ROW_REGS / 4; j++) {
-    const int i = lane + 64 * j;
-    v[j] = make_float4(0, 0, 0, 0);
-    if (i < q4) {
-      float4 acc = make_float4(0, 0, 0, 0);
-      if constexpr (NSPLIT > 0) {  // every partial load in flight at once
-        float4 p[NSPLIT];
+    for (int j = 0; j < J; j++) {
+      const int i = lane + 64 * j;
 #pragma unroll
-        for (int z = 0; z < NSPLIT; z++) p[z] = pr[z * (plane / 4) + i];
+      for (int z = 0; z < NSPLIT; z++) p[z][j] = in(j) ? pr[z * (plane / 4) + i] : z4;
+      bi[j] = in(j) ? b4[i] : z4;
+      c[j] = in(j) ? xr[i] : z4;
+    }
 #pragma unroll
-        for (int z = 0; z < NSPLIT; z++) acc.x += p[z].x, acc.y += p[z].y, acc.z += p[z].z, acc.w += p[z].w;
-      } else {
-        for (int z = 0; z < splits; z++) {
-          const float4 p = pr[z * (plane / 4) + i];
-          acc.x += p.x, acc.y += p.y, acc.z += p.z, acc.w += p.w;
-        }
-      }
+    for (int j = 0; j < J; j++) {
+      gg[j] = in(j) ? g4[lane + 64 * j] : z4;
+      bb[j] = in(j) ? lb4[lane + 64 * j] : z4;
+      if (g2) gg2[j] = in(j) ? g24[lane + 64 * j] : z4, bb2[j] = in(j) ? b24[lane + 64 * j] : z4;
+    }
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      float4 acc = z4;
+#pragma unroll
+      for (int z = 0; z < NSPLIT; z++) acc.x += p[z][j].x, acc.y += p[z][j].y, acc.z += p[z][j].z, acc.w += p[z][j].w;
+      const int i = lane + 64 * j;
       if (4 * i + 0 >= wrows) acc.x = 0.0f;
       if (4 * i + 1 >= wrows) acc.y = 0.0f;
       if (4 * i + 2 >= wrows) acc.z = 0.0f;
       if (4 * i + 3 >= wrows) acc.w = 0.0f;
-      const float4 bb = b4[i], c = xr[i];
-      v[j] = make_float4(c.x + alpha * (acc.x + bb.x), c.y + alpha * (acc.y + bb.y), c.z + alpha * (acc.z + bb.z),
-                         c.w + alpha * (acc.w + bb.w));
-      if (keep_x) xr[i] = v[j];
-      s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+      v[j] = make_float4(c[j].x + alpha * (acc.x + bi[j].x), c[j].y + alpha * (acc.y + bi[j].y),
+                         c[j].z + alpha * (acc.z + bi[j].z), c[j].w + alpha * (acc.w + bi[j].w));
     }
+  } else {
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int i = lane + 64 * j;
+      v[j] = z4;
+      if (in(j)) {
+        float4 acc = z4;
+        for (int z = 0; z < splits; z++) {
+          const float4 p = pr[z * (plane / 4) + i];
+          acc.x += p.x, acc.y += p.y, acc.z += p.z, acc.w += p.w;
+        }
+        if (4 * i + 0 >= wrows) acc.x = 0.0f;
+        if (4 * i + 1 >= wrows) acc.y = 0.0f;
+        if (4 * i + 2 >= wrows) acc.z = 0.0f;
+        if (4 * i + 3 >= wrows) acc.w = 0.0f;
+        const float4 bi = b4[i], c = xr[i];
+        v[j] = make_float4(c.x + alpha * (acc.x + bi.x), c.y + alpha * (acc.y + bi.y), c.z + alpha * (acc.z + bi.z),
+                           c.w + alpha * (acc.w + bi.w));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      gg[j] = in(j) ? g4[lane + 64 * j] : z4;
+      bb[j] = in(j) ? lb4[lane + 64 * j] : z4;
+      if (g2) gg2[j] = in(j) ? g24[lane + 64 * j] : z4, bb2[j] = in(j) ? b24[lane + 64 * j] : z4;
+    }
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    if (keep_x && in(j)) xr[lane + 64 * j] = v[j];
+    s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
   }
   const float mean = wave_sum(s) / (float)cols;
   float q = 0.0f;
 #pragma unroll
-  for (int j = 0; j < ROW_REGS / 4; j++) {
-    if (lane + 64 * j < q4) {
+  for (int j = 0; j < J; j++) {
+    if (in(j)) {
       float dx = v[j].x - mean, dy = v[j].y - mean, dz = v[j].z - mean, dw = v[j].w - mean;
       q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
     }
   }
   const float rstd = rsqrtf(wave_sum(q) / (float)cols + 1e-5f);
   OT *yy = y + (size_t)row * cols;
-  const float4 *g4 = (const float4 *)g, *lb4 = (const float4 *)b;
 #pragma unroll
-  for (int j = 0; j < ROW_REGS / 4; j++) {
-    const int i = lane + 64 * j;
-    if (i < q4) {
-      const float4 gg = g4[i], bb = lb4[i];
+  for (int j = 0; j < J; j++) {
+    if (in(j)) {
       float4 o;
-      o.x = (v[j].x - mean) * rstd * gg.x + bb.x;
-      o.y = (v[j].y - mean) * rstd * gg.y + bb.y;
-      o.z = (v[j].z - mean) * rstd * gg.z + bb.z;
-      o.w = (v[j].w - mean) * rstd * gg.w + bb.w;
-      store4(yy + 4 * i, o);
+      o.x = (v[j].x - mean) * rstd * gg[j].x + bb[j].x;
+      o.y = (v[j].y - mean) * rstd * gg[j].y + bb[j].y;
+      o.z = (v[j].z - mean) * rstd * gg[j].z + bb[j].z;
+      o.w = (v[j].w - mean) * rstd * gg[j].w + bb[j].w;
+      store4(yy + 4 * (lane + 64 * j), o);
       v[j] = o;
     }
   }
@@ -456,31 +499,28 @@ __global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__r
   // A second LayerNorm of y (the next block's first norm) into y2, from the registers.
   s = 0.0f;
 #pragma unroll
-  for (int j = 0; j < ROW_REGS / 4; j++)
-    if (lane + 64 * j < q4) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  for (int j = 0; j < J; j++)
+    if (in(j)) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
   const float mean2 = wave_sum(s) / (float)cols;
   q = 0.0f;
 #pragma unroll
-  for (int j = 0; j < ROW_REGS / 4; j++) {
-    if (lane + 64 * j < q4) {
+  for (int j = 0; j < J; j++) {
+    if (in(j)) {
       float dx = v[j].x - mean2, dy = v[j].y - mean2, dz = v[j].z - mean2, dw = v[j].w - mean2;
       q += (dx * dx + dy * dy) + (dz * dz + dw * dw);
     }
   }
   const float rstd2 = rsqrtf(wave_sum(q) / (float)cols + 1e-5f);
   _Float16 *y2r = y2 + (size_t)row * cols;
-  const float4 *g24 = (const float4 *)g2, *b24 = (const float4 *)b2;
 #pragma unroll
-  for (int j = 0; j < ROW_REGS / 4; j++) {
-    const int i = lane + 64 * j;
-    if (i < q4) {
-      const float4 gg = g24[i], bb = b24[i];
+  for (int j = 0; j < J; j++) {
+    if (in(j)) {
       float4 o;
-      o.x = (v[j].x - mean2) * rstd2 * gg.x + bb.x;
-      o.y = (v[j].y - mean2) * rstd2 * gg.y + bb.y;
-      o.z = (v[j].z - mean2) * rstd2 * gg.z + bb.z;
-      o.w = (v[j].w - mean2) * rstd2 * gg.w + bb.w;
-      store4(y2r + 4 * i, o);
+      o.x = (v[j].x - mean2) * rstd2 * gg2[j].x + bb2[j].x;
+      o.y = (v[j].y - mean2) * rstd2 * gg2[j].y + bb2[j].y;
+      o.z = (v[j].z - mean2) * rstd2 * gg2[j].z + bb2[j].z;
+      o.w = (v[j].w - mean2) * rstd2 * gg2[j].w + bb2[j].w;
+      store4(y2r + 4 * (lane + 64 * j), o);
     }
   }
 }
@@ -507,12 +547,21 @@ int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *
   if (cols <= ROW_REGS * 64 && cols % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 &&
       (uintptr_t)g % 16 == 0 && (uintptr_t)b % 16 == 0) {
     size_t lds = table ? (size_t)4 * cols * sizeof(float) : 0;
-    if (out16)
-      wh_launch(ctx, layer_norm_kernel<_Float16>, (rows + 3) / 4, 256, lds, x, g, b, (_Float16 *)y, rows, cols, table,
-                                                                             (_Float16 *)yr, hd);
-    else
-      wh_launch(ctx, layer_norm_kernel<float>, (rows + 3) / 4, 256, lds, x, g, b, (float *)y, rows, cols, table,
-                                                                          (float *)yr, hd);
+#define LN(OT, NJ) \
+  wh_launch(ctx, layer_norm_kernel<OT, NJ>, (rows + 3) / 4, 256, lds, x, g, b, (OT *)y, rows, cols, table, (OT *)yr, hd)
+    const int nj = cols % 256 ? 0 : cols / 256;
+    if (out16) {
+      if (nj == 3) LN(_Float16, 3);
+      else if (nj == 4) LN(_Float16, 4);
+      else if (nj == 5) LN(_Float16, 5);
+      else LN(_Float16, 0);
+    } else {
+      if (nj == 3) LN(float, 3);
+      else if (nj == 4) LN(float, 4);
+      else if (nj == 5) LN(float, 5);
+      else LN(float, 0);
+    }
+#undef LN
   } else {
     if (table || out16)
       return wh_fail(ctx, WH_EARG, "layer_norm: rope and f16 rows need cols %% 4 == 0, at most %d", ROW_REGS * 64);
@@ -531,9 +580,18 @@ int launch_split_residual_ln(wh_ctx *ctx, const float *part, int splits, const f
   ProfScope prof(ctx, "split_residual_ln", 0.0,
                  (double)rows * cols * (4.0 * splits + (keep_x ? 8 : 4) + (out16 ? 2 : 4) + (g2 ? 2 : 0)));
   const int grid = (rows + 3) / 4;
-#define SRL(OT, N)                                                                                                  \
-  wh_launch(ctx, split_residual_ln_kernel<OT, N>, grid, 256, 0, part, splits, bias, wrows, alpha, x, g, b, (OT *)y, \
-                                                                  rows, cols, keep_x, g2, b2, (_Float16 *)y2)
+#define SRL(OT, N)                                                                                                   \
+  do {                                                                                                               \
+    if (cols == 1024 && N > 0)                                                                                       \
+      wh_launch(ctx, split_residual_ln_kernel<OT, N, 4>, grid, 256, 0, part, splits, bias, wrows, alpha, x, g, b,      \
+                (OT *)y, rows, cols, keep_x, g2, b2, (_Float16 *)y2);                                                \
+    else if (cols == 1280 && N > 0)                                                                                  \
+      wh_launch(ctx, split_residual_ln_kernel<OT, N, 5>, grid, 256, 0, part, splits, bias, wrows, alpha, x, g, b,      \
+                (OT *)y, rows, cols, keep_x, g2, b2, (_Float16 *)y2);                                                \
+    else                                                                                                             \
+      wh_launch(ctx, split_residual_ln_kernel<OT, N, 0>, grid, 256, 0, part, splits, bias, wrows, alpha, x, g, b,      \
+                (OT *)y, rows, cols, keep_x, g2, b2, (_Float16 *)y2);                                                \
+  } while (0)
   if (out16) {
     if (splits == 2) SRL(_Float16, 2);
     else if (splits == 4) SRL(_Float16, 4);

@@ -852,28 +852,18 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     bool ok = false;
 #define PLAN(BM, BN, WM, WN, NS)                                                           \
   if (!ok && p.bm == BM && p.bn == BN && p.wm == WM && p.wn == WN && p.ns == NS) {          \
-    if constexpr (WT == WH_Q8_0) {                                                          \
-      if (p.var == 1) lds_launch<WT, BM, BN, WM, WN, NS, 1>(ctx, grid, args, sp, out16);    \
-      else if (p.var == 2) lds_launch<WT, BM, BN, WM, WN, NS, 2>(ctx, grid, args, sp, out16); \
-      else if (p.var == 3) lds_launch<WT, BM, BN, WM, WN, NS, 3>(ctx, grid, args, sp, out16); \
-      else lds_launch<WT, BM, BN, WM, WN, NS, 0>(ctx, grid, args, sp, out16);               \
-    } else lds_launch<WT, BM, BN, WM, WN, NS, 0>(ctx, grid, args, sp, out16);               \
+    lds_launch<WT, BM, BN, WM, WN, NS, 0>(ctx, grid, args, sp, out16);                      \
     ok = true;                                                                               \
   }
     PLAN(128, 128, 2, 4, 4)
-    PLAN(128, 128, 1, 4, 4)
-    PLAN(128, 128, 1, 4, 6)
-    PLAN(128, 256, 1, 4, 4)
-    PLAN(128, 256, 1, 8, 4)
     PLAN(64, 64, 2, 2, 4)
-    PLAN(64, 64, 2, 2, 8)
-    PLAN(64, 128, 1, 4, 6)
-    PLAN(128, 64, 1, 2, 4)
-    PLAN(64, 64, 1, 2, 6)
     PLAN(128, 128, 2, 4, 3)
     PLAN(64, 64, 2, 2, 3)
     PLAN(128, 128, 2, 2, 3)
     PLAN(256, 128, 4, 2, 3)
+    PLAN(128, 64, 2, 2, 3)
+    PLAN(128, 64, 2, 2, 4)
+    PLAN(64, 128, 2, 2, 4)
 #undef PLAN
     if (!ok) return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages", p.bm, p.bn, p.wm, p.wn, p.ns);
     if (int rc = wh_launched(ctx, "gemm")) return rc;

@@ -969,13 +969,13 @@ int record_block(wh_model *m, int layer, const Block &k, float *x, float *y, int
       CK(launch_attention(c, m->qk, nullptr, pos, y16, t, m->heads, hd, valid_dev, t, batch, 1, 1, ps));
     }
   }
-  CK(g16(y16, k.out, x, rows, WH_RESIDUAL, 1.0f, 0));
-  CK(ln16(k.norm_conv));
+  // The residual projections and the norm after them: one fused finish + LayerNorm kernel when the
+  // GEMM's plan splits k, else the GEMM's residual epilogue and a LayerNorm launch.
+  CK(launch_gemm_h_ln(c, y16, k.out, x, rows, 1.0f, k.norm_conv.w, k.norm_conv.b, y16, 1));
   CK(g16(y16, k.pw1, m->qk, rows, WH_BIAS, 0.0f, 0));
   CK(launch_conv_glu(c, m->qk, k.dw.w, k.dw.b, m->kernel, k.conv_norm.w, k.conv_norm.b, m->layer_norm_conv, y16, t, d,
                      valid_dev, t, batch, 1));
-  CK(g16(y16, k.pw2, x, rows, WH_RESIDUAL, 1.0f, 0));
-  CK(ln16(k.norm_ff2));
+  CK(launch_gemm_h_ln(c, y16, k.pw2, x, rows, 1.0f, k.norm_ff2.w, k.norm_ff2.b, y16, 1));
   CK(g16(y16, k.ff2[0], h16, rows, WH_SILU, 0.0f, 1));
   // The block output is norm_out(x), not the residual stream (x is not stored again).
   return launch_gemm_h_ln(c, h16, k.ff2[1], x, rows, 0.5f, k.norm_out.w, k.norm_out.b, y, 0, 0,

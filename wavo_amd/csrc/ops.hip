@@ -161,6 +161,9 @@ __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__
   const bool on = c < ch;
   const float *hs = h + (size_t)seg * t * 2 * ch;
   float4 acc[CF];
+  // The norm's weights, loaded with the inputs (they are used after the reductions).
+  const float4 gg = on ? *(const float4 *)(g + c) : make_float4(0, 0, 0, 0);
+  const float4 bb = on ? *(const float4 *)(gb + c) : make_float4(0, 0, 0, 0);
   {
     float4 tap[K];
     const float4 bias = on ? *(const float4 *)(wb + c) : make_float4(0, 0, 0, 0);
@@ -172,13 +175,22 @@ __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__
     }
 #pragma unroll
     for (int i = 0; i < CF; i++) acc[i] = bias;
+    // Every input frame's loads first (from a clamped in-bounds address, zeroed after), so the wave
+    // waits for one memory round trip rather than one per frame.
+    float4 xs[SPAN], gs[SPAN];
+#pragma unroll
+    for (int r = 0; r < SPAN; r++) {
+      const int src = f0 - pad + r;
+      const size_t at = (size_t)(src >= 0 && src < lim ? src : 0) * 2 * ch + (on ? c : 0);
+      xs[r] = *(const float4 *)(hs + at);
+      gs[r] = *(const float4 *)(hs + at + ch);
+    }
 #pragma unroll
     for (int r = 0; r < SPAN; r++) {
       const int src = f0 - pad + r;
       float4 v = make_float4(0, 0, 0, 0);
       if (on && src >= 0 && src < lim) {
-        const float4 x = *(const float4 *)(hs + (size_t)src * 2 * ch + c);
-        const float4 gt = *(const float4 *)(hs + (size_t)src * 2 * ch + ch + c);
+        const float4 x = xs[r], gt = gs[r];
         v.x = x.x / (1.0f + __expf(-gt.x));
         v.y = x.y / (1.0f + __expf(-gt.y));
         v.z = x.z / (1.0f + __expf(-gt.z));
@@ -231,7 +243,6 @@ __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__
     }
   }
   if (!on) return;
-  const float4 gg = *(const float4 *)(g + c), bb = *(const float4 *)(gb + c);
 #pragma unroll
   for (int i = 0; i < CF; i++) {
     const int f = f0 + i;

@@ -59,11 +59,11 @@ GemmPlan gemm_plan_for(const wh_ctx *ctx, int m, int cols, int k) {
     p = {128, 128, 2, 4, 4, 1};
   else if (t128 * 4 <= cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
     // Long k over few tiles (the FFN's down projection, 750 × 1024 × 4096): k split 4 ways over
-    // 128×64 tiles of 4 wavefronts (64×32 per wavefront, as the 8-wave 128×128 tiles) in three
-    // stages, so that two workgroups share a CU and their barriers do not align (measured in the
-    // encoder step: 4.67 against 4.75 ms per 60 s call for 128×128 tiles of 8 wavefronts, 4.92 for
-    // 128×64 tiles in four stages, one per CU).
-    p = {128, 64, 2, 2, 3, 4};
+    // 96×64 tiles of 2 wavefronts (96×32 per wavefront: each dequantized W fragment feeds three
+    // MFMAs) in three stages: 512 workgroups, two per CU, whose barriers do not align (measured in
+    // the encoder step, 60 s: 4.64 ms, against 4.68 for 128×64 tiles of 4 wavefronts, 4.75 for
+    // 128×128 tiles of 8 wavefronts, 4.92 for 128×64 tiles in four stages, one per CU).
+    p = {96, 64, 1, 2, 3, 4};
   else if (t128 * 4 <= 2L * cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
     // The same with up to two workgroups per CU (Whisper's fc2, 1500 × 1280 × 5120: 1.18 + its
     // finish against 1.82 ms per call for 64×64 tiles whole).

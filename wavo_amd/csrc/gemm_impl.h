@@ -864,6 +864,10 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     PLAN(128, 64, 2, 2, 3)
     PLAN(128, 64, 2, 2, 4)
     PLAN(64, 128, 2, 2, 4)
+    PLAN(96, 128, 1, 4, 3)
+    PLAN(96, 128, 1, 4, 4)
+    PLAN(96, 64, 1, 2, 3)
+    PLAN(96, 128, 1, 4, 6)
 #undef PLAN
     if (!ok) return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages", p.bm, p.bn, p.wm, p.wn, p.ns);
     if (int rc = wh_launched(ctx, "gemm")) return rc;

@@ -36,6 +36,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int KB = 32;  // keys per block
 constexpr int QW = 4;   // wavefronts (16 queries each) per workgroup
+// Key blocks whose DMA runs ahead of the MFMAs (measured: two or three, at one workgroup per CU
+// for their LDS, are slower than one at two per CU).
+constexpr int PD = 1;
 constexpr int TS = 20;  // floats per row of the band skew buffer: its writes and reads hit distinct banks
 
 // Scratch layout of one call: the packed operands, each array 256-byte aligned.
@@ -178,7 +181,6 @@ __global__ __launch_bounds__(256) void pack_kernel(const T *__restrict__ k, int 
 
 // ---------------------------------------------------------------------------------- flash kernel
 
-// PD: key blocks whose DMA runs ahead of the MFMAs.
 template <int NC, bool REL, int PD>
 __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
   constexpr int DP = NC * 32;          // head dims padded to the MFMA's k
@@ -496,8 +498,6 @@ int flash_lds(int dp, bool rel, int pd) {
   return (pd + 1) * 2 * kbytes + (rel ? (ng + pd) * kbytes + QW * 48 * TS * 4 : 4);
 }
 
-// Key blocks whose DMA runs ahead of the MFMAs in the flash kernel.
-int flash_pd(const wh_ctx *ctx) { return ctx->attn_pd > 0 ? ctx->attn_pd : 1; }
 
 // Key splits per query tile: workgroups for every slot the CUs hold at once (LDS-bound: two per CU
 // for 128-dim relative attention) while every split keeps ≥ 3 key blocks.
@@ -506,7 +506,7 @@ int kv_splits(const wh_ctx *ctx, int t, int heads, int hd, int batch, bool rel) 
   if (ctx->attn_split > 0) return std::min(ctx->attn_split, std::max(nkb, 1));
   const int cus = ctx->cus > 0 ? ctx->cus : 256;
   const int dp = hd <= 32 ? 32 : hd <= 64 ? 64 : 128;
-  const long slots = (long)cus * std::max(1, std::min(2, 160 * 1024 / flash_lds(dp, rel, flash_pd(ctx))));
+  const long slots = (long)cus * std::max(1, std::min(2, 160 * 1024 / flash_lds(dp, rel, PD)));
   const long items = (long)((t + 16 * QW - 1) / (16 * QW)) * heads * batch;
   int ns = 1;
   while (ns < 4 && items * ns * 2 <= slots && nkb / (2 * ns) >= 3) ns *= 2;
@@ -533,19 +533,11 @@ int launch_flash(wh_ctx *ctx, const Args &a, int heads, int batch, int dp) {
   const double bytes = 2.0 * batch * a.t * heads * a.hd * (REL ? 6 : 4) + (a.o16 ? 2.0 : 4.0) * batch * a.t * heads * a.hd;
   ProfScope prof(ctx, REL ? "attention_rel" : "attention", (REL ? 6.0 : 4.0) * tt, bytes);
   const dim3 grid((a.t + 16 * QW - 1) / (16 * QW), heads, batch * a.nsplit);
-  const int pd = flash_pd(ctx);
-#define FLASH(NC)                                                                                    \
-  do {                                                                                               \
-    if (pd == 3) wh_launch(ctx, flash_kernel<NC, REL, 3>, grid, 64 * QW, 0, a);                      \
-    else if (pd == 2) wh_launch(ctx, flash_kernel<NC, REL, 2>, grid, 64 * QW, 0, a);                 \
-    else wh_launch(ctx, flash_kernel<NC, REL, 1>, grid, 64 * QW, 0, a);                              \
-  } while (0)
   switch (dp) {
-    case 32: FLASH(1); break;
-    case 64: FLASH(2); break;
-    default: FLASH(4); break;
+    case 32: wh_launch(ctx, flash_kernel<1, REL, PD>, grid, 64 * QW, 0, a); break;
+    case 64: wh_launch(ctx, flash_kernel<2, REL, PD>, grid, 64 * QW, 0, a); break;
+    default: wh_launch(ctx, flash_kernel<4, REL, PD>, grid, 64 * QW, 0, a); break;
   }
-#undef FLASH
   if (int rc = wh_launched(ctx, "attention")) return rc;
   if (a.nsplit > 1) {
     const size_t n = (size_t)batch * a.t * heads * (a.hd / 4);

@@ -83,7 +83,6 @@ GemmPlan gemm_plan_for(const wh_ctx *ctx, int m, int cols, int k) {
       p = {o[3], o[4], o[5], o[6], o[7], o[8]};
       if (k % (64 * p.split)) p.split = 1;
     }
-  if (ctx->gemm_pp >= 0) p.var = ctx->gemm_pp;  // tuning override (wh_tune "gemm_pp")
   return p;
 }
 

@@ -12,7 +12,6 @@
 // Launch shapes of the LDS-DMA kernel (tile, wavefronts, k step, split).
 struct GemmPlan {
   int bm, bn, wm, wn, ns, split;
-  int var = 0;  // kernel variant bits: 1 DMA spread over the substeps, 2 16-byte DMA of quantized rows
 };
 
 // The launch plan of an m × cols × k GEMM (gemm.hip).
@@ -530,28 +529,23 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
 // distinct banks) and leave as 8 consecutive columns per lane: 16-byte loads of c for the residual
 // modes and 16-byte stores, with the bias, the epilogue, the dual columns and the padding columns
 // (epi(0 + bias), as the reference's zero rows give) applied on the way.
-template <int WT, int BM, int BN, int WM, int WN, int NSQ, bool SPLIT, bool OUT16, int VAR>
+template <int WT, int BM, int BN, int WM, int WN, int NSQ, bool SPLIT, bool OUT16>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
   static_assert(TM >= 1 && TN >= 1, "32×32 MFMA tiles per wave");
   constexpr int PAIR1 = WT == WH_Q8_0 ? 68 : WT == WH_Q4_0 ? 36 : 128;  // W bytes of 64 weights
   constexpr bool WCH = WT == WH_F16;                                     // W moves in 16-byte chunks
-  // VAR bit 0: the DMA of a step spread over the substeps; bit 1: quantized rows moved by 16-byte
-  // DMA into LDS rows padded to 16 bytes (WROW), the last chunk of a row read from 16 bytes before
-  // the row's end (its bytes past WROW − 16 land 12 bytes further on).
-  constexpr bool SPREAD = VAR & 1, W16 = (VAR & 2) && !WCH;
-  constexpr int WROW = W16 ? (PAIR1 + 15) / 16 * 16 : PAIR1, WSH = WROW - PAIR1;
-  constexpr int A_ST = BM * 128, W_ST = BN * WROW, ST = A_ST + W_ST;
+  constexpr int A_ST = BM * 128, W_ST = BN * PAIR1, ST = A_ST + W_ST;
   constexpr int CROW = BN + 8;                                           // f32 per epilogue LDS row
   constexpr int C_BYTES = BM * CROW * 4;
   // NSQ stages asked for, as many as fit in the 160 KiB of LDS.
   constexpr int NS = NSQ * ST + 16 <= 160 * 1024 ? NSQ : (160 * 1024 - 16) / ST;
   static_assert(NS >= 3, "at least three stages");
-  static_assert((WCH || W16) ? W_ST % 1024 == 0 : W_ST % 256 == 0, "whole DMA instructions");
+  static_assert(WCH || W_ST % 256 == 0, "whole DMA instructions");
   constexpr int W_RG = NS * A_ST;                               // the W stages follow the a stages
   constexpr int NIA = A_ST / 1024;                              // a: 16-byte DMA instructions per stage
-  constexpr int NIW = (WCH || W16) ? W_ST / 1024 : W_ST / 256;  // W: 16-byte or 4-byte ones
+  constexpr int NIW = WCH ? W_ST / 1024 : W_ST / 256;           // W: 16-byte or 4-byte ones
   constexpr int PA = (NIA + NW - 1) / NW, PW = (NIW + NW - 1) / NW, PI = PA + PW;
   static_assert((NS - 2) * PI < 64, "vmcnt holds the DMA of NS - 2 steps");
   // (+16: the odd block of the last W row reads one dword past its row, unused)
@@ -600,11 +594,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
       const int r = 8 * n + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
       woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * lc);
       wlds[i] = 1024 * n;
-    } else if constexpr (W16) {
-      constexpr int CH = WROW / 16;  // chunks per row
-      const int ci = 64 * n + lane, r = ci / CH, c = ci % CH;
-      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + (c < CH - 1 ? 16 * c : PAIR1 - 16));
-      wlds[i] = 1024 * n;
     } else {
       const int sidx = 64 * n + lane, r = sidx / (PAIR1 / 4), dwi = sidx % (PAIR1 / 4);
       woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 4 * dwi);
@@ -614,17 +603,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   const uint8_t *abase = (const uint8_t *)P.a + (size_t)kb * 128;
   const uint8_t *wbase = P.w + (size_t)kb * PAIR1;
   const uint32_t lds0 = lds_addr(lds);
-  // The wave's DMA instructions of step kt into ring slot `slot`: all of them (part < 0), or those
-  // whose index (a instructions first) is `part` modulo 4.
-  auto issue = [&](int kt, int slot, int part = -1) {
+  auto issue = [&](int kt, int slot) {
     const uint8_t *ab = abase + (size_t)kt * 128, *wb = wbase + (size_t)kt * PAIR1;
 #pragma unroll
-    for (int i = 0; i < PA; i++)
-      if (part < 0 || i % 4 == part) dma16s(ab, aoff[i], lds0 + slot * A_ST + alds[i]);
+    for (int i = 0; i < PA; i++) dma16s(ab, aoff[i], lds0 + slot * A_ST + alds[i]);
 #pragma unroll
     for (int i = 0; i < PW; i++) {
-      if (part >= 0 && (PA + i) % 4 != part) continue;
-      if constexpr (WCH || W16) dma16s(wb, woff[i], lds0 + W_RG + slot * W_ST + wlds[i]);
+      if constexpr (WCH) dma16s(wb, woff[i], lds0 + W_RG + slot * W_ST + wlds[i]);
       else dma4s(wb, woff[i], lds0 + W_RG + slot * W_ST + wlds[i]);
     }
   };
@@ -644,7 +629,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   constexpr int ND = Q8 ? 10 : WT == WH_Q4_0 ? 5 : 16;  // dwords per lane per W row and step
   constexpr int NSC = Q8 ? 2 : 1;                       // scale dwords per lane per W row and step
   constexpr int BLK = PAIR1 / 2;
-  const uint32_t w_row = W_RG + (wn + lrow) * WROW;
+  const uint32_t w_row = W_RG + (wn + lrow) * PAIR1;
   const uint32_t w_dat = Q8 ? w_row + 8 * g : w_row + (g ? BLK + 2 : 0), w_sc = w_row + (g ? BLK - 2 : 0);
   uint32_t wf_off[4];
 #pragma unroll
@@ -660,29 +645,24 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
       if constexpr (WCH) {
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-          const uint4 x = *(const uint4 *)(lds + wf_off[s] + slot * W_ST + j * 32 * WROW);
+          const uint4 x = *(const uint4 *)(lds + wf_off[s] + slot * W_ST + j * 32 * PAIR1);
           w[j][4 * s] = x.x, w[j][4 * s + 1] = x.y, w[j][4 * s + 2] = x.z, w[j][4 * s + 3] = x.w;
         }
         sc[j][0] = 0;
       } else if constexpr (Q8) {
         // Pair bytes 2 + 8g .. (block 0, substeps 0-1: dwords 0-2 and 4-6 from byte 8g) and
         // 36 + 8g .. (block 1, substeps 2-3: dwords 9-10 and 13-14); the scales at bytes 0 and 34.
-        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * WROW);
+        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * PAIR1);
         constexpr int at[10] = {0, 1, 2, 4, 5, 6, 9, 10, 13, 14};
 #pragma unroll
-        for (int i = 0; i < 9; i++) w[j][i] = q[at[i]];
-        // Byte 56 + 8g: for g = 1 past byte 64 (W16: moved by WSH).
-        w[j][9] = *(const uint32_t *)(lds + w_dat + (W16 && g ? WSH : 0) + 56 + slot * W_ST + j * 32 * WROW);
-        const uint32_t *r = (const uint32_t *)(lds + w_row + slot * W_ST + j * 32 * WROW);
+        for (int i = 0; i < 10; i++) w[j][i] = q[at[i]];
+        const uint32_t *r = (const uint32_t *)(lds + w_row + slot * W_ST + j * 32 * PAIR1);
         sc[j][0] = r[0], sc[j][1] = r[8];
       } else {
-        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * WROW);
+        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * PAIR1);
 #pragma unroll
         for (int i = 0; i < ND; i++) w[j][i] = q[i];
-        if constexpr (W16)  // g = 1: dwords 3-4 start at byte 32 (moved by WSH)
-          w[j][3] = *(const uint32_t *)(lds + w_dat + (g ? WSH : 0) + 12 + slot * W_ST + j * 32 * WROW),
-          w[j][4] = *(const uint32_t *)(lds + w_dat + (g ? WSH : 0) + 16 + slot * W_ST + j * 32 * WROW);
-        sc[j][0] = *(const uint32_t *)(lds + w_sc + slot * W_ST + j * 32 * WROW);
+        sc[j][0] = *(const uint32_t *)(lds + w_sc + slot * W_ST + j * 32 * PAIR1);
       }
     }
   };
@@ -732,17 +712,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
     // Step kt (S = kt modulo the unroll: ring slot S % NS, register set S % 2).
     auto step = [&](auto S_c, int kt) {
       constexpr int S = decltype(S_c)::value, slot = S % NS, cur = S & 1;
-      // SPREAD: the DMA of step kt + NS − 2 (begun after the previous step's barrier) continues
-      // between the substeps, so that the 8 waves do not queue all their DMA at once.
-      const bool pend = SPREAD && kt >= 1 && kt + NS - 2 < nk;
-      constexpr int pslot = (S + NS - 2) % NS;
-      if (pend) issue(kt + NS - 2, pslot, 1);
       read_a(af[1], slot, 1);
       mma(af[0], wq[cur], sc[cur], std::integral_constant<int, 0>{});
-      if (pend) issue(kt + NS - 2, pslot, 2);
       read_a(af[0], slot, 2);
       mma(af[1], wq[cur], sc[cur], std::integral_constant<int, 1>{});
-      if (pend) issue(kt + NS - 2, pslot, 3);
       read_a(af[1], slot, 3);
       mma(af[0], wq[cur], sc[cur], std::integral_constant<int, 2>{});
       if (kt + 1 < nk) {
@@ -750,7 +723,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
         if (kt + NS - 2 < nk) wait_vm<(NS - 3) * PI>();
         else dma_wait();
         __syncthreads();
-        if (kt + NS - 1 < nk) issue(kt + NS - 1, (slot + NS - 1) % NS, SPREAD ? 0 : -1);
+        if (kt + NS - 1 < nk) issue(kt + NS - 1, (slot + NS - 1) % NS);
         read_w(wq[cur ^ 1], sc[cur ^ 1], (slot + 1) % NS);
         read_a(af[0], (slot + 1) % NS, 0);
       }
@@ -812,11 +785,11 @@ __global__ __launch_bounds__(256) void split_finish_kernel(const float *__restri
   }
 }
 
-template <int WT, int BM, int BN, int WM, int WN, int NS, int VAR>
+template <int WT, int BM, int BN, int WM, int WN, int NS>
 void lds_launch(wh_ctx *ctx, dim3 grid, const LdsArgs &a, bool split, bool out16) {
-  if (split) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, true, false, VAR>, grid, 64 * WM * WN, 0, a);
-  else if (out16) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, true, VAR>, grid, 64 * WM * WN, 0, a);
-  else wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, false, VAR>, grid, 64 * WM * WN, 0, a);
+  if (split) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, true, false>, grid, 64 * WM * WN, 0, a);
+  else if (out16) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, true>, grid, 64 * WM * WN, 0, a);
+  else wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, false>, grid, 64 * WM * WN, 0, a);
 }
 
 template <int WT>
@@ -840,8 +813,8 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
   static const char *tn = WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
   // Named by kernel variant and call shape: m x rows x k, epilogue, output type, row width.
   char name[128];
-  snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s%s %dx%dx%d e%d %s w%d", tn, p.bm, p.bn, p.wm, p.wn, p.ns,
-           p.split > 1 ? (p.split == 2 ? "_s2" : "_s4") : "", p.var ? (p.var == 1 ? "_v1" : p.var == 2 ? "_v2" : "_v3") : "", m, l->rows, l->k, epi,
+  snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s %dx%dx%d e%d %s w%d", tn, p.bm, p.bn, p.wm, p.wn, p.ns,
+           p.split > 1 ? (p.split == 2 ? "_s2" : "_s4") : "", m, l->rows, l->k, epi,
            out16 ? "f16" : "f32", l->cols + l->dual);
   const double width = l->cols + l->dual;
   const double bytes = (double)l->rows * l->row_bytes + 2.0 * m * l->k +
@@ -852,7 +825,7 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     bool ok = false;
 #define PLAN(BM, BN, WM, WN, NS)                                                           \
   if (!ok && p.bm == BM && p.bn == BN && p.wm == WM && p.wn == WN && p.ns == NS) {          \
-    lds_launch<WT, BM, BN, WM, WN, NS, 0>(ctx, grid, args, sp, out16);                      \
+    lds_launch<WT, BM, BN, WM, WN, NS>(ctx, grid, args, sp, out16);                         \
     ok = true;                                                                               \
   }
     PLAN(128, 128, 2, 4, 4)

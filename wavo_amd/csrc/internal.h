@@ -42,10 +42,6 @@ struct wh_ctx {
   std::vector<std::array<int, 9>> gemm_shape_plans;
   // Attention key-split override set by wh_tune("attn_split", "n") (tuning sweeps only): 0 = chosen per shape.
   int attn_split = 0;
-  // Flash-attention DMA depth override set by wh_tune("attn_pd", "n") (tuning sweeps only): 0 = chosen.
-  int attn_pd = 0;
-  // Ping-pong GEMM override set by wh_tune("gemm_pp", "0" / "1" / "-1") (tuning only): -1 = chosen per shape.
-  int gemm_pp = -1;
   // wh_tune("mel_raw", "1") (checks only): the frontends write each filter's sum before the logarithm.
   int mel_raw = 0;
   // wh_tune("whisper_host", "1") (checks only): wh_whisper_decode picks each token on the host.

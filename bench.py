@@ -397,6 +397,63 @@ def decode_steps(gpu, tokens=224):
             "us_per_token": round(ms * 1e3, 2), "tokens_per_s": round(1e3 / ms, 1), "window_search": search}
 
 
+def decoders(gpu, model, host, pcm, melb, outb, mel_frames, frames, width, seconds):
+    """The TDT decode of the step's output on the host (as the reference runs it) and on the device,
+    and audio to tokens on the device; host clock."""
+    dec = []
+    tokens = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        tokens = model.greedy(host)
+        dec.append(time.perf_counter() - t0)
+
+    # The same decode on the device, over the encoder output still in HBM.
+    ddec = []
+    dtokens = []
+    for i in range(7):
+        t0 = time.perf_counter()
+        dtokens = model.greedy_device(outb, frames, width)
+        if i >= 2:
+            ddec.append(time.perf_counter() - t0)
+    log(f"TDT decode: host {statistics.median(dec) * 1e3:.1f} ms, device {statistics.median(ddec) * 1e3:.2f} ms "
+        f"({len(dtokens)} tokens, {'equal' if dtokens == tokens else 'different'})")
+
+    # Audio to tokens on the device: the PCM upload, the reference's Parakeet frontend (wh_model_mel,
+    # into the same mel buffer the step reads), the encoder and the TDT decode; host clock.
+    pcm_b = gpu.upload(pcm)
+    assert model.mel_frames(len(pcm)) == mel_frames
+
+    def audio_to_tokens():
+        gpu.write(pcm_b, pcm)
+        model.mel_device(pcm_b, len(pcm), melb)
+        model.encode_device(melb, mel_frames, outb)
+        return model.greedy_device(outb, frames, width)
+
+    e2e = []
+    for i in range(9):
+        t0 = time.perf_counter()
+        e2e_tokens = audio_to_tokens()
+        if i >= 2:
+            e2e.append(time.perf_counter() - t0)
+    mel_prof = profiled(gpu, lambda: model.mel_device(pcm_b, len(pcm), melb))
+    mel_us = sum(r["ms"] for r in mel_prof) * 1e3
+    e2e_med = statistics.median(e2e)
+    log(f"audio to tokens on the device: {e2e_med * 1e3:.2f} ms ({seconds / e2e_med:.0f}x real time), "
+        f"frontend {mel_us:.1f} us, {len(e2e_tokens)} tokens")
+    return {
+        "tdt_decode_ms": round(statistics.median(dec) * 1e3, 2),
+        "tdt_tokens": len(tokens),
+        "tdt_device": {"ms_median": round(statistics.median(ddec) * 1e3, 3), "tokens": len(dtokens),
+                       "equal_to_host": dtokens == tokens,
+                       "what": "wh_model_greedy_device over the resident encoder output, host clock"},
+        "audio_to_tokens": {"ms_median": round(e2e_med * 1e3, 3), "rtfx": round(seconds / e2e_med, 1),
+                            "tokens": len(e2e_tokens), "frontend_us": round(mel_us, 2),
+                            "frontend_kernels": {r["kernel"]: round(r["ms"] * 1e3, 2) for r in mel_prof},
+                            "what": "PCM upload (pageable) + the Parakeet log-mel frontend (wh_model_mel) + encoder + "
+                                    "TDT decode on the device + tokens read back, host clock, median of 7 after 2"},
+    }
+
+
 def traffic_for(name):
     """HBM bytes per launch for this GEMM configuration from a committed rocprofv3 summary, if any."""
     path = os.path.join(ROOT, "profiles", "gemm_traffic.txt")
@@ -468,6 +525,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-gemv", action="store_true", help="skip the decoder GEMV and decoder step measurements")
     ap.add_argument("--no-configs", action="store_true", help="skip the encoder timings of the other BASELINE configs")
+    ap.add_argument("--no-decode", action="store_true", help="skip the TDT decode and audio-to-tokens timings")
     ap.add_argument("--replay", metavar="NAME", default=None,
                     help="only the back-to-back launches of this GEMM configuration (a roofline.kernel value), "
                          "or 'attention_rel' for the Parakeet attention call, for rocprofv3 passes over exactly "
@@ -542,46 +600,9 @@ def main():
         if i >= 2:
             io.append(time.perf_counter() - t0)
     io_med = statistics.median(io)
-    dec = []
-    tokens = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        tokens = model.greedy(host)
-        dec.append(time.perf_counter() - t0)
-
-    # The same decode on the device, over the encoder output still in HBM.
-    ddec = []
-    dtokens = []
-    for i in range(7):
-        t0 = time.perf_counter()
-        dtokens = model.greedy_device(outb, frames, width)
-        if i >= 2:
-            ddec.append(time.perf_counter() - t0)
-    log(f"TDT decode: host {statistics.median(dec) * 1e3:.1f} ms, device {statistics.median(ddec) * 1e3:.2f} ms "
-        f"({len(dtokens)} tokens, {'equal' if dtokens == tokens else 'different'})")
-
-    # Audio to tokens on the device: the PCM upload, the reference's Parakeet frontend (wh_model_mel,
-    # into the same mel buffer the step reads), the encoder and the TDT decode; host clock.
-    pcm_b = gpu.upload(pcm)
-    assert model.mel_frames(len(pcm)) == mel_frames
-
-    def audio_to_tokens():
-        gpu.write(pcm_b, pcm)
-        model.mel_device(pcm_b, len(pcm), melb)
-        model.encode_device(melb, mel_frames, outb)
-        return model.greedy_device(outb, frames, width)
-
-    e2e = []
-    for i in range(9):
-        t0 = time.perf_counter()
-        e2e_tokens = audio_to_tokens()
-        if i >= 2:
-            e2e.append(time.perf_counter() - t0)
-    mel_prof = profiled(gpu, lambda: model.mel_device(pcm_b, len(pcm), melb))
-    mel_us = sum(r["ms"] for r in mel_prof) * 1e3
-    e2e_med = statistics.median(e2e)
-    log(f"audio to tokens on the device: {e2e_med * 1e3:.2f} ms ({args.seconds / e2e_med:.0f}x real time), "
-        f"frontend {mel_us:.1f} us, {len(e2e_tokens)} tokens")
+    decode = None
+    if not args.no_decode:
+        decode = decoders(gpu, model, host, pcm, melb, outb, mel_frames, frames, width, args.seconds)
 
     # One call with every launch stamped: per-kernel in-step durations.
     prof = profiled(gpu, step)
@@ -661,16 +682,7 @@ def main():
         "host_io": {"ms_median": round(io_med * 1e3, 3), "rtfx": round(args.seconds / io_med, 1),
                     "what": "mel upload (pageable host memory) + encoder call + output read-back, host clock"},
         "host_frontend_ms": round(statistics.median(fe) * 1e3, 2),
-        "tdt_decode_ms": round(statistics.median(dec) * 1e3, 2),
-        "tdt_tokens": len(tokens),
-        "tdt_device": {"ms_median": round(statistics.median(ddec) * 1e3, 3), "tokens": len(dtokens),
-                       "equal_to_host": dtokens == tokens,
-                       "what": "wh_model_greedy_device over the resident encoder output, host clock"},
-        "audio_to_tokens": {"ms_median": round(e2e_med * 1e3, 3), "rtfx": round(args.seconds / e2e_med, 1),
-                            "tokens": len(e2e_tokens), "frontend_us": round(mel_us, 2),
-                            "frontend_kernels": {r["kernel"]: round(r["ms"] * 1e3, 2) for r in mel_prof},
-                            "what": "PCM upload (pageable) + the Parakeet log-mel frontend (wh_model_mel) + encoder + "
-                                    "TDT decode on the device + tokens read back, host clock, median of 7 after 2"},
+        **(decode or {}),
         "load": load,
         "gemv": gemv,
         "other_configs": others,

@@ -109,6 +109,18 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// f(integral_constant<I>, kb0 + I) for I = S .. N − 1 while kb0 + I < nkb: a loop body unrolled with its
+// position in the period known at compile time.
+template <int S, int N, class F>
+__device__ __forceinline__ void unrolled_blocks(F &f, int kb0, int nkb) {
+  if constexpr (S < N) {
+    if (kb0 + S < nkb) {
+      f(std::integral_constant<int, S>{}, kb0 + S);
+      unrolled_blocks<S + 1, N>(f, kb0, nkb);
+    }
+  }
+}
+
 // Chunk rotation of LDS rows of CH 16-byte chunks: the 16 lanes that read one chunk column of 16
 // consecutive rows hit 16 distinct 4-bank groups (rows of 256, 128 or 64 bytes).
 template <int CH>
@@ -305,8 +317,12 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
     for (int x = 0; x < PD; x++)
       if (kb0 + x < nkb) issue(kb0 + x, x, NG - 1 + x, false);
   }
-  int kvs = 0, ps0 = 0;  // K/V slot of block kb; group slot of its band's first group
-  for (int kb = kb0; kb < nkb; kb++) {
+  // Block kb's K/V slot and its band's first group slot repeat with period PERIOD: the loop is
+  // unrolled by it, so that every slot offset is a compile-time constant (no per-block address
+  // arithmetic).
+  constexpr int PERIOD = REL ? (NP % NKV == 0 ? NP : NKV * NP) : NKV;
+  auto block = [&](auto I_c, int kb) {
+    constexpr int kvs = decltype(I_c)::value % NKV, ps0 = REL ? decltype(I_c)::value % (REL ? NP : 1) : 0;
     // Block kb has landed (blocks after it may still be in flight); every wave is done with kb − 1,
     // whose K/V slot and first band group take block kb + PD.
     if (kb + PD - 1 < nkb) wait_vm<(PD - 1) * PER>();
@@ -316,6 +332,19 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
     const int j0 = kb * KB;
     const _Float16 *kt = (const _Float16 *)(lds + kvs * 2 * KBYTES);
     const _Float16 *vtl = kt + KB * DP;
+    // The block's Vᵀ fragments are read now, ahead of the scores: their LDS latency overlaps the
+    // QKᵀ and band MFMAs instead of the PV ones (the band's wave fence would keep them after it).
+    // A Vᵀ row (one dim) has 4 chunks of 8 keys, rotated by row / 4; the lane's 8 k-slots are keys
+    // 4g + v and 16 + 4g + v, as its P values.
+    half8 vf[OT];
+#pragma unroll
+    for (int ot = 0; ot < OT; ot++) {
+      const int row = 16 * ot + li, rr = row >> 2;
+      const _Float16 *vr = vtl + row * KB;
+      const half4 a0 = *(const half4 *)(vr + 8 * (((g >> 1) + rr) & 3) + 4 * (g & 1));
+      const half4 a1 = *(const half4 *)(vr + 8 * ((2 + (g >> 1) + rr) & 3) + 4 * (g & 1));
+      vf[ot] = half8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+    }
 
     // Scores Sᵀ for the two 16-key tiles: lane holds keys 16·jt + 4g + v of query li.
     float s[2][4];
@@ -394,21 +423,16 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
       }
     l = l * alpha + ps;
 
-    // Oᵀ += Vᵀ·Pᵀ: the lane's 8 k-slots are keys 4g + v and 16 + 4g + v, as its P values.  A Vᵀ row
-    // (one dim) has 4 chunks of 8 keys, rotated by row / 4.
+    // Oᵀ += Vᵀ·Pᵀ, the accumulators first rescaled when some query's maximum rose (α = 1 for the
+    // others: the same values; after the first blocks the maximum seldom moves).
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-    for (int ot = 0; ot < OT; ot++) {
-      om[ot] *= alpha;
-      const int row = 16 * ot + li, rr = row >> 2;
-      const _Float16 *vr = vtl + row * KB;
-      const half4 a0 = *(const half4 *)(vr + 8 * (((g >> 1) + rr) & 3) + 4 * (g & 1));
-      const half4 a1 = *(const half4 *)(vr + 8 * ((2 + (g >> 1) + rr) & 3) + 4 * (g & 1));
-      const half8 a = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-      om[ot] = mfma(a, pf, om[ot]);
+      for (int ot = 0; ot < OT; ot++) om[ot] *= alpha;
     }
-    kvs = kvs + 1 == NKV ? 0 : kvs + 1;
-    if constexpr (REL) ps0 = ps0 + 1 == NP ? 0 : ps0 + 1;
-  }
+#pragma unroll
+    for (int ot = 0; ot < OT; ot++) om[ot] = mfma(vf[ot], pf, om[ot]);
+  };
+  for (int kb = kb0; kb < nkb; kb += PERIOD) unrolled_blocks<0, PERIOD>(block, kb, nkb);
 
   // The row sums over the 4 lanes of each query, then Oᵀ tile ot holds dims 16·ot + 4g + v.
   l += __shfl_xor(l, 16, 64);

@@ -223,8 +223,8 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
   uint8_t *st = smem;                                                  // GV_NS stages
   const int items = P.k / 64;
   float *as = (float *)(smem + GV_NS * GV_STAGE);                      // a: items × AS
-  float *part = as + items * AS;                                       // 256 partial sums
-  float *rsum = part + 256;                                            // the workgroup's row sums
+  float *part = as + items * AS;          // every stage's 256 partial sums (per_wg × 256), summed after the loop
+  float *rsum = part + 256 * P.per_wg;    // the workgroup's row sums
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int s0 = blockIdx.x * P.per_wg, s1 = min(s0 + P.per_wg, P.stages);
@@ -372,25 +372,27 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
         }
       }
     }
-    part[tid] = sum;
-    __syncthreads();
-    if (tid < nrows) {
-      // The row's items in order, 4 at a time (items % 4 == 0 when k % 256 == 0; else a tail).
-      float acc = 0.0f;
-      const float *pr = part + tid * items;
-      int i = 0;
-      if ((items & 3) == 0) {
-#pragma unroll 4
-        for (; i < items; i += 4) {
-          const float4 v = *(const float4 *)(pr + i);
-          acc += ((v.x + v.y) + (v.z + v.w));
-        }
-      }
-      for (; i < items; i++) acc += pr[i];
-      rsum[(s - s0) * P.rps + tid] = acc;
-    }
+    part[(s - s0) * 256 + tid] = sum;  // the thread's own slot: no barrier until after the loop
   }
-  // The epilogue of the workgroup's rows at once, off the streaming loop.
+  // The rows' items in order, 4 at a time (items % 4 == 0 when k % 256 == 0; else a tail), for
+  // every stage of the workgroup at once, off the streaming loop; then the epilogue.
+  __syncthreads();
+  const int nsr = (s1 - s0) * P.rps;  // the workgroup's stage rows (the last stage's may pass `rows`)
+  for (int j = tid; j < nsr; j += 256) {
+    const int st = j / P.rps, rl = j - st * P.rps;
+    const float *pr = part + st * 256 + rl * items;
+    float acc = 0.0f;
+    int i = 0;
+    if ((items & 3) == 0) {
+#pragma unroll 4
+      for (; i < items; i += 4) {
+        const float4 v = *(const float4 *)(pr + i);
+        acc += ((v.x + v.y) + (v.z + v.w));
+      }
+    }
+    for (; i < items; i++) acc += pr[i];
+    rsum[j] = acc;
+  }
   __syncthreads();
   const int r0 = s0 * P.rps, r1 = min(s1 * P.rps, P.rows);
   const bool res = P.epi == WH_RESIDUAL || P.epi == WH_GELU_RESIDUAL;
@@ -431,7 +433,7 @@ int gemv_stream(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int e
   P.per_wg = (P.stages + wgs - 1) / wgs;
   const int grid = (P.stages + P.per_wg - 1) / P.per_wg;
   P.total = (size_t)l->rows * l->row_bytes;
-  const size_t lds = (size_t)GV_NS * GV_STAGE + 4 * (size_t)items * 68 + 4 * 256 + 4 * (size_t)P.per_wg * P.rps;
+  const size_t lds = (size_t)GV_NS * GV_STAGE + 4 * (size_t)items * 68 + 4 * (256 + (size_t)P.rps) * P.per_wg;
   if (lds > 160 * 1024) return 1;  // (positive: not an error) the caller takes the general kernel
   // Named by type and shape (rows x k): the profile tells the decoder's GEMVs apart.
   char tn[64];

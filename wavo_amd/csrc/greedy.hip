@@ -319,10 +319,10 @@ __global__ __launch_bounds__(256) void tdt_step_kernel(TdtArgs a) {
     hv[i] = a.h_old[min(j, n - 1)];
   }
   int token = 0;
+  float ev[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // the emitted token's embedding row (zero for the first predict)
   if constexpr (!INIT) {
-    const TdtState *st = a.st;
-    if (st->done) return;
-    // The parts' first maxima (token rows, duration rows): every part loaded first.
+    // The parts' first maxima (token rows, duration rows): every part loaded first, with the state
+    // (one round trip).
     float4 q[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -330,6 +330,8 @@ __global__ __launch_bounds__(256) void tdt_step_kernel(TdtArgs a) {
       q[i] = *(const float4 *)(a.part + 4 * min(p, a.parts - 1));  // clamped: no branch
       if (p >= a.parts) q[i] = float4{0.0f, -1.0f, 0.0f, -1.0f};
     }
+    const TdtState *st = a.st;
+    if (st->done) return;
 #pragma unroll
     for (int k = 0; k < 2; k++) {
       float v = -FLT_MAX;
@@ -377,6 +379,13 @@ __global__ __launch_bounds__(256) void tdt_step_kernel(TdtArgs a) {
     }
     const int done = nt >= st->frames || (a.cfg.global && left <= 0);
     const int idle = (!emit || done) ? 1 : 0;
+    // The decision's dependent loads go out together: the token's embedding row (layer 0's input)
+    // and, below, the next frame's encoder row.
+    {
+      const float *row = a.embed + (size_t)min(max(token, 0), a.cfg.classes - 1) * n;
+#pragma unroll
+      for (int i = 0; i < 4; i++) ev[i] = row[min(tid + 256 * i, n - 1)];  // clamped: no branch
+    }
     // The next frame's encoder row, for the next joint input: each workgroup its slice.
     if (!done) {
       const float *e = st->enc + (size_t)nt * st->width;
@@ -403,12 +412,10 @@ __global__ __launch_bounds__(256) void tdt_step_kernel(TdtArgs a) {
     for (int j = blockIdx.x * 256 + tid; j < a.joint; j += gridDim.x * 256) a.erow[j] = e[j];
   }
   // Layer 0's input [embedding row of the token | h]: the first predict has a zero input.
-  const float *row = a.embed + (size_t)token * n;
-  stage<4>(xin, n, [&](int j) { return INIT ? 0.0f : row[j]; });
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int j = tid + 256 * i;
-    if (j < n) xin[n + j] = hv[i];
+    if (j < n) xin[j] = ev[i], xin[n + j] = hv[i];
   }
   __syncthreads();
   cell.finish(a, 0, xin, a.h_new);

@@ -150,29 +150,98 @@ __device__ __forceinline__ float wave_sums(float (&v)[N]) {
   return s;
 }
 
+// ------------------------------------------------------------------ weight rows staged through LDS
+// A workgroup's weight rows are one run of contiguous bytes (the joint's or the predictor's 4·RW
+// consecutive rows) or four (an LSTM workgroup's four cells: rows g·n + 4·blockIdx.x .. + 3 of gate
+// g).  They go into LDS in whole 16-byte chunks, a coalesced 16-byte load per lane and chunk with
+// every load of a round issued before any store, and the products read them from LDS: one memory
+// round trip for all of a wavefront's rows.  (Each lane loading its 2-byte-aligned half blocks as a
+// few dwords straight from global memory took ~5 µs for a wavefront's 8 rows: many small requests
+// per row.)  A run starts `lead` = its offset & 15 bytes into its first chunk.  The chunks copied
+// cover the run's bytes and stay inside the layer's allocation, which is 256-byte aligned (so offsets
+// and addresses agree mod 16) with 256 bytes of zeros after its last row.
+constexpr int STAGE_P = 8;  // chunks per thread and round: 32 KiB per workgroup and round
+
+// LDS chunks given to a run of `bytes` bytes (its lead is a multiple of 4: rows of whole dwords).
+__host__ __device__ constexpr int run_chunks(size_t bytes) { return (int)((bytes + 12 + 15) / 16); }
+
+template <int RUNS>
+struct Runs {
+  const uint8_t *w;
+  size_t start[RUNS];  // byte offsets of the runs in w
+  int len;             // chunks copied per run (≤ cpr)
+  int cpr;             // LDS chunks per run
+
+  __device__ __forceinline__ const uint4 *base(int g) const { return (const uint4 *)(w + (start[g] & ~(size_t)15)); }
+  // Where run g's first byte lands in LDS.
+  __device__ __forceinline__ const uint8_t *at(const uint4 *lds, int g) const {
+    return (const uint8_t *)(lds + g * cpr) + (start[g] & 15);
+  }
+};
+
+// One run of `nrows` rows of rb bytes from row `first` (fewer than the run's LDS room at a layer's end:
+// only the chunks of the rows that exist are copied).
+__device__ __forceinline__ Runs<1> one_run(const uint8_t *w, size_t rb, int first, int nrows, int cpr) {
+  Runs<1> r;
+  r.w = w, r.start[0] = (size_t)first * rb, r.cpr = cpr;
+  r.len = (int)(((r.start[0] & 15) + (size_t)nrows * rb + 15) / 16);
+  return r;
+}
+
+// One round of a staging copy: chunks j0 + tid + 256·i (i < STAGE_P / RUNS) of every run.
+template <int RUNS>
+struct StageRound {
+  static constexpr int PR = STAGE_P / RUNS;
+  uint4 v[STAGE_P];
+
+  __device__ __forceinline__ void load(const Runs<RUNS> &r, int j0) {
+#pragma unroll
+    for (int g = 0; g < RUNS; g++)
+#pragma unroll
+      for (int i = 0; i < PR; i++) v[g * PR + i] = r.base(g)[min(j0 + (int)threadIdx.x + 256 * i, r.len - 1)];  // clamped
+  }
+  // Unconditional (lanes past the end write the last chunk again, the same bytes): a store behind a
+  // branch lets the compiler sink its load there, after the waits that precede it.
+  __device__ __forceinline__ void store(uint4 *lds, const Runs<RUNS> &r, int j0) const {
+#pragma unroll
+    for (int g = 0; g < RUNS; g++)
+#pragma unroll
+      for (int i = 0; i < PR; i++) lds[g * r.cpr + min(j0 + (int)threadIdx.x + 256 * i, r.len - 1)] = v[g * PR + i];
+  }
+};
+
+// The rounds after the first (runs longer than 256·STAGE_P / RUNS chunks), a round trip each.
+template <int RUNS>
+__device__ __forceinline__ void stage_rest(uint4 *lds, const Runs<RUNS> &r) {
+  constexpr int STEP = 256 * StageRound<RUNS>::PR;
+  for (int j0 = STEP; j0 < r.len; j0 += STEP) {
+    StageRound<RUNS> s;
+    s.load(r, j0);
+    s.store(lds, r, j0);
+  }
+}
+
 // RW consecutive rows from r0 (those below `rows`) of a layer with k ≤ 1024 inputs, held by one
-// wavefront: load() issues every weight and bias load (from addresses clamped into the layer, so that
-// no load sits behind a branch and the wavefront waits once), finish() multiplies with x in LDS and
-// sums; lane 64·i/RW gets row i's value (plus bias).
+// wavefront and staged in LDS (row r at run + (r − rr0)·rb, rr0 the run's first row); lane 64·i/RW
+// gets row i's value (plus bias).
 template <int WT, int RW>
 struct Rows {
-  Half<WT> h[RW];
   float b;
   int r0, rows, k;
 
-  __device__ __forceinline__ void load(const uint8_t *__restrict__ w, size_t rb, const float *__restrict__ bias,
-                                       int first, int nrows, int kk) {
+  // The bias load, issued with the kernel's other loads.
+  __device__ __forceinline__ void init(const float *__restrict__ bias, int first, int nrows, int kk) {
     r0 = first, rows = nrows, k = kk;
-    const int lane = threadIdx.x & 63, hb = min(lane, k / 16 - 1);
-#pragma unroll
-    for (int i = 0; i < RW; i++) h[i].load(w + (size_t)min(r0 + i, rows - 1) * rb, hb);
-    b = bias[min(r0 + lane * RW / 64, rows - 1)];
+    b = bias[min(r0 + (int)(threadIdx.x & 63) * RW / 64, rows - 1)];
   }
 
   // The value of row r0 + lane·RW/64 (0 past the rows).
-  __device__ __forceinline__ float finish(const float *x) const {
+  __device__ __forceinline__ float finish(const uint8_t *run, int rr0, size_t rb, const float *x) const {
     const int lane = threadIdx.x & 63, hb = min(lane, k / 16 - 1);
     const bool on = lane < k / 16;
+    Half<WT> h[RW];
+#pragma unroll
+    for (int i = 0; i < RW; i++) h[i].load(run + (size_t)(min(r0 + i, rows - 1) - rr0) * rb, hb);
     float v[RW];
 #pragma unroll
     for (int i = 0; i < RW; i++) v[i] = on && r0 + i < rows ? h[i].dot(hb, x) : 0.0f;
@@ -180,18 +249,24 @@ struct Rows {
   }
 };
 
-// Stages n ≤ 256·P values into LDS: every load into registers first (one round trip), then the stores.
+// LDS of the joint's and the predictor's weight rows (4·RW rows per workgroup).
+template <int WT>
+__host__ __device__ constexpr int rows_cpr(size_t rb) { return run_chunks(4 * rows_per_wave<WT>() * rb); }
+
+// Stages n ≤ 256·P values into LDS: every load into registers first (one round trip), then the stores,
+// unconditional as the staged rows' (lanes past n write value n − 1 again).
 template <int P, typename F>
 __device__ __forceinline__ void stage(float *dst, int n, F value) {
   float v[P];
 #pragma unroll
   for (int i = 0; i < P; i++) v[i] = value(min((int)threadIdx.x + 256 * i, n - 1));  // clamped: no branch
 #pragma unroll
-  for (int i = 0; i < P; i++) {
-    const int j = threadIdx.x + 256 * i;
-    if (j < n) dst[j] = v[i];
-  }
+  for (int i = 0; i < P; i++) dst[min((int)threadIdx.x + 256 * i, n - 1)] = v[i];
 }
+
+// Keeps a loaded value's load where it is: the compiler would otherwise sink it into the branch that
+// uses it, behind the decision's own round trip.
+__device__ __forceinline__ void pin(float v) { asm volatile("" : : "v"(v)); }
 
 __device__ __forceinline__ float sigm(float v) { return 1.0f / (1.0f + expf(-v)); }
 
@@ -202,20 +277,28 @@ __device__ __forceinline__ float sigm(float v) { return 1.0f / (1.0f + expf(-v))
 template <int WT>
 __global__ __launch_bounds__(256) void tdt_joint_kernel(TdtArgs a) {
   constexpr int RW = rows_per_wave<WT>();
-  extern __shared__ float z[];
+  extern __shared__ uint4 lds[];
   __shared__ float bv[2][4];
   __shared__ int bi[2][4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  // The weights and z (written by the previous decision's last kernel) in one round trip.
-  const int r0 = (blockIdx.x * 4 + wave) * RW;
+  // The workgroup's rows and z (written by the previous decision's last kernel) in one round trip.
+  const int g0 = blockIdx.x * 4 * RW, r0 = g0 + wave * RW;
+  const Runs<1> run = one_run(a.out_w, a.out_rb, g0, min(4 * RW, a.out_rows - g0), rows_cpr<WT>(a.out_rb));
+  StageRound<1> w0;
+  w0.load(run, 0);
   Rows<WT, RW> rows;
-  rows.load(a.out_w, a.out_rb, a.out_b, r0, a.out_rows, a.joint);
+  rows.init(a.out_b, r0, a.out_rows, a.joint);
+  float *z = (float *)(lds + run.cpr);
   const float *zg = a.z;
+  const int done = a.st->done;
   stage<4>(z, a.joint, [&](int j) { return zg[j]; });
-  if (a.st->done) return;
+  w0.store(lds, run, 0);
+  pin(rows.b);
+  if (done) return;
+  stage_rest(lds, run);
   __syncthreads();
   // Row r0 + i's value is in lane 64·i/RW: the first maximum over those lanes, in row order.
-  const float val = rows.finish(z);
+  const float val = rows.finish(run.at(lds, 0), g0, a.out_rb, z);
   const int r = r0 + lane * RW / 64;
   const bool mine = lane % (64 / RW) == 0 && r < a.out_rows;
   float tv = -FLT_MAX, dv = -FLT_MAX;
@@ -246,36 +329,53 @@ __global__ __launch_bounds__(256) void tdt_joint_kernel(TdtArgs a) {
   }
 }
 
+// LDS chunks per gate run of an LSTM workgroup (four cells' rows of one gate).
+__host__ __device__ constexpr int lstm_cpr(size_t rb) { return run_chunks(4 * rb); }
+
 // One LSTM layer's cell k (one per wavefront) over [x | h_old] (2n ≤ 2048 values in LDS): the four gate
-// rows k, n + k, 2n + k, 3n + k of the joined [Wx | Wh] with the bias, c' = σ(f)·c + σ(i)·tanh(g),
-// h' = σ(o)·tanh(c').
+// rows k, n + k, 2n + k, 3n + k of the joined [Wx | Wh] (staged in LDS with the workgroup's other
+// cells') with the bias, c' = σ(f)·c + σ(i)·tanh(g), h' = σ(o)·tanh(c').
 template <int WT>
 struct Cell {
-  Half<WT> h[4][2];
   float b[4], cold;
   int k, hbs;
 
-  // Every load of this wavefront's cell (weights, biases, its c) before it waits for anything, from
-  // addresses clamped into the layer (no load behind a branch).
-  __device__ __forceinline__ void load(const TdtArgs &a, int layer) {
-    const int n = a.n, lane = threadIdx.x & 63;
+  // The workgroup's four gate runs (n % 16 == 0: every workgroup has four cells).
+  __device__ __forceinline__ static Runs<4> runs(const TdtArgs &a, int layer) {
+    Runs<4> r;
+    r.w = a.lstm_w[layer], r.cpr = r.len = lstm_cpr(a.lstm_rb);
+#pragma unroll
+    for (int g = 0; g < 4; g++) r.start[g] = (size_t)(g * a.n + 4 * (int)blockIdx.x) * a.lstm_rb;
+    return r;
+  }
+
+  // The biases and the cell's c, issued with the kernel's other loads.
+  __device__ __forceinline__ void init(const TdtArgs &a, int layer) {
+    const int n = a.n;
     hbs = 2 * n / 16;
     k = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int kk = min(k, n - 1);
-    const uint8_t *w = a.lstm_w[layer];
     const float *bias = a.lstm_b[layer];
 #pragma unroll
+    for (int g = 0; g < 4; g++) b[g] = bias[g * n + kk];
+    cold = a.c[(size_t)layer * n + kk];
+  }
+  __device__ __forceinline__ void pin_loads() const {
+#pragma unroll
+    for (int g = 0; g < 4; g++) pin(b[g]);
+    pin(cold);
+  }
+
+  __device__ __forceinline__ void finish(const TdtArgs &a, int layer, const Runs<4> &run, const uint4 *lds,
+                                         const float *xin, float *h_new) const {
+    const int n = a.n, lane = threadIdx.x & 63, cell = threadIdx.x >> 6;
+    Half<WT> h[4][2];
+#pragma unroll
     for (int g = 0; g < 4; g++) {
-      b[g] = bias[g * n + kk];
-      const uint8_t *row = w + (size_t)(g * n + kk) * a.lstm_rb;
+      const uint8_t *row = run.at(lds, g) + (size_t)cell * a.lstm_rb;
 #pragma unroll
       for (int i = 0; i < 2; i++) h[g][i].load(row, min(lane + 64 * i, hbs - 1));
     }
-    cold = a.c[(size_t)layer * n + kk];
-  }
-
-  __device__ __forceinline__ void finish(const TdtArgs &a, int layer, const float *xin, float *h_new) const {
-    const int n = a.n, lane = threadIdx.x & 63;
     float acc[4];
 #pragma unroll
     for (int g = 0; g < 4; g++) {
@@ -305,33 +405,38 @@ struct Cell {
 // a zero input.
 template <int WT, bool INIT>
 __global__ __launch_bounds__(256) void tdt_step_kernel(TdtArgs a) {
-  extern __shared__ float xin[];
+  extern __shared__ uint4 lds[];
   __shared__ float sv[2][4];
   __shared__ int si[2][4];
   const int tid = threadIdx.x, n = a.n;
-  // The cell's weights and the old h do not depend on the decision: their loads go out first.
+  // The cells' weight rows, biases and c and the old h do not depend on the decision: their loads go
+  // out first.
   Cell<WT> cell;
-  cell.load(a, 0);
+  const Runs<4> run = Cell<WT>::runs(a, 0);
+  StageRound<4> w0;
+  w0.load(run, 0);
+  cell.init(a, 0);
+  float *xin = (float *)(lds + 4 * run.cpr);
   float hv[4];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int j = tid + 256 * i;
-    hv[i] = a.h_old[min(j, n - 1)];
+  for (int i = 0; i < 4; i++) hv[i] = a.h_old[min(tid + 256 * i, n - 1)];
+  // The parts' first maxima (token rows, duration rows): every part loaded with the rest, and the
+  // state (one round trip for all).
+  float4 q[4];
+  if constexpr (!INIT) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = *(const float4 *)(a.part + 4 * min(tid + 256 * i, a.parts - 1));  // clamped: no branch
   }
+  const int done0 = INIT ? 0 : a.st->done;
+  w0.store(lds, run, 0);
+#pragma unroll
+  for (int i = 0; i < 4; i++) xin[n + min(tid + 256 * i, n - 1)] = hv[i];  // the old h: layer 0's input's second half
+  cell.pin_loads();
+  if (done0) return;
   int token = 0;
   float ev[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // the emitted token's embedding row (zero for the first predict)
   if constexpr (!INIT) {
-    // The parts' first maxima (token rows, duration rows): every part loaded first, with the state
-    // (one round trip).
-    float4 q[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int p = tid + 256 * i;
-      q[i] = *(const float4 *)(a.part + 4 * min(p, a.parts - 1));  // clamped: no branch
-      if (p >= a.parts) q[i] = float4{0.0f, -1.0f, 0.0f, -1.0f};
-    }
     const TdtState *st = a.st;
-    if (st->done) return;
 #pragma unroll
     for (int k = 0; k < 2; k++) {
       float v = -FLT_MAX;
@@ -339,7 +444,7 @@ __global__ __launch_bounds__(256) void tdt_step_kernel(TdtArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         const float pv = k ? q[j].z : q[j].x;
-        const int pi = (int)(k ? q[j].w : q[j].y);
+        const int pi = tid + 256 * j < a.parts ? (int)(k ? q[j].w : q[j].y) : -1;  // clamped copies: none
         if (pi >= 0 && (i < 0 || better(pv, pi, v, i))) v = pv, i = pi;
       }
 #pragma unroll
@@ -411,28 +516,41 @@ __global__ __launch_bounds__(256) void tdt_step_kernel(TdtArgs a) {
     const float *e = a.st->enc;
     for (int j = blockIdx.x * 256 + tid; j < a.joint; j += gridDim.x * 256) a.erow[j] = e[j];
   }
+  stage_rest(lds, run);
   // Layer 0's input [embedding row of the token | h]: the first predict has a zero input.
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int j = tid + 256 * i;
-    if (j < n) xin[j] = ev[i], xin[n + j] = hv[i];
-  }
+  for (int i = 0; i < 4; i++) xin[min(tid + 256 * i, n - 1)] = ev[i];
   __syncthreads();
-  cell.finish(a, 0, xin, a.h_new);
+  cell.finish(a, 0, run, lds, xin, a.h_new);
 }
 
 // LSTM layer l ≥ 1 over [layer l − 1's new h | its own h]; nothing while idle.
 template <int WT>
 __global__ __launch_bounds__(256) void tdt_layer_kernel(TdtArgs a, int layer) {
-  extern __shared__ float xin[];
+  extern __shared__ uint4 lds[];
   Cell<WT> cell;
-  cell.load(a, layer);
-  if (a.nx->idle) return;
+  const Runs<4> run = Cell<WT>::runs(a, layer);
+  StageRound<4> w0;
+  w0.load(run, 0);
+  cell.init(a, layer);
   const int n = a.n;
+  float *xin = (float *)(lds + 4 * run.cpr);
   const float *x = a.h_new + (size_t)(layer - 1) * n, *h = a.h_old + (size_t)layer * n;
-  stage<8>(xin, 2 * n, [&](int j) { return j < n ? x[j] : h[j - n]; });
+  float xv[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int j = min((int)threadIdx.x + 256 * i, 2 * n - 1);  // clamped: no branch
+    xv[i] = j < n ? x[j] : h[j - n];
+  }
+  const int idle = a.nx->idle;
+  w0.store(lds, run, 0);
+#pragma unroll
+  for (int i = 0; i < 8; i++) xin[min((int)threadIdx.x + 256 * i, 2 * n - 1)] = xv[i];
+  cell.pin_loads();
+  if (idle) return;
+  stage_rest(lds, run);
   __syncthreads();
-  cell.finish(a, layer, xin, a.h_new + (size_t)layer * n);
+  cell.finish(a, layer, run, lds, xin, a.h_new + (size_t)layer * n);
 }
 
 // One TDT decision, last part: after an emission the joint's predictor projection of the last layer's
@@ -442,14 +560,18 @@ __global__ __launch_bounds__(256) void tdt_layer_kernel(TdtArgs a, int layer) {
 template <int WT>
 __global__ __launch_bounds__(256) void tdt_pred_kernel(TdtArgs a) {
   constexpr int RW = rows_per_wave<WT>();
-  extern __shared__ float hin[];
+  extern __shared__ uint4 lds[];
   const TdtState *nx = a.nx;
   const int n = a.n, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // Everything this kernel reads goes out before the wait for the state: the weights, the new h,
   // and for this wavefront's rows the next encoder row and the current projection.
-  const int r0 = (blockIdx.x * 4 + wave) * RW, r = r0 + lane * RW / 64, rc = min(r, a.joint - 1);
+  const int g0 = blockIdx.x * 4 * RW, r0 = g0 + wave * RW, r = r0 + lane * RW / 64, rc = min(r, a.joint - 1);
+  const Runs<1> run = one_run(a.pred_w, a.pred_rb, g0, min(4 * RW, a.joint - g0), rows_cpr<WT>(a.pred_rb));
+  StageRound<1> w0;
+  w0.load(run, 0);
   Rows<WT, RW> rows;
-  rows.load(a.pred_w, a.pred_rb, a.pred_b, r0, a.joint, n);
+  rows.init(a.pred_b, r0, a.joint, n);
+  float *hin = (float *)(lds + run.cpr);
   const float *h = a.h_new + (size_t)(a.layers - 1) * n;
   float hv[4];
 #pragma unroll
@@ -457,14 +579,15 @@ __global__ __launch_bounds__(256) void tdt_pred_kernel(TdtArgs a) {
   const float erow = a.erow[rc];
   float pv = a.pred[rc];
   const bool mine = lane % (64 / RW) == 0 && r < a.joint;
-  if (!nx->idle) {
+  const int idle = nx->idle;
+  w0.store(lds, run, 0);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int j = tid + 256 * i;
-      if (j < n) hin[j] = hv[i];
-    }
+  for (int i = 0; i < 4; i++) hin[min(tid + 256 * i, n - 1)] = hv[i];
+  pin(rows.b), pin(erow), pin(pv);
+  if (!idle) {
+    stage_rest(lds, run);
     __syncthreads();
-    pv = rows.finish(hin);
+    pv = rows.finish(run.at(lds, 0), g0, a.pred_rb, hin);
     if (mine) a.pred[r] = pv;
     for (int j = blockIdx.x * 256 + tid; j < a.layers * n; j += gridDim.x * 256) a.h_old[j] = a.h_new[j];
   }
@@ -529,22 +652,23 @@ int launch_tdt_init(wh_ctx *ctx, TdtState *st, TdtState *nx, const TdtState &ini
 template <int WT>
 static int tdt_launch_t(wh_ctx *ctx, const TdtArgs &a, int what) {
   const int cells = (a.n + 3) / 4;
+  const size_t cell_lds = 64 * (size_t)lstm_cpr(a.lstm_rb) + 8 * a.n;
   switch (what) {
     case TDT_JOINT: {
       ProfScope prof(ctx, "tdt_joint", 2.0 * a.out_rows * a.joint, (double)a.out_rb * a.out_rows + 8.0 * a.joint);
-      wh_launch(ctx, tdt_joint_kernel<WT>, a.parts, 256, (size_t)4 * a.joint, a);
+      wh_launch(ctx, tdt_joint_kernel<WT>, a.parts, 256, 16 * (size_t)rows_cpr<WT>(a.out_rb) + 4 * a.joint, a);
       return wh_launched(ctx, "tdt joint");
     }
     case TDT_STEP:
     case TDT_INIT: {
       ProfScope prof(ctx, what == TDT_INIT ? "tdt_init_step" : "tdt_step", 16.0 * a.n * a.n,
                      (double)a.lstm_rb * 4 * a.n + 16.0 * a.parts);
-      if (what == TDT_INIT) wh_launch(ctx, tdt_step_kernel<WT, true>, cells, 256, (size_t)8 * a.n, a);
-      else wh_launch(ctx, tdt_step_kernel<WT, false>, cells, 256, (size_t)8 * a.n, a);
+      if (what == TDT_INIT) wh_launch(ctx, tdt_step_kernel<WT, true>, cells, 256, cell_lds, a);
+      else wh_launch(ctx, tdt_step_kernel<WT, false>, cells, 256, cell_lds, a);
       if (int rc = wh_launched(ctx, "tdt step")) return rc;
       for (int l = 1; l < a.layers; l++) {
         ProfScope pl(ctx, "tdt_layer", 16.0 * a.n * a.n, (double)a.lstm_rb * 4 * a.n);
-        wh_launch(ctx, tdt_layer_kernel<WT>, cells, 256, (size_t)8 * a.n, a, l);
+        wh_launch(ctx, tdt_layer_kernel<WT>, cells, 256, cell_lds, a, l);
         if (int rc = wh_launched(ctx, "tdt layer")) return rc;
       }
       return WH_OK;
@@ -552,7 +676,7 @@ static int tdt_launch_t(wh_ctx *ctx, const TdtArgs &a, int what) {
     default: {
       ProfScope prof(ctx, "tdt_pred", 2.0 * a.joint * a.n, (double)a.pred_rb * a.joint);
       const int rows = 4 * rows_per_wave<WT>();
-      wh_launch(ctx, tdt_pred_kernel<WT>, (a.joint + rows - 1) / rows, 256, (size_t)4 * a.n, a);
+      wh_launch(ctx, tdt_pred_kernel<WT>, (a.joint + rows - 1) / rows, 256, 16 * (size_t)rows_cpr<WT>(a.pred_rb) + 4 * a.n, a);
       return wh_launched(ctx, "tdt pred");
     }
   }
@@ -569,6 +693,11 @@ int launch_tdt(wh_ctx *ctx, const TdtArgs &a, int what) {
       a.n <= 0 || a.n % 16 || a.n > 1024 || a.joint <= 0 || a.joint % 16 || a.joint > 1024 || a.layers < 1 ||
       a.layers > 4 || a.parts != tdt_parts(a.type, a.out_rows) || a.parts > 1024 || a.out_rows != c.classes + c.ndur)
     return wh_fail(ctx, WH_EARG, "tdt: bad decoder configuration");
+  // The products read the rows from LDS as whole dwords (quantized rows: k % 64 == 0); with k ≤ 1024
+  // a workgroup's rows take at most 128 KiB of LDS (four F32 gate runs of four 8 KiB rows).
+  if ((a.out_rb | a.pred_rb | a.lstm_rb) % 4)
+    return wh_fail(ctx, WH_EARG, "tdt: rows of %zu / %zu / %zu bytes (the device decoder takes whole dwords)", a.out_rb,
+                   a.pred_rb, a.lstm_rb);
   switch (a.type) {
     case WH_F32: return tdt_launch_t<WH_F32>(ctx, a, what);
     case WH_F16: return tdt_launch_t<WH_F16>(ctx, a, what);

@@ -121,33 +121,96 @@ struct Half {
 template <int WT>
 constexpr int rows_per_wave() { return WT == WH_F32 ? 4 : 8; }
 
-// Sums each of the N = 2^m values of every lane over the wavefront with 6 + N − 2 shuffles instead of
-// 6·N: each exchange halves the values a lane holds (a lane keeps half, its partner the other half),
-// then the single value is summed over the lanes that hold the same one.  Afterwards lane 64·v/N..
-// holds value v's sum (lanes with bit 5 − j of the lane index set hold the upper half at step j).
+// Cross-lane steps of the wave reductions, on the VALU instead of the LDS crossbar (__shfl_xor is a
+// ds_bpermute, ~100 cycles of latency per dependent step): DPP moves within rows of 16 lanes, and
+// gfx950's row swaps across them.
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1, 0, 3, 2]: lane ^ 1
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2, 3, 0, 1]: lane ^ 2
+constexpr int DPP_ROR8 = 0x128;        // row_ror:8: lane ^ 8
+constexpr int DPP_HALF_MIRROR = 0x141; // lane i of 8 from lane 7 − i
+constexpr int DPP_MIRROR = 0x140;      // lane i of 16 from lane 15 − i
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
+
+// v_permlane32_swap: x becomes (x of lanes 0..31 | y of lanes 0..31), y (x of lanes 32..63 | y of
+// lanes 32..63).  With x, y a lane's two values, x + y is then, in lanes 0..31, x plus the partner
+// lane's (l + 32) x, and in lanes 32..63 y plus the partner's (l − 32) y.
+template <typename T>
+__device__ __forceinline__ void swap32(T &x, T &y) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, y), false, false);
+  x = __builtin_bit_cast(T, (unsigned)r[0]), y = __builtin_bit_cast(T, (unsigned)r[1]);
+}
+// v_permlane16_swap: x becomes rows (x0, y0, x2, y2), y rows (x1, y1, x3, y3): the same for lane bit 4.
+template <typename T>
+__device__ __forceinline__ void swap16(T &x, T &y) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, y), false, false);
+  x = __builtin_bit_cast(T, (unsigned)r[0]), y = __builtin_bit_cast(T, (unsigned)r[1]);
+}
+
+// Sums each of the N = 4 or 8 values of every lane over the wavefront; afterwards lanes 64·v/N ..
+// 64·(v + 1)/N − 1 hold value v's sum.  Each halving step pairs a lane with the one that differs in
+// a lane bit (5, 4, then 3 for N = 8) and leaves it half its values (the upper half where the bit is
+// set) plus the partner's of the same half; then the lanes that hold the same value sum it.
 template <int N>
 __device__ __forceinline__ float wave_sums(float (&v)[N]) {
-  const int lane = threadIdx.x & 63;
-  float cur[N];
+  static_assert(N == 4 || N == 8, "4 or 8 values");
+  float c[N];
 #pragma unroll
-  for (int i = 0; i < N; i++) cur[i] = v[i];
-  int n = N;
+  for (int i = 0; i < N; i++) c[i] = v[i];
 #pragma unroll
-  for (int o = 32; n > 1; o >>= 1) {
-    const bool up = lane & o;
-    n >>= 1;
-#pragma unroll
-    for (int i = 0; i < N / 2; i++)
-      if (i < n) {
-        const float keep = up ? cur[n + i] : cur[i], send = up ? cur[i] : cur[n + i];
-        cur[i] = keep + __shfl_xor(send, o, 64);
-      }
+  for (int i = 0; i < N / 2; i++) {
+    float x = c[i], y = c[N / 2 + i];
+    swap32(x, y);
+    c[i] = x + y;
   }
-  float s = cur[0];
-  // The lanes that share this value: those equal in the bits used above.
 #pragma unroll
-  for (int o = 64 / N / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  for (int i = 0; i < N / 4; i++) {
+    float x = c[i], y = c[N / 4 + i];
+    swap16(x, y);
+    c[i] = x + y;
+  }
+  float s;
+  if constexpr (N == 8) {
+    const bool up = threadIdx.x & 8;
+    s = (up ? c[1] : c[0]) + dpp_f<DPP_ROR8>(up ? c[0] : c[1]);
+  } else {
+    s = c[0];
+  }
+  // The lanes that share the value: 8 (N = 8) or 16 consecutive ones.
+  s += dpp_f<DPP_XOR1>(s);
+  s += dpp_f<DPP_XOR2>(s);
+  s += dpp_f<DPP_HALF_MIRROR>(s);
+  if constexpr (N == 4) s += dpp_f<DPP_MIRROR>(s);
   return s;
+}
+
+// (v, i) becomes the first maximum of itself and (ov, oi): the greater value, or an equal one at the
+// smaller index; index −1 is none.
+__device__ __forceinline__ void take_first_max(float &v, int &i, float ov, int oi) {
+  if (oi >= 0 && (i < 0 || better(ov, oi, v, i))) v = ov, i = oi;
+}
+
+// The first maximum of every lane's (v, i) over the wavefront, in every lane.
+__device__ __forceinline__ void wave_first_max(float &v, int &i) {
+  take_first_max(v, i, dpp_f<DPP_XOR1>(v), dpp_i<DPP_XOR1>(i));
+  take_first_max(v, i, dpp_f<DPP_XOR2>(v), dpp_i<DPP_XOR2>(i));
+  take_first_max(v, i, dpp_f<DPP_HALF_MIRROR>(v), dpp_i<DPP_HALF_MIRROR>(i));
+  take_first_max(v, i, dpp_f<DPP_MIRROR>(v), dpp_i<DPP_MIRROR>(i));
+  // Rows: after a swap both registers hold a pair of row results, the same pair for both rows.
+  float x = v, y = v;
+  int a = i, b = i;
+  swap16(x, y), swap16(a, b);
+  v = x, i = a;
+  take_first_max(v, i, y, b);
+  x = v, y = v, a = i, b = i;
+  swap32(x, y), swap32(a, b);
+  v = x, i = a;
+  take_first_max(v, i, y, b);
 }
 
 // ------------------------------------------------------------------ weight rows staged through LDS
@@ -307,13 +370,8 @@ __global__ __launch_bounds__(256) void tdt_joint_kernel(TdtArgs a) {
     if (r < a.cfg.classes) tv = val, ti = r;
     else dv = val, di = r - a.cfg.classes;
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float otv = __shfl_xor(tv, o, 64), odv = __shfl_xor(dv, o, 64);
-    const int oti = __shfl_xor(ti, o, 64), odi = __shfl_xor(di, o, 64);
-    if (oti >= 0 && (ti < 0 || better(otv, oti, tv, ti))) tv = otv, ti = oti;
-    if (odi >= 0 && (di < 0 || better(odv, odi, dv, di))) dv = odv, di = odi;
-  }
+  wave_first_max(tv, ti);
+  wave_first_max(dv, di);
   if (lane == 0) bv[0][wave] = tv, bi[0][wave] = ti, bv[1][wave] = dv, bi[1][wave] = di;
   __syncthreads();
   if (tid == 0) {
@@ -389,7 +447,7 @@ struct Cell {
     const float own = wave_sums<4>(acc);
     float gate[4];
 #pragma unroll
-    for (int g = 0; g < 4; g++) gate[g] = __shfl(own, 16 * g, 64) + b[g];
+    for (int g = 0; g < 4; g++) gate[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, own), 16 * g)) + b[g];
     if (lane == 0 && k < n) {
       const float cc = sigm(gate[1]) * cold + sigm(gate[0]) * tanhf(gate[2]);
       a.c[(size_t)layer * n + k] = cc;
@@ -447,12 +505,7 @@ __global__ __launch_bounds__(256) void tdt_step_kernel(TdtArgs a) {
         const int pi = tid + 256 * j < a.parts ? (int)(k ? q[j].w : q[j].y) : -1;  // clamped copies: none
         if (pi >= 0 && (i < 0 || better(pv, pi, v, i))) v = pv, i = pi;
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(v, o, 64);
-        const int oi = __shfl_xor(i, o, 64);
-        if (oi >= 0 && (i < 0 || better(ov, oi, v, i))) v = ov, i = oi;
-      }
+      wave_first_max(v, i);
       if ((tid & 63) == 0) sv[k][tid >> 6] = v, si[k][tid >> 6] = i;
     }
     __syncthreads();

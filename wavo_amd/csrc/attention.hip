@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "internal.h"
+#include "xlane.h"
 
 namespace {
 
@@ -406,8 +407,7 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
     }
     float bm = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    bm = xlane::bit5(xlane::bit4(bm, xlane::Max{}), xlane::Max{});  // the query's 4 lanes (l ^ 16, l ^ 32)
     const float mn = fmaxf(m, bm);
     const float alpha = __builtin_amdgcn_exp2f(m - mn);
     m = mn;
@@ -435,8 +435,7 @@ __global__ __launch_bounds__(64 * QW) void flash_kernel(Args A) {
   for (int kb = kb0; kb < nkb; kb += PERIOD) unrolled_blocks<0, PERIOD>(block, kb, nkb);
 
   // The row sums over the 4 lanes of each query, then Oᵀ tile ot holds dims 16·ot + 4g + v.
-  l += __shfl_xor(l, 16, 64);
-  l += __shfl_xor(l, 32, 64);
+  l = xlane::bit5(xlane::bit4(l, xlane::Add{}), xlane::Add{});
   if (qi >= t) return;
   if (ns > 1) {  // partial output: unnormalized O, and (m, l) of this key run (m in natural-log units)
     const int batch = gridDim.z / ns;

@@ -13,6 +13,7 @@
 #include <cstdio>
 
 #include "internal.h"
+#include "xlane.h"
 
 namespace {
 
@@ -151,8 +152,7 @@ __global__ __launch_bounds__(256) void gemv_wave_kernel(const float *__restrict_
       const uint8_t *wr = w + (size_t)row * row_bytes;
       for (int it = lane; it < items; it += 64) s += item_dot<WT, PAIR>(wr, it, as);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    s = xlane::wave_sum(s);
     if (lane == 0) {
       float *cp = c + offset + row;
       *cp = epilogue(epi, alpha, s + bias[row], *cp);
@@ -205,11 +205,7 @@ constexpr int GV_STAGE = 16384;  // bytes per stage (whole DMA instructions of 1
 // block pair, or 64 F16 weights) of one row of the stage from LDS, `a` from LDS, and sums the
 // products in f32 (per block Σ q·a, then × d, as gemm.wgsl:244-262); a row's items are summed in
 // order through LDS.  W is not rounded (Pass::gemv semantics).
-__device__ __forceinline__ float gv_wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ __forceinline__ float gv_wave_sum(float v) { return xlane::wave_sum(v); }
 
 template <int WT, bool D16>
 __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
@@ -547,16 +543,14 @@ __global__ __launch_bounds__(KEYS) void attend_kernel(const float *__restrict__ 
     if (i < pairs) acc += qs[2 * i] * half_bits(ku[i] & 0xffffu) + qs[2 * i + 1] * half_bits(ku[i] >> 16);
   const float x = tid < cnt ? acc * scale : -INFINITY;
   float m = x;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  m = xlane::wave_max(m);
   if (lane == 0) red[wave] = m;
   __syncthreads();
   m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float e = tid < cnt ? __expf(x - m) : 0.0f;
   p[tid] = e;
   float l = e;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
+  l = xlane::wave_sum(l);
   if (lane == 0) red[4 + wave] = l;
   __syncthreads();
   l = red[4] + red[5] + red[6] + red[7];

@@ -17,6 +17,7 @@
 #include <cfloat>
 
 #include "internal.h"
+#include "xlane.h"
 
 namespace {
 
@@ -121,37 +122,6 @@ struct Half {
 template <int WT>
 constexpr int rows_per_wave() { return WT == WH_F32 ? 4 : 8; }
 
-// Cross-lane steps of the wave reductions, on the VALU instead of the LDS crossbar (__shfl_xor is a
-// ds_bpermute, ~100 cycles of latency per dependent step): DPP moves within rows of 16 lanes, and
-// gfx950's row swaps across them.
-constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1, 0, 3, 2]: lane ^ 1
-constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2, 3, 0, 1]: lane ^ 2
-constexpr int DPP_ROR8 = 0x128;        // row_ror:8: lane ^ 8
-constexpr int DPP_HALF_MIRROR = 0x141; // lane i of 8 from lane 7 − i
-constexpr int DPP_MIRROR = 0x140;      // lane i of 16 from lane 15 − i
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
-
-// v_permlane32_swap: x becomes (x of lanes 0..31 | y of lanes 0..31), y (x of lanes 32..63 | y of
-// lanes 32..63).  With x, y a lane's two values, x + y is then, in lanes 0..31, x plus the partner
-// lane's (l + 32) x, and in lanes 32..63 y plus the partner's (l − 32) y.
-template <typename T>
-__device__ __forceinline__ void swap32(T &x, T &y) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, y), false, false);
-  x = __builtin_bit_cast(T, (unsigned)r[0]), y = __builtin_bit_cast(T, (unsigned)r[1]);
-}
-// v_permlane16_swap: x becomes rows (x0, y0, x2, y2), y rows (x1, y1, x3, y3): the same for lane bit 4.
-template <typename T>
-__device__ __forceinline__ void swap16(T &x, T &y) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, y), false, false);
-  x = __builtin_bit_cast(T, (unsigned)r[0]), y = __builtin_bit_cast(T, (unsigned)r[1]);
-}
-
 // Sums each of the N = 4 or 8 values of every lane over the wavefront; afterwards lanes 64·v/N ..
 // 64·(v + 1)/N − 1 hold value v's sum.  Each halving step pairs a lane with the one that differs in
 // a lane bit (5, 4, then 3 for N = 8) and leaves it half its values (the upper half where the bit is
@@ -165,27 +135,27 @@ __device__ __forceinline__ float wave_sums(float (&v)[N]) {
 #pragma unroll
   for (int i = 0; i < N / 2; i++) {
     float x = c[i], y = c[N / 2 + i];
-    swap32(x, y);
+    xlane::swap32(x, y);
     c[i] = x + y;
   }
 #pragma unroll
   for (int i = 0; i < N / 4; i++) {
     float x = c[i], y = c[N / 4 + i];
-    swap16(x, y);
+    xlane::swap16(x, y);
     c[i] = x + y;
   }
   float s;
   if constexpr (N == 8) {
     const bool up = threadIdx.x & 8;
-    s = (up ? c[1] : c[0]) + dpp_f<DPP_ROR8>(up ? c[0] : c[1]);
+    s = (up ? c[1] : c[0]) + xlane::dpp<xlane::ROR8>(up ? c[0] : c[1]);
   } else {
     s = c[0];
   }
   // The lanes that share the value: 8 (N = 8) or 16 consecutive ones.
-  s += dpp_f<DPP_XOR1>(s);
-  s += dpp_f<DPP_XOR2>(s);
-  s += dpp_f<DPP_HALF_MIRROR>(s);
-  if constexpr (N == 4) s += dpp_f<DPP_MIRROR>(s);
+  s += xlane::dpp<xlane::XOR1>(s);
+  s += xlane::dpp<xlane::XOR2>(s);
+  s += xlane::dpp<xlane::HALF_MIRROR>(s);
+  if constexpr (N == 4) s += xlane::dpp<xlane::MIRROR>(s);
   return s;
 }
 
@@ -197,18 +167,18 @@ __device__ __forceinline__ void take_first_max(float &v, int &i, float ov, int o
 
 // The first maximum of every lane's (v, i) over the wavefront, in every lane.
 __device__ __forceinline__ void wave_first_max(float &v, int &i) {
-  take_first_max(v, i, dpp_f<DPP_XOR1>(v), dpp_i<DPP_XOR1>(i));
-  take_first_max(v, i, dpp_f<DPP_XOR2>(v), dpp_i<DPP_XOR2>(i));
-  take_first_max(v, i, dpp_f<DPP_HALF_MIRROR>(v), dpp_i<DPP_HALF_MIRROR>(i));
-  take_first_max(v, i, dpp_f<DPP_MIRROR>(v), dpp_i<DPP_MIRROR>(i));
+  take_first_max(v, i, xlane::dpp<xlane::XOR1>(v), xlane::dpp<xlane::XOR1>(i));
+  take_first_max(v, i, xlane::dpp<xlane::XOR2>(v), xlane::dpp<xlane::XOR2>(i));
+  take_first_max(v, i, xlane::dpp<xlane::HALF_MIRROR>(v), xlane::dpp<xlane::HALF_MIRROR>(i));
+  take_first_max(v, i, xlane::dpp<xlane::MIRROR>(v), xlane::dpp<xlane::MIRROR>(i));
   // Rows: after a swap both registers hold a pair of row results, the same pair for both rows.
   float x = v, y = v;
   int a = i, b = i;
-  swap16(x, y), swap16(a, b);
+  xlane::swap16(x, y), xlane::swap16(a, b);
   v = x, i = a;
   take_first_max(v, i, y, b);
   x = v, y = v, a = i, b = i;
-  swap32(x, y), swap32(a, b);
+  xlane::swap32(x, y), xlane::swap32(a, b);
   v = x, i = a;
   take_first_max(v, i, y, b);
 }

@@ -2,25 +2,17 @@
 // LayerNorm (+RoPE), im2col, the Conformer conv module's middle (GLU, depthwise conv, norm, SiLU),
 // Parakeet's 3×3 stride-2 subsampling convs and flatten, argmax, and fills.  Semantics follow
 // src/gpu/ops.wgsl and src/gpu/spatial.wgsl (cited per kernel); the layout is one wavefront per row
-// (64 lanes over the channels, reductions by cross-lane shuffles) instead of a 256-thread
+// (64 lanes over the channels, reductions across the lanes) instead of a 256-thread
 // workgroup per row, so a row's data stays in registers and short rows keep every lane busy.
 #include <algorithm>
 
 #include "internal.h"
+#include "xlane.h"
 
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
+using xlane::wave_max;
+using xlane::wave_sum;
 
 constexpr int ROW_REGS = 32;  // row values per lane held in registers: rows up to 2048
 

@@ -242,20 +242,38 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
 #pragma unroll
   for (int i = 0; i < GV_NS - 1; i++)
     if (s0 + i < s1) issue(s0 + i);
-  // `a` (and the norm's g, b) into LDS.  Every load of a thread is issued before any is used, so the
-  // prologue costs one round trip (with the first stages' DMA), not one per loop iteration.
+  // `a` (and the norm's g, b) into LDS.  Every load is issued before any is used, wavefront 0's loads
+  // for the norm's statistics with the rest and all from clamped addresses (a load behind a branch
+  // waits there), so the prologue costs one round trip, with the first stages' DMA.
   const int q4 = P.k / 4;
-  const bool vec = ((uintptr_t)P.a % 16 == 0) && q4 <= 16 * 256;
+  constexpr int AV = 8;  // float4 of `a` per thread on the vector path: k ≤ 8192
+  const bool vec = ((uintptr_t)P.a % 16 == 0) && q4 <= AV * 256;
+  const float4 *a4 = (const float4 *)P.a;
+  float4 av[AV], gv[AV], bv[AV];
+  if (vec) {
+#pragma unroll
+    for (int t = 0; t < AV; t++)
+      if (256 * t < q4) {  // uniform: only the rounds that hold part of the row
+        const int i = min(tid + 256 * t, q4 - 1);
+        av[t] = a4[i];
+        if (P.ln_g) gv[t] = ((const float4 *)P.ln_g)[i], bv[t] = ((const float4 *)P.ln_b)[i];
+      }
+  }
   __shared__ float stat[2];
   if (P.ln_g && wave == 0) {
     // The norm before this product, with layer_norm_kernel's arithmetic (one wave sums in the same
     // order, zeros past the row), so the normalized row equals the standalone kernel's bit for bit.
-    const float4 *a4 = (const float4 *)P.a;
     float sm = 0.0f, q = 0.0f, mean;
     if (q4 <= 16 * 64) {
       float4 v[16];
 #pragma unroll
-      for (int t = 0; t < 16; t++) v[t] = lane + 64 * t < q4 ? a4[lane + 64 * t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      for (int t = 0; t < 16; t++) {
+        v[t] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (64 * t < q4) {  // uniform
+          const float4 x = a4[min(lane + 64 * t, q4 - 1)];
+          if (lane + 64 * t < q4) v[t] = x;
+        }
+      }
 #pragma unroll
       for (int t = 0; t < 16; t++) sm += (v[t].x + v[t].y) + (v[t].z + v[t].w);
       mean = gv_wave_sum(sm) / (float)P.k;
@@ -281,19 +299,12 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
     if (lane == 0) stat[0] = mean, stat[1] = rstd;
   }
   if (vec) {
-    const float4 *a4 = (const float4 *)P.a;
-    float4 av[16], gv[16], bv[16];
-#pragma unroll
-    for (int t = 0; t < 16; t++) {
-      const int i = tid + 256 * t;
-      av[t] = i < q4 ? a4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (P.ln_g && i < q4) gv[t] = ((const float4 *)P.ln_g)[i], bv[t] = ((const float4 *)P.ln_b)[i];
-    }
     if (P.ln_g) {
       __syncthreads();  // the norm's statistics
       const float mean = stat[0], rstd = stat[1];
 #pragma unroll
-      for (int t = 0; t < 16; t++) {
+      for (int t = 0; t < AV; t++) {
+        if (256 * t >= q4) break;
         av[t].x = (av[t].x - mean) * rstd * gv[t].x + bv[t].x;
         av[t].y = (av[t].y - mean) * rstd * gv[t].y + bv[t].y;
         av[t].z = (av[t].z - mean) * rstd * gv[t].z + bv[t].z;
@@ -301,9 +312,11 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
       }
     }
 #pragma unroll
-    for (int t = 0; t < 16; t++) {
-      const int i = tid + 256 * t;  // float4 i: elements 4i .. 4i + 3 of item 4i / 64
-      if (i < q4) *(float4 *)(as + (i >> 4) * AS + 4 * (i & 15)) = av[t];
+    for (int t = 0; t < AV; t++) {
+      if (256 * t >= q4) break;
+      // float4 i: elements 4i .. 4i + 3 of item 4i / 64 (threads past the row store the last one again)
+      const int i = min(tid + 256 * t, q4 - 1);
+      *(float4 *)(as + (i >> 4) * AS + 4 * (i & 15)) = av[t];
     }
   } else {
     if (P.ln_g) __syncthreads();

@@ -245,6 +245,14 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
   // `a` (and the norm's g, b) into LDS.  Every load is issued before any is used, wavefront 0's loads
   // for the norm's statistics with the rest and all from clamped addresses (a load behind a branch
   // waits there), so the prologue costs one round trip, with the first stages' DMA.
+  // The epilogue's bias and output (residual modes) of this thread's first row and the cache column,
+  // loaded with the prologue's loads (pinned below, where the prologue waits anyway) instead of after
+  // the streaming loop.
+  const int r0 = s0 * P.rps, r1 = min(s1 * P.rps, P.rows);
+  const bool res = P.epi == WH_RESIDUAL || P.epi == WH_GELU_RESIDUAL;
+  const int er = min(r0 + tid, P.rows - 1);
+  const float eb = P.bias[er], ec = res ? P.c[P.offset + er] : 0.0f;
+  const int pcol = P.pack.dcol ? *P.pack.dcol : P.pack.col;  // the cache column (the step's position)
   const int q4 = P.k / 4;
   constexpr int AV = 8;  // float4 of `a` per thread on the vector path: k ≤ 8192
   const bool vec = ((uintptr_t)P.a % 16 == 0) && q4 <= AV * 256;
@@ -324,6 +332,7 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
     for (int i = tid; i < P.k; i += 256)
       as[(i >> 6) * AS + (i & 63)] = P.ln_g ? (P.a[i] - mean) * rstd * P.ln_g[i] + P.ln_b[i] : P.a[i];
   }
+  asm volatile("" : : "v"(eb), "v"(ec), "v"(pcol));
   const int row_l = tid / items, it = tid % items;
   for (int s = s0; s < s1; s++) {
     if (s + GV_NS - 2 < s1) gv_wait_vm<(GV_NS - 2) * PER>();
@@ -403,12 +412,10 @@ __global__ __launch_bounds__(256) void gemv_stream_kernel(GemvArgs P) {
     rsum[j] = acc;
   }
   __syncthreads();
-  const int r0 = s0 * P.rps, r1 = min(s1 * P.rps, P.rows);
-  const bool res = P.epi == WH_RESIDUAL || P.epi == WH_GELU_RESIDUAL;
-  const int pcol = P.pack.dcol ? *P.pack.dcol : P.pack.col;
   for (int row = r0 + tid; row < r1; row += 256) {
     float *cp = P.c + P.offset + row;
-    const float v = epilogue(P.epi, P.alpha, rsum[row - r0] + P.bias[row], res ? *cp : 0.0f);
+    const bool first = row == r0 + tid;
+    const float v = epilogue(P.epi, P.alpha, rsum[row - r0] + (first ? eb : P.bias[row]), res ? (first ? ec : *cp) : 0.0f);
     *cp = v;
     const int x = row - P.pack.lo;  // the cache's K then V values: pair x / 2, half x % 2 of launch_pack
     if (P.pack.cache && x >= 0 && x < 2 * P.pack.d && pcol < P.pack.cols) {

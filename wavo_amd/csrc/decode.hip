@@ -623,10 +623,42 @@ __global__ __launch_bounds__(KEYS) void attend_kernel(const float *__restrict__ 
 }
 
 // Per head, the parts of attend_kernel rescaled to their common maximum, summed and normalized
-// (decode.wgsl:121-147).
+// (decode.wgsl:121-147).  Up to CP parts (the 1500-frame cross attention has 6) and 128 dimensions,
+// every part's values are loaded first (clamped: one round trip, not one per part and pass), then
+// combined in the order of the general loop below, so both give the same bits.
+constexpr int CP = 8;
 __global__ void combine_kernel(const float *__restrict__ part, float *__restrict__ o, int n, int hd) {
   const int parts = (n + KEYS - 1) / KEYS;
   const float *base = part + (size_t)blockIdx.x * parts * (hd + 2);
+  if (parts <= CP && hd <= 2 * 64 && blockDim.x == 64) {
+    const int tid = threadIdx.x;
+    float pm[CP], pl[CP], pv[CP][2];
+#pragma unroll
+    for (int c = 0; c < CP; c++) {
+      const float *bc = base + min(c, parts - 1) * (hd + 2);
+      pm[c] = bc[hd], pl[c] = bc[hd + 1];
+#pragma unroll
+      for (int j = 0; j < 2; j++) pv[c][j] = bc[min(tid + 64 * j, hd - 1)];
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < CP; c++)
+      if (c < parts) m = fmaxf(m, pm[c]);
+    float l = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CP; c++)
+      if (c < parts) l += __expf(pm[c] - m) * pl[c];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int i = tid + 64 * j;
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CP; c++)
+        if (c < parts) acc += __expf(pm[c] - m) * pv[c][j];
+      if (i < hd) o[blockIdx.x * hd + i] = acc / l;
+    }
+    return;
+  }
   float m = -INFINITY;
   for (int c = 0; c < parts; c++) m = fmaxf(m, base[c * (hd + 2) + hd]);
   float l = 0.0f;

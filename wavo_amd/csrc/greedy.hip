@@ -35,12 +35,7 @@ __device__ __forceinline__ void wg_argmax(const float *__restrict__ x, int n, fl
     const float y = x[j];
     if (bi == n || better(y, j, bv, bi)) bv = y, bi = j;
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o, 64);
-    const int oi = __shfl_xor(bi, o, 64);
-    if (oi < n && (bi == n || better(ov, oi, bv, bi))) bv = ov, bi = oi;
-  }
+  xlane::wave_first_max(bv, bi, [n](float ov, int oi, float v, int i) { return oi < n && (i == n || better(ov, oi, v, i)); });
   if ((tid & 63) == 0) sv[tid >> 6] = bv, si[tid >> 6] = bi;
   __syncthreads();
   v = sv[0], i = si[0];
@@ -159,28 +154,9 @@ __device__ __forceinline__ float wave_sums(float (&v)[N]) {
   return s;
 }
 
-// (v, i) becomes the first maximum of itself and (ov, oi): the greater value, or an equal one at the
-// smaller index; index −1 is none.
-__device__ __forceinline__ void take_first_max(float &v, int &i, float ov, int oi) {
-  if (oi >= 0 && (i < 0 || better(ov, oi, v, i))) v = ov, i = oi;
-}
-
-// The first maximum of every lane's (v, i) over the wavefront, in every lane.
+// The first maximum of every lane's (v, i) over the wavefront, in every lane; index −1 is none.
 __device__ __forceinline__ void wave_first_max(float &v, int &i) {
-  take_first_max(v, i, xlane::dpp<xlane::XOR1>(v), xlane::dpp<xlane::XOR1>(i));
-  take_first_max(v, i, xlane::dpp<xlane::XOR2>(v), xlane::dpp<xlane::XOR2>(i));
-  take_first_max(v, i, xlane::dpp<xlane::HALF_MIRROR>(v), xlane::dpp<xlane::HALF_MIRROR>(i));
-  take_first_max(v, i, xlane::dpp<xlane::MIRROR>(v), xlane::dpp<xlane::MIRROR>(i));
-  // Rows: after a swap both registers hold a pair of row results, the same pair for both rows.
-  float x = v, y = v;
-  int a = i, b = i;
-  xlane::swap16(x, y), xlane::swap16(a, b);
-  v = x, i = a;
-  take_first_max(v, i, y, b);
-  x = v, y = v, a = i, b = i;
-  xlane::swap32(x, y), xlane::swap32(a, b);
-  v = x, i = a;
-  take_first_max(v, i, y, b);
+  xlane::wave_first_max(v, i, [](float ov, int oi, float bv, int bi) { return oi >= 0 && (bi < 0 || better(ov, oi, bv, bi)); });
 }
 
 // ------------------------------------------------------------------ weight rows staged through LDS
@@ -769,8 +745,9 @@ constexpr int WR_THREADS = 256, WR_IDS = 4 * WR_THREADS, WP_PARTS = 64;  // voca
 __device__ __forceinline__ float lane4(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
 
 // (value, id) pairs: the greater value, the lower id among equals (the first maximum).
+__device__ __forceinline__ bool first_max_better(float ov, int oi, float v, int i) { return ov > v || (ov == v && oi < i); }
 __device__ __forceinline__ void first_max(float &v, int &i, float ov, int oi) {
-  if (ov > v || (ov == v && oi < i)) v = ov, i = oi;
+  if (first_max_better(ov, oi, v, i)) v = ov, i = oi;
 }
 
 // The state's view of the rules: which ids die.
@@ -798,9 +775,7 @@ __device__ __forceinline__ Rules rules_of(const WhisperPickArgs &a, int n, int l
 template <int N>
 __device__ __forceinline__ void block_max(float (&v)[N], float *red) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1)
-#pragma unroll
-    for (int t = 0; t < N; t++) v[t] = fmaxf(v[t], __shfl_xor(v[t], o, 64));
+  for (int t = 0; t < N; t++) v[t] = xlane::wave_max(v[t]);
   __syncthreads();
   if ((threadIdx.x & 63) == 0)
 #pragma unroll
@@ -844,11 +819,8 @@ __global__ __launch_bounds__(WR_THREADS) void whisper_rules_kernel(WhisperPickAr
     if (v[e] > bv) bv = v[e], bi = i;
     if (ts && i < vocab && (ti == INT_MAX || v[e] > tv)) tv = v[e], ti = i;
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    first_max(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
-    first_max(tv, ti, __shfl_xor(tv, o, 64), __shfl_xor(ti, o, 64));
-  }
+  xlane::wave_first_max(bv, bi, first_max_better);
+  xlane::wave_first_max(tv, ti, first_max_better);
   if ((tid & 63) == 0) redv[tid >> 6] = bv, redi[tid >> 6] = bi, redv[4 + (tid >> 6)] = tv, redi[4 + (tid >> 6)] = ti;
   block_max(mx, redf);
   // The sums against this workgroup's maxima.
@@ -858,8 +830,7 @@ __global__ __launch_bounds__(WR_THREADS) void whisper_rules_kernel(WhisperPickAr
     if (i0 + e >= r.begin && isfinite(v[e])) s[0] += exp((double)(v[e] - mx[0]));
     if (logprobs && isfinite(v[e])) s[1] += exp((double)(v[e] - mx[2]));
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) s[0] += __shfl_xor(s[0], o, 64), s[1] += __shfl_xor(s[1], o, 64);
+  s[0] = xlane::wave_sum(s[0]), s[1] = xlane::wave_sum(s[1]);
   if ((tid & 63) == 0) redd[tid >> 6] = s[0], redd[4 + (tid >> 6)] = s[1];
   __syncthreads();
   if (tid != 0) return;
@@ -880,23 +851,14 @@ __global__ __launch_bounds__(64) void whisper_pick_kernel(WhisperPickArgs a, int
   const bool mine = lane < parts;
   // The common maxima, then the sums rescaled to them.
   float tmax = mine ? p.tmax : -INFINITY, text = mine ? p.text : -INFINITY, fmx = mine ? p.fmax : -INFINITY;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    tmax = fmaxf(tmax, __shfl_xor(tmax, o, 64));
-    text = fmaxf(text, __shfl_xor(text, o, 64));
-    fmx = fmaxf(fmx, __shfl_xor(fmx, o, 64));
-  }
+  tmax = xlane::wave_max(tmax), text = xlane::wave_max(text), fmx = xlane::wave_max(fmx);
   double s_ts = mine && isfinite(p.tmax) ? p.s_ts * exp((double)p.tmax - (double)tmax) : 0.0;
   double s_all = mine && isfinite(p.fmax) ? p.s_all * exp((double)p.fmax - (double)fmx) : 0.0;
   float bv = mine ? p.best_v : -INFINITY, tv = mine ? p.ts_v : -INFINITY;
   int bi = mine ? p.best_i : INT_MAX, ti = mine ? p.ts_i : INT_MAX;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    s_ts += __shfl_xor(s_ts, o, 64);
-    s_all += __shfl_xor(s_all, o, 64);
-    first_max(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
-    first_max(tv, ti, __shfl_xor(tv, o, 64), __shfl_xor(ti, o, 64));
-  }
+  s_ts = xlane::wave_sum(s_ts), s_all = xlane::wave_sum(s_all);
+  xlane::wave_first_max(bv, bi, first_max_better);
+  xlane::wave_first_max(tv, ti, first_max_better);
   if (lane != 0) return;
   // The timestamps' total probability against the best text token (src/whisper/search.rs:99-110);
   // when it wins, the text dies and the first maximum is over the timestamps.

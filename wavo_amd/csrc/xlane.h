@@ -23,6 +23,13 @@ __device__ __forceinline__ float dpp(float v) {
 }
 template <int CTRL>
 __device__ __forceinline__ int dpp(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false); }
+template <int CTRL>
+__device__ __forceinline__ double dpp(double v) {  // both halves
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+  const int lo = __builtin_amdgcn_mov_dpp((int)(unsigned)u, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(unsigned)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, (unsigned long long)(unsigned)lo | ((unsigned long long)(unsigned)hi << 32));
+}
 
 // v_permlane32_swap: x becomes (x of lanes 0..31 | y of lanes 0..31), y (x of lanes 32..63 | y of
 // lanes 32..63).  With x = y = a lane's value, every lane then holds its own value and that of lane
@@ -39,25 +46,40 @@ __device__ __forceinline__ void swap16(T &x, T &y) {
   const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, x), __builtin_bit_cast(unsigned, y), false, false);
   x = __builtin_bit_cast(T, (unsigned)r[0]), y = __builtin_bit_cast(T, (unsigned)r[1]);
 }
+// The same for 64-bit values, half by half.
+__device__ __forceinline__ void swap32(double &x, double &y) {
+  unsigned long long u = __builtin_bit_cast(unsigned long long, x), w = __builtin_bit_cast(unsigned long long, y);
+  unsigned xl = (unsigned)u, xh = (unsigned)(u >> 32), yl = (unsigned)w, yh = (unsigned)(w >> 32);
+  swap32(xl, yl), swap32(xh, yh);
+  x = __builtin_bit_cast(double, (unsigned long long)xl | ((unsigned long long)xh << 32));
+  y = __builtin_bit_cast(double, (unsigned long long)yl | ((unsigned long long)yh << 32));
+}
+__device__ __forceinline__ void swap16(double &x, double &y) {
+  unsigned long long u = __builtin_bit_cast(unsigned long long, x), w = __builtin_bit_cast(unsigned long long, y);
+  unsigned xl = (unsigned)u, xh = (unsigned)(u >> 32), yl = (unsigned)w, yh = (unsigned)(w >> 32);
+  swap16(xl, yl), swap16(xh, yh);
+  x = __builtin_bit_cast(double, (unsigned long long)xl | ((unsigned long long)xh << 32));
+  y = __builtin_bit_cast(double, (unsigned long long)yl | ((unsigned long long)yh << 32));
+}
 
 // op(v, v of lane l ^ 32) and op(v, v of lane l ^ 16), for a commutative op.
-template <class Op>
-__device__ __forceinline__ float bit5(float v, Op op) {
-  float x = v, y = v;
+template <typename T, class Op>
+__device__ __forceinline__ T bit5(T v, Op op) {
+  T x = v, y = v;
   swap32(x, y);
   return op(x, y);
 }
-template <class Op>
-__device__ __forceinline__ float bit4(float v, Op op) {
-  float x = v, y = v;
+template <typename T, class Op>
+__device__ __forceinline__ T bit4(T v, Op op) {
+  T x = v, y = v;
   swap16(x, y);
   return op(x, y);
 }
 
 // The xor butterfly over all six lane bits.  Bits 2 .. 0 after bits 5 .. 3: lane + 4 within the row
 // differs from lane ^ 4 only in bit 3, whose lanes hold equal values by then.
-template <class Op>
-__device__ __forceinline__ float butterfly(float v, Op op) {
+template <typename T, class Op>
+__device__ __forceinline__ T butterfly(T v, Op op) {
   v = bit5(v, op);
   v = bit4(v, op);
   v = op(v, dpp<ROR8>(v));
@@ -67,7 +89,8 @@ __device__ __forceinline__ float butterfly(float v, Op op) {
 }
 
 struct Add {
-  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+  template <typename T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
 };
 struct Max {
   __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
@@ -75,6 +98,31 @@ struct Max {
 
 // The sum and the maximum over the wavefront, in every lane.
 __device__ __forceinline__ float wave_sum(float v) { return butterfly(v, Add{}); }
+__device__ __forceinline__ double wave_sum(double v) { return butterfly(v, Add{}); }
 __device__ __forceinline__ float wave_max(float v) { return butterfly(v, Max{}); }
+
+// The first maximum of every lane's (v, i) (the greater value, or an equal one at the smaller index;
+// i < 0 or better() false: none) over the wavefront, in every lane.  A selection by a total order: the
+// result does not depend on the order in which lanes meet (values that are NaN aside).
+template <class Better>
+__device__ __forceinline__ void wave_first_max(float &v, int &i, Better better) {
+  auto take = [&](float ov, int oi) {
+    if (better(ov, oi, v, i)) v = ov, i = oi;
+  };
+  take(dpp<XOR1>(v), dpp<XOR1>(i));
+  take(dpp<XOR2>(v), dpp<XOR2>(i));
+  take(dpp<HALF_MIRROR>(v), dpp<HALF_MIRROR>(i));
+  take(dpp<MIRROR>(v), dpp<MIRROR>(i));
+  // Rows: after a swap both registers hold a pair of row results, the same pair for both rows.
+  float x = v, y = v;
+  int a = i, b = i;
+  swap16(x, y), swap16(a, b);
+  v = x, i = a;
+  take(y, b);
+  x = v, y = v, a = i, b = i;
+  swap32(x, y), swap32(a, b);
+  v = x, i = a;
+  take(y, b);
+}
 
 }  // namespace xlane

@@ -338,7 +338,7 @@ def other_configs(gpu, model, reps=10):
     return out
 
 
-def decode_steps(gpu, tokens=224):
+def decode_steps(gpu, tokens=224, search=True):
     """Whisper-large-v3-turbo-shaped decoder steps (4 layers, d 1280, 20 heads, 51866-token head, cross
     attention over 1500 encoder frames, q8_0), `tokens` steps back to back after one warm-up pass."""
     import numpy as np
@@ -368,6 +368,12 @@ def decode_steps(gpu, tokens=224):
         state["pos"] += 1
 
     ms = time_region(gpu, one, tokens)
+    if not search:
+        m.free()
+        return {"workload": f"whisper-large-v3-turbo-shaped decoder step (4 layers, d {d}, {cfg['dec_heads']} heads, "
+                            f"{vocab}-token head, cross attention over {frames} frames, q8_0), {tokens} steps back to "
+                            "back, one recorded pass per step",
+                "us_per_token": round(ms * 1e3, 2), "tokens_per_s": round(1e3 / ms, 1), "window_search": None}
     # One window's search (wh_whisper_decode over the same encoder output, SOT prompt): picks on the
     # device against every step's logits read back and picked on the host; host clock, median of 5
     # after 2 warm-ups.
@@ -526,6 +532,7 @@ def main():
     ap.add_argument("--no-gemv", action="store_true", help="skip the decoder GEMV and decoder step measurements")
     ap.add_argument("--no-configs", action="store_true", help="skip the encoder timings of the other BASELINE configs")
     ap.add_argument("--no-decode", action="store_true", help="skip the TDT decode and audio-to-tokens timings")
+    ap.add_argument("--no-search", action="store_true", help="skip the Whisper window search after the decoder steps")
     ap.add_argument("--replay", metavar="NAME", default=None,
                     help="only the back-to-back launches of this GEMM configuration (a roofline.kernel value), "
                          "or 'attention_rel' for the Parakeet attention call, for rocprofv3 passes over exactly "
@@ -647,11 +654,11 @@ def main():
     if gemv:
         log(f"GEMV per token {gemv['us_per_token']} us, {gemv['achieved']} GB/s ({gemv['frac'] * 100:.1f}% of HBM); "
             f"kernels {gemv['kernel_frac'] * 100:.1f}%; head {gemv.get('head', {}).get('frac', 0) * 100:.1f}%")
-        gemv["decode_step"] = decode_steps(gpu)
+        gemv["decode_step"] = decode_steps(gpu, search=not args.no_search)
         ws = gemv["decode_step"]["window_search"]
-        log(f"decoder step {gemv['decode_step']['us_per_token']} us per token; window search {ws['ids']} ids: device "
-            f"{ws['device_ms']} ms ({ws['device_us_per_id']} us/id), host picks {ws['host_ms']} ms "
-            f"({ws['host_us_per_id']} us/id), {'equal' if ws['equal'] else 'different'}")
+        log(f"decoder step {gemv['decode_step']['us_per_token']} us per token" + ("" if not ws else
+            f"; window search {ws['ids']} ids: device {ws['device_ms']} ms ({ws['device_us_per_id']} us/id), host "
+            f"picks {ws['host_ms']} ms ({ws['host_us_per_id']} us/id), {'equal' if ws['equal'] else 'different'}"))
 
     others = None if args.no_configs else other_configs(gpu, model)
     if others:

@@ -183,10 +183,12 @@ __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__
       float4 v = make_float4(0, 0, 0, 0);
       if (on && src >= 0 && src < lim) {
         const float4 x = xs[r], gt = gs[r];
-        v.x = x.x / (1.0f + __expf(-gt.x));
-        v.y = x.y / (1.0f + __expf(-gt.y));
-        v.z = x.z / (1.0f + __expf(-gt.z));
-        v.w = x.w / (1.0f + __expf(-gt.w));
+        // GLU: a·σ(b), σ by the hardware reciprocal (1 ulp) as a·(1 / (1 + e^−b)), the reference's two
+        // roundings, instead of an IEEE division (~10 instructions) on every input frame of the span.
+        v.x = x.x * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.x));
+        v.y = x.y * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.y));
+        v.z = x.z * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.z));
+        v.w = x.w * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.w));
       }
       // Output frame i takes tap k = r − i.
 #pragma unroll
@@ -244,10 +246,10 @@ __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__
     v.y = (acc[i].y - mean[i]) * rstd[i] * gg.y + bb.y;
     v.z = (acc[i].z - mean[i]) * rstd[i] * gg.z + bb.z;
     v.w = (acc[i].w - mean[i]) * rstd[i] * gg.w + bb.w;
-    v.x = v.x / (1.0f + __expf(-v.x));
-    v.y = v.y / (1.0f + __expf(-v.y));
-    v.z = v.z / (1.0f + __expf(-v.z));
-    v.w = v.w / (1.0f + __expf(-v.w));
+    v.x = v.x * __builtin_amdgcn_rcpf(1.0f + __expf(-v.x));  // SiLU, as the GLU above
+    v.y = v.y * __builtin_amdgcn_rcpf(1.0f + __expf(-v.y));
+    v.z = v.z * __builtin_amdgcn_rcpf(1.0f + __expf(-v.z));
+    v.w = v.w * __builtin_amdgcn_rcpf(1.0f + __expf(-v.w));
     store4(y + ((size_t)seg * t + f) * ch + c, v);
   }
 }

@@ -132,7 +132,7 @@ __global__ void im2col_kernel(const float *__restrict__ x, float *__restrict__ c
 // frames of one window with one thread per 4 channels: each thread slides over the CF + kernel − 1
 // frames its outputs need, keeping their GLU values and its 4·kernel taps in registers (the taps of
 // 4 channels are 4·kernel consecutive floats), so h is read once per workgroup plus the kernel − 1
-// frames of overlap.  The norm's row sums go through the wavefront shuffles and LDS.  Frames are
+// frames of overlap.  The norm's row sums go through wavefront reductions and LDS.  Frames are
 // [batch][t]; the conv does not cross windows.  OT = float, or _Float16 for a consumer GEMM.
 constexpr int CF = 4;  // 4 frames per workgroup: a 750-frame window spreads over 188 CUs
 constexpr int CG_MAXK = 31;

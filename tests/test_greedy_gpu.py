@@ -65,6 +65,16 @@ def test_tdt_two_layers(gpu, wtype):
         assert len(trace) > 64  # more than two recorded runs of decisions
 
 
+def test_tdt_f32_wide(gpu):
+    """F32 weights at the C1 decoder's widths (hidden 640, joint 640): a workgroup's weight rows no longer
+    fit one 32 KiB staging round (the joint's 16 rows of 2560 bytes, each LSTM gate's 4 rows of 5120
+    bytes), so the later rounds of the copy into LDS run, for both LSTM layers."""
+    path = decoder_model(gguf.F32, hidden=640, joint=640)
+    om, m = ox.Model(path), wa.Model(gpu, path)
+    for frames, seed in ((300, 4), (120, 5)):
+        check(gpu, m, om, random_enc(frames, 640, seed))
+
+
 def test_tdt_blanks_and_symbol_limit(gpu):
     """A decoder that emits blanks about half the time (decisions whose predictor launches are switched
     off), with a per-frame limit of two symbols over durations {0, 1, 2}: emissions at duration 0, and

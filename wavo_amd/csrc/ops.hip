@@ -288,9 +288,26 @@ __global__ void first_depthwise_kernel(const float *__restrict__ x, const float 
   const int t1 = half_len(t), f1 = half_len(f), f2 = half_len(f1);
   const int r = 2 * t0 + blockIdx.y;  // output row + 1
   const int pw = 4 * f2 + 3;
-  for (int e = threadIdx.x; e < 7 * pw; e += blockDim.x) {
-    const int tm = 4 * r + e / pw - 7, fm = e % pw - 3;
-    xs[e] = (tm >= 0 && tm < t && fm >= 0 && fm < f) ? x[(size_t)tm * f + fm] : 0.0f;
+  // The patch: every load of a thread issued before its stores (one round trip, not one per element
+  // group), from clamped addresses, for the first 8 groups of blockDim.x elements (the whole patch of
+  // 128 mel bins with 256 threads); any rest by the loop after.
+  {
+    constexpr int G = 8;
+    float v[G];
+#pragma unroll
+    for (int q = 0; q < G; q++) {
+      const int e = min((int)threadIdx.x + q * (int)blockDim.x, 7 * pw - 1);
+      const int tm = 4 * r + e / pw - 7, fm = e % pw - 3;
+      const bool in = tm >= 0 && tm < t && fm >= 0 && fm < f;
+      const float xv = x[in ? (size_t)tm * f + fm : 0];
+      v[q] = in ? xv : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < G; q++) xs[min((int)threadIdx.x + q * (int)blockDim.x, 7 * pw - 1)] = v[q];
+    for (int e = threadIdx.x + G * blockDim.x; e < 7 * pw; e += blockDim.x) {
+      const int tm = 4 * r + e / pw - 7, fm = e % pw - 3;
+      xs[e] = (tm >= 0 && tm < t && fm >= 0 && fm < f) ? x[(size_t)tm * f + fm] : 0.0f;
+    }
   }
   __syncthreads();
   const bool masked = r > half_len(t1);

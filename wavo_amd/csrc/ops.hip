@@ -287,7 +287,7 @@ __global__ void first_depthwise_kernel(const float *__restrict__ x, const float 
   extern __shared__ float xs[];  // 7 rows × pw columns; column 4·fo + j is input column 4·fo + j − 3
   const int t1 = half_len(t), f1 = half_len(f), f2 = half_len(f1);
   const int r = 2 * t0 + blockIdx.y;  // output row + 1
-  const int pw = 4 * f2 + 3;
+  const int pw = 4 * f2 + 4;  // the 4·f2 + 3 columns used, rows padded to 16 bytes
   // The patch: every load of a thread issued before its stores (one round trip, not one per element
   // group), from clamped addresses, for the first 8 groups of blockDim.x elements (the whole patch of
   // 128 mel bins with 256 threads); any rest by the loop after.
@@ -317,6 +317,16 @@ __global__ void first_depthwise_kernel(const float *__restrict__ x, const float 
     for (int q = 0; q < 9; q++) a[q] = w0[q * ch + c], wd[q] = w[q * ch + c];
     const float bias0 = b0[c], bias = b[c];
     for (int fo = 0; fo < f2; fo++) {
+      // The 7×7 input window of output column fo (rows 0..6, columns 4·fo .. 4·fo + 6), read as two
+      // 16-byte chunks per row (the same values in every lane: broadcast reads) instead of 81 scalars.
+      float px[7][8];
+#pragma unroll
+      for (int rr = 0; rr < 7; rr++) {
+        const float4 *row4 = (const float4 *)xs + rr * (pw / 4) + fo;  // 16-byte aligned (pw % 4 == 0)
+        const float4 c0 = row4[0], c1 = row4[1];
+        px[rr][0] = c0.x, px[rr][1] = c0.y, px[rr][2] = c0.z, px[rr][3] = c0.w;
+        px[rr][4] = c1.x, px[rr][5] = c1.y, px[rr][6] = c1.z, px[rr][7] = c1.w;
+      }
       float acc = bias;
 #pragma unroll
       for (int i = 0; i < 3; i++) {
@@ -325,17 +335,17 @@ __global__ void first_depthwise_kernel(const float *__restrict__ x, const float 
         for (int j = 0; j < 3; j++) {
           const int fi = 2 * fo + j;
           if (ti >= 1 && ti <= t1 && fi >= 1 && fi <= f1) {
-            const float *p = xs + 2 * i * pw + 4 * fo + 2 * j;
+            const int r0 = 2 * i, c = 2 * j;
             float v = bias0;
-            v += a[0] * p[0];
-            v += a[1] * p[1];
-            v += a[2] * p[2];
-            v += a[3] * p[pw];
-            v += a[4] * p[pw + 1];
-            v += a[5] * p[pw + 2];
-            v += a[6] * p[2 * pw];
-            v += a[7] * p[2 * pw + 1];
-            v += a[8] * p[2 * pw + 2];
+            v += a[0] * px[r0][c];
+            v += a[1] * px[r0][c + 1];
+            v += a[2] * px[r0][c + 2];
+            v += a[3] * px[r0 + 1][c];
+            v += a[4] * px[r0 + 1][c + 1];
+            v += a[5] * px[r0 + 1][c + 2];
+            v += a[6] * px[r0 + 2][c];
+            v += a[7] * px[r0 + 2][c + 1];
+            v += a[8] * px[r0 + 2][c + 2];
             acc += wd[i * 3 + j] * fmaxf(v, 0.0f);
           }
         }
@@ -683,7 +693,7 @@ int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *
   ProfScope prof(ctx, w0 ? "first_depthwise" : "depthwise", 0.0,
                  4.0 * rows * half_len(w0 ? half_len(f) : f) * ch * (w0 ? 1 : 4));
   if (w0) {
-    const size_t lds = sizeof(float) * 7 * (4 * (size_t)half_len(half_len(f)) + 3);
+    const size_t lds = sizeof(float) * 7 * (4 * (size_t)half_len(half_len(f)) + 4);
     if (lds > 64 * 1024) return wh_fail(ctx, WH_EARG, "depthwise: %d mel bins is more than one workgroup's patch holds", f);
     wh_launch(ctx, first_depthwise_kernel, dim3(1, rows), threads < 64 ? 64 : threads, lds, x, w, b, y, w0, b0, t, f, ch, t0);
   } else {

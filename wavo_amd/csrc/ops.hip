@@ -316,6 +316,7 @@ __global__ void first_depthwise_kernel(const float *__restrict__ x, const float 
 #pragma unroll
     for (int q = 0; q < 9; q++) a[q] = w0[q * ch + c], wd[q] = w[q * ch + c];
     const float bias0 = b0[c], bias = b[c];
+    float carry[3] = {0.0f, 0.0f, 0.0f};  // ReLU(conv0) at conv1 column 2·fo, from the previous column's j = 2
     for (int fo = 0; fo < f2; fo++) {
       // The 7×7 input window of output column fo (rows 0..6, columns 4·fo .. 4·fo + 6), read as two
       // 16-byte chunks per row (the same values in every lane: broadcast reads) instead of 81 scalars.
@@ -334,7 +335,9 @@ __global__ void first_depthwise_kernel(const float *__restrict__ x, const float 
 #pragma unroll
         for (int j = 0; j < 3; j++) {
           const int fi = 2 * fo + j;
-          if (ti >= 1 && ti <= t1 && fi >= 1 && fi <= f1) {
+          if (j == 0 && fo > 0) {  // the same conv0 value the previous column computed as its j = 2
+            if (ti >= 1 && ti <= t1 && fi >= 1 && fi <= f1) acc += wd[i * 3] * carry[i];
+          } else if (ti >= 1 && ti <= t1 && fi >= 1 && fi <= f1) {
             const int r0 = 2 * i, c = 2 * j;
             float v = bias0;
             v += a[0] * px[r0][c];
@@ -346,7 +349,9 @@ __global__ void first_depthwise_kernel(const float *__restrict__ x, const float 
             v += a[6] * px[r0 + 2][c];
             v += a[7] * px[r0 + 2][c + 1];
             v += a[8] * px[r0 + 2][c + 2];
-            acc += wd[i * 3 + j] * fmaxf(v, 0.0f);
+            const float rv = fmaxf(v, 0.0f);
+            if (j == 2) carry[i] = rv;
+            acc += wd[i * 3 + j] * rv;
           }
         }
       }

@@ -425,6 +425,16 @@ def test_relative_attention_many_splits(valid):
         g.close()
 
 
+@pytest.mark.parametrize("t,f,ch", [(7, 16, 256), (3, 8, 64), (2, 16, 128), (5, 4, 32)])
+def test_flatten_power_of_two(gpu, t, f, ch):
+    """The LDS transpose path of flatten (f and ch powers of two, f·ch ≤ 4096, as after Parakeet's
+    subsampling): a permutation, so bit for bit."""
+    x = rnd(t * f * ch, 27).reshape(t, f, ch)
+    xb, fb = gpu.upload(x), gpu.buffer(t * f * ch)
+    gpu.flatten(xb, fb, t, f, ch)
+    assert np.array_equal(gpu.read(fb, (t, f * ch)), ox.flatten(x, t, f, ch))
+
+
 @pytest.mark.parametrize("valid_drop", [0, 1])
 def test_subsampling(gpu, valid_drop):
     t, f, ch = 29, 11, 5

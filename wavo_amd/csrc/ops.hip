@@ -262,13 +262,28 @@ __global__ void depthwise_kernel(const float *__restrict__ x, const float *__res
                                  float *__restrict__ y, int t, int f, int ch, int t0) {
   const int fo = blockIdx.x, k = blockIdx.y, fh = half_len(f);
   for (int c = threadIdx.x; c < ch; c += blockDim.x) {
-    float acc = b[c];
+    // The 9 taps and inputs loaded first (clamped to an in-bounds element, unused ones skipped
+    // below): one memory round trip rather than one per tap behind its bounds test.
+    float wv[9], xv[9];
+#pragma unroll
     for (int i = 0; i < 3; i++) {
-      int ti = 2 * (t0 + k) + i;
+      const int ti = 2 * (t0 + k) + i;
+#pragma unroll
       for (int j = 0; j < 3; j++) {
-        int fi = 2 * fo + j;
-        if (ti >= 1 && ti <= t && fi >= 1 && fi <= f)
-          acc += w[(i * 3 + j) * ch + c] * x[((size_t)(2 * k + i) * f + fi - 1) * ch + c];
+        const int fi = 2 * fo + j;
+        const bool in = ti >= 1 && ti <= t && fi >= 1 && fi <= f;
+        wv[i * 3 + j] = w[(i * 3 + j) * ch + c];
+        xv[i * 3 + j] = x[in ? ((size_t)(2 * k + i) * f + fi - 1) * ch + c : (size_t)c];
+      }
+    }
+    float acc = b[c];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const int ti = 2 * (t0 + k) + i;
+#pragma unroll
+      for (int j = 0; j < 3; j++) {
+        const int fi = 2 * fo + j;
+        if (ti >= 1 && ti <= t && fi >= 1 && fi <= f) acc += wv[i * 3 + j] * xv[i * 3 + j];
       }
     }
     y[((size_t)(t0 + k) * fh + fo) * ch + c] = acc;
@@ -360,7 +375,33 @@ __global__ void first_depthwise_kernel(const float *__restrict__ x, const float 
   }
 }
 
-// [t][f][ch] → [t][ch·f] (spatial.wgsl:112-119).
+// [t][f][ch] → [t][ch·f] (spatial.wgsl:112-119), f and ch powers of two with f·ch ≤ 256·P: a frame's
+// f × ch block through LDS, read and written coalesced (the strided reads of the plain kernel below
+// touch one float per 1 KiB), every load before any store.  LDS rows are padded by 4 floats, so the
+// transposed reads of 64 lanes (16 rows × 4 columns) hit 64 distinct banks when ch % 64 == 0.
+template <int P>
+__global__ __launch_bounds__(256) void flatten_lds_kernel(const float *__restrict__ x, float *__restrict__ y, int lf,
+                                                          int lch) {
+  extern __shared__ float tl[];
+  const int n = 1 << (lf + lch), cp = (1 << lch) + 4, tid = threadIdx.x;
+  const float *xr = x + (size_t)blockIdx.x * n;
+  float *yr = y + (size_t)blockIdx.x * n;
+  float v[P];
+#pragma unroll
+  for (int q = 0; q < P; q++) v[q] = xr[min(tid + 256 * q, n - 1)];  // clamped: no branch
+#pragma unroll
+  for (int q = 0; q < P; q++) {
+    const int e = min(tid + 256 * q, n - 1);  // input element e = fi·ch + c (past n: the last again)
+    tl[(e >> lch) * cp + (e & ((1 << lch) - 1))] = v[q];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < P; q++) {
+    const int e = tid + 256 * q;  // output element e = c·f + fi
+    if (e < n) yr[e] = tl[(e & ((1 << lf) - 1)) * cp + (e >> lf)];
+  }
+}
+
 __global__ void flatten_kernel(const float *__restrict__ x, float *__restrict__ y, int f, int ch) {
   const int n = f * ch;
   const float *xr = x + (size_t)blockIdx.x * n;
@@ -712,7 +753,13 @@ int launch_flatten(wh_ctx *ctx, const float *x, float *y, int t, int f, int ch) 
   if (t < 0 || f <= 0 || ch <= 0) return wh_fail(ctx, WH_EARG, "flatten: bad shape");
   if (!t) return WH_OK;
   ProfScope prof(ctx, "flatten", 0.0, 8.0 * t * f * ch);
-  wh_launch(ctx, flatten_kernel, t, 256, 0, x, y, f, ch);
+  const bool pow2 = (f & (f - 1)) == 0 && (ch & (ch - 1)) == 0;
+  if (pow2 && (long)f * ch <= 16 * 256) {
+    const int lf = __builtin_ctz(f), lch = __builtin_ctz(ch);
+    wh_launch(ctx, flatten_lds_kernel<16>, t, 256, sizeof(float) * (size_t)f * (ch + 4), x, y, lf, lch);
+  } else {
+    wh_launch(ctx, flatten_kernel, t, 256, 0, x, y, f, ch);
+  }
   return wh_launched(ctx, "flatten");
 }
 

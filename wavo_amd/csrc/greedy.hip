@@ -113,17 +113,21 @@ struct Half {
   }
 };
 
-// Rows per wavefront in the joint's and the predictor's products.
+// Rows per wavefront in the joint's output layer (8198 rows of the C1 shape over 513 workgroups: two
+// per CU, so each wavefront's chain of products is half as long as with 8 rows).
 template <int WT>
-constexpr int rows_per_wave() { return WT == WH_F32 ? 4 : 8; }
+constexpr int rows_per_wave() { return 4; }
+// Rows per wavefront of the predictor's projection (joint outputs: 640 rows over 80 workgroups).
+template <int WT>
+constexpr int pred_rows_per_wave() { return 2; }
 
-// Sums each of the N = 4 or 8 values of every lane over the wavefront; afterwards lanes 64·v/N ..
+// Sums each of the N = 2, 4 or 8 values of every lane over the wavefront; afterwards lanes 64·v/N ..
 // 64·(v + 1)/N − 1 hold value v's sum.  Each halving step pairs a lane with the one that differs in
 // a lane bit (5, 4, then 3 for N = 8) and leaves it half its values (the upper half where the bit is
 // set) plus the partner's of the same half; then the lanes that hold the same value sum it.
 template <int N>
 __device__ __forceinline__ float wave_sums(float (&v)[N]) {
-  static_assert(N == 4 || N == 8, "4 or 8 values");
+  static_assert(N == 2 || N == 4 || N == 8, "2, 4 or 8 values");
   float c[N];
 #pragma unroll
   for (int i = 0; i < N; i++) c[i] = v[i];
@@ -146,11 +150,12 @@ __device__ __forceinline__ float wave_sums(float (&v)[N]) {
   } else {
     s = c[0];
   }
-  // The lanes that share the value: 8 (N = 8) or 16 consecutive ones.
+  // The lanes that share the value: 8 (N = 8), 16 (N = 4) or 32 (N = 2) consecutive ones.
   s += xlane::dpp<xlane::XOR1>(s);
   s += xlane::dpp<xlane::XOR2>(s);
   s += xlane::dpp<xlane::HALF_MIRROR>(s);
-  if constexpr (N == 4) s += xlane::dpp<xlane::MIRROR>(s);
+  if constexpr (N <= 4) s += xlane::dpp<xlane::MIRROR>(s);
+  if constexpr (N == 2) s = xlane::bit4(s, xlane::Add{});
   return s;
 }
 
@@ -261,6 +266,8 @@ struct Rows {
 // LDS of the joint's and the predictor's weight rows (4·RW rows per workgroup).
 template <int WT>
 __host__ __device__ constexpr int rows_cpr(size_t rb) { return run_chunks(4 * rows_per_wave<WT>() * rb); }
+template <int WT>
+__host__ __device__ constexpr int pred_rows_cpr(size_t rb) { return run_chunks(4 * pred_rows_per_wave<WT>() * rb); }
 
 // Stages n ≤ 256·P values into LDS: every load into registers first (one round trip), then the stores,
 // unconditional as the staged rows' (lanes past n write value n − 1 again).
@@ -558,14 +565,14 @@ __global__ __launch_bounds__(256) void tdt_layer_kernel(TdtArgs a, int layer) {
 // step kernel copied, and the next state becomes the current one.
 template <int WT>
 __global__ __launch_bounds__(256) void tdt_pred_kernel(TdtArgs a) {
-  constexpr int RW = rows_per_wave<WT>();
+  constexpr int RW = pred_rows_per_wave<WT>();
   extern __shared__ uint4 lds[];
   const TdtState *nx = a.nx;
   const int n = a.n, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // Everything this kernel reads goes out before the wait for the state: the weights, the new h,
   // and for this wavefront's rows the next encoder row and the current projection.
   const int g0 = blockIdx.x * 4 * RW, r0 = g0 + wave * RW, r = r0 + lane * RW / 64, rc = min(r, a.joint - 1);
-  const Runs<1> run = one_run(a.pred_w, a.pred_rb, g0, min(4 * RW, a.joint - g0), rows_cpr<WT>(a.pred_rb));
+  const Runs<1> run = one_run(a.pred_w, a.pred_rb, g0, min(4 * RW, a.joint - g0), pred_rows_cpr<WT>(a.pred_rb));
   StageRound<1> w0;
   w0.load(run, 0);
   Rows<WT, RW> rows;
@@ -674,15 +681,15 @@ static int tdt_launch_t(wh_ctx *ctx, const TdtArgs &a, int what) {
     }
     default: {
       ProfScope prof(ctx, "tdt_pred", 2.0 * a.joint * a.n, (double)a.pred_rb * a.joint);
-      const int rows = 4 * rows_per_wave<WT>();
-      wh_launch(ctx, tdt_pred_kernel<WT>, (a.joint + rows - 1) / rows, 256, 16 * (size_t)rows_cpr<WT>(a.pred_rb) + 4 * a.n, a);
+      const int rows = 4 * pred_rows_per_wave<WT>();
+      wh_launch(ctx, tdt_pred_kernel<WT>, (a.joint + rows - 1) / rows, 256, 16 * (size_t)pred_rows_cpr<WT>(a.pred_rb) + 4 * a.n, a);
       return wh_launched(ctx, "tdt pred");
     }
   }
 }
 
 int tdt_parts(int type, int out_rows) {
-  const int rows = 4 * (type == WH_F32 ? rows_per_wave<WH_F32>() : rows_per_wave<WH_Q8_0>());
+  const int rows = 4 * rows_per_wave<WH_Q8_0>();  // the same for every type
   return (out_rows + rows - 1) / rows;
 }
 

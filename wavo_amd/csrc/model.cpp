@@ -1275,7 +1275,7 @@ int tdt_greedy(const wh_model *m, const float *enc, int frames, int width, uint3
 // The TDT loop's device buffers in tdt_buf: [h_old | h_new | c] ([layers][hidden] each), the joint's
 // predictor projection, the next frame's encoder row and the next joint input ([joint] each), the
 // joint's partial maxima [parts][4], and the two state records; each part on a 64-float boundary.
-constexpr int TDT_PARTS = 1024;  // the most the joint's launch may have (32768 output rows)
+constexpr int TDT_PARTS = 1024;  // the most the joint's launch may have (16384 output rows)
 
 struct TdtBufs {
   float *h_old, *h_new, *c, *pred, *erow, *z, *part;

@@ -29,45 +29,55 @@
 #include "internal.h"
 #include "gemm_impl.h"
 
-// Chosen per GEMM shape from measurements on MI355X (random operands, inside the encoder step):
-// many output tiles → 128×128 tiles of 8 wavefronts; fewer → 64×64 tiles of 4 wavefronts, and when
-// even those leave CUs idle, k split 2 or 4 ways.  Four LDS stages of 64-wide k steps.
+// Chosen per GEMM shape from measurements on MI355X (random operands, inside the encoder step, or
+// replayed back to back for m ≥ 1024): many output tiles → 256×256, 192×128 or 128×128 tiles; fewer
+// → 64×64 tiles of 4 wavefronts, and when even those leave CUs idle, k split 2 or 4 ways.  Ring slots
+// of 64-wide k steps (a slot is refilled NS steps ahead, so NS − 1 steps hide the DMA's latency).
 GemmPlan gemm_plan_for(const wh_ctx *ctx, int m, int cols, int k) {
   const int cus = ctx->cus > 0 ? ctx->cus : 256;
   const long t128 = (long)((cols + 127) / 128) * ((m + 127) / 128), t64 = (long)((cols + 63) / 64) * ((m + 63) / 64);
-  GemmPlan p{64, 64, 2, 2, 4, 1};
-  // Grids of several workgroups per CU (batched windows, m ≈ 12000): three stages, so two
-  // workgroups share a CU (measured 187 against 221 µs at 12000×4096×1024); a single wave of
-  // workgroups (one 750-frame window) runs faster with four.
-  if (t128 >= 4L * cus) p = {128, 128, 2, 4, 3, 1};
+  GemmPlan p{64, 64, 2, 2, 3, 1};
+  const long t256 = (long)((cols + 255) / 256) * ((m + 255) / 256);
+  if (t128 >= 2L * cus && m >= 4096 && k >= 1024) {
+    // Two or more rounds of 128×128 tiles over many rows and a long k (batched windows, m ≈ 12000):
+    // wide outputs with at least two rounds of 256×256 tiles take those (8 wavefronts of 128×64, one
+    // workgroup per CU: the least a and W traffic per output — 12000×4096×1024 154 µs against 172 for
+    // 192×128 and 189 for 128×128); the others 192×128 tiles of 4 wavefronts, two workgroups per CU
+    // (12000×3072×1024 119 µs, 12000×1024×1024 44, 12000×1024×4096 152, against 131, 56 and 162 for
+    // 256×256 and 124, 47 and 162 for 128×128 tiles of 8).  (The batched position projection,
+    // 1515×24576×1024, streams its 27 MB of W from HBM in the step: 128×128 tiles, 2304 of them,
+    // run it in 128 µs there, 256×256 tiles in 189.)
+    if (cols >= 4096 && t256 >= 2L * cus) p = {256, 256, 2, 4, 2, 1};
+    else p = {192, 128, 2, 2, 2, 1};
+  } else if (t128 >= 4L * cus) p = {128, 128, 2, 4, 2, 1};
   else if (t128 > cus && t128 <= 2L * cus && k < 4096)
     // Between one and two 128×128 tiles per CU (a 1500-frame window's wide projections): 256×128
     // tiles of 8 wavefronts with 64×64 wave tiles, one per CU, read each a fragment for twice the
     // columns (measured in the Whisper encoder: 6.05 against 6.16 ms per call, fc1 1.28 against
     // 1.35 ms, than 4-wave 128×128 tiles two per CU; at m = 12000 they are slower).
-    p = {256, 128, 4, 2, 3, 1};
+    p = {256, 128, 4, 2, 2, 1};
   else if (t128 > cus && (t128 <= 2L * cus || k >= 4096))
     // More tiles than CUs with a long k (16 windows' FFN down projection): 4-wave workgroups in
-    // three stages, two per CU, take them in one round or fewer (measured in the encoder: 16 × 60 s
+    // two slots, two per CU, take them in one round or fewer (measured in the encoder: 16 × 60 s
     // FFN down 8.0 against 8.6 ms per call; the 16 windows' 1024 × 1024 projections stay with 8-wave
     // workgroups, 3.13 against 3.22).
-    p = {128, 128, 2, 2, 3, 1};
+    p = {128, 128, 2, 2, 2, 1};
   else if (t128 * 4 >= 3L * cus)
     // Three quarters of a tile per CU or more (the FFN's first projection at 750 frames): 128×128
     // tiles; fewer (the qkv projection, 144 tiles) run faster as 64×64 tiles (4.96 against 4.98 ms
     // per 60 s call).
-    p = {128, 128, 2, 4, 4, 1};
+    p = {128, 128, 2, 4, 3, 1};
   else if (t128 * 4 <= cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
     // Long k over few tiles (the FFN's down projection, 750 × 1024 × 4096): k split 4 ways over
     // 96×64 tiles of 2 wavefronts (96×32 per wavefront: each dequantized W fragment feeds three
-    // MFMAs) in three stages: 512 workgroups, two per CU, whose barriers do not align (measured in
+    // MFMAs) in two slots: 512 workgroups, two per CU, whose barriers do not align (measured in
     // the encoder step, 60 s: 4.64 ms, against 4.68 for 128×64 tiles of 4 wavefronts, 4.75 for
-    // 128×128 tiles of 8 wavefronts, 4.92 for 128×64 tiles in four stages, one per CU).
-    p = {96, 64, 1, 2, 3, 4};
+    // 128×128 tiles of 8 wavefronts, 4.92 for 128×64 tiles in three slots, one per CU).
+    p = {96, 64, 1, 2, 2, 4};
   else if (t128 * 4 <= 2L * cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
     // The same with up to two workgroups per CU (Whisper's fc2, 1500 × 1280 × 5120: 1.18 + its
     // finish against 1.82 ms per call for 64×64 tiles whole).
-    p = {128, 128, 2, 2, 3, 4};
+    p = {128, 128, 2, 2, 2, 4};
   else if (t64 < cus)
     // Split only while every split keeps at least 16 k steps: shorter ones spend more on the
     // pipeline's fill and the partial sums than the extra workgroups win (k = 1024 runs faster whole).
@@ -75,12 +85,12 @@ GemmPlan gemm_plan_for(const wh_ctx *ctx, int m, int cols, int k) {
       p.split *= 2;
   if (ctx->gemm_plan[0]) {  // tuning override (wh_tune "gemm_plan"): bm, bn, wm, wn, stages, split
     const int *o = ctx->gemm_plan;
-    p = {o[0], o[1], o[2], o[3], o[4], o[5]};
+    p = {o[0], o[1], o[2], o[3], o[4], o[5], o[6]};
     if (k % (64 * p.split)) p.split = 1;
   }
   for (const auto &o : ctx->gemm_shape_plans)  // tuning override for one shape (wh_tune "gemm_shape_plans")
     if (o[0] == m && o[1] == cols && o[2] == k) {
-      p = {o[3], o[4], o[5], o[6], o[7], o[8]};
+      p = {o[3], o[4], o[5], o[6], o[7], o[8], o[9]};
       if (k % (64 * p.split)) p.split = 1;
     }
   return p;

@@ -4,6 +4,7 @@
 #pragma once
 #include <algorithm>
 #include <cstdio>
+#include <cstring>
 #include <mutex>
 #include <type_traits>
 #include <utility>
@@ -11,7 +12,7 @@
 
 // Launch shapes of the LDS-DMA kernel (tile, wavefronts, k step, split).
 struct GemmPlan {
-  int bm, bn, wm, wn, ns, split;
+  int bm, bn, wm, wn, ns, split, pipe = 0;
 };
 
 // The launch plan of an m × cols × k GEMM (gemm.hip).
@@ -275,7 +276,13 @@ __device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" :
 // The same from a wave-uniform base address (SGPRs) plus a per-lane 32-bit byte offset, so that a
 // loop moves the whole DMA by scalar adds.  `lds` must be wave-uniform (it goes to M0).
 __device__ __forceinline__ void dma16s(const void *base, uint32_t off, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+  // (the base through readfirstlane: a scalar value even where the scalar registers run short; the
+  // halves as unsigned 32-bit values, since readfirstlane returns int and must not sign-extend)
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint64_t bs = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(bs), "{m0}"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4s(const void *base, uint32_t off, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
@@ -390,27 +397,59 @@ __device__ __forceinline__ void unrolled_steps(F &f, int kt0, int nk) {
   }
 }
 
-// The epilogue's store of a BM × BN tile whose f32 sums sit in LDS (cl, rows of `crow` floats): NT
-// threads take 8 consecutive columns each (16-byte loads of c for the residual modes, 16-byte stores),
-// applying the bias (bb, loaded by the caller for the thread's fixed column group), the epilogue, the
-// dual columns (bd) and the padding columns (epi(0 + bias), as the reference's zero rows give); a
-// split GEMM stores its plain partial sums into plane tz instead.
-template <int BM, int BN, int NT, bool SPLIT, bool OUT16>
+// Scheduling groups for one substep: NM MFMAs one at a time, the ND LDS reads spread over the first
+// half of them and the NV VALU instructions over all of them.
+template <int NM, int ND, int NV, int T = 0>
+__device__ __forceinline__ void sched_interleave() {
+  if constexpr (T < NM) {
+    constexpr int H = NM / 2 > 0 ? NM / 2 : 1;
+    constexpr int d = T < H ? (ND * (T + 1) + H - 1) / H - (ND * T + H - 1) / H : 0;
+    constexpr int v = (NV * (T + 1) + NM - 1) / NM - (NV * T + NM - 1) / NM;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+    if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);  // LDS read
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x002, v, 0);  // VALU
+    sched_interleave<NM, ND, NV, T + 1>();
+  }
+}
+
+// f(integral_constant<I>) for I = B, B + S, .. < E.
+template <int B, int E, int S, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + S, E, S>(f);
+  }
+}
+
+// The epilogue's store of NR rows × BN columns of a tile whose f32 sums sit in LDS (cl, rows of `crow`
+// floats): NT threads take 8 consecutive columns each (16-byte loads of c for the residual modes,
+// 16-byte stores), applying the bias (bb, loaded by the caller for the thread's fixed column group),
+// the epilogue, the dual columns (bd) and the padding columns (epi(0 + bias), as the reference's zero
+// rows give); a split GEMM stores its plain partial sums into plane tz instead.  A pass holds, for
+// every row group of RPW tile rows (one per row of wavefronts), PGR of its rows from row 32·i0: LDS
+// row r is tile row (r / PGR)·RPW + 32·i0 + r % PGR (PGR = RPW, i0 = 0: the whole tile in order).
+template <int NR, int RPW, int PGR, int BN, int NT, bool SPLIT, bool OUT16>
 __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, int crow, int tid, int m0, int n0,
-                                             int tz, const float (&bb)[8], const float (&bd)[8]) {
+                                             int tz, int i0, const float (&bb)[8], const float (&bd)[8]) {
   constexpr int G8 = BN / 8;
   const int m = P.m, rows = P.rows;
-  static_assert((BM * G8) % NT == 0, "whole rounds of column groups");
+  static_assert((NR * G8) % NT == 0, "whole rounds of column groups");
+  static_assert(PGR % 32 == 0 && RPW % PGR == 0, "passes of whole 32-row groups");
+  const int m0p = m0 + 32 * i0;  // tile row of LDS row r: m0p + trow(r)
+  auto trow = [](int r) { return (r / PGR) * RPW + r % PGR; };
+  constexpr int BM = NR;
   if constexpr (OUT16 && !SPLIT) {
     // A tile inside a packed range (the host keeps each range on whole tiles): f16 rows per head or,
     // transposed, 8 rows of one column per store; the epilogue as below (no residual, no dual).
-    for (int o = 0; o < P.nho; o++) {
+#pragma unroll
+    for (int o = 0; o < 2; o++) {  // constant indices: the ranges stay in the kernel arguments
+      if (o >= P.nho) break;
       const HeadsOut &h = P.ho[o];
       if (n0 < h.col0 || n0 >= h.col0 + h.cols) continue;
       if (h.tr) {
 #pragma unroll
         for (int it = 0; it < BM * G8 / NT; it++) {
-          const int e = tid + it * NT, c = e % BN, r0 = 8 * (e / BN), row0 = m0 + r0, col = n0 + c;
+          const int e = tid + it * NT, c = e % BN, r0 = 8 * (e / BN), row0 = m0p + trow(r0), col = n0 + c;
           if (row0 >= h.rs || col >= P.cols) continue;
           const float b = P.bias[col];
           half8 y;
@@ -422,7 +461,7 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
       } else {
 #pragma unroll
         for (int it = 0; it < BM * G8 / NT; it++) {
-          const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0 + r, col = n0 + c8;
+          const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0p + trow(r), col = n0 + c8;
           if (row + h.r0 >= h.rs || col >= P.cols) continue;
           half8 y;
           if (row < m) {
@@ -441,9 +480,62 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
       return;
     }
   }
+  if constexpr (!SPLIT) {
+    // A tile of real, non-dual columns only (every tile but the edge ones): the epilogue mode chosen
+    // once per tile, no per-column checks, pairs converted to f16 by one instruction.
+    if (n0 + BN <= rows && n0 >= P.dual) {
+      auto run = [&](auto E_c) {
+        constexpr int E = decltype(E_c)::value;
+#pragma unroll
+        for (int it = 0; it < BM * G8 / NT; it++) {
+          const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0p + trow(r), col = n0 + c8;
+          if (row >= m) continue;
+          const float4 x0 = *(const float4 *)(cl + r * crow + c8), x1 = *(const float4 *)(cl + r * crow + c8 + 4);
+          const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+          const size_t at = (size_t)row * P.ldc + col;
+          float y[8];
+          if constexpr (!OUT16 && (E == WH_RESIDUAL || E == WH_GELU_RESIDUAL)) {
+            const float4 c0 = *(const float4 *)((const float *)P.c + at), c1 = *(const float4 *)((const float *)P.c + at + 4);
+            const float cc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+            for (int q = 0; q < 8; q++) y[q] = E == WH_RESIDUAL ? cc[q] + P.alpha * (x[q] + bb[q]) : cc[q] + gelu(x[q] + bb[q]);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 8; q++) y[q] = epilogue(E, 0.0f, x[q] + bb[q], nullptr);
+          }
+          if constexpr (OUT16) {
+            typedef float float2v __attribute__((ext_vector_type(2)));
+            half8 h;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+              const half2 p = __builtin_convertvector(float2v{y[2 * q], y[2 * q + 1]}, half2);
+              h[2 * q] = p[0], h[2 * q + 1] = p[1];
+            }
+            *(half8 *)((_Float16 *)P.c + at) = h;
+          } else {
+            *(float4 *)((float *)P.c + at) = make_float4(y[0], y[1], y[2], y[3]);
+            *(float4 *)((float *)P.c + at + 4) = make_float4(y[4], y[5], y[6], y[7]);
+          }
+        }
+      };
+      switch (P.epi) {
+        case WH_SILU: run(std::integral_constant<int, WH_SILU>{}); return;
+        case WH_RELU: run(std::integral_constant<int, WH_RELU>{}); return;
+        case WH_GELU: run(std::integral_constant<int, WH_GELU>{}); return;
+        case WH_TANH: run(std::integral_constant<int, WH_TANH>{}); return;
+        case WH_RESIDUAL:
+          if constexpr (!OUT16) { run(std::integral_constant<int, WH_RESIDUAL>{}); return; }
+          break;
+        case WH_GELU_RESIDUAL:
+          if constexpr (!OUT16) { run(std::integral_constant<int, WH_GELU_RESIDUAL>{}); return; }
+          break;
+        default: run(std::integral_constant<int, WH_BIAS>{}); return;
+      }
+    }
+  }
 #pragma unroll
   for (int it = 0; it < BM * G8 / NT; it++) {
-    const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0 + r, col = n0 + c8;
+    const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0p + trow(r), col = n0 + c8;
     if (row >= m || col >= P.cols) continue;  // cols % 32 == 0: a group is inside or past
     const float4 x0 = *(const float4 *)(cl + r * crow + c8), x1 = *(const float4 *)(cl + r * crow + c8 + 4);
     float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
@@ -508,48 +600,68 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
 // c tile BM × BN per workgroup of WM × WN wavefronts, each a (BM/WM) × (BN/WN) block of 32×32 MFMA
 // tiles, over the k range of its split (the 64-wide k steps divided evenly over gridDim.z).
 //
-// Pipeline.  The k loop moves in 64-wide steps through a ring of NS LDS stages that the LDS DMA
-// fills NS − 1 steps ahead, from scalar base addresses (a step costs the vector units nothing but
-// the dequantization).  A step is 4 substeps of 16 k; each wave reads the a fragments of substep
-// s + 1 while the MFMAs of substep s run, and the W data of the next step after the one barrier of
-// the step, which sits after substep 2: there every wave has waited for the next stage's DMA and has
-// finished reading the stage of the previous step, so the DMA of step kt + NS − 1 goes into that
-// stage.  The loop is unrolled by the ring length so that every LDS offset is an immediate.  Each
-// wave issues the same number of DMA instructions per step (a wave without an instruction of its
-// own repeats another wave's: identical bytes to the same place), so a vmcnt immediate waits for
-// exactly one step.
+// Pipeline.  The k loop moves in 64-wide steps through a ring of NS LDS slots that the LDS DMA
+// fills NS steps ahead, from scalar base addresses (a step costs the vector units nothing but the
+// dequantization).  A step is 4 substeps of 16 k; each wave reads the a fragments of substep s + 1
+// while the MFMAs of substep s run, and the W data of the next step after the one barrier of the
+// step, which sits after substep 2: there every wave has waited for the next stage's DMA and has read
+// everything it needs of the current slot into registers (the last substep's a fragments before the
+// third substep's MFMAs, the step's W data one step earlier), so the DMA of step kt + NS goes into
+// the current slot right after the barrier, and a stage has NS − 1 steps to land.  The loop is
+// unrolled by the ring length so that every LDS offset is an immediate.  The DMA of a stage is spread
+// over the wavefronts, each instruction issued once (an instruction costs the memory pipeline the same
+// ~16 cycles whatever its width, so W rows move in 16-byte chunks too).
 //
 // LDS layout: the a stages (rows of 8 16-byte chunks, chunk c of row r at (c + r/2) % 8 — the 16
 // lanes that LDS serves together read 16 rows and hit all 64 banks once), then the W stages: F16
-// rows like a, or quantized rows of one block pair (68 or 36 bytes, as stored).  At substep s, the
+// rows like a, or quantized rows of one block pair (68 or 36 bytes, as stored) in LDS rows of 80 or
+// 48 bytes (whole 16-byte chunks from the pair's start).  At substep s, the
 // lane of MFMA column n and k half g takes k slots 32g + 8s .. + 8 — block g of its W row's pair —
 // and the a fragments the same slots.
 //
 // Epilogue.  The accumulators go through LDS (f32, rows padded so the two lane halves of a tile hit
 // distinct banks) and leave as 8 consecutive columns per lane: 16-byte loads of c for the residual
 // modes and 16-byte stores, with the bias, the epilogue, the dual columns and the padding columns
-// (epi(0 + bias), as the reference's zero rows give) applied on the way.
-template <int WT, int BM, int BN, int WM, int WN, int NSQ, bool SPLIT, bool OUT16>
+// (epi(0 + bias), as the reference's zero rows give) applied on the way.  A tile whose f32 sums do
+// not fit in the ring's LDS goes through in passes of whole 32-row MFMA tiles of every wavefront.
+template <int WT, int BM, int BN, int WM, int WN, int NSQ, bool SPLIT, bool OUT16, int PIPE>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
   static_assert(TM >= 1 && TN >= 1, "32×32 MFMA tiles per wave");
   constexpr int PAIR1 = WT == WH_Q8_0 ? 68 : WT == WH_Q4_0 ? 36 : 128;  // W bytes of 64 weights
   constexpr bool WCH = WT == WH_F16;                                     // W moves in 16-byte chunks
-  constexpr int A_ST = BM * 128, W_ST = BN * PAIR1, ST = A_ST + W_ST;
+  // A quantized W row's block pair moves as whole 16-byte chunks from its (4-byte aligned) start: 5
+  // chunks (80 LDS bytes) for Q8_0, 3 (48) for Q4_0; the bytes past the pair are the next pair's (or
+  // the allocation's tail slack) and are never read.  F16 rows move like a.
+  constexpr int WROW = WCH ? 128 : (PAIR1 + 15) / 16 * 16, WCK = WROW / 16;  // LDS bytes, chunks per W row
+  constexpr int A_ST = BM * 128, W_ST = BN * WROW, ST = A_ST + W_ST;
   constexpr int CROW = BN + 8;                                           // f32 per epilogue LDS row
-  constexpr int C_BYTES = BM * CROW * 4;
-  // NSQ stages asked for, as many as fit in the 160 KiB of LDS.
+  // NSQ slots asked for, as many as fit in the 160 KiB of LDS.
   constexpr int NS = NSQ * ST + 16 <= 160 * 1024 ? NSQ : (160 * 1024 - 16) / ST;
-  static_assert(NS >= 3, "at least three stages");
-  static_assert(WCH || W_ST % 256 == 0, "whole DMA instructions");
+  static_assert(NS >= 2, "at least two slots");
+  static_assert(W_ST % 1024 == 0, "whole DMA instructions");
   constexpr int W_RG = NS * A_ST;                               // the W stages follow the a stages
   constexpr int NIA = A_ST / 1024;                              // a: 16-byte DMA instructions per stage
-  constexpr int NIW = WCH ? W_ST / 1024 : W_ST / 256;           // W: 16-byte or 4-byte ones
-  constexpr int PA = (NIA + NW - 1) / NW, PW = (NIW + NW - 1) / NW, PI = PA + PW;
-  static_assert((NS - 2) * PI < 64, "vmcnt holds the DMA of NS - 2 steps");
+  constexpr int NIW = W_ST / 1024;                              // W: 16-byte DMA instructions per stage
+  // The wavefronts that issue the DMA: all of them; in the ping-pong loop the a tile by all of them
+  // and the W rows by the four of the second group.
+  constexpr int NWA = NW, NWI = PIPE == 2 ? 4 : NW;
+  // Instructions per wavefront and stage: PA / PW at most; the first NIA % NWI (NIW % NWI) wavefronts
+  // take one more than the others.  vmcnt immediates count PI = the fewest a wavefront issues per stage:
+  // loads complete in order, so waiting until at most m·PI remain waits for everything older than the
+  // wavefront's last m stages (and at most a few of their instructions besides).
+  constexpr int PA = (NIA + NWA - 1) / NWA, PW = (NIW + NWI - 1) / NWI, PI = NIA / NWA + NIW / NWI;
+  static_assert((NS - 1) * PI < 64, "vmcnt holds the DMA of NS - 1 steps");
   // (+16: the odd block of the last W row reads one dword past its row, unused)
-  constexpr int LDS_BYTES = NS * ST + 16 > C_BYTES ? NS * ST + 16 : C_BYTES;
+  constexpr int RING = NS * ST + 16;
+  // Epilogue passes: PG of each wavefront's TM 32-row tiles at a time, the most that fit in the ring
+  // (the whole tile when it fits).
+  constexpr int PG = BM * CROW * 4 <= RING ? TM
+                     : (TM % 2 == 0 && BM / 2 * CROW * 4 <= RING) ? TM / 2
+                     : (TM % 4 == 0 && BM / 4 * CROW * 4 <= RING) ? TM / 4 : 1;
+  constexpr int C_BYTES = WM * 32 * PG * CROW * 4;
+  constexpr int LDS_BYTES = RING > C_BYTES ? RING : C_BYTES;
   __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -579,39 +691,46 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   // Per-lane byte offsets of this wave's DMA instructions from the step's base addresses (rows past
   // m or rows are clamped: their products land in outputs that are discarded or zeroed), and the
   // instructions' LDS offsets in a stage.
+  const int wi = PIPE == 2 ? wave % 4 : wave;  // the wavefront's index among the W-issuing ones
   uint32_t aoff[PA], alds[PA];
 #pragma unroll
   for (int i = 0; i < PA; i++) {
-    const int n = (wave + NW * i) % NIA, r = 8 * n + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
+    const int n = (wave + NWA * i) % NIA, r = 8 * n + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
     aoff[i] = (uint32_t)(((size_t)min(m0 + r, m - 1) * k + 8 * lc) * 2);
     alds[i] = 1024 * n;
   }
   uint32_t woff[PW], wlds[PW];
 #pragma unroll
   for (int i = 0; i < PW; i++) {
-    const int n = (wave + NW * i) % NIW;
+    const int n = (wi + NWI * i) % NIW;
     if constexpr (WCH) {
       const int r = 8 * n + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
       woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * lc);
       wlds[i] = 1024 * n;
     } else {
-      const int sidx = 64 * n + lane, r = sidx / (PAIR1 / 4), dwi = sidx % (PAIR1 / 4);
-      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 4 * dwi);
-      wlds[i] = 256 * n;
+      const int t = 64 * n + lane, r = t / WCK, c = t % WCK;
+      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * c);
+      wlds[i] = 1024 * n;
     }
   }
   const uint8_t *abase = (const uint8_t *)P.a + (size_t)kb * 128;
   const uint8_t *wbase = P.w + (size_t)kb * PAIR1;
   const uint32_t lds0 = lds_addr(lds);
+  auto issue_a = [&](int kt, int slot) {
+    const uint8_t *ab = abase + (size_t)kt * 128;
+#pragma unroll
+    for (int i = 0; i < PA; i++)
+      if (NIA % NWA == 0 || i < NIA / NWA || wave + NWA * i < NIA) dma16s(ab, aoff[i], lds0 + slot * A_ST + alds[i]);
+  };
+  auto issue_w = [&](int kt, int slot) {
+    const uint8_t *wb = wbase + (size_t)kt * PAIR1;
+#pragma unroll
+    for (int i = 0; i < PW; i++)
+      if (NIW % NWI == 0 || i < NIW / NWI || wi + NWI * i < NIW) dma16s(wb, woff[i], lds0 + W_RG + slot * W_ST + wlds[i]);
+  };
   auto issue = [&](int kt, int slot) {
-    const uint8_t *ab = abase + (size_t)kt * 128, *wb = wbase + (size_t)kt * PAIR1;
-#pragma unroll
-    for (int i = 0; i < PA; i++) dma16s(ab, aoff[i], lds0 + slot * A_ST + alds[i]);
-#pragma unroll
-    for (int i = 0; i < PW; i++) {
-      if constexpr (WCH) dma16s(wb, woff[i], lds0 + W_RG + slot * W_ST + wlds[i]);
-      else dma4s(wb, woff[i], lds0 + W_RG + slot * W_ST + wlds[i]);
-    }
+    issue_a(kt, slot);
+    issue_w(kt, slot);
   };
 
   // The lane's k chunk (of 8 in a step) at substep s.  Q8_0: 2s + g — block s/2 of the pair at
@@ -629,7 +748,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   constexpr int ND = Q8 ? 10 : WT == WH_Q4_0 ? 5 : 16;  // dwords per lane per W row and step
   constexpr int NSC = Q8 ? 2 : 1;                       // scale dwords per lane per W row and step
   constexpr int BLK = PAIR1 / 2;
-  const uint32_t w_row = W_RG + (wn + lrow) * PAIR1;
+  const uint32_t w_row = W_RG + (wn + lrow) * WROW;
   const uint32_t w_dat = Q8 ? w_row + 8 * g : w_row + (g ? BLK + 2 : 0), w_sc = w_row + (g ? BLK - 2 : 0);
   uint32_t wf_off[4];
 #pragma unroll
@@ -645,24 +764,24 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
       if constexpr (WCH) {
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-          const uint4 x = *(const uint4 *)(lds + wf_off[s] + slot * W_ST + j * 32 * PAIR1);
+          const uint4 x = *(const uint4 *)(lds + wf_off[s] + slot * W_ST + j * 32 * WROW);
           w[j][4 * s] = x.x, w[j][4 * s + 1] = x.y, w[j][4 * s + 2] = x.z, w[j][4 * s + 3] = x.w;
         }
         sc[j][0] = 0;
       } else if constexpr (Q8) {
         // Pair bytes 2 + 8g .. (block 0, substeps 0-1: dwords 0-2 and 4-6 from byte 8g) and
         // 36 + 8g .. (block 1, substeps 2-3: dwords 9-10 and 13-14); the scales at bytes 0 and 34.
-        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * PAIR1);
+        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * WROW);
         constexpr int at[10] = {0, 1, 2, 4, 5, 6, 9, 10, 13, 14};
 #pragma unroll
         for (int i = 0; i < 10; i++) w[j][i] = q[at[i]];
-        const uint32_t *r = (const uint32_t *)(lds + w_row + slot * W_ST + j * 32 * PAIR1);
+        const uint32_t *r = (const uint32_t *)(lds + w_row + slot * W_ST + j * 32 * WROW);
         sc[j][0] = r[0], sc[j][1] = r[8];
       } else {
-        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * PAIR1);
+        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * WROW);
 #pragma unroll
         for (int i = 0; i < ND; i++) w[j][i] = q[i];
-        sc[j][0] = *(const uint32_t *)(lds + w_sc + slot * W_ST + j * 32 * PAIR1);
+        sc[j][0] = *(const uint32_t *)(lds + w_sc + slot * W_ST + j * 32 * WROW);
       }
     }
   };
@@ -688,9 +807,155 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
     }
   };
 #pragma unroll
-  for (int s = 0; s < NS - 1; s++)
+  for (int s = 0; s < NS; s++)
     if (s < nk) issue(s, s);
-  {
+  if constexpr (PIPE == 1) {
+    // W one substep ahead: the fragments of substep s + 1 are dequantized (and its a fragments read)
+    // while the MFMAs of substep s run, so no MFMA waits for the VALU that makes its operand; the
+    // scheduling groups interleave one MFMA at a time with its share of the LDS reads and the VALU.
+    uint32_t wq[TN][ND], sc[TN][NSC];
+    half8 af[2][TM], bq[2][TN];
+    auto deq = [&](half8 (&b)[TN], auto s_c) {
+#pragma unroll
+      for (int j = 0; j < TN; j++) b[j] = wfrag(wq, sc, j, s_c);
+    };
+    auto mm = [&](const half8 (&f)[TM], const half8 (&b)[TN]) {
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int i = 0; i < TM; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], b[j], acc[i][j], 0, 0, 0);
+    };
+    constexpr int VQ = WCH ? 0 : (Q8 ? 12 : 10) * TN;  // VALU of one substep's dequantization
+    if (nk > 0) {
+      if (nk >= NS) wait_vm<(NS - 1) * PI>();  // stages 1 .. NS - 1 may be in flight
+      else dma_wait();
+      __syncthreads();
+      read_w(wq, sc, 0);
+      read_a(af[0], 0, 0);
+      deq(bq[0], std::integral_constant<int, 0>{});
+    }
+    auto step = [&](auto S_c, int kt) {
+      constexpr int S = decltype(S_c)::value, slot = S % NS;
+      read_a(af[1], slot, 1);
+      deq(bq[1], std::integral_constant<int, 1>{});
+      mm(af[0], bq[0]);
+      sched_interleave<TM * TN, TM, VQ>();
+      read_a(af[0], slot, 2);
+      deq(bq[0], std::integral_constant<int, 2>{});
+      mm(af[1], bq[1]);
+      sched_interleave<TM * TN, TM, VQ>();
+      read_a(af[1], slot, 3);
+      deq(bq[1], std::integral_constant<int, 3>{});
+      mm(af[0], bq[0]);
+      sched_interleave<TM * TN, TM, VQ>();
+      if (kt + 1 < nk) {
+        // Stage kt + 1 has landed for every wave, and every wave is done reading slot kt.
+        if (kt + NS - 1 < nk) wait_vm<(NS - 2) * PI>();  // stages kt + 2 .. kt + NS - 1 may be in flight
+        else dma_wait();
+        __syncthreads();
+        if (kt + NS < nk) issue(kt + NS, slot);  // into the slot this step has finished reading
+      }
+      // The next step's W data, a fragments and first W fragments (after the last step: read from a
+      // stale slot and never used), beside the last substep's MFMAs.
+      mm(af[1], bq[1]);
+      read_w(wq, sc, (slot + 1) % NS);
+      read_a(af[0], (slot + 1) % NS, 0);
+      deq(bq[0], std::integral_constant<int, 0>{});
+      sched_interleave<TM * TN, TM + TN * (WCH ? 4 : ND + NSC), VQ>();
+    };
+    constexpr int UNR = NS % 2 ? 2 * NS : NS;
+    for (int kt0 = 0; kt0 < nk; kt0 += UNR) unrolled_steps<0, UNR>(step, kt0, nk);
+  } else if constexpr (PIPE == 2) {
+    // Ping-pong.  Two groups of four wavefronts (group 1 = waves 4-7; a workgroup's wavefronts go to
+    // the SIMDs round-robin, so every SIMD holds one of each) take turns, offset by half a step: while
+    // one group runs the 4·TM·TN MFMAs of a k step from registers (its a fragments read one substep
+    // ahead), the other group reads and dequantizes its W fragments of its next step.  So the
+    // dequantization's VALU runs beside the other group's MFMAs on every SIMD.  One barrier per half
+    // step; group 1 starts one barrier later.  Stage i is read by group 0 between barriers 2i + 1 and
+    // 2i + 3 and by group 1 between 2i + 2 and 2i + 4, so its slot refills after barrier 2i + 4 with
+    // stage i + NS: the a tile by all eight wavefronts during their MFMAs of step i + 1 (one DMA
+    // instruction after the first MFMA of each substep), the W rows by group 1 during its
+    // dequantization of step i + 1.  Stage i + 1 must land by barrier 2i + 3: group 0 waits for its part
+    // at the end of its MFMAs of step i, group 1 at the end of its dequantization of step i.
+    static_assert(WM == 2 && WN == 4 && NS >= 3, "two groups of four wavefronts, three or more slots");
+    static_assert(NIA % NW == 0 && NIA / NW <= 4, "at most one a-tile DMA instruction per wavefront and substep");
+    const bool g1 = wave >= 4;
+    constexpr int QA = NIA / NW, QW = NIW / 4;  // DMA instructions per wavefront and stage (W: the fewest)
+    uint32_t wq[TN][ND], sc[TN][NSC];
+    half8 af[2][TM], wf[4][TN];
+    // The MFMAs of substep s; a-tile DMA instruction s of stage kd (if any) after the first.
+    auto mm = [&](const half8 (&f)[TM], const half8 (&b)[TN], const uint8_t *ab, int slot_d, auto s_c) {
+      constexpr int SS = decltype(s_c)::value;
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], b[j], acc[i][j], 0, 0, 0);
+          if constexpr (SS < QA)
+            if (i == 0 && j == 0) dma16s(ab, aoff[SS], lds0 + slot_d * A_ST + alds[SS]);
+        }
+    };
+    // Prologue: stages 0 .. NS − 2, the a tiles by all, the W rows by group 1.
+#pragma unroll
+    for (int s = 0; s < NS - 1; s++)
+      if (s < nk) {
+        issue_a(s, s);
+        if (g1) issue_w(s, s);
+      }
+    if (nk >= NS - 1) {  // stage 0 has landed
+      if (g1) wait_vm<(NS - 2) * (QA + QW)>();
+      else wait_vm<(NS - 2) * QA>();
+    } else {
+      dma_wait();
+    }
+    __syncthreads();
+    if (g1) __syncthreads();
+    auto step = [&](auto S_c, int kt) {
+      constexpr int S = decltype(S_c)::value, slot = S % NS, dslot = (S + NS - 1) % NS;
+      const bool more = kt + NS - 1 < nk;  // stage kt + NS − 1 exists (into the slot of step kt − 1)
+      // Preparation of step kt.
+      read_w(wq, sc, slot);
+      static_for<0, 4, 1>([&](auto s_c) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) wf[decltype(s_c)::value][j] = wfrag(wq, sc, j, s_c);
+      });
+      read_a(af[0], slot, 0);
+      // The fragments exist in registers here (kept from being recomputed inside the MFMA phase).
+#pragma unroll
+      for (int s = 0; s < 4; s++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) asm volatile("" : "+v"(wf[s][j]));
+      if (g1) {
+        if (more) issue_w(kt + NS - 1, dslot);
+        // Group 1's a-tile part of stage kt + 1 (issued in its MFMAs of step kt − 1) and W rows of it
+        // have landed: only the W rows just issued may remain.
+        if (kt + 1 < nk) {
+          if (more) wait_vm<QW>();
+          else dma_wait();
+        }
+      }
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      // The MFMAs of step kt, with this wavefront's a-tile DMA of stage kt + NS − 1; each substep's a
+      // fragments read before the previous substep's MFMAs.
+      // (After the last stage, the last one again: into the slot of step kt − 1, which nothing reads
+      // any more, so that every step issues the same instructions with no branch between MFMAs.)
+      const uint8_t *ab = abase + (size_t)(uint32_t)__builtin_amdgcn_readfirstlane(more ? kt + NS - 1 : nk - 1) * 128;
+      read_a(af[1], slot, 1);
+      mm(af[0], wf[0], ab, dslot, std::integral_constant<int, 0>{});
+      read_a(af[0], slot, 2);
+      mm(af[1], wf[1], ab, dslot, std::integral_constant<int, 1>{});
+      read_a(af[1], slot, 3);
+      mm(af[0], wf[2], ab, dslot, std::integral_constant<int, 2>{});
+      mm(af[1], wf[3], ab, dslot, std::integral_constant<int, 3>{});
+      if (!g1 && kt + 1 < nk) wait_vm<QA>();  // group 0's part of stage kt + 1 has landed (this step's may remain)
+      __builtin_amdgcn_sched_barrier(0);
+      if (!g1 || kt + 1 < nk) __syncthreads();
+    };
+    constexpr int UNR = NS;
+    for (int kt0 = 0; kt0 < nk; kt0 += UNR) unrolled_steps<0, UNR>(step, kt0, nk);
+    dma_wait();  // the repeated stages of the last steps, before the epilogue reuses the LDS
+  } else {
     uint32_t wq[2][TN][ND], sc[2][TN][NSC];
     half8 af[2][TM];
     // Substep s of a step: dequantize the lane's W fragment (quantized) and run the TM × TN MFMAs.
@@ -703,7 +968,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
       }
     };
     if (nk > 0) {
-      if (nk - 1 >= NS - 2) wait_vm<(NS - 2) * PI>();  // stages 1 .. NS - 2 may be in flight
+      if (nk >= NS) wait_vm<(NS - 1) * PI>();  // stages 1 .. NS - 1 may be in flight
       else dma_wait();
       __syncthreads();
       read_w(wq[0], sc[0], 0);
@@ -719,11 +984,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
       read_a(af[1], slot, 3);
       mma(af[0], wq[cur], sc[cur], std::integral_constant<int, 2>{});
       if (kt + 1 < nk) {
-        // Stage kt + 1 has landed for every wave, and every wave is done with stage kt − 1.
-        if (kt + NS - 2 < nk) wait_vm<(NS - 3) * PI>();
+        // Stage kt + 1 has landed for every wave, and every wave is done reading slot kt.
+        if (kt + NS - 1 < nk) wait_vm<(NS - 2) * PI>();  // stages kt + 2 .. kt + NS - 1 may be in flight
         else dma_wait();
         __syncthreads();
-        if (kt + NS - 1 < nk) issue(kt + NS - 1, (slot + NS - 1) % NS);
+        if (kt + NS < nk) issue(kt + NS, slot);  // into the slot this step has finished reading
         read_w(wq[cur ^ 1], sc[cur ^ 1], (slot + 1) % NS);
         read_a(af[0], (slot + 1) % NS, 0);
       }
@@ -747,17 +1012,25 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
     for (int q = 0; q < 8; q++)
       if (ecol + q < P.dual) bd[q] = P.bias[P.cols + ecol + q];
   }
-  __syncthreads();
   float *cl = (float *)lds;
+  // Pass i0: 32-row tiles i0 .. i0 + PG − 1 of every wavefront; LDS row (wave row)·32·PG + 32·(i − i0)
+  // + the row in the MFMA tile.
+  const int crow0 = (wave / WN) * 32 * PG;
+  // (passes unrolled at compile time, so that the accumulators are only ever indexed by constants)
+  auto pass = [&](auto I0_c) {
+    constexpr int i0 = decltype(I0_c)::value;
+    __syncthreads();
 #pragma unroll
-  for (int i = 0; i < TM; i++)
+    for (int i = i0; i < i0 + PG; i++)
 #pragma unroll
-    for (int j = 0; j < TN; j++)
+      for (int j = 0; j < TN; j++)
 #pragma unroll
-      for (int v = 0; v < 16; v++)
-        cl[(wm + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow] = acc[i][j][v];
-  __syncthreads();
-  store_c_tile<BM, BN, 64 * NW, SPLIT, OUT16>(P, cl, CROW, tid, m0, n0, tz, bb, bd);
+        for (int v = 0; v < 16; v++)
+          cl[(crow0 + 32 * (i - i0) + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow] = acc[i][j][v];
+    __syncthreads();
+    store_c_tile<WM * 32 * PG, BM / WM, 32 * PG, BN, 64 * NW, SPLIT, OUT16>(P, cl, CROW, tid, m0, n0, tz, i0, bb, bd);
+  };
+  static_for<0, TM, PG>(pass);
 }
 
 // Split-k finish: c = epi(Σ_z part[z] + bias) with the partial sums added in split order (the same
@@ -785,11 +1058,18 @@ __global__ __launch_bounds__(256) void split_finish_kernel(const float *__restri
   }
 }
 
-template <int WT, int BM, int BN, int WM, int WN, int NS>
-void lds_launch(wh_ctx *ctx, dim3 grid, const LdsArgs &a, bool split, bool out16) {
-  if (split) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, true, false>, grid, 64 * WM * WN, 0, a);
-  else if (out16) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, true>, grid, 64 * WM * WN, 0, a);
-  else wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, false>, grid, 64 * WM * WN, 0, a);
+template <int WT, int BM, int BN, int WM, int WN, int NS, int PIPE>
+int lds_launch(wh_ctx *ctx, dim3 grid, const LdsArgs &a, bool split, bool out16) {
+  constexpr int WROW = WT == WH_Q8_0 ? 80 : WT == WH_Q4_0 ? 48 : 128;  // LDS bytes per W row (the kernel's)
+  if constexpr (PIPE == 2 && (WT == WH_F16 || NS * (BM * 128 + BN * WROW) + 16 > 160 * 1024)) {
+    // (not built: the ring would exceed the LDS, or F16 rows, which need no dequantization to hide)
+    return wh_fail(ctx, WH_EARG, "gemm: no ping-pong kernel for %d slots of a %dx%d tile of this weight type", NS, BM, BN);
+  } else {
+    if (split) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, true, false, PIPE>, grid, 64 * WM * WN, 0, a);
+    else if (out16) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, true, PIPE>, grid, 64 * WM * WN, 0, a);
+    else wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, false, PIPE>, grid, 64 * WM * WN, 0, a);
+    return WH_OK;
+  }
 }
 
 template <int WT>
@@ -813,9 +1093,11 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
   static const char *tn = WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
   // Named by kernel variant and call shape: m x rows x k, epilogue, output type, row width.
   char name[128];
-  snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s %dx%dx%d e%d %s w%d", tn, p.bm, p.bn, p.wm, p.wn, p.ns,
-           p.split > 1 ? (p.split == 2 ? "_s2" : "_s4") : "", m, l->rows, l->k, epi,
-           out16 ? "f16" : "f32", l->cols + l->dual);
+  char sp[8] = "";
+  if (p.split > 1) snprintf(sp, sizeof sp, "_s%d", p.split);
+  if (p.pipe) snprintf(sp + strlen(sp), sizeof sp - strlen(sp), "_p%d", p.pipe);
+  snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s %dx%dx%d e%d %s w%d", tn, p.bm, p.bn, p.wm, p.wn, p.ns, sp, m,
+           l->rows, l->k, epi, out16 ? "f16" : "f32", l->cols + l->dual);
   const double width = l->cols + l->dual;
   const double bytes = (double)l->rows * l->row_bytes + 2.0 * m * l->k +
                        (out16 ? 2.0 : 4.0) * m * width * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
@@ -823,25 +1105,31 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     ProfScope prof(ctx, name, 2.0 * m * l->rows * l->k, bytes);
     const bool sp = p.split > 1;
     bool ok = false;
-#define PLAN(BM, BN, WM, WN, NS)                                                           \
-  if (!ok && p.bm == BM && p.bn == BN && p.wm == WM && p.wn == WN && p.ns == NS) {          \
-    lds_launch<WT, BM, BN, WM, WN, NS>(ctx, grid, args, sp, out16);                         \
-    ok = true;                                                                               \
+#define PLANP(BM, BN, WM, WN, NS, PIPE)                                                               \
+  if (!ok && p.bm == BM && p.bn == BN && p.wm == WM && p.wn == WN && p.ns == NS && p.pipe == PIPE) {      \
+    if (int rc = lds_launch<WT, BM, BN, WM, WN, NS, PIPE>(ctx, grid, args, sp, out16)) return rc;          \
+    ok = true;                                                                                            \
   }
-    PLAN(128, 128, 2, 4, 4)
-    PLAN(64, 64, 2, 2, 4)
+#define PLAN(BM, BN, WM, WN, NS) PLANP(BM, BN, WM, WN, NS, 0)
     PLAN(128, 128, 2, 4, 3)
     PLAN(64, 64, 2, 2, 3)
-    PLAN(128, 128, 2, 2, 3)
-    PLAN(256, 128, 4, 2, 3)
-    PLAN(128, 64, 2, 2, 3)
-    PLAN(128, 64, 2, 2, 4)
-    PLAN(64, 128, 2, 2, 4)
-    PLAN(96, 128, 1, 4, 3)
-    PLAN(96, 128, 1, 4, 4)
-    PLAN(96, 64, 1, 2, 3)
-    PLAN(96, 128, 1, 4, 6)
+    PLAN(128, 128, 2, 4, 2)
+    PLAN(128, 128, 2, 2, 2)
+    PLAN(256, 128, 4, 2, 2)
+    PLAN(96, 64, 1, 2, 2)
+    PLAN(192, 128, 2, 2, 2)
+    PLAN(256, 256, 2, 4, 2)
+    PLANP(256, 256, 2, 2, 2, 1)
+    PLANP(256, 128, 2, 2, 2, 1)
+    PLANP(128, 256, 2, 2, 2, 1)
+    PLANP(256, 256, 2, 4, 2, 1)
+    PLANP(128, 128, 2, 4, 2, 1)
+    PLANP(192, 128, 2, 2, 2, 1)
+    PLANP(256, 256, 2, 4, 3, 2)
+    PLANP(256, 128, 2, 4, 3, 2)
+    PLANP(128, 256, 2, 4, 3, 2)
 #undef PLAN
+#undef PLANP
     if (!ok) return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages", p.bm, p.bn, p.wm, p.wn, p.ns);
     if (int rc = wh_launched(ctx, "gemm")) return rc;
   }

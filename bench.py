@@ -8,8 +8,10 @@ N(0, 0.02), written as a GGUF file and loaded through the C ABI).  After --warmu
 of the --steps timed calls is bracketed by HIP events on the library's stream (the calls after the
 second replay a recorded HIP graph of the step); `ms_per_step` is their median and `value` = audio
 seconds ÷ that median (RTFx).  `host_io` is the same call timed on the host from the mel's upload
-(host → HBM) to the output's read-back (HBM → host), PCIe included; it is reported beside `value`,
-never as it.  `host_frontend_ms` (the numpy log-mel of the synthetic audio) and `tdt_decode_ms` (the
+(host → HBM) to the output's read-back (HBM → host), PCIe included, and `host_io_pinned` the same from
+and into page-locked host memory (wh_host_alloc; the RTFx the survey defines, from mel H2D to output
+D2H); both are reported beside `value`, never as it (the value is the throughput with the input
+resident in HBM).  `host_frontend_ms` (the numpy log-mel of the synthetic audio) and `tdt_decode_ms` (the
 TDT greedy decode on the host, as the reference runs it) are separate; `tdt_device` is the same decode
 on the device over the resident encoder output (wh_model_greedy_device, host clock, median of 5 calls
 after 2), with whether its tokens equal the host decode's.  `audio_to_tokens` is the whole path on the
@@ -34,12 +36,14 @@ the head alone, and `gemv.decode_step` the whole decoder step replayed as one re
 token for 224 tokens.
 
 `other_configs` times the encoder call of BASELINE's other configurations: configs[0] (GigaAM-v3 shape,
-11 s), configs[2] (Whisper-large-v3-turbo encoder, one 30 s window) and configs[3] (Parakeet over 16
-windows of ≤ 60 s cut at pauses, one padded batch).
+11 s), configs[2] (Whisper-large-v3-turbo encoder, one 30 s window) and configs[3] — one padded batch of
+16 windows of ≤ 60 s cut at pauses (with every kernel's roofline in that batch, `C3_kernels`, and its
+dominant GEMM, `C3_roofline`), and the whole 2 h workload through every batch of 16, the remainder batch
+included (`C3_parakeet_2h`).
 
 `cpu_baseline` is the C parity oracle (the restated wavo CPU backend: portable f16-rounded GEMM,
-AVX2+FMA, OpenMP) on the same model, on this host: the median of 3 warm 60 s calls on all threads, and
-one 10 s call on 1 thread.  `load` times wh_model_load of the GGUF with the file dropped from the page
+AVX2+FMA, OpenMP) on this host: configs[1] on the same model and mel, the median of 10 warm calls on
+all threads (after 2), one 10 s call on 1 thread, and `other_configs` for configs[0], [2] and [3].  `load` times wh_model_load of the GGUF with the file dropped from the page
 cache, and warm.
 """
 
@@ -283,6 +287,56 @@ def gemv_cold(gpu):
     return out
 
 
+def c3_long(gpu, model, seconds=7200.0, batch=16, reps=3):
+    """BASELINE configs[3] as configured: `seconds` of the long-form audio (seeded 0.3–1.5 s pauses every
+    5–20 s) cut at its pauses into ≤ 60 s segments (src/split.rs:42-65), every segment through the
+    config[1] encoder in padded batches of `batch` — the last batch holds the remainder — as the
+    reference runs every piece of a long input (src/lib.rs:844-886).  The PCM is uploaded once; each
+    segment's log-mel is made on the device (wh_model_mel) into its row of its batch's zero-filled mel
+    buffer (timed separately, `mel_ms`).  The timed region is the encoder calls of all batches, one
+    HIP-event region around them, median of `reps` passes after one warm-up pass."""
+    from wavo_amd import synth
+
+    pcm, gaps = synth.long_audio(seconds, seed=11)
+    segs = synth.split_at_gaps(len(pcm) / synth.SR, gaps)
+    pb = gpu.upload(pcm)
+    span = [(int(round(a * synth.SR)), int(round(b * synth.SR))) for a, b in segs]
+    mfs = [model.mel_frames(e - s) for s, e in span]
+    mels = 128
+    groups = [list(range(i, min(i + batch, len(segs)))) for i in range(0, len(segs), batch)]
+    frames, width = model.frames(max(mfs))
+    bufs = []
+    for g in groups:
+        mf = max(mfs[i] for i in g)
+        mb = gpu.buffer(len(g) * mf * mels)
+        bufs.append((mb, mf, [mfs[i] for i in g], len(g)))
+
+    def make_mels():
+        for (mb, mf, _, _), g in zip(bufs, groups):
+            gpu.zero(mb)
+            for j, i in enumerate(g):
+                model.mel_device(pb.offset(span[i][0]), span[i][1] - span[i][0], mb.offset(j * mf * mels))
+
+    mel_ms = time_region(gpu, make_mels, 1)
+    ob = gpu.buffer(batch * frames * width)
+
+    def run_all():
+        for mb, mf, valid, n in bufs:
+            model.encode_batch_device(mb, n, mf, valid, ob)
+
+    run_all()
+    gpu.sync()
+    ms = statistics.median(time_region(gpu, run_all, 1) for _ in range(reps))
+    del bufs, ob, pb
+    return {"segments": len(segs), "batches": len(groups), "last_batch": len(groups[-1]),
+            "segment_s": {"min": round(min(b - a for a, b in segs), 1), "max": round(max(b - a for a, b in segs), 1)},
+            "audio_s": seconds, "ms": round(ms, 3), "rtfx": round(seconds / (ms * 1e-3), 1),
+            "mel_ms": round(mel_ms, 3),
+            "what": "all batches of 16 (the last one the remainder) of 2 h of long-form audio cut at its pauses; "
+                    "encoder calls only (mel resident, made on the device beforehand: mel_ms), one HIP-event "
+                    f"region around the whole pass, median of {reps} passes after one"}
+
+
 def other_configs(gpu, model, reps=10):
     """The encoder call of BASELINE's other configurations on this GPU, HIP events around each call,
     median of `reps` after 3 warm-ups: configs[0] GigaAM-v3 shape (11 s, 275 frames), configs[2]
@@ -313,9 +367,22 @@ def other_configs(gpu, model, reps=10):
     mb, ob = gpu.upload(batch), gpu.buffer(16 * frames * width)
     valid = [x.shape[0] for x in mels]
     audio = sum(b - a for a, b in segs)
-    ms = timed(lambda: model.encode_batch_device(mb, 16, mf, valid, ob))
+    batch_step = lambda: model.encode_batch_device(mb, 16, mf, valid, ob)
+    ms = timed(batch_step)
     out["C3_parakeet_16_windows"] = {"ms": round(ms, 3), "audio_s": round(audio, 1), "rtfx": round(audio / (ms * 1e-3), 1)}
+    # Per-kernel rooflines of the batch (one call with every launch kernel-stamped): the GEMMs at
+    # m = 16 × 750 rows, where the matrix cores can be filled.
+    recs = profiled(gpu, batch_step)
+    top = sorted(recs, key=lambda r: -r["ms"])[:8]
+    out["C3_kernels"] = {r["kernel"]: {**kernel_roofline(r), "ms_per_call": round(r["ms"], 4)} for r in top}
+    gemms = [r for r in recs if GEMM_NAME.match(r["kernel"]) and r["kernel"].startswith("gemm_q8_0")]
+    dom = max(gemms, key=lambda r: r["ms"])
+    out["C3_roofline"] = {"kernel": dom["kernel"], **kernel_roofline(dom),
+                          "all_q8_0_gemms_tflops": round(sum(r["flops"] for r in gemms) /
+                                                         (sum(r["ms"] for r in gemms) * 1e-3) / 1e12, 2),
+                          "kernel_ms_per_call": round(sum(r["ms"] for r in recs), 3)}
     del mb, ob
+    out["C3_parakeet_2h"] = c3_long(gpu, model)
     # GigaAM.
     m0 = wa.Model(gpu, synth.model_path("gigaam"))
     mel0 = synth.gigaam_mel(synth.audio(11.0, seed=1))
@@ -488,6 +555,12 @@ def host_cpu():
 
 
 def cpu_baseline(path, mel, seconds, gpu_out):
+    """The C parity oracle (the restated wavo CPU backend, src/cpu/: portable f16-rounded GEMM, AVX2+FMA,
+    OpenMP over all threads) on this host: configs[1] (the step's 60 s mel and model: 2 warm-up calls,
+    then the median of 10), one 10 s call on one thread, and the other configurations — configs[0]
+    (GigaAM 11 s: median of 10 after 2), configs[2] (the Whisper encoder over one 30 s window:
+    one call: its 32 layers over a window cost ~15 s of CPU work) and configs[3] (three segments of the
+    long-form audio, each once after one warm-up call: the per-segment median)."""
     import numpy as np
 
     import oracle
@@ -496,13 +569,17 @@ def cpu_baseline(path, mel, seconds, gpu_out):
     om = oracle.Model(path)
     threads = oracle.lib().ox_threads()
     log(f"CPU baseline: oracle on {threads} threads")
-    times = []
-    want = None
-    for i in range(4):  # one warm-up, then 3 timed
-        t0 = time.perf_counter()
-        want = om.encode(mel)
-        if i:
-            times.append(time.perf_counter() - t0)
+
+    def runs(model, x, warm, timed):
+        ts, y = [], None
+        for i in range(warm + timed):
+            t0 = time.perf_counter()
+            y = model.encode(x)
+            if i >= warm:
+                ts.append(time.perf_counter() - t0)
+        return ts, y
+
+    times, want = runs(om, mel, 2, 10)
     med = statistics.median(times)
     err = float(np.linalg.norm(gpu_out - want) / np.linalg.norm(want))
     # One thread over a 10 s clip (a bounded sample of the same workload).
@@ -513,12 +590,39 @@ def cpu_baseline(path, mel, seconds, gpu_out):
     one = time.perf_counter() - t0
     oracle.lib().ox_set_threads(threads)
     log(f"CPU {med:.2f} s median on {threads} threads, {one:.2f} s for 10 s on 1 thread; rel L2 {err:.2e}")
+    others = {}
+    # the first three segments of the long-form audio, each alone (as the reference runs them).
+    pcm, gaps = synth.long_audio(3 * 60.0, seed=11)
+    segs = synth.split_at_gaps(len(pcm) / synth.SR, gaps)[:3]
+    seg_t = []
+    for a, b in segs:
+        x = synth.parakeet_mel(pcm[int(a * synth.SR):int(b * synth.SR)])
+        ts, _ = runs(om, x, 1, 1)
+        seg_t.append((b - a, ts[0]))
+    sm = statistics.median(t for _, t in seg_t)
+    others["C3_segments"] = {"value": round(sum(a for a, _ in seg_t) / sum(t for _, t in seg_t), 3), "unit": "audio s/s",
+                             "seconds_median": round(sm, 3), "segments_s": [round(a, 1) for a, _ in seg_t],
+                             "sample": "three ≤ 60 s segments of the long-form audio, each once after one warm-up call"}
+    del om
+    m0 = oracle.Model(synth.model_path("gigaam"))
+    ts, _ = runs(m0, synth.gigaam_mel(synth.audio(11.0, seed=1)), 2, 10)
+    others["C0_gigaam_11s"] = {"value": round(11.0 / statistics.median(ts), 3), "unit": "audio s/s",
+                               "seconds_median": round(statistics.median(ts), 4), "calls": len(ts)}
+    del m0
+    m2 = oracle.Model(synth.model_path("whisper"))
+    ts, _ = runs(m2, synth.whisper_mel(synth.audio(30.0, seed=2)), 0, 1)
+    others["C2_whisper_encoder_30s"] = {"value": round(30.0 / ts[0], 3), "unit": "audio s/s",
+                                        "seconds": round(ts[0], 3), "calls": 1,
+                                        "sample": "one call (~15 s of CPU work: the encoder's 32 layers over a 30 s window)"}
+    del m2
+    log(f"CPU other configs: {others}")
     return {"value": round(seconds / med, 3), "unit": "audio s/s", "cores": threads, "kind": "port",
-            "seconds_median": round(med, 3), "calls": len(times),
+            "seconds_median": round(med, 3), "seconds_min": round(min(times), 3), "calls": len(times),
             "one_thread": {"value": round(10.0 / one, 3), "unit": "audio s/s", "seconds": round(one, 3),
                            "sample": "one 10 s call"},
+            "other_configs": others,
             "host": host_cpu(),
-            "sample": f"median of 3 warm encoder calls on the same {seconds:.0f} s mel and model (after one warm-up), "
+            "sample": f"median of 10 warm encoder calls on the same {seconds:.0f} s mel and model (after 2 warm-ups), "
                       f"all threads; the restated wavo CPU backend (portable f16-rounded GEMM); GPU-vs-CPU rel L2 {err:.2e}"}
 
 
@@ -607,6 +711,20 @@ def main():
         if i >= 2:
             io.append(time.perf_counter() - t0)
     io_med = statistics.median(io)
+    # The same from page-locked host buffers (wh_host_alloc): §8(d)'s RTFx from mel H2D to output D2H.
+    pin_mel, pin_out = gpu.host_array(mel.shape), gpu.host_array((frames, width))
+    pin_mel.array[:] = mel
+    iop = []
+    for i in range(12):
+        t0 = time.perf_counter()
+        gpu.write(melb, pin_mel.array)
+        step()
+        gpu.read_into(outb, pin_out.array)
+        if i >= 2:
+            iop.append(time.perf_counter() - t0)
+    iop_med = statistics.median(iop)
+    pin_mel.free()
+    pin_out.free()
     decode = None
     if not args.no_decode:
         decode = decoders(gpu, model, host, pcm, melb, outb, mel_frames, frames, width, args.seconds)
@@ -688,6 +806,10 @@ def main():
         "hbm_copy": copy,
         "host_io": {"ms_median": round(io_med * 1e3, 3), "rtfx": round(args.seconds / io_med, 1),
                     "what": "mel upload (pageable host memory) + encoder call + output read-back, host clock"},
+        "host_io_pinned": {"ms_median": round(iop_med * 1e3, 3), "rtfx": round(args.seconds / iop_med, 1),
+                           "calls": len(iop),
+                           "what": "mel upload from page-locked host memory (wh_host_alloc) + encoder call + output "
+                                   "read-back into page-locked memory, host clock, median of 10 after 2"},
         "host_frontend_ms": round(statistics.median(fe) * 1e3, 2),
         **(decode or {}),
         "load": load,

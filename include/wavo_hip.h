@@ -65,6 +65,11 @@ int wh_device_info(wh_ctx *ctx, char *name, size_t name_len, int *compute_units,
 /* Gpu::buffer / readback (src/gpu/mod.rs:675-697): n_f32 floats of device memory, uninitialized. */
 int wh_alloc(wh_ctx *ctx, size_t n_f32, float **dptr);
 int wh_free(wh_ctx *ctx, void *dptr);
+/* Page-locked host memory for wh_write / wh_read (the DMA engines copy it without a bounce buffer):
+ * the counterpart of the mapped staging and readback buffers of Gpu::write and Gpu::run
+ * (src/gpu/mod.rs:687-697, :741-750, :969-1002).  wh_host_free waits for the queued work first. */
+int wh_host_alloc(wh_ctx *ctx, size_t bytes, void **host);
+int wh_host_free(wh_ctx *ctx, void *host);
 /* Gpu::write / upload (src/gpu/mod.rs:741-750): bytes from host memory, complete on return. */
 int wh_write(wh_ctx *ctx, void *dst, const void *src, size_t bytes);
 /* Device-to-device copy on the stream. */
@@ -169,8 +174,10 @@ int wh_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, 
  * The same kernels and results as wh_gemm; the f16 copy of `a` and the split-k partial sums go to a
  * fixed workspace of wh_gemm_noalloc_limit() bytes (32 MiB) that each device holds for the life of
  * the process, instead of the context's growable scratch.  A call whose workspace would exceed it
- * returns WH_EARG without launching.  Calls on one device share the workspace: calls that overlap
- * on a device (other streams or contexts) race.  Not while per-launch profiling (wh_profile 1) is on. */
+ * returns WH_EARG without launching.  Calls on one device share the workspace, so callers must
+ * serialize them: a call from another stream (or context) while the device's previous call may still
+ * be running is refused with WH_EARG (calls under stream capture are not checked; their replays must
+ * not overlap either).  Not while per-launch profiling (wh_profile 1) is on. */
 int wh_gemm_noalloc(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, int epi, float alpha);
 size_t wh_gemm_noalloc_limit(void);
 /* Pass::gemv (src/gpu/mod.rs:1461-1467): c[offset + j] = epi(a·W[j] + b[j]) for one row a, W not

@@ -47,3 +47,30 @@ def test_null_context_arguments_are_rejected():
     assert L.wh_gemm(None, None, None, None, 1, 0, 0.0) == wa.EARG
     assert L.wh_linear_width(None) == 0
     assert L.wh_attend_len(4100, 2, 40) == 17 * 2 * 42
+
+
+def test_static_library_links_a_c_program(tmp_path):
+    # libwavo_hip.a, the library a host program links (the Rust shim's build script does): a C program
+    # that includes the header and calls the ABI links against it with the HIP runtime alone and runs
+    # (without a GPU, wh_open reports the error; on a GPU box it opens device 0).
+    lib_a = os.path.join(ROOT, "wavo_amd", "libwavo_hip.a")
+    assert os.path.exists(lib_a), "build the library first (__graft_entry__.build)"
+    src = tmp_path / "main.c"
+    src.write_text(r'''
+#include <stdio.h>
+#include "wavo_hip.h"
+int main(void) {
+  wh_ctx *ctx = NULL;
+  int rc = wh_open(-1, &ctx);
+  printf("limit %zu open %d %s\n", wh_gemm_noalloc_limit(), rc, rc ? wh_last_error(NULL) : "ok");
+  if (!rc) wh_close(ctx);
+  return 0;
+}
+''')
+    exe = tmp_path / "main"
+    import subprocess
+    subprocess.run(["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-x", "c++", str(src), "-x", "none", lib_a,
+                    "-I", os.path.join(ROOT, "include"), "-o", str(exe)], check=True, capture_output=True, timeout=300)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.startswith(f"limit {32 << 20} open "), out.stdout

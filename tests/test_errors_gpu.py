@@ -63,3 +63,20 @@ def test_bad_shapes_leave_context_usable(gpu):
         gpu.linear([(w.tobytes(), gguf.F32, 64, 64), (w[:, :32].copy().tobytes(), gguf.F32, 32, 64)])
     assert e.value.code == wa.EARG
     still_works(gpu)
+
+
+def test_whisper_window_past_the_model(gpu):
+    # More encoder frames than the model's window: refused with a message naming both counts, before
+    # the decoder's buffers exist; a fitting call afterwards works.
+    from wavo_amd import synth
+
+    m = wa.Model(gpu, synth.model_path("whisper", small=True))
+    frames, width = m.frames(1)  # Whisper: the model's window, whatever the mel
+    enc = gpu.buffer((frames + 64) * width)
+    with pytest.raises(wa.WavoError) as e:
+        m.whisper_begin(enc, frames + 64)
+    assert e.value.code == wa.EARG and f"{frames + 64} encoder frames" in str(e.value)
+    gpu.zero(enc)
+    m.whisper_begin(enc, frames)
+    m.free()
+    still_works(gpu)

@@ -315,6 +315,44 @@ def test_parakeet_batch16(gpu):
     print(f"16 windows of {[round(b - a, 1) for a, b in segs]} s: worst rel L2 {worst:.2e}, TDT near-tie flips {flips}")
 
 
+def test_parakeet_batch_ragged(gpu):
+    """A batch of 3 windows of different lengths (the remainder batch of configs[3]'s long input, which
+    the reference runs piece by piece, src/lib.rs:844-886): each window's valid frames against the
+    oracle's encoder on that window alone, and its TDT tokens; then the same three windows in the other
+    order, which must give each window the same output bit for bit."""
+    path = synth.model_path("parakeet", directory=MODELS)
+    clips = [synth.audio(47.3, seed=21), synth.audio(12.3, seed=22), synth.audio(31.1, seed=23)]
+    mels = [synth.parakeet_mel(c) for c in clips]
+    mf = max(x.shape[0] for x in mels)
+    om, m = ox.Model(path), wa.Model(gpu, path)
+    frames, width = m.frames(mf)
+
+    def run(order):
+        batch = np.zeros((len(order), mf, mels[0].shape[1]), np.float32)
+        for j, i in enumerate(order):
+            batch[j, :mels[i].shape[0]] = mels[i]
+        mb, ob = gpu.upload(batch), gpu.buffer(len(order) * frames * width)
+        m.encode_batch_device(mb, len(order), mf, [mels[i].shape[0] for i in order], ob)
+        out = gpu.read(ob, (len(order), frames, width))
+        return {i: out[j] for j, i in enumerate(order)}
+
+    got = run([0, 1, 2])
+    flips = []
+    for i, x in enumerate(mels):
+        want = om.encode(x)
+        g = got[i][:want.shape[0], :want.shape[1]]
+        err = rel_l2(g, want)
+        assert err < ENCODER_TOL, (i, err)
+        flip = check_tdt(m, om, g, want)
+        if flip is not None:
+            flips.append((i, flip))
+    back = run([2, 1, 0])
+    for i, x in enumerate(mels):
+        rows = m.frames(x.shape[0])[0]  # the window's own encoder frames
+        assert np.array_equal(back[i][:rows], got[i][:rows]), f"window {i} differs with its position in the batch"
+    print(f"3 windows of {[round(len(c) / synth.SR, 1) for c in clips]} s: TDT near-tie flips {flips}")
+
+
 @pytest.mark.parametrize("name", ["parakeet", "gigaam", "whisper"])
 def test_graph_replays_equal_eager_calls(gpu, name):
     # The second call with the same buffers is recorded into a HIP graph and later ones replay it.

@@ -1,7 +1,8 @@
 """wh_gemm_noalloc, the GEMM entry point that allocates nothing (its workspace is a fixed device array),
 against wh_gemm, the entry point it varies, through the C ABI: bit for bit equal outputs on two calls in
-a row, the second with a smaller input (the workspace keeps the first call's contents), and a call whose
-workspace would exceed the limit refused without launching."""
+a row, the second with a smaller input (the workspace keeps the first call's contents), a call whose
+workspace would exceed the limit refused without launching, and a call from another stream refused
+while the device's previous call may still run."""
 
 import ctypes
 
@@ -64,3 +65,32 @@ def test_noalloc_refuses_past_its_workspace(gpu):
     small = gpu.upload(np.ones((16, k), np.float32))
     assert noalloc(gpu, small, lin, c, 16, wa.BIAS) == 0
     gpu.sync()
+
+
+def test_noalloc_refuses_an_overlapping_call_from_another_stream(gpu):
+    # Two contexts on device 0, each with its own stream: while the first context's queued calls may
+    # still run, a call from the second is refused (the workspace is shared); once the first has
+    # drained, the second's call runs and equals wh_gemm.
+    # ~80 µs of kernels per call (no k split: 8 MB of workspace), more than the ~20 µs a call takes to queue
+    m, n, k = 2048, 4096, 2048
+    other = wa.Gpu(0)
+    try:
+        lin1, lin2 = layer(gpu, n, k, wa.Q8_0, 5), layer(other, n, k, wa.Q8_0, 5)
+        rng = np.random.default_rng(6)
+        x = rng.standard_normal((m, k), dtype=np.float32)
+        a1, a2 = gpu.upload(x), other.upload(x)
+        c1, c2, want_b = gpu.buffer(m * lin1.width), other.buffer(m * lin2.width), other.buffer(m * lin2.width)
+        gpu.sync()
+        for _ in range(40):  # a backlog of ~2 ms queued on the first context's stream
+            assert noalloc(gpu, a1, lin1, c1, m, wa.BIAS) == 0, wa.lib().wh_last_error(gpu.h).decode()
+        rc = noalloc(other, a2, lin2, c2, m, wa.BIAS)
+        assert rc == wa.EARG, "an overlapping call from another stream was accepted"
+        assert "overlap" in wa.lib().wh_last_error(other.h).decode()
+        gpu.sync()
+        assert noalloc(other, a2, lin2, c2, m, wa.BIAS) == 0, wa.lib().wh_last_error(other.h).decode()
+        other.gemm(a2, lin2, want_b, m, wa.BIAS)
+        got, want = other.read(c2, (m, lin2.width)), other.read(want_b, (m, lin2.width))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        other.sync()
+    finally:
+        other.close()

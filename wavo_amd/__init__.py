@@ -33,6 +33,8 @@ SIGNATURES = {
     "wh_device_info": (_i, [_vp, ctypes.c_char_p, _sz, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "wh_alloc": (_i, [_vp, _sz, ctypes.POINTER(_vp)]),
     "wh_free": (_i, [_vp, _vp]),
+    "wh_host_alloc": (_i, [_vp, _sz, ctypes.POINTER(_vp)]),
+    "wh_host_free": (_i, [_vp, _vp]),
     "wh_write": (_i, [_vp, _vp, _vp, _sz]),
     "wh_copy": (_i, [_vp, _vp, _vp, _sz]),
     "wh_zero": (_i, [_vp, _vp, _sz]),
@@ -142,6 +144,31 @@ class Buffer:
     def offset(self, floats):
         """A raw pointer `floats` f32 into the buffer."""
         return self.ptr + 4 * floats
+
+
+class HostArray:
+    """Page-locked host memory from wh_host_alloc, viewed as a numpy array (`.array`)."""
+
+    def __init__(self, gpu, shape, dtype=np.float32):
+        self.gpu = gpu
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        p = _vp()
+        gpu._check(lib().wh_host_alloc(gpu.h, n, ctypes.byref(p)))
+        self.ptr = p.value
+        buf = (ctypes.c_uint8 * max(n, 1)).from_address(self.ptr)
+        self.array = np.frombuffer(buf, dtype=dtype, count=int(np.prod(shape))).reshape(shape)
+
+    def free(self):
+        if getattr(self, "ptr", None) and self.gpu.h:
+            self.array = None
+            lib().wh_host_free(self.gpu.h, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 class Linear:
@@ -336,6 +363,14 @@ class Gpu:
         out = np.empty(shape, dtype)
         self._check(lib().wh_read(self.h, out.ctypes.data, _p(buf) + offset_bytes, out.nbytes))
         return out
+
+    def host_array(self, shape, dtype=np.float32):
+        """Page-locked host memory (HostArray; its numpy view is `.array`)."""
+        return HostArray(self, shape, dtype)
+
+    def read_into(self, buf, out, offset_bytes=0):
+        """wh_read into an existing C-contiguous numpy array (e.g. a HostArray's)."""
+        self._check(lib().wh_read(self.h, out.ctypes.data, _p(buf) + offset_bytes, out.nbytes))
 
     def copy(self, dst, src, nbytes):
         """Device-to-device copy of nbytes with the library's copy kernel."""

@@ -222,26 +222,38 @@ int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m
 constexpr size_t NOALLOC_BYTES = (size_t)32 << 20;
 static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
 
+namespace {
+constexpr int NOALLOC_DEVICES = 64;
+// Per device: the workspace address, the failed lookup's error, and the last call's stream with an
+// event recorded after its kernels (created at set-up, with the address).
+struct NoallocDevice {
+  void *addr = nullptr;
+  hipError_t err = hipSuccess;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+};
+std::mutex noalloc_mu;
+NoallocDevice noalloc_dev[NOALLOC_DEVICES];
+}  // namespace
+
 int gemm_noalloc_init(wh_ctx *ctx) {
-  constexpr int MAX_DEVICES = 64;
-  static std::mutex mu;
-  static void *addr[MAX_DEVICES] = {};
-  static hipError_t err[MAX_DEVICES] = {};
-  std::lock_guard<std::mutex> lock(mu);
+  std::lock_guard<std::mutex> lock(noalloc_mu);
   ctx->noalloc = nullptr;
-  if (ctx->device < 0 || ctx->device >= MAX_DEVICES) return WH_EGPU;
-  if (!addr[ctx->device] && err[ctx->device] == hipSuccess) {
+  if (ctx->device < 0 || ctx->device >= NOALLOC_DEVICES) return WH_EGPU;
+  NoallocDevice &d = noalloc_dev[ctx->device];
+  if (!d.addr && d.err == hipSuccess) {
     void *p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && p) e = hipEventCreateWithFlags(&d.done, hipEventDisableTiming);
     if (e != hipSuccess || !p) {
       (void)hipGetLastError();
-      err[ctx->device] = e != hipSuccess ? e : hipErrorInvalidSymbol;
+      d.err = e != hipSuccess ? e : hipErrorInvalidSymbol;
     } else {
-      addr[ctx->device] = p;
+      d.addr = p;
     }
   }
-  ctx->noalloc = addr[ctx->device];
-  ctx->noalloc_error = ctx->noalloc ? hipSuccess : err[ctx->device];
+  ctx->noalloc = d.addr;
+  ctx->noalloc_error = ctx->noalloc ? hipSuccess : d.err;
   return ctx->noalloc ? WH_OK : WH_EGPU;
 }
 
@@ -261,7 +273,33 @@ int wh_gemm_noalloc(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, i
   if (need > NOALLOC_BYTES)
     return wh_fail(ctx, WH_EARG, "wh_gemm_noalloc: %d x %d x %d needs %zu bytes of workspace, more than its %zu", m,
                    l->rows, l->k, need, NOALLOC_BYTES);
-  return gemm_f32_ws(ctx, a, l, c, m, ldc, epi, alpha, (uint8_t *)ctx->noalloc);
+  // The workspace is shared by every call on the device: a call from another stream while the last
+  // call's kernels may still run would corrupt both, so it is refused (calls must be serialized).  A
+  // stream under capture is neither checked nor remembered (its kernels run at replay).
+  std::lock_guard<std::mutex> lock(noalloc_mu);
+  NoallocDevice &d = noalloc_dev[ctx->device];
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(ctx->stream, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    cs = hipStreamCaptureStatusNone;
+  }
+  const bool capturing = cs != hipStreamCaptureStatusNone;
+  if (!capturing && d.last && d.last != ctx->stream) {
+    const hipError_t q = hipEventQuery(d.done);
+    if (q != hipSuccess) {
+      (void)hipGetLastError();
+      if (q == hipErrorNotReady)
+        return wh_fail(ctx, WH_EARG,
+                       "wh_gemm_noalloc: the last call on device %d (another stream) may still be running; its "
+                       "workspace is shared, so calls on one device must not overlap", ctx->device);
+    }
+  }
+  const int rc = gemm_f32_ws(ctx, a, l, c, m, ldc, epi, alpha, (uint8_t *)ctx->noalloc);
+  if (rc == WH_OK && !capturing) {
+    if (hipEventRecord(d.done, ctx->stream) == hipSuccess) d.last = ctx->stream;
+    else (void)hipGetLastError();
+  }
+  return rc;
 }
 
 int launch_to_half(wh_ctx *ctx, const float *x, void *y, size_t n) {

@@ -516,6 +516,7 @@ struct wh_model {
   struct Graph {
     std::vector<intptr_t> key;
     hipGraphExec_t exec = nullptr;
+    hipGraph_t graph = nullptr;  // kept for the life of its exec (as a recorded pass keeps it)
   };
   std::vector<Graph> graphs;
   std::vector<intptr_t> pending;  // the arguments of the last eager call
@@ -825,8 +826,24 @@ std::vector<float> rope_table(int frames, int hd, double theta) {
 int parakeet_frames(int mel_frames) { return half_len(half_len(half_len(mel_frames - 1))); }
 
 // Grows the arena to `frames` encoder frames × `batch` windows (rounded up to 64 frames).
+// A recorded graph is destroyed only once the stream has drained: a launch of it may still be queued
+// (replays are asynchronous), and destroying an exec with a pending launch leaves the runtime (and
+// any tool that follows the launch, such as a kernel tracer) holding freed state.
+// The graph the exec was instantiated from lives as long as the exec: a launch tracer can refer back
+// to the graph's nodes when the exec is launched (a kernel trace of the replayed TDT loop and window
+// search read freed memory when the graph was destroyed right after instantiation).
+void destroy_graph(wh_model *m, hipGraphExec_t exec, hipGraph_t graph, bool &drained) {
+  if (!drained) {
+    (void)hipStreamSynchronize(m->ctx->stream);
+    drained = true;
+  }
+  (void)hipGraphExecDestroy(exec);
+  if (graph) (void)hipGraphDestroy(graph);
+}
+
 void drop_graphs(wh_model *m) {
-  for (auto &g : m->graphs) (void)hipGraphExecDestroy(g.exec);
+  bool drained = false;
+  for (auto &g : m->graphs) destroy_graph(m, g.exec, g.graph, drained);
   m->graphs.clear();
   m->pending.clear();
 }
@@ -1081,23 +1098,28 @@ int run_recorded(wh_model *m, std::vector<intptr_t> key, F &&record) {
   hipError_t e = hipStreamEndCapture(c->stream, &graph);
   hipGraphExec_t exec = nullptr;
   if (rc == WH_OK && e == hipSuccess && graph) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-  if (graph) (void)hipGraphDestroy(graph);
+  if (rc != WH_OK || e != hipSuccess || !exec) {
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+  }
   if (rc != WH_OK) return rc;
   if (e != hipSuccess || !exec) {  // recording failed: stay eager for this model
     (void)hipGetLastError();
     m->use_graph = false;
     return record();
   }
-  // Stale generations are never matched again: drop them, and keep at most 8 recordings.
+  // Stale generations are never matched again: drop them, and keep at most 8 recordings (each
+  // destroyed once its queued launches are done).
+  bool drained = false;
   for (size_t i = 0; i < m->graphs.size();)
     if (m->graphs[i].key[m->graphs[i].key.size() - 2] != m->epoch ||
         m->graphs[i].key.back() != c->scratch_epoch || m->graphs.size() >= 8) {
-      (void)hipGraphExecDestroy(m->graphs[i].exec);
+      destroy_graph(m, m->graphs[i].exec, m->graphs[i].graph, drained);
       m->graphs.erase(m->graphs.begin() + i);
     } else {
       i++;
     }
-  m->graphs.push_back({key, exec});
+  m->graphs.push_back({key, exec, graph});
   e = hipGraphLaunch(exec, c->stream);
   if (e != hipSuccess) return wh_fail(c, WH_EGPU, "graph launch: %s", hipGetErrorString(e));
   return WH_OK;
@@ -1845,6 +1867,9 @@ int wh_whisper_begin(wh_model *m, const float *enc, int frames) {
   if (!m || !enc || frames <= 0 || m->arch != WHISPER) return WH_EARG;
   const int d = m->d;
   wh_ctx *c = m->ctx;
+  if (frames > m->frames)  // before anything is allocated
+    return wh_fail(c, WH_EARG, "wh_whisper_begin: %d encoder frames, more than the model's window of %d", frames,
+                   m->frames);
   if (m->own.empty()) {
     for (int i = 0; i < m->dec_layers; i++) {
       float *a = nullptr, *b = nullptr;
@@ -1867,7 +1892,6 @@ int wh_whisper_begin(wh_model *m, const float *enc, int frames) {
     (void)vp;
     if (!m->dx || !m->dy || !m->dqkv || !m->dh || !m->datt || !m->dpart || !m->dscratch) return WH_EOOM;
   }
-  if (frames > m->frames) return WH_EARG;
   // Decoder::record_cross (src/transformer.rs:243-248).
   for (int i = 0; i < m->dec_layers; i++) {
     CK(lin(m, enc, m->dl[i].cross_kv, m->dscratch, frames, WH_BIAS));

@@ -304,6 +304,30 @@ int wh_free(wh_ctx *ctx, void *dptr) {
   return WH_OK;
 }
 
+int wh_host_alloc(wh_ctx *ctx, size_t bytes, void **host) {
+  if (!ctx || !host) return WH_EARG;
+  (void)hipSetDevice(ctx->device);
+  void *p = nullptr;
+  hipError_t e = hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return wh_fail(ctx, e == hipErrorOutOfMemory ? WH_EOOM : WH_EGPU, "hipHostMalloc of %zu bytes: %s", bytes,
+                   hipGetErrorString(e));
+  }
+  *host = p;
+  return WH_OK;
+}
+
+int wh_host_free(wh_ctx *ctx, void *host) {
+  if (!ctx) return WH_EARG;
+  if (!host) return WH_OK;
+  (void)hipSetDevice(ctx->device);
+  (void)hipStreamSynchronize(ctx->stream);  // no queued copy from or into it
+  hipError_t e = hipHostFree(host);
+  if (e != hipSuccess) return wh_fail(ctx, WH_EGPU, "hipHostFree: %s", hipGetErrorString(e));
+  return WH_OK;
+}
+
 int wh_write(wh_ctx *ctx, void *dst, const void *src, size_t bytes) {
   if (!ctx || (!dst && bytes) || (!src && bytes)) return WH_EARG;
   if (!bytes) return WH_OK;

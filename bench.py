@@ -60,6 +60,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "encoder RTFx (audio s/s) at 1 MI355X; q8_0 GEMM % MFMA peak; GEMV % HBM BW"
+GRAPHS = True  # --no-graphs: every model launches its kernels eagerly (for rocprofv3 kernel traces)
 PEAK_F16 = 2500.0     # TFLOP/s, MI355X dense fp16 MFMA
 PEAK_HBM = 8000.0     # GB/s
 GEMM_NAME = re.compile(r"^gemm_(\w+?)_(\d+)x(\d+)_w(\d+)x(\d+)_n(\d+)(_s\d)? (\d+)x(\d+)x(\d+) e(\d+) (f16|f32) w(\d+)$")
@@ -416,6 +417,8 @@ def decode_steps(gpu, tokens=224, search=True):
     t0 = time.time()
     path = synth.model_path("whisper")
     m = wa.Model(gpu, path)
+    if not GRAPHS:
+        m.graphs(False)
     log(f"whisper model ready in {time.time() - t0:.1f} s")
     cfg = synth.CONFIGS["whisper"]
     frames, d, vocab = cfg["frames"], cfg["d"], cfg["vocab"]
@@ -637,11 +640,15 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the encoder timings of the other BASELINE configs")
     ap.add_argument("--no-decode", action="store_true", help="skip the TDT decode and audio-to-tokens timings")
     ap.add_argument("--no-search", action="store_true", help="skip the Whisper window search after the decoder steps")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="launch every kernel eagerly instead of replaying recorded HIP graphs (kernel traces)")
     ap.add_argument("--replay", metavar="NAME", default=None,
                     help="only the back-to-back launches of this GEMM configuration (a roofline.kernel value), "
                          "or 'attention_rel' for the Parakeet attention call, for rocprofv3 passes over exactly "
                          "those launches")
     args = ap.parse_args()
+    global GRAPHS
+    GRAPHS = not args.no_graphs
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path (asked for {max(args.gpus, world)}). "
@@ -675,6 +682,8 @@ def main():
     gpu = wa.Gpu(0)
     load = load_times(wa, gpu, path)
     model = wa.Model(gpu, path)
+    if not GRAPHS:
+        model.graphs(False)
     log(f"loaded on {gpu.name or 'gfx950'} ({gpu.cus} CUs): {load}")
     pcm = synth.audio(args.seconds, seed=1)
     fe = []

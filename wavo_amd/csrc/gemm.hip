@@ -63,10 +63,12 @@ GemmPlan gemm_plan_for(const wh_ctx *ctx, int m, int cols, int k) {
     // workgroups, 3.13 against 3.22).
     p = {128, 128, 2, 2, 2, 1};
   else if (t128 * 4 >= 3L * cus)
-    // Three quarters of a tile per CU or more (the FFN's first projection at 750 frames): 128×128
-    // tiles; fewer (the qkv projection, 144 tiles) run faster as 64×64 tiles (4.96 against 4.98 ms
-    // per 60 s call).
-    p = {128, 128, 2, 4, 3, 1};
+    // Three quarters of a tile per CU or more (the FFN's first projection at 750 frames): 96×128 tiles
+    // of one row of 4 wavefronts (96×32 each: every W fragment dequantized once per workgroup and fed
+    // to three MFMAs; 256 workgroups, one per CU) for k ≥ 1024 (60 s step 4.285 against 4.324 ms for
+    // 128×128 tiles of 2×4), else 128×128 tiles; fewer tiles (the qkv projection, 144) run faster as
+    // 64×64 tiles (4.96 against 4.98 ms per 60 s call; 96×128 tiles for it: 4.51 against 4.32).
+    p = k >= 1024 ? GemmPlan{96, 128, 1, 4, 3, 1} : GemmPlan{128, 128, 2, 4, 3, 1};
   else if (t128 * 4 <= cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
     // Long k over few tiles (the FFN's down projection, 750 × 1024 × 4096): k split 4 ways over
     // 96×64 tiles of 2 wavefronts (96×32 per wavefront: each dequantized W fragment feeds three

@@ -397,21 +397,6 @@ __device__ __forceinline__ void unrolled_steps(F &f, int kt0, int nk) {
   }
 }
 
-// Scheduling groups for one substep: NM MFMAs one at a time, the ND LDS reads spread over the first
-// half of them and the NV VALU instructions over all of them.
-template <int NM, int ND, int NV, int T = 0>
-__device__ __forceinline__ void sched_interleave() {
-  if constexpr (T < NM) {
-    constexpr int H = NM / 2 > 0 ? NM / 2 : 1;
-    constexpr int d = T < H ? (ND * (T + 1) + H - 1) / H - (ND * T + H - 1) / H : 0;
-    constexpr int v = (NV * (T + 1) + NM - 1) / NM - (NV * T + NM - 1) / NM;
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
-    if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);  // LDS read
-    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x002, v, 0);  // VALU
-    sched_interleave<NM, ND, NV, T + 1>();
-  }
-}
-
 // f(integral_constant<I>) for I = B, B + S, .. < E.
 template <int B, int E, int S, class F>
 __device__ __forceinline__ void static_for(F &&f) {
@@ -806,66 +791,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
       return dequant_frag<WT>(w[j], sh, half2{d, d}, s);
     }
   };
-#pragma unroll
-  for (int s = 0; s < NS; s++)
-    if (s < nk) issue(s, s);
-  if constexpr (PIPE == 1) {
-    // W one substep ahead: the fragments of substep s + 1 are dequantized (and its a fragments read)
-    // while the MFMAs of substep s run, so no MFMA waits for the VALU that makes its operand; the
-    // scheduling groups interleave one MFMA at a time with its share of the LDS reads and the VALU.
-    uint32_t wq[TN][ND], sc[TN][NSC];
-    half8 af[2][TM], bq[2][TN];
-    auto deq = [&](half8 (&b)[TN], auto s_c) {
-#pragma unroll
-      for (int j = 0; j < TN; j++) b[j] = wfrag(wq, sc, j, s_c);
-    };
-    auto mm = [&](const half8 (&f)[TM], const half8 (&b)[TN]) {
-#pragma unroll
-      for (int j = 0; j < TN; j++)
-#pragma unroll
-        for (int i = 0; i < TM; i++) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], b[j], acc[i][j], 0, 0, 0);
-    };
-    constexpr int VQ = WCH ? 0 : (Q8 ? 12 : 10) * TN;  // VALU of one substep's dequantization
-    if (nk > 0) {
-      if (nk >= NS) wait_vm<(NS - 1) * PI>();  // stages 1 .. NS - 1 may be in flight
-      else dma_wait();
-      __syncthreads();
-      read_w(wq, sc, 0);
-      read_a(af[0], 0, 0);
-      deq(bq[0], std::integral_constant<int, 0>{});
-    }
-    auto step = [&](auto S_c, int kt) {
-      constexpr int S = decltype(S_c)::value, slot = S % NS;
-      read_a(af[1], slot, 1);
-      deq(bq[1], std::integral_constant<int, 1>{});
-      mm(af[0], bq[0]);
-      sched_interleave<TM * TN, TM, VQ>();
-      read_a(af[0], slot, 2);
-      deq(bq[0], std::integral_constant<int, 2>{});
-      mm(af[1], bq[1]);
-      sched_interleave<TM * TN, TM, VQ>();
-      read_a(af[1], slot, 3);
-      deq(bq[1], std::integral_constant<int, 3>{});
-      mm(af[0], bq[0]);
-      sched_interleave<TM * TN, TM, VQ>();
-      if (kt + 1 < nk) {
-        // Stage kt + 1 has landed for every wave, and every wave is done reading slot kt.
-        if (kt + NS - 1 < nk) wait_vm<(NS - 2) * PI>();  // stages kt + 2 .. kt + NS - 1 may be in flight
-        else dma_wait();
-        __syncthreads();
-        if (kt + NS < nk) issue(kt + NS, slot);  // into the slot this step has finished reading
-      }
-      // The next step's W data, a fragments and first W fragments (after the last step: read from a
-      // stale slot and never used), beside the last substep's MFMAs.
-      mm(af[1], bq[1]);
-      read_w(wq, sc, (slot + 1) % NS);
-      read_a(af[0], (slot + 1) % NS, 0);
-      deq(bq[0], std::integral_constant<int, 0>{});
-      sched_interleave<TM * TN, TM + TN * (WCH ? 4 : ND + NSC), VQ>();
-    };
-    constexpr int UNR = NS % 2 ? 2 * NS : NS;
-    for (int kt0 = 0; kt0 < nk; kt0 += UNR) unrolled_steps<0, UNR>(step, kt0, nk);
-  } else if constexpr (PIPE == 2) {
+  if constexpr (PIPE == 2) {
     // Ping-pong.  Two groups of four wavefronts (group 1 = waves 4-7; a workgroup's wavefronts go to
     // the SIMDs round-robin, so every SIMD holds one of each) take turns, offset by half a step: while
     // one group runs the 4·TM·TN MFMAs of a k step from registers (its a fragments read one substep
@@ -956,6 +882,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
     for (int kt0 = 0; kt0 < nk; kt0 += UNR) unrolled_steps<0, UNR>(step, kt0, nk);
     dma_wait();  // the repeated stages of the last steps, before the epilogue reuses the LDS
   } else {
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+      if (s < nk) issue(s, s);
     uint32_t wq[2][TN][ND], sc[2][TN][NSC];
     half8 af[2][TM];
     // Substep s of a step: dequantize the lane's W fragment (quantized) and run the TM × TN MFMAs.
@@ -1119,15 +1048,8 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     PLAN(96, 64, 1, 2, 2)
     PLAN(192, 128, 2, 2, 2)
     PLAN(256, 256, 2, 4, 2)
-    PLANP(256, 256, 2, 2, 2, 1)
-    PLANP(256, 128, 2, 2, 2, 1)
-    PLANP(128, 256, 2, 2, 2, 1)
-    PLANP(256, 256, 2, 4, 2, 1)
-    PLANP(128, 128, 2, 4, 2, 1)
-    PLANP(192, 128, 2, 2, 2, 1)
-    PLANP(256, 256, 2, 4, 3, 2)
-    PLANP(256, 128, 2, 4, 3, 2)
-    PLANP(128, 256, 2, 4, 3, 2)
+    PLAN(96, 128, 1, 4, 3)
+    PLANP(256, 256, 2, 4, 3, 2)  // the ping-pong loop (tuning only: not faster than the plain one)
 #undef PLAN
 #undef PLANP
     if (!ok) return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages", p.bm, p.bn, p.wm, p.wn, p.ns);

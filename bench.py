@@ -63,7 +63,7 @@ METRIC = "encoder RTFx (audio s/s) at 1 MI355X; q8_0 GEMM % MFMA peak; GEMV % HB
 GRAPHS = True  # --no-graphs: every model launches its kernels eagerly (for rocprofv3 kernel traces)
 PEAK_F16 = 2500.0     # TFLOP/s, MI355X dense fp16 MFMA
 PEAK_HBM = 8000.0     # GB/s
-GEMM_NAME = re.compile(r"^gemm_(\w+?)_(\d+)x(\d+)_w(\d+)x(\d+)_n(\d+)(_s\d)? (\d+)x(\d+)x(\d+) e(\d+) (f16|f32) w(\d+)$")
+GEMM_NAME = re.compile(r"^gemm_(\w+?)_(\d+)x(\d+)_w(\d+)x(\d+)_n(\d+)(_s\d)?(_p\d)?(_k\d)? (\d+)x(\d+)x(\d+) e(\d+) (f16|f32) w(\d+)$")
 MFMA_KERNELS = ("attention", "attention_rel")
 
 
@@ -127,13 +127,14 @@ def gemm_replay(name, reps=50):
     from wavo_amd import gguf
 
     g = GEMM_NAME.match(name)
-    tn, bm, bn, wm, wn, ns, split, m, n, k, epi, out, width = g.groups()
+    tn, bm, bn, wm, wn, ns, split, pipe, kgroups, m, n, k, epi, out, width = g.groups()
     wtype = {"q8_0": wa.Q8_0, "q4_0": wa.Q4_0, "f16": wa.F16}[tn]
     rng = np.random.default_rng(5)
     w = gguf.encode(rng.standard_normal(int(n) * int(k), dtype=np.float32) * np.float32(0.02), wtype)
     f16 = out == "f16"
     g2 = wa.Gpu(0)
-    g2.tune("gemm_plan", f"{bm},{bn},{wm},{wn},{ns},{split[2:] if split else 1}")  # the plan of the step
+    g2.tune("gemm_plan", f"{bm},{bn},{wm},{wn},{ns},{split[2:] if split else 1},"  # the plan of the step
+                         f"{pipe[2:] if pipe else 0},{kgroups[2:] if kgroups else 1}")
     # A split GEMM's kernel alone, as it runs in the step (where the following fused LayerNorm kernel
     # adds the partial sums); a C-ABI call would add its own finishing kernel.
     g2.tune("gemm_kernel_only", 1)

@@ -86,8 +86,9 @@ void *wh_stream(wh_ctx *ctx);
 /* Tuning and measurement overrides (no counterpart in the reference, whose kernel choices are fixed
  * per device tier, src/gpu/mod.rs:50-107).  Only an explicit call changes them; a fresh context
  * chooses every launch plan itself.  Keys:
- *   "gemm_plan"        "bm,bn,wm,wn,slots,split[,pipeline]" for every GEMM of the main kernel ("" clears);
- *   "gemm_shape_plans" "m,cols,k:bm,bn,wm,wn,slots,split[,pipeline];..." per call shape ("" clears);
+ *   "gemm_plan"        "bm,bn,wm,wn,slots,split[,pipeline[,kgroups]]" for every GEMM of the main kernel
+ *                      ("" clears);
+ *   "gemm_shape_plans" "m,cols,k:bm,bn,wm,wn,slots,split[,pipeline[,kgroups]];..." per call shape ("" clears);
  *   "gemm_kernel_only" "1": a k-split GEMM call stops after its GEMM kernel and leaves c unwritten
  *                      (to time that kernel alone, as a model step runs it); "0" restores;
  *   "attn_split"       "n": attention splits its key range n ways (0 = chosen per shape);

@@ -112,6 +112,42 @@ def test_gemm_more_tiles_than_cus(gpu, m, n, k):
         c0 = gpu.read(cb, (m, n))
 
 
+# Every kernel variant the GEMM builds: tile, wavefronts per tile row and column, ring slots, k split,
+# loop variant (2: ping-pong), k groups — forced through wh_tune("gemm_plan") on one shape with edge
+# tiles in both directions and dual columns.
+PLANS = ["128,128,2,4,3,1", "64,64,2,2,3,1", "128,128,2,4,2,1", "128,128,2,2,2,1", "256,128,4,2,2,1",
+         "96,64,1,2,2,1", "192,128,2,2,2,1", "256,256,2,4,2,1", "96,128,1,4,3,1", "256,256,2,4,3,1,2",
+         "64,64,2,2,4,1,0,2", "96,64,1,2,2,1,0,2", "96,128,1,4,3,1,0,2",
+         "96,64,1,2,2,4", "128,128,2,2,2,4", "64,64,2,2,3,2", "64,64,2,2,4,2,0,2", "96,64,1,2,2,4,0,2"]
+
+
+@pytest.mark.parametrize("wtype", [wa.Q8_0, wa.Q4_0, wa.F16])
+@pytest.mark.parametrize("plan", PLANS)
+def test_gemm_every_plan(gpu, wtype, plan):
+    if wtype == wa.F16 and plan.split(",")[6:7] == ["2"]:
+        pytest.skip("the ping-pong loop is built for quantized W only (F16 rows need no dequantization)")
+    m, n, k, d = 300, 320, 1024, 64
+    w = np.random.default_rng(1).normal(0, 0.02, (n, k)).astype(np.float32)
+    raw = ox.quantize(w, wtype)
+    bias = rnd(n + d, 2)
+    ol = ox.Linear(wtype, k, [(raw, n)], bias[:n])
+    a = rnd(m * k, 3).reshape(m, k)
+    c0 = rnd(m * (n + d), 4).reshape(m, n + d)
+    gpu.tune("gemm_plan", plan)
+    try:
+        l = gpu.linear([(raw, wtype, k, n)], bias)
+        assert l.width == n + d
+        ab = gpu.upload(a)
+        for e, alpha in ((wa.BIAS, 0.0), (wa.RESIDUAL, 0.5), (wa.SILU, 0.0)):
+            cb = gpu.upload(c0)
+            gpu.gemm(ab, l, cb, m, e, alpha)
+            want = ox.gemm_wide(a, ol, m, e, alpha, c=c0, bias2=bias[n:], dual=d)
+            close(gpu.read(cb, c0.shape), want, tol=2e-5 * max(1.0, float(np.abs(want).max())),
+                  what=f"plan {plan} type {wtype} epi {e}")
+    finally:
+        gpu.tune("gemm_plan", "")
+
+
 def test_gemm_padded_k(gpu):
     # k = 40 is padded to 64 by Gpu::conv; input rows are 64 wide with zeros after 40 (from im2col).
     n, k, m = 64, 40, 37

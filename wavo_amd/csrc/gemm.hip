@@ -66,9 +66,10 @@ GemmPlan gemm_plan_for(const wh_ctx *ctx, int m, int cols, int k) {
     // Three quarters of a tile per CU or more (the FFN's first projection at 750 frames): 96×128 tiles
     // of one row of 4 wavefronts (96×32 each: every W fragment dequantized once per workgroup and fed
     // to three MFMAs; 256 workgroups, one per CU) for k ≥ 1024 (60 s step 4.285 against 4.324 ms for
-    // 128×128 tiles of 2×4), else 128×128 tiles; fewer tiles (the qkv projection, 144) run faster as
-    // 64×64 tiles (4.96 against 4.98 ms per 60 s call; 96×128 tiles for it: 4.51 against 4.32).
-    p = k >= 1024 ? GemmPlan{96, 128, 1, 4, 3, 1} : GemmPlan{128, 128, 2, 4, 3, 1};
+    // 128×128 tiles of 2×4), in two k groups (15.7 against 16.0 µs in the step), else 128×128 tiles;
+    // fewer tiles (the qkv projection, 144) run faster as 64×64 tiles (4.96 against 4.98 ms per 60 s
+    // call; 96×128 tiles for it: 4.51 against 4.32).
+    p = k >= 1024 ? GemmPlan{96, 128, 1, 4, 3, 1, 0, 2} : GemmPlan{128, 128, 2, 4, 3, 1};
   else if (t128 * 4 <= cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
     // Long k over few tiles (the FFN's down projection, 750 × 1024 × 4096): k split 4 ways over
     // 96×64 tiles of 2 wavefronts (96×32 per wavefront: each dequantized W fragment feeds three
@@ -80,21 +81,29 @@ GemmPlan gemm_plan_for(const wh_ctx *ctx, int m, int cols, int k) {
     // The same with up to two workgroups per CU (Whisper's fc2, 1500 × 1280 × 5120: 1.18 + its
     // finish against 1.82 ms per call for 64×64 tiles whole).
     p = {128, 128, 2, 2, 2, 4};
-  else if (t64 < cus)
+  else if (t64 < cus) {
     // Split only while every split keeps at least 16 k steps: shorter ones spend more on the
     // pipeline's fill and the partial sums than the extra workgroups win (k = 1024 runs faster whole).
     while (p.split < 4 && t64 * p.split < 2L * cus && k % (2 * p.split * 64) == 0 && k / (2 * p.split * 64) >= 16)
       p.split *= 2;
-  if (ctx->gemm_plan[0]) {  // tuning override (wh_tune "gemm_plan"): bm, bn, wm, wn, stages, split
+    // Unsplit: two k groups of 4 wavefronts over a 4-slot ring (one workgroup per CU; the 750-frame
+    // 1024 × 1024 projections 9.5 against 10.0 µs in the step; deeper rings alone are slower there:
+    // 10.8 for 5 slots, 11.4 for 8).
+    if (p.split == 1 && k % 128 == 0) p = {64, 64, 2, 2, 4, 1, 0, 2};
+  } else if (t64 < 2L * cus)
+    // One to two 64×64 tiles per CU (the 750-frame pointwise projection, 750 × 2048 × 1024): 96×64
+    // tiles of one row of 2 wavefronts in two k groups, one workgroup per CU (11.7 against 12.7 µs
+    // in the step for 64×64 tiles; 12.2 with 4 slots).
+    p = {96, 64, 1, 2, 2, 1, 0, 2};
+  if (ctx->gemm_plan[0]) {  // tuning override (wh_tune "gemm_plan"): bm, bn, wm, wn, stages, split, pipeline, kgroups
     const int *o = ctx->gemm_plan;
-    p = {o[0], o[1], o[2], o[3], o[4], o[5], o[6]};
-    if (k % (64 * p.split)) p.split = 1;
+    p = {o[0], o[1], o[2], o[3], o[4], o[5], o[6], std::max(1, o[7])};
   }
   for (const auto &o : ctx->gemm_shape_plans)  // tuning override for one shape (wh_tune "gemm_shape_plans")
-    if (o[0] == m && o[1] == cols && o[2] == k) {
-      p = {o[3], o[4], o[5], o[6], o[7], o[8], o[9]};
-      if (k % (64 * p.split)) p.split = 1;
-    }
+    if (o[0] == m && o[1] == cols && o[2] == k) p = {o[3], o[4], o[5], o[6], o[7], o[8], o[9], std::max(1, o[10])};
+  // Whole k steps per split and k group.
+  if (k % (64 * p.wk)) p.wk = 1;
+  if (k % (64 * p.wk * p.split)) p.split = 1;
   return p;
 }
 

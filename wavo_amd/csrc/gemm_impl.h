@@ -10,9 +10,10 @@
 #include <utility>
 #include "internal.h"
 
-// Launch shapes of the LDS-DMA kernel (tile, wavefronts, k step, split).
+// Launch shapes of the LDS-DMA kernel: tile, wavefronts per tile row and column, ring slots, k split
+// over workgroups, loop variant, k groups (wavefront sets that take the k steps in turn).
 struct GemmPlan {
-  int bm, bn, wm, wn, ns, split, pipe = 0;
+  int bm, bn, wm, wn, ns, split, pipe = 0, wk = 1;
 };
 
 // The launch plan of an m × cols × k GEMM (gemm.hip).
@@ -609,9 +610,11 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
 // modes and 16-byte stores, with the bias, the epilogue, the dual columns and the padding columns
 // (epi(0 + bias), as the reference's zero rows give) applied on the way.  A tile whose f32 sums do
 // not fit in the ring's LDS goes through in passes of whole 32-row MFMA tiles of every wavefront.
-template <int WT, int BM, int BN, int WM, int WN, int NSQ, bool SPLIT, bool OUT16, int PIPE>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
-  constexpr int NW = WM * WN;
+template <int WT, int BM, int BN, int WM, int WN, int NSQ, bool SPLIT, bool OUT16, int PIPE, int WK>
+__global__ __launch_bounds__(64 * WM * WN * WK) void gemm_lds_kernel(LdsArgs P) {
+  constexpr int NW = WM * WN;  // wavefronts of one k group
+  constexpr int NWT = NW * WK;  // of the workgroup
+  static_assert(WK == 1 || (WK == 2 && PIPE == 0), "k groups in the plain loop");
   constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
   static_assert(TM >= 1 && TN >= 1, "32×32 MFMA tiles per wave");
   constexpr int PAIR1 = WT == WH_Q8_0 ? 68 : WT == WH_Q4_0 ? 36 : 128;  // W bytes of 64 weights
@@ -620,18 +623,20 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   // chunks (80 LDS bytes) for Q8_0, 3 (48) for Q4_0; the bytes past the pair are the next pair's (or
   // the allocation's tail slack) and are never read.  F16 rows move like a.
   constexpr int WROW = WCH ? 128 : (PAIR1 + 15) / 16 * 16, WCK = WROW / 16;  // LDS bytes, chunks per W row
-  constexpr int A_ST = BM * 128, W_ST = BN * WROW, ST = A_ST + W_ST;
+  // A ring slot holds WK consecutive 64-wide k steps (sub-stages): the a tile's, then the W rows'.
+  constexpr int A_ST0 = BM * 128, W_ST0 = BN * WROW;
+  constexpr int A_ST = WK * A_ST0, W_ST = WK * W_ST0, ST = A_ST + W_ST;
   constexpr int CROW = BN + 8;                                           // f32 per epilogue LDS row
   // NSQ slots asked for, as many as fit in the 160 KiB of LDS.
   constexpr int NS = NSQ * ST + 16 <= 160 * 1024 ? NSQ : (160 * 1024 - 16) / ST;
   static_assert(NS >= 2, "at least two slots");
-  static_assert(W_ST % 1024 == 0, "whole DMA instructions");
+  static_assert(A_ST0 % 1024 == 0 && W_ST0 % 1024 == 0, "whole DMA instructions per sub-stage");
   constexpr int W_RG = NS * A_ST;                               // the W stages follow the a stages
   constexpr int NIA = A_ST / 1024;                              // a: 16-byte DMA instructions per stage
   constexpr int NIW = W_ST / 1024;                              // W: 16-byte DMA instructions per stage
   // The wavefronts that issue the DMA: all of them; in the ping-pong loop the a tile by all of them
   // and the W rows by the four of the second group.
-  constexpr int NWA = NW, NWI = PIPE == 2 ? 4 : NW;
+  constexpr int NWA = NWT, NWI = PIPE == 2 ? 4 : NWT;
   // Instructions per wavefront and stage: PA / PW at most; the first NIA % NWI (NIW % NWI) wavefronts
   // take one more than the others.  vmcnt immediates count PI = the fewest a wavefront issues per stage:
   // loads complete in order, so waiting until at most m·PI remain waits for everything older than the
@@ -668,10 +673,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
     }
   }
   const int n0 = tx * BN, m0 = ty * BM;
-  const int wm = (wave / WN) * (BM / WM), wn = (wave % WN) * (BN / WN);
+  // k group kg of the wavefront (it computes sub-stage kg of every slot) and its place wv in the group.
+  const int kg = WK == 1 ? 0 : wave / NW, wv = WK == 1 ? wave : wave % NW;
+  const int wm = (wv / WN) * (BM / WM), wn = (wv % WN) * (BN / WN);
   const int lrow = lane & 31, g = lane >> 5;
   const int m = P.m, k = P.k, rows = P.rows;
-  const int nkt = k / 64, kb = nkt * tz / (int)gridDim.z, nk = nkt * (tz + 1) / (int)gridDim.z - kb;
+  // Slots of WK k steps: the split's range kb .. kb + nk − 1.
+  const int nkt = k / (64 * WK), kb = nkt * tz / (int)gridDim.z, nk = nkt * (tz + 1) / (int)gridDim.z - kb;
 
   // Per-lane byte offsets of this wave's DMA instructions from the step's base addresses (rows past
   // m or rows are clamped: their products land in outputs that are discarded or zeroed), and the
@@ -680,35 +688,36 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   uint32_t aoff[PA], alds[PA];
 #pragma unroll
   for (int i = 0; i < PA; i++) {
-    const int n = (wave + NWA * i) % NIA, r = 8 * n + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
-    aoff[i] = (uint32_t)(((size_t)min(m0 + r, m - 1) * k + 8 * lc) * 2);
+    const int n = (wave + NWA * i) % NIA, sub = n / (A_ST0 / 1024), nn = n % (A_ST0 / 1024);
+    const int r = 8 * nn + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
+    aoff[i] = (uint32_t)(((size_t)min(m0 + r, m - 1) * k + 8 * lc) * 2 + 128 * sub);
     alds[i] = 1024 * n;
   }
   uint32_t woff[PW], wlds[PW];
 #pragma unroll
   for (int i = 0; i < PW; i++) {
-    const int n = (wi + NWI * i) % NIW;
+    const int n = (wi + NWI * i) % NIW, sub = n / (W_ST0 / 1024), nn = n % (W_ST0 / 1024);
     if constexpr (WCH) {
-      const int r = 8 * n + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
-      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * lc);
+      const int r = 8 * nn + lane / 8, lc = ((lane % 8) - (r >> 1)) & 7;
+      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * lc + PAIR1 * sub);
       wlds[i] = 1024 * n;
     } else {
-      const int t = 64 * n + lane, r = t / WCK, c = t % WCK;
-      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * c);
+      const int t = 64 * nn + lane, r = t / WCK, c = t % WCK;
+      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * c + PAIR1 * sub);
       wlds[i] = 1024 * n;
     }
   }
-  const uint8_t *abase = (const uint8_t *)P.a + (size_t)kb * 128;
-  const uint8_t *wbase = P.w + (size_t)kb * PAIR1;
+  const uint8_t *abase = (const uint8_t *)P.a + (size_t)kb * 128 * WK;
+  const uint8_t *wbase = P.w + (size_t)kb * PAIR1 * WK;
   const uint32_t lds0 = lds_addr(lds);
   auto issue_a = [&](int kt, int slot) {
-    const uint8_t *ab = abase + (size_t)kt * 128;
+    const uint8_t *ab = abase + (size_t)kt * 128 * WK;
 #pragma unroll
     for (int i = 0; i < PA; i++)
       if (NIA % NWA == 0 || i < NIA / NWA || wave + NWA * i < NIA) dma16s(ab, aoff[i], lds0 + slot * A_ST + alds[i]);
   };
   auto issue_w = [&](int kt, int slot) {
-    const uint8_t *wb = wbase + (size_t)kt * PAIR1;
+    const uint8_t *wb = wbase + (size_t)kt * PAIR1 * WK;
 #pragma unroll
     for (int i = 0; i < PW; i++)
       if (NIW % NWI == 0 || i < NIW / NWI || wi + NWI * i < NIW) dma16s(wb, woff[i], lds0 + W_RG + slot * W_ST + wlds[i]);
@@ -729,11 +738,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   // scale in the high half of the dword before); F16 chunks like a.
   uint32_t a_off[4];
 #pragma unroll
-  for (int s = 0; s < 4; s++) a_off[s] = (wm + lrow) * 128 + 16 * ((chunk(s) + (lrow >> 1)) & 7);
+  for (int s = 0; s < 4; s++) a_off[s] = kg * A_ST0 + (wm + lrow) * 128 + 16 * ((chunk(s) + (lrow >> 1)) & 7);
   constexpr int ND = Q8 ? 10 : WT == WH_Q4_0 ? 5 : 16;  // dwords per lane per W row and step
   constexpr int NSC = Q8 ? 2 : 1;                       // scale dwords per lane per W row and step
   constexpr int BLK = PAIR1 / 2;
-  const uint32_t w_row = W_RG + (wn + lrow) * WROW;
+  const uint32_t w_row = W_RG + kg * W_ST0 + (wn + lrow) * WROW;
   const uint32_t w_dat = Q8 ? w_row + 8 * g : w_row + (g ? BLK + 2 : 0), w_sc = w_row + (g ? BLK - 2 : 0);
   uint32_t wf_off[4];
 #pragma unroll
@@ -931,7 +940,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   // ends every wavefront's reads of the stages.  A thread's 8-column group is the same on every row
   // it stores (64·NW is a multiple of BN / 8), so its bias values are loaded once, before the barrier.
   constexpr int G8 = BN / 8;  // 8-column groups per row
-  static_assert((64 * NW) % G8 == 0, "fixed column group per thread");
+  static_assert((64 * NWT) % G8 == 0, "fixed column group per thread");
   const int ecol = n0 + 8 * (tid % G8);
   float bb[8] = {}, bd[8] = {};
   if (!SPLIT && ecol < P.cols) {
@@ -944,20 +953,30 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_lds_kernel(LdsArgs P) {
   float *cl = (float *)lds;
   // Pass i0: 32-row tiles i0 .. i0 + PG − 1 of every wavefront; LDS row (wave row)·32·PG + 32·(i − i0)
   // + the row in the MFMA tile.
-  const int crow0 = (wave / WN) * 32 * PG;
+  const int crow0 = (wv / WN) * 32 * PG;
   // (passes unrolled at compile time, so that the accumulators are only ever indexed by constants)
   auto pass = [&](auto I0_c) {
     constexpr int i0 = decltype(I0_c)::value;
     __syncthreads();
+    // k group 0 stores its sums, then group 1 adds its own (the same lane of the same place: a fixed
+    // order of the two halves' sums).
+    static_for<0, WK, 1>([&](auto G_c) {
+      constexpr int G = decltype(G_c)::value;
+      if (G > 0) __syncthreads();
+      if (kg == G) {
 #pragma unroll
-    for (int i = i0; i < i0 + PG; i++)
+        for (int i = i0; i < i0 + PG; i++)
 #pragma unroll
-      for (int j = 0; j < TN; j++)
+          for (int j = 0; j < TN; j++)
 #pragma unroll
-        for (int v = 0; v < 16; v++)
-          cl[(crow0 + 32 * (i - i0) + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow] = acc[i][j][v];
+            for (int v = 0; v < 16; v++) {
+              float &x = cl[(crow0 + 32 * (i - i0) + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow];
+              x = G == 0 ? acc[i][j][v] : x + acc[i][j][v];
+            }
+      }
+    });
     __syncthreads();
-    store_c_tile<WM * 32 * PG, BM / WM, 32 * PG, BN, 64 * NW, SPLIT, OUT16>(P, cl, CROW, tid, m0, n0, tz, i0, bb, bd);
+    store_c_tile<WM * 32 * PG, BM / WM, 32 * PG, BN, 64 * NWT, SPLIT, OUT16>(P, cl, CROW, tid, m0, n0, tz, i0, bb, bd);
   };
   static_for<0, TM, PG>(pass);
 }
@@ -987,16 +1006,17 @@ __global__ __launch_bounds__(256) void split_finish_kernel(const float *__restri
   }
 }
 
-template <int WT, int BM, int BN, int WM, int WN, int NS, int PIPE>
+template <int WT, int BM, int BN, int WM, int WN, int NS, int PIPE, int WK>
 int lds_launch(wh_ctx *ctx, dim3 grid, const LdsArgs &a, bool split, bool out16) {
   constexpr int WROW = WT == WH_Q8_0 ? 80 : WT == WH_Q4_0 ? 48 : 128;  // LDS bytes per W row (the kernel's)
   if constexpr (PIPE == 2 && (WT == WH_F16 || NS * (BM * 128 + BN * WROW) + 16 > 160 * 1024)) {
     // (not built: the ring would exceed the LDS, or F16 rows, which need no dequantization to hide)
     return wh_fail(ctx, WH_EARG, "gemm: no ping-pong kernel for %d slots of a %dx%d tile of this weight type", NS, BM, BN);
   } else {
-    if (split) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, true, false, PIPE>, grid, 64 * WM * WN, 0, a);
-    else if (out16) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, true, PIPE>, grid, 64 * WM * WN, 0, a);
-    else wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, false, PIPE>, grid, 64 * WM * WN, 0, a);
+    constexpr int NT = 64 * WM * WN * WK;
+    if (split) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, true, false, PIPE, WK>, grid, NT, 0, a);
+    else if (out16) wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, true, PIPE, WK>, grid, NT, 0, a);
+    else wh_launch(ctx, gemm_lds_kernel<WT, BM, BN, WM, WN, NS, false, false, PIPE, WK>, grid, NT, 0, a);
     return WH_OK;
   }
 }
@@ -1022,9 +1042,10 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
   static const char *tn = WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
   // Named by kernel variant and call shape: m x rows x k, epilogue, output type, row width.
   char name[128];
-  char sp[8] = "";
+  char sp[24] = "";
   if (p.split > 1) snprintf(sp, sizeof sp, "_s%d", p.split);
   if (p.pipe) snprintf(sp + strlen(sp), sizeof sp - strlen(sp), "_p%d", p.pipe);
+  if (p.wk > 1) snprintf(sp + strlen(sp), sizeof sp - strlen(sp), "_k%d", p.wk);
   snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s %dx%dx%d e%d %s w%d", tn, p.bm, p.bn, p.wm, p.wn, p.ns, sp, m,
            l->rows, l->k, epi, out16 ? "f16" : "f32", l->cols + l->dual);
   const double width = l->cols + l->dual;
@@ -1034,12 +1055,13 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     ProfScope prof(ctx, name, 2.0 * m * l->rows * l->k, bytes);
     const bool sp = p.split > 1;
     bool ok = false;
-#define PLANP(BM, BN, WM, WN, NS, PIPE)                                                               \
-  if (!ok && p.bm == BM && p.bn == BN && p.wm == WM && p.wn == WN && p.ns == NS && p.pipe == PIPE) {      \
-    if (int rc = lds_launch<WT, BM, BN, WM, WN, NS, PIPE>(ctx, grid, args, sp, out16)) return rc;          \
-    ok = true;                                                                                            \
+#define PLANK(BM, BN, WM, WN, NS, PIPE, WK)                                                                       \
+  if (!ok && p.bm == BM && p.bn == BN && p.wm == WM && p.wn == WN && p.ns == NS && p.pipe == PIPE && p.wk == WK) { \
+    if (int rc = lds_launch<WT, BM, BN, WM, WN, NS, PIPE, WK>(ctx, grid, args, sp, out16)) return rc;               \
+    ok = true;                                                                                                      \
   }
-#define PLAN(BM, BN, WM, WN, NS) PLANP(BM, BN, WM, WN, NS, 0)
+#define PLANP(BM, BN, WM, WN, NS, PIPE) PLANK(BM, BN, WM, WN, NS, PIPE, 1)
+#define PLAN(BM, BN, WM, WN, NS) PLANK(BM, BN, WM, WN, NS, 0, 1)
     PLAN(128, 128, 2, 4, 3)
     PLAN(64, 64, 2, 2, 3)
     PLAN(128, 128, 2, 4, 2)
@@ -1049,10 +1071,16 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     PLAN(192, 128, 2, 2, 2)
     PLAN(256, 256, 2, 4, 2)
     PLAN(96, 128, 1, 4, 3)
+    PLANK(64, 64, 2, 2, 4, 0, 2)
+    PLANK(96, 64, 1, 2, 2, 0, 2)
+    PLANK(96, 128, 1, 4, 3, 0, 2)
     PLANP(256, 256, 2, 4, 3, 2)  // the ping-pong loop (tuning only: not faster than the plain one)
 #undef PLAN
 #undef PLANP
-    if (!ok) return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages", p.bm, p.bn, p.wm, p.wn, p.ns);
+#undef PLANK
+    if (!ok)
+      return wh_fail(ctx, WH_EARG, "gemm: no kernel for tile %dx%d, %dx%d waves, %d stages, %d k groups", p.bm, p.bn,
+                     p.wm, p.wn, p.ns, p.wk);
     if (int rc = wh_launched(ctx, "gemm")) return rc;
   }
   if (p.split > 1 && !splits && !ctx->gemm_kernel_only) {

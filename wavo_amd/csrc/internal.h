@@ -30,16 +30,16 @@ struct wh_ctx {
   int cus = 0;
   // Per head, the parts of an attend launch done so far (0 between launches: the last part resets it).
   int *attend_count = nullptr;
-  // GEMM launch-plan override set by wh_tune("gemm_plan", "bm,bn,wm,wn,slots,split[,pipeline]") (tuning sweeps
-  // only): all zero = chosen per shape.
-  int gemm_plan[7] = {0, 0, 0, 0, 0, 0, 0};
+  // GEMM launch-plan override set by wh_tune("gemm_plan", "bm,bn,wm,wn,slots,split[,pipeline[,kgroups]]") (tuning
+  // sweeps only): all zero = chosen per shape.
+  int gemm_plan[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   // wh_tune("gemm_kernel_only", "1") (measurement only): a split GEMM call stops after the GEMM kernel, leaving
   // its partial sums unfinished, so that the kernel can be timed alone as it runs inside a model step
   // (where the next kernel finishes the sums).
   int gemm_kernel_only = 0;
-  // Per-shape overrides set by wh_tune("gemm_shape_plans", "m,cols,k:bm,bn,wm,wn,slots,split[,pipeline];…"); tuning
-  // sweeps inside a model's step only).
-  std::vector<std::array<int, 10>> gemm_shape_plans;
+  // Per-shape overrides set by wh_tune("gemm_shape_plans", "m,cols,k:bm,bn,wm,wn,slots,split[,pipeline[,kgroups]];…")
+  // (tuning sweeps inside a model's step only).
+  std::vector<std::array<int, 11>> gemm_shape_plans;
   // Attention key-split override set by wh_tune("attn_split", "n") (tuning sweeps only): 0 = chosen per shape.
   int attn_split = 0;
   // wh_tune("mel_raw", "1") (checks only): the frontends write each filter's sum before the logarithm.

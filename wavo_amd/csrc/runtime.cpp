@@ -372,19 +372,21 @@ int wh_tune(wh_ctx *ctx, const char *key, const char *value) {
   if (!ctx || !key) return WH_EARG;
   const char *v = value ? value : "";
   if (!strcmp(key, "gemm_plan")) {
-    int o[7] = {0, 0, 0, 0, 0, 0, 0};
-    if (*v && (sscanf(v, "%d,%d,%d,%d,%d,%d,%d", &o[0], &o[1], &o[2], &o[3], &o[4], &o[5], &o[6]) < 6 || o[5] < 1 ||
-               o[5] > 4))
-      return wh_fail(ctx, WH_EARG, "wh_tune gemm_plan: \"bm,bn,wm,wn,stages,split[,pipeline]\" (split 1..4) or \"\"");
+    int o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (*v && (sscanf(v, "%d,%d,%d,%d,%d,%d,%d,%d", &o[0], &o[1], &o[2], &o[3], &o[4], &o[5], &o[6], &o[7]) < 6 ||
+               o[5] < 1 || o[5] > 4 || o[7] < 0 || o[7] > 2))
+      return wh_fail(ctx, WH_EARG,
+                     "wh_tune gemm_plan: \"bm,bn,wm,wn,stages,split[,pipeline[,kgroups]]\" (split 1..4, kgroups 1..2) or \"\"");
     memcpy(ctx->gemm_plan, o, sizeof o);
   } else if (!strcmp(key, "gemm_shape_plans")) {
     ctx->gemm_shape_plans.clear();
     for (const char *q = v; *q;) {
-      std::array<int, 10> o{};
-      if (sscanf(q, "%d,%d,%d:%d,%d,%d,%d,%d,%d,%d", &o[0], &o[1], &o[2], &o[3], &o[4], &o[5], &o[6], &o[7], &o[8],
-                 &o[9]) < 9 ||
-          o[8] < 1 || o[8] > 4)
-        return wh_fail(ctx, WH_EARG, "wh_tune gemm_shape_plans: \"m,cols,k:bm,bn,wm,wn,stages,split[,pipeline];...\"");
+      std::array<int, 11> o{};
+      if (sscanf(q, "%d,%d,%d:%d,%d,%d,%d,%d,%d,%d,%d", &o[0], &o[1], &o[2], &o[3], &o[4], &o[5], &o[6], &o[7], &o[8],
+                 &o[9], &o[10]) < 9 ||
+          o[8] < 1 || o[8] > 4 || o[10] < 0 || o[10] > 2)
+        return wh_fail(ctx, WH_EARG,
+                       "wh_tune gemm_shape_plans: \"m,cols,k:bm,bn,wm,wn,stages,split[,pipeline[,kgroups]];...\"");
       ctx->gemm_shape_plans.push_back(o);
       const char *n = strchr(q, ';');
       if (!n) break;

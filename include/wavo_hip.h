@@ -92,6 +92,8 @@ void *wh_stream(wh_ctx *ctx);
  *   "gemm_kernel_only" "1": a k-split GEMM call stops after its GEMM kernel and leaves c unwritten
  *                      (to time that kernel alone, as a model step runs it); "0" restores;
  *   "attn_split"       "n": attention splits its key range n ways (0 = chosen per shape);
+ *   "position_cache"   "0": the Parakeet encoder recomputes its relative-position projection every call
+ *                      instead of keeping it for the frame count its buffer holds (to time it); "1" restores;
  *   "mel_raw"          "1": wh_model_mel writes each filter's sum before the logarithm, without the
  *                      normalization or scaling (to check the transforms bit for bit); "0" restores;
  *   "whisper_host"     "1": wh_whisper_decode reads every step's logits back and picks on the host

@@ -380,3 +380,59 @@ def test_graph_replays_equal_eager_calls(gpu, name):
         # Eager work of the program's own between the replays.
         gpu.zero(other)
         gpu.sync()
+
+
+@pytest.mark.parametrize("graphs", [False, True])
+def test_position_projection_kept_per_frame_count(gpu, graphs):
+    """The Parakeet position projection depends only on the frame count t and the weights, so a call
+    at the t whose projection its buffers hold skips that GEMM (a tag on the device, checked by the
+    kernel: a recorded pass stays right whatever t a later call leaves there).  Calls alternating
+    between two frame counts, one window (packed positions) and a batch of two (plain), eagerly or
+    recorded and replayed, with a call over fewer blocks in between: every output is the same bytes
+    as from a context that recomputes the projection every call."""
+    path = synth.model_path("parakeet", small=True, directory=MODELS)
+    mels = [synth.parakeet_mel(synth.audio(s, 5)) for s in (3.0, 2.2)]
+    ref_ctx = wa.Gpu(0)
+    try:
+        ref_ctx.tune("position_cache", 0)
+        ref = wa.Model(ref_ctx, path)
+        want = [ref.encode(x) for x in mels]
+        d = ref.frames(mels[0].shape[0])[1]  # the model width
+        x0 = np.random.default_rng(2).normal(0, 1, (30, d)).astype(np.float32)
+        xw = ref_ctx.upload(x0)
+        ref.blocks_device(xw, 30, 1)
+        want_blocks = ref_ctx.read(xw, (30, d)).copy()
+        mf = max(x.shape[0] for x in mels)
+        batch = np.zeros((2, mf, mels[0].shape[1]), np.float32)
+        for i, x in enumerate(mels):
+            batch[i, :x.shape[0]] = x
+        fb, wb = ref.frames(mf)
+        bb, ob = ref_ctx.upload(batch), ref_ctx.buffer(2 * fb * wb)
+        ref.encode_batch_device(bb, 2, mf, [x.shape[0] for x in mels], ob)
+        want_batch = ref_ctx.read(ob, (2, fb, wb)).copy()
+        ref.free()
+    finally:
+        ref_ctx.close()
+    m = wa.Model(gpu, path)
+    m.graphs(graphs)
+    bufs = []
+    for x in mels:
+        f, w = m.frames(x.shape[0])
+        bufs.append((gpu.upload(x), gpu.buffer(f * w), f, w))
+    bb, ob = gpu.upload(batch), gpu.buffer(2 * fb * wb)
+    for rnd in range(3):  # eager, recorded, replayed (with graphs)
+        for i in (0, 1, 0):
+            xb, outb, f, w = bufs[i]
+            gpu.zero(outb)
+            m.encode_device(xb, mels[i].shape[0], outb)
+            assert np.array_equal(gpu.read(outb, (f, w)), want[i]), f"round {rnd} window {i}"
+        gpu.zero(ob)
+        m.encode_batch_device(bb, 2, mf, [x.shape[0] for x in mels], ob)
+        assert np.array_equal(gpu.read(ob, (2, fb, wb)), want_batch), f"round {rnd} batch"
+    xw = gpu.upload(x0)
+    m.blocks_device(xw, 30, 1)  # packs one block's positions: the tag is cleared
+    assert np.array_equal(gpu.read(xw, (30, d)), want_blocks)
+    xb, outb, f, w = bufs[0]
+    m.encode_device(xb, mels[0].shape[0], outb)
+    assert np.array_equal(gpu.read(outb, (f, w)), want[0]), "after a call over fewer blocks"
+    m.free()

@@ -376,6 +376,10 @@ struct LdsArgs {
   size_t row_bytes;
   HeadsOut ho[2];  // column ranges written in attention's packed layout instead of into c (f16 outputs)
   int nho;
+  // Non-null: the launch does nothing when *skip == skip_val (c already holds this product: an
+  // input-independent GEMM whose output is kept between calls, tagged on the device).
+  const int *skip;
+  int skip_val;
 };
 
 // s_waitcnt with vmcnt = N (0..63) and no wait on the other counters (gfx9 encoding: vmcnt bits
@@ -654,6 +658,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_lds_kernel(LdsArgs P) 
   constexpr int LDS_BYTES = RING > C_BYTES ? RING : C_BYTES;
   __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
 
+  if (P.skip && *P.skip == P.skip_val) return;  // c already holds this product
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // Tile order.  Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2.
@@ -1028,7 +1033,10 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
   if ((p.split > 1 && !part) || nho) p.split = 1;  // packed ranges are written by the tiles' own epilogue
   if (splits) *splits = p.split;
   LdsArgs args{a, l->w, l->bias, p.split > 1 ? (void *)part : c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha,
-               l->row_bytes, {}, nho};
+               l->row_bytes, {}, nho, nullptr, 0};
+  // A tagged output (ctx->gemm_skip, set by the caller for this launch): whole-k plans only (a split
+  // launch's partial sums are finished by another kernel).
+  if (ctx->gemm_skip && p.split == 1) args.skip = ctx->gemm_skip, args.skip_val = ctx->gemm_skip_val;
   if (nho < 0 || nho > 2) return wh_fail(ctx, WH_EARG, "gemm: %d packed ranges", nho);
   for (int i = 0; i < nho; i++) {
     const HeadsOut &h = ho[i];
@@ -1046,13 +1054,14 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
   if (p.split > 1) snprintf(sp, sizeof sp, "_s%d", p.split);
   if (p.pipe) snprintf(sp + strlen(sp), sizeof sp - strlen(sp), "_p%d", p.pipe);
   if (p.wk > 1) snprintf(sp + strlen(sp), sizeof sp - strlen(sp), "_k%d", p.wk);
-  snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s %dx%dx%d e%d %s w%d", tn, p.bm, p.bn, p.wm, p.wn, p.ns, sp, m,
-           l->rows, l->k, epi, out16 ? "f16" : "f32", l->cols + l->dual);
+  snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s %dx%dx%d e%d %s w%d%s", tn, p.bm, p.bn, p.wm, p.wn, p.ns, sp,
+           m, l->rows, l->k, epi, out16 ? "f16" : "f32", l->cols + l->dual, args.skip ? " (tagged)" : "");
   const double width = l->cols + l->dual;
   const double bytes = (double)l->rows * l->row_bytes + 2.0 * m * l->k +
                        (out16 ? 2.0 : 4.0) * m * width * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
   {
-    ProfScope prof(ctx, name, 2.0 * m * l->rows * l->k, bytes);
+    // (a tagged launch is profiled as no work: it skips whenever its tag matches)
+    ProfScope prof(ctx, name, args.skip ? 0.0 : 2.0 * m * l->rows * l->k, args.skip ? 0.0 : bytes);
     const bool sp = p.split > 1;
     bool ok = false;
 #define PLANK(BM, BN, WM, WN, NS, PIPE, WK)                                                                       \

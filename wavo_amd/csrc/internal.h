@@ -42,6 +42,13 @@ struct wh_ctx {
   std::vector<std::array<int, 11>> gemm_shape_plans;
   // Attention key-split override set by wh_tune("attn_split", "n") (tuning sweeps only): 0 = chosen per shape.
   int attn_split = 0;
+  // Set by a caller around one GEMM call (null otherwise): the main kernel skips when *gemm_skip ==
+  // gemm_skip_val (its output already holds the product).
+  const int *gemm_skip = nullptr;
+  int gemm_skip_val = 0;
+  // wh_tune("position_cache", "0") (measurement): the Parakeet encoder recomputes its position
+  // projection every call instead of keeping it per frame count; "1" restores.
+  int no_position_cache = 0;
   // wh_tune("mel_raw", "1") (checks only): the frontends write each filter's sum before the logarithm.
   int mel_raw = 0;
   // wh_tune("whisper_host", "1") (checks only): wh_whisper_decode picks each token on the host.
@@ -243,6 +250,8 @@ int launch_attend(wh_ctx *ctx, const float *q, const uint32_t *kv, float *part, 
 int launch_pack(wh_ctx *ctx, const float *x, int src, int stride, uint32_t *y, int rows, int d,
                 int cols, int col, const int *dcol = nullptr);
 int launch_zero(wh_ctx *ctx, void *dst, size_t bytes);
+// *dst = v (one thread, on the context's stream).
+int launch_set_int(wh_ctx *ctx, int *dst, int v);
 // Device-to-device copy with a kernel (a graph node like any other launch).
 int launch_copy(wh_ctx *ctx, void *dst, const void *src, size_t bytes);
 int launch_add_rows(wh_ctx *ctx, float *x, const float *add, size_t n);

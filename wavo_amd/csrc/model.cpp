@@ -503,6 +503,11 @@ struct wh_model {
   // f16 [2t + 15][layers · d] (block i's at column i · d).
   wh_linear *pos_all = nullptr;
   void *posp = nullptr;
+  // Device tags of the position projection's outputs: the frame count t whose projection posp ([0])
+  // and ppk ([1]) hold (0: none).  The projection depends on t and the weights only, so a call at the
+  // tagged t skips its GEMM (decided on the device: a recorded pass stays right whatever t a later
+  // call leaves there).
+  int *pos_tag = nullptr;
   const void *pos16_cur = nullptr;  // its rows of this call
   int *valid_dev = nullptr;
   float *sub2 = nullptr;   // Parakeet conv3 output (the subsampling's second buffer)
@@ -854,7 +859,7 @@ int arena(wh_model *m, int frames, int batch) {
   m->epoch++;
   int F = (std::max(frames, m->cap) + 63) / 64 * 64, B = std::max(batch, std::max(m->cap_batch, 1));
   for (float *p : {m->x, m->y, m->h, m->qk, m->yr, m->pos, m->sub, m->sub2, m->rope, (float *)m->pos16, (float *)m->posp,
-                   (float *)m->ppk})
+                   (float *)m->ppk, (float *)m->pos_tag})
     if (p) {
       wh_free(m->ctx, p);
       for (auto &o : m->owned)
@@ -863,6 +868,7 @@ int arena(wh_model *m, int frames, int batch) {
   if (m->valid_dev) wh_free(m->ctx, m->valid_dev);
   m->x = m->y = m->h = m->qk = m->yr = m->pos = m->sub = m->sub2 = m->rope = nullptr;
   m->pos16 = m->posp = m->ppk = nullptr;
+  m->pos_tag = nullptr;
   m->valid_dev = nullptr;
   const int d = m->d;
   const size_t rows = (size_t)F * B;
@@ -909,7 +915,9 @@ int arena(wh_model *m, int frames, int batch) {
     CK(wh_write(m->ctx, m->pos, table.data(), table.size() * 4));
     m->pos16 = dev_alloc(m, (table.size() + 1) / 2);
     m->posp = dev_alloc(m, ((size_t)(2 * F + 15) * m->layers * d + 1) / 2);
-    if (!m->pos16 || !m->posp) return WH_EOOM;
+    m->pos_tag = (int *)dev_alloc(m, 2);
+    if (!m->pos16 || !m->posp || !m->pos_tag) return WH_EOOM;
+    CK(launch_zero(m->ctx, m->pos_tag, 2 * sizeof(int)));  // no projection held yet
     const int hd = d / m->heads;
     if (hd == 32 || hd == 64 || hd == 128) {
       int most = 0, tk, pfront, prows;
@@ -1003,6 +1011,23 @@ int record_block(wh_model *m, int layer, const Block &k, float *x, float *y, int
 
 namespace {
 
+// The position projection of a t-frame call into output `which` (0: posp, 1: ppk) by gemm(): tagged
+// with t on the device, so that the GEMM skips while its output holds t's projection.  A call over
+// fewer than all blocks (whole: false) packs only theirs: it runs untagged and clears the tag.
+template <class F>
+int position_projection(wh_model *m, int t, int which, bool whole, F &&gemm) {
+  if (m->ctx->no_position_cache || !whole) {
+    if (int rc = gemm()) return rc;
+    return launch_set_int(m->ctx, m->pos_tag + which, 0);
+  }
+  m->ctx->gemm_skip = m->pos_tag + which;
+  m->ctx->gemm_skip_val = t;
+  const int rc = gemm();
+  m->ctx->gemm_skip = nullptr;
+  if (rc) return rc;
+  return launch_set_int(m->ctx, m->pos_tag + which, t);
+}
+
 // Conformer::record (src/conformer.rs:107-116): `layers` blocks from m->x, output in m->x.
 int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layers) {
   if (m->relative && layers > 0) {  // every block's linear_pos(P) in one GEMM: [2t + 15][layers · d] f16
@@ -1013,9 +1038,14 @@ int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layer
       int tk, pfront, prows;
       attention_layout(t, m->heads, hd, 1, &tk, &pfront, &prows);
       const HeadsOut out{m->ppk, 0, layers * m->d, hd, prows, pfront, false};
-      CK(launch_gemm_h_heads(m->ctx, m->pos16_cur, m->pos_all, m->posp, 2 * t + 15, m->pos_all->cols, WH_BIAS, &out, 1));
+      CK(position_projection(m, t, 1, layers == m->layers, [&] {
+        return launch_gemm_h_heads(m->ctx, m->pos16_cur, m->pos_all, m->posp, 2 * t + 15, m->pos_all->cols, WH_BIAS,
+                                   &out, 1);
+      }));
     } else {
-      CK(launch_gemm_h(m->ctx, m->pos16_cur, m->pos_all, m->posp, 2 * t + 15, m->pos_all->cols, WH_BIAS, 0.0f, 1));
+      CK(position_projection(m, t, 0, layers == m->layers, [&] {
+        return launch_gemm_h(m->ctx, m->pos16_cur, m->pos_all, m->posp, 2 * t + 15, m->pos_all->cols, WH_BIAS, 0.0f, 1);
+      }));
     }
   }
   for (int i = 0; i < layers; i++) {

@@ -769,6 +769,16 @@ int launch_argmax(wh_ctx *ctx, const float *x, uint32_t *out, int n) {
   return wh_launched(ctx, "argmax");
 }
 
+__global__ void set_int_kernel(int *__restrict__ dst, int v) {
+  if (threadIdx.x == 0) *dst = v;
+}
+
+int launch_set_int(wh_ctx *ctx, int *dst, int v) {
+  if (!dst) return wh_fail(ctx, WH_EARG, "set_int: NULL");
+  wh_launch(ctx, set_int_kernel, 1, 64, 0, dst, v);
+  return wh_launched(ctx, "set_int");
+}
+
 int launch_zero(wh_ctx *ctx, void *dst, size_t bytes) {
   if (!bytes) return WH_OK;
   if (!dst) return wh_fail(ctx, WH_EARG, "zero: NULL");

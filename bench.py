@@ -645,8 +645,8 @@ def main():
                     help="launch every kernel eagerly instead of replaying recorded HIP graphs (kernel traces)")
     ap.add_argument("--replay", metavar="NAME", default=None,
                     help="only the back-to-back launches of this GEMM configuration (a roofline.kernel value), "
-                         "or 'attention_rel' for the Parakeet attention call, for rocprofv3 passes over exactly "
-                         "those launches")
+                         "'attention_rel' for the Parakeet attention call, or 'copy' for the copy kernel over "
+                         "256 MiB, for rocprofv3 passes over exactly those launches")
     args = ap.parse_args()
     global GRAPHS
     GRAPHS = not args.no_graphs
@@ -664,6 +664,12 @@ def main():
     import wavo_amd as wa
     from wavo_amd import synth
 
+    if args.replay == "copy":  # the copy kernel over 256 MiB: the traffic counters' calibration
+        g = wa.Gpu(0)
+        r = hbm_copy(g, 1 << 28)
+        g.close()
+        print(json.dumps({"replayed": args.replay, **r}), flush=True)
+        return
     if args.replay == "attention_rel":
         us, flops = attention_replay()
         print(json.dumps({"replayed": args.replay, "us_per_call": round(us, 3),

@@ -9,6 +9,7 @@
 #include <type_traits>
 #include <utility>
 #include "internal.h"
+#include "xlane.h"
 
 // Launch shapes of the LDS-DMA kernel: tile, wavefronts per tile row and column, ring slots, k split
 // over workgroups, loop variant, k groups (wavefront sets that take the k steps in turn).
@@ -707,8 +708,11 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_lds_kernel(LdsArgs P) 
       woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * lc + PAIR1 * sub);
       wlds[i] = 1024 * n;
     } else {
-      const int t = 64 * nn + lane, r = t / WCK, c = t % WCK;
-      woff[i] = (uint32_t)((size_t)min(n0 + r, rows - 1) * P.row_bytes + 16 * c + PAIR1 * sub);
+      // (Q8_0: rows 16-31 of each 32-row block start 8 bytes into their LDS row, see read_w; a
+      // clamped row 0 — a one-row W, never read — is not moved, as nothing precedes it)
+      const int t = 64 * nn + lane, r = t / WCK, c = t % WCK, row = min(n0 + r, rows - 1);
+      const int shift = WT == WH_Q8_0 && (r & 16) && row > 0 ? 8 : 0;
+      woff[i] = (uint32_t)((size_t)row * P.row_bytes + 16 * c + PAIR1 * sub - shift);
       wlds[i] = 1024 * n;
     }
   }
@@ -747,7 +751,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_lds_kernel(LdsArgs P) 
   constexpr int ND = Q8 ? 10 : WT == WH_Q4_0 ? 5 : 16;  // dwords per lane per W row and step
   constexpr int NSC = Q8 ? 2 : 1;                       // scale dwords per lane per W row and step
   constexpr int BLK = PAIR1 / 2;
-  const uint32_t w_row = W_RG + kg * W_ST0 + (wn + lrow) * WROW;
+  const uint32_t w_row = W_RG + kg * W_ST0 + (wn + lrow) * WROW + (Q8 ? 8 * ((lrow >> 4) & 1) : 0);
   const uint32_t w_dat = Q8 ? w_row + 8 * g : w_row + (g ? BLK + 2 : 0), w_sc = w_row + (g ? BLK - 2 : 0);
   uint32_t wf_off[4];
 #pragma unroll
@@ -769,13 +773,25 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_lds_kernel(LdsArgs P) 
         sc[j][0] = 0;
       } else if constexpr (Q8) {
         // Pair bytes 2 + 8g .. (block 0, substeps 0-1: dwords 0-2 and 4-6 from byte 8g) and
-        // 36 + 8g .. (block 1, substeps 2-3: dwords 9-10 and 13-14); the scales at bytes 0 and 34.
-        const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * WROW);
+        // 36 + 8g .. (block 1, substeps 2-3: dwords 9-10 and 13-14), read as the 16 dwords from byte
+        // 8g in 8-byte reads: with 80-byte LDS rows, rows r and r + 16 of a 32-row block would share
+        // banks, so rows 16-31 sit 8 bytes further into their LDS row (measured on gfx950: single
+        // dwords from the rows as stored cost 6 bank-conflict cycles per read, 8-byte reads from the
+        // moved rows none).  The scales at bytes 0 and 34: dword 0 of lane group 0's span (lanes
+        // 32-63 take it from lane − 32) and dword 8 − 2g.
+        const uint2 *q = (const uint2 *)(lds + w_dat + slot * W_ST + j * 32 * WROW);
+        uint32_t d[16];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const uint2 v = q[i];
+          d[2 * i] = v.x, d[2 * i + 1] = v.y;
+        }
         constexpr int at[10] = {0, 1, 2, 4, 5, 6, 9, 10, 13, 14};
 #pragma unroll
-        for (int i = 0; i < 10; i++) w[j][i] = q[at[i]];
-        const uint32_t *r = (const uint32_t *)(lds + w_row + slot * W_ST + j * 32 * WROW);
-        sc[j][0] = r[0], sc[j][1] = r[8];
+        for (int i = 0; i < 10; i++) w[j][i] = d[at[i]];
+        uint32_t s0 = d[0], s0b = d[0];
+        xlane::swap32(s0, s0b);  // lanes 32-63: lane − 32's dword 0
+        sc[j][0] = s0, sc[j][1] = g ? d[6] : d[8];
       } else {
         const uint32_t *q = (const uint32_t *)(lds + w_dat + slot * W_ST + j * 32 * WROW);
 #pragma unroll

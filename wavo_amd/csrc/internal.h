@@ -237,9 +237,11 @@ int launch_attention(wh_ctx *ctx, const void *qk, const void *v, const void *pos
 // Scratch bytes launch_attention uses for t frames × batch windows (rel: relative positions) on
 // this context's device (its CU count sets the key splits).
 size_t attention_scratch_bytes(const wh_ctx *ctx, int t, int heads, int hd, int batch, int rel);
+// y f32, or f16 with out16 (for a consumer that rounds its input to f16 anyway: a GEMM).
 int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *b0, const float *w,
-                     const float *b, float *y, int t, int f, int ch, int t0, int rows);
-int launch_flatten(wh_ctx *ctx, const float *x, float *y, int t, int f, int ch);
+                     const float *b, void *y, int t, int f, int ch, int t0, int rows, int out16 = 0);
+// x and y f32, or both f16 (f16).
+int launch_flatten(wh_ctx *ctx, const void *x, void *y, int t, int f, int ch, int f16 = 0);
 int launch_argmax(wh_ctx *ctx, const float *x, uint32_t *out, int n);
 int launch_step_args(wh_ctx *ctx, uint32_t *ids, int token, int pos);
 // With dn (device memory), the key count is *dn + n (at most cols).

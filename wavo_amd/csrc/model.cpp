@@ -1060,6 +1060,11 @@ int lin(wh_model *m, const float *a, const wh_linear *l, float *c, int rows, int
   return launch_gemm(m->ctx, a, l, c, rows, l->cols + l->dual, epi, alpha);
 }
 
+// The same with `a` already f16, the output f32 or (out16) f16.
+int lin_h(wh_model *m, const _Float16 *a, const wh_linear *l, void *c, int rows, int epi, int out16) {
+  return launch_gemm_h(m->ctx, a, l, c, rows, l->cols + l->dual, epi, 0.0f, out16);
+}
+
 // Parakeet Encoder::record (src/parakeet/encoder.rs:103-124) over `batch` windows of mel_frames
 // [batch][mel_frames][mels]; window b's first valid[b] mel frames are real.  One window: kestrel
 // masking as the reference (conv0/conv2 see the valid frames, conv5 the whole image).  Several
@@ -1082,20 +1087,24 @@ int parakeet_record(wh_model *m, const float *mel, int batch, int mel_frames, co
   wh_ctx *c = m->ctx;
   const int rows1 = 2 * t + 1;  // conv2's output rows from −1 on
   const size_t per = (size_t)rows1 * f2 * ch;
+  // The outputs whose only reader is a GEMM (which rounds its input to f16, RNE, as these kernels
+  // round their stores) are f16: conv2's (into sub), conv5's (into h), conv6's and the flattened rows.
+  // conv3's output stays f32: the depthwise conv5 reads it at full precision.
+  _Float16 *sub16 = (_Float16 *)m->sub, *h16 = (_Float16 *)m->h, *qk16 = (_Float16 *)m->qk;
   for (int b = 0; b < batch; b++) {
     int v = std::min(std::max(valid[b], 1), mel_frames);
     CK(launch_depthwise(c, mel + (size_t)b * mel_frames * mels, m->sc0.w, m->sc0.b, m->sc2.w, m->sc2.b,
-                        m->sub + per * b, v, mels, ch, 0, rows1));
+                        sub16 + per * b, v, mels, ch, 0, rows1, 1));
   }
-  CK(lin(m, m->sub, m->conv3, m->sub2, rows1 * f2 * batch, WH_RELU));
+  CK(lin_h(m, sub16, m->conv3, m->sub2, rows1 * f2 * batch, WH_RELU, 0));
   for (int b = 0; b < batch; b++) {
     int img = batch == 1 ? t2 : half_len(half_len(std::min(std::max(valid[b], 1), mel_frames)));
-    CK(launch_depthwise(c, m->sub2 + per * b, nullptr, nullptr, m->sc5.w, m->sc5.b, m->h + (size_t)b * t * f * ch,
-                        img, f2, ch, 0, t));
+    CK(launch_depthwise(c, m->sub2 + per * b, nullptr, nullptr, m->sc5.w, m->sc5.b, h16 + (size_t)b * t * f * ch,
+                        img, f2, ch, 0, t, 1));
   }
-  CK(lin(m, m->h, m->conv6, m->qk, t * f * batch, WH_RELU));
-  CK(launch_flatten(c, m->qk, m->h, t * batch, f, ch));
-  CK(lin(m, m->h, m->pre_out, m->x, t * batch, WH_BIAS));
+  CK(lin_h(m, h16, m->conv6, qk16, t * f * batch, WH_RELU, 1));
+  CK(launch_flatten(c, qk16, h16, t * batch, f, ch, 1));
+  CK(lin_h(m, h16, m->pre_out, m->x, t * batch, WH_BIAS, 0));
   CK(record_blocks(m, t, batch, batch > 1 ? m->valid_dev : nullptr, m->layers));
   return lin(m, m->x, m->joint_enc, out, t * batch, WH_BIAS);
 }

@@ -257,9 +257,11 @@ __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__
 __host__ __device__ __forceinline__ int half_len(int n) { return (n - 1) / 2 + 1; }
 
 // Depthwise 3×3 stride-2 pad-1 conv + bias over the image [t][f][ch]; x holds rows 2·t0 − 1..;
-// output rows t0 + blockIdx.y of y [⌈t/2⌉][⌈f/2⌉][ch] (spatial.wgsl:31-48).
+// output rows t0 + blockIdx.y of y [⌈t/2⌉][⌈f/2⌉][ch] (spatial.wgsl:31-48), f32 or, for a consumer
+// that rounds it to f16 anyway (a GEMM), f16 (TO).
+template <typename TO>
 __global__ void depthwise_kernel(const float *__restrict__ x, const float *__restrict__ w, const float *__restrict__ b,
-                                 float *__restrict__ y, int t, int f, int ch, int t0) {
+                                 TO *__restrict__ y, int t, int f, int ch, int t0) {
   const int fo = blockIdx.x, k = blockIdx.y, fh = half_len(f);
   for (int c = threadIdx.x; c < ch; c += blockDim.x) {
     // The 9 taps and inputs loaded first (clamped to an in-bounds element, unused ones skipped
@@ -286,7 +288,7 @@ __global__ void depthwise_kernel(const float *__restrict__ x, const float *__res
         if (ti >= 1 && ti <= t && fi >= 1 && fi <= f) acc += wv[i * 3 + j] * xv[i * 3 + j];
       }
     }
-    y[((size_t)(t0 + k) * fh + fo) * ch + c] = acc;
+    y[((size_t)(t0 + k) * fh + fo) * ch + c] = (TO)acc;
   }
 }
 
@@ -294,9 +296,10 @@ __global__ void depthwise_kernel(const float *__restrict__ x, const float *__res
 // blockIdx.y of a chunk (output row 2·t0 − 1 + blockIdx.y; rows from ⌈t/4⌉ on zero, as masked)
 // (spatial.wgsl:50-107; src/parakeet/cpu.rs:103-152).  A workgroup makes the whole output row, one
 // thread per channel: the row's 7 × (4·f2 + 3) input patch goes to LDS once and each thread keeps
-// its channel's 18 taps in registers across the f2 positions.
+// its channel's 18 taps in registers across the f2 positions.  Output f32 or f16 (TO), as above.
+template <typename TO>
 __global__ void first_depthwise_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                       const float *__restrict__ b, float *__restrict__ y,
+                                       const float *__restrict__ b, TO *__restrict__ y,
                                        const float *__restrict__ w0, const float *__restrict__ b0, int t,
                                        int f, int ch, int t0) {
   extern __shared__ float xs[];  // 7 rows × pw columns; column 4·fo + j is input column 4·fo + j − 3
@@ -370,7 +373,7 @@ __global__ void first_depthwise_kernel(const float *__restrict__ x, const float 
           }
         }
       }
-      y[((size_t)blockIdx.y * f2 + fo) * ch + c] = masked ? 0.0f : acc;
+      y[((size_t)blockIdx.y * f2 + fo) * ch + c] = (TO)(masked ? 0.0f : acc);
     }
   }
 }
@@ -379,16 +382,16 @@ __global__ void first_depthwise_kernel(const float *__restrict__ x, const float 
 // f × ch block through LDS, read and written coalesced (the strided reads of the plain kernel below
 // touch one float per 1 KiB), every load before any store.  LDS rows are padded by 4 floats, so the
 // transposed reads of 64 lanes (16 rows × 4 columns) hit 64 distinct banks when ch % 64 == 0.
-template <int P>
-__global__ __launch_bounds__(256) void flatten_lds_kernel(const float *__restrict__ x, float *__restrict__ y, int lf,
-                                                          int lch) {
+// Elements of type T (f32, or f16 between a GEMM's f16 output and the next GEMM).
+template <int P, typename T>
+__global__ __launch_bounds__(256) void flatten_lds_kernel(const T *__restrict__ x, T *__restrict__ y, int lf, int lch) {
   extern __shared__ float tl[];
   const int n = 1 << (lf + lch), cp = (1 << lch) + 4, tid = threadIdx.x;
-  const float *xr = x + (size_t)blockIdx.x * n;
-  float *yr = y + (size_t)blockIdx.x * n;
+  const T *xr = x + (size_t)blockIdx.x * n;
+  T *yr = y + (size_t)blockIdx.x * n;
   float v[P];
 #pragma unroll
-  for (int q = 0; q < P; q++) v[q] = xr[min(tid + 256 * q, n - 1)];  // clamped: no branch
+  for (int q = 0; q < P; q++) v[q] = (float)xr[min(tid + 256 * q, n - 1)];  // clamped: no branch
 #pragma unroll
   for (int q = 0; q < P; q++) {
     const int e = min(tid + 256 * q, n - 1);  // input element e = fi·ch + c (past n: the last again)
@@ -398,14 +401,15 @@ __global__ __launch_bounds__(256) void flatten_lds_kernel(const float *__restric
 #pragma unroll
   for (int q = 0; q < P; q++) {
     const int e = tid + 256 * q;  // output element e = c·f + fi
-    if (e < n) yr[e] = tl[(e & ((1 << lf) - 1)) * cp + (e >> lf)];
+    if (e < n) yr[e] = (T)tl[(e & ((1 << lf) - 1)) * cp + (e >> lf)];
   }
 }
 
-__global__ void flatten_kernel(const float *__restrict__ x, float *__restrict__ y, int f, int ch) {
+template <typename T>
+__global__ void flatten_kernel(const T *__restrict__ x, T *__restrict__ y, int f, int ch) {
   const int n = f * ch;
-  const float *xr = x + (size_t)blockIdx.x * n;
-  float *yr = y + (size_t)blockIdx.x * n;
+  const T *xr = x + (size_t)blockIdx.x * n;
+  T *yr = y + (size_t)blockIdx.x * n;
   for (int e = threadIdx.x; e < n; e += blockDim.x) yr[e] = xr[(e % f) * ch + e / f];
 }
 
@@ -732,34 +736,45 @@ int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb
 }
 
 int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *b0, const float *w,
-                     const float *b, float *y, int t, int f, int ch, int t0, int rows) {
+                     const float *b, void *y, int t, int f, int ch, int t0, int rows, int out16) {
   if (t <= 0 || f <= 0 || ch <= 0 || t0 < 0 || rows < 0) return wh_fail(ctx, WH_EARG, "depthwise: bad shape");
   if (!rows) return WH_OK;
   int threads = ch >= 256 ? 256 : ((ch + 63) / 64) * 64;
+  const double ob = out16 ? 2.0 : 4.0;  // output bytes per value
   ProfScope prof(ctx, w0 ? "first_depthwise" : "depthwise", 0.0,
-                 4.0 * rows * half_len(w0 ? half_len(f) : f) * ch * (w0 ? 1 : 4));
+                 rows * half_len(w0 ? half_len(f) : f) * ch * (w0 ? ob : ob + 4.0 * 4));
   if (w0) {
     const size_t lds = sizeof(float) * 7 * (4 * (size_t)half_len(half_len(f)) + 4);
     if (lds > 64 * 1024) return wh_fail(ctx, WH_EARG, "depthwise: %d mel bins is more than one workgroup's patch holds", f);
-    wh_launch(ctx, first_depthwise_kernel, dim3(1, rows), threads < 64 ? 64 : threads, lds, x, w, b, y, w0, b0, t, f, ch, t0);
+    const dim3 grid(1, rows);
+    const int nt = threads < 64 ? 64 : threads;
+    if (out16) wh_launch(ctx, first_depthwise_kernel<_Float16>, grid, nt, lds, x, w, b, (_Float16 *)y, w0, b0, t, f, ch, t0);
+    else wh_launch(ctx, first_depthwise_kernel<float>, grid, nt, lds, x, w, b, (float *)y, w0, b0, t, f, ch, t0);
   } else {
-    dim3 grid(half_len(f), rows);
-    wh_launch(ctx, depthwise_kernel, grid, threads, 0, x, w, b, y, t, f, ch, t0);
+    const dim3 grid(half_len(f), rows);
+    if (out16) wh_launch(ctx, depthwise_kernel<_Float16>, grid, threads, 0, x, w, b, (_Float16 *)y, t, f, ch, t0);
+    else wh_launch(ctx, depthwise_kernel<float>, grid, threads, 0, x, w, b, (float *)y, t, f, ch, t0);
   }
   return wh_launched(ctx, "depthwise");
 }
 
-int launch_flatten(wh_ctx *ctx, const float *x, float *y, int t, int f, int ch) {
-  if (t < 0 || f <= 0 || ch <= 0) return wh_fail(ctx, WH_EARG, "flatten: bad shape");
-  if (!t) return WH_OK;
-  ProfScope prof(ctx, "flatten", 0.0, 8.0 * t * f * ch);
+template <typename T>
+static void flatten_t(wh_ctx *ctx, const T *x, T *y, int t, int f, int ch) {
   const bool pow2 = (f & (f - 1)) == 0 && (ch & (ch - 1)) == 0;
   if (pow2 && (long)f * ch <= 16 * 256) {
     const int lf = __builtin_ctz(f), lch = __builtin_ctz(ch);
-    wh_launch(ctx, flatten_lds_kernel<16>, t, 256, sizeof(float) * (size_t)f * (ch + 4), x, y, lf, lch);
+    wh_launch(ctx, flatten_lds_kernel<16, T>, t, 256, sizeof(float) * (size_t)f * (ch + 4), x, y, lf, lch);
   } else {
-    wh_launch(ctx, flatten_kernel, t, 256, 0, x, y, f, ch);
+    wh_launch(ctx, flatten_kernel<T>, t, 256, 0, x, y, f, ch);
   }
+}
+
+int launch_flatten(wh_ctx *ctx, const void *x, void *y, int t, int f, int ch, int f16) {
+  if (t < 0 || f <= 0 || ch <= 0) return wh_fail(ctx, WH_EARG, "flatten: bad shape");
+  if (!t) return WH_OK;
+  ProfScope prof(ctx, "flatten", 0.0, (f16 ? 4.0 : 8.0) * t * f * ch);
+  if (f16) flatten_t(ctx, (const _Float16 *)x, (_Float16 *)y, t, f, ch);
+  else flatten_t(ctx, (const float *)x, (float *)y, t, f, ch);
   return wh_launched(ctx, "flatten");
 }
 

@@ -59,6 +59,9 @@ def tdt_parity(om, got, want):
 # summing in different orders, so their logits differ by about 1e-6 of the output layer's Lipschitz
 # bound times |z|; a flipped decision needs an oracle top-2 gap of that order.
 TDT_TIE_REL = 1e-4
+# After a near-tie flip the two decoders carry different predictor states; the encoder rows bring them
+# back to the same decisions within this many frames, from where on every entry must agree again.
+TDT_RESYNC_FRAMES = 50
 
 
 def tdt_device_parity(om, tokens, enc):
@@ -66,8 +69,9 @@ def tdt_device_parity(om, tokens, enc):
     Identical, or else the first flipped decision is a near tie: it lies after the oracle's decision
     that emitted the last shared token (the lists agree up to it) and at a frame no later than either
     list's first differing entry, and some oracle decision in that window has a top-2 gap of at most
-    TDT_TIE_REL times the joint output layer's Lipschitz bound.  Returns None or (index, frame,
-    smallest gap in the window, bound)."""
+    TDT_TIE_REL times the joint output layer's Lipschitz bound; and the lists agree again, entry for
+    entry, from some frame within TDT_RESYNC_FRAMES after it (no second divergence goes unchecked).
+    Returns None or (index, frame, smallest gap in the window, bound)."""
     want, trace, gaps = om.tdt_trace(enc)
     if tokens == want:
         return None
@@ -86,4 +90,7 @@ def tdt_device_parity(om, tokens, enc):
     gap = float(min(gaps[k] for k in window))
     bound = TDT_TIE_REL * om.tdt_lipschitz()
     assert gap <= bound, f"token {i} (frame {frame}) differs; smallest gap in decisions {start}.. is {gap:.3g} > bound {bound:.3g}"
+    later = lambda lst, g: [e for e in lst if e[1] >= g]
+    assert any(later(tokens, g) == later(want, g) for g in range(frame + 1, frame + TDT_RESYNC_FRAMES + 1)), (
+        f"after the near tie at token {i} (frame {frame}) the lists do not agree again within {TDT_RESYNC_FRAMES} frames")
     return i, frame, gap, bound

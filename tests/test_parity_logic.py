@@ -1,10 +1,12 @@
 """The token-parity checks themselves, with flips planted in CPU-side logits: a near-tie flip under
-typical noise passes, a flip at a frame whose discrepancy is far above the typical noise fails."""
+typical noise passes, a flip at a frame whose discrepancy is far above the typical noise fails; for the
+device TDT decoder, a near-tie flip after which the lists agree again passes, one after which they keep
+differing fails."""
 
 import numpy as np
 import pytest
 
-from parity import ctc_parity, top2_gap
+from parity import ctc_parity, tdt_device_parity, top2_gap
 
 
 def noisy(w, eps, seed):
@@ -36,3 +38,44 @@ def test_a_flip_far_above_the_noise_fails():
 
 def test_top2_gap():
     assert top2_gap([1.0, 3.0, 2.5]) == pytest.approx(0.5)
+
+
+class TdtTrace:
+    """The oracle's side of tdt_device_parity: its (token, frame) list, its decisions (frame, token) and
+    their top-2 gaps, and the joint's Lipschitz bound."""
+
+    def __init__(self, want, trace, gaps, lipschitz=1.0):
+        self.want, self.trace, self.gaps, self.lipschitz = want, trace, gaps, lipschitz
+
+    def tdt_trace(self, enc):
+        return self.want, self.trace, self.gaps
+
+    def tdt_lipschitz(self):
+        return self.lipschitz
+
+
+WANT = [(5, 0), (7, 2), (9, 4), (3, 10), (4, 60), (6, 70)]
+TRACE = [(f, t) for t, f in WANT]
+
+
+def test_tdt_identical_lists_pass():
+    assert tdt_device_parity(TdtTrace(WANT, TRACE, [1.0] * 6), list(WANT), None) is None
+
+
+def test_tdt_near_tie_then_agreement_passes():
+    got = [(5, 0), (7, 2), (8, 4), (3, 10), (4, 60), (6, 70)]
+    om = TdtTrace(WANT, TRACE, [1.0, 1.0, 1e-9, 1.0, 1.0, 1.0])
+    assert tdt_device_parity(om, got, None)[:2] == (2, 4)
+
+
+def test_tdt_near_tie_then_lasting_difference_fails():
+    got = [(5, 0), (7, 2), (8, 4), (1, 10), (2, 60), (2, 70)]
+    om = TdtTrace(WANT, TRACE, [1.0, 1.0, 1e-9, 1.0, 1.0, 1.0])
+    with pytest.raises(AssertionError, match="do not agree again"):
+        tdt_device_parity(om, got, None)
+
+
+def test_tdt_flip_without_a_near_tie_fails():
+    got = [(5, 0), (7, 2), (8, 4), (3, 10), (4, 60), (6, 70)]
+    with pytest.raises(AssertionError, match="smallest gap"):
+        tdt_device_parity(TdtTrace(WANT, TRACE, [1.0] * 6), got, None)

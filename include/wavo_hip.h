@@ -91,6 +91,8 @@ void *wh_stream(wh_ctx *ctx);
  *   "gemm_shape_plans" "m,cols,k:bm,bn,wm,wn,slots,split[,pipeline[,kgroups]];..." per call shape ("" clears);
  *   "gemm_kernel_only" "1": a k-split GEMM call stops after its GEMM kernel and leaves c unwritten
  *                      (to time that kernel alone, as a model step runs it); "0" restores;
+ *   "gemm_group"       "n": the GEMM's XCDs take tiles in groups of n row tiles, column by column inside a
+ *                      group (0 = chosen per plan; the output is the same bit for bit);
  *   "attn_split"       "n": attention splits its key range n ways (0 = chosen per shape);
  *   "position_cache"   "0": the Parakeet encoder recomputes its relative-position projection every call
  *                      instead of keeping it for the frame count its buffer holds (to time it); "1" restores;

@@ -324,7 +324,7 @@ class Gpu:
 
     def tune(self, key, value):
         """Tuning and measurement overrides (wh_tune): gemm_plan, gemm_shape_plans, gemm_kernel_only,
-        attn_split, position_cache, and the check switches mel_raw, whisper_host, whisper_logprobs, attend_merge,
+        gemm_group, attn_split, position_cache, and the check switches mel_raw, whisper_host, whisper_logprobs, attend_merge,
         attn_pack."""
         self._check(lib().wh_tune(self.h, key.encode(), str(value).encode()))
 

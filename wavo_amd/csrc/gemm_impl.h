@@ -381,6 +381,8 @@ struct LdsArgs {
   // input-independent GEMM whose output is kept between calls, tagged on the device).
   const int *skip;
   int skip_val;
+  // Row tiles per group of the tile order (1: row by row; see the kernel's tile order).
+  int group;
 };
 
 // s_waitcnt with vmcnt = N (0..63) and no wait on the other counters (gfx9 encoding: vmcnt bits
@@ -663,19 +665,19 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_lds_kernel(LdsArgs P) 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // Tile order.  Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its own L2.
-  // The grid is renumbered so that an XCD takes a contiguous run of (split, row tile, column tile):
-  // one k split and a band of row tiles over all column tiles, in order, so that the workgroups
-  // running at once on an XCD share their rows of a and the XCDs do not all fetch the same a
-  // (measured against the dispatch order and against bands of column tiles: Parakeet 60 s
-  // 5.02 against 5.18 and 5.12 ms per call, 16 windows 30.9 against 31.9 ms).
+  // The grid is renumbered so that an XCD takes a contiguous run l of tiles of one k split, and the
+  // run is ordered in groups of P.group row tiles, column by column inside a group: an XCD's tiles
+  // then form a rectangle of row tiles x column tiles, whose rows of a and of w its L2 fetches once.
+  // (P.group 1: a band of row tiles over all column tiles, which fetches the whole of w per XCD.)
   int tx = blockIdx.x, ty = blockIdx.y, tz = blockIdx.z;
   {
     const int nx = gridDim.x, ny = gridDim.y, total = nx * ny * gridDim.z;
     if (total % 8 == 0) {
       const int lin = tx + nx * (ty + ny * tz), l = (lin % 8) * (total / 8) + lin / 8;
       tz = l / (nx * ny);
-      ty = (l % (nx * ny)) / nx;
-      tx = l % nx;
+      const int e = l % (nx * ny), g0 = e / (P.group * nx) * P.group, gh = min(P.group, ny - g0), w = e - g0 * nx;
+      ty = g0 + w % gh;
+      tx = w / gh;
     }
   }
   const int n0 = tx * BN, m0 = ty * BM;
@@ -1049,7 +1051,7 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
   if ((p.split > 1 && !part) || nho) p.split = 1;  // packed ranges are written by the tiles' own epilogue
   if (splits) *splits = p.split;
   LdsArgs args{a, l->w, l->bias, p.split > 1 ? (void *)part : c, m, l->rows, l->cols, l->k, l->dual, ldc, epi, alpha,
-               l->row_bytes, {}, nho, nullptr, 0};
+               l->row_bytes, {}, nho, nullptr, 0, 1};
   // A tagged output (ctx->gemm_skip, set by the caller for this launch): whole-k plans only (a split
   // launch's partial sums are finished by another kernel).
   if (ctx->gemm_skip && p.split == 1) args.skip = ctx->gemm_skip, args.skip_val = ctx->gemm_skip_val;
@@ -1063,6 +1065,11 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     args.ho[i] = h;
   }
   dim3 grid((l->cols + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.split);
+  // Tile order: k-group plans (few tiles per CU, w from HBM) in groups of 2 row tiles, the others row
+  // by row (Parakeet 60 s in-step: the 750x4096x1024 up projections 15.5 -> 14.8 us, while the
+  // 64x64 qkv projection, a single k group, slows with every group size above 1).
+  const int group = ctx->gemm_group ? ctx->gemm_group : p.wk > 1 ? 2 : 1;
+  args.group = std::max(1, std::min(group, (int)grid.y));
   static const char *tn = WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
   // Named by kernel variant and call shape: m x rows x k, epilogue, output type, row width.
   char name[128];

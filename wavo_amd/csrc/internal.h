@@ -40,6 +40,9 @@ struct wh_ctx {
   // Per-shape overrides set by wh_tune("gemm_shape_plans", "m,cols,k:bm,bn,wm,wn,slots,split[,pipeline[,kgroups]];…")
   // (tuning sweeps inside a model's step only).
   std::vector<std::array<int, 11>> gemm_shape_plans;
+  // GEMM tile-order override set by wh_tune("gemm_group", "n") (tuning sweeps only): n row tiles per
+  // group of the order; 0 = chosen per shape.
+  int gemm_group = 0;
   // Attention key-split override set by wh_tune("attn_split", "n") (tuning sweeps only): 0 = chosen per shape.
   int attn_split = 0;
   // Set by a caller around one GEMM call (null otherwise): the main kernel skips when *gemm_skip ==

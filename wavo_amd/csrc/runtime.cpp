@@ -396,6 +396,8 @@ int wh_tune(wh_ctx *ctx, const char *key, const char *value) {
     ctx->gemm_kernel_only = atoi(v) != 0;
   } else if (!strcmp(key, "position_cache")) {
     ctx->no_position_cache = atoi(v) == 0;
+  } else if (!strcmp(key, "gemm_group")) {
+    ctx->gemm_group = std::max(0, atoi(v));
   } else if (!strcmp(key, "attn_split")) {
     ctx->attn_split = std::max(0, std::min(atoi(v), 64));
   } else if (!strcmp(key, "mel_raw")) {

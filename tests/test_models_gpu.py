@@ -89,17 +89,24 @@ def test_parakeet_small(gpu, wtype):
 def test_parakeet_attention_reads_in_place(gpu, small, seconds):
     """One window's attention reads K and the position rows where the projections wrote them, and Vᵀ
     from the qkv projection's epilogue (no packing launch).  The operands are the same f16 values as
-    after packing, so the encoder output equals the packed path's (wh_tune attn_pack) bit for bit."""
+    after packing, so the encoder output equals the packed path's (wh_tune attn_pack) bit for bit.
+    Each setting runs eagerly, then recorded, then replayed (a tuning change is not replayed from a
+    recording made before it)."""
     m = wa.Model(gpu, synth.model_path("parakeet", small=small, directory=MODELS))
     mel = synth.parakeet_mel(synth.audio(seconds, seed=9))
     direct = m.encode(mel)
-    gpu.tune("attn_pack", 1)
-    try:
-        packed = m.encode(mel)
-    finally:
-        gpu.tune("attn_pack", 0)
-    assert direct.shape == packed.shape
-    assert np.array_equal(direct, packed), float(np.abs(direct - packed).max())
+    outs = {}
+    for key in ("attn_pack",):
+        gpu.tune(key, 1)
+        try:
+            outs[key] = [m.encode(mel) for _ in range(3)]
+        finally:
+            gpu.tune(key, 0)
+    outs["default"] = [m.encode(mel) for _ in range(3)]
+    for key, runs in outs.items():
+        for got in runs:
+            assert got.shape == direct.shape
+            assert np.array_equal(direct, got), (key, float(np.abs(direct - got).max()))
 
 
 def test_parakeet_kestrel_valid(gpu):

@@ -62,6 +62,9 @@ struct wh_ctx {
   // wh_tune("attend_merge", "1") (checks only): attention over a key count known at launch merges its
   // parts in its last workgroup, as for a count in device memory, instead of a second kernel.
   int attend_merge = 0;
+  // Bumped by every wh_tune call: the model's recorded calls carry it in their keys, so that a call
+  // recorded before a tuning change is not replayed after it.
+  long tune_epoch = 0;
   // wh_tune("attn_pack", "1") (checks only): the encoder's attention packs K, Vᵀ and the position rows
   // in a launch of its own, as for padded batches, instead of reading them where they were written.
   int attn_pack = 0;

@@ -1111,10 +1111,12 @@ int parakeet_record(wh_model *m, const float *mel, int batch, int mel_frames, co
 
 // Runs `record` (a function queuing kernels only) for the call identified by `key`: eagerly the first
 // time, recorded into a HIP graph the second time, replayed from then on.  Buffers the graph names
-// must not move: the key carries the arena's and the scratch's generations.
+// must not move: the key carries the arena's and the scratch's generations (and the context's tuning
+// generation: a recording made under other launch plans is not replayed).
 template <typename F>
 int run_recorded(wh_model *m, std::vector<intptr_t> key, F &&record) {
   wh_ctx *c = m->ctx;
+  key.push_back(c->tune_epoch);
   key.push_back(m->epoch);
   key.push_back(c->scratch_epoch);
   if (!m->use_graph || c->prof) return record();
@@ -1151,8 +1153,9 @@ int run_recorded(wh_model *m, std::vector<intptr_t> key, F &&record) {
   // destroyed once its queued launches are done).
   bool drained = false;
   for (size_t i = 0; i < m->graphs.size();)
-    if (m->graphs[i].key[m->graphs[i].key.size() - 2] != m->epoch ||
-        m->graphs[i].key.back() != c->scratch_epoch || m->graphs.size() >= 8) {
+    if (m->graphs[i].key[m->graphs[i].key.size() - 3] != c->tune_epoch ||
+        m->graphs[i].key[m->graphs[i].key.size() - 2] != m->epoch || m->graphs[i].key.back() != c->scratch_epoch ||
+        m->graphs.size() >= 8) {
       destroy_graph(m, m->graphs[i].exec, m->graphs[i].graph, drained);
       m->graphs.erase(m->graphs.begin() + i);
     } else {

@@ -370,6 +370,7 @@ void *wh_stream(wh_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 
 int wh_tune(wh_ctx *ctx, const char *key, const char *value) {
   if (!ctx || !key) return WH_EARG;
+  ctx->tune_epoch++;
   const char *v = value ? value : "";
   if (!strcmp(key, "gemm_plan")) {
     int o[8] = {0, 0, 0, 0, 0, 0, 0, 0};

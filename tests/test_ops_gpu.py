@@ -494,9 +494,11 @@ def test_flatten_power_of_two(gpu, t, f, ch):
     assert np.array_equal(gpu.read(fb, (t, f * ch)), ox.flatten(x, t, f, ch))
 
 
+# ch = 5: one channel per thread; ch % 4 == 0: four channels and four output columns per thread (a
+# partial group of columns at f 11, 13 and 40).
 @pytest.mark.parametrize("valid_drop", [0, 1])
-def test_subsampling(gpu, valid_drop):
-    t, f, ch = 29, 11, 5
+@pytest.mark.parametrize("t,f,ch", [(29, 11, 5), (29, 11, 8), (29, 13, 12), (37, 32, 64), (29, 40, 4)])
+def test_subsampling(gpu, valid_drop, t, f, ch):
     valid = t - valid_drop
     mel = rnd(t * f, 19).reshape(t, f)
     ws = [rnd(ch * 9, 20 + i) if i % 2 == 0 else rnd(ch, 20 + i) for i in range(6)]

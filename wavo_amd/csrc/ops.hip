@@ -285,10 +285,61 @@ __global__ void depthwise_kernel(const float *__restrict__ x, const float *__res
 #pragma unroll
       for (int j = 0; j < 3; j++) {
         const int fi = 2 * fo + j;
-        if (ti >= 1 && ti <= t && fi >= 1 && fi <= f) acc += wv[i * 3 + j] * xv[i * 3 + j];
+        if (ti >= 1 && ti <= t && fi >= 1 && fi <= f) acc = fmaf(wv[i * 3 + j], xv[i * 3 + j], acc);
       }
     }
     y[((size_t)(t0 + k) * fh + fo) * ch + c] = (TO)acc;
+  }
+}
+
+// The same conv for ch % 4 == 0 and 16-byte aligned rows: a thread makes DW_COLS consecutive output
+// columns of 4 channels (item (row, column group, channel quad), quads fastest), its 3 × (2·DW_COLS + 1)
+// input quads and 9 tap quads all loaded before the first product (one memory round trip; adjacent
+// outputs share their edge column), the sums in the same tap order as depthwise_kernel.
+constexpr int DW_COLS = 4;
+template <typename TO>
+__global__ __launch_bounds__(256) void depthwise4_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                         const float *__restrict__ b, TO *__restrict__ y, int t, int f,
+                                                         int ch, int t0, int rows) {
+  constexpr int NI = 2 * DW_COLS + 1;
+  const int q4 = ch / 4, fh = half_len(f), groups = (fh + DW_COLS - 1) / DW_COLS;
+  const long item = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (item >= (long)rows * groups * q4) return;
+  const int c4 = (int)(item % q4), grp = (int)((item / q4) % groups), k = (int)(item / ((long)q4 * groups));
+  const int fo0 = grp * DW_COLS, c = 4 * c4;
+  float4 xv[3][NI], wv[9];
+#pragma unroll
+  for (int i = 0; i < 3; i++) {
+    const int ti = 2 * (t0 + k) + i;
+#pragma unroll
+    for (int jj = 0; jj < NI; jj++) {
+      const int fi = 2 * fo0 + jj;  // input column fi − 1 (padding at fi = 0 and past f)
+      const bool in = ti >= 1 && ti <= t && fi >= 1 && fi <= f;
+      xv[i][jj] = *(const float4 *)(x + (in ? ((size_t)(2 * k + i) * f + fi - 1) * ch + c : (size_t)c));
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 9; q++) wv[q] = *(const float4 *)(w + (size_t)q * ch + c);
+  const float4 bias = *(const float4 *)(b + c);
+#pragma unroll
+  for (int o = 0; o < DW_COLS; o++) {
+    const int fo = fo0 + o;
+    if (fo >= fh) break;
+    float4 acc = bias;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const int ti = 2 * (t0 + k) + i;
+#pragma unroll
+      for (int j = 0; j < 3; j++) {
+        const int fi = 2 * fo + j;
+        if (ti >= 1 && ti <= t && fi >= 1 && fi <= f) {
+          const float4 a = wv[i * 3 + j], v = xv[i][2 * o + j];
+          acc.x = fmaf(a.x, v.x, acc.x), acc.y = fmaf(a.y, v.y, acc.y);
+          acc.z = fmaf(a.z, v.z, acc.z), acc.w = fmaf(a.w, v.w, acc.w);
+        }
+      }
+    }
+    store4(y + ((size_t)(t0 + k) * fh + fo) * ch + c, acc);
   }
 }
 
@@ -750,6 +801,12 @@ int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *
     const int nt = threads < 64 ? 64 : threads;
     if (out16) wh_launch(ctx, first_depthwise_kernel<_Float16>, grid, nt, lds, x, w, b, (_Float16 *)y, w0, b0, t, f, ch, t0);
     else wh_launch(ctx, first_depthwise_kernel<float>, grid, nt, lds, x, w, b, (float *)y, w0, b0, t, f, ch, t0);
+  } else if (ch % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)b % 16 == 0 &&
+             (uintptr_t)y % (out16 ? 8 : 16) == 0) {
+    const long items = (long)rows * ((half_len(f) + DW_COLS - 1) / DW_COLS) * (ch / 4);
+    const int blocks = (int)((items + 255) / 256);
+    if (out16) wh_launch(ctx, depthwise4_kernel<_Float16>, blocks, 256, 0, x, w, b, (_Float16 *)y, t, f, ch, t0, rows);
+    else wh_launch(ctx, depthwise4_kernel<float>, blocks, 256, 0, x, w, b, (float *)y, t, f, ch, t0, rows);
   } else {
     const dim3 grid(half_len(f), rows);
     if (out16) wh_launch(ctx, depthwise_kernel<_Float16>, grid, threads, 0, x, w, b, (_Float16 *)y, t, f, ch, t0);

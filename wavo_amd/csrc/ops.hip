@@ -17,8 +17,16 @@ using xlane::wave_sum;
 constexpr int ROW_REGS = 32;  // row values per lane held in registers: rows up to 2048
 
 __device__ __forceinline__ void store4(float *p, float4 v) { *(float4 *)p = v; }
+// The f32 values rounded to f16 (RNE), as a GEMM rounds an f32 input: the empty asm keeps the compiler
+// from fusing the last multiply-add into an f16-rounding one (v_fma_mix*), which rounds once from the
+// exact sum instead.
+__device__ __forceinline__ float as_f32(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
 __device__ __forceinline__ void store4(_Float16 *p, float4 v) {
   typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  v.x = as_f32(v.x), v.y = as_f32(v.y), v.z = as_f32(v.z), v.w = as_f32(v.w);
   *(h4 *)p = h4{(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
 }
 
@@ -288,7 +296,7 @@ __global__ void depthwise_kernel(const float *__restrict__ x, const float *__res
         if (ti >= 1 && ti <= t && fi >= 1 && fi <= f) acc = fmaf(wv[i * 3 + j], xv[i * 3 + j], acc);
       }
     }
-    y[((size_t)(t0 + k) * fh + fo) * ch + c] = (TO)acc;
+    y[((size_t)(t0 + k) * fh + fo) * ch + c] = (TO)as_f32(acc);
   }
 }
 
@@ -343,88 +351,114 @@ __global__ __launch_bounds__(256) void depthwise4_kernel(const float *__restrict
   }
 }
 
-// conv0 (1 → ch, 3×3 s2 p1) + ReLU, never stored, then the depthwise conv2 + bias, into row
-// blockIdx.y of a chunk (output row 2·t0 − 1 + blockIdx.y; rows from ⌈t/4⌉ on zero, as masked)
-// (spatial.wgsl:50-107; src/parakeet/cpu.rs:103-152).  A workgroup makes the whole output row, one
-// thread per channel: the row's 7 × (4·f2 + 3) input patch goes to LDS once and each thread keeps
-// its channel's 18 taps in registers across the f2 positions.  Output f32 or f16 (TO), as above.
+// conv0 (1 → ch, 3×3 s2 p1) + ReLU, never stored, then the depthwise conv2 + bias, into rows
+// 2·blockIdx.y and 2·blockIdx.y + 1 of a chunk (chunk row q is output row 2·t0 − 1 + q; rows from ⌈t/4⌉
+// on zero, as masked) (spatial.wgsl:50-107; src/parakeet/cpu.rs:103-152).  A workgroup makes two
+// whole output rows, one thread per channel: their 11 × (4·f2 + 3) input patch goes to LDS once, each
+// thread keeps its channel's 18 taps in registers across the f2 positions, and the two rows share the
+// conv0 row between them (5 conv0 rows per column, not 6).  Along the columns, the conv0 values and
+// the input chunk a column shares with the next are carried over.  Output f32 or f16 (TO), as above.
 template <typename TO>
 __global__ void first_depthwise_kernel(const float *__restrict__ x, const float *__restrict__ w,
                                        const float *__restrict__ b, TO *__restrict__ y,
                                        const float *__restrict__ w0, const float *__restrict__ b0, int t,
-                                       int f, int ch, int t0) {
-  extern __shared__ float xs[];  // 7 rows × pw columns; column 4·fo + j is input column 4·fo + j − 3
+                                       int f, int ch, int t0, int rows) {
+  // FD_ROWS rows × pw columns; column 4·fo + j is input column 4·fo + j − 3
+  extern __shared__ __attribute__((aligned(16))) float xs[];
+  constexpr int FD_ROWS = 11;
   const int t1 = half_len(t), f1 = half_len(f), f2 = half_len(f1);
-  const int r = 2 * t0 + blockIdx.y;  // output row + 1
-  const int pw = 4 * f2 + 4;  // the 4·f2 + 3 columns used, rows padded to 16 bytes
-  // The patch: every load of a thread issued before its stores (one round trip, not one per element
-  // group), from clamped addresses, for the first 8 groups of blockDim.x elements (the whole patch of
-  // 128 mel bins with 256 threads); any rest by the loop after.
+  const int q0 = 2 * blockIdx.y;  // the workgroup's first chunk row
+  const int r = 2 * t0 + q0;      // its output row + 1
+  const int pw = 4 * f2 + 4;      // the 4·f2 + 3 columns used, rows padded to 16 bytes
+  // The patch (input rows 4r − 7 .. 4r + 3): every load of a thread issued before its stores (one
+  // round trip, not one per element group), from clamped addresses, for the first 8 groups of
+  // blockDim.x elements (the whole patch of 128 mel bins with 256 threads); any rest by the loop after.
   {
     constexpr int G = 8;
     float v[G];
 #pragma unroll
     for (int q = 0; q < G; q++) {
-      const int e = min((int)threadIdx.x + q * (int)blockDim.x, 7 * pw - 1);
+      const int e = min((int)threadIdx.x + q * (int)blockDim.x, FD_ROWS * pw - 1);
       const int tm = 4 * r + e / pw - 7, fm = e % pw - 3;
       const bool in = tm >= 0 && tm < t && fm >= 0 && fm < f;
       const float xv = x[in ? (size_t)tm * f + fm : 0];
       v[q] = in ? xv : 0.0f;
     }
 #pragma unroll
-    for (int q = 0; q < G; q++) xs[min((int)threadIdx.x + q * (int)blockDim.x, 7 * pw - 1)] = v[q];
-    for (int e = threadIdx.x + G * blockDim.x; e < 7 * pw; e += blockDim.x) {
+    for (int q = 0; q < G; q++) xs[min((int)threadIdx.x + q * (int)blockDim.x, FD_ROWS * pw - 1)] = v[q];
+    for (int e = threadIdx.x + G * blockDim.x; e < FD_ROWS * pw; e += blockDim.x) {
       const int tm = 4 * r + e / pw - 7, fm = e % pw - 3;
       xs[e] = (tm >= 0 && tm < t && fm >= 0 && fm < f) ? x[(size_t)tm * f + fm] : 0.0f;
     }
   }
   __syncthreads();
-  const bool masked = r > half_len(t1);
+  const bool masked0 = r > half_len(t1), masked1 = r + 1 > half_len(t1), second = q0 + 1 < rows;
   for (int c = threadIdx.x; c < ch; c += blockDim.x) {
     float a[9], wd[9];
 #pragma unroll
     for (int q = 0; q < 9; q++) a[q] = w0[q * ch + c], wd[q] = w[q * ch + c];
     const float bias0 = b0[c], bias = b[c];
-    float carry[3] = {0.0f, 0.0f, 0.0f};  // ReLU(conv0) at conv1 column 2·fo, from the previous column's j = 2
-    for (int fo = 0; fo < f2; fo++) {
-      // The 7×7 input window of output column fo (rows 0..6, columns 4·fo .. 4·fo + 6), read as two
-      // 16-byte chunks per row (the same values in every lane: broadcast reads) instead of 81 scalars.
-      float px[7][8];
+    // ReLU(conv0) at conv1 rows 2r − 2 + u (u = 0..4) and columns 2·fo + jj (jj = 0..2).  Taps on
+    // padding (a row or column outside 1..t1, 1..f1) contribute zero, so every tap is summed without a
+    // branch: the rows' factor is folded into output row o's taps wm[o] once, the columns' into the
+    // values (column 2·fo + 1 ≤ 2·f2 − 1 ≤ f1 is always inside; 2·fo + 2 not at the last column when
+    // f1 is odd; column jj = 0 is the previous column's jj = 2, and padding for fo = 0).  The factors
+    // are multiplied in, not selected: a select lets the compiler branch around each conv0 sum, which
+    // splits the column into dozens of blocks.
+    float wm[2][9];
 #pragma unroll
-      for (int rr = 0; rr < 7; rr++) {
-        const float4 *row4 = (const float4 *)xs + rr * (pw / 4) + fo;  // 16-byte aligned (pw % 4 == 0)
-        const float4 c0 = row4[0], c1 = row4[1];
-        px[rr][0] = c0.x, px[rr][1] = c0.y, px[rr][2] = c0.z, px[rr][3] = c0.w;
-        px[rr][4] = c1.x, px[rr][5] = c1.y, px[rr][6] = c1.z, px[rr][7] = c1.w;
-      }
-      float acc = bias;
+    for (int o = 0; o < 2; o++)
 #pragma unroll
       for (int i = 0; i < 3; i++) {
-        const int ti = 2 * r + i - 2;
+        const int ti = 2 * (r + o) + i - 2;
+        const float rv = ti >= 1 && ti <= t1 ? 1.0f : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 3; j++) {
-          const int fi = 2 * fo + j;
-          if (j == 0 && fo > 0) {  // the same conv0 value the previous column computed as its j = 2
-            if (ti >= 1 && ti <= t1 && fi >= 1 && fi <= f1) acc += wd[i * 3] * carry[i];
-          } else if (ti >= 1 && ti <= t1 && fi >= 1 && fi <= f1) {
-            const int r0 = 2 * i, c = 2 * j;
-            float v = bias0;
-            v += a[0] * px[r0][c];
-            v += a[1] * px[r0][c + 1];
-            v += a[2] * px[r0][c + 2];
-            v += a[3] * px[r0 + 1][c];
-            v += a[4] * px[r0 + 1][c + 1];
-            v += a[5] * px[r0 + 1][c + 2];
-            v += a[6] * px[r0 + 2][c];
-            v += a[7] * px[r0 + 2][c + 1];
-            v += a[8] * px[r0 + 2][c + 2];
-            const float rv = fmaxf(v, 0.0f);
-            if (j == 2) carry[i] = rv;
-            acc += wd[i * 3 + j] * rv;
+        for (int j = 0; j < 3; j++) wm[o][i * 3 + j] = wd[i * 3 + j] * rv;
+      }
+    float cv[5][3];
+#pragma unroll
+    for (int u = 0; u < 5; u++) cv[u][2] = 0.0f;
+    // The 11 × 8 input window of column fo (patch columns 4·fo .. 4·fo + 7) as two 16-byte chunks per
+    // row, the second of which is the next column's first: two buffers that swap roles every column
+    // (the loop unrolled by two, so no chunk is copied).
+    float4 ca[FD_ROWS], cb[FD_ROWS];
+    const auto column = [&](int fo, const float4 *lo, float4 *hi) {
+#pragma unroll
+      for (int rr = 0; rr < FD_ROWS; rr++) hi[rr] = ((const float4 *)xs)[rr * (pw / 4) + fo + 1];
+      const float c2 = 2 * fo + 2 <= f1 ? 1.0f : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 5; u++) {
+        cv[u][0] = cv[u][2];
+#pragma unroll
+        for (int jj = 1; jj < 3; jj++) {
+          float v = bias0;
+#pragma unroll
+          for (int d = 0; d < 3; d++) {
+            const float4 l = lo[2 * u + d], h = hi[2 * u + d];
+            const float row[8] = {l.x, l.y, l.z, l.w, h.x, h.y, h.z, h.w};
+#pragma unroll
+            for (int e = 0; e < 3; e++) v = fmaf(a[3 * d + e], row[2 * jj + e], v);
           }
+          cv[u][jj] = jj == 2 ? fmaxf(v, 0.0f) * c2 : fmaxf(v, 0.0f);
         }
       }
-      y[((size_t)blockIdx.y * f2 + fo) * ch + c] = (TO)(masked ? 0.0f : acc);
+#pragma unroll
+      for (int o = 0; o < 2; o++) {
+        float acc = bias;
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+#pragma unroll
+          for (int j = 0; j < 3; j++) acc = fmaf(wm[o][i * 3 + j], cv[2 * o + i][j], acc);
+        acc = as_f32(acc);
+        if (o == 0) y[((size_t)q0 * f2 + fo) * ch + c] = (TO)(masked0 ? 0.0f : acc);
+        else if (second) y[((size_t)(q0 + 1) * f2 + fo) * ch + c] = (TO)(masked1 ? 0.0f : acc);
+      }
+    };
+#pragma unroll
+    for (int rr = 0; rr < FD_ROWS; rr++) ca[rr] = ((const float4 *)xs)[rr * (pw / 4)];
+    for (int fo = 0; fo < f2; fo += 2) {
+      column(fo, ca, cb);
+      if (fo + 1 < f2) column(fo + 1, cb, ca);
     }
   }
 }
@@ -795,12 +829,13 @@ int launch_depthwise(wh_ctx *ctx, const float *x, const float *w0, const float *
   ProfScope prof(ctx, w0 ? "first_depthwise" : "depthwise", 0.0,
                  rows * half_len(w0 ? half_len(f) : f) * ch * (w0 ? ob : ob + 4.0 * 4));
   if (w0) {
-    const size_t lds = sizeof(float) * 7 * (4 * (size_t)half_len(half_len(f)) + 4);
+    const size_t lds = sizeof(float) * 11 * (4 * (size_t)half_len(half_len(f)) + 4);
     if (lds > 64 * 1024) return wh_fail(ctx, WH_EARG, "depthwise: %d mel bins is more than one workgroup's patch holds", f);
-    const dim3 grid(1, rows);
+    const dim3 grid(1, (rows + 1) / 2);
     const int nt = threads < 64 ? 64 : threads;
-    if (out16) wh_launch(ctx, first_depthwise_kernel<_Float16>, grid, nt, lds, x, w, b, (_Float16 *)y, w0, b0, t, f, ch, t0);
-    else wh_launch(ctx, first_depthwise_kernel<float>, grid, nt, lds, x, w, b, (float *)y, w0, b0, t, f, ch, t0);
+    if (out16)
+      wh_launch(ctx, first_depthwise_kernel<_Float16>, grid, nt, lds, x, w, b, (_Float16 *)y, w0, b0, t, f, ch, t0, rows);
+    else wh_launch(ctx, first_depthwise_kernel<float>, grid, nt, lds, x, w, b, (float *)y, w0, b0, t, f, ch, t0, rows);
   } else if (ch % 4 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)b % 16 == 0 &&
              (uintptr_t)y % (out16 ? 8 : 16) == 0) {
     const long items = (long)rows * ((half_len(f) + DW_COLS - 1) / DW_COLS) * (ch / 4);

@@ -956,7 +956,7 @@ bool packed_attention(const wh_model *m, int batch, const int *valid_dev) {
 }
 
 int record_block(wh_model *m, int layer, const Block &k, float *x, float *y, int t, int batch, const int *valid_dev,
-                 bool pre, const Chan *next) {
+                 bool pre, const Chan *next, bool out16) {
   wh_ctx *c = m->ctx;
   const int d = m->d, hd = d / m->heads, rows = t * batch;
   void *y16 = y, *h16 = m->h;
@@ -1002,8 +1002,9 @@ int record_block(wh_model *m, int layer, const Block &k, float *x, float *y, int
                      valid_dev, t, batch, 1));
   CK(launch_gemm_h_ln(c, y16, k.pw2, x, rows, 1.0f, k.norm_ff2.w, k.norm_ff2.b, y16, 1));
   CK(g16(y16, k.ff2[0], h16, rows, WH_SILU, 0.0f, 1));
-  // The block output is norm_out(x), not the residual stream (x is not stored again).
-  return launch_gemm_h_ln(c, h16, k.ff2[1], x, rows, 0.5f, k.norm_out.w, k.norm_out.b, y, 0, 0,
+  // The block output is norm_out(x), not the residual stream (x is not stored again); f16 (out16) when
+  // its only reader is the GEMM after the last block.
+  return launch_gemm_h_ln(c, h16, k.ff2[1], x, rows, 0.5f, k.norm_out.w, k.norm_out.b, y, out16 ? 1 : 0, 0,
                           next ? next->w : nullptr, next ? next->b : nullptr, next ? m->yr : nullptr);
 }
 
@@ -1028,8 +1029,9 @@ int position_projection(wh_model *m, int t, int which, bool whole, F &&gemm) {
   return launch_set_int(m->ctx, m->pos_tag + which, t);
 }
 
-// Conformer::record (src/conformer.rs:107-116): `layers` blocks from m->x, output in m->x.
-int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layers) {
+// Conformer::record (src/conformer.rs:107-116): `layers` blocks from m->x, output in m->x — f32, or
+// with out16 f16 (the f32 values rounded, RNE, as the GEMM reading them would round them).
+int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layers, bool out16 = false) {
   if (m->relative && layers > 0) {  // every block's linear_pos(P) in one GEMM: [2t + 15][layers · d] f16
     if (packed_attention(m, batch, valid_dev)) {
       // One window: written as attention's packed position rows, [layer · head][prows][hd] from row
@@ -1050,7 +1052,7 @@ int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layer
   }
   for (int i = 0; i < layers; i++) {
     const Chan *next = i + 1 < layers ? &m->blocks[i + 1].norm_ff1 : nullptr;
-    CK(record_block(m, i, m->blocks[i], m->x, m->y, t, batch, valid_dev, i > 0, next));
+    CK(record_block(m, i, m->blocks[i], m->x, m->y, t, batch, valid_dev, i > 0, next, out16 && !next));
     std::swap(m->x, m->y);
   }
   return WH_OK;
@@ -1105,8 +1107,8 @@ int parakeet_record(wh_model *m, const float *mel, int batch, int mel_frames, co
   CK(lin_h(m, h16, m->conv6, qk16, t * f * batch, WH_RELU, 1));
   CK(launch_flatten(c, qk16, h16, t * batch, f, ch, 1));
   CK(lin_h(m, h16, m->pre_out, m->x, t * batch, WH_BIAS, 0));
-  CK(record_blocks(m, t, batch, batch > 1 ? m->valid_dev : nullptr, m->layers));
-  return lin(m, m->x, m->joint_enc, out, t * batch, WH_BIAS);
+  CK(record_blocks(m, t, batch, batch > 1 ? m->valid_dev : nullptr, m->layers, true));
+  return lin_h(m, (const _Float16 *)m->x, m->joint_enc, out, t * batch, WH_BIAS, 0);
 }
 
 // Runs `record` (a function queuing kernels only) for the call identified by `key`: eagerly the first
@@ -1202,8 +1204,8 @@ int gigaam_encode(wh_model *m, const float *mel, int mel_frames, float *out) {
     CK(lin(m, m->h, m->conv0, m->qk, t1, WH_RELU));
     CK(launch_im2col(c, m->qk, m->h, t1, d, 5, 2, 2, 1, 0, 0));
     CK(lin(m, m->h, m->conv2, m->x, t, WH_RELU));
-    CK(record_blocks(m, t, 1, nullptr, m->layers));
-    return lin(m, m->x, m->head, out, t, WH_BIAS);
+    CK(record_blocks(m, t, 1, nullptr, m->layers, true));
+    return lin_h(m, (const _Float16 *)m->x, m->head, out, t, WH_BIAS, 0);
   });
 }
 

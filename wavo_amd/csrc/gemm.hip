@@ -351,8 +351,10 @@ int launch_gemm_h_heads(wh_ctx *ctx, const void *a16, const wh_linear *l, void *
 }
 
 int launch_gemm_h_ln(wh_ctx *ctx, const void *a16, const wh_linear *l, float *x, int m, float alpha, const float *g,
-                     const float *b, void *y, int out16, int keep_x, const float *g2, const float *b2, void *y2) {
-  if (int rc = check(ctx, a16, l, x, m, WH_RESIDUAL)) return rc;
+                     const float *b, void *y, int out16, int keep_x, const float *g2, const float *b2, void *y2,
+                     int residual) {
+  const int epi = residual ? WH_RESIDUAL : WH_BIAS;
+  if (int rc = check(ctx, a16, l, x, m, epi)) return rc;
   if (m == 0) return WH_OK;
   if (g2 && (out16 || !b2 || !y2)) return wh_fail(ctx, WH_EARG, "gemm_h_ln: the second norm takes an f32 y");
   const int cols = l->cols;
@@ -362,14 +364,14 @@ int launch_gemm_h_ln(wh_ctx *ctx, const void *a16, const wh_linear *l, float *x,
     if ((rc = launch_layer_norm(ctx, x, g, b, y, m, cols, nullptr, nullptr, 0, out16))) return rc;
     return g2 ? launch_layer_norm(ctx, (const float *)y, g2, b2, y2, m, cols, nullptr, nullptr, 0, 1) : WH_OK;
   };
-  if (l->dual || !lds_path(l, x, cols)) return unfused(launch_gemm_h(ctx, a16, l, x, m, cols, WH_RESIDUAL, alpha, 0));
+  if (l->dual || !lds_path(l, x, cols)) return unfused(launch_gemm_h(ctx, a16, l, x, m, cols, epi, alpha, 0));
   const size_t pb = split_bytes(ctx, l, m);
   float *part = nullptr;
   if (pb && !(part = (float *)wh_scratch(ctx, pb))) return WH_EOOM;
   int splits = 1;
-  if (int rc = launch_lds(ctx, (const _Float16 *)a16, l, x, m, cols, WH_RESIDUAL, alpha, false, part, &splits)) return rc;
+  if (int rc = launch_lds(ctx, (const _Float16 *)a16, l, x, m, cols, epi, alpha, false, part, &splits)) return rc;
   if (splits > 1)
-    return launch_split_residual_ln(ctx, part, splits, l->bias, l->rows, alpha, x, g, b, y, m, cols, out16, keep_x, g2,
-                                    b2, y2);
+    return launch_split_residual_ln(ctx, part, splits, l->bias, l->rows, residual ? alpha : 1.0f, x, g, b, y, m, cols,
+                                    out16, keep_x, g2, b2, y2, residual);
   return unfused(WH_OK);
 }

@@ -186,7 +186,8 @@ int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int
 // and the norm run as one kernel (launch_split_residual_ln); otherwise the GEMM's own epilogue adds
 // the residual and the norm follows.  Needs l->cols == cols of x and no dual outputs.  keep_x = 0:
 // x is not needed afterwards (the fused kernel need not store it).  g2: a second LayerNorm of y (f32)
-// into y2 (f16) — the next block's first norm.
+// into y2 (f16) — the next block's first norm.  residual = 0: x = l(a16) + bias (the bias epilogue; x
+// is not read), then the norm.
 // A GEMM whose columns col0 .. col0 + cols − 1, heads of hd, go to dst in attention's packed layout
 // instead of into c: rows per head (tr false: [head][rs][hd], this call's rows from row r0, rows m ..
 // rs − r0 − 1 as zeros where tiles reach them) or transposed (tr: [head][hd][rs], r0 = 0, zeros for
@@ -200,10 +201,11 @@ int launch_gemm_h_heads(wh_ctx *ctx, const void *a16, const wh_linear *l, void *
                         const HeadsOut *outs, int n);
 int launch_gemm_h_ln(wh_ctx *ctx, const void *a16, const wh_linear *l, float *x, int m, float alpha, const float *g,
                      const float *b, void *y, int out16, int keep_x = 1, const float *g2 = nullptr,
-                     const float *b2 = nullptr, void *y2 = nullptr);
+                     const float *b2 = nullptr, void *y2 = nullptr, int residual = 1);
 int launch_split_residual_ln(wh_ctx *ctx, const float *part, int splits, const float *bias, int wrows, float alpha,
                              float *x, const float *g, const float *b, void *y, int rows, int cols, int out16,
-                             int keep_x = 1, const float *g2 = nullptr, const float *b2 = nullptr, void *y2 = nullptr);
+                             int keep_x = 1, const float *g2 = nullptr, const float *b2 = nullptr, void *y2 = nullptr,
+                             int residual = 1);
 // f32 → f16 (RNE) of n values (n % 4 == 0).
 int launch_to_half(wh_ctx *ctx, const float *x, void *y, size_t n);
 // A decoder cache column written by a GEMV as well: outputs lo .. lo + 2d (a K row then a V row of d

@@ -1030,8 +1030,10 @@ int position_projection(wh_model *m, int t, int which, bool whole, F &&gemm) {
 }
 
 // Conformer::record (src/conformer.rs:107-116): `layers` blocks from m->x, output in m->x — f32, or
-// with out16 f16 (the f32 values rounded, RNE, as the GEMM reading them would round them).
-int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layers, bool out16 = false) {
+// with out16 f16 (the f32 values rounded, RNE, as the GEMM reading them would round them).  pre: the
+// first block's norm_ff1 of m->x is already in m->yr (f16).
+int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layers, bool out16 = false,
+                  bool pre = false) {
   if (m->relative && layers > 0) {  // every block's linear_pos(P) in one GEMM: [2t + 15][layers · d] f16
     if (packed_attention(m, batch, valid_dev)) {
       // One window: written as attention's packed position rows, [layer · head][prows][hd] from row
@@ -1052,7 +1054,7 @@ int record_blocks(wh_model *m, int t, int batch, const int *valid_dev, int layer
   }
   for (int i = 0; i < layers; i++) {
     const Chan *next = i + 1 < layers ? &m->blocks[i + 1].norm_ff1 : nullptr;
-    CK(record_block(m, i, m->blocks[i], m->x, m->y, t, batch, valid_dev, i > 0, next, out16 && !next));
+    CK(record_block(m, i, m->blocks[i], m->x, m->y, t, batch, valid_dev, i > 0 || pre, next, out16 && !next));
     std::swap(m->x, m->y);
   }
   return WH_OK;
@@ -1106,8 +1108,15 @@ int parakeet_record(wh_model *m, const float *mel, int batch, int mel_frames, co
   }
   CK(lin_h(m, h16, m->conv6, qk16, t * f * batch, WH_RELU, 1));
   CK(launch_flatten(c, qk16, h16, t * batch, f, ch, 1));
-  CK(lin_h(m, h16, m->pre_out, m->x, t * batch, WH_BIAS, 0));
-  CK(record_blocks(m, t, batch, batch > 1 ? m->valid_dev : nullptr, m->layers, true));
+  // The projection's output (the residual stream) and the first block's norm_ff1 of it (f16, into yr):
+  // one kernel after a k-split GEMM.
+  if (m->layers > 0) {
+    const Chan &n1 = m->blocks[0].norm_ff1;
+    CK(launch_gemm_h_ln(c, h16, m->pre_out, m->x, t * batch, 1.0f, n1.w, n1.b, m->yr, 1, 1, nullptr, nullptr, nullptr, 0));
+  } else {
+    CK(lin_h(m, h16, m->pre_out, m->x, t * batch, WH_BIAS, 0));
+  }
+  CK(record_blocks(m, t, batch, batch > 1 ? m->valid_dev : nullptr, m->layers, true, m->layers > 0));
   return lin_h(m, (const _Float16 *)m->x, m->joint_enc, out, t * batch, WH_BIAS, 0);
 }
 

@@ -553,7 +553,8 @@ __global__ __launch_bounds__(256) void copy16_kernel(u32x4 *__restrict__ y, cons
 // The finish of a k-split GEMM with the residual epilogue, fused with the LayerNorm of its result:
 // x[row] += alpha·(Σ_z part[z][row] + bias) (the partial sums added in split order from 0, the W
 // padding columns ≥ wrows contributing epi(0 + bias) as the GEMM gives them), then y = LN(x[row])
-// with the arithmetic of layer_norm_kernel.  One wavefront per row; NJ as in layer_norm_kernel, and
+// with the arithmetic of layer_norm_kernel.  res = 0: the bias epilogue instead, x[row] = Σ + bias
+// (alpha 1, x not read).  One wavefront per row; NJ as in layer_norm_kernel, and
 // every load (partial sums, bias, x, the norms' weights) issued before the first use.
 template <typename OT, int NSPLIT, int NJ>
 __global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__restrict__ part, int splits,
@@ -563,7 +564,7 @@ __global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__r
                                                                 int rows, int cols, int keep_x,
                                                                 const float *__restrict__ g2,
                                                                 const float *__restrict__ b2,
-                                                                _Float16 *__restrict__ y2) {
+                                                                _Float16 *__restrict__ y2, int res) {
   constexpr int J = NJ ? NJ : ROW_REGS / 4;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int row = blockIdx.x * 4 + w;
@@ -585,7 +586,7 @@ __global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__r
 #pragma unroll
       for (int z = 0; z < NSPLIT; z++) p[z][j] = in(j) ? pr[z * (plane / 4) + i] : z4;
       bi[j] = in(j) ? b4[i] : z4;
-      c[j] = in(j) ? xr[i] : z4;
+      c[j] = res && in(j) ? xr[i] : z4;
     }
 #pragma unroll
     for (int j = 0; j < J; j++) {
@@ -621,7 +622,7 @@ __global__ __launch_bounds__(256) void split_residual_ln_kernel(const float *__r
         if (4 * i + 1 >= wrows) acc.y = 0.0f;
         if (4 * i + 2 >= wrows) acc.z = 0.0f;
         if (4 * i + 3 >= wrows) acc.w = 0.0f;
-        const float4 bi = b4[i], c = xr[i];
+        const float4 bi = b4[i], c = res ? xr[i] : z4;
         v[j] = make_float4(c.x + alpha * (acc.x + bi.x), c.y + alpha * (acc.y + bi.y), c.z + alpha * (acc.z + bi.z),
                            c.w + alpha * (acc.w + bi.w));
       }
@@ -739,25 +740,26 @@ int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *
 
 int launch_split_residual_ln(wh_ctx *ctx, const float *part, int splits, const float *bias, int wrows, float alpha,
                              float *x, const float *g, const float *b, void *y, int rows, int cols, int out16,
-                             int keep_x, const float *g2, const float *b2, void *y2) {
+                             int keep_x, const float *g2, const float *b2, void *y2, int residual) {
   if (rows <= 0 || cols <= 0 || cols % 4 || cols > ROW_REGS * 64 || splits < 1 || !part || !bias || !x || !g || !b || !y ||
       (uintptr_t)part % 16 || (uintptr_t)bias % 16 || (uintptr_t)x % 16 || (uintptr_t)g % 16 || (uintptr_t)b % 16 ||
       (uintptr_t)y % 16 || (g2 && (!b2 || !y2 || (uintptr_t)g2 % 16 || (uintptr_t)b2 % 16 || (uintptr_t)y2 % 16)))
     return wh_fail(ctx, WH_EARG, "split_residual_ln: bad arguments (%d x %d, %d splits)", rows, cols, splits);
   ProfScope prof(ctx, "split_residual_ln", 0.0,
-                 (double)rows * cols * (4.0 * splits + (keep_x ? 8 : 4) + (out16 ? 2 : 4) + (g2 ? 2 : 0)));
+                 (double)rows * cols *
+                     (4.0 * splits + (residual ? 4 : 0) + (keep_x ? 4 : 0) + (out16 ? 2 : 4) + (g2 ? 2 : 0)));
   const int grid = (rows + 3) / 4;
 #define SRL(OT, N)                                                                                                   \
   do {                                                                                                               \
     if (cols == 1024 && N > 0)                                                                                       \
       wh_launch(ctx, split_residual_ln_kernel<OT, N, 4>, grid, 256, 0, part, splits, bias, wrows, alpha, x, g, b,      \
-                (OT *)y, rows, cols, keep_x, g2, b2, (_Float16 *)y2);                                                \
+                (OT *)y, rows, cols, keep_x, g2, b2, (_Float16 *)y2, residual);                                 \
     else if (cols == 1280 && N > 0)                                                                                  \
       wh_launch(ctx, split_residual_ln_kernel<OT, N, 5>, grid, 256, 0, part, splits, bias, wrows, alpha, x, g, b,      \
-                (OT *)y, rows, cols, keep_x, g2, b2, (_Float16 *)y2);                                                \
+                (OT *)y, rows, cols, keep_x, g2, b2, (_Float16 *)y2, residual);                                 \
     else                                                                                                             \
       wh_launch(ctx, split_residual_ln_kernel<OT, N, 0>, grid, 256, 0, part, splits, bias, wrows, alpha, x, g, b,      \
-                (OT *)y, rows, cols, keep_x, g2, b2, (_Float16 *)y2);                                                \
+                (OT *)y, rows, cols, keep_x, g2, b2, (_Float16 *)y2, residual);                                 \
   } while (0)
   if (out16) {
     if (splits == 2) SRL(_Float16, 2);

@@ -88,8 +88,10 @@ def test_parakeet_small(gpu, wtype):
 @pytest.mark.parametrize("small,seconds", [(True, 3.0), (False, 60.0), (False, 7.3)])
 def test_parakeet_attention_reads_in_place(gpu, small, seconds):
     """One window's attention reads K and the position rows where the projections wrote them, and Vᵀ
-    from the qkv projection's epilogue (no packing launch).  The operands are the same f16 values as
-    after packing, so the encoder output equals the packed path's (wh_tune attn_pack) bit for bit.
+    from the qkv projection's epilogue (no packing launch); at full size (256 channels) the
+    subsampling's last conv writes its image flattened (no flatten launch).  The values are the same
+    f16 values as after the separate launches, so the encoder output equals that path's (wh_tune
+    attn_pack) bit for bit.
     Each setting runs eagerly, then recorded, then replayed (a tuning change is not replayed from a
     recording made before it)."""
     m = wa.Model(gpu, synth.model_path("parakeet", small=small, directory=MODELS))

@@ -449,7 +449,10 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
 #pragma unroll
           for (int q = 0; q < 8; q++)
             y[q] = (_Float16)(row0 + q < m ? epilogue(P.epi, 0.0f, cl[(r0 + q) * crow + c] + b, nullptr) : 0.0f);
-          *(half8 *)(h.dst + (size_t)(col - h.col0) * h.rs + row0) = y;  // head j, dim i: row j·hd + i
+          // head j, dim i: row j·hd + i; blocked: 8 rows of one block (row0 % 8 == 0, blk % 8 == 0)
+          const size_t at = h.blk ? (size_t)(row0 / h.blk) * h.cols * h.blk + (size_t)(col - h.col0) * h.blk + row0 % h.blk
+                                  : (size_t)(col - h.col0) * h.rs + row0;
+          *(half8 *)(h.dst + at) = y;
         }
       } else {
 #pragma unroll
@@ -1060,7 +1063,8 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     const HeadsOut &h = ho[i];
     // Whole tiles, inside the real columns, no dual columns; 16-byte stores.
     if (!out16 || h.col0 % p.bn || h.cols % p.bn || h.col0 + h.cols > l->rows || h.col0 < l->dual || h.hd % 8 ||
-        h.cols % h.hd || (uintptr_t)h.dst % 16 || h.r0 < 0 || (h.tr ? h.r0 || h.rs % 8 || h.rs < m : h.rs < h.r0 + m))
+        h.cols % h.hd || (uintptr_t)h.dst % 16 || h.r0 < 0 || (h.tr ? h.r0 || h.rs % 8 || h.rs < m : h.rs < h.r0 + m) ||
+        h.blk < 0 || (h.blk && (!h.tr || h.blk % 8 || h.hd != h.cols)))
       return wh_fail(ctx, WH_EARG, "gemm: packed output %d off the %d-column tiles or its layout", i, p.bn);
     args.ho[i] = h;
   }

@@ -66,7 +66,9 @@ struct wh_ctx {
   // recorded before a tuning change is not replayed after it.
   long tune_epoch = 0;
   // wh_tune("attn_pack", "1") (checks only): the encoder's attention packs K, Vᵀ and the position rows
-  // in a launch of its own, as for padded batches, instead of reading them where they were written.
+  // in a launch of its own, as for padded batches, instead of reading them where they were written;
+  // and the Parakeet subsampling flattens its image in a launch of its own instead of in the last
+  // conv's GEMM epilogue.
   int attn_pack = 0;
   std::string name;
   std::string error;
@@ -191,11 +193,14 @@ int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int
 // A GEMM whose columns col0 .. col0 + cols − 1, heads of hd, go to dst in attention's packed layout
 // instead of into c: rows per head (tr false: [head][rs][hd], this call's rows from row r0, rows m ..
 // rs − r0 − 1 as zeros where tiles reach them) or transposed (tr: [head][hd][rs], r0 = 0, zeros for
-// rows m .. rs − 1).
+// rows m .. rs − 1).  Transposed with blk > 0 (one head, hd = cols, blk % 8 == 0): rows in blocks of
+// blk, [row / blk][col − col0][row % blk] — a [t][f][ch] image flattened to [t][ch·f] rows (blk = f) —
+// rows from rs on not written.
 struct HeadsOut {
   _Float16 *dst;
   int col0, cols, hd, rs, r0;
   bool tr;
+  int blk;
 };
 int launch_gemm_h_heads(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int ldc, int epi,
                         const HeadsOut *outs, int n);

@@ -1106,15 +1106,25 @@ int parakeet_record(wh_model *m, const float *mel, int batch, int mel_frames, co
     CK(launch_depthwise(c, m->sub2 + per * b, nullptr, nullptr, m->sc5.w, m->sc5.b, h16 + (size_t)b * t * f * ch,
                         img, f2, ch, 0, t, 1));
   }
-  CK(lin_h(m, h16, m->conv6, qk16, t * f * batch, WH_RELU, 1));
-  CK(launch_flatten(c, qk16, h16, t * batch, f, ch, 1));
+  // conv6, then its [t][f][ch] image flattened to [t][ch·f] rows: by the GEMM's epilogue (rows in
+  // blocks of f, into qk) when every tile plan's width divides ch, else by a launch of its own (into h).
+  const _Float16 *flat = h16;
+  if (ch % 256 == 0 && f % 8 == 0 && !c->attn_pack) {
+    const int rows = t * f * batch;
+    const HeadsOut out{qk16, 0, ch, ch, rows, 0, true, f};
+    CK(launch_gemm_h_heads(c, h16, m->conv6, qk16, rows, m->conv6->cols, WH_RELU, &out, 1));
+    flat = qk16;
+  } else {
+    CK(lin_h(m, h16, m->conv6, qk16, t * f * batch, WH_RELU, 1));
+    CK(launch_flatten(c, qk16, h16, t * batch, f, ch, 1));
+  }
   // The projection's output (the residual stream) and the first block's norm_ff1 of it (f16, into yr):
   // one kernel after a k-split GEMM.
   if (m->layers > 0) {
     const Chan &n1 = m->blocks[0].norm_ff1;
-    CK(launch_gemm_h_ln(c, h16, m->pre_out, m->x, t * batch, 1.0f, n1.w, n1.b, m->yr, 1, 1, nullptr, nullptr, nullptr, 0));
+    CK(launch_gemm_h_ln(c, flat, m->pre_out, m->x, t * batch, 1.0f, n1.w, n1.b, m->yr, 1, 1, nullptr, nullptr, nullptr, 0));
   } else {
-    CK(lin_h(m, h16, m->pre_out, m->x, t * batch, WH_BIAS, 0));
+    CK(lin_h(m, flat, m->pre_out, m->x, t * batch, WH_BIAS, 0));
   }
   CK(record_blocks(m, t, batch, batch > 1 ? m->valid_dev : nullptr, m->layers, true, m->layers > 0));
   return lin_h(m, (const _Float16 *)m->x, m->joint_enc, out, t * batch, WH_BIAS, 0);

@@ -104,9 +104,10 @@ void *wh_stream(wh_ctx *ctx);
  *                      probability (to check them); "0" restores;
  *   "attend_merge"     "1": wh_attend merges its 256-key parts in the launch's last workgroup (the
  *                      path of a decoder step's self-attention) instead of a second kernel; "0" restores;
- *   "attn_pack"        "1": a model's encoder attention packs K, Vᵀ and the position rows in a launch
- *                      of its own (the padded-batch path) for one window too, and the Parakeet
- *                      subsampling flattens its image in a launch of its own (checks); "0" restores.
+ *   "epilogue_fusion"  "0": the encoders run in launches of their own what GEMM epilogues do otherwise
+ *                      (attention's packed K, Vᵀ and position rows for one window, as the padded-batch
+ *                      path does; the Parakeet subsampling's flatten; the conv module's GLU), the check
+ *                      of those epilogues; "1" restores.
  * Unknown keys and malformed values return WH_EARG. */
 int wh_tune(wh_ctx *ctx, const char *key, const char *value);
 /* Profiling (no counterpart in the reference, whose timing lives in `wavo bench` and GPU timestamp

@@ -89,21 +89,20 @@ def test_parakeet_small(gpu, wtype):
 def test_parakeet_attention_reads_in_place(gpu, small, seconds):
     """One window's attention reads K and the position rows where the projections wrote them, and Vᵀ
     from the qkv projection's epilogue (no packing launch); at full size (256 channels) the
-    subsampling's last conv writes its image flattened (no flatten launch).  The values are the same
-    f16 values as after the separate launches, so the encoder output equals that path's (wh_tune
-    attn_pack) bit for bit.
+    subsampling's last conv writes its image flattened (no flatten launch), and the conv module's first
+    pointwise conv applies the GLU in its epilogue.  The values are the same as after the separate
+    launches, so the encoder output equals that path's (wh_tune epilogue_fusion 0) bit for bit.
     Each setting runs eagerly, then recorded, then replayed (a tuning change is not replayed from a
     recording made before it)."""
     m = wa.Model(gpu, synth.model_path("parakeet", small=small, directory=MODELS))
     mel = synth.parakeet_mel(synth.audio(seconds, seed=9))
     direct = m.encode(mel)
     outs = {}
-    for key in ("attn_pack",):
-        gpu.tune(key, 1)
-        try:
-            outs[key] = [m.encode(mel) for _ in range(3)]
-        finally:
-            gpu.tune(key, 0)
+    gpu.tune("epilogue_fusion", 0)
+    try:
+        outs["separate launches"] = [m.encode(mel) for _ in range(3)]
+    finally:
+        gpu.tune("epilogue_fusion", 1)
     outs["default"] = [m.encode(mel) for _ in range(3)]
     for key, runs in outs.items():
         for got in runs:

@@ -325,7 +325,7 @@ class Gpu:
     def tune(self, key, value):
         """Tuning and measurement overrides (wh_tune): gemm_plan, gemm_shape_plans, gemm_kernel_only,
         gemm_group, attn_split, position_cache, and the check switches mel_raw, whisper_host, whisper_logprobs, attend_merge,
-        attn_pack."""
+        epilogue_fusion."""
         self._check(lib().wh_tune(self.h, key.encode(), str(value).encode()))
 
     def profile(self, mode):

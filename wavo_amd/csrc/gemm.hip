@@ -124,6 +124,7 @@ bool lds_path(const wh_linear *l, const void *c, int ldc) {
          ldc % 8 == 0 && (uintptr_t)c % 16 == 0;
 }
 
+
 // Scratch bytes for the split-k partial sums of an m-row GEMM (0 when it does not split).
 size_t split_bytes(const wh_ctx *ctx, const wh_linear *l, int m) {
   const GemmPlan p = gemm_plan_for(ctx, m, l->cols, l->k);
@@ -187,9 +188,16 @@ int launch_typed(wh_ctx *ctx, const void *a, const wh_linear *l, void *c, int m,
 
 }  // namespace
 
-static int check(wh_ctx *ctx, const void *a, const wh_linear *l, const void *c, int m, int epi) {
+bool gemm_glu_ok(const wh_linear *l, const void *c) {
+  return l && !l->dual && l->rows == l->cols && l->cols % 16 == 0 && lds_path(l, c, l->cols / 2);
+}
+
+// glu: the caller takes EPI_GLU (launch_gemm_h only; the public entry points take WH_BIAS .. WH_TANH).
+static int check(wh_ctx *ctx, const void *a, const wh_linear *l, const void *c, int m, int epi, bool glu = false) {
   if (m < 0 || !l || (m && (!a || !c))) return wh_fail(ctx, WH_EARG, "gemm: bad arguments (m %d)", m);
-  if (epi < WH_BIAS || epi > WH_TANH) return wh_fail(ctx, WH_EARG, "gemm: epilogue %d", epi);
+  if ((epi < WH_BIAS || epi > WH_TANH) && !(glu && epi == EPI_GLU))
+    return wh_fail(ctx, WH_EARG, "gemm: epilogue %d", epi);
+  if (epi == EPI_GLU && !gemm_glu_ok(l, c)) return wh_fail(ctx, WH_EARG, "gemm: GLU epilogue off its layout");
   if ((uintptr_t)a % 16) return wh_fail(ctx, WH_EARG, "gemm: a must be 16-byte aligned");
   return WH_OK;
 }
@@ -325,10 +333,14 @@ int launch_to_half(wh_ctx *ctx, const float *x, void *y, size_t n) {
 
 int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int ldc, int epi, float alpha,
                   int out16) {
-  if (int rc = check(ctx, a16, l, c, m, epi)) return rc;
+  if (int rc = check(ctx, a16, l, c, m, epi, true)) return rc;
   if (out16 && (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL))
     return wh_fail(ctx, WH_EARG, "gemm: residual epilogues accumulate into f32 outputs");
+  if (epi == EPI_GLU && (out16 || ldc != l->cols / 2))
+    return wh_fail(ctx, WH_EARG, "gemm: the GLU epilogue writes f32 rows of cols / 2");
   if (m == 0) return WH_OK;
+  // (no split-k partials for the GLU epilogue: the main kernel finishes its own tiles)
+  if (epi == EPI_GLU) return launch_lds(ctx, (const _Float16 *)a16, l, c, m, ldc, epi, alpha, false, nullptr);
   if (lds_path(l, c, ldc)) {
     const size_t pb = split_bytes(ctx, l, m);
     float *part = nullptr;

@@ -488,6 +488,15 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
           if (row >= m) continue;
           const float4 x0 = *(const float4 *)(cl + r * crow + c8), x1 = *(const float4 *)(cl + r * crow + c8 + 4);
           const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+          if constexpr (E == EPI_GLU) {  // 4 channels from the group [a₀..a₃ | g₀..g₃] at col
+            float4 v;
+            v.x = (x[0] + bb[0]) * __builtin_amdgcn_rcpf(1.0f + __expf(-(x[4] + bb[4])));
+            v.y = (x[1] + bb[1]) * __builtin_amdgcn_rcpf(1.0f + __expf(-(x[5] + bb[5])));
+            v.z = (x[2] + bb[2]) * __builtin_amdgcn_rcpf(1.0f + __expf(-(x[6] + bb[6])));
+            v.w = (x[3] + bb[3]) * __builtin_amdgcn_rcpf(1.0f + __expf(-(x[7] + bb[7])));
+            *(float4 *)((float *)P.c + (size_t)row * P.ldc + col / 2) = v;
+            continue;
+          }
           const size_t at = (size_t)row * P.ldc + col;
           float y[8];
           if constexpr (!OUT16 && (E == WH_RESIDUAL || E == WH_GELU_RESIDUAL)) {
@@ -525,6 +534,9 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
         case WH_GELU_RESIDUAL:
           if constexpr (!OUT16) { run(std::integral_constant<int, WH_GELU_RESIDUAL>{}); return; }
           break;
+        case EPI_GLU:
+          if constexpr (!OUT16) { run(std::integral_constant<int, EPI_GLU>{}); return; }
+          break;
         default: run(std::integral_constant<int, WH_BIAS>{}); return;
       }
     }
@@ -544,6 +556,15 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
 #pragma unroll
     for (int q = 0; q < 8; q++)
       if (col + q >= rows) x[q] = 0.0f;
+    if (!OUT16 && P.epi == EPI_GLU) {  // as in the interior path (the host keeps whole groups of real columns)
+      float4 v;
+      v.x = (x[0] + bb[0]) * __builtin_amdgcn_rcpf(1.0f + __expf(-(x[4] + bb[4])));
+      v.y = (x[1] + bb[1]) * __builtin_amdgcn_rcpf(1.0f + __expf(-(x[5] + bb[5])));
+      v.z = (x[2] + bb[2]) * __builtin_amdgcn_rcpf(1.0f + __expf(-(x[6] + bb[6])));
+      v.w = (x[3] + bb[3]) * __builtin_amdgcn_rcpf(1.0f + __expf(-(x[7] + bb[7])));
+      *(float4 *)((float *)P.c + (size_t)row * P.ldc + col / 2) = v;
+      continue;
+    }
     const size_t at = (size_t)row * P.ldc + col;
     float y[8];
     if (!OUT16 && (P.epi == WH_RESIDUAL || P.epi == WH_GELU_RESIDUAL)) {
@@ -1083,7 +1104,7 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
   if (p.wk > 1) snprintf(sp + strlen(sp), sizeof sp - strlen(sp), "_k%d", p.wk);
   snprintf(name, sizeof name, "gemm_%s_%dx%d_w%dx%d_n%d%s %dx%dx%d e%d %s w%d%s", tn, p.bm, p.bn, p.wm, p.wn, p.ns, sp,
            m, l->rows, l->k, epi, out16 ? "f16" : "f32", l->cols + l->dual, args.skip ? " (tagged)" : "");
-  const double width = l->cols + l->dual;
+  const double width = epi == EPI_GLU ? l->cols / 2 : l->cols + l->dual;
   const double bytes = (double)l->rows * l->row_bytes + 2.0 * m * l->k +
                        (out16 ? 2.0 : 4.0) * m * width * (epi == WH_RESIDUAL || epi == WH_GELU_RESIDUAL ? 2 : 1);
   {

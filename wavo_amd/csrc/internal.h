@@ -23,6 +23,12 @@ struct wh_prof_rec {
 };
 
 constexpr int ATTEND_HEADS = 1024;  // heads of one attend launch, at most
+// An internal GEMM epilogue (beside WH_BIAS .. WH_TANH): the GLU of the Conformer conv module over a
+// weight whose output columns come in groups of 8, [a₀..a₃ | g₀..g₃] (4 channels, rows permuted at
+// load): output row r, column col/2 + q = (x_q + b_q)·σ(x_{q+4} + b_{q+4}) for the group at col, σ as
+// 1/(1 + e^−x) by the hardware reciprocal (conv_glu_kernel's arithmetic); c is cols/2 wide (ldc), f32,
+// and the GEMM does not split k.
+constexpr int EPI_GLU = 7;
 
 struct wh_ctx {
   int device = 0;
@@ -65,11 +71,10 @@ struct wh_ctx {
   // Bumped by every wh_tune call: the model's recorded calls carry it in their keys, so that a call
   // recorded before a tuning change is not replayed after it.
   long tune_epoch = 0;
-  // wh_tune("attn_pack", "1") (checks only): the encoder's attention packs K, Vᵀ and the position rows
-  // in a launch of its own, as for padded batches, instead of reading them where they were written;
-  // and the Parakeet subsampling flattens its image in a launch of its own instead of in the last
-  // conv's GEMM epilogue.
-  int attn_pack = 0;
+  // wh_tune("epilogue_fusion", "0") (checks only): the encoders run in launches of their own what
+  // GEMM epilogues do otherwise — attention's K, Vᵀ and position rows packed (as for padded batches),
+  // the Parakeet subsampling's image flattened, the conv module's GLU; "1" restores.
+  int unfused = 0;
   std::string name;
   std::string error;
   // Profiling (wh_profile): 0 off (default), 1 events around every launch, 2 named regions only.
@@ -181,6 +186,8 @@ int launch_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m
 // The same with `a` already rounded to f16 (its producer wrote f16): half the A traffic.  With
 // out16 the outputs are stored as f16 (for a consumer that rounds them to f16 anyway); residual
 // epilogues need f32 outputs.
+// Whether launch_gemm_h can run l with EPI_GLU into c (the main kernel, whole groups of 8 real columns).
+bool gemm_glu_ok(const wh_linear *l, const void *c);
 int launch_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int ldc, int epi,
                   float alpha, int out16);
 // x += alpha·(l(a16) + bias) followed by y = LayerNorm(x; g, b) (y f16 with out16): a GEMM with the
@@ -235,9 +242,11 @@ int launch_layer_norm(wh_ctx *ctx, const float *x, const float *g, const float *
                       int cols, const float *table, void *yr, int head_dim, int out16 = 0);
 int launch_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int kernel, int stride,
                   int pad, int batch, long x_batch_stride, long col_batch_stride);
+// layout of h: 0 [x | gates] per frame, 1 groups of 8 [x₀..x₃ | g₀..g₃] per 4 channels, 2 the GLU
+// already applied ([t][ch]; EPI_GLU).
 int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb, int kernel,
                     const float *g, const float *b, int layer_norm, void *y, int t, int ch,
-                    const int *valid_dev, int valid, int batch, int out16 = 0);
+                    const int *valid_dev, int valid, int batch, int out16 = 0, int layout = 0);
 // qk / v / pos are f32 (in16 == 0) or f16; o is f32 or f16 (out16).  pos rows are pos_stride
 // elements apart (0: heads · hd).
 // The packed attention operands' shape for one window of t keys (relative: with position rows).

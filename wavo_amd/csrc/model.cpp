@@ -355,6 +355,38 @@ class Loader {
     return l;
   }
 
+  // The conv module's first pointwise conv (2·ch output rows: the GLU's x rows, then its gates) with
+  // its rows permuted into groups of 8, [x 4j .. 4j+3 | gates 4j .. 4j+3] for j = 0 .. ch/4 − 1, so
+  // that a GEMM epilogue holds every channel's x and gate in one lane (EPI_GLU); *groups says whether
+  // it did (ch % 4 == 0), else the rows stay as stored.  Whole rows move: the products are unchanged.
+  wh_linear *glu_groups(const std::string &name, bool bias, bool *groups) {
+    *groups = false;
+    if (!err.empty()) return nullptr;
+    const Tensor *t = need(name + ".weight");
+    if (!t) return nullptr;
+    int k = (int)t->dims[0];
+    for (size_t d = 1; d + 1 < t->dims.size(); d++) k *= (int)t->dims[d];
+    const int rows = (int)t->dims.back(), ch = rows / 2;
+    if (rows % 8) return linear({name}, bias);
+    const size_t rb = wh_type_bytes(t->type, (size_t)k);
+    std::vector<uint8_t> host(rb * rows);
+    std::vector<float> b, bo = bias ? f32s(name + ".bias", rows) : std::vector<float>();
+    for (int r = 0; r < rows; r++) {
+      const int j = r / 8, q = r % 8, src = q < 4 ? 4 * j + q : ch + 4 * j + q - 4;
+      memcpy(host.data() + (size_t)r * rb, t->data + (size_t)src * rb, rb);
+      if (bias) b.push_back(bo[src]);
+    }
+    wh_tensor w{host.data(), t->type, k, rows};
+    wh_linear *l = nullptr;
+    if (linear_new(ctx_, &w, 1, b.empty() ? nullptr : b.data(), (int)b.size(), 0, &l, nullptr)) {
+      fail(name + ": " + ctx_->error);
+      return nullptr;
+    }
+    linears.push_back(l);
+    *groups = true;
+    return l;
+  }
+
   // One linear layer from weight tensors joined along k: row r is [names[0] row r | names[1] row r |
   // ...] (the LSTM's [Wx | Wh] over [x | h]).  Same type and rows; whole 32-weight blocks each.
   wh_linear *joined(const std::vector<std::string> &names, const std::vector<float> &bias) {
@@ -416,6 +448,7 @@ constexpr int WHISPER_MAX_NEW = 256, WHISPER_CONTEXT = 448;  // src/whisper/sear
 struct Block {
   Chan norm_ff1, norm_attn, norm_conv, norm_ff2, norm_out, conv_norm, dw;
   wh_linear *ff1[2] = {}, *ff2[2] = {}, *out = nullptr, *pw1 = nullptr, *pw2 = nullptr;
+  bool pw1_groups = false;  // pw1's output columns in GLU groups of 8 (Loader::glu_groups)
   wh_linear *qk = nullptr, *v = nullptr;     // rotary: q stacked over k, and v
   wh_linear *qkv = nullptr;  // relative: [q + u | k | v | q + v]
 };
@@ -604,7 +637,7 @@ void load_block(Loader &L, wh_model *m, int i, Block &k) {
   }
   k.out = L.linear({p + "attn.linear_out"}, bias);
   k.norm_conv = L.norm(p + "norm_conv", d, true);
-  k.pw1 = L.linear({p + "conv.pointwise1"}, bias);
+  k.pw1 = L.glu_groups(p + "conv.pointwise1", bias, &k.pw1_groups);
   if (m->layer_norm_conv) {
     k.conv_norm = L.norm(p + "conv.ln", d, true);
   } else {
@@ -952,7 +985,7 @@ int arena(wh_model *m, int frames, int batch) {
 // window (padded batches pack per call), head dims the packed layout holds unpadded.
 bool packed_attention(const wh_model *m, int batch, const int *valid_dev) {
   const int hd = m->d / m->heads;
-  return m->relative && m->ppk && batch == 1 && !valid_dev && (hd == 32 || hd == 64 || hd == 128) && !m->ctx->attn_pack;
+  return m->relative && m->ppk && batch == 1 && !valid_dev && (hd == 32 || hd == 64 || hd == 128) && !m->ctx->unfused;
 }
 
 int record_block(wh_model *m, int layer, const Block &k, float *x, float *y, int t, int batch, const int *valid_dev,
@@ -997,9 +1030,18 @@ int record_block(wh_model *m, int layer, const Block &k, float *x, float *y, int
   // The residual projections and the norm after them: one fused finish + LayerNorm kernel when the
   // GEMM's plan splits k, else the GEMM's residual epilogue and a LayerNorm launch.
   CK(launch_gemm_h_ln(c, y16, k.out, x, rows, 1.0f, k.norm_conv.w, k.norm_conv.b, y16, 1));
-  CK(g16(y16, k.pw1, m->qk, rows, WH_BIAS, 0.0f, 0));
+  // The conv module: pw1 and its GLU in one GEMM (its epilogue) when pw1's rows are in GLU groups,
+  // then the depthwise conv, norm and SiLU.
+  int glu = 0;  // the layout of pw1's output for launch_conv_glu
+  if (k.pw1_groups && !c->unfused && gemm_glu_ok(k.pw1, m->qk)) {
+    CK(launch_gemm_h(c, y16, k.pw1, m->qk, rows, k.pw1->cols / 2, EPI_GLU, 0.0f, 0));
+    glu = 2;
+  } else {
+    CK(g16(y16, k.pw1, m->qk, rows, WH_BIAS, 0.0f, 0));
+    glu = k.pw1_groups ? 1 : 0;
+  }
   CK(launch_conv_glu(c, m->qk, k.dw.w, k.dw.b, m->kernel, k.conv_norm.w, k.conv_norm.b, m->layer_norm_conv, y16, t, d,
-                     valid_dev, t, batch, 1));
+                     valid_dev, t, batch, 1, glu));
   CK(launch_gemm_h_ln(c, y16, k.pw2, x, rows, 1.0f, k.norm_ff2.w, k.norm_ff2.b, y16, 1));
   CK(g16(y16, k.ff2[0], h16, rows, WH_SILU, 0.0f, 1));
   // The block output is norm_out(x), not the residual stream (x is not stored again); f16 (out16) when
@@ -1109,7 +1151,7 @@ int parakeet_record(wh_model *m, const float *mel, int batch, int mel_frames, co
   // conv6, then its [t][f][ch] image flattened to [t][ch·f] rows: by the GEMM's epilogue (rows in
   // blocks of f, into qk) when every tile plan's width divides ch, else by a launch of its own (into h).
   const _Float16 *flat = h16;
-  if (ch % 256 == 0 && f % 8 == 0 && !c->attn_pack) {
+  if (ch % 256 == 0 && f % 8 == 0 && !c->unfused) {
     const int rows = t * f * batch;
     const HeadsOut out{qk16, 0, ch, ch, rows, 0, true, f};
     CK(launch_gemm_h_heads(c, h16, m->conv6, qk16, rows, m->conv6->cols, WH_RELU, &out, 1));

@@ -136,13 +136,17 @@ __global__ void im2col_kernel(const float *__restrict__ x, float *__restrict__ c
 
 // The Conformer conv module between the pointwise convs (ops.wgsl:121-164; src/cpu/ops.rs:137-182):
 // h [t][2ch] → GLU x·σ(gate) (zero from the window's valid frames on) → depthwise conv (odd kernel,
-// centred, w [ch][kernel]) + bias → LayerNorm or affine → SiLU.  A workgroup takes CF consecutive
+// centred, w [ch][kernel]) + bias → LayerNorm or affine → SiLU.  Layouts of h (GLU_*): x in columns
+// 0..ch−1 and the gates after them; interleaved in groups of 8, [x₀..x₃ | g₀..g₃] per 4 channels (the
+// pointwise conv's rows permuted at load); or the GLU already applied, [t][ch] (by that GEMM's
+// epilogue, with this kernel's arithmetic).  A workgroup takes CF consecutive
 // frames of one window with one thread per 4 channels: each thread slides over the CF + kernel − 1
 // frames its outputs need, keeping their GLU values and its 4·kernel taps in registers (the taps of
 // 4 channels are 4·kernel consecutive floats), so h is read once per workgroup plus the kernel − 1
 // frames of overlap.  The norm's row sums go through wavefront reductions and LDS.  Frames are
 // [batch][t]; the conv does not cross windows.  OT = float, or _Float16 for a consumer GEMM.
 constexpr int CF = 4;  // 4 frames per workgroup: a 750-frame window spreads over 188 CUs
+enum { GLU_PLAIN = 0, GLU_GROUPS = 1, GLU_DONE = 2 };
 constexpr int CG_MAXK = 31;
 
 template <typename OT, int K>
@@ -150,7 +154,7 @@ __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__
                                                        const float *__restrict__ wb, int kernel,
                                                        const float *__restrict__ g, const float *__restrict__ gb,
                                                        int layer_norm, OT *__restrict__ y, int t, int ch,
-                                                       const int *__restrict__ valid_dev, int valid) {
+                                                       const int *__restrict__ valid_dev, int valid, int layout) {
   constexpr int SPAN = CF + K - 1;
   __shared__ float red[2][4][CF];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
@@ -159,7 +163,10 @@ __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__
   const int pad = K / 2;
   const int c = 4 * tid;
   const bool on = c < ch;
-  const float *hs = h + (size_t)seg * t * 2 * ch;
+  // Floats per frame of h, and this thread's offsets of its x and gate quads in a frame.
+  const int fw = layout == GLU_DONE ? ch : 2 * ch;
+  const int ox = layout == GLU_GROUPS ? 2 * c : c, og = layout == GLU_GROUPS ? 2 * c + 4 : c + ch;
+  const float *hs = h + (size_t)seg * t * fw;
   float4 acc[CF];
   // The norm's weights, loaded with the inputs (they are used after the reductions).
   const float4 gg = on ? *(const float4 *)(g + c) : make_float4(0, 0, 0, 0);
@@ -181,22 +188,27 @@ __global__ __launch_bounds__(256) void conv_glu_kernel(const float *__restrict__
 #pragma unroll
     for (int r = 0; r < SPAN; r++) {
       const int src = f0 - pad + r;
-      const size_t at = (size_t)(src >= 0 && src < lim ? src : 0) * 2 * ch + (on ? c : 0);
-      xs[r] = *(const float4 *)(hs + at);
-      gs[r] = *(const float4 *)(hs + at + ch);
+      const size_t at = (size_t)(src >= 0 && src < lim ? src : 0) * fw;
+      xs[r] = *(const float4 *)(hs + at + (on ? ox : 0));
+      if (layout != GLU_DONE) gs[r] = *(const float4 *)(hs + at + (on ? og : 0));
     }
 #pragma unroll
     for (int r = 0; r < SPAN; r++) {
       const int src = f0 - pad + r;
       float4 v = make_float4(0, 0, 0, 0);
       if (on && src >= 0 && src < lim) {
-        const float4 x = xs[r], gt = gs[r];
-        // GLU: a·σ(b), σ by the hardware reciprocal (1 ulp) as a·(1 / (1 + e^−b)), the reference's two
-        // roundings, instead of an IEEE division (~10 instructions) on every input frame of the span.
-        v.x = x.x * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.x));
-        v.y = x.y * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.y));
-        v.z = x.z * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.z));
-        v.w = x.w * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.w));
+        const float4 x = xs[r];
+        if (layout == GLU_DONE) {
+          v = x;
+        } else {
+          // GLU: a·σ(b), σ by the hardware reciprocal (1 ulp) as a·(1 / (1 + e^−b)), the reference's
+          // two roundings, instead of an IEEE division (~10 instructions) on every input frame of the span.
+          const float4 gt = gs[r];
+          v.x = x.x * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.x));
+          v.y = x.y * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.y));
+          v.z = x.z * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.z));
+          v.w = x.w * __builtin_amdgcn_rcpf(1.0f + __expf(-gt.w));
+        }
       }
       // Output frame i takes tap k = r − i.
 #pragma unroll
@@ -788,11 +800,12 @@ int launch_im2col(wh_ctx *ctx, const float *x, float *col, int t, int ch, int ke
 
 template <typename OT>
 static void conv_glu_k(wh_ctx *ctx, dim3 grid, int threads, const float *h, const float *w, const float *wb, int kernel,
-                const float *g, const float *b, int layer_norm, OT *y, int t, int ch, const int *valid_dev, int valid) {
+                const float *g, const float *b, int layer_norm, OT *y, int t, int ch, const int *valid_dev, int valid,
+                int layout) {
 #define CG(K)                                                                                                      \
   case K:                                                                                                          \
     wh_launch(ctx, conv_glu_kernel<OT, K>, grid, threads, 0, h, w, wb, kernel, g, b, layer_norm, y, t, ch, valid_dev, \
-                                                              valid);                                              \
+              valid, layout);                                                                                      \
     break;
   switch (kernel) {
     CG(1) CG(3) CG(5) CG(7) CG(9) CG(11) CG(13) CG(15) CG(17) CG(19) CG(21) CG(23) CG(25) CG(27) CG(29) CG(31)
@@ -802,23 +815,24 @@ static void conv_glu_k(wh_ctx *ctx, dim3 grid, int threads, const float *h, cons
 
 int launch_conv_glu(wh_ctx *ctx, const float *h, const float *w, const float *wb, int kernel, const float *g,
                     const float *b, int layer_norm, void *y, int t, int ch, const int *valid_dev, int valid,
-                    int batch, int out16) {
-  if (t <= 0 || ch <= 0 || ch > 1024 || ch % 4 || kernel <= 0 || kernel % 2 == 0 || kernel > CG_MAXK || batch <= 0)
+                    int batch, int out16, int layout) {
+  if (t <= 0 || ch <= 0 || ch > 1024 || ch % 4 || kernel <= 0 || kernel % 2 == 0 || kernel > CG_MAXK || batch <= 0 ||
+      layout < GLU_PLAIN || layout > GLU_DONE)
     return wh_fail(ctx, WH_EARG, "conv_glu: bad shape (t %d, ch %d, kernel %d): ch %% 4 == 0, ch <= 1024, odd kernel <= %d",
                    t, ch, kernel, CG_MAXK);
   if ((uintptr_t)h % 16 || (uintptr_t)w % 16 || (uintptr_t)wb % 16 || (uintptr_t)g % 16 || (uintptr_t)b % 16 ||
       (uintptr_t)y % 16)
     return wh_fail(ctx, WH_EARG, "conv_glu: buffers must be 16-byte aligned");
   const int frames = t * batch;
-  ProfScope prof(ctx, "conv_glu", 0.0, (8.0 + (out16 ? 2.0 : 4.0)) * frames * ch);
+  ProfScope prof(ctx, "conv_glu", 0.0, ((layout == GLU_DONE ? 4.0 : 8.0) + (out16 ? 2.0 : 4.0)) * frames * ch);
   dim3 grid((t + CF - 1) / CF, batch);
   const int threads = (ch / 4 + 63) / 64 * 64;
   if (out16)
     conv_glu_k<_Float16>(ctx, grid, threads, h, w, wb, kernel, g, b, layer_norm, (_Float16 *)y, t, ch, valid_dev,
-                         valid < 0 ? t : valid);
+                         valid < 0 ? t : valid, layout);
   else
     conv_glu_k<float>(ctx, grid, threads, h, w, wb, kernel, g, b, layer_norm, (float *)y, t, ch, valid_dev,
-                      valid < 0 ? t : valid);
+                      valid < 0 ? t : valid, layout);
   return wh_launched(ctx, "conv_glu");
 }
 

@@ -407,8 +407,8 @@ int wh_tune(wh_ctx *ctx, const char *key, const char *value) {
     ctx->whisper_host = atoi(v) != 0;
   } else if (!strcmp(key, "whisper_logprobs")) {
     ctx->whisper_logprobs = atoi(v) != 0;
-  } else if (!strcmp(key, "attn_pack")) {
-    ctx->attn_pack = atoi(v) != 0;
+  } else if (!strcmp(key, "epilogue_fusion")) {
+    ctx->unfused = atoi(v) == 0;
   } else if (!strcmp(key, "attend_merge")) {
     ctx->attend_merge = atoi(v) != 0;
   } else {

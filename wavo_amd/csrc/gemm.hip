@@ -370,7 +370,8 @@ int launch_gemm_h_ln(wh_ctx *ctx, const void *a16, const wh_linear *l, float *x,
   if (m == 0) return WH_OK;
   if (g2 && (out16 || !b2 || !y2)) return wh_fail(ctx, WH_EARG, "gemm_h_ln: the second norm takes an f32 y");
   const int cols = l->cols;
-  // The GEMM adds the residual into x, then one or two LayerNorm launches.
+  // The GEMM adds the residual into x, then one or two LayerNorm launches (one pass for both norms,
+  // the fused finish kernel without partial sums, measured slower at 11616 rows: 51 against ~24 µs).
   auto unfused = [&](int rc) {
     if (rc) return rc;
     if ((rc = launch_layer_norm(ctx, x, g, b, y, m, cols, nullptr, nullptr, 0, out16))) return rc;

@@ -23,6 +23,7 @@ struct wh_prof_rec {
 };
 
 constexpr int ATTEND_HEADS = 1024;  // heads of one attend launch, at most
+constexpr int ROW_REGS = 32;  // row values per lane the row kernels hold in registers: rows up to 2048
 // An internal GEMM epilogue (beside WH_BIAS .. WH_TANH): the GLU of the Conformer conv module over a
 // weight whose output columns come in groups of 8, [a₀..a₃ | g₀..g₃] (4 channels, rows permuted at
 // load): output row r, column col/2 + q = (x_q + b_q)·σ(x_{q+4} + b_{q+4}) for the group at col, σ as

@@ -14,7 +14,6 @@ namespace {
 using xlane::wave_max;
 using xlane::wave_sum;
 
-constexpr int ROW_REGS = 32;  // row values per lane held in registers: rows up to 2048
 
 __device__ __forceinline__ void store4(float *p, float4 v) { *(float4 *)p = v; }
 // The f32 values rounded to f16 (RNE), as a GEMM rounds an f32 input: the empty asm keeps the compiler

@@ -421,10 +421,25 @@ __device__ __forceinline__ void static_for(F &&f) {
 // rows give); a split GEMM stores its plain partial sums into plane tz instead.  A pass holds, for
 // every row group of RPW tile rows (one per row of wavefronts), PGR of its rows from row 32·i0: LDS
 // row r is tile row (r / PGR)·RPW + 32·i0 + r % PGR (PGR = RPW, i0 = 0: the whole tile in order).
-template <int NR, int RPW, int PGR, int BN, int NT, bool SPLIT, bool OUT16>
+template <int NR, int RPW, int PGR, int BN, int NT, bool SPLIT, bool OUT16, bool TWO = false>
 __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, int crow, int tid, int m0, int n0,
-                                             int tz, int i0, const float (&bb)[8], const float (&bd)[8]) {
+                                             int tz, int i0, const float (&bb)[8], const float (&bd)[8],
+                                             const float *cl2 = nullptr) {
   constexpr int G8 = BN / 8;
+  // The tile's sums: with TWO the two k groups' planes added as they are read (group 0's + group 1's).
+  auto rd4 = [&](int off) {
+    float4 a = *(const float4 *)(cl + off);
+    if constexpr (TWO) {
+      const float4 b = *(const float4 *)(cl2 + off);
+      a.x += b.x, a.y += b.y, a.z += b.z, a.w += b.w;
+    }
+    return a;
+  };
+  auto rd1 = [&](int off) {
+    float a = cl[off];
+    if constexpr (TWO) a += cl2[off];
+    return a;
+  };
   const int m = P.m, rows = P.rows;
   static_assert((NR * G8) % NT == 0, "whole rounds of column groups");
   static_assert(PGR % 32 == 0 && RPW % PGR == 0, "passes of whole 32-row groups");
@@ -448,7 +463,7 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
           half8 y;
 #pragma unroll
           for (int q = 0; q < 8; q++)
-            y[q] = (_Float16)(row0 + q < m ? epilogue(P.epi, 0.0f, cl[(r0 + q) * crow + c] + b, nullptr) : 0.0f);
+            y[q] = (_Float16)(row0 + q < m ? epilogue(P.epi, 0.0f, rd1((r0 + q) * crow + c) + b, nullptr) : 0.0f);
           // head j, dim i: row j·hd + i; blocked: 8 rows of one block (row0 % 8 == 0, blk % 8 == 0)
           const size_t at = h.blk ? (size_t)(row0 / h.blk) * h.cols * h.blk + (size_t)(col - h.col0) * h.blk + row0 % h.blk
                                   : (size_t)(col - h.col0) * h.rs + row0;
@@ -461,7 +476,7 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
           if (row + h.r0 >= h.rs || col >= P.cols) continue;
           half8 y;
           if (row < m) {
-            const float4 x0 = *(const float4 *)(cl + r * crow + c8), x1 = *(const float4 *)(cl + r * crow + c8 + 4);
+            const float4 x0 = rd4(r * crow + c8), x1 = rd4(r * crow + c8 + 4);
             const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
             for (int q = 0; q < 8; q++) y[q] = (_Float16)epilogue(P.epi, 0.0f, x[q] + bb[q], nullptr);
@@ -486,7 +501,7 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
         for (int it = 0; it < BM * G8 / NT; it++) {
           const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0p + trow(r), col = n0 + c8;
           if (row >= m) continue;
-          const float4 x0 = *(const float4 *)(cl + r * crow + c8), x1 = *(const float4 *)(cl + r * crow + c8 + 4);
+          const float4 x0 = rd4(r * crow + c8), x1 = rd4(r * crow + c8 + 4);
           const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
           if constexpr (E == EPI_GLU) {  // 4 channels from the group [a₀..a₃ | g₀..g₃] at col
             float4 v;
@@ -545,7 +560,7 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
   for (int it = 0; it < BM * G8 / NT; it++) {
     const int e = tid + it * NT, r = e / G8, c8 = 8 * (e % G8), row = m0p + trow(r), col = n0 + c8;
     if (row >= m || col >= P.cols) continue;  // cols % 32 == 0: a group is inside or past
-    const float4 x0 = *(const float4 *)(cl + r * crow + c8), x1 = *(const float4 *)(cl + r * crow + c8 + 4);
+    const float4 x0 = rd4(r * crow + c8), x1 = rd4(r * crow + c8 + 4);
     float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
     if constexpr (SPLIT) {
       float *cp = (float *)P.c + ((size_t)tz * m + row) * P.cols + col;
@@ -678,10 +693,12 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_lds_kernel(LdsArgs P) 
   constexpr int RING = NS * ST + 16;
   // Epilogue passes: PG of each wavefront's TM 32-row tiles at a time, the most that fit in the ring
   // (the whole tile when it fits).
-  constexpr int PG = BM * CROW * 4 <= RING ? TM
-                     : (TM % 2 == 0 && BM / 2 * CROW * 4 <= RING) ? TM / 2
-                     : (TM % 4 == 0 && BM / 4 * CROW * 4 <= RING) ? TM / 4 : 1;
-  constexpr int C_BYTES = WM * 32 * PG * CROW * 4;
+  // (k groups: one plane of the pass per group)
+  constexpr int PG = WK * BM * CROW * 4 <= RING ? TM
+                     : (TM % 2 == 0 && WK * BM / 2 * CROW * 4 <= RING) ? TM / 2
+                     : (TM % 4 == 0 && WK * BM / 4 * CROW * 4 <= RING) ? TM / 4 : 1;
+  constexpr int CPL = WM * 32 * PG * CROW;  // floats of one plane of a pass
+  constexpr int C_BYTES = WK * CPL * 4;
   constexpr int LDS_BYTES = RING > C_BYTES ? RING : C_BYTES;
   __shared__ __attribute__((aligned(16))) uint8_t lds[LDS_BYTES];
 
@@ -1005,25 +1022,19 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_lds_kernel(LdsArgs P) 
   auto pass = [&](auto I0_c) {
     constexpr int i0 = decltype(I0_c)::value;
     __syncthreads();
-    // k group 0 stores its sums, then group 1 adds its own (the same lane of the same place: a fixed
-    // order of the two halves' sums).
-    static_for<0, WK, 1>([&](auto G_c) {
-      constexpr int G = decltype(G_c)::value;
-      if (G > 0) __syncthreads();
-      if (kg == G) {
+    // Each k group stores its sums in a plane of its own, both at once; the stores below add group
+    // 0's and group 1's (a fixed order of the two halves' sums).
+    float *mine = cl + kg * CPL;
 #pragma unroll
-        for (int i = i0; i < i0 + PG; i++)
+    for (int i = i0; i < i0 + PG; i++)
 #pragma unroll
-          for (int j = 0; j < TN; j++)
+      for (int j = 0; j < TN; j++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-              float &x = cl[(crow0 + 32 * (i - i0) + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow];
-              x = G == 0 ? acc[i][j][v] : x + acc[i][j][v];
-            }
-      }
-    });
+        for (int v = 0; v < 16; v++)
+          mine[(crow0 + 32 * (i - i0) + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow] = acc[i][j][v];
     __syncthreads();
-    store_c_tile<WM * 32 * PG, BM / WM, 32 * PG, BN, 64 * NWT, SPLIT, OUT16>(P, cl, CROW, tid, m0, n0, tz, i0, bb, bd);
+    store_c_tile<WM * 32 * PG, BM / WM, 32 * PG, BN, 64 * NWT, SPLIT, OUT16, (WK > 1)>(P, cl, CROW, tid, m0, n0, tz, i0,
+                                                                                     bb, bd, cl + CPL);
   };
   static_for<0, TM, PG>(pass);
 }

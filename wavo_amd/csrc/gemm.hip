@@ -75,8 +75,10 @@ GemmPlan gemm_plan_for(const wh_ctx *ctx, int m, int cols, int k) {
     // 96×64 tiles of 2 wavefronts (96×32 per wavefront: each dequantized W fragment feeds three
     // MFMAs) in two slots: 512 workgroups, two per CU, whose barriers do not align (measured in
     // the encoder step, 60 s: 4.64 ms, against 4.68 for 128×64 tiles of 4 wavefronts, 4.75 for
-    // 128×128 tiles of 8 wavefronts, 4.92 for 128×64 tiles in three slots, one per CU).
-    p = {96, 64, 1, 2, 2, 4};
+    // 128×128 tiles of 8 wavefronts, 4.92 for 128×64 tiles in three slots, one per CU); in two k
+    // groups where they divide every split (14.3 against 15.0 µs in the step, the groups' sums in
+    // LDS planes of their own).
+    p = {96, 64, 1, 2, 2, 4, 0, k % (4 * 128) == 0 ? 2 : 1};
   else if (t128 * 4 <= 2L * cus && k % (4 * 64) == 0 && k / (4 * 64) >= 16)
     // The same with up to two workgroups per CU (Whisper's fc2, 1500 × 1280 × 5120: 1.18 + its
     // finish against 1.82 ms per call for 64×64 tiles whole).

@@ -171,6 +171,18 @@ def test_gemm_tile_orders_agree(gpu, plan):
         assert np.array_equal(o, outs[0]), f"plan {plan}: {group} row tiles per group"
 
 
+def test_gemm_rejects_internal_epilogues(gpu):
+    # The library's own epilogues past WH_TANH (the conv module's GLU) are not callers' to ask for.
+    m, n, k = 4, 64, 64
+    l = gpu.linear([(ox.quantize(rnd(n * k, 1).reshape(n, k), wa.Q8_0), wa.Q8_0, k, n)], rnd(n, 2))
+    ab, cb = gpu.upload(rnd(m * k, 3).reshape(m, k)), gpu.buffer(m * n)
+    for epi in (7, -1):
+        with pytest.raises(wa.WavoError, match="epilogue"):
+            gpu.gemm(ab, l, cb, m, epi)
+        with pytest.raises(wa.WavoError, match="epilogue"):
+            gpu.gemm_h(ab, l, cb, m, epi)
+
+
 def test_gemm_padded_k(gpu):
     # k = 40 is padded to 64 by Gpu::conv; input rows are 64 wide with zeros after 40 (from im2col).
     n, k, m = 64, 40, 37

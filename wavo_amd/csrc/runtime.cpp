@@ -687,6 +687,8 @@ int wh_gemm(wh_ctx *ctx, const float *a, const wh_linear *l, float *c, int m, in
 
 int wh_gemm_h(wh_ctx *ctx, const void *a16, const wh_linear *l, void *c, int m, int epi, float alpha, int out16) {
   if (!ctx || !l) return WH_EARG;
+  // (the library's internal epilogues, past WH_TANH, are not part of the interface)
+  if (epi < WH_BIAS || epi > WH_TANH) return wh_fail(ctx, WH_EARG, "gemm: epilogue %d", epi);
   return launch_gemm_h(ctx, a16, l, c, m, l->cols + l->dual, epi, alpha, out16);
 }
 

@@ -424,7 +424,7 @@ __device__ __forceinline__ void static_for(F &&f) {
 template <int NR, int RPW, int PGR, int BN, int NT, bool SPLIT, bool OUT16, bool TWO = false>
 __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, int crow, int tid, int m0, int n0,
                                              int tz, int i0, const float (&bb)[8], const float (&bd)[8],
-                                             const float *cl2 = nullptr) {
+                                             const float *cl2 = nullptr, int ccol = 0) {
   constexpr int G8 = BN / 8;
   // The tile's sums: with TWO the two k groups' planes added as they are read (group 0's + group 1's).
   auto rd4 = [&](int off) {
@@ -454,12 +454,46 @@ __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, 
       if (o >= P.nho) break;
       const HeadsOut &h = P.ho[o];
       if (n0 < h.col0 || n0 >= h.col0 + h.cols) continue;
-      if (h.tr) {
+      if (h.tr && ccol) {
+        // The tile staged column by column (ccol floats per LDS column): a column's 8 rows are two
+        // 16-byte reads.  Lanes down the rows of a column (rows per head of Vᵀ are contiguous), or,
+        // blocked, along the columns in pairs of 8-row halves (a block's columns follow each other).
+        // Every item's bias loaded before the first store (a load after a store to memory that may
+        // alias it would wait for a round trip per item).
+        constexpr int ITS = (BM * G8 + NT - 1) / NT;
+        float bi[ITS];
+#pragma unroll
+        for (int it = 0; it < ITS; it++) {
+          const int e = tid + it * NT, c = h.blk ? (e >> 1) % BN : e / (BM / 8);
+          bi[it] = e < BM * G8 && n0 + c < P.cols ? P.bias[n0 + c] : 0.0f;
+        }
+#pragma unroll
+        for (int it = 0; it < ITS; it++) {
+          const int e = tid + it * NT;
+          if (e >= BM * G8) break;
+          const int c = h.blk ? (e >> 1) % BN : e / (BM / 8);
+          const int r0 = h.blk ? 8 * ((e & 1) + 2 * (e / (2 * BN))) : 8 * (e % (BM / 8));
+          const int row0 = m0p + trow(r0), col = n0 + c;
+          if (row0 >= h.rs || col >= P.cols) continue;
+          const float b = bi[it];
+          const float4 x0 = rd4(c * ccol + r0), x1 = rd4(c * ccol + r0 + 4);
+          const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+          half8 y;
+#pragma unroll
+          for (int q = 0; q < 8; q++) y[q] = (_Float16)(row0 + q < m ? epilogue(P.epi, 0.0f, x[q] + b, nullptr) : 0.0f);
+          const size_t at = h.blk ? (size_t)(row0 / h.blk) * h.cols * h.blk + (size_t)(col - h.col0) * h.blk + row0 % h.blk
+                                  : (size_t)(col - h.col0) * h.rs + row0;
+          *(half8 *)(h.dst + at) = y;
+        }
+      } else if (h.tr) {
+        // A lane's column is the same in every round (NT % BN == 0): its bias loaded once, before the
+        // stores.
+        static_assert(NT % BN == 0, "a fixed column per lane");
+        const float b = n0 + tid % BN < P.cols ? P.bias[n0 + tid % BN] : 0.0f;
 #pragma unroll
         for (int it = 0; it < BM * G8 / NT; it++) {
           const int e = tid + it * NT, c = e % BN, r0 = 8 * (e / BN), row0 = m0p + trow(r0), col = n0 + c;
           if (row0 >= h.rs || col >= P.cols) continue;
-          const float b = P.bias[col];
           half8 y;
 #pragma unroll
           for (int q = 0; q < 8; q++)
@@ -1018,6 +1052,17 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_lds_kernel(LdsArgs P) 
   // Pass i0: 32-row tiles i0 .. i0 + PG − 1 of every wavefront; LDS row (wave row)·32·PG + 32·(i − i0)
   // + the row in the MFMA tile.
   const int crow0 = (wv / WN) * 32 * PG;
+  // A tile of a transposed packed range (Vᵀ, flattened image rows) is staged column by column, CCOL
+  // floats per column (its 4-row runs written 16 bytes at a time; the padding spreads a 16-lane pass
+  // over every bank), when that fits in a plane.
+  constexpr int NRP = WM * 32 * PG, CCOL = NRP + 4;
+  constexpr bool TCM = OUT16 && !SPLIT && BN * CCOL <= CPL;
+  bool trt = false;
+  if constexpr (TCM) {
+#pragma unroll
+    for (int o = 0; o < 2; o++)
+      if (o < P.nho && P.ho[o].tr && n0 >= P.ho[o].col0 && n0 < P.ho[o].col0 + P.ho[o].cols) trt = true;
+  }
   // (passes unrolled at compile time, so that the accumulators are only ever indexed by constants)
   auto pass = [&](auto I0_c) {
     constexpr int i0 = decltype(I0_c)::value;
@@ -1025,16 +1070,27 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_lds_kernel(LdsArgs P) 
     // Each k group stores its sums in a plane of its own, both at once; the stores below add group
     // 0's and group 1's (a fixed order of the two halves' sums).
     float *mine = cl + kg * CPL;
+    if (TCM && trt) {
 #pragma unroll
-    for (int i = i0; i < i0 + PG; i++)
+      for (int i = i0; i < i0 + PG; i++)
 #pragma unroll
-      for (int j = 0; j < TN; j++)
+        for (int j = 0; j < TN; j++)
 #pragma unroll
-        for (int v = 0; v < 16; v++)
-          mine[(crow0 + 32 * (i - i0) + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow] = acc[i][j][v];
+          for (int v4 = 0; v4 < 4; v4++)
+            *(float4 *)(mine + (wn + 32 * j + lrow) * CCOL + crow0 + 32 * (i - i0) + 8 * v4 + 4 * g) =
+                make_float4(acc[i][j][4 * v4], acc[i][j][4 * v4 + 1], acc[i][j][4 * v4 + 2], acc[i][j][4 * v4 + 3]);
+    } else {
+#pragma unroll
+      for (int i = i0; i < i0 + PG; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+          for (int v = 0; v < 16; v++)
+            mine[(crow0 + 32 * (i - i0) + 8 * (v >> 2) + 4 * g + (v & 3)) * CROW + wn + 32 * j + lrow] = acc[i][j][v];
+    }
     __syncthreads();
-    store_c_tile<WM * 32 * PG, BM / WM, 32 * PG, BN, 64 * NWT, SPLIT, OUT16, (WK > 1)>(P, cl, CROW, tid, m0, n0, tz, i0,
-                                                                                     bb, bd, cl + CPL);
+    store_c_tile<WM * 32 * PG, BM / WM, 32 * PG, BN, 64 * NWT, SPLIT, OUT16, (WK > 1)>(
+        P, cl, CROW, tid, m0, n0, tz, i0, bb, bd, cl + CPL, TCM && trt ? CCOL : 0);
   };
   static_for<0, TM, PG>(pass);
 }

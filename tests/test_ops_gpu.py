@@ -151,24 +151,31 @@ def test_gemm_every_plan(gpu, wtype, plan):
 @pytest.mark.parametrize("plan", ["96,128,1,4,3,1,0,2", "96,64,1,2,2,4", "64,64,2,2,3,1"])
 def test_gemm_tile_orders_agree(gpu, plan):
     # The order in which XCDs take the tiles (groups of 1, 2, 3 and all row tiles, column by column
-    # inside a group; a ragged last group at 3) changes no bit of the output.
-    m, n, k = 700, 1024, 1024
-    w = np.random.default_rng(5).normal(0, 0.02, (n, k)).astype(np.float32)
-    l = gpu.linear([(ox.quantize(w, wa.Q8_0), wa.Q8_0, k, n)], rnd(n, 6))
-    ab = gpu.upload(rnd(m * k, 7).reshape(m, k))
-    outs = []
-    gpu.tune("gemm_plan", plan)
-    try:
-        for group in (1, 2, 3, 64):
-            gpu.tune("gemm_group", str(group))
-            cb = gpu.buffer(m * n)
-            gpu.gemm(ab, l, cb, m, wa.BIAS, 0.0)
-            outs.append(gpu.read(cb, (m, n)))
-    finally:
-        gpu.tune("gemm_plan", "")
-        gpu.tune("gemm_group", "0")
-    for group, o in zip((2, 3, 64), outs[1:]):
-        assert np.array_equal(o, outs[0]), f"plan {plan}: {group} row tiles per group"
+    # inside a group; a ragged last group at 3) changes no bit of the output; n = 960 gives tile
+    # counts that are not multiples of the 8 XCDs (the first XCDs take one tile more), checked
+    # against the oracle too.
+    m, k = 700, 1024
+    for n in (1024, 960):
+        w = np.random.default_rng(5).normal(0, 0.02, (n, k)).astype(np.float32)
+        raw, bias = ox.quantize(w, wa.Q8_0), rnd(n, 6)
+        l = gpu.linear([(raw, wa.Q8_0, k, n)], bias)
+        a = rnd(m * k, 7).reshape(m, k)
+        ab = gpu.upload(a)
+        outs = []
+        gpu.tune("gemm_plan", plan)
+        try:
+            for group in (1, 2, 3, 64):
+                gpu.tune("gemm_group", str(group))
+                cb = gpu.buffer(m * n)
+                gpu.gemm(ab, l, cb, m, wa.BIAS, 0.0)
+                outs.append(gpu.read(cb, (m, n)))
+        finally:
+            gpu.tune("gemm_plan", "")
+            gpu.tune("gemm_group", "0")
+        for group, o in zip((2, 3, 64), outs[1:]):
+            assert np.array_equal(o, outs[0]), f"plan {plan}, n {n}: {group} row tiles per group"
+        want = ox.gemm(a, ox.Linear(wa.Q8_0, k, [(raw, n)], bias), m, ox.BIAS)
+        close(outs[0], want, tol=2e-5 * max(1.0, float(np.abs(want).max())), what=f"plan {plan}, n {n}")
 
 
 def test_gemm_rejects_internal_epilogues(gpu):

@@ -744,16 +744,15 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_lds_kernel(LdsArgs P) 
   // run is ordered in groups of P.group row tiles, column by column inside a group: an XCD's tiles
   // then form a rectangle of row tiles x column tiles, whose rows of a and of w its L2 fetches once.
   // (P.group 1: a band of row tiles over all column tiles, which fetches the whole of w per XCD.)
+  // (XCD x takes the linear ids ≡ x mod 8: total / 8 of them, one more for the first total % 8.)
   int tx = blockIdx.x, ty = blockIdx.y, tz = blockIdx.z;
   {
     const int nx = gridDim.x, ny = gridDim.y, total = nx * ny * gridDim.z;
-    if (total % 8 == 0) {
-      const int lin = tx + nx * (ty + ny * tz), l = (lin % 8) * (total / 8) + lin / 8;
-      tz = l / (nx * ny);
-      const int e = l % (nx * ny), g0 = e / (P.group * nx) * P.group, gh = min(P.group, ny - g0), w = e - g0 * nx;
-      ty = g0 + w % gh;
-      tx = w / gh;
-    }
+    const int lin = tx + nx * (ty + ny * tz), x = lin % 8, l = x * (total / 8) + min(x, total % 8) + lin / 8;
+    tz = l / (nx * ny);
+    const int e = l % (nx * ny), g0 = e / (P.group * nx) * P.group, gh = min(P.group, ny - g0), w = e - g0 * nx;
+    ty = g0 + w % gh;
+    tx = w / gh;
   }
   const int n0 = tx * BN, m0 = ty * BM;
   // k group kg of the wavefront (it computes sub-stage kg of every slot) and its place wv in the group.

@@ -1156,10 +1156,11 @@ int launch_lds_t(wh_ctx *ctx, const _Float16 *a, const wh_linear *l, void *c, in
     args.ho[i] = h;
   }
   dim3 grid((l->cols + p.bn - 1) / p.bn, (m + p.bm - 1) / p.bm, p.split);
-  // Tile order: k-group plans (few tiles per CU, w from HBM) in groups of 2 row tiles, the others row
-  // by row (Parakeet 60 s in-step: the 750x4096x1024 up projections 15.5 -> 14.8 us, while the
-  // 64x64 qkv projection, a single k group, slows with every group size above 1).
-  const int group = ctx->gemm_group ? ctx->gemm_group : p.wk > 1 ? 2 : 1;
+  // Tile order: k-group plans under 1024 rows (few tiles per CU, w from HBM) in groups of 2 row
+  // tiles, the others row by row (Parakeet 60 s in-step: the 750x4096x1024 up projections 15.5 ->
+  // 14.8 us, while the 64x64 qkv projection, a single k group, slows with every group size above 1;
+  // Whisper's 1500x1280x1280 k-group projection takes 17.5 us in groups of 2, 15.0 row by row).
+  const int group = ctx->gemm_group ? ctx->gemm_group : p.wk > 1 && m < 1024 ? 2 : 1;
   args.group = std::max(1, std::min(group, (int)grid.y));
   static const char *tn = WT == WH_F16 ? "f16" : WT == WH_Q8_0 ? "q8_0" : "q4_0";
   // Named by kernel variant and call shape: m x rows x k, epilogue, output type, row width.

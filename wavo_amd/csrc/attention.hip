@@ -477,11 +477,24 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
                                                       int batch, int t, int heads, int hd, void *__restrict__ o, int os,
                                                       long bo, int o16) {
   const int q4 = hd / 4;
-  const size_t n = (size_t)batch * t * heads * q4;
-  for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (size_t)gridDim.x * 256) {
+  // With (window, head) pairs a multiple of 8, the flash kernel ran pair run x of 8 on XCD x (its
+  // items in contiguous runs per XCD, the query tiles and key splits of a pair together); workgroup
+  // g runs on XCD g % 8, so it takes that XCD's pairs, where their partial outputs were written.
+  const int pairs = batch * heads;
+  const bool runs = pairs % 8 == 0 && gridDim.x % 8 == 0;
+  const int per = runs ? pairs / 8 : pairs, x = runs ? blockIdx.x % 8 : 0;
+  const size_t n = (size_t)per * t * q4, first = runs ? blockIdx.x / 8 : blockIdx.x,
+               stride = runs ? gridDim.x / 8 : gridDim.x;
+  for (size_t e = first * 256 + threadIdx.x; e < n; e += stride * 256) {
     const int d = 4 * (int)(e % q4);
     const size_t r = e / q4;
-    const int head = (int)(r % heads), i = (int)((r / heads) % t), b = (int)(r / ((size_t)heads * t));
+    int head, i, b;
+    if (runs) {  // the run's pairs one after another, query rows in order inside a pair
+      const int pr = x * per + (int)(r / t);
+      i = (int)(r % t), head = pr % heads, b = pr / heads;
+    } else {
+      head = (int)(r % heads), i = (int)((r / heads) % t), b = (int)(r / ((size_t)heads * t));
+    }
     // Splits in groups of four, each group's loads in flight at once; a running maximum rescales
     // the sums when a later group raises it (one group: the plain two-pass merge, same order).
     float mx = -INFINITY, den = 0.0f;
@@ -569,7 +582,7 @@ int launch_flash(wh_ctx *ctx, const Args &a, int heads, int batch, int dp) {
   if (int rc = wh_launched(ctx, "attention")) return rc;
   if (a.nsplit > 1) {
     const size_t n = (size_t)batch * a.t * heads * (a.hd / 4);
-    const int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
+    const int blocks = (int)std::min<size_t>((n + 255) / 256 + 7, 4096) / 8 * 8;  // whole runs of 8 (per XCD)
     ProfScope pc(ctx, "attention_combine", 0.0, 4.0 * a.nsplit * batch * a.t * heads * (a.hd + 2.0) +
                                                     (a.o16 ? 2.0 : 4.0) * batch * a.t * heads * a.hd);
     wh_launch(ctx, combine_kernel, blocks, 256, 0, a.po, a.pml, a.nsplit, batch, a.t, heads, a.hd, a.o, a.os, a.bo, a.o16);

@@ -414,13 +414,6 @@ __device__ __forceinline__ void static_for(F &&f) {
   }
 }
 
-// The epilogue's store of NR rows × BN columns of a tile whose f32 sums sit in LDS (cl, rows of `crow`
-// floats): NT threads take 8 consecutive columns each (16-byte loads of c for the residual modes,
-// 16-byte stores), applying the bias (bb, loaded by the caller for the thread's fixed column group),
-// the epilogue, the dual columns (bd) and the padding columns (epi(0 + bias), as the reference's zero
-// rows give); a split GEMM stores its plain partial sums into plane tz instead.  A pass holds, for
-// every row group of RPW tile rows (one per row of wavefronts), PGR of its rows from row 32·i0: LDS
-// row r is tile row (r / PGR)·RPW + 32·i0 + r % PGR (PGR = RPW, i0 = 0: the whole tile in order).
 // The row-major epilogue's lane order and the half of its 8 columns a lane reads first (rows of
 // BN + 8 floats in LDS).  gfx950 serves a 16-byte LDS read in four passes of 16 lanes (the two
 // half-waves, each split by the parity of lane bits 2-4), and a lane's two reads of one row land in
@@ -446,6 +439,13 @@ __device__ __forceinline__ int epi_half(int r) {
   return BN == 64 ? r & 1 : 0;
 }
 
+// The epilogue's store of NR rows × BN columns of a tile whose f32 sums sit in LDS (cl, rows of `crow`
+// floats): NT threads take 8 consecutive columns each (16-byte loads of c for the residual modes,
+// 16-byte stores), applying the bias (bb, loaded by the caller for the thread's fixed column group),
+// the epilogue, the dual columns (bd) and the padding columns (epi(0 + bias), as the reference's zero
+// rows give); a split GEMM stores its plain partial sums into plane tz instead.  A pass holds, for
+// every row group of RPW tile rows (one per row of wavefronts), PGR of its rows from row 32·i0: LDS
+// row r is tile row (r / PGR)·RPW + 32·i0 + r % PGR (PGR = RPW, i0 = 0: the whole tile in order).
 template <int NR, int RPW, int PGR, int BN, int NT, bool SPLIT, bool OUT16, bool TWO = false>
 __device__ __forceinline__ void store_c_tile(const LdsArgs &P, const float *cl, int crow, int tid, int m0, int n0,
                                              int tz, int i0, const float (&bb)[8], const float (&bd)[8],

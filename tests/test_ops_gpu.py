@@ -483,12 +483,14 @@ def test_relative_attention(gpu, t, heads, hd, valid):
     close(gpu.read(ob, (t, d)), want, tol=ATT_TOL)
 
 
+@pytest.mark.parametrize("heads", [8, 3])
 @pytest.mark.parametrize("valid", [None, 400])
-def test_relative_attention_many_splits(valid):
+def test_relative_attention_many_splits(valid, heads):
     """Key blocks split 8 ways (more than the merge's group of four: its running-maximum rescale, and
     splits past the valid keys that contribute nothing), through a context opened with the tuning
-    override."""
-    t, heads, hd = 750, 8, 128
+    override.  8 heads: each XCD merges the heads whose partial outputs it wrote; 3 heads (window-head
+    pairs not a multiple of 8): the merge's plain order."""
+    t, hd = 750, 128
     g = wa.Gpu(0)
     g.tune("attn_split", 8)
     try:

@@ -421,9 +421,9 @@ __device__ __forceinline__ void static_for(F &&f) {
 // pass of a 64-column tile, which holds four rows, a 3-way bank conflict.  There lane bits 1 and 2 and
 // bits 4 and 5 are swapped and odd rows read their high half first: each pass then hits 16 distinct
 // 4-bank groups (found by enumerating lane-bit permutations and half rules over every pass; the
-// 750-frame step 4.06-4.09 -> 4.04 ms).  128- and 256-column tiles keep the plain order: their
-// conflict-free orders (2-way conflicts before) measured slower in the 16-window batch, 24.69
-// against 24.50 ms.
+// 750-frame step 4.06-4.09 -> 4.04 ms).  128- and 256-column tiles keep the plain order (2-way
+// conflicts): their conflict-free orders measured slower, the 128-column one in the 750-frame step
+// (4.05 against 4.04 ms), the 256-column one in the 16-window batch (24.69 against 24.50 ms).
 template <int BN>
 __device__ __forceinline__ int epi_lane(int tid) {
   if constexpr (BN == 64) {
